@@ -1,0 +1,230 @@
+/*
+ * nott_hip.h — C ABI of libnott_hip.so, the MI355X (gfx950) backward-pass
+ * library behind Nott's layer, loss and optimizer modules.
+ *
+ * The reference (MoonFlowww/Thot, namespace Nott) has no C ABI: every
+ * backward op is a libtorch autograd node recorded by a torch::nn module
+ * that Nott builds.  Each entry point below replaces the ATen kernel that
+ * one of those nodes dispatches; the comment on each names the Nott call
+ * site (reference file:line, relative to the reference's src/) whose
+ * backward it computes.
+ *
+ * Conventions (all entry points):
+ *   - Return an int status: NOTT_OK (0) or a negative NOTT_ERR_* code.
+ *     Nothing throws across the ABI.  nott_last_error(ctx) gives the text.
+ *   - Every pointer is a device pointer owned by the caller unless the
+ *     comment says otherwise.  Tensors are dense and contiguous in the
+ *     layout named.  Launches are asynchronous on the context's stream
+ *     (nott_set_stream); nothing synchronises unless stated.
+ *   - `dtype` names the storage type of activations and activation
+ *     gradients (x, y, dy, dx, logits, q/k/v …).  Arithmetic is fp32 for
+ *     both dtypes.  Parameter gradients (dw, db, dgamma, dbeta) and
+ *     per-row / per-channel statistics are always fp32.
+ *   - `accumulate` = 0 overwrites a parameter-gradient output, 1 adds into
+ *     it (libtorch AccumulateGrad semantics on a zero_grad'ed .grad()).
+ *   - A context is bound to one device and is not re-entrant; calls that
+ *     share a context must be serialised by the caller.
+ */
+#ifndef NOTT_HIP_H
+#define NOTT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NOTT_ABI_VERSION 1
+
+enum {
+    NOTT_OK = 0,
+    NOTT_ERR_INVALID_ARG = -1,   /* shape / option error  -> std::invalid_argument */
+    NOTT_ERR_UNSUPPORTED = -2,   /* valid but not built    -> std::invalid_argument */
+    NOTT_ERR_HIP = -3,           /* HIP runtime failure    -> std::runtime_error    */
+    NOTT_ERR_ALLOC = -4,         /* workspace allocation   -> std::runtime_error    */
+    NOTT_ERR_DEVICE = -5         /* kernel-detected data error (e.g. label out of range) */
+};
+
+typedef enum { NOTT_F32 = 0, NOTT_BF16 = 1 } nott_dtype;
+typedef enum { NOTT_NCHW = 0, NOTT_NHWC = 1 } nott_layout;
+
+typedef struct nott_ctx_s* nott_ctx;
+
+/* ---- context --------------------------------------------------------- */
+/* Owns: device id, the launch stream, a grow-only workspace arena and a
+ * device error word.  Replaces nothing in the reference (libtorch keeps
+ * this state in its caching allocator and per-device stream pool). */
+int nott_create(int device, nott_ctx* out);
+int nott_destroy(nott_ctx ctx);
+int nott_set_stream(nott_ctx ctx, void* hip_stream);   /* NULL = legacy default stream */
+void* nott_get_stream(nott_ctx ctx);
+const char* nott_last_error(nott_ctx ctx);
+const char* nott_status_string(int status);
+int nott_abi_version(void);
+/* Synchronises the stream and returns the number of data errors kernels
+ * reported since the last call (labels out of range), then clears it. */
+int nott_device_errors(nott_ctx ctx, int64_t* count);
+/* Device-side workspace currently held, in bytes. */
+int nott_workspace_bytes(nott_ctx ctx, int64_t* bytes);
+
+/* ---- conv2d ------------------------------------------------------------
+ * Replaces the autograd node of torch::nn::Conv2d built by
+ * Nott::Layer::Details::build_registered_layer(Owner&, const Conv2dDescriptor&, size_t)
+ * (layer/details/conv.hpp:140-191, module created at :177; options :39-49).
+ * Layout NCHW is the reference default; NHWC is its ChannelsLast mode
+ * (core.hpp:2546-2561, conv.hpp:178-182).  groups must be 1, padding_mode
+ * "zeros".  Output size p = (h + 2*pad_h - dil_h*(r-1) - 1)/stride_h + 1. */
+typedef struct nott_conv2d_desc {
+    int64_t n, c, h, w;        /* input  x  [n, c, h, w] (logical)          */
+    int64_t k;                 /* output channels; weight [k, c, r, s]      */
+    int64_t r, s;              /* kernel height, width                      */
+    int64_t stride_h, stride_w;
+    int64_t pad_h, pad_w;
+    int64_t dil_h, dil_w;
+    int64_t groups;            /* must be 1 */
+    int32_t layout;            /* nott_layout of x, y, dx, dy; weight always KCRS */
+    int32_t reserved;
+} nott_conv2d_desc;
+
+/* y = conv(x, w) + b (b fp32, nullable); w in dtype.  Forward that feeds the
+ * backward (conv.hpp:177 forward). */
+int nott_conv2d_fwd(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                    const void* x, const void* w, const float* b, void* y);
+/* dgrad: dx = conv_transpose(dy, w).  (ATen convolution_backward, input grad) */
+int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                         const void* dy, const void* w, void* dx);
+/* wgrad: dw[k,c,r,s] = sum_{n,p,q} dy * x(shifted); db[k] = sum dy (db nullable).
+ * dw, db fp32.  (ATen convolution_backward, weight and bias grads) */
+int nott_conv2d_bwd_weight(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                           const void* x, const void* dy, float* dw, float* db,
+                           int accumulate);
+
+/* ---- linear ------------------------------------------------------------
+ * Replaces torch::nn::Linear built by build_registered_layer(Owner&, const
+ * FCDescriptor&, size_t) (layer/details/fc.hpp:32-49, module at :40) and the
+ * q/k/v/out projections of MultiHeadAttentionImpl (attention/details/head.hpp:38-41).
+ * x [m, kin], w [nout, kin] (dtype), b [nout] fp32 nullable, y [m, nout]. */
+int nott_linear_fwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                    const void* x, const void* w, const float* b, void* y);
+/* dx = dy·w (nullable), dw = dyᵀ·x (fp32, nullable), db = Σ_rows dy (fp32, nullable). */
+int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                    const void* dy, const void* x, const void* w,
+                    void* dx, float* dw, float* db, int accumulate);
+
+/* ---- ReLU -------------------------------------------------------------
+ * Replaces the relu node applied after every layer by
+ * Nott::Activation::Details::apply (activation/apply.hpp:24-57, ReLU at
+ * activation/details/relu.hpp:13).  dx = (y <= 0) ? 0 : dy  (y = relu output). */
+int nott_relu_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* x, void* y);
+int nott_relu_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* y, const void* dy, void* dx);
+
+/* ---- max-pool / global average pool -------------------------------------
+ * Replaces torch::nn::MaxPool2d / AdaptiveAvgPool2d({1,1}) built by
+ * build_registered_layer(Owner&, const PoolingDescriptor&, size_t)
+ * (layer/details/pooling.hpp:132-149 and :164-167; options :41-57). */
+typedef struct nott_pool2d_desc {
+    int64_t n, c, h, w;
+    int64_t kh, kw;
+    int64_t stride_h, stride_w;
+    int64_t pad_h, pad_w;
+    int64_t dil_h, dil_w;
+    int32_t ceil_mode;
+    int32_t layout;            /* NOTT_NCHW only */
+} nott_pool2d_desc;
+/* y = max over window, argmax = flat index ih*w+iw within the (n,c) plane
+ * (int64).  Tie rule: first maximum in scan order; a NaN always wins. */
+int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                       const void* x, void* y, int64_t* argmax);
+/* dx[argmax] += dy, summed in output scan order for overlapping windows. */
+int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                       const int64_t* argmax, const void* dy, void* dx);
+/* y[nc] = mean over hw; dx[nc, i] = dy[nc] / hw. */
+int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
+                            const void* x, void* y);
+int nott_avgpool_global_bwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
+                            const void* dy, void* dx);
+
+/* ---- batch norm (training mode) -----------------------------------------
+ * Replaces torch::nn::BatchNorm2d built by build_registered_layer(Owner&,
+ * const BatchNorm2dDescriptor&, size_t) (layer/details/batchnorm.hpp:38-59).
+ * x [n, c, hw] NCHW; gamma, beta, mean, rstd, running stats fp32 [c].
+ * Forward saves mean and rstd = 1/sqrt(var_biased + eps); running stats are
+ * updated with momentum and the unbiased variance (nullable). */
+int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                         const void* x, const float* gamma, const float* beta,
+                         double eps, double momentum, float* running_mean, float* running_var,
+                         void* y, float* mean, float* rstd);
+int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                         const void* x, const void* dy, const float* mean, const float* rstd,
+                         const float* gamma, void* dx, float* dgamma, float* dbeta,
+                         int accumulate);
+
+/* ---- layer norm ---------------------------------------------------------
+ * Replaces torch::nn::LayerNorm of TransformerEncoderLayerImpl
+ * (block/details/transformers/classic.hpp:403-404, final norm :495).
+ * x, y, dy, dx [rows, d] (dtype); gamma, beta [d] (dtype); mean, rstd
+ * [rows] fp32; dgamma, dbeta [d] fp32. */
+int nott_layernorm_fwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d,
+                       const void* x, const void* gamma, const void* beta, double eps,
+                       void* y, float* mean, float* rstd);
+int nott_layernorm_bwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d,
+                       const void* x, const void* dy, const float* mean, const float* rstd,
+                       const void* gamma, void* dx, float* dgamma, float* dbeta,
+                       int accumulate);
+
+/* ---- softmax cross-entropy ------------------------------------------------
+ * Replaces F::cross_entropy called by Nott::Loss::Details::compute(const
+ * CrossEntropyDescriptor&, ...) (loss/details/ce.hpp:21-37), mean reduction,
+ * ignore_index -100, optional label smoothing, no class weights.
+ * logits, dlogits [n, c] (dtype); labels int64 [n].  One pass computes
+ * dlogits = grad_scale·(softmax − (1−ε)·onehot − ε/c)/n_valid and, if loss
+ * is non-NULL, the mean loss (fp32 scalar). */
+int nott_softmax_xent_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c,
+                          const void* logits, const int64_t* labels,
+                          double label_smoothing, double grad_scale,
+                          void* dlogits, float* loss);
+
+/* ---- scaled dot-product attention -----------------------------------------
+ * Replaces ScaledDotProductKernelImpl::forward (attention/details/kernel.hpp:20-96):
+ * s = q·kᵀ·scale, causal mask triu(1) -> -inf, p = softmax(s), o = p·v.
+ * q, o, dO, dq [b, h, t, dh]; k, v, dk, dv [b, h, s, dh] (dtype);
+ * lse [b, h, t] fp32 = log Σ exp(s).  Dropout must be 0. */
+typedef struct nott_attn_desc {
+    int64_t b, h, t, s, dh;
+    int32_t causal;
+    int32_t reserved;
+    double scale;              /* reference: 1/sqrt(dh) */
+} nott_attn_desc;
+int nott_attention_fwd(nott_ctx ctx, const nott_attn_desc* d, nott_dtype dtype,
+                       const void* q, const void* k, const void* v, void* o, float* lse);
+int nott_attention_bwd(nott_ctx ctx, const nott_attn_desc* d, nott_dtype dtype,
+                       const void* q, const void* k, const void* v, const void* o,
+                       const void* dO, const float* lse, void* dq, void* dk, void* dv);
+
+/* ---- Adam / AdamW --------------------------------------------------------
+ * Replaces torch::optim::Adam::step / AdamW::step inherited by
+ * Nott::Optimizer::Details::Adam / AdamW (optimizer/details/adam.hpp:63-154,
+ * 159-250; options :18-60), stepped by Model::step_optimizers
+ * (core.hpp:3820, 5049-5057).  One launch updates a flat buffer of n
+ * parameters.  p and g are p_dtype / g_dtype; m, v fp32.  `step` is the
+ * post-increment step count t (>= 1).  decoupled = 0: Adam (L2 into g);
+ * 1: AdamW (p *= 1 - lr·wd first).  zero_grad_after = 1 also writes g = 0
+ * (Model::zero_grad, core.hpp:2425-2442).  amsgrad is not supported. */
+int nott_adam_step(nott_ctx ctx, int decoupled, int64_t n,
+                   void* p, nott_dtype p_dtype, void* g, nott_dtype g_dtype,
+                   float* m, float* v,
+                   double lr, double beta1, double beta2, double eps, double weight_decay,
+                   int64_t step, int zero_grad_after);
+
+/* ---- utilities used by the host modules ---------------------------------- */
+/* dst = a + b elementwise (residual gradient fan-in, block/details/blocks/residual.hpp:131). */
+int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, void* dst);
+/* Dtype conversion fp32 <-> bf16 (round to nearest even). */
+int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype src_dtype, void* dst, nott_dtype dst_dtype);
+/* Fill n fp32 words with zero using a kernel (safe under graph capture). */
+int nott_zero(nott_ctx ctx, int64_t bytes, void* dst);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NOTT_HIP_H */

@@ -1,0 +1,247 @@
+"""GPU parity of the bandwidth-bound kernels against the CPU oracle, through
+the C ABI (thot_amd.ops -> libnott_hip.so).  Same seeded inputs on both sides;
+bf16 inputs are rounded once and the oracle sees the rounded values."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import check, dev, host, host_input
+from oracle_lib import f32, rng
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["f32", "bf16"]
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from thot_amd import ops as _ops
+    assert torch.cuda.is_available()
+    return _ops
+
+
+# ------------------------------------------------------------------ adam
+@pytest.mark.parametrize("decoupled,wd,step", [(1, 0.01, 10), (0, 0.0, 1), (0, 0.01, 3), (1, 0.0, 2)])
+@pytest.mark.parametrize("n", [1, 7, 4096 + 3, 1 << 20])
+def test_adam_fp32_bit_exact(ops, oracle, decoupled, wd, step, n):
+    g = rng(1000 + n + step)
+    p = f32(g.standard_normal(n) * 0.02)
+    gr = f32(g.standard_normal(n) * 1e-3)
+    m = f32(g.standard_normal(n) * 1e-4) if step > 1 else np.zeros(n, np.float32)
+    v = f32(np.abs(g.standard_normal(n)) * 1e-7) if step > 1 else np.zeros(n, np.float32)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=wd)
+    pd, gd, md, vd = dev(p), dev(gr), dev(m), dev(v)
+    ops.adam_step(pd, gd, md, vd, step=step, decoupled=bool(decoupled), **hp)
+    pe, me, ve = oracle.adam_step(decoupled, p, gr, m, v, hp["lr"], hp["beta1"], hp["beta2"], hp["eps"], wd, step)
+    # identical fp32 operation order: bit-exact
+    assert np.array_equal(host(pd).view(np.int32), pe.view(np.int32))
+    assert np.array_equal(host(md).view(np.int32), me.view(np.int32))
+    assert np.array_equal(host(vd).view(np.int32), ve.view(np.int32))
+
+
+def test_adam_unaligned_and_zero_grad(ops, oracle):
+    g = rng(5)
+    n = 1001
+    base = [torch.zeros(n + 1, device="cuda") for _ in range(4)]
+    p, gr, m, v = (b[1:] for b in base)  # 4-byte offset: scalar path
+    p.copy_(dev(f32(g.standard_normal(n))))
+    gr.copy_(dev(f32(g.standard_normal(n) * 1e-2)))
+    pe, me, ve = oracle.adam_step(1, host(p), host(gr), host(m), host(v), 1e-3, 0.9, 0.999, 1e-8, 0.01, 1)
+    ops.adam_step(p, gr, m, v, lr=1e-3, weight_decay=0.01, step=1, decoupled=True, zero_grad=True)
+    assert np.array_equal(host(p), pe) and np.array_equal(host(m), me) and np.array_equal(host(v), ve)
+    assert torch.count_nonzero(gr).item() == 0
+
+
+def test_adam_bf16_params(ops, oracle):
+    g = rng(6)
+    n = 100003
+    p = host_input(g.standard_normal(n) * 0.02, "bf16")
+    gr = host_input(g.standard_normal(n) * 1e-3, "bf16")
+    m = f32(g.standard_normal(n) * 1e-4)
+    v = f32(np.abs(g.standard_normal(n)) * 1e-7)
+    pd, gd, md, vd = dev(p, "bf16"), dev(gr, "bf16"), dev(m), dev(v)
+    ops.adam_step(pd, gd, md, vd, lr=3e-4, weight_decay=0.01, step=10, decoupled=True)
+    pe, me, ve = oracle.adam_step(1, p, gr, m, v, 3e-4, 0.9, 0.999, 1e-8, 0.01, 10)
+    # moments are fp32 and see exactly the same inputs: bit-exact
+    assert np.array_equal(host(md), me) and np.array_equal(host(vd), ve)
+    # p is rounded to bf16 once at the end
+    assert np.array_equal(host(pd), host_input(pe, "bf16"))
+
+
+def test_adam_rejects_bad_arguments(ops):
+    from thot_amd._abi import NottInvalidArgument
+    p = torch.zeros(8, device="cuda")
+    with pytest.raises(NottInvalidArgument):
+        ops.adam_step(p, p.clone(), p.clone(), p.clone(), lr=1e-3, step=0, decoupled=True)
+    with pytest.raises(NottInvalidArgument):
+        ops.adam_step(p, p.clone(), p.clone(), p.clone(), lr=1e-3, beta1=1.0, step=1, decoupled=True)
+
+
+# ------------------------------------------------------------------ relu
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n", [1, 5, 64 * 1000 + 3])
+def test_relu(ops, oracle, dt, n):
+    g = rng(n)
+    x = host_input(g.standard_normal(n), dt)
+    x[:: 5] = 0.0
+    if n > 4:
+        x[3] = np.nan
+    dy = host_input(g.standard_normal(n), dt)
+    y = ops.relu_fwd(dev(x, dt))
+    ye = oracle.relu_fwd(x)
+    assert np.array_equal(np.isnan(host(y)), np.isnan(ye))
+    check(host(y), ye, dt, "relu y", rtol=0, atol=0)
+    dx = ops.relu_bwd(y, dev(dy, dt))
+    check(host(dx), oracle.relu_bwd(ye, dy), dt, "relu dx", rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_add_cast_zero(ops, dt):
+    g = rng(9)
+    a, b = host_input(g.standard_normal(1003), dt), host_input(g.standard_normal(1003), dt)
+    out = ops.add(dev(a, dt), dev(b, dt))
+    check(host(out), host_input(a + b, dt), dt, "add", rtol=0, atol=0)
+    x = f32(g.standard_normal(999))
+    xb = ops.cast(dev(x), torch.bfloat16)
+    assert np.array_equal(host(xb), host_input(x, "bf16"))
+    t = dev(x)
+    ops.zero_(t)
+    assert torch.count_nonzero(t).item() == 0
+
+
+# ----------------------------------------------------------------- pools
+POOLS = [
+    # n, c, h, w, k, stride, pad, dil, ceil
+    (64, 32, 28, 28, (2, 2), (2, 2), (0, 0), (1, 1), False),   # small CNN pool 1
+    (64, 64, 14, 14, (2, 2), (2, 2), (0, 0), (1, 1), False),   # small CNN pool 2
+    (4, 64, 112, 112, (3, 3), (2, 2), (1, 1), (1, 1), False),  # ResNet-18 stem pool (batch slice)
+    (2, 3, 9, 8, (3, 3), (2, 2), (0, 0), (1, 1), True),
+    (2, 3, 9, 9, (2, 2), (1, 1), (0, 0), (2, 2), False),
+]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", POOLS)
+def test_maxpool(ops, oracle, dt, case):
+    n, c, h, w, k, st, pd, dl, ceil = case
+    g = rng(h * w + c)
+    x = g.standard_normal((n, c, h, w))
+    x = np.maximum(x, 0.0)  # post-ReLU ties, as in the reference's small CNN
+    x = host_input(x, dt)
+    d = ops.pool_desc((n, c, h, w), k, st, pd, dl, ceil)
+    y, idx = ops.maxpool2d_fwd(dev(x, dt), d)
+    ye, idxe = oracle.maxpool2d_fwd(d, x)
+    assert np.array_equal(host(idx).astype(np.int64) if idx.dtype != torch.int64 else idx.cpu().numpy(), idxe), \
+        "argmax routing must be bit-exact"
+    check(host(y), ye, dt, "maxpool y", rtol=0, atol=0)
+    dy = host_input(g.standard_normal(ye.shape), dt)
+    dx = ops.maxpool2d_bwd(idx, dev(dy, dt), d)
+    check(host(dx), oracle.maxpool2d_bwd(d, idxe, dy), dt, "maxpool dx")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_avgpool_global(ops, oracle, dt):
+    g = rng(77)
+    x = host_input(g.standard_normal((64, 512, 7, 7)), dt)
+    y = ops.avgpool_global_fwd(dev(x, dt))
+    check(host(y), oracle.avgpool_global_fwd(x), dt, "avgpool y")
+    dy = host_input(g.standard_normal((64, 512, 1, 1)), dt)
+    dx = ops.avgpool_global_bwd(dev(dy, dt), (7, 7))
+    check(host(dx), oracle.avgpool_global_bwd(dy, (7, 7)), dt, "avgpool dx")
+
+
+# -------------------------------------------------------------- batchnorm
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape", [(64, 64, 56, 56), (64, 512, 7, 7), (3, 5, 4, 3)])
+def test_batchnorm(ops, oracle, dt, shape):
+    n, c, h, w = shape
+    g = rng(n * c + h)
+    x = host_input(g.standard_normal(shape) * 1.5 + 0.3, dt)
+    gamma = f32(1 + 0.1 * g.standard_normal(c))
+    beta = f32(0.1 * g.standard_normal(c))
+    rm, rv = f32(np.zeros(c)), f32(np.ones(c))
+    rmd, rvd = dev(rm), dev(rv)
+    y, mean, rstd = ops.batchnorm2d_fwd(dev(x, dt), dev(gamma), dev(beta), 1e-5, 0.1, rmd, rvd)
+    ye, me, re_, rme, rve = oracle.batchnorm2d_fwd(x, gamma, beta, 1e-5, 0.1, rm, rv)
+    check(host(mean), me, "f32", "bn mean", atol=1e-5)
+    check(host(rstd), re_, "f32", "bn rstd")
+    check(host(y), ye, dt, "bn y")
+    check(host(rmd), rme, "f32", "bn running_mean", atol=1e-5)
+    check(host(rvd), rve, "f32", "bn running_var")
+    dy = host_input(g.standard_normal(shape), dt)
+    dx, dg, db = ops.batchnorm2d_bwd(dev(x, dt), dev(dy, dt), mean, rstd, dev(gamma))
+    dxe, dge, dbe = oracle.batchnorm2d_bwd(x, dy, host(mean), host(rstd), gamma)
+    check(host(dx), dxe, dt, "bn dx")
+    check(host(dg), dge, "f32", "bn dgamma")
+    check(host(db), dbe, "f32", "bn dbeta")
+
+
+# -------------------------------------------------------------- layernorm
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("rows,d", [(2048, 1024), (37, 256), (5, 1000), (3, 3000), (64, 4)])
+def test_layernorm(ops, oracle, dt, rows, d):
+    g = rng(rows + d)
+    x = host_input(g.standard_normal((rows, d)), dt)
+    gamma = host_input(1 + 0.1 * g.standard_normal(d), dt)
+    beta = host_input(0.1 * g.standard_normal(d), dt)
+    y, mean, rstd = ops.layernorm_fwd(dev(x, dt), dev(gamma, dt), dev(beta, dt))
+    ye, me, re_ = oracle.layernorm_fwd(x, gamma, beta)
+    check(host(mean), me, "f32", "ln mean")
+    check(host(rstd), re_, "f32", "ln rstd")
+    check(host(y), ye, dt, "ln y")
+    dy = host_input(g.standard_normal((rows, d)), dt)
+    dx, dg, db = ops.layernorm_bwd(dev(x, dt), dev(dy, dt), mean, rstd, dev(gamma, dt))
+    dxe, dge, dbe = oracle.layernorm_bwd(x, dy, host(mean), host(rstd), gamma)
+    check(host(dx), dxe, dt, "ln dx")
+    check(host(dg), dge, "f32", "ln dgamma")
+    check(host(db), dbe, "f32", "ln dbeta")
+    # accumulate into existing grads
+    dg2, db2 = dg.clone(), db.clone()
+    ops.layernorm_bwd(dev(x, dt), dev(dy, dt), mean, rstd, dev(gamma, dt), dg2, db2, accumulate=True)
+    check(host(dg2), 2 * dge, "f32", "ln dgamma accumulate")
+
+
+def test_layernorm_full_size_invariants(ops):
+    """C3a shape 16384 x 1024: per-row Σdx = 0 and Σdx·x̂ = 0 (exact in reals)."""
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(16384, 1024, device="cuda", generator=g)
+    gamma = 1 + 0.1 * torch.randn(1024, device="cuda", generator=g)
+    beta = torch.zeros(1024, device="cuda")
+    dy = torch.randn(16384, 1024, device="cuda", generator=g)
+    y, mean, rstd = ops.layernorm_fwd(x, gamma, beta)
+    dx, dg, db = ops.layernorm_bwd(x, dy, mean, rstd, gamma)
+    xh = (x - mean[:, None]) * rstd[:, None]
+    scale = dx.abs().mean().item() * 1024
+    assert dx.sum(1).abs().max().item() < 1e-4 * scale
+    assert (dx * xh).sum(1).abs().max().item() < 1e-3 * scale
+    torch.testing.assert_close(db, dy.sum(0), rtol=1e-4, atol=1e-3)
+    torch.testing.assert_close(dg, (dy * xh).sum(0), rtol=1e-4, atol=1e-3)
+
+
+# ---------------------------------------------------------- cross-entropy
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n,c,eps,ignore", [(64, 10, 0.0, False), (64, 1000, 0.0, False), (33, 1001, 0.1, True),
+                                            (256, 32000, 0.0, False), (8, 40000, 0.05, True), (5, 7, 0.0, False)])
+def test_softmax_xent(ops, oracle, dt, n, c, eps, ignore):
+    g = rng(n + c)
+    z = host_input(g.standard_normal((n, c)) * 2.0, dt)
+    y = g.integers(0, c, n).astype(np.int64)
+    if ignore:
+        y[:: 4] = -100
+    dl, loss = ops.softmax_xent_bwd(dev(z, dt), torch.from_numpy(y).cuda(), label_smoothing=eps)
+    dle, losse = oracle.softmax_xent(z, y, eps)
+    check(host(dl), dle, dt, "xent dlogits")
+    check(loss.item(), losse, "f32", "xent loss", rtol=1e-5)
+    # label gather is exact: the target column carries the −(1−ε)/n term
+    rows = np.nonzero(y != -100)[0]
+    assert (host(dl)[rows, y[rows]] < 0).all()
+
+
+def test_softmax_xent_bad_label_is_reported(ops):
+    z = torch.randn(4, 10, device="cuda")
+    y = torch.tensor([1, 2, 10, -5], device="cuda")
+    ctx = ops.context()
+    ctx.device_errors()
+    dl, _ = ops.softmax_xent_bwd(z, y)
+    assert ctx.device_errors() == 2
+    assert torch.count_nonzero(dl[2:]).item() == 0

@@ -1,0 +1,175 @@
+// Fused single-pass Adam / AdamW over a flat parameter buffer.
+//
+// Replaces torch::optim::Adam::step / AdamW::step as inherited by
+// Nott::Optimizer::Details::Adam / AdamW (reference optimizer/details/adam.hpp:63,159),
+// which libtorch runs as 6–9 separate elementwise passes per tensor.  The
+// per-element operation order, including where libtorch's vectorised CPU
+// kernels fuse a multiply-add, follows libtorch's step (bias corrections in
+// double on the host, moments and update in fp32 on the device), so results
+// match the reference bit for bit:
+//   Adam :  g' = fma(p, wd, g)                    (if wd != 0)
+//   AdamW:  p  = p·(1 − lr·wd)                    (if wd != 0)
+//   m = fma(g', 1−β1, m·β1) ;  v = fma((1−β2)·g', g', v·β2)
+//   p = p + (−lr/bc1 · m) / (sqrt(v)/sqrt(bc2) + eps)
+// sqrt and the divisions are correctly rounded (HIP's default for fp32).
+// One launch streams p, g, m, v once: 28 B/param fp32, 22 B/param for
+// bf16 p and g.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace {
+
+struct AdamScalars {
+    float beta1, beta2, one_m_b1, one_m_b2;
+    float wd, decay;          // decay = 1 - lr*wd (AdamW)
+    float neg_step;           // -(lr / bc1)
+    float bc2_sqrt;           // sqrt(bc2)
+    float eps;
+};
+
+// MODE 0: no weight decay; 1: Adam (L2 added to the gradient); 2: AdamW (decoupled).
+template <int MODE>
+__device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v, const AdamScalars& s) {
+    // Only the explicit fmaf calls may fuse; p·decay must round before the
+    // final add, as it does in the reference.
+#pragma clang fp contract(off)
+    if (MODE == 2) p = p * s.decay;
+    if (MODE == 1) g = __builtin_fmaf(p, s.wd, g);
+    const float mb = m * s.beta1;
+    m = __builtin_fmaf(g, s.one_m_b1, mb);
+    const float vb = v * s.beta2;
+    const float ag = s.one_m_b2 * g;
+    v = __builtin_fmaf(ag, g, vb);
+    const float denom = __builtin_sqrtf(v) / s.bc2_sqrt + s.eps;
+    const float num = s.neg_step * m;
+    p = p + num / denom;
+}
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 2;   // float4 groups per thread
+
+// Vector path: every pointer aligned to its 4-element group.
+template <typename TP, typename TG, int MODE, bool ZERO>
+__global__ __launch_bounds__(kThreads) void adam_vec_kernel(TP* __restrict__ p, TG* __restrict__ g,
+                                                            float* __restrict__ m, float* __restrict__ v,
+                                                            int64_t nvec, AdamScalars s) {
+    const int64_t base = ((int64_t)blockIdx.x * kThreads * kUnroll) + threadIdx.x;
+    f32x4 pv[kUnroll], gv[kUnroll], mv[kUnroll], vv[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + (int64_t)u * kThreads;
+        if (i < nvec) {
+            pv[u] = Vec4<TP>::ld(p + 4 * i);
+            gv[u] = Vec4<TG>::ld(g + 4 * i);
+            mv[u] = *reinterpret_cast<const f32x4*>(m + 4 * i);
+            vv[u] = *reinterpret_cast<const f32x4*>(v + 4 * i);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t i = base + (int64_t)u * kThreads;
+        if (i < nvec) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float pe = pv[u][e], me = mv[u][e], ve = vv[u][e];
+                adam_elem<MODE>(pe, gv[u][e], me, ve, s);
+                pv[u][e] = pe;
+                mv[u][e] = me;
+                vv[u][e] = ve;
+            }
+            Vec4<TP>::st(p + 4 * i, pv[u]);
+            *reinterpret_cast<f32x4*>(m + 4 * i) = mv[u];
+            *reinterpret_cast<f32x4*>(v + 4 * i) = vv[u];
+            if (ZERO) Vec4<TG>::st(g + 4 * i, f32x4{0.f, 0.f, 0.f, 0.f});
+        }
+    }
+}
+
+// Scalar path for the tail and for unaligned buffers.
+template <typename TP, typename TG, int MODE, bool ZERO>
+__global__ __launch_bounds__(kThreads) void adam_scalar_kernel(TP* __restrict__ p, TG* __restrict__ g,
+                                                               float* __restrict__ m, float* __restrict__ v,
+                                                               int64_t begin, int64_t n, AdamScalars s) {
+    const int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    float pe = Io<TP>::ld(p, i), me = m[i], ve = v[i];
+    adam_elem<MODE>(pe, Io<TG>::ld(g, i), me, ve, s);
+    Io<TP>::st(p, i, pe);
+    m[i] = me;
+    v[i] = ve;
+    if (ZERO) Io<TG>::st(g, i, 0.f);
+}
+
+template <typename TP, typename TG, int MODE, bool ZERO>
+int launch(nott_ctx ctx, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s) {
+    TP* pp = static_cast<TP*>(p);
+    TG* gg = static_cast<TG*>(g);
+    const bool aligned = (((uintptr_t)p % (4 * sizeof(TP))) == 0) && (((uintptr_t)g % (4 * sizeof(TG))) == 0) &&
+                         (((uintptr_t)m % 16) == 0) && (((uintptr_t)v % 16) == 0);
+    int64_t done = 0;
+    if (aligned) {
+        const int64_t nvec = n / 4;
+        if (nvec > 0) {
+            const int64_t blocks = nott::ceil_div(nvec, (int64_t)kThreads * kUnroll);
+            hipLaunchKernelGGL((adam_vec_kernel<TP, TG, MODE, ZERO>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                               ctx->stream, pp, gg, m, v, nvec, s);
+        }
+        done = nvec * 4;
+    }
+    if (done < n) {
+        const int64_t blocks = nott::ceil_div(n - done, (int64_t)kThreads);
+        hipLaunchKernelGGL((adam_scalar_kernel<TP, TG, MODE, ZERO>), dim3((unsigned)blocks), dim3(kThreads), 0,
+                           ctx->stream, pp, gg, m, v, done, n, s);
+    }
+    return nott::launch_status(ctx, "adam_kernel");
+}
+
+template <typename TP, typename TG, int MODE>
+int dispatch_zero(nott_ctx ctx, int zero, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s) {
+    return zero ? launch<TP, TG, MODE, true>(ctx, n, p, g, m, v, s) : launch<TP, TG, MODE, false>(ctx, n, p, g, m, v, s);
+}
+
+template <typename TP, typename TG>
+int dispatch_flags(nott_ctx ctx, int mode, int zero, int64_t n, void* p, void* g, float* m, float* v,
+                   const AdamScalars& s) {
+    if (mode == 2) return dispatch_zero<TP, TG, 2>(ctx, zero, n, p, g, m, v, s);
+    if (mode == 1) return dispatch_zero<TP, TG, 1>(ctx, zero, n, p, g, m, v, s);
+    return dispatch_zero<TP, TG, 0>(ctx, zero, n, p, g, m, v, s);
+}
+
+}  // namespace
+
+extern "C" int nott_adam_step(nott_ctx ctx, int decoupled, int64_t n, void* p, nott_dtype p_dtype, void* g,
+                              nott_dtype g_dtype, float* m, float* v, double lr, double beta1, double beta2,
+                              double eps, double weight_decay, int64_t step, int zero_grad_after) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, n >= 0, "nott_adam_step: n must be >= 0");
+    NOTT_REQUIRE(ctx, nott::valid_dtype(p_dtype) && nott::valid_dtype(g_dtype), "nott_adam_step: bad dtype");
+    NOTT_REQUIRE(ctx, step >= 1, "nott_adam_step: step must be >= 1 (post-increment count)");
+    NOTT_REQUIRE(ctx, lr >= 0.0 && eps >= 0.0 && weight_decay >= 0.0, "nott_adam_step: negative lr/eps/weight_decay");
+    NOTT_REQUIRE(ctx, beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0, "nott_adam_step: betas must be in [0, 1)");
+    if (n == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, p && g && m && v, "nott_adam_step: null buffer");
+    nott::DeviceScope scope(ctx->device);
+
+    const double bc1 = 1.0 - std::pow(beta1, (double)step);
+    const double bc2 = 1.0 - std::pow(beta2, (double)step);
+    AdamScalars s;
+    s.beta1 = (float)beta1;
+    s.beta2 = (float)beta2;
+    s.one_m_b1 = (float)(1.0 - beta1);
+    s.one_m_b2 = (float)(1.0 - beta2);
+    s.wd = (float)weight_decay;
+    s.decay = (float)(1.0 - lr * weight_decay);
+    s.neg_step = (float)(-(lr / bc1));
+    s.bc2_sqrt = (float)std::sqrt(bc2);
+    s.eps = (float)eps;
+    // libtorch skips the weight-decay term entirely when wd == 0.
+    const int mode = weight_decay == 0.0 ? 0 : (decoupled ? 2 : 1);
+
+    if (p_dtype == NOTT_F32 && g_dtype == NOTT_F32) return dispatch_flags<float, float>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
+    if (p_dtype == NOTT_BF16 && g_dtype == NOTT_BF16) return dispatch_flags<bf16_t, bf16_t>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
+    if (p_dtype == NOTT_F32 && g_dtype == NOTT_BF16) return dispatch_flags<float, bf16_t>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
+    return dispatch_flags<bf16_t, float>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
+}

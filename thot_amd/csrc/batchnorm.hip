@@ -1,0 +1,303 @@
+// BatchNorm2d (training mode) forward and backward, NCHW.
+//
+// Replaces torch::nn::BatchNorm2d built by build_registered_layer(Owner&,
+// const BatchNorm2dDescriptor&, size_t) (reference layer/details/batchnorm.hpp:38-59;
+// eps 1e-5, momentum 0.1, affine, running stats), i.e. ATen native_batch_norm
+// and native_batch_norm_backward.
+//   forward : μ_c, var_c (biased) over (n, hw); rstd = 1/sqrt(var + eps);
+//             y = (x − μ)·rstd·γ + β; running = (1−m)·running + m·stat (unbiased var)
+//   backward: dβ = Σdy; dγ = Σdy·x̂; dx = γ·rstd·(dy − Σdy/M − x̂·Σ(dy·x̂)/M)
+// Each pass is a per-(channel, slice) partial reduction followed by a tiny
+// per-channel finalize and one streaming apply pass.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+template <int NW>
+__device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[wid] = a;
+        red[NW + wid] = b;
+    }
+    __syncthreads();
+    float ta = 0.f, tb = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        ta += red[i];
+        tb += red[NW + i];
+    }
+    __syncthreads();
+    a = ta;
+    b = tb;
+}
+
+// Partial sums of (x − pivot) and (x − pivot)² over planes [n0, n1) of
+// channel blockIdx.x.  pivot = x[0, c, 0] keeps the variance well conditioned.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict__ x, int64_t n, int64_t c, int64_t hw,
+                                                            int64_t per_split, float* __restrict__ partial) {
+    __shared__ float red[2 * kWaves];
+    const int64_t ch = blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * per_split;
+    const int64_t n1 = std::min<int64_t>(n, n0 + per_split);
+    const float pivot = Io<T>::ld(x, ch * hw);
+    float s1 = 0.f, s2 = 0.f;
+    for (int64_t i = n0; i < n1; ++i) {
+        const T* p = x + (i * c + ch) * hw;
+        if (VEC) {
+            for (int64_t j = (int64_t)threadIdx.x * 4; j < hw; j += kThreads * 4) {
+                f32x4 v = Vec4<T>::ld(p + j);
+                const float a = v.x - pivot, b = v.y - pivot, cc = v.z - pivot, d = v.w - pivot;
+                s1 += (a + b) + (cc + d);
+                s2 += (a * a + b * b) + (cc * cc + d * d);
+            }
+        } else {
+            for (int64_t j = threadIdx.x; j < hw; j += kThreads) {
+                const float a = Io<T>::ld(p, j) - pivot;
+                s1 += a;
+                s2 += a * a;
+            }
+        }
+    }
+    block_sum2<kWaves>(s1, s2, red);
+    if (threadIdx.x == 0) {
+        partial[(ch * gridDim.y + blockIdx.y) * 2 + 0] = s1;
+        partial[(ch * gridDim.y + blockIdx.y) * 2 + 1] = s2;
+    }
+}
+
+// Per channel: mean, rstd, running stats and the affine coefficients
+// y = a·x + b used by the apply pass.
+template <typename T>
+__global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict__ partial, int64_t c, int64_t splits,
+                                int64_t hw, int64_t m, const float* __restrict__ gamma, const float* __restrict__ beta,
+                                float eps, float momentum, float* __restrict__ running_mean,
+                                float* __restrict__ running_var, float* __restrict__ mean, float* __restrict__ rstd,
+                                float* __restrict__ coef) {
+    const int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (ch >= c) return;
+    const float pivot = Io<T>::ld(x, ch * hw);
+    double s1 = 0.0, s2 = 0.0;
+    for (int64_t s = 0; s < splits; ++s) {
+        s1 += partial[(ch * splits + s) * 2 + 0];
+        s2 += partial[(ch * splits + s) * 2 + 1];
+    }
+    const double md = s1 / (double)m;
+    double var = s2 / (double)m - md * md;
+    if (var < 0.0) var = 0.0;
+    const float mu = (float)(md + pivot);
+    const float rs = (float)(1.0 / sqrt(var + (double)eps));
+    mean[ch] = mu;
+    rstd[ch] = rs;
+    const float g = gamma ? gamma[ch] : 1.f, b = beta ? beta[ch] : 0.f;
+    coef[2 * ch + 0] = g * rs;
+    coef[2 * ch + 1] = b - mu * g * rs;
+    if (running_mean) {
+        const double unbiased = m > 1 ? var * (double)m / (double)(m - 1) : var;
+        running_mean[ch] = (1.f - momentum) * running_mean[ch] + momentum * mu;
+        running_var[ch] = (1.f - momentum) * running_var[ch] + momentum * (float)unbiased;
+    }
+}
+
+// y = a_c·x + b_c over the whole tensor.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t total,
+                                                             int64_t c, int64_t hw, const float* __restrict__ coef) {
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * (VEC ? 4 : 1);
+    if (i >= total) return;
+    const int64_t ch = (i / hw) % c;
+    const float a = coef[2 * ch], b = coef[2 * ch + 1];
+    if (VEC) {
+        f32x4 v = Vec4<T>::ld(x + i);
+        v.x = v.x * a + b; v.y = v.y * a + b; v.z = v.z * a + b; v.w = v.w * a + b;
+        Vec4<T>::st(y + i, v);
+    } else {
+        Io<T>::st(y, i, Io<T>::ld(x, i) * a + b);
+    }
+}
+
+// Backward partial sums of dy and dy·(x − μ).
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                                 const float* __restrict__ mean, int64_t n, int64_t c,
+                                                                 int64_t hw, int64_t per_split,
+                                                                 float* __restrict__ partial) {
+    __shared__ float red[2 * kWaves];
+    const int64_t ch = blockIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * per_split;
+    const int64_t n1 = std::min<int64_t>(n, n0 + per_split);
+    const float mu = mean[ch];
+    float s1 = 0.f, s2 = 0.f;
+    for (int64_t i = n0; i < n1; ++i) {
+        const int64_t base = (i * c + ch) * hw;
+        if (VEC) {
+            for (int64_t j = (int64_t)threadIdx.x * 4; j < hw; j += kThreads * 4) {
+                f32x4 g = Vec4<T>::ld(dy + base + j), v = Vec4<T>::ld(x + base + j);
+                s1 += (g.x + g.y) + (g.z + g.w);
+                s2 += (g.x * (v.x - mu) + g.y * (v.y - mu)) + (g.z * (v.z - mu) + g.w * (v.w - mu));
+            }
+        } else {
+            for (int64_t j = threadIdx.x; j < hw; j += kThreads) {
+                const float g = Io<T>::ld(dy, base + j);
+                s1 += g;
+                s2 += g * (Io<T>::ld(x, base + j) - mu);
+            }
+        }
+    }
+    block_sum2<kWaves>(s1, s2, red);
+    if (threadIdx.x == 0) {
+        partial[(ch * gridDim.y + blockIdx.y) * 2 + 0] = s1;
+        partial[(ch * gridDim.y + blockIdx.y) * 2 + 1] = s2;
+    }
+}
+
+// dγ, dβ and the coefficients of dx = A·dy + B·x + C.
+__global__ void bn_bwd_finalize(const float* __restrict__ partial, int64_t c, int64_t splits, int64_t m,
+                                const float* __restrict__ mean, const float* __restrict__ rstd,
+                                const float* __restrict__ gamma, float* __restrict__ dgamma,
+                                float* __restrict__ dbeta, int accumulate, float* __restrict__ coef) {
+    const int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (ch >= c) return;
+    double sdy = 0.0, sdyxc = 0.0;
+    for (int64_t s = 0; s < splits; ++s) {
+        sdy += partial[(ch * splits + s) * 2 + 0];
+        sdyxc += partial[(ch * splits + s) * 2 + 1];
+    }
+    const double rs = rstd[ch], mu = mean[ch];
+    const double sdyx = sdyxc * rs;  // Σ dy·x̂
+    if (dgamma) dgamma[ch] = accumulate ? dgamma[ch] + (float)sdyx : (float)sdyx;
+    if (dbeta) dbeta[ch] = accumulate ? dbeta[ch] + (float)sdy : (float)sdy;
+    const double g = gamma ? gamma[ch] : 1.0;
+    const double A = g * rs;
+    const double B = -g * rs * rs * sdyx / (double)m;
+    const double C = -g * rs * sdy / (double)m - B * mu;
+    coef[3 * ch + 0] = (float)A;
+    coef[3 * ch + 1] = (float)B;
+    coef[3 * ch + 2] = (float)C;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                                T* __restrict__ dx, int64_t total, int64_t c,
+                                                                int64_t hw, const float* __restrict__ coef) {
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * (VEC ? 4 : 1);
+    if (i >= total) return;
+    const int64_t ch = (i / hw) % c;
+    const float A = coef[3 * ch], B = coef[3 * ch + 1], C = coef[3 * ch + 2];
+    if (VEC) {
+        f32x4 g = Vec4<T>::ld(dy + i), v = Vec4<T>::ld(x + i);
+        f32x4 r;
+        r.x = A * g.x + B * v.x + C; r.y = A * g.y + B * v.y + C;
+        r.z = A * g.z + B * v.z + C; r.w = A * g.w + B * v.w + C;
+        Vec4<T>::st(dx + i, r);
+    } else {
+        Io<T>::st(dx, i, A * Io<T>::ld(dy, i) + B * Io<T>::ld(x, i) + C);
+    }
+}
+
+int64_t pick_splits(int64_t n, int64_t c) {
+    int64_t s = nott::ceil_div(2048, c);
+    return std::max<int64_t>(1, std::min<int64_t>(s, n));
+}
+
+template <typename T>
+int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const float* gamma, const float* beta,
+        float eps, float momentum, float* rm, float* rv, void* yv, float* mean, float* rstd) {
+    const T* x = static_cast<const T*>(xv);
+    T* y = static_cast<T*>(yv);
+    const int64_t splits0 = pick_splits(n, c);
+    const int64_t per = nott::ceil_div(n, splits0);
+    const int64_t splits = nott::ceil_div(n, per);
+    float* ws = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)(2 * c * splits + 2 * c)));
+    if (!ws) return NOTT_ERR_ALLOC;
+    float* partial = ws;
+    float* coef = ws + 2 * c * splits;
+    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 && ((uintptr_t)yv % (4 * sizeof(T))) == 0;
+    const dim3 g1((unsigned)c, (unsigned)splits);
+    if (vec)
+        hipLaunchKernelGGL((bn_stats_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
+    else
+        hipLaunchKernelGGL((bn_stats_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
+    hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, x, partial,
+                       c, splits, hw, n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
+    const int64_t total = n * c * hw;
+    if (vec)
+        hipLaunchKernelGGL((bn_affine_kernel<T, true>), dim3((unsigned)nott::ceil_div(total / 4, kThreads)),
+                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
+    else
+        hipLaunchKernelGGL((bn_affine_kernel<T, false>), dim3((unsigned)nott::ceil_div(total, kThreads)),
+                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
+    return nott::launch_status(ctx, "batchnorm_fwd");
+}
+
+template <typename T>
+int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const void* dyv, const float* mean,
+        const float* rstd, const float* gamma, void* dxv, float* dgamma, float* dbeta, int accumulate) {
+    const T* x = static_cast<const T*>(xv);
+    const T* dy = static_cast<const T*>(dyv);
+    T* dx = static_cast<T*>(dxv);
+    const int64_t splits0 = pick_splits(n, c);
+    const int64_t per = nott::ceil_div(n, splits0);
+    const int64_t splits = nott::ceil_div(n, per);
+    float* ws = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)(2 * c * splits + 3 * c)));
+    if (!ws) return NOTT_ERR_ALLOC;
+    float* partial = ws;
+    float* coef = ws + 2 * c * splits;
+    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 &&
+                     ((uintptr_t)dyv % (4 * sizeof(T))) == 0 && ((uintptr_t)dxv % (4 * sizeof(T))) == 0;
+    const dim3 g1((unsigned)c, (unsigned)splits);
+    if (vec)
+        hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
+                           per, partial);
+    else
+        hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
+                           per, partial);
+    hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, partial, c,
+                       splits, n * hw, mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
+    if (dx) {
+        const int64_t total = n * c * hw;
+        if (vec)
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>), dim3((unsigned)nott::ceil_div(total / 4, kThreads)),
+                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef);
+        else
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), dim3((unsigned)nott::ceil_div(total, kThreads)),
+                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef);
+    }
+    return nott::launch_status(ctx, "batchnorm_bwd");
+}
+
+}  // namespace
+
+extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
+                                    const float* gamma, const float* beta, double eps, double momentum,
+                                    float* running_mean, float* running_var, void* y, float* mean, float* rstd) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_fwd: bad shape");
+    NOTT_REQUIRE(ctx, (running_mean == nullptr) == (running_var == nullptr),
+                 "nott_batchnorm2d_fwd: running_mean and running_var go together");
+    NOTT_REQUIRE(ctx, x && y && mean && rstd, "nott_batchnorm2d_fwd: null buffer");
+    NOTT_REQUIRE(ctx, c <= 65535, "nott_batchnorm2d_fwd: too many channels");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
+                                          running_var, y, mean, rstd)
+                             : fwd<bf16_t>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
+                                           running_var, y, mean, rstd);
+}
+
+extern "C" int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
+                                    const void* dy, const float* mean, const float* rstd, const float* gamma, void* dx,
+                                    float* dgamma, float* dbeta, int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_bwd: bad shape");
+    NOTT_REQUIRE(ctx, x && dy && mean && rstd, "nott_batchnorm2d_bwd: null buffer");
+    NOTT_REQUIRE(ctx, c <= 65535, "nott_batchnorm2d_bwd: too many channels");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? bwd<float>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate)
+                             : bwd<bf16_t>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate);
+}

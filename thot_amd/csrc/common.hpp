@@ -1,0 +1,183 @@
+// Shared device and host helpers for libnott_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <string>
+
+#include "nott_hip.h"
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+struct nott_ctx_s {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;            // grow-only device workspace
+    size_t ws_bytes = 0;
+    unsigned long long* err_word = nullptr;  // device counter of data errors
+    int num_cu = 256;
+    std::string last_error;
+};
+
+namespace nott {
+
+// Sets the calling thread's device to the context's device for the scope.
+struct DeviceScope {
+    int prev = -1;
+    bool changed = false;
+    explicit DeviceScope(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+            changed = (hipSetDevice(dev) == hipSuccess);
+        }
+    }
+    ~DeviceScope() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+int fail(nott_ctx ctx, int status, const std::string& msg);
+int hip_fail(nott_ctx ctx, hipError_t e, const char* what);
+// Returns a workspace pointer of at least `bytes` (grows by re-allocation
+// after synchronising the stream); nullptr on failure (error already set).
+void* workspace(nott_ctx ctx, size_t bytes);
+// Checks the last launch and records an error message.
+int launch_status(nott_ctx ctx, const char* kernel);
+
+inline size_t dtype_size(nott_dtype t) { return t == NOTT_BF16 ? 2 : 4; }
+inline bool valid_dtype(int t) { return t == NOTT_F32 || t == NOTT_BF16; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace nott
+
+#define NOTT_CHECK_CTX(ctx)                                          \
+    do {                                                             \
+        if (!(ctx)) return NOTT_ERR_INVALID_ARG;                     \
+    } while (0)
+
+#define NOTT_REQUIRE(ctx, cond, msg)                                 \
+    do {                                                             \
+        if (!(cond)) return nott::fail((ctx), NOTT_ERR_INVALID_ARG, (msg)); \
+    } while (0)
+
+#define NOTT_HIP(ctx, expr)                                          \
+    do {                                                             \
+        hipError_t _e = (expr);                                      \
+        if (_e != hipSuccess) return nott::hip_fail((ctx), _e, #expr); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef uint16_t bf16_t;   // bf16 storage
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+
+// Round to nearest even; NaN maps to a quiet NaN of the same sign.
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+template <typename T> struct Io;
+template <> struct Io<float> {
+    static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Io<bf16_t> {
+    static __device__ __forceinline__ float ld(const bf16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+    static __device__ __forceinline__ void st(bf16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+
+// 4-element vector load/store in either storage type (8 or 16 bytes).
+template <typename T> struct Vec4;
+template <> struct Vec4<float> {
+    static __device__ __forceinline__ f32x4 ld(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+    static __device__ __forceinline__ void st(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+};
+template <> struct Vec4<bf16_t> {
+    static __device__ __forceinline__ f32x4 ld(const bf16_t* p) {
+        u32x2 u = *reinterpret_cast<const u32x2*>(p);
+        f32x4 r;
+        r.x = __builtin_bit_cast(float, u.x << 16);
+        r.y = __builtin_bit_cast(float, u.x & 0xffff0000u);
+        r.z = __builtin_bit_cast(float, u.y << 16);
+        r.w = __builtin_bit_cast(float, u.y & 0xffff0000u);
+        return r;
+    }
+    static __device__ __forceinline__ void st(bf16_t* p, f32x4 v) {
+        u32x2 u;
+        u.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+        u.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+        *reinterpret_cast<u32x2*>(p) = u;
+    }
+};
+
+// DPP move within a row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Full 64-lane sum; every lane receives the result.  Within a row of 16
+// lanes: DPP quad_perm / half-mirror / mirror; across rows: xor shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);  // row_half_mirror
+    v += dpp_f32<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+// Block-wide sum over NWAVES waves through LDS; all threads get the result.
+// `red` must hold NWAVES floats; the call contains two barriers.
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t += red[i];
+    __syncthreads();
+    return t;
+}
+
+template <int NWAVES>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NWAVES; ++i) t = fmaxf(t, red[i]);
+    __syncthreads();
+    return t;
+}

@@ -1,0 +1,235 @@
+// Bandwidth-bound elementwise kernels: ReLU forward/backward, residual add,
+// casts, zero fill and global average pool forward/backward.
+//
+// ReLU backward replaces libtorch's threshold_backward for the ReLU that
+// Nott applies after every layer (reference activation/apply.hpp:24-57,
+// activation/details/relu.hpp:13): dx = (y <= 0) ? 0 : dy.
+// Global average pool replaces AdaptiveAvgPool2d({1,1}) (layer/details/pooling.hpp:164-167).
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct ReluFwd {
+    __device__ __forceinline__ float operator()(float x) const { return (x > 0.f || x != x) ? x : 0.f; }
+};
+
+// dx = (y <= 0) ? 0 : dy; a NaN y passes dy through (threshold_backward semantics).
+struct ReluBwd {
+    __device__ __forceinline__ float operator()(float y, float dy) const { return (y <= 0.f) ? 0.f : dy; }
+};
+
+struct Add {
+    __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kThreads) void unary_vec(const T* __restrict__ x, T* __restrict__ y, int64_t n, F f) {
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        f32x4 a = Vec4<T>::ld(x + i);
+        a.x = f(a.x); a.y = f(a.y); a.z = f(a.z); a.w = f(a.w);
+        Vec4<T>::st(y + i, a);
+    } else {
+        for (int64_t j = i; j < n; ++j) Io<T>::st(y, j, f(Io<T>::ld(x, j)));
+    }
+}
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kThreads) void binary_vec(const T* __restrict__ a, const T* __restrict__ b,
+                                                       T* __restrict__ y, int64_t n, F f) {
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (i + 4 <= n) {
+        f32x4 u = Vec4<T>::ld(a + i), v = Vec4<T>::ld(b + i);
+        u.x = f(u.x, v.x); u.y = f(u.y, v.y); u.z = f(u.z, v.z); u.w = f(u.w, v.w);
+        Vec4<T>::st(y + i, u);
+    } else {
+        for (int64_t j = i; j < n; ++j) Io<T>::st(y, j, f(Io<T>::ld(a, j), Io<T>::ld(b, j)));
+    }
+}
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kThreads) void unary_scalar(const T* __restrict__ x, T* __restrict__ y, int64_t n, F f) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) Io<T>::st(y, i, f(Io<T>::ld(x, i)));
+}
+
+template <typename T, typename F>
+__global__ __launch_bounds__(kThreads) void binary_scalar(const T* __restrict__ a, const T* __restrict__ b,
+                                                          T* __restrict__ y, int64_t n, F f) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) Io<T>::st(y, i, f(Io<T>::ld(a, i), Io<T>::ld(b, i)));
+}
+
+template <typename T>
+bool aligned4(const void* p) {
+    return ((uintptr_t)p % (4 * sizeof(T))) == 0;
+}
+
+template <typename T, typename F>
+int run_unary(nott_ctx ctx, int64_t n, const void* x, void* y, F f, const char* name) {
+    if (n == 0) return NOTT_OK;
+    if (aligned4<T>(x) && aligned4<T>(y)) {
+        const int64_t blocks = nott::ceil_div(nott::ceil_div(n, 4), kThreads);
+        hipLaunchKernelGGL((unary_vec<T, F>), dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream,
+                           static_cast<const T*>(x), static_cast<T*>(y), n, f);
+    } else {
+        const int64_t blocks = nott::ceil_div(n, kThreads);
+        hipLaunchKernelGGL((unary_scalar<T, F>), dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream,
+                           static_cast<const T*>(x), static_cast<T*>(y), n, f);
+    }
+    return nott::launch_status(ctx, name);
+}
+
+template <typename T, typename F>
+int run_binary(nott_ctx ctx, int64_t n, const void* a, const void* b, void* y, F f, const char* name) {
+    if (n == 0) return NOTT_OK;
+    if (aligned4<T>(a) && aligned4<T>(b) && aligned4<T>(y)) {
+        const int64_t blocks = nott::ceil_div(nott::ceil_div(n, 4), kThreads);
+        hipLaunchKernelGGL((binary_vec<T, F>), dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream,
+                           static_cast<const T*>(a), static_cast<const T*>(b), static_cast<T*>(y), n, f);
+    } else {
+        const int64_t blocks = nott::ceil_div(n, kThreads);
+        hipLaunchKernelGGL((binary_scalar<T, F>), dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream,
+                           static_cast<const T*>(a), static_cast<const T*>(b), static_cast<T*>(y), n, f);
+    }
+    return nott::launch_status(ctx, name);
+}
+
+template <typename TS, typename TD>
+__global__ __launch_bounds__(kThreads) void cast_kernel(const TS* __restrict__ s, TD* __restrict__ d, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) Io<TD>::st(d, i, Io<TS>::ld(s, i));
+}
+
+__global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ p, int64_t nwords,
+                                                        uint8_t* __restrict__ tail, int64_t ntail) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < nwords) p[i] = 0u;
+    if (i < ntail) tail[i] = 0;
+}
+
+// One wave per (n, c) plane: mean over hw.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void avgpool_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                               int64_t nc, int64_t hw) {
+    const int64_t plane = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (plane >= nc) return;
+    const T* xp = x + plane * hw;
+    float acc = 0.f;
+    for (int64_t i = lane; i < hw; i += 64) acc += Io<T>::ld(xp, i);
+    acc = wave_sum(acc);
+    if (lane == 0) Io<T>::st(y, plane, acc / (float)hw);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void avgpool_bwd_kernel(const T* __restrict__ dy, T* __restrict__ dx,
+                                                               int64_t nc, int64_t hw) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nc * hw) return;
+    Io<T>::st(dx, i, Io<T>::ld(dy, i / hw) / (float)hw);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nott_relu_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* x, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n >= 0, "nott_relu_fwd: bad dtype or size");
+    NOTT_REQUIRE(ctx, n == 0 || (x && y), "nott_relu_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? run_unary<float>(ctx, n, x, y, ReluFwd{}, "relu_fwd")
+                             : run_unary<bf16_t>(ctx, n, x, y, ReluFwd{}, "relu_fwd");
+}
+
+int nott_relu_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* y, const void* dy, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n >= 0, "nott_relu_bwd: bad dtype or size");
+    NOTT_REQUIRE(ctx, n == 0 || (y && dy && dx), "nott_relu_bwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? run_binary<float>(ctx, n, y, dy, dx, ReluBwd{}, "relu_bwd")
+                             : run_binary<bf16_t>(ctx, n, y, dy, dx, ReluBwd{}, "relu_bwd");
+}
+
+int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, void* dst) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n >= 0, "nott_add: bad dtype or size");
+    NOTT_REQUIRE(ctx, n == 0 || (a && b && dst), "nott_add: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? run_binary<float>(ctx, n, a, b, dst, Add{}, "add")
+                             : run_binary<bf16_t>(ctx, n, a, b, dst, Add{}, "add");
+}
+
+int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype st, void* dst, nott_dtype dt) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(st) && nott::valid_dtype(dt) && n >= 0, "nott_cast: bad dtype or size");
+    NOTT_REQUIRE(ctx, n == 0 || (src && dst), "nott_cast: null buffer");
+    if (n == 0) return NOTT_OK;
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(n, kThreads));
+    if (st == NOTT_F32 && dt == NOTT_BF16)
+        hipLaunchKernelGGL((cast_kernel<float, bf16_t>), grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const float*>(src), static_cast<bf16_t*>(dst), n);
+    else if (st == NOTT_BF16 && dt == NOTT_F32)
+        hipLaunchKernelGGL((cast_kernel<bf16_t, float>), grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const bf16_t*>(src), static_cast<float*>(dst), n);
+    else if (st == NOTT_F32)
+        hipLaunchKernelGGL((cast_kernel<float, float>), grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const float*>(src), static_cast<float*>(dst), n);
+    else
+        hipLaunchKernelGGL((cast_kernel<bf16_t, bf16_t>), grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const bf16_t*>(src), static_cast<bf16_t*>(dst), n);
+    return nott::launch_status(ctx, "cast");
+}
+
+int nott_zero(nott_ctx ctx, int64_t bytes, void* dst) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, bytes >= 0, "nott_zero: negative size");
+    if (bytes == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, dst != nullptr, "nott_zero: null buffer");
+    NOTT_REQUIRE(ctx, ((uintptr_t)dst % 4) == 0, "nott_zero: buffer must be 4-byte aligned");
+    nott::DeviceScope scope(ctx->device);
+    const int64_t nwords = bytes / 4, ntail = bytes % 4;
+    uint8_t* tail = static_cast<uint8_t*>(dst) + nwords * 4;
+    const int64_t work = nwords > ntail ? nwords : ntail;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)nott::ceil_div(work, kThreads)), dim3(kThreads), 0, ctx->stream,
+                       static_cast<uint32_t*>(dst), nwords, tail, ntail);
+    return nott::launch_status(ctx, "zero");
+}
+
+int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw, const void* x, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && nc >= 0 && hw > 0, "nott_avgpool_global_fwd: bad arguments");
+    if (nc == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && y, "nott_avgpool_global_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(nc, kThreads / 64));
+    if (dtype == NOTT_F32)
+        hipLaunchKernelGGL(avgpool_fwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const float*>(x), static_cast<float*>(y), nc, hw);
+    else
+        hipLaunchKernelGGL(avgpool_fwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), nc, hw);
+    return nott::launch_status(ctx, "avgpool_fwd");
+}
+
+int nott_avgpool_global_bwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw, const void* dy, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && nc >= 0 && hw > 0, "nott_avgpool_global_bwd: bad arguments");
+    if (nc == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, dy && dx, "nott_avgpool_global_bwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(nc * hw, kThreads));
+    if (dtype == NOTT_F32)
+        hipLaunchKernelGGL(avgpool_bwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const float*>(dy), static_cast<float*>(dx), nc, hw);
+    else
+        hipLaunchKernelGGL(avgpool_bwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), nc, hw);
+    return nott::launch_status(ctx, "avgpool_bwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,325 @@
+// LayerNorm forward (saves mean / rstd) and backward.
+//
+// Replaces torch::nn::LayerNorm as TransformerEncoderLayerImpl builds it
+// (reference block/details/transformers/classic.hpp:399-404, final norm :495;
+// eps 1e-5, elementwise affine), i.e. ATen native_layer_norm and
+// native_layer_norm_backward.
+//   forward : x̂ = (x − μ)·rstd, rstd = 1/sqrt(var_biased + eps), y = x̂·γ + β
+//   backward: g = dy·γ; dx = rstd·(g − Σg/d − x̂·Σ(g·x̂)/d)
+//             dγ = Σ_rows dy·x̂, dβ = Σ_rows dy
+// One wavefront owns one row: the row's x and dy stay in VGPRs, the two row
+// sums are DPP/shuffle wave reductions, and every lane keeps running dγ / dβ
+// sums for its columns.  Blocks write per-block column partials; a second
+// kernel reduces them (deterministic order).
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kWaves = kThreads / 64;
+constexpr int kRowsInFlight = 2;
+
+// Column group g of lane `lane` covers columns [(g*64 + lane)*4, +4).
+template <typename T, int DPL>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t d, int lane, float (&v)[DPL]) {
+#pragma unroll
+    for (int g = 0; g < DPL / 4; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
+        f32x4 t = c0 < d ? Vec4<T>::ld(p + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        v[4 * g + 0] = t.x; v[4 * g + 1] = t.y; v[4 * g + 2] = t.z; v[4 * g + 3] = t.w;
+    }
+}
+
+template <typename T, int DPL>
+__device__ __forceinline__ void store_row(T* __restrict__ p, int64_t d, int lane, const float (&v)[DPL]) {
+#pragma unroll
+    for (int g = 0; g < DPL / 4; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
+        if (c0 < d) Vec4<T>::st(p + c0, f32x4{v[4 * g + 0], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]});
+    }
+}
+
+template <typename T, int DPL>
+__global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ x, const T* __restrict__ gamma,
+                                                          const T* __restrict__ beta, float eps, T* __restrict__ y,
+                                                          float* __restrict__ mean, float* __restrict__ rstd,
+                                                          int64_t rows, int64_t d) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float gm[DPL], bt[DPL];
+    load_row<T, DPL>(gamma, d, lane, gm);
+    load_row<T, DPL>(beta, d, lane, bt);
+    const float inv_d = 1.f / (float)d;
+    for (int64_t r = (int64_t)blockIdx.x * kWaves + wid; r < rows; r += (int64_t)gridDim.x * kWaves) {
+        float v[DPL];
+        load_row<T, DPL>(x + r * d, d, lane, v);
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) s += v[e];
+        const float mu = wave_sum(s) * inv_d;
+        float ss = 0.f;
+#pragma unroll
+        for (int g = 0; g < DPL / 4; ++g) {
+            const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float t = (c0 + e < d) ? v[4 * g + e] - mu : 0.f;
+                ss += t * t;
+            }
+        }
+        const float rs = 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) v[e] = (v[e] - mu) * rs * gm[e] + bt[e];
+        store_row<T, DPL>(y + r * d, d, lane, v);
+        if (lane == 0) {
+            mean[r] = mu;
+            rstd[r] = rs;
+        }
+    }
+}
+
+template <typename T, int DPL>
+__global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                          const float* __restrict__ mean, const float* __restrict__ rstd,
+                                                          const T* __restrict__ gamma, T* __restrict__ dx,
+                                                          float* __restrict__ partial, int64_t rows, int64_t d) {
+    extern __shared__ float lds[];  // [kWaves][2][d]
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float gm[DPL];
+    load_row<T, DPL>(gamma, d, lane, gm);
+    float dg[DPL], db[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) dg[e] = db[e] = 0.f;
+    const float inv_d = 1.f / (float)d;
+    const int64_t stride = (int64_t)gridDim.x * kWaves * kRowsInFlight;
+    for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wid) * kRowsInFlight; r0 < rows; r0 += stride) {
+        float xv[kRowsInFlight][DPL], gv[kRowsInFlight][DPL];
+        float mu[kRowsInFlight], rs[kRowsInFlight];
+#pragma unroll
+        for (int i = 0; i < kRowsInFlight; ++i) {
+            const int64_t r = r0 + i;
+            if (r < rows) {
+                load_row<T, DPL>(x + r * d, d, lane, xv[i]);
+                load_row<T, DPL>(dy + r * d, d, lane, gv[i]);
+                mu[i] = mean[r];
+                rs[i] = rstd[r];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kRowsInFlight; ++i) {
+            const int64_t r = r0 + i;
+            if (r >= rows) break;
+            float sg = 0.f, sgx = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) {
+                const float xh = (xv[i][e] - mu[i]) * rs[i];
+                const float dyv = gv[i][e];
+                dg[e] += dyv * xh;
+                db[e] += dyv;
+                const float g = dyv * gm[e];
+                sg += g;
+                sgx += g * xh;
+                xv[i][e] = xh;
+                gv[i][e] = g;
+            }
+            sg = wave_sum(sg) * inv_d;
+            sgx = wave_sum(sgx) * inv_d;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) xv[i][e] = rs[i] * (gv[i][e] - sg - xv[i][e] * sgx);
+            store_row<T, DPL>(dx + r * d, d, lane, xv[i]);
+        }
+    }
+    // Combine the waves' column sums and write this block's partial row.
+#pragma unroll
+    for (int g = 0; g < DPL / 4; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (c0 + e < d) {
+                lds[(wid * 2 + 0) * d + c0 + e] = dg[4 * g + e];
+                lds[(wid * 2 + 1) * d + c0 + e] = db[4 * g + e];
+            }
+        }
+    }
+    __syncthreads();
+    for (int64_t j = threadIdx.x; j < 2 * d; j += kThreads) {
+        const int which = j >= d;
+        const int64_t col = j - which * d;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += lds[(w * 2 + which) * d + col];
+        partial[((int64_t)blockIdx.x * 2 + which) * d + col] = s;
+    }
+}
+
+// Sums `nparts` partial rows of 2·d floats into dgamma / dbeta.  One wave per
+// 64 columns of one output; 4 waves split the partial rows.
+__global__ __launch_bounds__(kThreads) void col_reduce_kernel(const float* __restrict__ partial, int64_t nparts,
+                                                              int64_t d, float* __restrict__ dgamma,
+                                                              float* __restrict__ dbeta, int accumulate) {
+    __shared__ float red[kWaves][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int which = blockIdx.y;
+    const int64_t col = (int64_t)blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (col < d) {
+        for (int64_t b = wid; b < nparts; b += kWaves) s += partial[(b * 2 + which) * d + col];
+    }
+    red[wid][lane] = s;
+    __syncthreads();
+    if (wid == 0 && col < d) {
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) t += red[w][lane];
+        float* out = which ? dbeta : dgamma;
+        if (out) out[col] = accumulate ? out[col] + t : t;
+    }
+}
+
+// Generic row kernels (any d): one block per row, three passes over the row.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_fwd_generic(const T* __restrict__ x, const T* __restrict__ gamma,
+                                                           const T* __restrict__ beta, float eps, T* __restrict__ y,
+                                                           float* __restrict__ mean, float* __restrict__ rstd,
+                                                           int64_t d) {
+    __shared__ float red[kWaves];
+    const int64_t r = blockIdx.x;
+    const T* xr = x + r * d;
+    float s = 0.f;
+    for (int64_t j = threadIdx.x; j < d; j += kThreads) s += Io<T>::ld(xr, j);
+    const float mu = block_sum<kWaves>(s, red) / (float)d;
+    float ss = 0.f;
+    for (int64_t j = threadIdx.x; j < d; j += kThreads) {
+        const float t = Io<T>::ld(xr, j) - mu;
+        ss += t * t;
+    }
+    const float rs = 1.f / sqrtf(block_sum<kWaves>(ss, red) / (float)d + eps);
+    for (int64_t j = threadIdx.x; j < d; j += kThreads)
+        Io<T>::st(y + r * d, j, (Io<T>::ld(xr, j) - mu) * rs * Io<T>::ld(gamma, j) + Io<T>::ld(beta, j));
+    if (threadIdx.x == 0) {
+        mean[r] = mu;
+        rstd[r] = rs;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void ln_bwd_generic(const T* __restrict__ x, const T* __restrict__ dy,
+                                                           const float* __restrict__ mean,
+                                                           const float* __restrict__ rstd, const T* __restrict__ gamma,
+                                                           T* __restrict__ dx, float* __restrict__ partial, int64_t d) {
+    __shared__ float red[kWaves];
+    const int64_t r = blockIdx.x;
+    const float mu = mean[r], rs = rstd[r];
+    float sg = 0.f, sgx = 0.f;
+    for (int64_t j = threadIdx.x; j < d; j += kThreads) {
+        const float xh = (Io<T>::ld(x, r * d + j) - mu) * rs;
+        const float dyv = Io<T>::ld(dy, r * d + j);
+        const float g = dyv * Io<T>::ld(gamma, j);
+        sg += g;
+        sgx += g * xh;
+        partial[(r * 2 + 0) * d + j] = dyv * xh;
+        partial[(r * 2 + 1) * d + j] = dyv;
+    }
+    sg = block_sum<kWaves>(sg, red) / (float)d;
+    sgx = block_sum<kWaves>(sgx, red) / (float)d;
+    for (int64_t j = threadIdx.x; j < d; j += kThreads) {
+        const float xh = (Io<T>::ld(x, r * d + j) - mu) * rs;
+        const float g = Io<T>::ld(dy, r * d + j) * Io<T>::ld(gamma, j);
+        Io<T>::st(dx, r * d + j, rs * (g - sg - xh * sgx));
+    }
+}
+
+template <typename T>
+bool vec_ok(const void* p) {
+    return ((uintptr_t)p % (4 * sizeof(T))) == 0;
+}
+
+template <typename T>
+int fwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* gamma, const void* beta, float eps, void* y,
+        float* mean, float* rstd) {
+    const T* xx = static_cast<const T*>(x);
+    const T* gg = static_cast<const T*>(gamma);
+    const T* bb = static_cast<const T*>(beta);
+    T* yy = static_cast<T*>(y);
+    const bool vec = d % 4 == 0 && vec_ok<T>(x) && vec_ok<T>(gamma) && vec_ok<T>(beta) && vec_ok<T>(y);
+    const int64_t blocks = std::min<int64_t>(nott::ceil_div(rows, kWaves), (int64_t)ctx->num_cu * 8);
+    const dim3 grid((unsigned)std::max<int64_t>(blocks, 1));
+    if (vec && d <= 256)
+        hipLaunchKernelGGL((ln_fwd_kernel<T, 4>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
+    else if (vec && d <= 512)
+        hipLaunchKernelGGL((ln_fwd_kernel<T, 8>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
+    else if (vec && d <= 1024)
+        hipLaunchKernelGGL((ln_fwd_kernel<T, 16>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
+    else if (vec && d <= 2048)
+        hipLaunchKernelGGL((ln_fwd_kernel<T, 32>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
+    else
+        hipLaunchKernelGGL(ln_fwd_generic<T>, dim3((unsigned)rows), dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy,
+                           mean, rstd, d);
+    return nott::launch_status(ctx, "layernorm_fwd");
+}
+
+template <typename T>
+int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, const float* mean, const float* rstd,
+        const void* gamma, void* dx, float* dgamma, float* dbeta, int accumulate) {
+    const T* xx = static_cast<const T*>(x);
+    const T* dd = static_cast<const T*>(dy);
+    const T* gg = static_cast<const T*>(gamma);
+    T* out = static_cast<T*>(dx);
+    const bool vec = d % 4 == 0 && d <= 2048 && vec_ok<T>(x) && vec_ok<T>(dy) && vec_ok<T>(gamma) && vec_ok<T>(dx);
+    int64_t nparts;
+    if (vec) {
+        nparts = std::min<int64_t>(nott::ceil_div(rows, kWaves * kRowsInFlight), (int64_t)ctx->num_cu * 2);
+        nparts = std::max<int64_t>(nparts, 1);
+    } else {
+        nparts = rows;
+    }
+    float* partial = static_cast<float*>(nott::workspace(ctx, sizeof(float) * 2 * (size_t)d * (size_t)nparts));
+    if (!partial) return NOTT_ERR_ALLOC;
+    const dim3 grid((unsigned)nparts);
+    const size_t lds = sizeof(float) * kWaves * 2 * (size_t)d;
+    if (vec && d <= 256)
+        hipLaunchKernelGGL((ln_bwd_kernel<T, 4>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+    else if (vec && d <= 512)
+        hipLaunchKernelGGL((ln_bwd_kernel<T, 8>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+    else if (vec && d <= 1024)
+        hipLaunchKernelGGL((ln_bwd_kernel<T, 16>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+    else if (vec)
+        hipLaunchKernelGGL((ln_bwd_kernel<T, 32>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+    else
+        hipLaunchKernelGGL(ln_bwd_generic<T>, grid, dim3(kThreads), 0, ctx->stream, xx, dd, mean, rstd, gg, out, partial, d);
+    if (dgamma || dbeta)
+        hipLaunchKernelGGL(col_reduce_kernel, dim3((unsigned)nott::ceil_div(d, 64), 2), dim3(kThreads), 0, ctx->stream,
+                           partial, nparts, d, dgamma, dbeta, accumulate);
+    return nott::launch_status(ctx, "layernorm_bwd");
+}
+
+}  // namespace
+
+extern "C" int nott_layernorm_fwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d, const void* x,
+                                  const void* gamma, const void* beta, double eps, void* y, float* mean, float* rstd) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && rows >= 0 && d > 0, "nott_layernorm_fwd: bad arguments");
+    if (rows == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && gamma && beta && y && mean && rstd, "nott_layernorm_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, rows, d, x, gamma, beta, (float)eps, y, mean, rstd)
+                             : fwd<bf16_t>(ctx, rows, d, x, gamma, beta, (float)eps, y, mean, rstd);
+}
+
+extern "C" int nott_layernorm_bwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d, const void* x,
+                                  const void* dy, const float* mean, const float* rstd, const void* gamma, void* dx,
+                                  float* dgamma, float* dbeta, int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && rows >= 0 && d > 0, "nott_layernorm_bwd: bad arguments");
+    NOTT_REQUIRE(ctx, rows == 0 || (x && dy && mean && rstd && gamma && dx), "nott_layernorm_bwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    if (rows == 0) {
+        // Σ over no rows: the parameter gradients are zero (or unchanged).
+        if (!accumulate) {
+            if (dgamma && nott_zero(ctx, sizeof(float) * d, dgamma) != NOTT_OK) return NOTT_ERR_HIP;
+            if (dbeta && nott_zero(ctx, sizeof(float) * d, dbeta) != NOTT_OK) return NOTT_ERR_HIP;
+        }
+        return NOTT_OK;
+    }
+    return dtype == NOTT_F32 ? bwd<float>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate)
+                             : bwd<bf16_t>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate);
+}

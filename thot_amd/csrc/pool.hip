@@ -1,0 +1,147 @@
+// MaxPool2d forward (values + int64 argmax) and backward (argmax routing), NCHW.
+//
+// Replaces torch::nn::MaxPool2d built by build_registered_layer(Owner&, const
+// PoolingDescriptor&, size_t) (reference layer/details/pooling.hpp:132-149),
+// i.e. ATen max_pool2d_with_indices and its backward.
+//   forward : window scan rows-then-columns from the first in-bounds tap; the
+//             index moves on a strictly greater value or on a NaN; argmax is
+//             the flat index ih·w + iw inside the (n, c) plane.
+//   backward: dx[argmax] += dy.  Computed as a gather: each input element
+//             sums the dy of the windows that cover it and chose it, in
+//             output scan order, so overlapping windows need no atomics and
+//             the fp32 sum order equals the reference's scatter order.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct PoolGeom {
+    int64_t h, w, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                               int64_t* __restrict__ argmax, int64_t planes,
+                                                               PoolGeom g) {
+    const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t per_plane = g.oh * g.ow;
+    if (o >= planes * per_plane) return;
+    const int64_t pl = o / per_plane;
+    const int64_t rem = o - pl * per_plane;
+    const int64_t oh = rem / g.ow, ow = rem - oh * g.ow;
+    const T* xp = x + pl * g.h * g.w;
+    int64_t ih0 = oh * g.sh - g.ph, iw0 = ow * g.sw - g.pw;
+    const int64_t ih1 = std::min<int64_t>(ih0 + (g.kh - 1) * g.dh + 1, g.h);
+    const int64_t iw1 = std::min<int64_t>(iw0 + (g.kw - 1) * g.dw + 1, g.w);
+    while (ih0 < 0) ih0 += g.dh;
+    while (iw0 < 0) iw0 += g.dw;
+    int64_t best = ih0 * g.w + iw0;
+    float bv = -INFINITY;
+    for (int64_t ih = ih0; ih < ih1; ih += g.dh)
+        for (int64_t iw = iw0; iw < iw1; iw += g.dw) {
+            const float v = Io<T>::ld(xp, ih * g.w + iw);
+            if (v > bv || v != v) {
+                bv = v;
+                best = ih * g.w + iw;
+            }
+        }
+    Io<T>::st(y, o, bv);
+    argmax[o] = best;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(const int64_t* __restrict__ argmax,
+                                                               const T* __restrict__ dy, T* __restrict__ dx,
+                                                               int64_t planes, PoolGeom g) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t per_plane = g.h * g.w;
+    if (i >= planes * per_plane) return;
+    const int64_t pl = i / per_plane;
+    const int64_t idx = i - pl * per_plane;
+    const int64_t ih = idx / g.w, iw = idx - ih * g.w;
+    // Output rows whose window can contain ih: oh·sh − ph ≤ ih ≤ oh·sh − ph + (kh−1)·dh.
+    const int64_t num_h = ih + g.ph - (g.kh - 1) * g.dh;
+    int64_t oh0 = num_h <= 0 ? 0 : (num_h + g.sh - 1) / g.sh;
+    int64_t oh1 = std::min<int64_t>((ih + g.ph) / g.sh, g.oh - 1);
+    const int64_t num_w = iw + g.pw - (g.kw - 1) * g.dw;
+    int64_t ow0 = num_w <= 0 ? 0 : (num_w + g.sw - 1) / g.sw;
+    int64_t ow1 = std::min<int64_t>((iw + g.pw) / g.sw, g.ow - 1);
+    const int64_t* ap = argmax + pl * g.oh * g.ow;
+    const T* gp = dy + pl * g.oh * g.ow;
+    float acc = 0.f;
+    for (int64_t oh = oh0; oh <= oh1; ++oh)
+        for (int64_t ow = ow0; ow <= ow1; ++ow) {
+            const int64_t o = oh * g.ow + ow;
+            if (ap[o] == idx) acc += Io<T>::ld(gp, o);
+        }
+    Io<T>::st(dx, i, acc);
+}
+
+int64_t pool_out(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d, int ceil_mode) {
+    int64_t num = in + 2 * p - d * (k - 1) - 1 + (ceil_mode ? s - 1 : 0);
+    int64_t out = (num >= 0 ? num / s : -((-num + s - 1) / s)) + 1;
+    if (ceil_mode && (out - 1) * s >= in + p) --out;
+    return out;
+}
+
+int check_desc(nott_ctx ctx, const nott_pool2d_desc* d, PoolGeom* g) {
+    NOTT_REQUIRE(ctx, d != nullptr, "pool: null descriptor");
+    NOTT_REQUIRE(ctx, d->layout == NOTT_NCHW, "pool: only NCHW is supported");
+    NOTT_REQUIRE(ctx, d->n >= 0 && d->c >= 0 && d->h > 0 && d->w > 0, "pool: bad input shape");
+    NOTT_REQUIRE(ctx, d->kh > 0 && d->kw > 0 && d->stride_h > 0 && d->stride_w > 0 && d->dil_h > 0 && d->dil_w > 0,
+                 "pool: kernel, stride and dilation must be positive");
+    NOTT_REQUIRE(ctx, d->pad_h >= 0 && d->pad_w >= 0 && 2 * d->pad_h <= d->kh && 2 * d->pad_w <= d->kw,
+                 "pool: pad should be at most half of the kernel size");
+    g->h = d->h; g->w = d->w; g->kh = d->kh; g->kw = d->kw;
+    g->sh = d->stride_h; g->sw = d->stride_w; g->ph = d->pad_h; g->pw = d->pad_w;
+    g->dh = d->dil_h; g->dw = d->dil_w;
+    g->oh = pool_out(d->h, d->kh, d->stride_h, d->pad_h, d->dil_h, d->ceil_mode);
+    g->ow = pool_out(d->w, d->kw, d->stride_w, d->pad_w, d->dil_w, d->ceil_mode);
+    NOTT_REQUIRE(ctx, g->oh > 0 && g->ow > 0, "pool: output size is too small");
+    return NOTT_OK;
+}
+
+}  // namespace
+
+extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x, void* y,
+                                  int64_t* argmax) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_maxpool2d_fwd: bad dtype");
+    PoolGeom g;
+    int st = check_desc(ctx, d, &g);
+    if (st != NOTT_OK) return st;
+    const int64_t planes = d->n * d->c, total = planes * g.oh * g.ow;
+    if (total == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && y && argmax, "nott_maxpool2d_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
+    if (dtype == NOTT_F32)
+        hipLaunchKernelGGL(maxpool_fwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const float*>(x), static_cast<float*>(y), argmax, planes, g);
+    else
+        hipLaunchKernelGGL(maxpool_fwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
+                           static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, planes, g);
+    return nott::launch_status(ctx, "maxpool_fwd");
+}
+
+extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const int64_t* argmax,
+                                  const void* dy, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_maxpool2d_bwd: bad dtype");
+    PoolGeom g;
+    int st = check_desc(ctx, d, &g);
+    if (st != NOTT_OK) return st;
+    const int64_t planes = d->n * d->c, total = planes * g.h * g.w;
+    if (total == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, argmax && dy && dx, "nott_maxpool2d_bwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
+    if (dtype == NOTT_F32)
+        hipLaunchKernelGGL(maxpool_bwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
+                           static_cast<const float*>(dy), static_cast<float*>(dx), planes, g);
+    else
+        hipLaunchKernelGGL(maxpool_bwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream, argmax,
+                           static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), planes, g);
+    return nott::launch_status(ctx, "maxpool_bwd");
+}
