@@ -1,0 +1,234 @@
+"""GPU parity of the MFMA kernels (Linear and Conv2d forward / dgrad / wgrad)
+against the CPU oracle, through the C ABI.  Same seeded inputs on both sides;
+bf16 inputs are rounded once and the oracle sees the rounded values.
+
+Shapes: the reference's golden conv cases (every stride / padding / dilation
+variant on the path), the small-CNN and ResNet-18
+layer shapes at reduced batch, and the standalone conv at full
+size through size-independent checks (per-image slices against the oracle,
+adjoint identities) plus a torch fp32 reference."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import check, dev, host, host_input
+from oracle_lib import conv_out, f32, rng
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = ["f32", "bf16"]
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from thot_amd import ops as _ops
+    assert torch.cuda.is_available()
+    return _ops
+
+
+# ------------------------------------------------------------------ linear
+LIN = [(1, 1, 1), (7, 5, 3), (64, 3136, 128), (64, 128, 10), (64, 512, 1000), (129, 70, 33), (256, 1024, 1024)]
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("m,kin,nout", LIN)
+def test_linear(ops, oracle, dt, m, kin, nout):
+    g = rng(11 + m + kin + nout)
+    x = host_input(g.standard_normal((m, kin)), dt)
+    w = host_input(g.standard_normal((nout, kin)) / math.sqrt(kin), dt)
+    b = f32(g.standard_normal(nout) * 0.1)
+    dy = host_input(g.standard_normal((m, nout)), dt)
+    y = ops.linear_fwd(dev(x, dt), dev(w, dt), dev(b))
+    dx, dw, db = ops.linear_bwd(dev(dy, dt), dev(x, dt), dev(w, dt))
+    torch.cuda.synchronize()
+    check(host(y), oracle.linear_fwd(x, w, b), dt, "linear y")
+    rdx, rdw, rdb = oracle.linear_bwd(dy, x, w)
+    check(host(dx), rdx, dt, "linear dx")
+    check(host(dw), rdw, "f32" if dt == "f32" else dt, "linear dw")
+    check(host(db), rdb, "f32" if dt == "f32" else dt, "linear db")
+
+
+def test_linear_golden(ops):
+    z = np.load(os.path.join(GOLD, "linear.npz"))
+    x, w, b, dy = (f32(z[k]) for k in ("x", "w", "b", "dy"))
+    y = ops.linear_fwd(dev(x), dev(w), dev(b))
+    dx, dw, db = ops.linear_bwd(dev(dy), dev(x), dev(w))
+    torch.cuda.synchronize()
+    check(host(y), z["y"], what="golden y")
+    check(host(dx), z["dx"], what="golden dx")
+    check(host(dw), z["dw"], what="golden dw")
+    check(host(db), z["db"], what="golden db")
+
+
+def test_linear_accumulate_and_partial_outputs(ops, oracle):
+    g = rng(3)
+    x, w, dy = f32(g.standard_normal((50, 40))), f32(g.standard_normal((30, 40))), f32(g.standard_normal((50, 30)))
+    dw0, db0 = f32(g.standard_normal((30, 40))), f32(g.standard_normal(30))
+    dwd, dbd = dev(dw0), dev(db0)
+    dx, _, _ = ops.linear_bwd(dev(dy), dev(x), dev(w), dw=dwd, db=dbd, accumulate=True)
+    _, dw2, db2 = ops.linear_bwd(dev(dy), dev(x), dev(w), need_dx=False)
+    torch.cuda.synchronize()
+    rdx, rdw, rdb = oracle.linear_bwd(dy, x, w)
+    check(host(dwd), dw0 + rdw, what="accumulated dw")
+    check(host(dbd), db0 + rdb, what="accumulated db")
+    check(host(dw2), rdw, what="dw without dx")
+    check(host(db2), rdb, what="db without dx")
+
+
+# -------------------------------------------------------------------- conv
+# (n, c, h, w, k, r, s, stride, pad, dil)
+CONV = [
+    (2, 3, 9, 9, 4, 3, 3, 1, 1, 1),            # 3x3 s1 p1
+    (2, 5, 11, 9, 6, 3, 3, 2, 1, 1),           # 3x3 s2 p1, odd sizes
+    (2, 3, 15, 15, 8, 7, 7, 2, 3, 1),          # ResNet stem 7x7 s2 p3
+    (2, 8, 10, 10, 16, 1, 1, 2, 0, 1),         # 1x1 s2 projection
+    (1, 4, 12, 10, 5, 3, 3, 1, 2, 2),          # dilation 2
+    (4, 1, 28, 28, 32, 3, 3, 1, 1, 1),         # configs[0] conv1 (batch 4)
+    (4, 32, 14, 14, 64, 3, 3, 1, 1, 1),        # configs[0] conv2 (batch 4)
+    (2, 64, 56, 56, 64, 3, 3, 1, 1, 1),        # ResNet stage 1
+    (2, 64, 56, 56, 128, 3, 3, 2, 1, 1),       # ResNet stage 2 entry
+    (2, 128, 28, 28, 128, 3, 3, 1, 1, 1),      # ResNet stage 2
+    (2, 256, 14, 14, 256, 3, 3, 1, 1, 1),      # ResNet stage 3
+    (2, 256, 14, 14, 512, 1, 1, 2, 0, 1),      # ResNet stage 4 projection
+    (2, 512, 7, 7, 512, 3, 3, 1, 1, 1),        # ResNet stage 4
+]
+
+
+def _desc(ops, case, layout=0):
+    n, c, h, w, k, r, s, st, pad, dil = case
+    return ops.conv_desc((n, c, h, w), (k, c, r, s), stride=(st, st), padding=(pad, pad), dilation=(dil, dil),
+                         layout=layout)
+
+
+def _inputs(case, dt, seed):
+    n, c, h, w, k, r, s, st, pad, dil = case
+    p, q = conv_out(h, r, st, pad, dil), conv_out(w, s, st, pad, dil)
+    g = rng(seed)
+    x = host_input(g.standard_normal((n, c, h, w)), dt)
+    wt = host_input(g.standard_normal((k, c, r, s)) / math.sqrt(c * r * s), dt)
+    b = f32(g.standard_normal(k) * 0.1)
+    dy = host_input(g.standard_normal((n, k, p, q)), dt)
+    return x, wt, b, dy
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", CONV, ids=lambda c: "n{}c{}h{}w{}k{}r{}s{}st{}p{}d{}".format(*c))
+def test_conv(ops, oracle, dt, case):
+    d = _desc(ops, case)
+    x, w, b, dy = _inputs(case, dt, sum(case))
+    y = ops.conv2d_fwd(dev(x, dt), dev(w, dt), dev(b), d)
+    dx = ops.conv2d_bwd_data(dev(dy, dt), dev(w, dt), d)
+    dw, db = ops.conv2d_bwd_weight(dev(x, dt), dev(dy, dt), d, need_db=True)
+    torch.cuda.synchronize()
+    check(host(y), oracle.conv2d_fwd(d, x, w, b), dt, "conv y")
+    check(host(dx), oracle.conv2d_bwd_data(d, dy, w), dt, "conv dx")
+    rdw, rdb = oracle.conv2d_bwd_weight(d, x, dy)
+    check(host(dw), rdw, dt, "conv dw")
+    check(host(db), rdb, dt, "conv db")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", [CONV[0], CONV[1], CONV[2], CONV[6]], ids=lambda c: "n{}c{}h{}w{}k{}".format(*c[:5]))
+def test_conv_nhwc(ops, oracle, dt, case):
+    """Channels-last layout (the reference's ChannelsLast mode) gives the same numbers."""
+    d = _desc(ops, case, layout=1)
+    dn = _desc(ops, case, layout=0)
+    x, w, b, dy = _inputs(case, dt, 7 + sum(case))
+    nhwc = lambda a: np.ascontiguousarray(a.transpose(0, 2, 3, 1))
+    y = ops.conv2d_fwd(dev(nhwc(x), dt), dev(w, dt), dev(b), d)
+    dx = ops.conv2d_bwd_data(dev(nhwc(dy), dt), dev(w, dt), d)
+    dw, db = ops.conv2d_bwd_weight(dev(nhwc(x), dt), dev(nhwc(dy), dt), d, need_db=True)
+    torch.cuda.synchronize()
+    check(host(y), nhwc(oracle.conv2d_fwd(dn, x, w, b)), dt, "nhwc y")
+    check(host(dx), nhwc(oracle.conv2d_bwd_data(dn, dy, w)), dt, "nhwc dx")
+    rdw, rdb = oracle.conv2d_bwd_weight(dn, x, dy)
+    check(host(dw), rdw, dt, "nhwc dw")
+    check(host(db), rdb, dt, "nhwc db")
+
+
+@pytest.mark.parametrize("name", ["conv3x3_s1p1_bias", "conv3x3_s2p1", "conv7x7_s2p3", "conv1x1_s2",
+                                  "conv3x3_dil2_rect"])
+def test_conv_golden(ops, name):
+    """The HIP path against vectors written by the reference's own Conv2d module."""
+    z = np.load(os.path.join(GOLD, name + ".npz"))
+    n, c, h, w, k, r, s, sh, sw, ph, pw, dh, dw_ = (int(v) for v in z["desc"])
+    d = ops.conv_desc((n, c, h, w), (k, c, r, s), stride=(sh, sw), padding=(ph, pw), dilation=(dh, dw_))
+    b = dev(f32(z["b"])) if "b" in z else None
+    y = ops.conv2d_fwd(dev(f32(z["x"])), dev(f32(z["w"])), b, d)
+    dx = ops.conv2d_bwd_data(dev(f32(z["dy"])), dev(f32(z["w"])), d)
+    dwt, dbt = ops.conv2d_bwd_weight(dev(f32(z["x"])), dev(f32(z["dy"])), d, need_db="db" in z)
+    torch.cuda.synchronize()
+    check(host(y), z["y"], what=f"{name} y")
+    check(host(dx), z["dx"], what=f"{name} dx")
+    check(host(dwt), z["dw"], what=f"{name} dw")
+    if "db" in z:
+        check(host(dbt), z["db"], what=f"{name} db")
+
+
+def test_conv_accumulate(ops, oracle):
+    case = CONV[0]
+    d = _desc(ops, case)
+    x, w, b, dy = _inputs(case, "f32", 99)
+    g = rng(5)
+    dw0, db0 = f32(g.standard_normal(w.shape)), f32(g.standard_normal(w.shape[0]))
+    dwd, dbd = dev(dw0), dev(db0)
+    ops.conv2d_bwd_weight(dev(x), dev(dy), d, dw=dwd, db=dbd, accumulate=True)
+    torch.cuda.synchronize()
+    rdw, rdb = oracle.conv2d_bwd_weight(d, x, dy)
+    check(host(dwd), dw0 + rdw, what="accumulated dw")
+    check(host(dbd), db0 + rdb, what="accumulated db")
+
+
+def test_conv_rejects_bad_descriptors(ops):
+    from thot_amd._abi import NottInvalidArgument
+    x = torch.zeros((1, 2, 5, 5), device="cuda")
+    w = torch.zeros((3, 2, 3, 3), device="cuda")
+    d = ops.conv_desc((1, 2, 5, 5), (3, 2, 3, 3), padding=(1, 1))
+    d.groups = 2
+    with pytest.raises(NottInvalidArgument):
+        ops.conv2d_fwd(x, w, None, d)
+    d = ops.conv_desc((1, 2, 5, 5), (3, 2, 3, 3), stride=(0, 1))
+    with pytest.raises((NottInvalidArgument, ZeroDivisionError)):
+        ops.conv2d_fwd(x, w, None, d)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_conv_bwd_full_size_config(ops, oracle, dt):
+    """configs[1] at full size (N=128, 64->128, 56x56, 3x3 s1 p1).
+
+    dgrad: images 0 and 127 against the oracle (dgrad is per image).
+    wgrad: against torch's fp32 convolution backward on the same (rounded)
+    inputs, plus the adjoint identity <dy, conv(x, w)> = <w, wgrad(x, dy)>
+    = <x, dgrad(dy, w)> in float64."""
+    N, C, K, H = 128, 64, 128, 56
+    d = ops.conv_desc((N, C, H, H), (K, C, 3, 3), padding=(1, 1))
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    x = torch.randn((N, C, H, H), generator=gen, device="cuda").to(tdt)
+    w = (torch.randn((K, C, 3, 3), generator=gen, device="cuda") / math.sqrt(C * 9)).to(tdt)
+    dy = torch.randn((N, K, H, H), generator=gen, device="cuda").to(tdt)
+    dx = ops.conv2d_bwd_data(dy, w, d)
+    dw, _ = ops.conv2d_bwd_weight(x, dy, d)
+    torch.cuda.synchronize()
+    d1 = ops.conv_desc((1, C, H, H), (K, C, 3, 3), padding=(1, 1))
+    wh = host(w)
+    for i in (0, N - 1):
+        check(host(dx[i:i + 1]), oracle.conv2d_bwd_data(d1, host(dy[i:i + 1]), wh), dt, f"dx image {i}")
+    # torch fp32 reference for the batch-summed weight gradient
+    xf, dyf = x.float(), dy.float()
+    ref_dw = torch.nn.grad.conv2d_weight(xf, (K, C, 3, 3), dyf, padding=1)
+    check(host(dw), host(ref_dw), dt, "dw vs torch fp32")
+    # adjoint identities in float64
+    xd, wd, dyd = x.double(), w.double(), dy.double()
+    y = torch.nn.functional.conv2d(xd, wd, padding=1)
+    lhs = float((y * dyd).sum())
+    via_w = float((wd * dw.double()).sum())
+    via_x = float((xd * dx.double()).sum())
+    scale = float(torch.sqrt((y * y).sum() * (dyd * dyd).sum()))
+    tol = 1e-6 if dt == "f32" else 2e-3
+    assert abs(via_w - lhs) <= tol * scale, (via_w, lhs)
+    assert abs(via_x - lhs) <= tol * scale, (via_x, lhs)

@@ -181,3 +181,25 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     __syncthreads();
     return t;
 }
+
+// Unsigned 32-bit division by a runtime-invariant divisor via multiply-high
+// (Granlund & Montgomery 1994): q = (mulhi(n, magic) + n) >> shift, exact for
+// every n < 2^32.  Used by the implicit-GEMM index decompositions.
+struct FastDiv {
+    uint32_t d = 1, magic = 0, shift = 0;
+    FastDiv() = default;
+    explicit FastDiv(uint32_t div) : d(div) {
+        uint32_t l = 0;
+        while (l < 32 && (uint64_t(1) << l) < div) ++l;
+        shift = l;
+        magic = (uint32_t)(((uint64_t(1) << 32) * ((uint64_t(1) << l) - div)) / div + 1);
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const {
+        const uint64_t hi = ((uint64_t)n * magic) >> 32;
+        return (uint32_t)((hi + n) >> shift);
+    }
+    __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+        q = div(n);
+        r = n - q * d;
+    }
+};

@@ -1,0 +1,395 @@
+// Conv2d forward, dgrad and wgrad as implicit GEMMs on the MFMA engine
+// (any kernel size, stride, padding, dilation; NCHW or NHWC; groups = 1).
+//
+// Replaces the autograd node of torch::nn::Conv2d built by
+// build_registered_layer(Owner&, const Conv2dDescriptor&, size_t) (reference
+// layer/details/conv.hpp:140-191, module created at :177), i.e. ATen
+// convolution and convolution_backward:
+//   fwd  : y[n,k,p,q]  = b[k] + Σ_{c,r,s} w[k,c,r,s]·x[n,c,p·sh−ph+r·dh, q·sw−pw+s·dw]
+//   dgrad: dx[n,c,h,w] = Σ_{k,r,s} w[k,c,r,s]·dy[n,k,(h+ph−r·dh)/sh,(w+pw−s·dw)/sw]
+//          (terms whose division is inexact or out of range drop out)
+//   wgrad: dw[k,c,r,s] = Σ_{n,p,q} dy[n,k,p,q]·x[n,c,p·sh−ph+r·dh, q·sw−pw+s·dw]
+//   db[k]              = Σ_{n,p,q} dy[n,k,p,q]
+// GEMM views: fwd M = n·p·q, N = k, K = c·r·s; dgrad M = n·h·w, N = c,
+// K = k·r·s; wgrad M = k, N = c·r·s, K = n·p·q (split-K).  The 3×3 stride-1
+// shapes that dominate the configs go to the specialised kernels in
+// conv3x3.hip when they apply.
+#include "gemm.hpp"
+#include "conv_fast.hpp"
+
+namespace {
+
+using namespace nott::gemm;
+using ::FastDiv;
+
+struct Geom {
+    int32_t n, c, h, w, k, r, s, p, q;
+    int32_t sh, sw, ph, pw, dh, dw;
+    int32_t nhwc;
+    FastDiv fd_pq, fd_q, fd_rs, fd_s, fd_hw, fd_w, fd_sh, fd_sw;
+};
+
+Geom make_geom(const nott_conv2d_desc* d, int64_t p, int64_t q) {
+    Geom g;
+    g.n = (int32_t)d->n; g.c = (int32_t)d->c; g.h = (int32_t)d->h; g.w = (int32_t)d->w;
+    g.k = (int32_t)d->k; g.r = (int32_t)d->r; g.s = (int32_t)d->s; g.p = (int32_t)p; g.q = (int32_t)q;
+    g.sh = (int32_t)d->stride_h; g.sw = (int32_t)d->stride_w; g.ph = (int32_t)d->pad_h; g.pw = (int32_t)d->pad_w;
+    g.dh = (int32_t)d->dil_h; g.dw = (int32_t)d->dil_w;
+    g.nhwc = d->layout == NOTT_NHWC;
+    g.fd_pq = FastDiv((uint32_t)(p * q));
+    g.fd_q = FastDiv((uint32_t)q);
+    g.fd_rs = FastDiv((uint32_t)(d->r * d->s));
+    g.fd_s = FastDiv((uint32_t)d->s);
+    g.fd_hw = FastDiv((uint32_t)(d->h * d->w));
+    g.fd_w = FastDiv((uint32_t)d->w);
+    g.fd_sh = FastDiv((uint32_t)d->stride_h);
+    g.fd_sw = FastDiv((uint32_t)d->stride_w);
+    return g;
+}
+
+__device__ __forceinline__ int64_t x_index(const Geom& g, int32_t n, int32_t c, int32_t h, int32_t w) {
+    return g.nhwc ? (((int64_t)n * g.h + h) * g.w + w) * g.c + c : (((int64_t)n * g.c + c) * g.h + h) * g.w + w;
+}
+__device__ __forceinline__ int64_t y_index(const Geom& g, int32_t n, int32_t k, int32_t p, int32_t q) {
+    return g.nhwc ? (((int64_t)n * g.p + p) * g.q + q) * g.k + k : (((int64_t)n * g.k + k) * g.p + p) * g.q + q;
+}
+
+// fwd A: R(m = (n,p,q), kk = (c,r,s)) = x[n, c, p·sh−ph+r·dh, q·sw−pw+s·dw].
+template <typename T>
+struct FwdALoader {
+    static constexpr bool kRowFast = true;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* x;
+    Geom g;
+    int64_t rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t m, int64_t k0) const {
+        T v[E];
+        uint32_t n = 0, pq = 0, p = 0, q = 0;
+        if (m < rows) {
+            g.fd_pq.divmod((uint32_t)m, n, pq);
+            g.fd_q.divmod(pq, p, q);
+        }
+        const int32_t h0 = (int32_t)p * g.sh - g.ph, w0 = (int32_t)q * g.sw - g.pw;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            T val = T(0);
+            const int64_t kk = k0 + e;
+            if (m < rows && kk < K) {
+                uint32_t c, rs, r, s;
+                g.fd_rs.divmod((uint32_t)kk, c, rs);
+                g.fd_s.divmod(rs, r, s);
+                const int32_t h = h0 + (int32_t)r * g.dh, w = w0 + (int32_t)s * g.dw;
+                if (h >= 0 && h < g.h && w >= 0 && w < g.w) val = x[x_index(g, n, c, h, w)];
+            }
+            v[e] = val;
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+// y[n,k,p,q] = acc + b[k]
+template <typename T>
+struct FwdStore {
+    T* y;
+    const float* b;
+    Geom g;
+    int64_t M;
+    __device__ __forceinline__ void store(int64_t m, int64_t kout, float v) const {
+        if (m >= M || kout >= g.k) return;
+        uint32_t n, pq, p, q;
+        g.fd_pq.divmod((uint32_t)m, n, pq);
+        g.fd_q.divmod(pq, p, q);
+        if (b) v += b[kout];
+        Io<T>::st(y, y_index(g, n, (int32_t)kout, p, q), v);
+    }
+};
+
+// dgrad A: R(m = (n,h,w), kk = (k,r,s)) = dy[n, k, p, q] when h+ph−r·dh = p·sh
+// and w+pw−s·dw = q·sw exactly, with p, q in range; else 0.
+template <typename T>
+struct DgradALoader {
+    static constexpr bool kRowFast = true;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* dy;
+    Geom g;
+    int64_t rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t m, int64_t k0) const {
+        T v[E];
+        uint32_t n = 0, hw = 0, h = 0, w = 0;
+        if (m < rows) {
+            g.fd_hw.divmod((uint32_t)m, n, hw);
+            g.fd_w.divmod(hw, h, w);
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            T val = T(0);
+            const int64_t kk = k0 + e;
+            if (m < rows && kk < K) {
+                uint32_t ko, rs, r, s;
+                g.fd_rs.divmod((uint32_t)kk, ko, rs);
+                g.fd_s.divmod(rs, r, s);
+                const int32_t ph = (int32_t)h + g.ph - (int32_t)r * g.dh;
+                const int32_t pw = (int32_t)w + g.pw - (int32_t)s * g.dw;
+                if (ph >= 0 && pw >= 0) {
+                    uint32_t p, remh, q, remw;
+                    g.fd_sh.divmod((uint32_t)ph, p, remh);
+                    g.fd_sw.divmod((uint32_t)pw, q, remw);
+                    if (remh == 0 && remw == 0 && (int32_t)p < g.p && (int32_t)q < g.q)
+                        val = dy[y_index(g, n, (int32_t)ko, p, q)];
+                }
+            }
+            v[e] = val;
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+// dgrad B: R(row = c, kk = (k,r,s)) = w[k, c, r, s].
+template <typename T>
+struct DgradBLoader {
+    static constexpr bool kRowFast = true;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* w;
+    Geom g;
+    int64_t rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t c, int64_t k0) const {
+        T v[E];
+        const int32_t rs_total = g.r * g.s;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int64_t kk = k0 + e;
+            T val = T(0);
+            if (c < rows && kk < K) {
+                uint32_t ko, rs;
+                g.fd_rs.divmod((uint32_t)kk, ko, rs);
+                val = w[((int64_t)ko * g.c + c) * rs_total + rs];
+            }
+            v[e] = val;
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+template <typename T>
+struct DgradStore {
+    T* dx;
+    Geom g;
+    int64_t M;
+    __device__ __forceinline__ void store(int64_t m, int64_t c, float v) const {
+        if (m >= M || c >= g.c) return;
+        uint32_t n, hw, h, w;
+        g.fd_hw.divmod((uint32_t)m, n, hw);
+        g.fd_w.divmod(hw, h, w);
+        Io<T>::st(dx, x_index(g, n, (int32_t)c, h, w), v);
+    }
+};
+
+// wgrad A: R(row = k, kk = (n,p,q)) = dy[n, k, p, q].
+template <typename T>
+struct WgradALoader {
+    static constexpr bool kRowFast = false;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* dy;
+    Geom g;
+    int64_t rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t ko, int64_t k0) const {
+        T v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int64_t kk = k0 + e;
+            T val = T(0);
+            if (ko < rows && kk < K) {
+                uint32_t n, pq, p, q;
+                g.fd_pq.divmod((uint32_t)kk, n, pq);
+                g.fd_q.divmod(pq, p, q);
+                val = dy[y_index(g, n, (int32_t)ko, p, q)];
+            }
+            v[e] = val;
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+// wgrad B: R(row = (c,r,s), kk = (n,p,q)) = x[n, c, p·sh−ph+r·dh, q·sw−pw+s·dw].
+template <typename T>
+struct WgradBLoader {
+    static constexpr bool kRowFast = false;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* x;
+    Geom g;
+    int64_t rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t col, int64_t k0) const {
+        T v[E];
+        uint32_t c = 0, rs = 0, r = 0, s = 0;
+        if (col < rows) {
+            g.fd_rs.divmod((uint32_t)col, c, rs);
+            g.fd_s.divmod(rs, r, s);
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int64_t kk = k0 + e;
+            T val = T(0);
+            if (col < rows && kk < K) {
+                uint32_t n, pq, p, q;
+                g.fd_pq.divmod((uint32_t)kk, n, pq);
+                g.fd_q.divmod(pq, p, q);
+                const int32_t h = (int32_t)p * g.sh - g.ph + (int32_t)r * g.dh;
+                const int32_t w = (int32_t)q * g.sw - g.pw + (int32_t)s * g.dw;
+                if (h >= 0 && h < g.h && w >= 0 && w < g.w) val = x[x_index(g, n, c, h, w)];
+            }
+            v[e] = val;
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+// dw[k][crs] fp32, row-major = KCRS.
+struct WgradStore {
+    float* dw;
+    int64_t M, N;
+    int accumulate;
+    __device__ __forceinline__ void store(int64_t ko, int64_t crs, float v) const {
+        if (ko >= M || crs >= N) return;
+        float* p = dw + ko * N + crs;
+        *p = accumulate ? *p + v : v;
+    }
+};
+
+// db[k] = Σ_{n,p,q} dy[n,k,p,q]; one workgroup per output channel,
+// deterministic order.
+template <typename T>
+__global__ __launch_bounds__(256) void conv_db_kernel(const T* __restrict__ dy, Geom g, float* __restrict__ db,
+                                                      int accumulate) {
+    __shared__ float red[4];
+    const int32_t ko = blockIdx.x;
+    const int64_t pq = (int64_t)g.p * g.q;
+    float s = 0.f;
+    for (int32_t n = 0; n < g.n; ++n) {
+        for (int64_t i = threadIdx.x; i < pq; i += 256) {
+            const int64_t idx = g.nhwc ? ((int64_t)n * pq + i) * g.k + ko : ((int64_t)n * g.k + ko) * pq + i;
+            s += Io<T>::ld(dy, idx);
+        }
+    }
+    s = block_sum<4>(s, red);
+    if (threadIdx.x == 0) db[ko] = accumulate ? db[ko] + s : s;
+}
+
+int64_t out_size(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d) { return (in + 2 * p - d * (k - 1) - 1) / s + 1; }
+
+int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) {
+    NOTT_REQUIRE(ctx, d != nullptr, "conv2d: null descriptor");
+    NOTT_REQUIRE(ctx, d->groups == 1, "conv2d: groups must be 1");
+    NOTT_REQUIRE(ctx, d->layout == NOTT_NCHW || d->layout == NOTT_NHWC, "conv2d: bad layout");
+    NOTT_REQUIRE(ctx, d->n >= 0 && d->c > 0 && d->h > 0 && d->w > 0 && d->k > 0 && d->r > 0 && d->s > 0,
+                 "conv2d: bad shape");
+    NOTT_REQUIRE(ctx, d->stride_h > 0 && d->stride_w > 0 && d->dil_h > 0 && d->dil_w > 0 && d->pad_h >= 0 &&
+                          d->pad_w >= 0,
+                 "conv2d: stride and dilation must be positive, padding non-negative");
+    *p = out_size(d->h, d->r, d->stride_h, d->pad_h, d->dil_h);
+    *q = out_size(d->w, d->s, d->stride_w, d->pad_w, d->dil_w);
+    NOTT_REQUIRE(ctx, *p > 0 && *q > 0, "conv2d: kernel larger than padded input");
+    // 32-bit index decompositions inside the kernels.
+    const int64_t big = std::max<int64_t>({d->n * d->c * d->h * d->w, d->n * d->k * *p * *q, d->k * d->c * d->r * d->s,
+                                           d->n * d->h * d->w, d->n * *p * *q});
+    NOTT_REQUIRE(ctx, big < (int64_t(1) << 31), "conv2d: tensor too large for 32-bit indexing");
+    return NOTT_OK;
+}
+
+template <typename T>
+int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* w, const float* b,
+        void* y) {
+    const Geom g = make_geom(d, p, q);
+    const int64_t M = d->n * p * q, K = d->c * d->r * d->s;
+    if (nott::conv_fast::fwd_applies(d, sizeof(T)))
+        return nott::conv_fast::fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
+    FwdALoader<T> la{static_cast<const T*>(x), g, M, K};
+    const bool v = ((uintptr_t)w % 16) == 0 && ((K * (int64_t)sizeof(T)) % 16) == 0;
+    RowKLoader<T> lb{static_cast<const T*>(w), K, d->k, K, v};
+    FwdStore<T> ep{static_cast<T*>(y), b, g, M};
+    return run<T>(ctx, la, lb, ep, M, d->k, K, 1);
+}
+
+template <typename T>
+int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* dy, const void* w, void* dx) {
+    if (nott::conv_fast::dgrad_applies(d, sizeof(T)))
+        return nott::conv_fast::dgrad<T>(ctx, d, static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx));
+    const Geom g = make_geom(d, p, q);
+    const int64_t M = d->n * d->h * d->w, K = d->k * d->r * d->s;
+    DgradALoader<T> la{static_cast<const T*>(dy), g, M, K};
+    DgradBLoader<T> lb{static_cast<const T*>(w), g, d->c, K};
+    DgradStore<T> ep{static_cast<T*>(dx), g, M};
+    return run<T>(ctx, la, lb, ep, M, d->c, K, 1);
+}
+
+template <typename T>
+int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* dy, float* dw,
+          float* db, int accumulate) {
+    const Geom g = make_geom(d, p, q);
+    if (dw) {
+        int st;
+        if (nott::conv_fast::wgrad_applies(d, sizeof(T))) {
+            st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
+        } else {
+            const int64_t M = d->k, N = d->c * d->r * d->s, K = d->n * p * q;
+            WgradALoader<T> la{static_cast<const T*>(dy), g, M, K};
+            WgradBLoader<T> lb{static_cast<const T*>(x), g, N, K};
+            WgradStore ep{dw, M, N, accumulate};
+            st = run<T>(ctx, la, lb, ep, M, N, K);
+        }
+        if (st != NOTT_OK) return st;
+    }
+    if (db) {
+        hipLaunchKernelGGL(conv_db_kernel<T>, dim3((unsigned)d->k), dim3(256), 0, ctx->stream,
+                           static_cast<const T*>(dy), g, db, accumulate);
+        return nott::launch_status(ctx, "conv_db");
+    }
+    return NOTT_OK;
+}
+
+}  // namespace
+
+extern "C" int nott_conv2d_fwd(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x, const void* w,
+                               const float* b, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_fwd: bad dtype");
+    int64_t p, q;
+    int st = check_desc(ctx, d, &p, &q);
+    if (st != NOTT_OK) return st;
+    if (d->n == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && w && y, "nott_conv2d_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, d, p, q, x, w, b, y) : fwd<bf16_t>(ctx, d, p, q, x, w, b, y);
+}
+
+extern "C" int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* dy,
+                                    const void* w, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_bwd_data: bad dtype");
+    int64_t p, q;
+    int st = check_desc(ctx, d, &p, &q);
+    if (st != NOTT_OK) return st;
+    if (d->n == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, dy && w && dx, "nott_conv2d_bwd_data: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? dgrad<float>(ctx, d, p, q, dy, w, dx) : dgrad<bf16_t>(ctx, d, p, q, dy, w, dx);
+}
+
+extern "C" int nott_conv2d_bwd_weight(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x,
+                                      const void* dy, float* dw, float* db, int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_bwd_weight: bad dtype");
+    int64_t p, q;
+    int st = check_desc(ctx, d, &p, &q);
+    if (st != NOTT_OK) return st;
+    nott::DeviceScope scope(ctx->device);
+    if (d->n == 0) {
+        if (!accumulate) {
+            if (dw && nott_zero(ctx, (int64_t)sizeof(float) * d->k * d->c * d->r * d->s, dw) != NOTT_OK) return NOTT_ERR_HIP;
+            if (db && nott_zero(ctx, (int64_t)sizeof(float) * d->k, db) != NOTT_OK) return NOTT_ERR_HIP;
+        }
+        return NOTT_OK;
+    }
+    NOTT_REQUIRE(ctx, dy && (!dw || x), "nott_conv2d_bwd_weight: null buffer");
+    return dtype == NOTT_F32 ? wgrad<float>(ctx, d, p, q, x, dy, dw, db, accumulate)
+                             : wgrad<bf16_t>(ctx, d, p, q, x, dy, dw, db, accumulate);
+}

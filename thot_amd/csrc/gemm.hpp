@@ -1,0 +1,314 @@
+// Generic MFMA GEMM engine for gfx950: C[M×N] = Σ_k A(m,k)·B(k,n), fp32
+// accumulate, operands fp32 or bf16.
+//
+// The engine owns tiling, LDS staging, the MFMA inner loop and split-K; the
+// caller supplies two loaders (how to read A(m,k) and B(k,n) from memory,
+// including implicit-im2col gathers for convolutions) and an epilogue (how
+// to write C(m,n)).  Specialised kernels (conv3x3.hip) handle the hot shapes;
+// this engine covers every shape, stride, padding and transpose correctly.
+//
+// Tile: BM×BN = 128×128 per 256-thread workgroup (4 waves as 2×2, each wave
+// 64×64 = 4×4 MFMA 16×16 tiles).  The k-step holds 64 bytes of k per row:
+// 32 bf16 (one v_mfma_f32_16x16x32_bf16) or 16 fp32 (four
+// v_mfma_f32_16x16x4f32).  LDS keeps both operands k-contiguous per row
+// ([row][k], 80-byte padded rows), double-buffered with register prefetch.
+//
+// MFMA operand layout (16×16 output tile): lane l supplies row (l % 16) of A
+// and column (l % 16) of B, each as the 16 bytes at k-byte-offset 16·(l/16).
+// A and B use the same lane→k assignment, so the product is exact whatever
+// order the instruction sums the 64-byte k-slice in.  Accumulator: lane l
+// holds column l % 16, rows 4·(l/16) + {0,1,2,3}.
+#pragma once
+
+#include "common.hpp"
+
+namespace nott {
+namespace gemm {
+
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int kThreads = 256;
+constexpr int kRowBytes = 64;        // k extent of one LDS row
+constexpr int kLdsStride = 80;       // padded LDS row pitch (bytes)
+constexpr int kChunksPerRow = kRowBytes / 16;
+
+template <typename T> struct KTraits;
+template <> struct KTraits<float> {
+    static constexpr int kElemsPerChunk = 4;
+    static constexpr int BK = 16;
+};
+template <> struct KTraits<bf16_t> {
+    static constexpr int kElemsPerChunk = 8;
+    static constexpr int BK = 32;
+};
+
+// Packs elements into a 16-byte chunk.
+template <typename T> struct Pack;
+template <> struct Pack<float> {
+    static __device__ __forceinline__ u32x4 make(const float (&v)[4]) {
+        u32x4 r;
+        r.x = __builtin_bit_cast(uint32_t, v[0]);
+        r.y = __builtin_bit_cast(uint32_t, v[1]);
+        r.z = __builtin_bit_cast(uint32_t, v[2]);
+        r.w = __builtin_bit_cast(uint32_t, v[3]);
+        return r;
+    }
+};
+template <> struct Pack<bf16_t> {
+    static __device__ __forceinline__ u32x4 make(const bf16_t (&v)[8]) {
+        u32x4 r;
+        r.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+        r.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+        r.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+        r.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+        return r;
+    }
+};
+
+// Raw element access in storage type (no conversion).
+template <typename T>
+__device__ __forceinline__ T raw_ld(const T* p, int64_t i) { return p[i]; }
+
+// ---------------------------------------------------------------------------
+// Loaders.  A loader describes an operand as R(row, k) for row in [0, rows)
+// and k in [0, K): for A, row = m; for B, row = n.  Out-of-range elements
+// read as zero.  Each loader provides
+//   static constexpr bool kRowFast   lane mapping: true -> consecutive lanes
+//                                    take consecutive rows (k-strided memory);
+//                                    false -> consecutive lanes walk k.
+//   u32x4 chunk(row, k0)             the 16-byte chunk of k0 .. k0+E-1.
+// ---------------------------------------------------------------------------
+
+// Row-major, k contiguous: R(row, k) = p[row·ld + k].
+template <typename T>
+struct RowKLoader {
+    static constexpr bool kRowFast = false;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* p;
+    int64_t ld, rows, K;
+    bool vec;  // p and ld allow aligned 16-byte loads
+    __device__ __forceinline__ u32x4 chunk(int64_t row, int64_t k0) const {
+        if (row < rows && vec && k0 + E <= K) return *reinterpret_cast<const u32x4*>(p + row * ld + k0);
+        T v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = (row < rows && k0 + e < K) ? p[row * ld + k0 + e] : T(0);
+        return Pack<T>::make(v);
+    }
+};
+
+// k-strided, row contiguous: R(row, k) = p[k·ld + row]  (a transposed operand).
+template <typename T>
+struct ColKLoader {
+    static constexpr bool kRowFast = true;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* p;
+    int64_t ld, rows, K;
+    __device__ __forceinline__ u32x4 chunk(int64_t row, int64_t k0) const {
+        T v[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = (row < rows && k0 + e < K) ? p[(k0 + e) * ld + row] : T(0);
+        return Pack<T>::make(v);
+    }
+};
+
+// Epilogue: row-major C[m·ldc + n] (fp32 or T), optional bias[n], optional
+// accumulate into existing fp32 values.
+template <typename TC>
+struct RowMajorStore {
+    TC* c;
+    int64_t ldc, M, N;
+    const float* bias;   // per column, nullable
+    int accumulate;
+    __device__ __forceinline__ void store(int64_t m, int64_t n, float v) const {
+        if (m >= M || n >= N) return;
+        if (bias) v += bias[n];
+        if (accumulate) v += Io<TC>::ld(c, m * ldc + n);
+        Io<TC>::st(c, m * ldc + n, v);
+    }
+};
+
+// Split-K partial store: ws[split][m][n] fp32 (dense M×N).
+struct PartialStore {
+    float* ws;
+    int64_t M, N;
+    __device__ __forceinline__ void store(int64_t m, int64_t n, float v) const {
+        if (m < M && n < N) ws[((int64_t)blockIdx.z * M + m) * N + n] = v;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// LDS fill: each of the 256 threads moves (BM·4)/256 = 2 chunks per operand.
+// ---------------------------------------------------------------------------
+template <class L>
+__device__ __forceinline__ void map_chunk(int i, int& row, int& ch) {
+    // i in [0, 512): chunk index inside the 128-row × 4-chunk tile.
+    if (L::kRowFast) {
+        row = i & 127;
+        ch = i >> 7;
+    } else {
+        row = i >> 2;
+        ch = i & 3;
+    }
+}
+
+template <class L>
+__device__ __forceinline__ void fetch(const L& ld, int64_t row0, int64_t k0, u32x4 (&r)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        int row, ch;
+        map_chunk<L>(threadIdx.x + j * kThreads, row, ch);
+        r[j] = ld.chunk(row0 + row, k0 + ch * L::E);
+    }
+}
+
+template <class L>
+__device__ __forceinline__ void stash(char* lds, const u32x4 (&r)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        int row, ch;
+        map_chunk<L>(threadIdx.x + j * kThreads, row, ch);
+        *reinterpret_cast<u32x4*>(lds + row * kLdsStride + ch * 16) = r[j];
+    }
+}
+
+// One 64-byte k-slice of MFMAs for this wave's 64×64 sub-tile.
+template <typename T>
+__device__ __forceinline__ void mma_slice(const char* la, const char* lb, int wm, int wn, f32x4 (&acc)[4][4]) {
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        a[i] = *reinterpret_cast<const u32x4*>(la + (wm * 64 + i * 16 + r16) * kLdsStride + kq * 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        b[j] = *reinterpret_cast<const u32x4*>(lb + (wn * 64 + j * 16 + r16) * kLdsStride + kq * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (sizeof(T) == 2) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[i]),
+                                                                    __builtin_bit_cast(bf16x8, b[j]), acc[i][j], 0, 0, 0);
+            } else {
+                const f32x4 af = __builtin_bit_cast(f32x4, a[i]);
+                const f32x4 bf = __builtin_bit_cast(f32x4, b[j]);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc[i][j], 0, 0, 0);
+            }
+        }
+}
+
+// grid: x = ceil(N/BN), y = ceil(M/BM), z = splits (k range per split = k_per_split).
+template <typename T, class LA, class LB, class EP>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(LA la, LB lb, EP ep, int64_t M, int64_t N, int64_t K,
+                                                        int64_t k_per_split) {
+    __shared__ __attribute__((aligned(16))) char lds[2][2][BM * kLdsStride];
+    constexpr int BK = KTraits<T>::BK;
+    const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+    const int64_t kb = (int64_t)blockIdx.z * k_per_split;
+    const int64_t ke = std::min<int64_t>(K, kb + k_per_split);
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wm = wid >> 1, wn = wid & 1;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
+    u32x4 ra[2], rb[2];
+    if (nk > 0) {
+        fetch(la, m0, kb, ra);
+        fetch(lb, n0, kb, rb);
+        stash<LA>(lds[0][0], ra);
+        stash<LB>(lds[0][1], rb);
+    }
+    __syncthreads();
+    for (int64_t t = 0; t < nk; ++t) {
+        const int cur = (int)(t & 1);
+        const bool more = t + 1 < nk;
+        if (more) {
+            // Loaders zero-fill past K; the split's own end is enforced by
+            // clamping through a bounded view of K.
+            const int64_t k1 = kb + (t + 1) * BK;
+            fetch(la, m0, k1, ra);
+            fetch(lb, n0, k1, rb);
+        }
+        mma_slice<T>(lds[cur][0], lds[cur][1], wm, wn, acc);
+        if (more) {
+            stash<LA>(lds[cur ^ 1][0], ra);
+            stash<LB>(lds[cur ^ 1][1], rb);
+        }
+        __syncthreads();
+    }
+    // Epilogue: lane holds column (lane % 16), rows 4·(lane/16)+e of each 16×16 tile.
+    const int col = lane & 15, rq = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ep.store(m0 + wm * 64 + i * 16 + rq + e, n0 + wn * 64 + j * 16 + col, acc[i][j][e]);
+}
+
+// Sums split-K partials ws[s][m][n] in split order and hands each total to
+// the epilogue (deterministic).
+template <class EP>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t splits, int64_t M,
+                                                            int64_t N, EP ep) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= M * N) return;
+    float s = 0.f;
+    for (int64_t z = 0; z < splits; ++z) s += ws[z * M * N + i];
+    ep.store(i / N, i % N, s);
+}
+
+// Picks a split count that gives the grid at least ~2 workgroups per CU
+// while keeping each split at least `min_k` long.
+inline int64_t pick_splits(int64_t tiles, int64_t K, int64_t num_cu, int64_t bk) {
+    int64_t want = std::max<int64_t>(1, (2 * num_cu + tiles - 1) / tiles);
+    const int64_t max_by_k = std::max<int64_t>(1, K / (8 * bk));
+    return std::min<int64_t>(want, max_by_k);
+}
+
+// Runs C = A·B with loaders la, lb and epilogue ep.  When the k range is
+// split, partials go to the context workspace and the reduce kernel applies
+// ep; otherwise the GEMM kernel applies ep directly.  Loaders must report
+// their true K (they zero-fill past it); splits cut K into equal ranges.
+template <typename T, class LA, class LB, class EP>
+int run(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64_t N, int64_t K, int64_t splits = 0) {
+    if (M <= 0 || N <= 0) return NOTT_OK;
+    constexpr int BK = KTraits<T>::BK;
+    const int64_t tn = ceil_div(N, BN), tm = ceil_div(M, BM);
+    if (tn > 0x7fffffff || tm > 65535) return fail(ctx, NOTT_ERR_UNSUPPORTED, "gemm: grid too large");
+    if (splits <= 0) splits = pick_splits(tn * tm, K, ctx->num_cu, BK);
+    splits = std::max<int64_t>(1, std::min<int64_t>(splits, 65535));
+    // Split boundaries on BK multiples so that a chunk never straddles two splits.
+    int64_t kps = ceil_div(ceil_div(K, splits), BK) * BK;
+    splits = std::max<int64_t>(1, ceil_div(K, kps));
+    if (K <= 0) {
+        kps = 0;
+        splits = 1;
+    }
+    if (splits == 1) {
+        hipLaunchKernelGGL((gemm_kernel<T, LA, LB, EP>), dim3((unsigned)tn, (unsigned)tm, 1), dim3(kThreads), 0,
+                           ctx->stream, la, lb, ep, M, N, K, std::max<int64_t>(kps, 1));
+        return launch_status(ctx, "gemm_kernel");
+    }
+    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(splits * M * N)));
+    if (!ws) return NOTT_ERR_ALLOC;
+    PartialStore ps{ws, M, N};
+    hipLaunchKernelGGL((gemm_kernel<T, LA, LB, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
+                       dim3(kThreads), 0, ctx->stream, la, lb, ps, M, N, K, kps);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, ctx->stream,
+                       ws, splits, M, N, ep);
+    return launch_status(ctx, "gemm_splitk");
+}
+
+}  // namespace gemm
+}  // namespace nott

@@ -1,0 +1,125 @@
+// Linear forward and backward on the MFMA GEMM engine.
+//
+// Replaces torch::nn::Linear as built by build_registered_layer(Owner&, const
+// FCDescriptor&, size_t) (reference layer/details/fc.hpp:32-49, module at :40)
+// and the q/k/v/out projections of MultiHeadAttentionImpl
+// (attention/details/head.hpp:38-41), i.e. ATen addmm / mm and their backward:
+//   y  = x·wᵀ + b         (NT: both operands k-contiguous)
+//   dx = dy·w             (NN: w is k-strided)
+//   dw = dyᵀ·x            (TN: both k-strided; split-K over rows)
+//   db = Σ_rows dy        (folded into the dw GEMM as an extra all-ones column)
+#include "gemm.hpp"
+
+namespace {
+
+using namespace nott::gemm;
+
+template <typename T>
+bool vec16(const void* p, int64_t ld) {
+    return ((uintptr_t)p % 16) == 0 && ((ld * (int64_t)sizeof(T)) % 16) == 0;
+}
+
+// B operand of dw with one extra virtual row of ones: R(row=i, k=m) = x[m·kin + i]
+// for i < kin and 1 for i == kin (that output column is db).
+template <typename T>
+struct ColKOnesLoader {
+    static constexpr bool kRowFast = true;
+    static constexpr int E = KTraits<T>::kElemsPerChunk;
+    const T* p;
+    int64_t ld, rows, K;   // rows = kin (the ones row is index `rows`)
+    bool ones;
+    __device__ __forceinline__ u32x4 chunk(int64_t row, int64_t k0) const {
+        T v[E];
+        const T one = sizeof(T) == 2 ? T(0x3f80) : T(1);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const bool ink = k0 + e < K;
+            if (row < rows) v[e] = ink ? p[(k0 + e) * ld + row] : T(0);
+            else v[e] = (ones && row == rows && ink) ? one : T(0);
+        }
+        return Pack<T>::make(v);
+    }
+};
+
+// dw[o][i] for i < kin, db[o] for i == kin.
+struct DwDbStore {
+    float* dw;
+    float* db;
+    int64_t nout, kin;
+    int accumulate;
+    __device__ __forceinline__ void store(int64_t o, int64_t i, float v) const {
+        if (o >= nout) return;
+        if (i < kin) {
+            if (!dw) return;
+            float* p = dw + o * kin + i;
+            *p = accumulate ? *p + v : v;
+        } else if (i == kin && db) {
+            db[o] = accumulate ? db[o] + v : v;
+        }
+    }
+};
+
+template <typename T>
+int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
+    const T* xp = static_cast<const T*>(x);
+    const T* wp = static_cast<const T*>(w);
+    RowKLoader<T> la{xp, kin, m, kin, vec16<T>(x, kin)};
+    RowKLoader<T> lb{wp, kin, nout, kin, vec16<T>(w, kin)};
+    RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
+    return run<T>(ctx, la, lb, ep, m, nout, kin, 1);
+}
+
+template <typename T>
+int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, const void* x, const void* w, void* dx,
+        float* dw, float* db, int accumulate) {
+    const T* dyp = static_cast<const T*>(dy);
+    if (dx) {
+        RowKLoader<T> la{dyp, nout, m, nout, vec16<T>(dy, nout)};
+        ColKLoader<T> lb{static_cast<const T*>(w), kin, kin, nout};
+        RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
+        const int st = run<T>(ctx, la, lb, ep, m, kin, nout, 1);
+        if (st != NOTT_OK) return st;
+    }
+    if (dw || db) {
+        ColKLoader<T> la{dyp, nout, nout, m};
+        ColKOnesLoader<T> lb{static_cast<const T*>(x), kin, kin, m, db != nullptr};
+        DwDbStore ep{dw, db, nout, kin, accumulate};
+        const int st = run<T>(ctx, la, lb, ep, nout, kin + 1, m);
+        if (st != NOTT_OK) return st;
+    }
+    return NOTT_OK;
+}
+
+}  // namespace
+
+extern "C" int nott_linear_fwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout, const void* x,
+                               const void* w, const float* b, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_linear_fwd: bad dtype");
+    NOTT_REQUIRE(ctx, m >= 0 && kin > 0 && nout > 0, "nott_linear_fwd: need m >= 0, kin > 0, nout > 0");
+    if (m == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && w && y, "nott_linear_fwd: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, m, kin, nout, x, w, b, y) : fwd<bf16_t>(ctx, m, kin, nout, x, w, b, y);
+}
+
+extern "C" int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout, const void* dy,
+                               const void* x, const void* w, void* dx, float* dw, float* db, int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_linear_bwd: bad dtype");
+    NOTT_REQUIRE(ctx, m >= 0 && kin > 0 && nout > 0, "nott_linear_bwd: need m >= 0, kin > 0, nout > 0");
+    NOTT_REQUIRE(ctx, dy != nullptr || m == 0, "nott_linear_bwd: null dy");
+    NOTT_REQUIRE(ctx, !dx || w, "nott_linear_bwd: dx needs w");
+    NOTT_REQUIRE(ctx, !(dw || db) || x || m == 0, "nott_linear_bwd: dw needs x");
+    nott::DeviceScope scope(ctx->device);
+    if (m == 0) {
+        // Empty batch: dx is empty; the parameter gradients sum over nothing.
+        if (!accumulate) {
+            if (dw && nott_zero(ctx, (int64_t)sizeof(float) * nout * kin, dw) != NOTT_OK) return NOTT_ERR_HIP;
+            if (db && nott_zero(ctx, (int64_t)sizeof(float) * nout, db) != NOTT_OK) return NOTT_ERR_HIP;
+        }
+        return NOTT_OK;
+    }
+    return dtype == NOTT_F32 ? bwd<float>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate)
+                             : bwd<bf16_t>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate);
+}

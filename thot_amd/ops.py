@@ -153,14 +153,15 @@ def zero_(t: torch.Tensor) -> torch.Tensor:
 
 # --------------------------------------------------------------- cross-entropy
 def softmax_xent_bwd(logits: torch.Tensor, labels: torch.Tensor, *, label_smoothing: float = 0.0,
-                     grad_scale: float = 1.0, with_loss: bool = True):
+                     grad_scale: float = 1.0, with_loss: bool = True, out: Optional[torch.Tensor] = None):
     """Returns (dlogits, loss) of mean softmax cross-entropy (ignore_index -100)."""
     _check(logits, "logits")
     if logits.dim() != 2:
         raise ValueError("logits must be [n, c]")
     n, c = logits.shape
     _check(labels, "labels", shape=(n,), dtype=torch.int64, device=logits.device)
-    dl = torch.empty_like(logits)
+    dl = torch.empty_like(logits) if out is None else out
+    _check(dl, "out", shape=logits.shape, dtype=logits.dtype, device=logits.device)
     loss = torch.empty((), dtype=torch.float32, device=logits.device) if with_loss else None
     _ctx_for(logits).call("nott_softmax_xent_bwd", nott_dtype(logits.dtype), n, c, _ptr(logits), _ptr(labels),
                           float(label_smoothing), float(grad_scale), _ptr(dl), _ptr(loss))
@@ -183,14 +184,15 @@ def layernorm_fwd(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps:
 
 def layernorm_bwd(x: torch.Tensor, dy: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor, gamma: torch.Tensor,
                   dgamma: Optional[torch.Tensor] = None, dbeta: Optional[torch.Tensor] = None,
-                  accumulate: bool = False):
+                  accumulate: bool = False, out: Optional[torch.Tensor] = None):
     _check(x, "x")
     rows, d = x.reshape(-1, x.shape[-1]).shape
     _check(dy, "dy", shape=x.shape, dtype=x.dtype, device=x.device)
     _check(mean, "mean", shape=(rows,), dtype=torch.float32, device=x.device)
     _check(rstd, "rstd", shape=(rows,), dtype=torch.float32, device=x.device)
     _check(gamma, "gamma", shape=(d,), dtype=x.dtype, device=x.device)
-    dx = torch.empty_like(x)
+    dx = torch.empty_like(x) if out is None else out
+    _check(dx, "out", shape=x.shape, dtype=x.dtype, device=x.device)
     if dgamma is None:
         dgamma = torch.empty(d, dtype=torch.float32, device=x.device)
     if dbeta is None:
@@ -370,11 +372,13 @@ def conv2d_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor], d: C
     return y
 
 
-def conv2d_bwd_data(dy: torch.Tensor, w: torch.Tensor, d: Conv2dDesc) -> torch.Tensor:
+def conv2d_bwd_data(dy: torch.Tensor, w: torch.Tensor, d: Conv2dDesc,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
     xs, ys = _conv_shapes(d)
     _check(dy, "dy", shape=ys)
     _check(w, "w", shape=(d.k, d.c, d.r, d.s), dtype=dy.dtype, device=dy.device)
-    dx = torch.empty(xs, dtype=dy.dtype, device=dy.device)
+    dx = torch.empty(xs, dtype=dy.dtype, device=dy.device) if out is None else out
+    _check(dx, "out", shape=xs, dtype=dy.dtype, device=dy.device)
     _ctx_for(dy).call("nott_conv2d_bwd_data", C.byref(d), nott_dtype(dy.dtype), _ptr(dy), _ptr(w), _ptr(dx))
     return dx
 
