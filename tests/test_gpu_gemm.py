@@ -95,6 +95,9 @@ CONV = [
     (2, 256, 14, 14, 256, 3, 3, 1, 1, 1),      # ResNet stage 3
     (2, 256, 14, 14, 512, 1, 1, 2, 0, 1),      # ResNet stage 4 projection
     (2, 512, 7, 7, 512, 3, 3, 1, 1, 1),        # ResNet stage 4
+    (3, 64, 5, 13, 64, 3, 3, 1, 1, 1),         # 3x3 tile spanning three images
+    (2, 32, 60, 60, 128, 3, 3, 1, 1, 1),       # widest row the 3x3 kernel takes
+    (5, 128, 7, 7, 192, 3, 3, 1, 1, 1),        # ragged last pixel tile
 ]
 
 
