@@ -327,7 +327,8 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
     const Geom g = make_geom(d, p, q);
     if (dw) {
         int st;
-        if (nott::conv_fast::wgrad_applies(d, sizeof(T))) {
+        const bool aligned = ((uintptr_t)x % 16) == 0 && ((uintptr_t)dy % 16) == 0;
+        if (aligned && nott::conv_fast::wgrad_applies(d, sizeof(T))) {
             st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
         } else {
             const int64_t M = d->k, N = d->c * d->r * d->s, K = d->n * p * q;

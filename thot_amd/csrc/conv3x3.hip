@@ -279,6 +279,252 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     return launch_status(ctx, "conv3x3_same");
 }
 
+
+// ---------------------------------------------------------------------------
+// wgrad: dw[k, c, r, s] = Σ_{n,h,w} dy[n,k,h,w] · x[n, c, h−1+r, w−1+s]
+//
+// GEMM with M = 64 output channels k, N = 64 input channels c × 9 taps and
+// the reduction over pixels.  Pixels live in "slots": image row h occupies
+// slots [h·P, h·P + W) and slots [h·P + W, (h+1)·P) stay zero (P = W + 1
+// rounded up to a power of two).  dy and x share the slot numbering, so a
+// tap (r, s) is the slot offset (r−1)·P + (s−1) into x, and every pixel that
+// falls off the image reads a zero slot.  The reduction runs over all slots
+// of a band of TH rows (padding slots carry dy = 0).
+//
+// Per band, LDS holds dy[64 k][TH·P slots] and x[64 c][(TH+2)·P slots] (one
+// halo row above and below), each channel row padded by 16–32 bytes so the
+// 16 channels one MFMA operand reads fall in distinct banks; the padding is
+// zero and doubles as the guard read by the s = 0 / s = 2 shifts.  A lane's
+// MFMA k-slice is 8 (bf16) / 4 (fp32) consecutive slots: s = 1 is an aligned
+// 16-byte LDS read, s = 0 and s = 2 realign the neighbouring aligned chunks by
+// one element in registers.  Wave w owns channels 16w..16w+15 for all 9 taps
+// and all 64 k: 36 accumulator tiles, 13 LDS reads per 36 MFMAs.
+//
+// The pixel range is split across workgroups (whole bands each); partial
+// sums go to ws[split][tap][k][c] and conv3x3_wgrad_reduce_kernel adds them
+// in split order (deterministic).
+// ---------------------------------------------------------------------------
+template <typename T> struct WgCfg;
+template <> struct WgCfg<bf16_t> { static constexpr int TH = 4, E = 8, KSTEP = 32; };
+template <> struct WgCfg<float> { static constexpr int TH = 2, E = 4, KSTEP = 16; };
+
+struct WgradParams {
+    int32_t n, c, k, h, w;
+    int32_t bands_per_img, total_bands, bands_per_split;
+    int32_t a_pitch, b_pitch;       // LDS bytes per channel row (dy, x)
+    int32_t kblocks;
+};
+
+// Shift a 16-byte chunk by one element toward lower slots (s = 2: slots base+1..)
+// or toward higher slots (s = 0: slots base−1..).
+template <typename T>
+__device__ __forceinline__ u32x4 shift_lo(const u32x4& cur, const u32x4& next);  // elements [1..E] of cur:next
+template <typename T>
+__device__ __forceinline__ u32x4 shift_hi(const u32x4& prev, const u32x4& cur);  // elements [E-1] of prev, [0..E-2] of cur
+template <>
+__device__ __forceinline__ u32x4 shift_lo<bf16_t>(const u32x4& c, const u32x4& n) {
+    return u32x4{__builtin_amdgcn_alignbit(c.y, c.x, 16), __builtin_amdgcn_alignbit(c.z, c.y, 16),
+                 __builtin_amdgcn_alignbit(c.w, c.z, 16), __builtin_amdgcn_alignbit(n.x, c.w, 16)};
+}
+template <>
+__device__ __forceinline__ u32x4 shift_hi<bf16_t>(const u32x4& p, const u32x4& c) {
+    return u32x4{__builtin_amdgcn_alignbit(c.x, p.w, 16), __builtin_amdgcn_alignbit(c.y, c.x, 16),
+                 __builtin_amdgcn_alignbit(c.z, c.y, 16), __builtin_amdgcn_alignbit(c.w, c.z, 16)};
+}
+template <>
+__device__ __forceinline__ u32x4 shift_lo<float>(const u32x4& c, const u32x4& n) { return u32x4{c.y, c.z, c.w, n.x}; }
+template <>
+__device__ __forceinline__ u32x4 shift_hi<float>(const u32x4& p, const u32x4& c) { return u32x4{p.w, c.x, c.y, c.z}; }
+
+template <typename T, int P>
+__global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                                   float* __restrict__ ws, WgradParams p) {
+    constexpr int TH = WgCfg<T>::TH, E = WgCfg<T>::E, KSTEP = WgCfg<T>::KSTEP;
+    constexpr int CPR = P / E;                          // 16-byte chunks per slot row
+    constexpr int A_TOTAL = 64 * TH * CPR, B_TOTAL = 64 * (TH + 2) * CPR;   // 16-byte chunks per band
+    constexpr int A_TASKS = (A_TOTAL + kThreads - 1) / kThreads;             // per thread
+    constexpr int B_TASKS = (B_TOTAL + kThreads - 1) / kThreads;
+    constexpr int RB = P * (int)sizeof(T);              // bytes per slot row
+    constexpr int KSTEPS = TH * P / KSTEP;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* lds_a = smem;
+    char* lds_b = smem + 64 * p.a_pitch + 16;           // 16-byte zero guard in front of channel 0
+
+    const int kb = blockIdx.y % p.kblocks, cb = blockIdx.y / p.kblocks;
+    const int32_t b0 = blockIdx.x * p.bands_per_split;
+    const int32_t b1 = min(p.total_bands, b0 + p.bands_per_split);
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int64_t plane = (int64_t)p.h * p.w;
+
+    // Zero the guard and the per-channel paddings of x (never written by the fill).
+    {
+        const int pad = p.b_pitch - (TH + 2) * RB;
+        for (int i = threadIdx.x; i < 64 * (pad / 16) + 1; i += kThreads) {
+            char* dst = (i == 0) ? (lds_b - 16) : (lds_b + ((i - 1) / (pad / 16)) * p.b_pitch + (TH + 2) * RB +
+                                                   ((i - 1) % (pad / 16)) * 16);
+            *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+
+    f32x4 acc[4][9];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 ra[A_TASKS], rb[B_TASKS];
+    auto fetch = [&](int32_t band) {
+        const int32_t img = band / p.bands_per_img;
+        const int32_t h0 = (band - img * p.bands_per_img) * TH;
+        const T* dyb = dy + ((int64_t)img * p.k + kb * 64) * plane;
+        const T* xb = x + ((int64_t)img * p.c + cb * 64) * plane;
+#pragma unroll
+        for (int j = 0; j < A_TASKS; ++j) {
+            const int t = threadIdx.x + j * kThreads;
+            const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
+            const int h = h0 + row;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if ((A_TOTAL % kThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h) v = *reinterpret_cast<const u32x4*>(dyb + kk * plane + (int64_t)h * p.w + ch * E);
+            ra[j] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < B_TASKS; ++j) {
+            const int t = threadIdx.x + j * kThreads;
+            const int ch = t % CPR, row = (t / CPR) % (TH + 2), cc = t / (CPR * (TH + 2));
+            const int h = h0 - 1 + row;
+            u32x4 v = u32x4{0u, 0u, 0u, 0u};
+            if ((B_TOTAL % kThreads == 0 || t < B_TOTAL) && ch * E < p.w && h >= 0 && h < p.h)
+                v = *reinterpret_cast<const u32x4*>(xb + cc * plane + (int64_t)h * p.w + ch * E);
+            rb[j] = v;
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int j = 0; j < A_TASKS; ++j) {
+            const int t = threadIdx.x + j * kThreads;
+            const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
+            if (A_TOTAL % kThreads == 0 || t < A_TOTAL)
+                *reinterpret_cast<u32x4*>(lds_a + kk * p.a_pitch + row * RB + ch * 16) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < B_TASKS; ++j) {
+            const int t = threadIdx.x + j * kThreads;
+            const int ch = t % CPR, row = (t / CPR) % (TH + 2), cc = t / (CPR * (TH + 2));
+            if (B_TOTAL % kThreads == 0 || t < B_TOTAL)
+                *reinterpret_cast<u32x4*>(lds_b + cc * p.b_pitch + row * RB + ch * 16) = rb[j];
+        }
+    };
+
+    if (b0 < b1) fetch(b0);
+    const char* arow = lds_a + r16 * p.a_pitch;                 // + mt·16·a_pitch
+    const char* brow = lds_b + (wid * 16 + r16) * p.b_pitch;
+    for (int32_t band = b0; band < b1; ++band) {
+        __syncthreads();
+        stash();
+        __syncthreads();
+        if (band + 1 < b1) fetch(band + 1);
+#pragma unroll 2
+        for (int t = 0; t < KSTEPS; ++t) {
+            const int slot = t * KSTEP + kq * E;
+            u32x4 a[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                a[mt] = *reinterpret_cast<const u32x4*>(arow + mt * 16 * p.a_pitch + slot * (int)sizeof(T));
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const char* bp = brow + (slot + r * P) * (int)sizeof(T);
+                const u32x4 prev = *reinterpret_cast<const u32x4*>(bp - 16);
+                const u32x4 cur = *reinterpret_cast<const u32x4*>(bp);
+                const u32x4 next = *reinterpret_cast<const u32x4*>(bp + 16);
+                const u32x4 b_s0 = shift_hi<T>(prev, cur);
+                const u32x4 b_s2 = shift_lo<T>(cur, next);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    mfma_chunk<T>(a[mt], b_s0, acc[mt][r * 3 + 0]);
+                    mfma_chunk<T>(a[mt], cur, acc[mt][r * 3 + 1]);
+                    mfma_chunk<T>(a[mt], b_s2, acc[mt][r * 3 + 2]);
+                }
+            }
+        }
+    }
+    // Partials: ws[split][tap][k][c]; lane column = channel, rows = k.
+    const int32_t c = cb * 64 + wid * 16 + r16;
+    float* wsp = ws + (int64_t)blockIdx.x * 9 * p.k * p.c;
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int32_t k = kb * 64 + mt * 16 + kq * 4 + e;
+                wsp[((int64_t)tap * p.k + k) * p.c + c] = acc[mt][tap][e];
+            }
+}
+
+// dw[k][c][tap] (+)= Σ_split ws[split][tap][k][c]
+__global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* __restrict__ ws, int32_t splits,
+                                                                   int32_t k, int32_t c, float* __restrict__ dw,
+                                                                   int accumulate) {
+    const int64_t per = (int64_t)9 * k * c;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // i = (tap·k + kk)·c + cc
+    if (i >= per) return;
+    float s = 0.f;
+    for (int32_t z = 0; z < splits; ++z) s += ws[z * per + i];
+    const int32_t cc = (int32_t)(i % c);
+    const int64_t rest = i / c;
+    const int32_t kk = (int32_t)(rest % k), tap = (int32_t)(rest / k);
+    float* o = dw + ((int64_t)kk * c + cc) * 9 + tap;
+    *o = accumulate ? *o + s : s;
+}
+
+template <typename T>
+int wg_pitch(int rows, int rb) {
+    int pitch = rows * rb + 16;
+    if (((pitch / 16) & 1) == 0) pitch += 16;   // odd multiple of 16 bytes: 16 rows in distinct banks
+    return pitch;
+}
+
+template <typename T, int P>
+int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
+    constexpr int TH = WgCfg<T>::TH;
+    constexpr int RB = P * (int)sizeof(T);
+    WgradParams p;
+    p.n = (int32_t)d->n; p.c = (int32_t)d->c; p.k = (int32_t)d->k; p.h = (int32_t)d->h; p.w = (int32_t)d->w;
+    p.bands_per_img = (p.h + TH - 1) / TH;
+    p.total_bands = p.n * p.bands_per_img;
+    p.kblocks = p.k / 64;
+    p.a_pitch = wg_pitch<T>(TH, RB);
+    p.b_pitch = wg_pitch<T>(TH + 2, RB);
+    const int tiles = p.kblocks * (p.c / 64);
+    // About one workgroup per CU in total.
+    int64_t splits = std::max<int64_t>(1, std::min<int64_t>(p.total_bands, ceil_div((int64_t)ctx->num_cu, tiles)));
+    p.bands_per_split = (int32_t)ceil_div(p.total_bands, splits);
+    splits = ceil_div(p.total_bands, p.bands_per_split);
+    const size_t lds = (size_t)64 * p.a_pitch + 16 + (size_t)64 * p.b_pitch;
+    if (lds > 160 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad: band does not fit in LDS");
+    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)splits * 9 * p.k * p.c));
+    if (!ws) return NOTT_ERR_ALLOC;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3x3_wgrad_kernel<T, P>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P>), dim3((unsigned)splits, (unsigned)tiles), dim3(kThreads), lds,
+                       ctx->stream, x, dy, ws, p);
+    const int64_t per = (int64_t)9 * p.k * p.c;
+    hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per, 256)), dim3(256), 0, ctx->stream, ws,
+                       (int32_t)splits, p.k, p.c, dw, accumulate);
+    return launch_status(ctx, "conv3x3_wgrad");
+}
+
+int wgrad_slot_pitch(int64_t w) {
+    int P = 8;
+    while (P < w + 1) P <<= 1;
+    return P;
+}
+
 }  // namespace
 
 bool fwd_applies(const nott_conv2d_desc* d, size_t elem) {
@@ -292,7 +538,11 @@ bool dgrad_applies(const nott_conv2d_desc* d, size_t elem) {
     return same_shape(d) && d->k % cc == 0 && d->c % kTileCo == 0;
 }
 
-bool wgrad_applies(const nott_conv2d_desc*, size_t) { return false; }
+bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {
+    // 16-byte aligned image rows, a slot row of at most 64, whole 64-channel blocks.
+    const int e = elem == 2 ? 8 : 4;
+    return same_shape(d) && d->w % e == 0 && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 64 == 0;
+}
 
 template <typename T>
 int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
@@ -306,8 +556,13 @@ int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* d
 }
 
 template <typename T>
-int wgrad(nott_ctx ctx, const nott_conv2d_desc*, const T*, const T*, float*, int) {
-    return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad");
+int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
+    switch (wgrad_slot_pitch(d->w)) {
+        case 8: return run_wgrad<T, 8>(ctx, d, x, dy, dw, accumulate);
+        case 16: return run_wgrad<T, 16>(ctx, d, x, dy, dw, accumulate);
+        case 32: return run_wgrad<T, 32>(ctx, d, x, dy, dw, accumulate);
+        default: return run_wgrad<T, 64>(ctx, d, x, dy, dw, accumulate);
+    }
 }
 
 template int fwd<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, const float*, float*);
