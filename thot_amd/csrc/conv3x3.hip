@@ -42,8 +42,12 @@ template <typename T> struct Chunk;
 template <> struct Chunk<float> { static constexpr int CC = 16, SUB = 4; };   // channels per chunk / per 16 B
 template <> struct Chunk<bf16_t> { static constexpr int CC = 32, SUB = 8; };
 
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
-__device__ __forceinline__ int lds_off(int row, int sub) { return row * kRowB + ((sub ^ swz(row)) << 4); }
+// LDS layout of [row][4 × 16-byte sub-chunks] tiles: rows are grouped by 16
+// and stored sub-chunk-major inside a group, so the 16 lanes of a quarter-wave
+// that read 16 consecutive rows at the same sub-chunk touch 16 distinct
+// 16-byte slots of 256-byte blocks (4 LDS cycles per ds_read_b128, measured
+// with SQ_LDS_BANK_CONFLICT = 0), whatever row the run starts at.
+__device__ __forceinline__ int lds_off(int row, int sub) { return ((row >> 4) << 10) + (sub << 8) + ((row & 15) << 4); }
 
 struct SameParams {
     int32_t n, cin, h, w, cout;
@@ -51,6 +55,7 @@ struct SameParams {
     int32_t npix;              // n·h·w
     int32_t in_rows;           // LDS rows reserved for the input tile
     int32_t remap;             // XCD-aware block remap active
+    int32_t vec_store;         // 16-byte output runs stay inside one image plane
     FastDiv fd_hw, fd_w, fd_w2, fd_h2;
 };
 
@@ -108,11 +113,36 @@ __device__ __forceinline__ void mfma_chunk(const u32x4& a, const u32x4& b, f32x4
     }
 }
 
-template <typename T>
+// Register transpose of a SUB×SUB block: in[i] holds SUB pixels of channel i,
+// out[j] holds SUB channels of pixel j.
+__device__ __forceinline__ void transpose_block(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+    // bf16: dword d of in[i] = pixels (2d, 2d+1); dword e of out[j] = channels (2e, 2e+1).
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t a = in[2 * e][d], b = in[2 * e + 1][d];
+            out[2 * d][e] = (a & 0xffffu) | (b << 16);
+            out[2 * d + 1][e] = (a >> 16) | (b & 0xffff0000u);
+        }
+    }
+}
+__device__ __forceinline__ void transpose_block(const u32x4 (&in)[4], u32x4 (&out)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = u32x4{in[0][j], in[1][j], in[2][j], in[3][j]};
+}
+
+template <typename T> struct VecTasks;
+template <> struct VecTasks<bf16_t> { static constexpr int VT = 2; };
+template <> struct VecTasks<float> { static constexpr int VT = 3; };
+
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
                                                                   const float* __restrict__ bias, T* __restrict__ out,
                                                                   SameParams p) {
     constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
+    constexpr int VT = VEC ? VecTasks<T>::VT : 1;
+    constexpr int WT = (9 * kTileCo * 4) / kThreads;    // weight chunks per thread per channel chunk
     extern __shared__ __attribute__((aligned(16))) char smem[];
     char* lds_in = smem;
     char* lds_w = smem + p.in_rows * kRowB;
@@ -133,7 +163,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     p.fd_hw.divmod((uint32_t)m_last, n1, hw1);
     p.fd_w.divmod(hw1, h1, w1_);
     const int32_t v_hi = (int32_t)n1 * (p.h + 2) + (int32_t)h1 + 2;  // halo row below the last pixel
-    const int32_t nrows = (v_hi - v_lo + 1) * p.w2;                   // LDS rows used by this tile
+    const int32_t nvr = v_hi - v_lo + 1;                              // padded image rows in the tile
+    const int32_t nrows = nvr * p.w2;                                 // LDS rows used by this tile
 
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
@@ -158,38 +189,94 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 
     const int32_t nchunks = p.cin / CC;
     const T* wblk = wp + (int64_t)cb * nchunks * 9 * kTileCo * CC;
-    for (int32_t cc = 0; cc < nchunks; ++cc) {
-        // ---- stage the input tile: task = (LDS row, 16-byte sub-chunk) ----
-        const int32_t ntask = nrows * 4;
-        for (int32_t t = threadIdx.x; t < ntask; t += kThreads) {
-            const int32_t sub = t / nrows;        // consecutive lanes -> consecutive pixels
-            const int32_t row = t - sub * nrows;
-            uint32_t vr, col;
-            p.fd_w2.divmod((uint32_t)row, vr, col);
-            uint32_t img, hh;
-            p.fd_h2.divmod((uint32_t)(v_lo + (int32_t)vr), img, hh);
-            const int32_t h = (int32_t)hh - 1, w = (int32_t)col - 1;
-            T v[SUB];
-            if (h >= 0 && h < p.h && w >= 0 && w < p.w && (int32_t)img < p.n) {
-                const T* src = in + (((int64_t)img * p.cin + cc * CC + sub * SUB) * p.h + h) * p.w + w;
+
+    // Vector fill: task = (w-chunk of SUB pixels, padded row, channel group of
+    // SUB): SUB 16-byte loads (one per channel), a register transpose, SUB
+    // 16-byte LDS writes (one per pixel).  Halo rows / columns are zeroed once.
+    const int32_t wchunks = p.w / SUB;
+    const int32_t ntask = nvr * wchunks * 4;
+    u32x4 rin[VT][SUB];
+    auto fetch = [&](int32_t cc) {
+        if constexpr (VEC) {
 #pragma unroll
-                for (int j = 0; j < SUB; ++j) v[j] = src[(int64_t)j * p.hw];
-            } else {
+            for (int j = 0; j < VT; ++j) {
+                const int32_t t = threadIdx.x + j * kThreads;
+                const int32_t wc = t % wchunks, rest = t / wchunks;
+                const int32_t vr = rest % nvr, cig = rest / nvr;
+                uint32_t img, hh;
+                p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
+                const int32_t h = (int32_t)hh - 1;
+                if (t < ntask && h >= 0 && h < p.h) {
+                    const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w + wc * SUB;
 #pragma unroll
-                for (int j = 0; j < SUB; ++j) v[j] = T(0);
+                    for (int i = 0; i < SUB; ++i) rin[j][i] = *reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw);
+                }
             }
-            *reinterpret_cast<u32x4*>(lds_in + lds_off(row, sub)) = pack_sub<T>(v);
         }
-        // ---- stage the weight slice: 9 taps × 64 co × 64 bytes ----
+    };
+    auto stash = [&](int32_t cc) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int j = 0; j < VT; ++j) {
+                const int32_t t = threadIdx.x + j * kThreads;
+                const int32_t wc = t % wchunks, rest = t / wchunks;
+                const int32_t vr = rest % nvr, cig = rest / nvr;
+                uint32_t img, hh;
+                p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
+                const int32_t h = (int32_t)hh - 1;
+                if (t < ntask && h >= 0 && h < p.h) {
+                    u32x4 tr[SUB];
+                    transpose_block(rin[j], tr);
+                    const int32_t row0 = vr * p.w2 + 1 + wc * SUB;
+#pragma unroll
+                    for (int i = 0; i < SUB; ++i) *reinterpret_cast<u32x4*>(lds_in + lds_off(row0 + i, cig)) = tr[i];
+                }
+            }
+        } else {
+            for (int32_t t = threadIdx.x; t < nrows * 4; t += kThreads) {
+                const int32_t sub = t / nrows;        // consecutive lanes -> consecutive pixels
+                const int32_t row = t - sub * nrows;
+                uint32_t vr, col;
+                p.fd_w2.divmod((uint32_t)row, vr, col);
+                uint32_t img, hh;
+                p.fd_h2.divmod((uint32_t)(v_lo + (int32_t)vr), img, hh);
+                const int32_t h = (int32_t)hh - 1, w = (int32_t)col - 1;
+                T v[SUB];
+                if (h >= 0 && h < p.h && w >= 0 && w < p.w && (int32_t)img < p.n) {
+                    const T* src = in + (((int64_t)img * p.cin + cc * CC + sub * SUB) * p.h + h) * p.w + w;
+#pragma unroll
+                    for (int j = 0; j < SUB; ++j) v[j] = src[(int64_t)j * p.hw];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < SUB; ++j) v[j] = T(0);
+                }
+                *reinterpret_cast<u32x4*>(lds_in + lds_off(row, sub)) = pack_sub<T>(v);
+            }
+        }
+        // Weights come from L2 (every workgroup reads the same slice): loaded
+        // here rather than held in registers across the MFMA loop.
         const u32x4* wsrc = reinterpret_cast<const u32x4*>(wblk + (int64_t)cc * 9 * kTileCo * CC);
+        u32x4 rw[WT];
 #pragma unroll
-        for (int j = 0; j < (9 * kTileCo * 4) / kThreads; ++j) {
+        for (int j = 0; j < WT; ++j) rw[j] = wsrc[threadIdx.x + j * kThreads];
+#pragma unroll
+        for (int j = 0; j < WT; ++j) {
             const int t = threadIdx.x + j * kThreads;
-            const int row = t >> 2, sub = t & 3;
-            *reinterpret_cast<u32x4*>(lds_w + lds_off(row, sub)) = wsrc[t];
+            *reinterpret_cast<u32x4*>(lds_w + lds_off(t >> 2, t & 3)) = rw[j];
         }
+    };
+
+    if constexpr (VEC) {
+        for (int32_t t = threadIdx.x; t < ((nrows + 15) >> 4) * 64; t += kThreads)
+            *reinterpret_cast<u32x4*>(lds_in + t * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+    fetch(0);
+    for (int32_t cc = 0; cc < nchunks; ++cc) {
+        __syncthreads();     // previous chunk fully read (and, at cc = 0, the halo zeroing done)
+        stash(cc);
         __syncthreads();
-#pragma unroll
+        if (cc + 1 < nchunks) fetch(cc + 1);
+#pragma unroll 3
         for (int tap = 0; tap < 9; ++tap) {
             const int32_t toff = (tap / 3 - 1) * p.w2 + (tap % 3 - 1);
             u32x4 a[4], b[4];
@@ -208,24 +295,46 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) mfma_chunk<T>(a[mt], b[nt], acc[mt][nt]);
         }
-        __syncthreads();
     }
 
-    // ---- epilogue: lane holds column co = nt·16 + (lane % 16), pixels 4·(lane/16)+e ----
+    // ---- epilogue: the 256-pixel × 64-channel tile goes through LDS as
+    // [co][pixel] rows so that global stores are whole 16-byte runs of one
+    // output plane.  Lane holds column co = nt·16 + (lane % 16) and pixels
+    // 4·(lane/16) + e of each 16×16 accumulator tile.
+    __syncthreads();                       // all waves done with the input/weight tiles
+    constexpr int OP = kTilePix * (int)sizeof(T) + 16;   // LDS bytes per channel row
+    char* lds_o = smem;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
-        const int32_t co = cb * kTileCo + nt * 16 + r16;
-        const float bv = bias ? bias[co] : 0.f;
+        const int32_t col = nt * 16 + r16;
+        const float bv = bias ? bias[cb * kTileCo + col] : 0.f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int32_t m = m0 + wid * 64 + mt * 16 + kq * 4 + e;
-                if (m <= m_last) {
-                    uint32_t n, hw;
-                    p.fd_hw.divmod((uint32_t)m, n, hw);
-                    Io<T>::st(out, ((int64_t)n * p.cout + co) * p.hw + hw, acc[mt][nt][e] + bv);
-                }
+            const int px = wid * 64 + mt * 16 + kq * 4;
+            const f32x4 v = acc[mt][nt] + bv;
+            Vec4<T>::st(reinterpret_cast<T*>(lds_o + col * OP + px * (int)sizeof(T)), v);
+        }
+    }
+    __syncthreads();
+    constexpr int E16 = 16 / (int)sizeof(T);                 // pixels per 16-byte run
+    constexpr int RUNS = kTilePix / E16;                      // runs per channel row
+    const bool whole = p.vec_store != 0;                      // runs never cross an image or the tensor end
+    for (int t = threadIdx.x; t < kTileCo * RUNS; t += kThreads) {
+        const int col = t / RUNS, j = t % RUNS;
+        const int32_t m = m0 + j * E16;
+        if (m > m_last) continue;
+        const int32_t co = cb * kTileCo + col;
+        const char* src = lds_o + col * OP + j * 16;
+        uint32_t n, hw;
+        p.fd_hw.divmod((uint32_t)m, n, hw);
+        if (whole && m + E16 - 1 <= m_last) {
+            *reinterpret_cast<u32x4*>(out + ((int64_t)n * p.cout + co) * p.hw + hw) =
+                *reinterpret_cast<const u32x4*>(src);
+        } else {
+            for (int e = 0; e < E16 && m + e <= m_last; ++e) {
+                uint32_t ne, hwe;
+                p.fd_hw.divmod((uint32_t)(m + e), ne, hwe);
+                out[((int64_t)ne * p.cout + co) * p.hw + hwe] = reinterpret_cast<const T*>(src)[e];
             }
         }
     }
@@ -251,8 +360,9 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
              const float* bias, T* out) {
     constexpr int CC = Chunk<T>::CC;
     const size_t wbytes = sizeof(T) * (size_t)cout * cin * 9;
-    const int32_t in_rows = in_rows_bound(h, w);
-    const size_t lds = (size_t)in_rows * kRowB + (size_t)9 * kTileCo * kRowB;
+    const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
+    const size_t lds = std::max((size_t)in_rows * kRowB + (size_t)9 * kTileCo * kRowB,
+                                (size_t)kTileCo * (kTilePix * sizeof(T) + 16));
     if (lds > 80 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
     T* wp = static_cast<T*>(workspace(ctx, wbytes));
     if (!wp) return NOTT_ERR_ALLOC;
@@ -268,14 +378,25 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     p.fd_h2 = FastDiv((uint32_t)(h + 2));
     const int64_t tiles = ceil_div((int64_t)p.npix, kTilePix);
     p.remap = (tiles % 8 == 0) ? 1 : 0;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[sizeof(T) == 2]) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3x3_same_kernel<T>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
-        attr_set[sizeof(T) == 2] = true;
+    p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
+    // Vector fill when image rows are whole 16-byte chunks, the input is
+    // 16-byte aligned and the tile's fill tasks fit the per-thread registers.
+    const int32_t sub = Chunk<T>::SUB;
+    const int32_t max_vr = in_rows_bound(h, w) / (w + 2);
+    const bool vec = (w % sub) == 0 && ((uintptr_t)in % 16) == 0 &&
+                     (int64_t)max_vr * (w / sub) * 4 <= (int64_t)VecTasks<T>::VT * kThreads;
+    static bool attr_set[2][2] = {{false, false}, {false, false}};
+    if (!attr_set[sizeof(T) == 2][vec]) {
+        const void* fn = vec ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true>)
+                             : reinterpret_cast<const void*>(&conv3x3_same_kernel<T, false>);
+        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
+        attr_set[sizeof(T) == 2][vec] = true;
     }
-    hipLaunchKernelGGL((conv3x3_same_kernel<T>), dim3((unsigned)tiles, (unsigned)(cout / kTileCo)), dim3(kThreads), lds,
-                       ctx->stream, in, wp, bias, out, p);
+    const dim3 grid((unsigned)tiles, (unsigned)(cout / kTileCo));
+    if (vec)
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, true>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    else
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, false>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
     return launch_status(ctx, "conv3x3_same");
 }
 
@@ -292,9 +413,13 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
 // of a band of TH rows (padding slots carry dy = 0).
 //
 // Per band, LDS holds dy[64 k][TH·P slots] and x[64 c][(TH+2)·P slots] (one
-// halo row above and below), each channel row padded by 16–32 bytes so the
-// 16 channels one MFMA operand reads fall in distinct banks; the padding is
-// zero and doubles as the guard read by the s = 0 / s = 2 shifts.  A lane's
+// halo row above and below) as 16-byte chunks of slots, stored chunk-major
+// in groups of 16 channels: chunk j of channel ch sits in the 256-byte block
+// (ch / 16, j) at slot (ch ^ j) % 16.  The 16 lanes that read one chunk of 16
+// channels, and the 16 lanes that fill 16 consecutive chunks of one channel,
+// both touch 16 distinct slots (conflict-free ds_read/ds_write_b128).  x has
+// one zero guard block before and after each channel group, read by the
+// s = 0 / s = 2 shifts at the band edges.  A lane's
 // MFMA k-slice is 8 (bf16) / 4 (fp32) consecutive slots: s = 1 is an aligned
 // 16-byte LDS read, s = 0 and s = 2 realign the neighbouring aligned chunks by
 // one element in registers.  Wave w owns channels 16w..16w+15 for all 9 taps
@@ -311,9 +436,13 @@ template <> struct WgCfg<float> { static constexpr int TH = 2, E = 4, KSTEP = 16
 struct WgradParams {
     int32_t n, c, k, h, w;
     int32_t bands_per_img, total_bands, bands_per_split;
-    int32_t a_pitch, b_pitch;       // LDS bytes per channel row (dy, x)
     int32_t kblocks;
 };
+
+// Chunk j (16 bytes) of channel ch in a region of nch chunks per channel.
+__device__ __forceinline__ int wg_off(int ch, int j, int nch) {
+    return (ch >> 4) * (nch << 8) + (j << 8) + (((ch ^ j) & 15) << 4);
+}
 
 // Shift a 16-byte chunk by one element toward lower slots (s = 2: slots base+1..)
 // or toward higher slots (s = 0: slots base−1..).
@@ -346,9 +475,11 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
     constexpr int B_TASKS = (B_TOTAL + kThreads - 1) / kThreads;
     constexpr int RB = P * (int)sizeof(T);              // bytes per slot row
     constexpr int KSTEPS = TH * P / KSTEP;
+    constexpr int NA = TH * CPR;                        // dy chunks per channel
+    constexpr int NB = (TH + 2) * CPR + 2;              // x chunks per channel, with the two guards
     extern __shared__ __attribute__((aligned(16))) char smem[];
     char* lds_a = smem;
-    char* lds_b = smem + 64 * p.a_pitch + 16;           // 16-byte zero guard in front of channel 0
+    char* lds_b = smem + 64 * NA * 16;
 
     const int kb = blockIdx.y % p.kblocks, cb = blockIdx.y / p.kblocks;
     const int32_t b0 = blockIdx.x * p.bands_per_split;
@@ -357,14 +488,10 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
     const int r16 = lane & 15, kq = lane >> 4;
     const int64_t plane = (int64_t)p.h * p.w;
 
-    // Zero the guard and the per-channel paddings of x (never written by the fill).
-    {
-        const int pad = p.b_pitch - (TH + 2) * RB;
-        for (int i = threadIdx.x; i < 64 * (pad / 16) + 1; i += kThreads) {
-            char* dst = (i == 0) ? (lds_b - 16) : (lds_b + ((i - 1) / (pad / 16)) * p.b_pitch + (TH + 2) * RB +
-                                                   ((i - 1) % (pad / 16)) * 16);
-            *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
-        }
+    // Zero the guard chunks of x (never written by the fill).
+    for (int i = threadIdx.x; i < 64 * 2; i += kThreads) {
+        const int ch = i >> 1, j = (i & 1) ? NB - 1 : 0;
+        *reinterpret_cast<u32x4*>(lds_b + wg_off(ch, j, NB)) = u32x4{0u, 0u, 0u, 0u};
     }
 
     f32x4 acc[4][9];
@@ -385,7 +512,8 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
             const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
             const int h = h0 + row;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((A_TOTAL % kThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h) v = *reinterpret_cast<const u32x4*>(dyb + kk * plane + (int64_t)h * p.w + ch * E);
+            if ((A_TOTAL % kThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h)
+                v = *reinterpret_cast<const u32x4*>(dyb + kk * plane + (int64_t)h * p.w + ch * E);
             ra[j] = v;
         }
 #pragma unroll
@@ -405,20 +533,19 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
             const int t = threadIdx.x + j * kThreads;
             const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
             if (A_TOTAL % kThreads == 0 || t < A_TOTAL)
-                *reinterpret_cast<u32x4*>(lds_a + kk * p.a_pitch + row * RB + ch * 16) = ra[j];
+                *reinterpret_cast<u32x4*>(lds_a + wg_off(kk, row * CPR + ch, NA)) = ra[j];
         }
 #pragma unroll
         for (int j = 0; j < B_TASKS; ++j) {
             const int t = threadIdx.x + j * kThreads;
             const int ch = t % CPR, row = (t / CPR) % (TH + 2), cc = t / (CPR * (TH + 2));
             if (B_TOTAL % kThreads == 0 || t < B_TOTAL)
-                *reinterpret_cast<u32x4*>(lds_b + cc * p.b_pitch + row * RB + ch * 16) = rb[j];
+                *reinterpret_cast<u32x4*>(lds_b + wg_off(cc, 1 + row * CPR + ch, NB)) = rb[j];
         }
     };
 
     if (b0 < b1) fetch(b0);
-    const char* arow = lds_a + r16 * p.a_pitch;                 // + mt·16·a_pitch
-    const char* brow = lds_b + (wid * 16 + r16) * p.b_pitch;
+    const int cl = wid * 16 + r16;                              // this lane's x channel
     for (int32_t band = b0; band < b1; ++band) {
         __syncthreads();
         stash();
@@ -426,17 +553,17 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
         if (band + 1 < b1) fetch(band + 1);
 #pragma unroll 2
         for (int t = 0; t < KSTEPS; ++t) {
-            const int slot = t * KSTEP + kq * E;
+            const int ja = t * (KSTEP / E) + kq;                // dy chunk of this lane's k-slice
             u32x4 a[4];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
-                a[mt] = *reinterpret_cast<const u32x4*>(arow + mt * 16 * p.a_pitch + slot * (int)sizeof(T));
+                a[mt] = *reinterpret_cast<const u32x4*>(lds_a + wg_off(mt * 16 + r16, ja, NA));
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
-                const char* bp = brow + (slot + r * P) * (int)sizeof(T);
-                const u32x4 prev = *reinterpret_cast<const u32x4*>(bp - 16);
-                const u32x4 cur = *reinterpret_cast<const u32x4*>(bp);
-                const u32x4 next = *reinterpret_cast<const u32x4*>(bp + 16);
+                const int jb = 1 + ja + r * CPR;                // x chunk for s = 1 (guard-shifted)
+                const u32x4 prev = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb - 1, NB));
+                const u32x4 cur = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb, NB));
+                const u32x4 next = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb + 1, NB));
                 const u32x4 b_s0 = shift_hi<T>(prev, cur);
                 const u32x4 b_s2 = shift_lo<T>(cur, next);
 #pragma unroll
@@ -478,12 +605,6 @@ __global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* 
     *o = accumulate ? *o + s : s;
 }
 
-template <typename T>
-int wg_pitch(int rows, int rb) {
-    int pitch = rows * rb + 16;
-    if (((pitch / 16) & 1) == 0) pitch += 16;   // odd multiple of 16 bytes: 16 rows in distinct banks
-    return pitch;
-}
 
 template <typename T, int P>
 int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
@@ -494,14 +615,13 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     p.bands_per_img = (p.h + TH - 1) / TH;
     p.total_bands = p.n * p.bands_per_img;
     p.kblocks = p.k / 64;
-    p.a_pitch = wg_pitch<T>(TH, RB);
-    p.b_pitch = wg_pitch<T>(TH + 2, RB);
+    constexpr int CPR = P * (int)sizeof(T) / 16;
     const int tiles = p.kblocks * (p.c / 64);
     // About one workgroup per CU in total.
     int64_t splits = std::max<int64_t>(1, std::min<int64_t>(p.total_bands, ceil_div((int64_t)ctx->num_cu, tiles)));
     p.bands_per_split = (int32_t)ceil_div(p.total_bands, splits);
     splits = ceil_div(p.total_bands, p.bands_per_split);
-    const size_t lds = (size_t)64 * p.a_pitch + 16 + (size_t)64 * p.b_pitch;
+    const size_t lds = (size_t)64 * 16 * (TH * CPR + (TH + 2) * CPR + 2);
     if (lds > 160 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad: band does not fit in LDS");
     float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)splits * 9 * p.k * p.c));
     if (!ws) return NOTT_ERR_ALLOC;
