@@ -29,7 +29,9 @@ def check(got, want, dt: str = "f32", what: str = "", rtol=None, atol=None):
 
     fp32: rtol 1e-4, atol 1e-5·max(1, rms(want)) — the absolute floor scales
     with the output's magnitude so long fp32 reductions are judged relative
-    to what they sum.  bf16: rtol 2e-2, atol 1e-2·rms(want).
+    to what they sum.  bf16: rtol 2e-2, atol 2e-2·rms(want) — "rel 2e-2"
+    measured against the tensor's scale, since an element near zero that is
+    a sum of bf16-rounded products cannot meet 2e-2 of its own size.
     NaN positions must agree."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
@@ -42,7 +44,7 @@ def check(got, want, dt: str = "f32", what: str = "", rtol=None, atol=None):
     rms = float(np.sqrt(np.mean(w[np.isfinite(w)] ** 2))) if np.isfinite(w).any() else 1.0
     if dt == "bf16":
         rtol = 2e-2 if rtol is None else rtol
-        atol = 1e-2 * rms if atol is None else atol
+        atol = 2e-2 * rms if atol is None else atol
     else:
         rtol = 1e-4 if rtol is None else rtol
         atol = 1e-5 * max(1.0, rms) if atol is None else atol

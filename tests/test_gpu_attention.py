@@ -1,0 +1,118 @@
+"""GPU parity of the flash-style attention kernels (forward, dq/dk/dv) and of
+the multi-head attention module built from them, against the CPU oracle and
+the reference's own golden vectors, through the C ABI.
+
+configs[3] (B=8, H=16, T=1024, dh=64, causal, bf16) is checked at full size
+against a float32 torch reference of the same attention on the GPU (scores
+materialised, as the reference module does)."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import check, dev, host, host_input
+from oracle_lib import f32, rng
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from thot_amd import ops as _ops
+    assert torch.cuda.is_available()
+    return _ops
+
+
+@pytest.mark.parametrize("name", ["attention_causal", "attention_full"])
+def test_attention_golden(ops, name):
+    """The HIP path against vectors written by the reference's ScaledDotProductKernel."""
+    z = np.load(os.path.join(GOLD, name + ".npz"))
+    q, k, v, dO = (f32(z[n]) for n in ("q", "k", "v", "dO"))
+    b, h, t, dh = q.shape
+    d = ops.attn_desc(b, h, t, k.shape[2], dh, bool(z["causal"]))
+    o, lse = ops.attention_fwd(dev(q), dev(k), dev(v), d)
+    dq, dk, dv = ops.attention_bwd(dev(q), dev(k), dev(v), o, dev(dO), lse, d)
+    torch.cuda.synchronize()
+    check(host(o), z["o"], what="o")
+    check(host(dq), z["dq"], what="dq")
+    check(host(dk), z["dk"], what="dk")
+    check(host(dv), z["dv"], what="dv")
+
+
+CASES = [
+    (1, 2, 5, 5, 4, True),
+    (2, 3, 70, 70, 16, True),
+    (1, 2, 64, 64, 64, False),
+    (2, 2, 130, 130, 32, True),
+    (1, 1, 100, 77, 8, False),
+    (1, 2, 33, 100, 64, True),
+    (1, 1, 192, 192, 24, True),
+]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "b{}h{}t{}s{}d{}c{}".format(*c))
+def test_attention_vs_oracle(ops, oracle, dt, case):
+    b, h, t, s, dh, causal = case
+    g = rng(sum(case) + len(dt))
+    q = host_input(g.standard_normal((b, h, t, dh)), dt)
+    k = host_input(g.standard_normal((b, h, s, dh)), dt)
+    v = host_input(g.standard_normal((b, h, s, dh)), dt)
+    dO = host_input(g.standard_normal((b, h, t, dh)), dt)
+    d = ops.attn_desc(b, h, t, s, dh, causal)
+    o, lse = ops.attention_fwd(dev(q, dt), dev(k, dt), dev(v, dt), d)
+    ro, rlse = oracle.attention_fwd(d, q, k, v)
+    torch.cuda.synchronize()
+    check(host(o), ro, dt, "o")
+    check(host(lse), rlse, "f32" if dt == "f32" else dt, "lse")
+    # backward from the oracle's o (rounded like the GPU's) so both sides see the same inputs
+    o_in = host_input(ro, dt)
+    dq, dk, dv = ops.attention_bwd(dev(q, dt), dev(k, dt), dev(v, dt), dev(o_in, dt), dev(dO, dt), lse, d)
+    rdq, rdk, rdv = oracle.attention_bwd(d, q, k, v, o_in, dO)
+    torch.cuda.synchronize()
+    check(host(dq), rdq, dt, "dq")
+    check(host(dk), rdk, dt, "dk")
+    check(host(dv), rdv, dt, "dv")
+
+
+def _torch_attention_fp32(q, k, v, dO, causal, scale):
+    """float32 reference with materialised scores (the reference module's math)."""
+    q, k, v = (x.float().detach().clone().requires_grad_(True) for x in (q, k, v))
+    s = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
+    if causal:
+        t, sl = s.shape[-2], s.shape[-1]
+        mask = torch.triu(torch.ones(t, sl, dtype=torch.bool, device=s.device), 1)
+        s = s.masked_fill(mask, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    o = torch.matmul(p, v)
+    o.backward(dO.float())
+    return o.detach(), q.grad, k.grad, v.grad
+
+
+def test_attention_config4_full_size(ops):
+    """B=8, H=16, T=1024, dh=64, causal, bf16 (checked on 2 of the 8 batches)."""
+    B, H, T, Dh = 8, 16, 1024, 64
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    mk = lambda: torch.randn((B, H, T, Dh), generator=gen, device="cuda").to(torch.bfloat16)
+    q, k, v, dO = mk(), mk(), mk(), mk()
+    d = ops.attn_desc(B, H, T, T, Dh, True)
+    o, lse = ops.attention_fwd(q, k, v, d)
+    dq, dk, dv = ops.attention_bwd(q, k, v, o, dO, lse, d)
+    torch.cuda.synchronize()
+    for bsl in (slice(0, 1), slice(B - 1, B)):
+        ro, rdq, rdk, rdv = _torch_attention_fp32(q[bsl], k[bsl], v[bsl], dO[bsl], True, 1 / math.sqrt(Dh))
+        check(host(o[bsl]), host(ro), "bf16", "o")
+        check(host(dq[bsl]), host(rdq), "bf16", "dq")
+        check(host(dk[bsl]), host(rdk), "bf16", "dk")
+        check(host(dv[bsl]), host(rdv), "bf16", "dv")
+
+
+def test_attention_rejects_bad_descriptors(ops):
+    from thot_amd._abi import NottInvalidArgument
+    q = torch.zeros((1, 1, 4, 200), device="cuda")
+    d = ops.attn_desc(1, 1, 4, 4, 200, False)
+    with pytest.raises(NottInvalidArgument):
+        ops.attention_fwd(q, q, q, d)

@@ -1,0 +1,654 @@
+// Scaled dot-product attention forward and backward (flash-style, MFMA).
+//
+// Replaces ScaledDotProductKernelImpl::forward of the reference
+// (attention/details/kernel.hpp:20-96) and its autograd backward:
+//   s = q·kᵀ·scale (the reference divides by sqrt(dh), kernel.hpp:33),
+//   causal: s[i][j] = −inf for j > i (triu(1), kernel.hpp:86-91),
+//   p = softmax_j(s), o = p·v                          (kernel.hpp:93-95)
+//   dv = pᵀ·do;  dp = do·vᵀ;  ds = p∘(dp − rowsum(do∘o));
+//   dq = ds·k·scale;  dk = dsᵀ·q·scale
+// The reference materialises s and p ([b,h,t,s]); here one workgroup keeps a
+// 64-row block in registers and streams 64-row blocks of the other operand
+// through LDS, recomputing p from the saved log-sum-exp (lse = m + log l).
+//
+// Kernels: attn_fwd (o, lse), attn_dsum (rowsum(do∘o)), attn_dkdv (one
+// workgroup per key block, loops over query blocks) and attn_dq (one per
+// query block, loops over key blocks).  dq has its own pass instead of
+// atomics, so every result is deterministic.
+//
+// Register-resident probabilities: every score tile is computed in
+// "transposed" MFMA form so that its accumulator layout (lane l holds
+// column l%16, rows 4·(l/16)+e) is exactly the A-operand layout the next
+// MFMA needs for p or ds (row l%16, k-slots 4·(l/16)+e of each 16-wide tile).
+// For bf16 (k = 32 per MFMA) the two 16-wide tiles of a 32-slice are
+// interleaved as k-slots {4q..4q+3, 16+4q..16+4q+3}; the B operand of that
+// MFMA is stored in LDS transposed with its keys permuted the same way, so
+// it is still one 16-byte read per lane.
+#include "common.hpp"
+
+namespace {
+
+using nott::ceil_div;
+using nott::launch_status;
+using nott::workspace;
+
+constexpr int kThreads = 256;     // 4 waves, 16 rows each
+constexpr int BR = 64;            // rows per block (queries or keys)
+
+template <typename T> struct AT;
+template <> struct AT<float> { static constexpr int E = 4, SL = 16; };    // elems per 16 B, rows per 64-byte k-slice
+template <> struct AT<bf16_t> { static constexpr int E = 8, SL = 32; };
+
+// Tile of R rows × NCH 16-byte chunks: rows grouped by 16, chunk-major inside
+// a group, slot XOR-swizzled by the chunk index (conflict-free for 16 lanes
+// reading 16 rows of one chunk and for 16 lanes writing 16 chunks of a row).
+__device__ __forceinline__ int toff(int row, int ch, int nch) {
+    return (row >> 4) * (nch << 8) + (ch << 8) + (((row ^ ch) & 15) << 4);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ void mma(const u32x4& a, const u32x4& b, f32x4& acc) {
+    if constexpr (sizeof(T) == 2) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                      0, 0, 0);
+    } else {
+        const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
+    }
+}
+
+// MFMA whose A operand is the 64-byte k-slice `s` of register tiles v[t][e]
+// (t = 16-wide tile of the k dimension, e = its 4 slots per lane).  For fp32
+// the float vector goes to the MFMA directly: building a u32x4 from
+// bit-cast floats and casting it back makes hipcc (ROCm 7.2) feed the first
+// component to all four v_mfma_f32_16x16x4_f32 issues.
+template <typename T>
+__device__ __forceinline__ void mma_rf(const f32x4 (&v)[4], int s, const u32x4& b, f32x4& acc) {
+    if constexpr (sizeof(T) == 2) {
+        const f32x4 x = v[2 * s], y = v[2 * s + 1];
+        const u32x4 a = u32x4{pack_bf16(x.x, x.y), pack_bf16(x.z, x.w), pack_bf16(y.x, y.y), pack_bf16(y.z, y.w)};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                      0, 0, 0);
+    } else {
+        const f32x4 af = v[s];
+        const f32x4 bf = __builtin_bit_cast(f32x4, b);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], acc, 0, 0, 0);
+    }
+}
+
+// As mma_rf, but for bf16 the A values are split into a bf16 head and a bf16
+// remainder (two MFMAs), so the product carries ~16 mantissa bits of ds.
+// Used for ds, whose entries are differences (p∘(dp − rowsum)) and lose the
+// most to a single bf16 rounding.
+template <typename T>
+__device__ __forceinline__ void mma_rf2(const f32x4 (&v)[4], int s, const u32x4& b, f32x4& acc) {
+    if constexpr (sizeof(T) == 2) {
+        f32x4 lo[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) lo[t][e] = v[t][e] - bf16_to_f32(f32_to_bf16(v[t][e]));
+        mma_rf<T>(v, s, b, acc);
+        mma_rf<T>(lo, s, b, acc);
+    } else {
+        mma_rf<T>(v, s, b, acc);
+    }
+}
+
+// Loads 16 bytes (E elements) of row `row` starting at column c0 of a
+// [rows × dh] matrix, zero outside; vec = rows are 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ u32x4 load_chunk(const T* base, int row, int nrows, int c0, int dh, bool vec) {
+    constexpr int E = AT<T>::E;
+    if (row >= nrows || c0 >= dh) return u32x4{0u, 0u, 0u, 0u};
+    const T* p = base + (int64_t)row * dh + c0;
+    if (vec && c0 + E <= dh) return *reinterpret_cast<const u32x4*>(p);
+    T v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = (c0 + e < dh) ? p[e] : T(0);
+    if constexpr (E == 8) {
+        return u32x4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                     (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)};
+    } else {
+        return u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                     __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+    }
+}
+
+// Natural tile: rows r0..r0+63 of the matrix, [row][d], NCHD chunks per row.
+template <typename T, int NCHD>
+__device__ __forceinline__ void fill_nat(char* tile, const T* base, int r0, int nrows, int dh, bool vec) {
+    constexpr int E = AT<T>::E;
+    for (int t = threadIdx.x; t < BR * NCHD; t += kThreads) {
+        const int ch = t % NCHD, row = t / NCHD;
+        *reinterpret_cast<u32x4*>(tile + toff(row, ch, NCHD)) = load_chunk<T>(base, r0 + row, nrows, ch * E, dh, vec);
+    }
+}
+
+// Row (within a 64-row block) stored at k-slot position `pos` of the
+// transposed tile (the bf16 interleave described above; identity for fp32).
+template <typename T>
+__device__ __forceinline__ int perm_row(int pos) {
+    if constexpr (sizeof(T) == 2) {
+        const int s = pos >> 5, w = pos & 31, q = w >> 3, j = w & 7;
+        return (s << 5) + (j < 4 ? 4 * q + j : 16 + 4 * q + (j - 4));
+    } else {
+        return pos;
+    }
+}
+
+// Transposed tile: [d][row-position] for rows r0..r0+63, NCHT = 64·sizeof(T)/16
+// chunks per d-row; DP rows (padded head dim).  One task moves an E×E block:
+// E rows (at E consecutive positions) × E columns, transposed in registers.
+template <typename T, int DP>
+__device__ __forceinline__ void fill_trans(char* tile, const T* base, int r0, int nrows, int dh, bool vec) {
+    constexpr int E = AT<T>::E;
+    constexpr int NCHT = BR / E;
+    constexpr int TASKS = NCHT * (DP / E);
+    for (int t = threadIdx.x; t < TASKS; t += kThreads) {
+        const int pc = t % NCHT, dc = t / NCHT;     // position chunk, d chunk
+        u32x4 in[E], out[E];
+#pragma unroll
+        for (int i = 0; i < E; ++i) in[i] = load_chunk<T>(base, r0 + perm_row<T>(pc * E + i), nrows, dc * E, dh, vec);
+        if constexpr (E == 8) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t a = in[2 * e][d], b = in[2 * e + 1][d];
+                    out[2 * d][e] = (a & 0xffffu) | (b << 16);
+                    out[2 * d + 1][e] = (a >> 16) | (b & 0xffff0000u);
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out[j] = u32x4{in[0][j], in[1][j], in[2][j], in[3][j]};
+        }
+#pragma unroll
+        for (int i = 0; i < E; ++i) *reinterpret_cast<u32x4*>(tile + toff(dc * E + i, pc, NCHT)) = out[i];
+    }
+}
+
+// Fragment of 16 rows (r0..r0+15) of a natural/transposed tile at 64-byte k-slice s.
+__device__ __forceinline__ u32x4 frag(const char* tile, int r0, int s, int nch) {
+    const int lane = threadIdx.x & 63;
+    return *reinterpret_cast<const u32x4*>(tile + toff(r0 + (lane & 15), 4 * s + (lane >> 4), nch));
+}
+
+struct AttnParams {
+    int32_t t, s, dh;
+    int32_t causal;
+    float scale;
+    int32_t nqb, nkb;     // query / key blocks
+    int32_t vec;          // rows are 16-byte aligned (vector loads)
+};
+
+// ---------------------------------------------------------------- forward
+template <typename T, int NS>
+__global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                           const T* __restrict__ v, T* __restrict__ o,
+                                                           float* __restrict__ lse, AttnParams p) {
+    constexpr int SL = AT<T>::SL;
+    constexpr int DP = NS * SL;                 // padded head dim
+    constexpr int NCHD = DP * (int)sizeof(T) / 16;
+    constexpr int NCHT = BR * (int)sizeof(T) / 16;
+    constexpr int ND = DP / 16;                 // 16-wide d tiles
+    constexpr int KS = BR / SL;                 // 64-byte k-slices per 64-row block
+    constexpr int X = BR * NCHD * 16;           // bytes of one 64-row tile (natural or transposed)
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* lq = smem;
+    char* lk = smem + X;
+    char* lvt = smem + 2 * X;
+
+    const int bh = blockIdx.y;
+    const int qb = p.nqb - 1 - (int)blockIdx.x;      // heaviest (causal) blocks first
+    const int q0 = qb * BR;
+    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int my_q = q0 + wid * 16 + r16;            // this lane's query row (score layout)
+    const float sl2 = p.scale * 1.4426950408889634f;  // scale·log2(e)
+
+    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
+    float m = -INFINITY, l = 0.f;
+    f32x4 acc[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int kb_end = p.nkb;
+    if (p.causal) kb_end = min(kb_end, (q0 + BR - 1) / BR + 1);
+    for (int kb = 0; kb < kb_end; ++kb) {
+        const int k0 = kb * BR;
+        __syncthreads();
+        fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
+        fill_trans<T, DP>(lvt, v + koff, k0, p.s, p.dh, p.vec);
+        __syncthreads();
+        // scores in transposed form: lane holds s[my_q][k0 + 16·kt + 4·kq + e]
+        f32x4 sc[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            sc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) mma<T>(frag(lk, kt * 16, s, NCHD), frag(lq, wid * 16, s, NCHD), sc[kt]);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = k0 + kt * 16 + kq * 4 + e;
+                const bool ok = key < p.s && !(p.causal && key > my_q);
+                sc[kt][e] = ok ? sc[kt][e] * sl2 : -INFINITY;   // log2 domain
+                mx = fmaxf(mx, sc[kt][e]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m - m_new);
+        float rs = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float pe = (m_new == -INFINITY) ? 0.f : exp2f(sc[kt][e] - m_new);
+                sc[kt][e] = pe;
+                rs += pe;
+            }
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        l = l * alpha + rs;
+        m = m_new;
+        // O rows in the accumulator are 4·kq + e: fetch their alpha.
+        float al[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) al[e] = __shfl(alpha, kq * 4 + e, 64);
+#pragma unroll
+        for (int dt = 0; dt < ND; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[dt][e] *= al[e];
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) mma_rf<T>(sc, s, frag(lvt, dt * 16, s, NCHT), acc[dt]);
+    }
+    // o = acc / l (rows 4·kq + e of this wave's 16), lse = m + ln l (in natural log).
+    float li[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) li[e] = __shfl(l, kq * 4 + e, 64);
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+        const int d = dt * 16 + r16;
+        if (d >= p.dh) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = q0 + wid * 16 + kq * 4 + e;
+            if (row < p.t) Io<T>::st(o + qoff, (int64_t)row * p.dh + d, acc[dt][e] / li[e]);
+        }
+    }
+    if (kq == 0 && my_q < p.t) lse[(int64_t)bh * p.t + my_q] = (m + log2f(l)) * 0.6931471805599453f;
+}
+
+// ------------------------------------------------------- rowsum(do ∘ o)
+template <typename T>
+__global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ o, const T* __restrict__ dO,
+                                                        float* __restrict__ dsum, int64_t rows, int dh) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float s = 0.f;
+    for (int d = lane; d < dh; d += 64) s += Io<T>::ld(o, r * dh + d) * Io<T>::ld(dO, r * dh + d);
+    s = wave_sum(s);
+    if (lane == 0) dsum[r] = s;
+}
+
+// ------------------------------------------------------------ dk, dv
+template <typename T, int NS>
+__global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                            const T* __restrict__ v, const T* __restrict__ dO,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ dsum, T* __restrict__ dk,
+                                                            T* __restrict__ dv, AttnParams p) {
+    constexpr int SL = AT<T>::SL;
+    constexpr int DP = NS * SL;
+    constexpr int NCHD = DP * (int)sizeof(T) / 16;
+    constexpr int NCHT = BR * (int)sizeof(T) / 16;
+    constexpr int ND = DP / 16;
+    constexpr int KS = BR / SL;
+    constexpr int X = BR * NCHD * 16;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* lk = smem;
+    char* lv = smem + X;
+    char* lq = smem + 2 * X;
+    char* ldo = smem + 3 * X;
+    char* lqt = smem + 4 * X;
+    char* ldot = smem + 5 * X;
+    float* llse = reinterpret_cast<float*>(smem + 6 * X);
+    float* lds_ = llse + BR;
+
+    const int bh = blockIdx.y;
+    const int kb = blockIdx.x;
+    const int k0 = kb * BR;
+    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int my_k = k0 + wid * 16 + r16;   // this lane's key (score layout column)
+    const float sl2 = p.scale * 1.4426950408889634f;
+
+    fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
+    fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
+    f32x4 adk[ND], adv[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) adk[i] = adv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int qb_begin = p.causal ? k0 / BR : 0;
+    for (int qb = qb_begin; qb < p.nqb; ++qb) {
+        const int q0 = qb * BR;
+        __syncthreads();
+        fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
+        fill_nat<T, NCHD>(ldo, dO + qoff, q0, p.t, p.dh, p.vec);
+        fill_trans<T, DP>(lqt, q + qoff, q0, p.t, p.dh, p.vec);
+        fill_trans<T, DP>(ldot, dO + qoff, q0, p.t, p.dh, p.vec);
+        if (threadIdx.x < BR) {
+            const int row = q0 + threadIdx.x;
+            llse[threadIdx.x] = row < p.t ? lse[(int64_t)bh * p.t + row] * 1.4426950408889634f : 0.f;
+            lds_[threadIdx.x] = row < p.t ? dsum[(int64_t)bh * p.t + row] : 0.f;
+        }
+        __syncthreads();
+        // s and dp in transposed form: lane holds [q0 + 16·qt + 4·kq + e][my_k]
+        f32x4 pt[4], dpt[4];
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+            pt[qt] = dpt[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                mma<T>(frag(lq, qt * 16, s, NCHD), frag(lk, wid * 16, s, NCHD), pt[qt]);
+                mma<T>(frag(ldo, qt * 16, s, NCHD), frag(lv, wid * 16, s, NCHD), dpt[qt]);
+            }
+        }
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ql = qt * 16 + kq * 4 + e;
+                const int qrow = q0 + ql;
+                const bool ok = qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow);
+                const float pe = ok ? exp2f(pt[qt][e] * sl2 - llse[ql]) : 0.f;
+                pt[qt][e] = pe;
+                dpt[qt][e] = pe * (dpt[qt][e] - lds_[ql]);   // ds
+            }
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) {
+                mma_rf2<T>(pt, s, frag(ldot, dt * 16, s, NCHT), adv[dt]);
+                mma_rf2<T>(dpt, s, frag(lqt, dt * 16, s, NCHT), adk[dt]);
+            }
+    }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+        const int d = dt * 16 + r16;
+        if (d >= p.dh) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int key = k0 + wid * 16 + kq * 4 + e;
+            if (key < p.s) {
+                Io<T>::st(dk + koff, (int64_t)key * p.dh + d, adk[dt][e] * p.scale);
+                Io<T>::st(dv + koff, (int64_t)key * p.dh + d, adv[dt][e]);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------- dq
+// EXACT_DSUM: first sweep the key blocks once to form rowsum(p∘dp) in fp32
+// (= rowsum(do∘o) in exact arithmetic), write it for the dk/dv pass and use
+// it here.  The bf16 path needs this: rowsum(do∘o) taken from a bf16-rounded
+// o cancels badly against dp on rows with few unmasked keys.
+template <typename T, int NS, bool EXACT_DSUM>
+__global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                          const T* __restrict__ v, const T* __restrict__ dO,
+                                                          const float* __restrict__ lse,
+                                                          float* __restrict__ dsum, T* __restrict__ dq,
+                                                          AttnParams p) {
+    constexpr int SL = AT<T>::SL;
+    constexpr int DP = NS * SL;
+    constexpr int NCHD = DP * (int)sizeof(T) / 16;
+    constexpr int NCHT = BR * (int)sizeof(T) / 16;
+    constexpr int ND = DP / 16;
+    constexpr int KS = BR / SL;
+    constexpr int X = BR * NCHD * 16;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    char* lq = smem;
+    char* ldo = smem + X;
+    char* lk = smem + 2 * X;
+    char* lv = smem + 3 * X;
+    char* lkt = smem + 4 * X;
+
+    const int bh = blockIdx.y;
+    const int qb = p.nqb - 1 - (int)blockIdx.x;
+    const int q0 = qb * BR;
+    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int my_q = q0 + wid * 16 + r16;
+    const float sl2 = p.scale * 1.4426950408889634f;
+    const float my_lse = my_q < p.t ? lse[(int64_t)bh * p.t + my_q] * 1.4426950408889634f : 0.f;
+
+    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
+    fill_nat<T, NCHD>(ldo, dO + qoff, q0, p.t, p.dh, p.vec);
+    f32x4 acc[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int kb_end = p.nkb;
+    if (p.causal) kb_end = min(kb_end, (q0 + BR - 1) / BR + 1);
+    float my_ds;
+    if constexpr (EXACT_DSUM) {
+        float part = 0.f;
+        for (int kb = 0; kb < kb_end; ++kb) {
+            const int k0 = kb * BR;
+            __syncthreads();
+            fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
+            fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
+            __syncthreads();
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) {
+                f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < NS; ++s) {
+                    mma<T>(frag(lk, kt * 16, s, NCHD), frag(lq, wid * 16, s, NCHD), sc);
+                    mma<T>(frag(lv, kt * 16, s, NCHD), frag(ldo, wid * 16, s, NCHD), dp);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int key = k0 + kt * 16 + kq * 4 + e;
+                    const bool ok = my_q < p.t && key < p.s && !(p.causal && key > my_q);
+                    part += ok ? exp2f(sc[e] * sl2 - my_lse) * dp[e] : 0.f;
+                }
+            }
+        }
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        my_ds = part;
+        if (kq == 0 && my_q < p.t) dsum[(int64_t)bh * p.t + my_q] = my_ds;
+    } else {
+        my_ds = my_q < p.t ? dsum[(int64_t)bh * p.t + my_q] : 0.f;
+    }
+    for (int kb = 0; kb < kb_end; ++kb) {
+        const int k0 = kb * BR;
+        __syncthreads();
+        fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
+        fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
+        fill_trans<T, DP>(lkt, k + koff, k0, p.s, p.dh, p.vec);
+        __syncthreads();
+        // lane holds s / dp at [my_q][k0 + 16·kt + 4·kq + e]
+        f32x4 sc[4], dp[4];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            sc[kt] = dp[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                mma<T>(frag(lk, kt * 16, s, NCHD), frag(lq, wid * 16, s, NCHD), sc[kt]);
+                mma<T>(frag(lv, kt * 16, s, NCHD), frag(ldo, wid * 16, s, NCHD), dp[kt]);
+            }
+        }
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int key = k0 + kt * 16 + kq * 4 + e;
+                const bool ok = my_q < p.t && key < p.s && !(p.causal && key > my_q);
+                const float pe = ok ? exp2f(sc[kt][e] * sl2 - my_lse) : 0.f;
+                dp[kt][e] = pe * (dp[kt][e] - my_ds);
+            }
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int dt = 0; dt < ND; ++dt) mma_rf2<T>(dp, s, frag(lkt, dt * 16, s, NCHT), acc[dt]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < ND; ++dt) {
+        const int d = dt * 16 + r16;
+        if (d >= p.dh) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = q0 + wid * 16 + kq * 4 + e;
+            if (row < p.t) Io<T>::st(dq + qoff, (int64_t)row * p.dh + d, acc[dt][e] * p.scale);
+        }
+    }
+}
+
+int check(nott_ctx ctx, const nott_attn_desc* d, AttnParams* p, int elem) {
+    NOTT_REQUIRE(ctx, d != nullptr, "attention: null descriptor");
+    NOTT_REQUIRE(ctx, d->b >= 0 && d->h >= 0 && d->t >= 0 && d->s >= 0 && d->dh > 0, "attention: bad shape");
+    // LDS holds six 64-row tiles of the padded head dim in the dk/dv pass.
+    NOTT_REQUIRE(ctx, d->dh <= (elem == 2 ? 128 : 64), "attention: head dim above 128 (bf16) / 64 (fp32) is not supported");
+    NOTT_REQUIRE(ctx, d->b * d->h <= 65535, "attention: too many (batch, head) pairs");
+    NOTT_REQUIRE(ctx, d->t * d->dh < (int64_t(1) << 31) && d->s * d->dh < (int64_t(1) << 31),
+                 "attention: sequence too long");
+    NOTT_REQUIRE(ctx, !d->causal || d->s > 0, "attention: causal needs keys");
+    p->t = (int32_t)d->t; p->s = (int32_t)d->s; p->dh = (int32_t)d->dh;
+    p->causal = d->causal != 0;
+    p->scale = (float)d->scale;
+    p->nqb = (int32_t)ceil_div(d->t, BR);
+    p->nkb = (int32_t)ceil_div(d->s, BR);
+    p->vec = ((d->dh * elem) % 16) == 0;
+    return NOTT_OK;
+}
+
+template <typename T>
+int slices_for(int dh) {
+    const int sl = AT<T>::SL;
+    int ns = (dh + sl - 1) / sl;
+    int r = 1;
+    while (r < ns) r <<= 1;
+    return r;
+}
+
+template <typename T, int NS>
+constexpr size_t tile_bytes() { return (size_t)BR * NS * AT<T>::SL * sizeof(T); }
+
+template <typename T, int NS>
+int fwd_ns(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
+           void* o, float* lse) {
+    const size_t lds = 3 * tile_bytes<T, NS>();
+    if (lds > 64 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, NS>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, NS>), dim3((unsigned)p.nqb, (unsigned)(d->b * d->h)), dim3(kThreads), lds,
+                       ctx->stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                       static_cast<T*>(o), lse, p);
+    return launch_status(ctx, "attention_fwd");
+}
+
+template <typename T, int NS>
+int bwd_ns(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
+           const void* o, const void* dO, const float* lse, void* dq, void* dk, void* dv) {
+    const int64_t rows = d->b * d->h * d->t;
+    float* dsum = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)std::max<int64_t>(rows, 1)));
+    if (!dsum) return NOTT_ERR_ALLOC;
+    constexpr bool EXACT = sizeof(T) == 2;
+    const unsigned bh = (unsigned)(d->b * d->h);
+    const size_t lds_kv = 6 * tile_bytes<T, NS>() + 2 * BR * sizeof(float);
+    const size_t lds_q = 5 * tile_bytes<T, NS>();
+    if (lds_kv > 64 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dkdv_kernel<T, NS>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_kv);
+    if (lds_q > 64 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dq_kernel<T, NS, EXACT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_q);
+    // fp32: rowsum(do∘o) from o; bf16: the dq pass forms it exactly and runs first.
+    if (!EXACT)
+        hipLaunchKernelGGL(attn_dsum_kernel<T>, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, ctx->stream,
+                           static_cast<const T*>(o), static_cast<const T*>(dO), dsum, rows, (int)d->dh);
+    hipLaunchKernelGGL((attn_dq_kernel<T, NS, EXACT>), dim3((unsigned)p.nqb, bh), dim3(kThreads), lds_q, ctx->stream,
+                       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                       static_cast<const T*>(dO), lse, dsum, static_cast<T*>(dq), p);
+    hipLaunchKernelGGL((attn_dkdv_kernel<T, NS>), dim3((unsigned)p.nkb, bh), dim3(kThreads), lds_kv, ctx->stream,
+                       static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
+                       static_cast<const T*>(dO), lse, dsum, static_cast<T*>(dk), static_cast<T*>(dv), p);
+    return launch_status(ctx, "attention_bwd");
+}
+
+template <typename T>
+int fwd(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
+        void* o, float* lse) {
+    switch (slices_for<T>((int)d->dh)) {
+        case 1: return fwd_ns<T, 1>(ctx, d, p, q, k, v, o, lse);
+        case 2: return fwd_ns<T, 2>(ctx, d, p, q, k, v, o, lse);
+        default: return fwd_ns<T, 4>(ctx, d, p, q, k, v, o, lse);
+    }
+}
+
+template <typename T>
+int bwd(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
+        const void* o, const void* dO, const float* lse, void* dq, void* dk, void* dv) {
+    switch (slices_for<T>((int)d->dh)) {
+        case 1: return bwd_ns<T, 1>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
+        case 2: return bwd_ns<T, 2>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
+        default: return bwd_ns<T, 4>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
+    }
+}
+
+bool aligned16(const void* a) { return ((uintptr_t)a % 16) == 0; }
+
+}  // namespace
+
+extern "C" int nott_attention_fwd(nott_ctx ctx, const nott_attn_desc* d, nott_dtype dtype, const void* q,
+                                  const void* k, const void* v, void* o, float* lse) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_attention_fwd: bad dtype");
+    AttnParams p;
+    const int st = check(ctx, d, &p, (int)nott::dtype_size(dtype));
+    if (st != NOTT_OK) return st;
+    if (d->b * d->h * d->t == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, q && k && v && o && lse, "nott_attention_fwd: null buffer");
+    if (!(aligned16(q) && aligned16(k) && aligned16(v))) p.vec = 0;
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, d, p, q, k, v, o, lse) : fwd<bf16_t>(ctx, d, p, q, k, v, o, lse);
+}
+
+extern "C" int nott_attention_bwd(nott_ctx ctx, const nott_attn_desc* d, nott_dtype dtype, const void* q,
+                                  const void* k, const void* v, const void* o, const void* dO, const float* lse,
+                                  void* dq, void* dk, void* dv) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_attention_bwd: bad dtype");
+    AttnParams p;
+    const int st = check(ctx, d, &p, (int)nott::dtype_size(dtype));
+    if (st != NOTT_OK) return st;
+    if (d->b * d->h == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, q && k && v && o && dO && lse && dq && dk && dv, "nott_attention_bwd: null buffer");
+    if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dO))) p.vec = 0;
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? bwd<float>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv)
+                             : bwd<bf16_t>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
+}
