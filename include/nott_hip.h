@@ -221,8 +221,12 @@ int nott_adam_step(nott_ctx ctx, int decoupled, int64_t n,
 int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, void* dst);
 /* Dtype conversion fp32 <-> bf16 (round to nearest even). */
 int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype src_dtype, void* dst, nott_dtype dst_dtype);
-/* Fill n fp32 words with zero using a kernel (safe under graph capture). */
+/* Fill `bytes` bytes with zero using a kernel (safe under graph capture). */
 int nott_zero(nott_ctx ctx, int64_t bytes, void* dst);
+/* y = x · scale[0] with scale a device fp32 scalar: the chain-rule product
+ * of a loss gradient with the upstream gradient of the scalar loss, which
+ * libtorch's engine hands over as a device tensor. */
+int nott_scale(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* x, const float* scale, void* y);
 
 #ifdef __cplusplus
 }

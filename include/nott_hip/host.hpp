@@ -1,0 +1,582 @@
+// nott_hip/host.hpp — C++ host layer of the MI355X backward path, behind
+// Nott's layer / loss / optimizer interfaces.
+//
+// The reference builds each layer as a torch::nn module and lets libtorch
+// autograd run the backward (reference src/layer/details/conv.hpp:177,
+// fc.hpp:40, pooling.hpp:144,164, batchnorm.hpp:50, flatten.hpp:34,
+// activation/details/relu.hpp:13, loss/details/ce.hpp:36,
+// attention/details/kernel.hpp:20-96, optimizer/details/adam.hpp:63,159).
+// Here every such node is a torch::autograd::Function whose forward and
+// backward call libnott_hip through the C ABI (include/nott_hip.h) on the
+// caller's current HIP stream; libtorch keeps only the graph walk, tensor
+// storage and the caching allocator.
+//
+// Parameter gradients are written straight into `param.grad()` with the
+// ABI's accumulate flag (AccumulateGrad semantics on a zero_grad'ed grad),
+// and the function returns no gradient for the parameter, so libtorch never
+// runs an accumulation kernel.  Gradient fan-out (a tensor read by two
+// consumers, e.g. the residual skip) goes through Fork, whose backward sums
+// the two gradients with nott_add.
+//
+// Errors: a negative ABI status becomes std::invalid_argument (bad shapes or
+// options, as the reference's factories throw) or std::runtime_error
+// (launch / allocation failures).
+#pragma once
+
+#include <torch/torch.h>
+#include <c10/hip/HIPStream.h>
+
+#include <array>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "nott_hip.h"
+
+namespace Nott {
+namespace HIP {
+
+using torch::Tensor;
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+// ------------------------------------------------------------------ runtime
+inline nott_ctx context(int device) {
+    static std::mutex mu;
+    static std::array<nott_ctx, 64> ctxs{};
+    std::lock_guard<std::mutex> g(mu);
+    if (device < 0 || device >= (int)ctxs.size()) throw std::invalid_argument("Nott::HIP: bad device index");
+    if (!ctxs[device]) {
+        const int st = nott_create(device, &ctxs[device]);
+        if (st != NOTT_OK) throw std::runtime_error(std::string("nott_create: ") + nott_status_string(st));
+    }
+    return ctxs[device];
+}
+
+// The context of t's device, bound to that device's current HIP stream.
+inline nott_ctx bind(const Tensor& t) {
+    if (!t.is_cuda()) throw std::invalid_argument("Nott::HIP: tensor must live on a HIP device");
+    const int dev = t.device().index();
+    nott_ctx c = context(dev);
+    nott_set_stream(c, (void*)c10::hip::getCurrentHIPStream(dev).stream());
+    return c;
+}
+
+inline void check(int st, nott_ctx c, const char* what) {
+    if (st == NOTT_OK) return;
+    const std::string msg = std::string(what) + ": " + nott_last_error(c);
+    if (st == NOTT_ERR_INVALID_ARG || st == NOTT_ERR_UNSUPPORTED) throw std::invalid_argument(msg);
+    throw std::runtime_error(msg);
+}
+
+inline nott_dtype dtype_of(const Tensor& t) {
+    if (t.scalar_type() == torch::kFloat32) return NOTT_F32;
+    if (t.scalar_type() == torch::kBFloat16) return NOTT_BF16;
+    throw std::invalid_argument("Nott::HIP: tensors must be float32 or bfloat16");
+}
+
+// A defined, zero-element tensor stands for "absent" (e.g. no bias):
+// autograd::Function::apply records the device of every tensor argument, so
+// arguments must always be defined tensors.
+inline bool present(const Tensor& t) { return t.defined() && t.numel() > 0; }
+inline Tensor absent(const Tensor& like) { return torch::empty({0}, like.options().dtype(torch::kFloat32)); }
+inline Tensor or_absent(const Tensor& t, const Tensor& like) { return t.defined() ? t : absent(like); }
+
+inline void* ptr(const Tensor& t) { return present(t) ? t.data_ptr() : nullptr; }
+inline float* fptr(const Tensor& t) { return present(t) ? t.data_ptr<float>() : nullptr; }
+
+inline Tensor contig(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
+
+// Ensures p.grad() exists (zeros) so that backward can accumulate into it.
+inline Tensor grad_buffer(const Tensor& p) {
+    if (!present(p) || !p.requires_grad()) return Tensor();
+    if (!p.grad().defined()) {
+        torch::NoGradGuard ng;
+        const_cast<Tensor&>(p).mutable_grad() = torch::zeros_like(p);
+    }
+    return p.grad();
+}
+
+// --------------------------------------------------------------- Conv2d
+// geometry = {stride_h, stride_w, pad_h, pad_w, dil_h, dil_w}
+struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
+    static nott_conv2d_desc desc(const Tensor& x, const Tensor& w, const std::vector<int64_t>& g) {
+        nott_conv2d_desc d{};
+        d.n = x.size(0); d.c = x.size(1); d.h = x.size(2); d.w = x.size(3);
+        d.k = w.size(0); d.r = w.size(2); d.s = w.size(3);
+        d.stride_h = g[0]; d.stride_w = g[1]; d.pad_h = g[2]; d.pad_w = g[3]; d.dil_h = g[4]; d.dil_w = g[5];
+        d.groups = 1; d.layout = NOTT_NCHW;
+        return d;
+    }
+    // x: input; w: master weight (fp32, receives the gradient); wc: weight in
+    // the compute dtype (== w for fp32); b: fp32 bias or undefined.
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b, std::vector<int64_t> geom) {
+        x = contig(x);
+        const nott_conv2d_desc d = desc(x, wc, geom);
+        const int64_t p = (d.h + 2 * d.pad_h - d.dil_h * (d.r - 1) - 1) / d.stride_h + 1;
+        const int64_t q = (d.w + 2 * d.pad_w - d.dil_w * (d.s - 1) - 1) / d.stride_w + 1;
+        Tensor y = torch::empty({d.n, d.k, p, q}, x.options());
+        nott_ctx c = bind(x);
+        check(nott_conv2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), ptr(y)), c, "conv2d forward");
+        ctx->save_for_backward({x, w, wc, b});
+        ctx->saved_data["geom"] = geom;
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3];
+        Tensor dy = contig(grads[0]);
+        const auto geom = ctx->saved_data["geom"].toIntVector();
+        const nott_conv2d_desc d = desc(x, wc, geom);
+        nott_ctx c = bind(dy);
+        Tensor dx;
+        if (ctx->saved_data["needs_dx"].toBool()) {
+            dx = torch::empty_like(x);
+            check(nott_conv2d_bwd_data(c, &d, dtype_of(dy), ptr(dy), ptr(wc), ptr(dx)), c, "conv2d dgrad");
+        }
+        Tensor gw = grad_buffer(w), gb = grad_buffer(b);
+        if (gw.defined() || gb.defined())
+            check(nott_conv2d_bwd_weight(c, &d, dtype_of(dy), ptr(x), ptr(dy), fptr(gw), fptr(gb), 1), c,
+                  "conv2d wgrad");
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// --------------------------------------------------------------- Linear
+struct LinearFn : torch::autograd::Function<LinearFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b) {
+        x = contig(x);
+        const int64_t kin = x.size(-1), m = x.numel() / kin, nout = wc.size(0);
+        auto shape = x.sizes().vec();
+        shape.back() = nout;
+        Tensor y = torch::empty(shape, x.options());
+        nott_ctx c = bind(x);
+        check(nott_linear_fwd(c, dtype_of(x), m, kin, nout, ptr(x), ptr(wc), fptr(b), ptr(y)), c, "linear forward");
+        ctx->save_for_backward({x, w, wc, b});
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3];
+        Tensor dy = contig(grads[0]);
+        const int64_t kin = x.size(-1), m = x.numel() / kin, nout = wc.size(0);
+        nott_ctx c = bind(dy);
+        Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
+        Tensor gw = grad_buffer(w), gb = grad_buffer(b);
+        check(nott_linear_bwd(c, dtype_of(dy), m, kin, nout, ptr(dy), ptr(x), ptr(wc), ptr(dx), fptr(gw), fptr(gb), 1),
+              c, "linear backward");
+        return {dx, Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// ----------------------------------------------------------------- ReLU
+struct ReluFn : torch::autograd::Function<ReluFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x) {
+        x = contig(x);
+        Tensor y = torch::empty_like(x);
+        nott_ctx c = bind(x);
+        check(nott_relu_fwd(c, dtype_of(x), x.numel(), ptr(x), ptr(y)), c, "relu forward");
+        ctx->save_for_backward({y});
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        Tensor y = ctx->get_saved_variables()[0];
+        Tensor dy = contig(grads[0]);
+        Tensor dx = torch::empty_like(dy);
+        nott_ctx c = bind(dy);
+        check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dx)), c, "relu backward");
+        return {dx};
+    }
+};
+
+// ------------------------------------------------------------ MaxPool2d
+// geometry = {kh, kw, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, ceil_mode}
+struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
+    static nott_pool2d_desc desc(const Tensor& x, const std::vector<int64_t>& g) {
+        nott_pool2d_desc d{};
+        d.n = x.size(0); d.c = x.size(1); d.h = x.size(2); d.w = x.size(3);
+        d.kh = g[0]; d.kw = g[1]; d.stride_h = g[2]; d.stride_w = g[3]; d.pad_h = g[4]; d.pad_w = g[5];
+        d.dil_h = g[6]; d.dil_w = g[7]; d.ceil_mode = (int32_t)g[8]; d.layout = NOTT_NCHW;
+        return d;
+    }
+    static int64_t out(int64_t in, int64_t k, int64_t s, int64_t p, int64_t dl, bool ceil) {
+        int64_t num = in + 2 * p - dl * (k - 1) - 1 + (ceil ? s - 1 : 0);
+        int64_t o = num / s + 1;
+        if (ceil && (o - 1) * s >= in + p) --o;
+        return o;
+    }
+    static Tensor forward(AutogradContext* ctx, Tensor x, std::vector<int64_t> geom) {
+        x = contig(x);
+        const nott_pool2d_desc d = desc(x, geom);
+        const int64_t oh = out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, d.ceil_mode),
+                      ow = out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, d.ceil_mode);
+        Tensor y = torch::empty({d.n, d.c, oh, ow}, x.options());
+        Tensor idx = torch::empty({d.n, d.c, oh, ow}, x.options().dtype(torch::kInt64));
+        nott_ctx c = bind(x);
+        check(nott_maxpool2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(y), idx.data_ptr<int64_t>()), c, "maxpool forward");
+        ctx->save_for_backward({idx});
+        ctx->saved_data["geom"] = geom;
+        ctx->saved_data["xshape"] = x.sizes().vec();
+        ctx->mark_non_differentiable({idx});
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        Tensor idx = ctx->get_saved_variables()[0];
+        Tensor dy = contig(grads[0]);
+        const auto xs = ctx->saved_data["xshape"].toIntVector();
+        Tensor dx = torch::empty(xs, dy.options());
+        const nott_pool2d_desc d = desc(dx, ctx->saved_data["geom"].toIntVector());
+        nott_ctx c = bind(dy);
+        check(nott_maxpool2d_bwd(c, &d, dtype_of(dy), idx.data_ptr<int64_t>(), ptr(dy), ptr(dx)), c,
+              "maxpool backward");
+        return {dx, Tensor()};
+    }
+};
+
+// ------------------------------------------- AdaptiveAvgPool2d({1, 1})
+struct AvgPoolGlobalFn : torch::autograd::Function<AvgPoolGlobalFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x) {
+        x = contig(x);
+        Tensor y = torch::empty({x.size(0), x.size(1), 1, 1}, x.options());
+        nott_ctx c = bind(x);
+        check(nott_avgpool_global_fwd(c, dtype_of(x), x.size(0) * x.size(1), x.size(2) * x.size(3), ptr(x), ptr(y)), c,
+              "avgpool forward");
+        ctx->saved_data["xshape"] = x.sizes().vec();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        Tensor dy = contig(grads[0]);
+        const auto xs = ctx->saved_data["xshape"].toIntVector();
+        Tensor dx = torch::empty(xs, dy.options());
+        nott_ctx c = bind(dy);
+        check(nott_avgpool_global_bwd(c, dtype_of(dy), xs[0] * xs[1], xs[2] * xs[3], ptr(dy), ptr(dx)), c,
+              "avgpool backward");
+        return {dx};
+    }
+};
+
+// ---------------------------------------------------------- BatchNorm2d
+// Training mode (batch statistics; running stats updated in forward).
+struct BatchNorm2dFn : torch::autograd::Function<BatchNorm2dFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor gamma, Tensor beta, Tensor running_mean,
+                          Tensor running_var, double eps, double momentum) {
+        x = contig(x);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor y = torch::empty_like(x);
+        auto fo = x.options().dtype(torch::kFloat32);
+        Tensor mean = torch::empty({ch}, fo), rstd = torch::empty({ch}, fo);
+        nott_ctx c = bind(x);
+        check(nott_batchnorm2d_fwd(c, dtype_of(x), n, ch, hw, ptr(x), fptr(gamma), fptr(beta), eps, momentum,
+                                   fptr(running_mean), fptr(running_var), ptr(y), fptr(mean), fptr(rstd)),
+              c, "batchnorm forward");
+        ctx->save_for_backward({x, gamma, beta, mean, rstd});
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4];
+        Tensor dy = contig(grads[0]);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
+        Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
+        nott_ctx c = bind(dy);
+        check(nott_batchnorm2d_bwd(c, dtype_of(dy), n, ch, hw, ptr(x), ptr(dy), fptr(mean), fptr(rstd), fptr(gamma),
+                                   ptr(dx), fptr(gg), fptr(gbt), 1),
+              c, "batchnorm backward");
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// ------------------------------------------------------------ LayerNorm
+struct LayerNormFn : torch::autograd::Function<LayerNormFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor gamma, Tensor beta, Tensor gamma_c, Tensor beta_c,
+                          double eps) {
+        x = contig(x);
+        const int64_t d = x.size(-1), rows = x.numel() / d;
+        Tensor y = torch::empty_like(x);
+        auto fo = x.options().dtype(torch::kFloat32);
+        Tensor mean = torch::empty({rows}, fo), rstd = torch::empty({rows}, fo);
+        nott_ctx c = bind(x);
+        check(nott_layernorm_fwd(c, dtype_of(x), rows, d, ptr(x), ptr(gamma_c), ptr(beta_c), eps, ptr(y), fptr(mean),
+                                 fptr(rstd)),
+              c, "layernorm forward");
+        ctx->save_for_backward({x, gamma, beta, gamma_c, mean, rstd});
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], gamma = s[1], beta = s[2], gamma_c = s[3], mean = s[4], rstd = s[5];
+        Tensor dy = contig(grads[0]);
+        const int64_t d = x.size(-1), rows = x.numel() / d;
+        Tensor dx = torch::empty_like(x);
+        Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
+        nott_ctx c = bind(dy);
+        check(nott_layernorm_bwd(c, dtype_of(dy), rows, d, ptr(x), ptr(dy), fptr(mean), fptr(rstd), ptr(gamma_c),
+                                 ptr(dx), fptr(gg), fptr(gbt), 1),
+              c, "layernorm backward");
+        return {ctx->saved_data["needs_dx"].toBool() ? dx : Tensor(), Tensor(), Tensor(), Tensor(), Tensor(),
+                Tensor()};
+    }
+};
+
+// ------------------------------------------ scaled dot-product attention
+struct AttentionFn : torch::autograd::Function<AttentionFn> {
+    static nott_attn_desc desc(const Tensor& q, const Tensor& k, bool causal, double scale) {
+        nott_attn_desc d{};
+        d.b = q.size(0); d.h = q.size(1); d.t = q.size(2); d.s = k.size(2); d.dh = q.size(3);
+        d.causal = causal; d.scale = scale;
+        return d;
+    }
+    static Tensor forward(AutogradContext* ctx, Tensor q, Tensor k, Tensor v, bool causal, double scale) {
+        q = contig(q); k = contig(k); v = contig(v);
+        const nott_attn_desc d = desc(q, k, causal, scale);
+        Tensor o = torch::empty_like(q);
+        Tensor lse = torch::empty({d.b, d.h, d.t}, q.options().dtype(torch::kFloat32));
+        nott_ctx c = bind(q);
+        check(nott_attention_fwd(c, &d, dtype_of(q), ptr(q), ptr(k), ptr(v), ptr(o), fptr(lse)), c,
+              "attention forward");
+        ctx->save_for_backward({q, k, v, o, lse});
+        ctx->saved_data["causal"] = causal;
+        ctx->saved_data["scale"] = scale;
+        return o;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor q = s[0], k = s[1], v = s[2], o = s[3], lse = s[4];
+        Tensor dO = contig(grads[0]);
+        const nott_attn_desc d = desc(q, k, ctx->saved_data["causal"].toBool(), ctx->saved_data["scale"].toDouble());
+        Tensor dq = torch::empty_like(q), dk = torch::empty_like(k), dv = torch::empty_like(v);
+        nott_ctx c = bind(q);
+        check(nott_attention_bwd(c, &d, dtype_of(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(dO), fptr(lse), ptr(dq),
+                                 ptr(dk), ptr(dv)),
+              c, "attention backward");
+        return {dq, dk, dv, Tensor(), Tensor()};
+    }
+};
+
+// ---------------------------------------------------------------- Fork
+// Two uses of one tensor (residual skip): backward sums the two gradients.
+struct ForkFn : torch::autograd::Function<ForkFn> {
+    static variable_list forward(AutogradContext*, Tensor x) { return {x.view(x.sizes()), x.view(x.sizes())}; }
+    static variable_list backward(AutogradContext*, variable_list grads) {
+        if (!grads[0].defined()) return {grads[1]};
+        if (!grads[1].defined()) return {grads[0]};
+        Tensor a = contig(grads[0]), b = contig(grads[1]);
+        Tensor out = torch::empty_like(a);
+        nott_ctx c = bind(a);
+        check(nott_add(c, dtype_of(a), a.numel(), ptr(a), ptr(b), ptr(out)), c, "fork backward");
+        return {out};
+    }
+};
+
+// Residual join y = a + b (block/details/blocks/residual.hpp:131).
+struct AddFn : torch::autograd::Function<AddFn> {
+    static Tensor forward(AutogradContext*, Tensor a, Tensor b) {
+        a = contig(a); b = contig(b);
+        Tensor y = torch::empty_like(a);
+        nott_ctx c = bind(a);
+        check(nott_add(c, dtype_of(a), a.numel(), ptr(a), ptr(b), ptr(y)), c, "add forward");
+        return y;
+    }
+    static variable_list backward(AutogradContext*, variable_list grads) { return {grads[0], grads[0]}; }
+};
+
+// -------------------------------------------------- softmax cross-entropy
+// Mean reduction, ignore_index -100, label smoothing (loss/details/ce.hpp:21-37).
+// One fused pass computes the loss and dlogits; backward scales dlogits by
+// the upstream gradient of the scalar loss.
+struct CrossEntropyFn : torch::autograd::Function<CrossEntropyFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor logits, Tensor labels, double smoothing) {
+        logits = contig(logits);
+        labels = contig(labels);
+        Tensor dl = torch::empty_like(logits);
+        Tensor loss = torch::empty({}, logits.options().dtype(torch::kFloat32));
+        nott_ctx c = bind(logits);
+        check(nott_softmax_xent_bwd(c, dtype_of(logits), logits.size(0), logits.size(1), ptr(logits),
+                                    labels.data_ptr<int64_t>(), smoothing, 1.0, ptr(dl), fptr(loss)),
+              c, "cross-entropy");
+        ctx->save_for_backward({dl});
+        return loss;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        Tensor dl = ctx->get_saved_variables()[0];
+        Tensor g = grads[0].to(torch::kFloat32).contiguous();
+        Tensor out = torch::empty_like(dl);
+        nott_ctx c = bind(dl);
+        check(nott_scale(c, dtype_of(dl), dl.numel(), ptr(dl), g.data_ptr<float>(), ptr(out)), c, "cross-entropy bwd");
+        return {out, Tensor(), Tensor()};
+    }
+};
+
+// ============================================================== modules
+// Options mirror the reference's descriptors (conv.hpp:39-49, fc.hpp:19-30,
+// pooling.hpp:41-57, batchnorm.hpp:22-36).  Parameters are fp32 masters; in
+// mixed precision (compute_dtype bf16) each weight also has a bf16 working
+// copy that the optimizer refreshes after every step.
+// Mirrors Nott::Layer::Conv2dOptions (conv.hpp:39-49; bias defaults to true).
+struct Conv2dOptions {
+    int64_t in_channels = 1, out_channels = 1;
+    std::array<int64_t, 2> kernel_size{3, 3}, stride{1, 1}, padding{0, 0}, dilation{1, 1};
+    bool bias = true;
+};
+
+class Conv2dImpl : public torch::nn::Module {
+public:
+    explicit Conv2dImpl(const Conv2dOptions& o)
+        : geom_{o.stride[0], o.stride[1], o.padding[0], o.padding[1], o.dilation[0], o.dilation[1]} {
+        weight = register_parameter(
+            "weight", torch::empty({o.out_channels, o.in_channels, o.kernel_size[0], o.kernel_size[1]}));
+        if (o.bias) this->bias = register_parameter("bias", torch::zeros({o.out_channels}));
+    }
+    Tensor forward(const Tensor& x) {
+        const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
+        return Conv2dFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
+    }
+    Tensor weight, bias, weight_compute;
+private:
+    std::vector<int64_t> geom_;
+};
+TORCH_MODULE(Conv2d);
+
+class LinearImpl : public torch::nn::Module {
+public:
+    LinearImpl(int64_t in, int64_t out, bool bias = true) {
+        weight = register_parameter("weight", torch::empty({out, in}));
+        if (bias) this->bias = register_parameter("bias", torch::zeros({out}));
+    }
+    Tensor forward(const Tensor& x) {
+        const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
+        return LinearFn::apply(x, weight, wc, or_absent(bias, weight));
+    }
+    Tensor weight, bias, weight_compute;
+};
+TORCH_MODULE(Linear);
+
+class BatchNorm2dImpl : public torch::nn::Module {
+public:
+    explicit BatchNorm2dImpl(int64_t c, double eps = 1e-5, double momentum = 0.1) : eps_(eps), momentum_(momentum) {
+        weight = register_parameter("weight", torch::ones({c}));
+        bias = register_parameter("bias", torch::zeros({c}));
+        running_mean = register_buffer("running_mean", torch::zeros({c}));
+        running_var = register_buffer("running_var", torch::ones({c}));
+    }
+    Tensor forward(const Tensor& x) {
+        if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        return BatchNorm2dFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
+    }
+    Tensor weight, bias, running_mean, running_var;
+private:
+    double eps_, momentum_;
+};
+TORCH_MODULE(BatchNorm2d);
+
+inline Tensor relu(const Tensor& x) { return ReluFn::apply(x); }
+
+inline Tensor max_pool2d(const Tensor& x, int64_t k, int64_t stride, int64_t pad = 0, bool ceil_mode = false) {
+    return MaxPool2dFn::apply(x, std::vector<int64_t>{k, k, stride, stride, pad, pad, 1, 1, ceil_mode ? 1 : 0});
+}
+
+inline Tensor cross_entropy(const Tensor& logits, const Tensor& labels, double label_smoothing = 0.0) {
+    return CrossEntropyFn::apply(logits, labels, label_smoothing);
+}
+
+// Kaiming-uniform (HeUniform: kaiming_uniform_(a=0, fan_in, relu)) and bias
+// zero, reference initialization/apply.hpp:10-17,45-51; drawn from a torch
+// CPU generator seeded by the caller.
+inline void he_uniform_(Tensor& w, torch::Generator& gen) {
+    torch::NoGradGuard ng;
+    const int64_t fan_in = w.numel() / w.size(0);
+    const double bound = std::sqrt(6.0 / (double)fan_in);
+    Tensor cpu = torch::empty(w.sizes(), torch::kFloat32).uniform_(-bound, bound, gen);
+    w.copy_(cpu);
+}
+
+// ============================================================ optimizer
+// Fused Adam / AdamW over one flat arena (reference optimizer/details/adam.hpp:
+// 63-154, 159-250; stepped at core.hpp:3820, zero_grad(false) at :3823).
+// Every parameter and its gradient are re-pointed into flat fp32 buffers,
+// so one nott_adam_step launch updates all of them, then zeroes the grads.
+// Mixed precision: bf16 working copies of the given weights live in a flat
+// bf16 arena and are refreshed with one nott_cast after each step.
+class FusedAdam {
+public:
+    struct Options {
+        double lr = 1e-3, beta1 = 0.9, beta2 = 0.999, eps = 1e-8, weight_decay = 0.0;
+        bool decoupled = false;   // false: Adam (L2), true: AdamW
+    };
+    FusedAdam(std::vector<Tensor> params, Options o, std::vector<Tensor*> bf16_copies = {},
+              std::vector<Tensor> bf16_masters = {})
+        : o_(o) {
+        torch::NoGradGuard ng;
+        if (params.empty()) throw std::invalid_argument("FusedAdam: no parameters");
+        const auto dev = params[0].device();
+        int64_t total = 0;
+        std::vector<int64_t> off;
+        for (auto& p : params) {
+            off.push_back(total);
+            total += (p.numel() + 63) / 64 * 64;   // 256-byte aligned segments
+        }
+        auto fo = torch::TensorOptions().dtype(torch::kFloat32).device(dev);
+        P_ = torch::zeros({total}, fo);
+        G_ = torch::zeros({total}, fo);
+        M_ = torch::zeros({total}, fo);
+        V_ = torch::zeros({total}, fo);
+        for (size_t i = 0; i < params.size(); ++i) {
+            auto& p = params[i];
+            Tensor pv = P_.narrow(0, off[i], p.numel()).view(p.sizes());
+            pv.copy_(p.detach());
+            p.set_data(pv);
+            p.mutable_grad() = G_.narrow(0, off[i], p.numel()).view(p.sizes());
+        }
+        params_ = params;
+        // bf16 working copies: one arena aligned like the masters.
+        if (!bf16_copies.empty()) {
+            if (bf16_copies.size() != bf16_masters.size()) throw std::invalid_argument("FusedAdam: copy/master mismatch");
+            Pb_ = torch::zeros({total}, fo.dtype(torch::kBFloat16));
+            for (size_t j = 0; j < bf16_masters.size(); ++j) {
+                size_t i = 0;
+                while (i < params.size() && !params[i].is_same(bf16_masters[j])) ++i;
+                if (i == params.size()) throw std::invalid_argument("FusedAdam: bf16 master not among params");
+                *bf16_copies[j] = Pb_.narrow(0, off[i], params[i].numel()).view(params[i].sizes());
+            }
+            refresh_copies();
+        }
+    }
+    void step() {
+        ++t_;
+        nott_ctx c = bind(P_);
+        check(nott_adam_step(c, o_.decoupled ? 1 : 0, P_.numel(), ptr(P_), NOTT_F32, ptr(G_), NOTT_F32, fptr(M_),
+                             fptr(V_), o_.lr, o_.beta1, o_.beta2, o_.eps, o_.weight_decay, t_, 1),
+              c, "adam step");
+        if (Pb_.defined()) refresh_copies();
+    }
+    void zero_grad() {
+        nott_ctx c = bind(G_);
+        check(nott_zero(c, G_.numel() * 4, ptr(G_)), c, "zero_grad");
+    }
+    // Re-casts the bf16 working copies (after parameters were overwritten).
+    void refresh() {
+        if (Pb_.defined()) refresh_copies();
+    }
+    int64_t step_count() const { return t_; }
+    void set_lr(double lr) { o_.lr = lr; }
+    const Tensor& flat_params() const { return P_; }
+private:
+    void refresh_copies() {
+        nott_ctx c = bind(P_);
+        check(nott_cast(c, P_.numel(), ptr(P_), NOTT_F32, ptr(Pb_), NOTT_BF16), c, "bf16 copy");
+    }
+    Options o_;
+    std::vector<Tensor> params_;
+    Tensor P_, G_, M_, V_, Pb_;
+    int64_t t_ = 0;
+};
+
+}  // namespace HIP
+}  // namespace Nott

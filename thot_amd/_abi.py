@@ -80,6 +80,7 @@ SIGNATURES: dict[str, list] = {
     "nott_add": [vp, i32, i64, vp, vp, vp],
     "nott_cast": [vp, i64, vp, i32, vp, i32],
     "nott_zero": [vp, i64, vp],
+    "nott_scale": [vp, i32, i64, vp, fp, vp],
 }
 
 _RESTYPES = {

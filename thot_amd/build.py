@@ -66,6 +66,37 @@ def build_library(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB
 
 
+HOST_SRC = os.path.join(PKG_DIR, "host", "nott_host.cpp")
+
+
+def host_ext_path() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_nott_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_host(verbose: bool = True) -> str:
+    """Builds the C++ host layer (include/nott_hip/host.hpp) as a Python
+    extension with g++: host code only, every kernel lives in libnott_hip.so."""
+    import sysconfig
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    out = host_ext_path()
+    tmp = out + ".tmp"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+           "-DTORCH_EXTENSION_NAME=_nott_host", "-D_GLIBCXX_USE_CXX11_ABI=1",
+           f"-I{INCLUDE}", f"-I{tdir}/include", f"-I{tdir}/include/torch/csrc/api/include", "-I/opt/rocm/include",
+           "-I" + sysconfig.get_paths()["include"], HOST_SRC, "-o", tmp,
+           f"-L{PKG_DIR}", "-lnott_hip", f"-L{tdir}/lib", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-ltorch_hip", "-ltorch_python", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tdir}/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host extension build failed:\n{r.stderr[-6000:]}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
+    return out
+
+
 def clean() -> None:
     shutil.rmtree(BUILD, ignore_errors=True)
     if os.path.exists(LIB):
@@ -74,3 +105,5 @@ def clean() -> None:
 
 if __name__ == "__main__":
     build_library()
+    if "--lib-only" not in sys.argv:
+        build_host()

@@ -110,6 +110,13 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ p
     if (i < ntail) tail[i] = 0;
 }
 
+template <typename T>
+__global__ __launch_bounds__(kThreads) void scale_kernel(const T* __restrict__ x, const float* __restrict__ scale,
+                                                         T* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) Io<T>::st(y, i, Io<T>::ld(x, i) * scale[0]);
+}
+
 // One wave per (n, c) plane: mean over hw.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void avgpool_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
@@ -198,6 +205,22 @@ int nott_zero(nott_ctx ctx, int64_t bytes, void* dst) {
     hipLaunchKernelGGL(zero_kernel, dim3((unsigned)nott::ceil_div(work, kThreads)), dim3(kThreads), 0, ctx->stream,
                        static_cast<uint32_t*>(dst), nwords, tail, ntail);
     return nott::launch_status(ctx, "zero");
+}
+
+int nott_scale(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* x, const float* scale, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n >= 0, "nott_scale: bad dtype or size");
+    if (n == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && scale && y, "nott_scale: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const dim3 grid((unsigned)nott::ceil_div(n, kThreads));
+    if (dtype == NOTT_F32)
+        hipLaunchKernelGGL(scale_kernel<float>, grid, dim3(kThreads), 0, ctx->stream, static_cast<const float*>(x), scale,
+                           static_cast<float*>(y), n);
+    else
+        hipLaunchKernelGGL(scale_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream, static_cast<const bf16_t*>(x),
+                           scale, static_cast<bf16_t*>(y), n);
+    return nott::launch_status(ctx, "scale");
 }
 
 int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw, const void* x, void* y) {
