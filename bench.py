@@ -11,13 +11,18 @@ one batch of synthetic input already resident in HBM:
   ln_bwd    LayerNorm backward 16384x1024 (configs[2]a).  GB/s.
   xent      fused softmax-CE gradient 16384x32000 (configs[2]b).  GB/s.
   adamw     fused AdamW over a flat 1e8-parameter buffer (configs[2]c).  GB/s.
+  mha_bwd   causal MHA backward with projection grads.  TFLOP/s.
+  small_cnn configs[0] training step, batch 64 (fp32).  samples/s.
+  resnet18  configs[4] training step, batch 64 (bf16 or fp32).  samples/s.
 
 Besides `value`, the line carries `roofline` for the dominant kernel (its
 algorithmic work per launch over its HIP-event-timed launch duration on the
 launch stream) and `cpu_baseline`: the reference's own libtorch CPU path
 (oracle/_ref, kind "reference") or the plain-C oracle (kind "port"), timed on
-a bounded sample on this host's cores.  `extra` reports the LayerNorm-backward
-and AdamW bandwidth legs that BASELINE's metric also names.
+a bounded sample on this host's cores.  `extra` reports the other legs the
+metric names: LayerNorm-backward, AdamW and CE-gradient bandwidth (fp32 and
+bf16), conv backward in fp32, MHA backward, and the configs[0] / configs[4]
+training steps in samples/s (with their own CPU baselines).
 """
 from __future__ import annotations
 
@@ -34,6 +39,17 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
 METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HBM)"
+
+
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each divided by the factor
+# the same counter reads for a plain device copy of known size.  Keyed by
+# (workload, dtype, kernel); None where no pass has been recorded.
+TRAFFIC = {}
+
+
+def traffic_for(workload, dtype, kernel):
+    return TRAFFIC.get((workload, dtype, kernel))
 
 
 def host_cores() -> int:
@@ -128,7 +144,7 @@ class ConvBwd(Workload):
         w = f32(g.standard_normal((self.K, self.C, 3, 3)) / math.sqrt(self.C * 9))
         dy = f32(g.standard_normal((n, self.K, self.H, self.W)))
         sec = ref.conv2d_bwd_time(d, x, w, dy, 1)
-        iters = max(1, min(50, int(budget_s / max(sec, 1e-6))))
+        iters = max(1, min(500, int(budget_s / max(sec, 1e-6))))
         sec = ref.conv2d_bwd_time(d, x, w, dy, iters)
         flop = 2 * 2.0 * n * self.H * self.W * self.K * self.C * 9
         return {"value": flop / sec / 1e12, "unit": "TFLOP/s", "cores": ref.get_threads(), "kind": "reference",
@@ -234,7 +250,114 @@ class AdamW(Workload):
                           f"{sec * 1e3:.1f} ms"}
 
 
-WORKLOADS = {"conv_bwd": ConvBwd, "ln_bwd": LnBwd, "xent": Xent, "adamw": AdamW}
+class TrainStep(Workload):
+    """One full training step (forward, CE mean, backward, fused Adam/AdamW,
+    zero_grad) through the C++ host layer: configs[0] small CNN (fp32, Adam)
+    or configs[4] ResNet-18 (AdamW; fp32 or bf16 mixed precision), batch 64."""
+    unit = "samples/s"
+    bound = "mfma"
+    BATCH = 64
+
+    def __init__(self, dtype, model):
+        self.dtype = dtype
+        self.name = model
+
+    def setup(self, torch, ops):
+        import importlib
+        host = importlib.import_module("thot_amd._nott_host")
+        g = torch.Generator(device="cuda").manual_seed(4)
+        if self.name == "small_cnn":
+            self.tr = host.SmallCNNTrainer(0, 0, 1e-3)
+            self.x = torch.rand((self.BATCH, 1, 28, 28), generator=g, device="cuda")
+            self.y = torch.randint(0, 10, (self.BATCH,), generator=g, device="cuda")
+            # forward 2*MACs: conv1 1*32*9*784, conv2 32*64*9*196, fc 3136*128 + 128*10; training ~ 3x forward
+            self.flop_sample = 3 * 2.0 * (32 * 9 * 784 + 32 * 64 * 9 * 196 + 3136 * 128 + 128 * 10)
+        else:
+            self.tr = host.ResNet18Trainer(0, 0, self.dtype == "bf16", 1e-3, 1e-2, 1000)
+            self.x = torch.rand((self.BATCH, 3, 224, 224), generator=g, device="cuda")
+            self.y = torch.randint(0, 1000, (self.BATCH,), generator=g, device="cuda")
+            self.flop_sample = 3 * 2 * 1.814e9   # ResNet-18 at 224^2: 1.814 GMAC forward
+        self.tr.step(self.x, self.y)
+
+    def step(self):
+        self.tr.step(self.x, self.y)
+
+    def work_per_step(self):
+        return self.BATCH
+
+    def cpu_baseline(self, budget_s):
+        from oracle_lib import Ref
+        if not Ref.available():
+            return None
+        ref = Ref()
+        ref.set_threads(host_cores())
+        batch = 64 if self.name == "small_cnn" else 8
+        sec = ref.train_step_time(self.name, batch, 1)
+        iters = max(1, min(200, int(budget_s / max(sec, 1e-6))))
+        sec = ref.train_step_time(self.name, batch, iters)
+        what = "configs[0] small CNN + Adam" if self.name == "small_cnn" else "configs[4] ResNet-18 + AdamW"
+        return {"value": batch / sec, "unit": "samples/s", "cores": ref.get_threads(), "kind": "reference",
+                "sample": f"{what}, fp32 libtorch CPU step built from Nott's layer descriptors, batch {batch}, "
+                          f"{iters} steps x {sec * 1e3:.1f} ms"}
+
+
+class MhaBwd(Workload):
+    """causal multi-head attention backward, bf16, B=8, H=16,
+    T=1024, dh=64, with the projection-weight gradients of the 1024->3x1024
+    input and 1024->1024 output projections.  One step: output-projection
+    backward, head split of dO, attention backward, head merge of dq/dk/dv,
+    input-projection backward.  Work: 34.36 GFLOP causal core (dV, dP, dQ, dK
+    GEMMs) + 137.44 GFLOP projections."""
+    name = "mha_bwd"
+    unit = "TFLOP/s"
+    bound = "mfma"
+    B, H, T, DH = 8, 16, 1024, 64
+
+    def __init__(self, dtype):
+        self.dtype = dtype
+
+    def setup(self, torch, ops):
+        self.torch, self.ops = torch, ops
+        dt = torch.bfloat16 if self.dtype == "bf16" else torch.float32
+        B, H, T, DH = self.B, self.H, self.T, self.DH
+        E = H * DH
+        g = torch.Generator(device="cuda").manual_seed(5)
+        self.x = torch.randn((B * T, E), generator=g, device="cuda").to(dt)
+        self.w_in = (0.02 * torch.randn((3 * E, E), generator=g, device="cuda")).to(dt)
+        self.w_out = (0.02 * torch.randn((E, E), generator=g, device="cuda")).to(dt)
+        self.d = ops.attn_desc(B, H, T, T, DH, True)
+        qkv = torch.randn((3, B, H, T, DH), generator=g, device="cuda").to(dt)
+        self.q, self.k, self.v = qkv[0].contiguous(), qkv[1].contiguous(), qkv[2].contiguous()
+        self.o, self.lse = ops.attention_fwd(self.q, self.k, self.v, self.d)
+        self.attn_out = self.o.permute(0, 2, 1, 3).reshape(B * T, E).contiguous()
+        self.dy = torch.randn((B * T, E), generator=g, device="cuda").to(dt)
+        self.dw_in = torch.empty((3 * E, E), device="cuda")
+        self.db_in = torch.empty((3 * E,), device="cuda")
+        self.dw_out = torch.empty((E, E), device="cuda")
+        self.db_out = torch.empty((E,), device="cuda")
+        self.core_flop = 4 * 2.0 * B * H * DH * (T * (T + 1) / 2)
+        self.proj_flop = 2 * 2.0 * B * T * E * 3 * E + 2 * 2.0 * B * T * E * E
+        self.ev_a = [None, None]
+
+    def step(self):
+        torch, ops = self.torch, self.ops
+        B, H, T, DH = self.B, self.H, self.T, self.DH
+        dattn, _, _ = ops.linear_bwd(self.dy, self.attn_out, self.w_out, dw=self.dw_out, db=self.db_out)
+        dO = dattn.view(B, T, H, DH).permute(0, 2, 1, 3).contiguous()
+        if self.ev_a[0] is not None:
+            self.ev_a[0].record()
+        dq, dk, dv = ops.attention_bwd(self.q, self.k, self.v, self.o, dO, self.lse, self.d)
+        if self.ev_a[1] is not None:
+            self.ev_a[1].record()
+        dqkv = torch.stack((dq, dk, dv), 0).permute(1, 3, 0, 2, 4).reshape(B * T, 3 * H * DH)
+        ops.linear_bwd(dqkv, self.x, self.w_in, dw=self.dw_in, db=self.db_in)
+
+    def work_per_step(self):
+        return self.core_flop + self.proj_flop
+
+
+WORKLOADS = {"conv_bwd": ConvBwd, "ln_bwd": LnBwd, "xent": Xent, "adamw": AdamW, "mha_bwd": MhaBwd,
+             "small_cnn": lambda dt: TrainStep(dt, "small_cnn"), "resnet18": lambda dt: TrainStep(dt, "resnet18")}
 
 
 def time_workload(torch, wl, steps, warmup):
@@ -302,6 +425,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for cpu_baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run 3 plain 256 MiB device copies (the known-size kernel that calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -316,8 +442,15 @@ def main():
         sys.exit(2)
     torch.cuda.set_device(0)
     sys.path.insert(0, os.path.join(REPO, "tests"))
+    if args.copy_probe:
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
-    dtype = args.dtype or ("bf16" if args.workload == "conv_bwd" else "f32")
+    dtype = args.dtype or ("f32" if args.workload in ("ln_bwd", "xent", "adamw", "small_cnn") else "bf16")
     wl = WORKLOADS[args.workload](dtype)
     wl.setup(torch, ops)
     wl.ev0 = wl.ev1 = None
@@ -332,30 +465,81 @@ def main():
         ach = wl.flop_one / (per[dom] * 1e-3) / 1e12
         peak = MFMA_PEAK_TFLOPS[dtype]
         roof = {"bound": "mfma", "kernel": f"conv2d_{dom}", "achieved": round(ach, 2), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic_for("conv_bwd", dtype, dom),
                 "per_kernel_ms": {k: round(v, 4) for k, v in per.items()},
                 "per_kernel_tflops": {k: round(wl.flop_one / (v * 1e-3) / 1e12, 2) for k, v in per.items()}}
         metric_part = "conv-bwd TFLOP/s"
         cfg = {"workload": "conv2d_bwd (BASELINE configs[1])", "n": wl.N, "c_in": wl.C, "c_out": wl.K,
                "hw": wl.H, "kernel": "3x3 s1 p1", "layout": "NCHW", "bias": False}
+    elif args.workload == "mha_bwd":
+        kms = kernel_ms(torch, wl, args.steps, ["ev_a"])["ev_a"]
+        value = value_per_s / 1e12
+        ach = wl.core_flop / (kms * 1e-3) / 1e12
+        peak = MFMA_PEAK_TFLOPS[dtype]
+        roof = {"bound": "mfma", "kernel": "attention_bwd (dq + dkdv)", "achieved": round(ach, 2), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None, "launch_ms": round(kms, 4)}
+        metric_part = "MHA-bwd TFLOP/s"
+        cfg = {"workload": "mha_bwd (BASELINE configs[3])", "b": wl.B, "heads": wl.H, "t": wl.T, "dh": wl.DH,
+               "causal": True, "projections": "1024->3x1024 in, 1024->1024 out"}
+    elif args.workload in ("small_cnn", "resnet18"):
+        value = value_per_s
+        ach = wl.flop_sample * value / 1e12
+        peak = MFMA_PEAK_TFLOPS[dtype]
+        roof = {"bound": "mfma", "kernel": "whole training step (model FLOPs, ~3x forward)", "achieved": round(ach, 2),
+                "peak": peak, "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None}
+        metric_part = "train samples/s"
+        cfg = {"workload": f"{wl.name} training step (BASELINE configs[{0 if wl.name == 'small_cnn' else 4}])",
+               "batch": wl.BATCH, "optimizer": "Adam" if wl.name == "small_cnn" else "AdamW"}
     else:
         kms = simple_kernel_ms(torch, wl, args.steps)
         value = wl.work_per_step() / (ms * 1e-3) / 1e9
         ach = wl.work_per_step() / (kms * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": wl.name, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "launch_ms": round(kms, 4)}
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_for(wl.name, dtype, None),
+                "launch_ms": round(kms, 4)}
         metric_part = {"ln_bwd": "LN-bwd GB/s", "xent": "CE-grad GB/s", "adamw": "AdamW GB/s"}[wl.name]
         cfg = {"workload": wl.name}
 
     extra = {}
     if not args.no_extra and args.workload == "conv_bwd":
-        for nm, cls in (("ln_bwd", LnBwd), ("adamw", AdamW)):
+        del wl.x, wl.dy, wl.dx
+        torch.cuda.empty_cache()
+        for nm, cls in (("ln_bwd", LnBwd), ("adamw", AdamW), ("xent", Xent)):
             for dt in ("f32", "bf16"):
                 leg, lms, lk, gbs = run_bandwidth_leg(torch, ops, cls, dt, args.steps, args.warmup)
                 extra[f"{nm}_{dt}"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                        "kernel_ms": round(lk, 4)}
                 del leg
                 torch.cuda.empty_cache()
+        leg = ConvBwd("f32")
+        leg.setup(torch, ops)
+        lms = time_workload(torch, leg, max(3, args.steps // 4), 1)
+        extra["conv_bwd_f32"] = {"TFLOP/s": round(leg.work_per_step() / (lms * 1e-3) / 1e12, 2),
+                                 "frac_mfma": round(leg.work_per_step() / (lms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f32"], 4)}
+        del leg
+        torch.cuda.empty_cache()
+        leg = MhaBwd("bf16")
+        leg.setup(torch, ops)
+        lms = time_workload(torch, leg, args.steps, args.warmup)
+        ams = kernel_ms(torch, leg, args.steps, ["ev_a"])["ev_a"]
+        extra["mha_bwd_bf16"] = {"TFLOP/s": round(leg.work_per_step() / (lms * 1e-3) / 1e12, 2), "ms": round(lms, 4),
+                                 "core_TFLOP/s": round(leg.core_flop / (ams * 1e-3) / 1e12, 2)}
+        del leg
+        torch.cuda.empty_cache()
+        for model, dt in (("small_cnn", "f32"), ("resnet18", "bf16"), ("resnet18", "f32")):
+            leg = TrainStep(dt, model)
+            leg.setup(torch, ops)
+            lms = time_workload(torch, leg, args.steps, args.warmup)
+            rec = {"samples/s": round(leg.BATCH / (lms * 1e-3), 1), "ms_per_step": round(lms, 3),
+                   "batch": leg.BATCH}
+            if not args.no_cpu and dt == "f32":
+                try:
+                    rec["cpu_baseline"] = leg.cpu_baseline(args.cpu_budget / 2)
+                except Exception as e:
+                    rec["cpu_baseline"] = {"error": repr(e)}
+            extra[f"{model}_{dt}"] = rec
+            del leg
+            torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:

@@ -89,6 +89,156 @@ Nott::Layer::Details::Conv2dDescriptor conv_descriptor(const nott_conv2d_desc* d
     return desc;
 }
 
+// A chain of registered layers applied in order, each followed by its
+// activation (Model::forward applies registered_layer.activation after the
+// module, core.hpp:1719-1790).
+struct Chain {
+    Owner owner;
+    std::vector<Nott::Layer::Details::RegisteredLayer> layers;
+    size_t next = 0;
+    template <class D>
+    size_t add(const D& d) {
+        layers.push_back(Nott::Layer::Details::build_registered_layer(owner, d, next++));
+        return layers.size() - 1;
+    }
+    torch::Tensor run(size_t i, torch::Tensor x) {
+        auto y = layers[i].forward(std::move(x));
+        return Nott::Activation::Details::apply(layers[i].activation, std::move(y));
+    }
+};
+
+Nott::Layer::Details::Conv2dDescriptor conv_d(int64_t ci, int64_t co, int64_t k, int64_t stride, int64_t pad,
+                                              bool bias, bool relu) {
+    Nott::Layer::Details::Conv2dDescriptor d;
+    d.options.in_channels = ci;
+    d.options.out_channels = co;
+    d.options.kernel_size = {k, k};
+    d.options.stride = {stride, stride};
+    d.options.padding = {pad, pad};
+    d.options.bias = bias;
+    d.activation = relu ? Nott::Activation::ReLU : Nott::Activation::Identity;
+    d.initialization = Nott::Initialization::HeUniform;
+    return d;
+}
+
+Nott::Layer::Details::BatchNorm2dDescriptor bn_d(int64_t c, bool relu) {
+    Nott::Layer::Details::BatchNorm2dDescriptor d;
+    d.options.num_features = c;
+    d.activation = relu ? Nott::Activation::ReLU : Nott::Activation::Identity;
+    return d;
+}
+
+Nott::Layer::Details::FCDescriptor fc_d(int64_t in, int64_t out, bool relu) {
+    Nott::Layer::Details::FCDescriptor d;
+    d.options.in_features = in;
+    d.options.out_features = out;
+    d.activation = relu ? Nott::Activation::ReLU : Nott::Activation::Identity;
+    d.initialization = Nott::Initialization::HeUniform;
+    return d;
+}
+
+Nott::Layer::Details::PoolingDescriptor maxpool_d(int64_t k, int64_t stride, int64_t pad) {
+    Nott::Layer::Details::MaxPool2dOptions o;
+    o.kernel_size = {k, k};
+    o.stride = {stride, stride};
+    o.padding = {pad, pad};
+    return Nott::Layer::Details::PoolingDescriptor{o};
+}
+
+// Conv(1->32)+ReLU+MaxPool2 -> Conv(32->64)+ReLU+MaxPool2 -> FC(3136->128)+ReLU -> FC(128->10).
+struct SmallCnnRef {
+    Chain c;
+    SmallCnnRef() {
+        c.add(conv_d(1, 32, 3, 1, 1, true, true));
+        c.add(maxpool_d(2, 2, 0));
+        c.add(conv_d(32, 64, 3, 1, 1, true, true));
+        c.add(maxpool_d(2, 2, 0));
+        c.add(Nott::Layer::Details::FlattenDescriptor{});
+        c.add(fc_d(3136, 128, true));
+        c.add(fc_d(128, 10, false));
+    }
+    torch::Tensor forward(torch::Tensor x) {
+        for (size_t i = 0; i < c.layers.size(); ++i) x = c.run(i, x);
+        return x;
+    }
+};
+
+// ResNet-18 (7x7/2 stem + BN + ReLU + 3x3/2 max-pool, 4 stages of
+// 2 basic blocks, global average pool, FC 512->1000) from the same layer
+// descriptors; the residual add and the post-add ReLU are what Nott's
+// residual block applies (block/details/blocks/residual.hpp:131-132).
+struct ResNet18Ref {
+    Chain c;
+    struct Block { size_t c0, b0, c1, b1; long sc = -1, sb = -1; };
+    size_t stem, stem_bn, pool, gap, flat, fc;
+    std::vector<Block> blocks;
+    ResNet18Ref() {
+        stem = c.add(conv_d(3, 64, 7, 2, 3, false, false));
+        stem_bn = c.add(bn_d(64, true));
+        pool = c.add(maxpool_d(3, 2, 1));
+        int64_t in = 64;
+        const int64_t widths[4] = {64, 128, 256, 512};
+        for (int st = 0; st < 4; ++st) {
+            for (int j = 0; j < 2; ++j) {
+                const int64_t out = widths[st], stride = (st > 0 && j == 0) ? 2 : 1;
+                Block b;
+                b.c0 = c.add(conv_d(in, out, 3, stride, 1, false, false));
+                b.b0 = c.add(bn_d(out, true));
+                b.c1 = c.add(conv_d(out, out, 3, 1, 1, false, false));
+                b.b1 = c.add(bn_d(out, false));
+                if (stride != 1 || in != out) {
+                    b.sc = (long)c.add(conv_d(in, out, 1, stride, 0, false, false));
+                    b.sb = (long)c.add(bn_d(out, false));
+                }
+                blocks.push_back(b);
+                in = out;
+            }
+        }
+        Nott::Layer::Details::AdaptiveAvgPool2dOptions ao;
+        ao.output_size = {1, 1};
+        gap = c.add(Nott::Layer::Details::PoolingDescriptor{ao});
+        flat = c.add(Nott::Layer::Details::FlattenDescriptor{});
+        fc = c.add(fc_d(512, 1000, false));
+    }
+    torch::Tensor forward(torch::Tensor x) {
+        x = c.run(pool, c.run(stem_bn, c.run(stem, x)));
+        for (auto& b : blocks) {
+            auto y = c.run(b.b1, c.run(b.c1, c.run(b.b0, c.run(b.c0, x))));
+            auto s = b.sc >= 0 ? c.run((size_t)b.sb, c.run((size_t)b.sc, x)) : x;
+            x = torch::relu(y + s);
+        }
+        return c.run(fc, c.run(flat, c.run(gap, x)));
+    }
+};
+
+template <class Net>
+double time_train_steps(Net& net, torch::Tensor x, torch::Tensor y, bool decoupled, int iters) {
+    net.c.owner.train();
+    std::vector<torch::Tensor> params = net.c.owner.parameters();
+    Nott::Loss::Details::CrossEntropyDescriptor ce;
+    auto run = [&](auto& opt) {
+        auto step = [&] {   // core.hpp:3757-3823: forward, loss, backward, step, zero_grad
+            auto loss = Nott::Loss::Details::compute(ce, net.forward(x), y);
+            loss.backward();
+            opt.step();
+            opt.zero_grad(false);
+        };
+        step();   // warm-up (also initialises the optimizer state)
+        auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) step();
+        auto t1 = std::chrono::steady_clock::now();
+        return std::chrono::duration<double>(t1 - t0).count() / iters;
+    };
+    if (decoupled) {
+        Nott::Optimizer::Details::AdamWOptions o;
+        Nott::Optimizer::Details::AdamW opt(params, Nott::Optimizer::Details::to_torch_options(o));
+        return run(opt);
+    }
+    Nott::Optimizer::Details::AdamOptions o;
+    Nott::Optimizer::Details::Adam opt(params, Nott::Optimizer::Details::to_torch_options(o));
+    return run(opt);
+}
+
 }  // namespace
 
 extern "C" {
@@ -421,6 +571,29 @@ int ref_mha(int64_t b, int64_t t, int64_t e, int64_t heads, int causal, int with
                 out(grad_of(*mha, "v_proj.bias"), dbv);
                 out(grad_of(*mha, "out_proj.bias"), dbo);
             }
+        }
+    });
+}
+
+// Times `iters` full fp32 training steps on the CPU (forward, CE mean,
+// backward, Adam (model 0, configs[0]) or AdamW (model 1, configs[4]) step,
+// zero_grad) at the given batch; seconds per step in *sec.  Inputs
+// uniform[0,1), labels uniform, weights HeUniform from torch's CPU generator.
+int ref_train_step_time(int model, int64_t batch, int iters, double* sec) {
+    return guarded([&] {
+        torch::manual_seed(0);
+        if (model == 0) {
+            SmallCnnRef net;
+            auto x = torch::rand({batch, 1, 28, 28});
+            auto y = torch::randint(0, 10, {batch}, torch::kInt64);
+            *sec = time_train_steps(net, x, y, false, iters);
+        } else if (model == 1) {
+            ResNet18Ref net;
+            auto x = torch::rand({batch, 3, 224, 224});
+            auto y = torch::randint(0, 1000, {batch}, torch::kInt64);
+            *sec = time_train_steps(net, x, y, true, iters);
+        } else {
+            throw std::invalid_argument("model must be 0 (small CNN) or 1 (ResNet-18)");
         }
     });
 }

@@ -326,6 +326,14 @@ class Ref:
         self._ok(self.lib.ref_adamw_time(i64(n), C.c_int(iters), C.byref(sec)))
         return sec.value
 
+    def train_step_time(self, model: str, batch: int, iters: int) -> float:
+        """Seconds per fp32 CPU training step of "small_cnn" or
+        "resnet18" built from the reference's layer descriptors."""
+        sec = C.c_double()
+        which = {"small_cnn": 0, "resnet18": 1}[model]
+        self._ok(self.lib.ref_train_step_time(C.c_int(which), i64(batch), C.c_int(iters), C.byref(sec)))
+        return sec.value
+
     def attention(self, d: AttnDesc, q, k, v, dO):
         o = np.empty((d.b, d.h, d.t, d.dh), np.float32)
         dq = np.empty((d.b, d.h, d.t, d.dh), np.float32)
