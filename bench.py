@@ -144,7 +144,7 @@ class ConvBwd(Workload):
         w = f32(g.standard_normal((self.K, self.C, 3, 3)) / math.sqrt(self.C * 9))
         dy = f32(g.standard_normal((n, self.K, self.H, self.W)))
         sec = ref.conv2d_bwd_time(d, x, w, dy, 1)
-        iters = max(1, min(500, int(budget_s / max(sec, 1e-6))))
+        iters = max(1, min(20000, int(budget_s / max(sec, 1e-6))))
         sec = ref.conv2d_bwd_time(d, x, w, dy, iters)
         flop = 2 * 2.0 * n * self.H * self.W * self.K * self.C * 9
         return {"value": flop / sec / 1e12, "unit": "TFLOP/s", "cores": ref.get_threads(), "kind": "reference",
@@ -293,7 +293,7 @@ class TrainStep(Workload):
         ref.set_threads(host_cores())
         batch = 64 if self.name == "small_cnn" else 8
         sec = ref.train_step_time(self.name, batch, 1)
-        iters = max(1, min(200, int(budget_s / max(sec, 1e-6))))
+        iters = max(1, min(20000, int(budget_s / max(sec, 1e-6))))
         sec = ref.train_step_time(self.name, batch, iters)
         what = "configs[0] small CNN + Adam" if self.name == "small_cnn" else "configs[4] ResNet-18 + AdamW"
         return {"value": batch / sec, "unit": "samples/s", "cores": ref.get_threads(), "kind": "reference",
@@ -374,36 +374,39 @@ def time_workload(torch, wl, steps, warmup):
 
 
 def kernel_ms(torch, wl, steps, pairs_attr):
-    """Average duration of one launch group, from HIP events on torch's current
-    stream (the stream the C ABI launches on)."""
-    out = {}
-    totals = {k: 0.0 for k in pairs_attr}
+    """Average duration of each bracketed launch group, from HIP events recorded
+    on torch's current stream (the stream the C ABI launches on).  The steps
+    are queued back to back with one synchronisation at the end, so a start
+    event fires when the previous step's work drains, not when the host gets
+    round to the next launch."""
+    wl.step()
+    pairs = []
     for _ in range(steps):
-        pairs = {}
+        step_pairs = {}
         for k in pairs_attr:
-            pairs[k] = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-            getattr(wl, k)[0], getattr(wl, k)[1] = pairs[k]
+            step_pairs[k] = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            getattr(wl, k)[0], getattr(wl, k)[1] = step_pairs[k]
         wl.step()
-        torch.cuda.synchronize()
-        for k in pairs_attr:
-            totals[k] += pairs[k][0].elapsed_time(pairs[k][1])
+        pairs.append(step_pairs)
+    torch.cuda.synchronize()
+    out = {}
     for k in pairs_attr:
         getattr(wl, k)[0] = getattr(wl, k)[1] = None
-        out[k] = totals[k] / steps
+        out[k] = sum(p[k][0].elapsed_time(p[k][1]) for p in pairs) / steps
     return out
 
 
 def simple_kernel_ms(torch, wl, steps):
-    """Event-timed average of one whole step (for one-entry-point workloads)."""
+    """Event-timed average of one whole step (for one-entry-point workloads),
+    steps queued back to back on the launch stream."""
+    wl.step()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    tot = 0.0
+    e0.record()
     for _ in range(steps):
-        e0.record()
         wl.step()
-        e1.record()
-        torch.cuda.synchronize()
-        tot += e0.elapsed_time(e1)
-    return tot / steps
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def run_bandwidth_leg(torch, ops, cls, dtype, steps, warmup):

@@ -178,7 +178,8 @@ def test_batchnorm(ops, oracle, dt, shape):
 
 # -------------------------------------------------------------- layernorm
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("rows,d", [(2048, 1024), (37, 256), (5, 1000), (3, 3000), (64, 4)])
+@pytest.mark.parametrize("rows,d", [(2048, 1024), (37, 256), (5, 1000), (3, 3000), (64, 4), (4099, 512), (257, 2048),
+                                    (1029, 64)])
 def test_layernorm(ops, oracle, dt, rows, d):
     g = rng(rows + d)
     x = host_input(g.standard_normal((rows, d)), dt)

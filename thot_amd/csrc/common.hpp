@@ -126,22 +126,99 @@ template <> struct Vec4<bf16_t> {
     }
 };
 
+// One 16-byte group (4 fp32 or 8 bf16 elements) as floats.  NT = streaming
+// access (nontemporal: the line is not kept in the caches after use), for
+// data that is read or written exactly once.  raw() + unpack() split a load
+// so that a guarded load can be issued without converting inside the guard:
+// a conversion inside the branch makes the compiler wait for each load before
+// leaving it, which serialises a wave's loads.
+// (The fp32 raw type is f32x4, not u32x4: bit-casting u32x4 elements to
+// float makes this compiler split or drop parts of the 16-byte load.)
+template <typename T> struct Pack16;
+template <> struct Pack16<float> {
+    static constexpr int N = 4;
+    typedef f32x4 Raw;
+    template <bool NT = false>
+    static __device__ __forceinline__ Raw raw(const float* p) {
+        const Raw* q = reinterpret_cast<const Raw*>(p);
+        return NT ? __builtin_nontemporal_load(q) : *q;
+    }
+    static __device__ __forceinline__ void unpack(const Raw& u, float (&v)[4]) {
+        v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+    }
+    template <bool NT = false>
+    static __device__ __forceinline__ void ld(const float* p, float (&v)[4]) {
+        const f32x4* q = reinterpret_cast<const f32x4*>(p);
+        const f32x4 t = NT ? __builtin_nontemporal_load(q) : *q;
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+    template <bool NT = false>
+    static __device__ __forceinline__ void st(float* p, const float (&v)[4]) {
+        const f32x4 t = {v[0], v[1], v[2], v[3]};
+        f32x4* q = reinterpret_cast<f32x4*>(p);
+        if (NT) __builtin_nontemporal_store(t, q);
+        else *q = t;
+    }
+};
+template <> struct Pack16<bf16_t> {
+    static constexpr int N = 8;
+    typedef u32x4 Raw;
+    template <bool NT = false>
+    static __device__ __forceinline__ Raw raw(const bf16_t* p) {
+        const Raw* q = reinterpret_cast<const Raw*>(p);
+        return NT ? __builtin_nontemporal_load(q) : *q;
+    }
+    static __device__ __forceinline__ void unpack(const Raw& u, float (&v)[8]) {
+        v[0] = __builtin_bit_cast(float, u.x << 16); v[1] = __builtin_bit_cast(float, u.x & 0xffff0000u);
+        v[2] = __builtin_bit_cast(float, u.y << 16); v[3] = __builtin_bit_cast(float, u.y & 0xffff0000u);
+        v[4] = __builtin_bit_cast(float, u.z << 16); v[5] = __builtin_bit_cast(float, u.z & 0xffff0000u);
+        v[6] = __builtin_bit_cast(float, u.w << 16); v[7] = __builtin_bit_cast(float, u.w & 0xffff0000u);
+    }
+    template <bool NT = false>
+    static __device__ __forceinline__ void ld(const bf16_t* p, float (&v)[8]) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(p);
+        const u32x4 u = NT ? __builtin_nontemporal_load(q) : *q;
+        v[0] = __builtin_bit_cast(float, u.x << 16); v[1] = __builtin_bit_cast(float, u.x & 0xffff0000u);
+        v[2] = __builtin_bit_cast(float, u.y << 16); v[3] = __builtin_bit_cast(float, u.y & 0xffff0000u);
+        v[4] = __builtin_bit_cast(float, u.z << 16); v[5] = __builtin_bit_cast(float, u.z & 0xffff0000u);
+        v[6] = __builtin_bit_cast(float, u.w << 16); v[7] = __builtin_bit_cast(float, u.w & 0xffff0000u);
+    }
+    template <bool NT = false>
+    static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[8]) {
+        u32x4 u;
+        u.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        u.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        u.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
+        u.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+        u32x4* q = reinterpret_cast<u32x4*>(p);
+        if (NT) __builtin_nontemporal_store(u, q);
+        else *q = u;
+    }
+};
+
 // DPP move within a row of 16 lanes.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
+// Value of lane L (wave-uniform).
+template <int L>
+__device__ __forceinline__ float lane_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
+}
+
 // Full 64-lane sum; every lane receives the result.  Within a row of 16
-// lanes: DPP quad_perm / half-mirror / mirror; across rows: xor shuffles.
+// lanes: DPP quad_perm / half-mirror / mirror; across rows: lane reads.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
     v += dpp_f32<0x141>(v);  // row_half_mirror
     v += dpp_f32<0x140>(v);  // row_mirror
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    // Every lane of a 16-lane row now holds the row's sum; combine the four
+    // rows through scalar registers (no LDS round trip), in the order
+    // (r0 + r1) + (r2 + r3).
+    return (lane_f32<0>(v) + lane_f32<16>(v)) + (lane_f32<32>(v) + lane_f32<48>(v));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -149,9 +226,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_f32<0x4E>(v));
     v = fmaxf(v, dpp_f32<0x141>(v));
     v = fmaxf(v, dpp_f32<0x140>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    return fmaxf(fmaxf(lane_f32<0>(v), lane_f32<16>(v)), fmaxf(lane_f32<32>(v), lane_f32<48>(v)));
 }
 
 // Block-wide sum over NWAVES waves through LDS; all threads get the result.

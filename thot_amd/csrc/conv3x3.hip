@@ -589,20 +589,44 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
             }
 }
 
-// dw[k][c][tap] (+)= Σ_split ws[split][tap][k][c]
+// dw[k][c][tap] (+)= Σ_split ws[split][tap][k][c].  A block owns 64 float4
+// groups of the partial layout (lane = group, so each wave load is a 1 KB
+// coalesced run); its 4 waves take the splits round-robin with 8 loads in
+// flight each and combine in LDS in wave order, so the summation order is
+// fixed.  Requires c % 4 == 0 (the four floats of a group share kk and tap).
+constexpr int kWgReduceUnroll = 8;
 __global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* __restrict__ ws, int32_t splits,
                                                                    int32_t k, int32_t c, float* __restrict__ dw,
                                                                    int accumulate) {
+    __shared__ f32x4 red[4][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int64_t per = (int64_t)9 * k * c;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // i = (tap·k + kk)·c + cc
-    if (i >= per) return;
-    float s = 0.f;
-    for (int32_t z = 0; z < splits; ++z) s += ws[z * per + i];
+    const int64_t q = (int64_t)blockIdx.x * 64 + lane;   // float4 group: i = 4q = (tap·k + kk)·c + cc
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if (4 * q < per) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(ws) + q;
+        const int64_t zstride = per / 4;
+        int32_t z = wid;
+        for (; z + (kWgReduceUnroll - 1) * 4 < splits; z += kWgReduceUnroll * 4) {
+            f32x4 t[kWgReduceUnroll];
+#pragma unroll
+            for (int u = 0; u < kWgReduceUnroll; ++u) t[u] = src[(int64_t)(z + 4 * u) * zstride];
+#pragma unroll
+            for (int u = 0; u < kWgReduceUnroll; ++u) s += t[u];
+        }
+        for (; z < splits; z += 4) s += src[(int64_t)z * zstride];
+    }
+    red[wid][lane] = s;
+    __syncthreads();
+    if (wid != 0 || 4 * q >= per) return;
+    const f32x4 t = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    const int64_t i = 4 * q;
     const int32_t cc = (int32_t)(i % c);
     const int64_t rest = i / c;
     const int32_t kk = (int32_t)(rest % k), tap = (int32_t)(rest / k);
     float* o = dw + ((int64_t)kk * c + cc) * 9 + tap;
-    *o = accumulate ? *o + s : s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[9 * e] = accumulate ? o[9 * e] + t[e] : t[e];
 }
 
 
@@ -634,7 +658,7 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P>), dim3((unsigned)splits, (unsigned)tiles), dim3(kThreads), lds,
                        ctx->stream, x, dy, ws, p);
     const int64_t per = (int64_t)9 * p.k * p.c;
-    hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per, 256)), dim3(256), 0, ctx->stream, ws,
+    hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256), 0, ctx->stream, ws,
                        (int32_t)splits, p.k, p.c, dw, accumulate);
     return launch_status(ctx, "conv3x3_wgrad");
 }

@@ -13,29 +13,65 @@
 // kernel reduces them (deterministic order).
 #include "common.hpp"
 
+#include <initializer_list>
+
 namespace {
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kWaves = kThreads / 64;
-constexpr int kRowsInFlight = 2;
+// Rows a wave loads before it reduces: as many as fit 32 (fp32) or 64 (bf16)
+// VGPRs of row data per lane, at most 8 (d = 1024: 1 row fp32, 2 rows bf16,
+// i.e. 8 KB of x and dy in flight per wave; measured best at two 4-wave
+// blocks per CU).
+__host__ __device__ constexpr int rows_in_flight(int elem_bytes, int dpl) {
+    const int r = (elem_bytes == 2 ? 64 : 32) / (2 * dpl);
+    return r < 1 ? 1 : (r > 8 ? 8 : r);
+}
+constexpr int kReduceThreads = 1024;   // column reduction: 16 waves split the partial rows
+constexpr int kReduceWaves = kReduceThreads / 64;
+constexpr int kReduceUnroll = 8;
 
-// Column group g of lane `lane` covers columns [(g*64 + lane)*4, +4).
-template <typename T, int DPL>
+// Element e of a lane's DPL row values is column col(g, e) with g = e / G:
+// group g of lane `lane` covers the 16 bytes at columns [(g*64 + lane)*G, +G),
+// G = 4 (fp32) or 8 (bf16), so every wave access is a 1 KB coalesced run.
+template <typename T>
+__device__ __forceinline__ int64_t row_col(int lane, int e) {
+    constexpr int G = Pack16<T>::N;
+    return ((int64_t)(e / G) * 64 + lane) * G + e % G;
+}
+
+// Every lane issues all of its loads unconditionally (columns past d read
+// column 0 and are zeroed afterwards), so a row's loads stay in flight
+// together.
+template <typename T, int DPL, bool NT>
 __device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t d, int lane, float (&v)[DPL]) {
+    constexpr int G = Pack16<T>::N;
+    typename Pack16<T>::Raw raw[DPL / G > 0 ? DPL / G : 1];
 #pragma unroll
-    for (int g = 0; g < DPL / 4; ++g) {
-        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
-        f32x4 t = c0 < d ? Vec4<T>::ld(p + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
-        v[4 * g + 0] = t.x; v[4 * g + 1] = t.y; v[4 * g + 2] = t.z; v[4 * g + 3] = t.w;
+    for (int g = 0; g < DPL / G; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * G;
+        raw[g] = Pack16<T>::template raw<NT>(p + (c0 < d ? c0 : 0));
+    }
+#pragma unroll
+    for (int g = 0; g < DPL / G; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * G;
+        float t[G];
+        Pack16<T>::unpack(raw[g], t);
+#pragma unroll
+        for (int e = 0; e < G; ++e) v[G * g + e] = c0 < d ? t[e] : 0.f;
     }
 }
 
-template <typename T, int DPL>
+template <typename T, int DPL, bool NT>
 __device__ __forceinline__ void store_row(T* __restrict__ p, int64_t d, int lane, const float (&v)[DPL]) {
+    constexpr int G = Pack16<T>::N;
 #pragma unroll
-    for (int g = 0; g < DPL / 4; ++g) {
-        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
-        if (c0 < d) Vec4<T>::st(p + c0, f32x4{v[4 * g + 0], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]});
+    for (int g = 0; g < DPL / G; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * G;
+        float t[G];
+#pragma unroll
+        for (int e = 0; e < G; ++e) t[e] = v[G * g + e];
+        if (c0 < d) Pack16<T>::template st<NT>(p + c0, t);
     }
 }
 
@@ -46,30 +82,26 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
                                                           int64_t rows, int64_t d) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     float gm[DPL], bt[DPL];
-    load_row<T, DPL>(gamma, d, lane, gm);
-    load_row<T, DPL>(beta, d, lane, bt);
+    load_row<T, DPL, false>(gamma, d, lane, gm);
+    load_row<T, DPL, false>(beta, d, lane, bt);
     const float inv_d = 1.f / (float)d;
     for (int64_t r = (int64_t)blockIdx.x * kWaves + wid; r < rows; r += (int64_t)gridDim.x * kWaves) {
         float v[DPL];
-        load_row<T, DPL>(x + r * d, d, lane, v);
+        load_row<T, DPL, true>(x + r * d, d, lane, v);
         float s = 0.f;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) s += v[e];
         const float mu = wave_sum(s) * inv_d;
         float ss = 0.f;
 #pragma unroll
-        for (int g = 0; g < DPL / 4; ++g) {
-            const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float t = (c0 + e < d) ? v[4 * g + e] - mu : 0.f;
-                ss += t * t;
-            }
+        for (int e = 0; e < DPL; ++e) {
+            const float t = row_col<T>(lane, e) < d ? v[e] - mu : 0.f;
+            ss += t * t;
         }
         const float rs = 1.f / sqrtf(wave_sum(ss) * inv_d + eps);
 #pragma unroll
         for (int e = 0; e < DPL; ++e) v[e] = (v[e] - mu) * rs * gm[e] + bt[e];
-        store_row<T, DPL>(y + r * d, d, lane, v);
+        store_row<T, DPL, false>(y + r * d, d, lane, v);
         if (lane == 0) {
             mean[r] = mu;
             rstd[r] = rs;
@@ -85,24 +117,25 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     extern __shared__ float lds[];  // [kWaves][2][d]
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     float gm[DPL];
-    load_row<T, DPL>(gamma, d, lane, gm);
+    load_row<T, DPL, false>(gamma, d, lane, gm);
     float dg[DPL], db[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) dg[e] = db[e] = 0.f;
     const float inv_d = 1.f / (float)d;
+    constexpr int kRowsInFlight = rows_in_flight((int)sizeof(T), DPL);
     const int64_t stride = (int64_t)gridDim.x * kWaves * kRowsInFlight;
     for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wid) * kRowsInFlight; r0 < rows; r0 += stride) {
         float xv[kRowsInFlight][DPL], gv[kRowsInFlight][DPL];
         float mu[kRowsInFlight], rs[kRowsInFlight];
 #pragma unroll
         for (int i = 0; i < kRowsInFlight; ++i) {
-            const int64_t r = r0 + i;
-            if (r < rows) {
-                load_row<T, DPL>(x + r * d, d, lane, xv[i]);
-                load_row<T, DPL>(dy + r * d, d, lane, gv[i]);
-                mu[i] = mean[r];
-                rs[i] = rstd[r];
-            }
+            // Rows past the end re-read the last row (unconditional loads keep
+            // every row's loads in flight together); they are not stored.
+            const int64_t r = r0 + i < rows ? r0 + i : rows - 1;
+            load_row<T, DPL, true>(x + r * d, d, lane, xv[i]);
+            load_row<T, DPL, true>(dy + r * d, d, lane, gv[i]);
+            mu[i] = mean[r];
+            rs[i] = rstd[r];
         }
 #pragma unroll
         for (int i = 0; i < kRowsInFlight; ++i) {
@@ -125,19 +158,16 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
             sgx = wave_sum(sgx) * inv_d;
 #pragma unroll
             for (int e = 0; e < DPL; ++e) xv[i][e] = rs[i] * (gv[i][e] - sg - xv[i][e] * sgx);
-            store_row<T, DPL>(dx + r * d, d, lane, xv[i]);
+            store_row<T, DPL, true>(dx + r * d, d, lane, xv[i]);
         }
     }
     // Combine the waves' column sums and write this block's partial row.
 #pragma unroll
-    for (int g = 0; g < DPL / 4; ++g) {
-        const int64_t c0 = ((int64_t)g * 64 + lane) * 4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (c0 + e < d) {
-                lds[(wid * 2 + 0) * d + c0 + e] = dg[4 * g + e];
-                lds[(wid * 2 + 1) * d + c0 + e] = db[4 * g + e];
-            }
+    for (int e = 0; e < DPL; ++e) {
+        const int64_t col = row_col<T>(lane, e);
+        if (col < d) {
+            lds[(wid * 2 + 0) * d + col] = dg[e];
+            lds[(wid * 2 + 1) * d + col] = db[e];
         }
     }
     __syncthreads();
@@ -151,25 +181,40 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     }
 }
 
-// Sums `nparts` partial rows of 2·d floats into dgamma / dbeta.  One wave per
-// 64 columns of one output; 4 waves split the partial rows.
-__global__ __launch_bounds__(kThreads) void col_reduce_kernel(const float* __restrict__ partial, int64_t nparts,
-                                                              int64_t d, float* __restrict__ dgamma,
-                                                              float* __restrict__ dbeta, int accumulate) {
-    __shared__ float red[kWaves][64];
+// Sums `nparts` partial rows of 2·d floats into dgamma / dbeta.  A block owns
+// 64 columns of one output (lane = column, so every load is a 256-byte
+// coalesced run); its 16 waves take the partial rows round-robin, each with
+// kReduceUnroll independent loads in flight, and combine in LDS in wave order,
+// so the summation order is fixed.
+__global__ __launch_bounds__(kReduceThreads) void col_reduce_kernel(const float* __restrict__ partial, int64_t nparts,
+                                                                    int64_t d, float* __restrict__ dgamma,
+                                                                    float* __restrict__ dbeta, int accumulate) {
+    __shared__ float red[kReduceWaves][64];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int which = blockIdx.y;
     const int64_t col = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.f;
     if (col < d) {
-        for (int64_t b = wid; b < nparts; b += kWaves) s += partial[(b * 2 + which) * d + col];
+        const float* src = partial + (int64_t)which * d + col;
+        for (int64_t b = wid; b < nparts; b += kReduceUnroll * kReduceWaves) {
+            // all kReduceUnroll loads in flight at once (indices past the end
+            // re-read the last partial row and are not added)
+            float t[kReduceUnroll];
+#pragma unroll
+            for (int u = 0; u < kReduceUnroll; ++u) {
+                const int64_t i = b + u * kReduceWaves;
+                t[u] = src[(i < nparts ? i : nparts - 1) * 2 * d];
+            }
+#pragma unroll
+            for (int u = 0; u < kReduceUnroll; ++u) s += (b + u * kReduceWaves < nparts) ? t[u] : 0.f;
+        }
     }
     red[wid][lane] = s;
     __syncthreads();
     if (wid == 0 && col < d) {
         float t = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) t += red[w][lane];
+        for (int w = 0; w < kReduceWaves; ++w) t += red[w][lane];
         float* out = which ? dbeta : dgamma;
         if (out) out[col] = accumulate ? out[col] + t : t;
     }
@@ -228,9 +273,21 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_generic(const T* __restrict__
     }
 }
 
+// The vector kernels need 16-byte aligned rows of whole 16-byte groups.
 template <typename T>
-bool vec_ok(const void* p) {
-    return ((uintptr_t)p % (4 * sizeof(T))) == 0;
+bool vec_ok(int64_t d, std::initializer_list<const void*> ptrs) {
+    if (d % Pack16<T>::N != 0 || d > 2048) return false;
+    for (const void* p : ptrs)
+        if ((uintptr_t)p % 16 != 0) return false;
+    return true;
+}
+
+// Row values per lane for the vector kernels: 4, 8, 16 or 32, at least one
+// 16-byte group.
+template <typename T>
+int dpl_for(int64_t d) {
+    const int dpl = d <= 256 ? 4 : d <= 512 ? 8 : d <= 1024 ? 16 : 32;
+    return dpl < Pack16<T>::N ? Pack16<T>::N : dpl;
 }
 
 template <typename T>
@@ -240,16 +297,17 @@ int fwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* gamma,
     const T* gg = static_cast<const T*>(gamma);
     const T* bb = static_cast<const T*>(beta);
     T* yy = static_cast<T*>(y);
-    const bool vec = d % 4 == 0 && vec_ok<T>(x) && vec_ok<T>(gamma) && vec_ok<T>(beta) && vec_ok<T>(y);
+    const bool vec = vec_ok<T>(d, {x, gamma, beta, y});
     const int64_t blocks = std::min<int64_t>(nott::ceil_div(rows, kWaves), (int64_t)ctx->num_cu * 8);
     const dim3 grid((unsigned)std::max<int64_t>(blocks, 1));
-    if (vec && d <= 256)
+    const int dpl = vec ? dpl_for<T>(d) : 0;
+    if (dpl == 4)
         hipLaunchKernelGGL((ln_fwd_kernel<T, 4>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
-    else if (vec && d <= 512)
+    else if (dpl == 8)
         hipLaunchKernelGGL((ln_fwd_kernel<T, 8>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
-    else if (vec && d <= 1024)
+    else if (dpl == 16)
         hipLaunchKernelGGL((ln_fwd_kernel<T, 16>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
-    else if (vec && d <= 2048)
+    else if (dpl == 32)
         hipLaunchKernelGGL((ln_fwd_kernel<T, 32>), grid, dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy, mean, rstd, rows, d);
     else
         hipLaunchKernelGGL(ln_fwd_generic<T>, dim3((unsigned)rows), dim3(kThreads), 0, ctx->stream, xx, gg, bb, eps, yy,
@@ -264,10 +322,12 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
     const T* dd = static_cast<const T*>(dy);
     const T* gg = static_cast<const T*>(gamma);
     T* out = static_cast<T*>(dx);
-    const bool vec = d % 4 == 0 && d <= 2048 && vec_ok<T>(x) && vec_ok<T>(dy) && vec_ok<T>(gamma) && vec_ok<T>(dx);
+    const bool vec = vec_ok<T>(d, {x, dy, gamma, dx});
+    const int dpl = vec ? dpl_for<T>(d) : 0;
     int64_t nparts;
     if (vec) {
-        nparts = std::min<int64_t>(nott::ceil_div(rows, kWaves * kRowsInFlight), (int64_t)ctx->num_cu * 2);
+        nparts = std::min<int64_t>(nott::ceil_div(rows, kWaves * rows_in_flight((int)sizeof(T), dpl)),
+                                   (int64_t)ctx->num_cu * 2);
         nparts = std::max<int64_t>(nparts, 1);
     } else {
         nparts = rows;
@@ -276,18 +336,18 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
     if (!partial) return NOTT_ERR_ALLOC;
     const dim3 grid((unsigned)nparts);
     const size_t lds = sizeof(float) * kWaves * 2 * (size_t)d;
-    if (vec && d <= 256)
+    if (dpl == 4)
         hipLaunchKernelGGL((ln_bwd_kernel<T, 4>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
-    else if (vec && d <= 512)
+    else if (dpl == 8)
         hipLaunchKernelGGL((ln_bwd_kernel<T, 8>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
-    else if (vec && d <= 1024)
+    else if (dpl == 16)
         hipLaunchKernelGGL((ln_bwd_kernel<T, 16>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
-    else if (vec)
+    else if (dpl == 32)
         hipLaunchKernelGGL((ln_bwd_kernel<T, 32>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else
         hipLaunchKernelGGL(ln_bwd_generic<T>, grid, dim3(kThreads), 0, ctx->stream, xx, dd, mean, rstd, gg, out, partial, d);
     if (dgamma || dbeta)
-        hipLaunchKernelGGL(col_reduce_kernel, dim3((unsigned)nott::ceil_div(d, 64), 2), dim3(kThreads), 0, ctx->stream,
+        hipLaunchKernelGGL(col_reduce_kernel, dim3((unsigned)nott::ceil_div(d, 64), 2), dim3(kReduceThreads), 0, ctx->stream,
                            partial, nparts, d, dgamma, dbeta, accumulate);
     return nott::launch_status(ctx, "layernorm_bwd");
 }

@@ -22,14 +22,20 @@ __global__ __launch_bounds__(1024) void xent_count_kernel(const int64_t* __restr
     __shared__ float red[16];
     float cnt = 0.f;
     unsigned bad = 0;
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const int64_t y = labels[i];
-        if (y == kIgnoreIndex) continue;
-        if (y < 0 || y >= c) {
-            ++bad;
-            continue;
+    constexpr int kBatch = 16;   // labels per thread in flight
+    for (int64_t base = threadIdx.x; base < n; base += 1024 * kBatch) {
+        int64_t y[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int64_t i = base + (int64_t)u * 1024;
+            y[u] = labels[i < n ? i : n - 1];
         }
-        cnt += 1.f;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (base + (int64_t)u * 1024 >= n || y[u] == kIgnoreIndex) continue;
+            if (y[u] < 0 || y[u] >= c) ++bad;
+            else cnt += 1.f;
+        }
     }
     // counts up to 2^24 are exact in fp32; larger n is rejected on the host.
     const float total = block_sum<16>(cnt, red);
@@ -58,15 +64,19 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
     b = tb;
 }
 
-// One workgroup of NT threads per row; each thread holds EPT elements
-// (VEC-wide groups, strided by NT·VEC) of the row in registers.
-template <typename T, int NT, int EPT, int VEC>
+// One workgroup of NT threads per row; each thread holds EPT elements of the
+// row in registers.  VEC: 16-byte groups of G = 4 (fp32) or 8 (bf16)
+// elements, strided by NT·G, loaded unconditionally (past-the-end groups
+// re-read group 0 and count as −inf) so all of a thread's loads are in flight
+// together; otherwise single elements strided by NT.
+template <typename T, int NT, int EPT, bool VEC>
 __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logits, const int64_t* __restrict__ labels,
                                                       int64_t c, float smoothing, float grad_scale,
                                                       const int* __restrict__ nvalid, T* __restrict__ dlogits,
                                                       float* __restrict__ row_loss) {
     constexpr int NWAVES = NT / 64;
-    constexpr int NG = EPT / VEC;
+    constexpr int G = VEC ? Pack16<T>::N : 1;
+    constexpr int NG = EPT / G;
     __shared__ float red[2 * NWAVES];
     const int64_t row = blockIdx.x;
     const T* z = logits + row * c;
@@ -75,17 +85,25 @@ __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logi
     const bool valid = (y >= 0 && y < c);
 
     float v[EPT];
+    if constexpr (VEC) {
+        typename Pack16<T>::Raw raw[NG];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * VEC;
-        if (VEC == 4) {
-            if (j0 < c) {
-                f32x4 t = Vec4<T>::ld(z + j0);
-                v[g * 4 + 0] = t.x; v[g * 4 + 1] = t.y; v[g * 4 + 2] = t.z; v[g * 4 + 3] = t.w;
-            } else {
-                v[g * 4 + 0] = v[g * 4 + 1] = v[g * 4 + 2] = v[g * 4 + 3] = -INFINITY;
-            }
-        } else {
+        for (int g = 0; g < NG; ++g) {
+            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
+            raw[g] = Pack16<T>::template raw<true>(z + (j0 < c ? j0 : 0));
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
+            float t[G];
+            Pack16<T>::unpack(raw[g], t);
+#pragma unroll
+            for (int e = 0; e < G; ++e) v[g * G + e] = j0 < c ? t[e] : -INFINITY;
+        }
+    } else {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int64_t j0 = (int64_t)g * NT + threadIdx.x;
             v[g] = j0 < c ? Io<T>::ld(z, j0) : -INFINITY;
         }
     }
@@ -93,10 +111,14 @@ __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logi
         // Ignored (or out-of-range) row: zero gradient, no loss.
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * VEC;
-            if (VEC == 4) {
-                if (j0 < c) Vec4<T>::st(dz + j0, f32x4{0.f, 0.f, 0.f, 0.f});
-            } else if (j0 < c) {
+            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
+            if (j0 >= c) continue;
+            if constexpr (VEC) {
+                float t[G];
+#pragma unroll
+                for (int e = 0; e < G; ++e) t[e] = 0.f;
+                Pack16<T>::template st<true>(dz + j0, t);
+            } else {
                 Io<T>::st(dz, j0, 0.f);
             }
         }
@@ -120,19 +142,14 @@ __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logi
     const float hit = 1.f - smoothing;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * VEC;
-        if (VEC == 4) {
-            if (j0 < c) {
-                f32x4 t;
-                t.x = scale * (__expf(v[g * 4 + 0] - lse) - off - (j0 + 0 == y ? hit : 0.f));
-                t.y = scale * (__expf(v[g * 4 + 1] - lse) - off - (j0 + 1 == y ? hit : 0.f));
-                t.z = scale * (__expf(v[g * 4 + 2] - lse) - off - (j0 + 2 == y ? hit : 0.f));
-                t.w = scale * (__expf(v[g * 4 + 3] - lse) - off - (j0 + 3 == y ? hit : 0.f));
-                Vec4<T>::st(dz + j0, t);
-            }
-        } else if (j0 < c) {
-            Io<T>::st(dz, j0, scale * (__expf(v[g] - lse) - off - (j0 == y ? hit : 0.f)));
-        }
+        const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
+        if (j0 >= c) continue;
+        float t[G];
+#pragma unroll
+        for (int e = 0; e < G; ++e)
+            t[e] = scale * (__expf(v[g * G + e] - lse) - off - (j0 + e == y ? hit : 0.f));
+        if constexpr (VEC) Pack16<T>::template st<true>(dz + j0, t);
+        else Io<T>::st(dz, j0, t[0]);
     }
     if (threadIdx.x == 0 && row_loss) {
         const float zy = Io<T>::ld(z, y);
@@ -186,7 +203,7 @@ __global__ __launch_bounds__(1024) void xent_loss_kernel(const float* __restrict
 
 __global__ void xent_nan_kernel(float* __restrict__ loss) { *loss = __builtin_nanf(""); }
 
-template <typename T, int NT, int EPT, int VEC>
+template <typename T, int NT, int EPT, bool VEC>
 void launch_rows(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int64_t* labels, float eps,
                  float scale, const int* nvalid, void* dl, float* row_loss) {
     hipLaunchKernelGGL((xent_row_kernel<T, NT, EPT, VEC>), dim3((unsigned)n), dim3(NT), 0, ctx->stream,
@@ -196,17 +213,17 @@ void launch_rows(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const i
 template <typename T>
 void dispatch(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int64_t* labels, float eps, float scale,
               const int* nvalid, void* dl, float* row_loss) {
-    const bool vec = (c % 4 == 0) && ((uintptr_t)logits % (4 * sizeof(T)) == 0) && ((uintptr_t)dl % (4 * sizeof(T)) == 0);
-    if (vec && c <= 4 * 64 * 4)
-        launch_rows<T, 64, 16, 4>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
-    else if (vec && c <= 4 * 256 * 8)
-        launch_rows<T, 256, 32, 4>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
-    else if (vec && c <= 4 * 512 * 16)
-        launch_rows<T, 512, 64, 4>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+    const bool vec = (c % Pack16<T>::N == 0) && ((uintptr_t)logits % 16 == 0) && ((uintptr_t)dl % 16 == 0);
+    if (vec && c <= 64 * 16)
+        launch_rows<T, 64, 16, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+    else if (vec && c <= 256 * 32)
+        launch_rows<T, 256, 32, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+    else if (vec && c <= 512 * 64)
+        launch_rows<T, 512, 64, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (c <= 64 * 16)
-        launch_rows<T, 64, 16, 1>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+        launch_rows<T, 64, 16, false>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (c <= 512 * 32)
-        launch_rows<T, 512, 32, 1>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+        launch_rows<T, 512, 32, false>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else
         hipLaunchKernelGGL(xent_long_kernel<T>, dim3((unsigned)n), dim3(256), 0, ctx->stream,
                            static_cast<const T*>(logits), labels, c, eps, scale, nvalid, static_cast<T*>(dl), row_loss);
