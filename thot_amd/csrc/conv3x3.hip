@@ -14,14 +14,15 @@
 // 64 bytes) it stages in LDS:
 //   * the input tile once, as [padded pixel][channel] rows: every image row
 //     the tile touches plus one halo row above and below, each padded with a
-//     zero column on both sides, so that each of the 9 taps is a plain row
-//     offset ((r−1)·(W+2) + s−1) into the same LDS data and image borders read
-//     zeros;
+//     zero column on both sides (row pitch P = W+2 rounded up to odd), so
+//     that each of the 9 taps is a plain row offset ((r−1)·P + s−1) into the
+//     same LDS data and image borders read zeros;
 //   * the 9 × 64 × chunk weight slice, pre-arranged by conv3x3_wprep_kernel.
 // Each wave then runs 9 taps × (4 pixel tiles × 4 channel tiles) of
-// v_mfma_f32_16x16x32_bf16 (or 4× v_mfma_f32_16x16x4f32).  LDS rows are 64
-// bytes with the 16-byte sub-chunks XOR-swizzled by row so that 16
-// consecutive rows read by one MFMA operand hit distinct banks.
+// v_mfma_f32_16x16x32_bf16 (or 4× v_mfma_f32_16x16x4f32), loading the next
+// tap's operands while the current tap's MFMAs run.  LDS rows are 64 bytes,
+// grouped by 16 (lds_off) so that 16 consecutive rows read by one MFMA
+// operand hit distinct banks.
 //
 // conv3x3_wgrad_kernel computes dw[k, c, r, s] = Σ_{n,h,w} dy[n,k,h,w] ·
 // x[n, c, h−1+r, w−1+s] (ATen convolution_backward, weight grad).
@@ -51,7 +52,7 @@ __device__ __forceinline__ int lds_off(int row, int sub) { return ((row >> 4) <<
 
 struct SameParams {
     int32_t n, cin, h, w, cout;
-    int32_t hw, w2;            // h·w, w+2
+    int32_t hw, w2;            // h·w, LDS row pitch of a padded image row (odd, ≥ w+2)
     int32_t npix;              // n·h·w
     int32_t in_rows;           // LDS rows reserved for the input tile
     int32_t remap;             // XCD-aware block remap active
@@ -142,7 +143,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
                                                                   SameParams p) {
     constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
     constexpr int VT = VEC ? VecTasks<T>::VT : 1;
-    constexpr int WT = (9 * kTileCo * 4) / kThreads;    // weight chunks per thread per channel chunk
     extern __shared__ __attribute__((aligned(16))) char smem[];
     char* lds_in = smem;
     char* lds_w = smem + p.in_rows * kRowB;
@@ -180,6 +180,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         const int32_t vrow = (int32_t)n * (p.h + 2) + (int32_t)h + 1;
         abase[mt] = (vrow - v_lo) * p.w2 + (int32_t)w + 1;
     }
+    // LDS byte offsets of this lane's A fragments for every tap, and of its B
+    // fragments (tap · 4 + nt)·1024 past boff: the tap loop does no address
+    // arithmetic.
+    // Offsets are below 64 KiB: two per register.
+    uint32_t aoff2[9][2];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            aoff2[tap][h] = (uint32_t)lds_off(abase[2 * h] + (tap / 3 - 1) * p.w2 + (tap % 3 - 1), kq) |
+                            ((uint32_t)lds_off(abase[2 * h + 1] + (tap / 3 - 1) * p.w2 + (tap % 3 - 1), kq) << 16);
+    auto aoff = [&](int tap, int mt) -> uint32_t {
+        return (mt & 1) ? (aoff2[tap][mt >> 1] >> 16) : (aoff2[tap][mt >> 1] & 0xffffu);
+    };
+    const int32_t boff = lds_off(r16, kq);
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -193,45 +208,59 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     // Vector fill: task = (w-chunk of SUB pixels, padded row, channel group of
     // SUB): SUB 16-byte loads (one per channel), a register transpose, SUB
     // 16-byte LDS writes (one per pixel).  Halo rows / columns are zeroed once.
+    // Task order: the fastest lanes take WG consecutive w-chunks, then padded
+    // rows, then channel groups.  With an odd row pitch the 16 lanes of a
+    // quarter-wave then start their SUB-row runs at 16 distinct rows mod 16,
+    // so each of the SUB transposed writes is conflict-free.
+    constexpr int WG = 16 / SUB;
     const int32_t wchunks = p.w / SUB;
-    const int32_t ntask = nvr * wchunks * 4;
+    const int32_t wgroups = (wchunks + WG - 1) / WG;
+    const int32_t ntask = nvr * wgroups * WG * 4;
+    auto task_of = [&](int32_t t, int32_t& wc, int32_t& vr, int32_t& cig) {
+        const int32_t u = t / WG, u2 = u / nvr;
+        vr = u - u2 * nvr;
+        cig = u2 / wgroups;
+        wc = (u2 - cig * wgroups) * WG + (t % WG);
+    };
     u32x4 rin[VT][SUB];
-    auto fetch = [&](int32_t cc) {
-        if constexpr (VEC) {
+    // VEC fill task j of chunk cc: SUB global loads into rin[j] ...
+    auto fetch_task = [&](int j, int32_t cc) {
+        const int32_t t = threadIdx.x + j * kThreads;
+        int32_t wc, vr, cig;
+        task_of(t, wc, vr, cig);
+        uint32_t img, hh;
+        p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
+        const int32_t h = (int32_t)hh - 1;
+        if (t < ntask && wc < wchunks && h >= 0 && h < p.h) {
+            const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w + wc * SUB;
 #pragma unroll
-            for (int j = 0; j < VT; ++j) {
-                const int32_t t = threadIdx.x + j * kThreads;
-                const int32_t wc = t % wchunks, rest = t / wchunks;
-                const int32_t vr = rest % nvr, cig = rest / nvr;
-                uint32_t img, hh;
-                p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
-                const int32_t h = (int32_t)hh - 1;
-                if (t < ntask && h >= 0 && h < p.h) {
-                    const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w + wc * SUB;
-#pragma unroll
-                    for (int i = 0; i < SUB; ++i) rin[j][i] = *reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw);
-                }
-            }
+            for (int i = 0; i < SUB; ++i)
+                rin[j][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw));
         }
     };
+    // ... and the transpose + SUB LDS row writes into buffer `dst`.
+    auto stash_task = [&](int j, char* dst) {
+        const int32_t t = threadIdx.x + j * kThreads;
+        int32_t wc, vr, cig;
+        task_of(t, wc, vr, cig);
+        uint32_t img, hh;
+        p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
+        const int32_t h = (int32_t)hh - 1;
+        if (t < ntask && wc < wchunks && h >= 0 && h < p.h) {
+            u32x4 tr[SUB];
+            transpose_block(rin[j], tr);
+            const int32_t row0 = vr * p.w2 + 1 + wc * SUB;
+#pragma unroll
+            for (int i = 0; i < SUB; ++i) *reinterpret_cast<u32x4*>(dst + lds_off(row0 + i, cig)) = tr[i];
+        }
+    };
+    // Fill of chunk cc: VEC tasks from the registers loaded by fetch_task, or
+    // element loads straight into packed LDS rows; then the weight slice.
+    constexpr int WT = (9 * kTileCo * 4) / kThreads;    // weight chunks per thread per channel chunk
     auto stash = [&](int32_t cc) {
         if constexpr (VEC) {
 #pragma unroll
-            for (int j = 0; j < VT; ++j) {
-                const int32_t t = threadIdx.x + j * kThreads;
-                const int32_t wc = t % wchunks, rest = t / wchunks;
-                const int32_t vr = rest % nvr, cig = rest / nvr;
-                uint32_t img, hh;
-                p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
-                const int32_t h = (int32_t)hh - 1;
-                if (t < ntask && h >= 0 && h < p.h) {
-                    u32x4 tr[SUB];
-                    transpose_block(rin[j], tr);
-                    const int32_t row0 = vr * p.w2 + 1 + wc * SUB;
-#pragma unroll
-                    for (int i = 0; i < SUB; ++i) *reinterpret_cast<u32x4*>(lds_in + lds_off(row0 + i, cig)) = tr[i];
-                }
-            }
+            for (int j = 0; j < VT; ++j) stash_task(j, lds_in);
         } else {
             for (int32_t t = threadIdx.x; t < nrows * 4; t += kThreads) {
                 const int32_t sub = t / nrows;        // consecutive lanes -> consecutive pixels
@@ -267,33 +296,46 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     };
 
     if constexpr (VEC) {
+        // Halo rows / columns stay zero; the fill writes interior rows only.
         for (int32_t t = threadIdx.x; t < ((nrows + 15) >> 4) * 64; t += kThreads)
             *reinterpret_cast<u32x4*>(lds_in + t * 16) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < VT; ++j) fetch_task(j, 0);
     }
-    fetch(0);
     for (int32_t cc = 0; cc < nchunks; ++cc) {
         __syncthreads();     // previous chunk fully read (and, at cc = 0, the halo zeroing done)
         stash(cc);
         __syncthreads();
-        if (cc + 1 < nchunks) fetch(cc + 1);
-#pragma unroll 3
+        if constexpr (VEC) {
+            if (cc + 1 < nchunks) {
+#pragma unroll
+                for (int j = 0; j < VT; ++j) fetch_task(j, cc + 1);
+            }
+        }
+        // 9 taps × 16 MFMAs with the next tap's 8 operand fragments loaded
+        // while the current tap's MFMAs run (LDS addresses precomputed).
+        u32x4 a[2][4], b[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) a[0][mt] = *reinterpret_cast<const u32x4*>(lds_in + aoff(0, mt));
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) b[0][nt] = *reinterpret_cast<const u32x4*>(lds_w + boff + nt * 1024);
+#pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
-            const int32_t toff = (tap / 3 - 1) * p.w2 + (tap % 3 - 1);
-            u32x4 a[4], b[4];
+            const int cur = tap & 1, nxt = cur ^ 1;
+            if (tap + 1 < 9) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int32_t row = abase[mt] + toff;
-                a[mt] = *reinterpret_cast<const u32x4*>(lds_in + lds_off(row, kq));
-            }
+                for (int mt = 0; mt < 4; ++mt)
+                    a[nxt][mt] = *reinterpret_cast<const u32x4*>(lds_in + aoff(tap + 1, mt));
 #pragma unroll
-            for (int nt = 0; nt < 4; ++nt) {
-                const int row = tap * kTileCo + nt * 16 + r16;
-                b[nt] = *reinterpret_cast<const u32x4*>(lds_w + lds_off(row, kq));
+                for (int nt = 0; nt < 4; ++nt)
+                    b[nxt][nt] = *reinterpret_cast<const u32x4*>(lds_w + boff + ((tap + 1) * 4 + nt) * 1024);
             }
+            // keep the next tap's loads ahead of this tap's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < 4; ++nt) mfma_chunk<T>(a[mt], b[nt], acc[mt][nt]);
+                for (int nt = 0; nt < 4; ++nt) mfma_chunk<T>(a[cur][mt], b[cur][nt], acc[mt][nt]);
         }
     }
 
@@ -345,6 +387,10 @@ bool same_shape(const nott_conv2d_desc* d) {
            d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1 && d->dil_h == 1 && d->dil_w == 1 && d->w <= 64;
 }
 
+// LDS rows per padded image row: w + 2 (two halo columns), made odd so that
+// rows of consecutive image rows start at distinct offsets mod 16.
+int32_t row_pitch(int32_t w) { return (w + 2) | 1; }
+
 int32_t in_rows_bound(int32_t h, int32_t w) {
     const int32_t hw = h * w;
     // A run of kTilePix pixels starting at any column touches at most
@@ -352,8 +398,14 @@ int32_t in_rows_bound(int32_t h, int32_t w) {
     // each image adds its two halo rows.
     const int32_t rows = (kTilePix - 1 + w - 1) / w + 1;
     const int32_t imgs = (kTilePix - 1 + hw - 1) / hw + 1;
-    return (rows + 2 * imgs) * (w + 2);
+    return (rows + 2 * imgs) * row_pitch(w);
 }
+
+size_t same_lds_bytes(int32_t h, int32_t w, size_t elem) {
+    const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
+    return std::max((size_t)in_rows * kRowB + (size_t)9 * kTileCo * kRowB, (size_t)kTileCo * (kTilePix * elem + 16));
+}
+constexpr size_t kSameLdsMax = 80 * 1024;   // two workgroups per CU
 
 template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
@@ -361,9 +413,8 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     constexpr int CC = Chunk<T>::CC;
     const size_t wbytes = sizeof(T) * (size_t)cout * cin * 9;
     const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
-    const size_t lds = std::max((size_t)in_rows * kRowB + (size_t)9 * kTileCo * kRowB,
-                                (size_t)kTileCo * (kTilePix * sizeof(T) + 16));
-    if (lds > 80 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
+    if (same_lds_bytes(h, w, sizeof(T)) > kSameLdsMax)
+        return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
     T* wp = static_cast<T*>(workspace(ctx, wbytes));
     if (!wp) return NOTT_ERR_ALLOC;
     const int64_t welems = (int64_t)cout * cin * 9;
@@ -371,10 +422,10 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
                        ctx->stream, wsrc, wp, cout, cin);
     SameParams p;
     p.n = n; p.cin = cin; p.h = h; p.w = w; p.cout = cout;
-    p.hw = h * w; p.w2 = w + 2; p.npix = n * h * w; p.in_rows = in_rows;
+    p.hw = h * w; p.w2 = row_pitch(w); p.npix = n * h * w; p.in_rows = in_rows;
     p.fd_hw = FastDiv((uint32_t)(h * w));
     p.fd_w = FastDiv((uint32_t)w);
-    p.fd_w2 = FastDiv((uint32_t)(w + 2));
+    p.fd_w2 = FastDiv((uint32_t)row_pitch(w));
     p.fd_h2 = FastDiv((uint32_t)(h + 2));
     const int64_t tiles = ceil_div((int64_t)p.npix, kTilePix);
     p.remap = (tiles % 8 == 0) ? 1 : 0;
@@ -382,9 +433,11 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     // Vector fill when image rows are whole 16-byte chunks, the input is
     // 16-byte aligned and the tile's fill tasks fit the per-thread registers.
     const int32_t sub = Chunk<T>::SUB;
-    const int32_t max_vr = in_rows_bound(h, w) / (w + 2);
+    const int32_t max_vr = in_rows_bound(h, w) / row_pitch(w);
+    const int32_t wg = 16 / sub, wgroups = (w / sub + wg - 1) / wg;
     const bool vec = (w % sub) == 0 && ((uintptr_t)in % 16) == 0 &&
-                     (int64_t)max_vr * (w / sub) * 4 <= (int64_t)VecTasks<T>::VT * kThreads;
+                     (int64_t)max_vr * wgroups * wg * 4 <= (int64_t)VecTasks<T>::VT * kThreads;
+    const size_t lds = same_lds_bytes(h, w, sizeof(T));
     static bool attr_set[2][2] = {{false, false}, {false, false}};
     if (!attr_set[sizeof(T) == 2][vec]) {
         const void* fn = vec ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true>)
@@ -673,13 +726,15 @@ int wgrad_slot_pitch(int64_t w) {
 
 bool fwd_applies(const nott_conv2d_desc* d, size_t elem) {
     const int cc = elem == 2 ? Chunk<bf16_t>::CC : Chunk<float>::CC;
-    return same_shape(d) && d->c % cc == 0 && d->k % kTileCo == 0;
+    return same_shape(d) && d->c % cc == 0 && d->k % kTileCo == 0 &&
+           same_lds_bytes((int32_t)d->h, (int32_t)d->w, elem) <= kSameLdsMax;
 }
 
 bool dgrad_applies(const nott_conv2d_desc* d, size_t elem) {
     const int cc = elem == 2 ? Chunk<bf16_t>::CC : Chunk<float>::CC;
     // dgrad's input channels are the conv's outputs (k), its outputs the conv's inputs (c).
-    return same_shape(d) && d->k % cc == 0 && d->c % kTileCo == 0;
+    return same_shape(d) && d->k % cc == 0 && d->c % kTileCo == 0 &&
+           same_lds_bytes((int32_t)d->h, (int32_t)d->w, elem) <= kSameLdsMax;
 }
 
 bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {

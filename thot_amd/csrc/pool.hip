@@ -78,6 +78,90 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(const int64_t* __
     Io<T>::st(dx, i, acc);
 }
 
+// 32-bit index versions (tensors below 2^31 elements, the common case):
+// every division is a multiply-high by a precomputed reciprocal.
+struct PoolGeom32 {
+    int32_t h, w, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
+    FastDiv fd_out_plane, fd_ow, fd_in_plane, fd_w, fd_sh, fd_sw;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel32(const T* __restrict__ x, T* __restrict__ y,
+                                                                 int64_t* __restrict__ argmax, uint32_t total,
+                                                                 PoolGeom32 g) {
+    const uint32_t o = blockIdx.x * kThreads + threadIdx.x;
+    if (o >= total) return;
+    uint32_t pl, rem, oh, ow;
+    g.fd_out_plane.divmod(o, pl, rem);
+    g.fd_ow.divmod(rem, oh, ow);
+    const T* xp = x + (int64_t)pl * g.h * g.w;
+    int32_t ih0 = (int32_t)oh * g.sh - g.ph, iw0 = (int32_t)ow * g.sw - g.pw;
+    const int32_t ih1 = min(ih0 + (g.kh - 1) * g.dh + 1, g.h);
+    const int32_t iw1 = min(iw0 + (g.kw - 1) * g.dw + 1, g.w);
+    while (ih0 < 0) ih0 += g.dh;
+    while (iw0 < 0) iw0 += g.dw;
+    int32_t best = ih0 * g.w + iw0;
+    float bv = -INFINITY;
+    for (int32_t ih = ih0; ih < ih1; ih += g.dh)
+        for (int32_t iw = iw0; iw < iw1; iw += g.dw) {
+            const float v = Io<T>::ld(xp, ih * g.w + iw);
+            if (v > bv || v != v) {
+                bv = v;
+                best = ih * g.w + iw;
+            }
+        }
+    Io<T>::st(y, o, bv);
+    argmax[o] = best;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* __restrict__ argmax,
+                                                                 const T* __restrict__ dy, T* __restrict__ dx,
+                                                                 uint32_t total, PoolGeom32 g) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= total) return;
+    uint32_t pl, idx, ih, iw;
+    g.fd_in_plane.divmod(i, pl, idx);
+    g.fd_w.divmod(idx, ih, iw);
+    // Output rows whose window can contain ih: oh·sh − ph ≤ ih ≤ oh·sh − ph + (kh−1)·dh.
+    const int32_t num_h = (int32_t)ih + g.ph - (g.kh - 1) * g.dh;
+    const int32_t oh0 = num_h <= 0 ? 0 : (int32_t)g.fd_sh.div((uint32_t)(num_h + g.sh - 1));
+    const int32_t oh1 = min((int32_t)g.fd_sh.div(ih + (uint32_t)g.ph), g.oh - 1);
+    const int32_t num_w = (int32_t)iw + g.pw - (g.kw - 1) * g.dw;
+    const int32_t ow0 = num_w <= 0 ? 0 : (int32_t)g.fd_sw.div((uint32_t)(num_w + g.sw - 1));
+    const int32_t ow1 = min((int32_t)g.fd_sw.div(iw + (uint32_t)g.pw), g.ow - 1);
+    const int64_t* ap = argmax + (int64_t)pl * g.oh * g.ow;
+    const T* gp = dy + (int64_t)pl * g.oh * g.ow;
+    float acc = 0.f;
+    for (int32_t oh = oh0; oh <= oh1; ++oh)
+        for (int32_t ow = ow0; ow <= ow1; ++ow) {
+            const int32_t o = oh * g.ow + ow;
+            if (ap[o] == (int64_t)idx) acc += Io<T>::ld(gp, o);
+        }
+    Io<T>::st(dx, i, acc);
+}
+
+PoolGeom32 geom32(const PoolGeom& g) {
+    PoolGeom32 r;
+    r.h = (int32_t)g.h; r.w = (int32_t)g.w; r.oh = (int32_t)g.oh; r.ow = (int32_t)g.ow;
+    r.kh = (int32_t)g.kh; r.kw = (int32_t)g.kw; r.sh = (int32_t)g.sh; r.sw = (int32_t)g.sw;
+    r.ph = (int32_t)g.ph; r.pw = (int32_t)g.pw; r.dh = (int32_t)g.dh; r.dw = (int32_t)g.dw;
+    r.fd_out_plane = FastDiv((uint32_t)(g.oh * g.ow));
+    r.fd_ow = FastDiv((uint32_t)g.ow);
+    r.fd_in_plane = FastDiv((uint32_t)(g.h * g.w));
+    r.fd_w = FastDiv((uint32_t)g.w);
+    r.fd_sh = FastDiv((uint32_t)g.sh);
+    r.fd_sw = FastDiv((uint32_t)g.sw);
+    return r;
+}
+
+// The 32-bit kernels apply when every flat index (and every window bound the
+// scan forms) fits comfortably in int32.
+bool fits32(int64_t planes, const PoolGeom& g) {
+    const int64_t lim = int64_t(1) << 30;
+    return planes * g.h * g.w < lim && planes * g.oh * g.ow < lim && g.h * g.w + g.kh * g.dh * g.w < lim;
+}
+
 int64_t pool_out(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d, int ceil_mode) {
     int64_t num = in + 2 * p - d * (k - 1) - 1 + (ceil_mode ? s - 1 : 0);
     int64_t out = (num >= 0 ? num / s : -((-num + s - 1) / s)) + 1;
@@ -116,7 +200,15 @@ extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     NOTT_REQUIRE(ctx, x && y && argmax, "nott_maxpool2d_fwd: null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
-    if (dtype == NOTT_F32)
+    if (fits32(planes, g)) {
+        const PoolGeom32 g32 = geom32(g);
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL(maxpool_fwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream,
+                               static_cast<const float*>(x), static_cast<float*>(y), argmax, (uint32_t)total, g32);
+        else
+            hipLaunchKernelGGL(maxpool_fwd_kernel32<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
+                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, (uint32_t)total, g32);
+    } else if (dtype == NOTT_F32)
         hipLaunchKernelGGL(maxpool_fwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
                            static_cast<const float*>(x), static_cast<float*>(y), argmax, planes, g);
     else
@@ -137,7 +229,15 @@ extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     NOTT_REQUIRE(ctx, argmax && dy && dx, "nott_maxpool2d_bwd: null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
-    if (dtype == NOTT_F32)
+    if (fits32(planes, g)) {
+        const PoolGeom32 g32 = geom32(g);
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL(maxpool_bwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
+                               static_cast<const float*>(dy), static_cast<float*>(dx), (uint32_t)total, g32);
+        else
+            hipLaunchKernelGGL(maxpool_bwd_kernel32<bf16_t>, grid, dim3(kThreads), 0, ctx->stream, argmax,
+                               static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), (uint32_t)total, g32);
+    } else if (dtype == NOTT_F32)
         hipLaunchKernelGGL(maxpool_bwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
                            static_cast<const float*>(dy), static_cast<float*>(dx), planes, g);
     else
