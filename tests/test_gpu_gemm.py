@@ -31,7 +31,9 @@ def ops():
 
 
 # ------------------------------------------------------------------ linear
-LIN = [(1, 1, 1), (7, 5, 3), (64, 3136, 128), (64, 128, 10), (64, 512, 1000), (129, 70, 33), (256, 1024, 1024)]
+LIN = [(1, 1, 1), (7, 5, 3), (64, 3136, 128), (64, 128, 10), (64, 512, 1000), (129, 70, 33), (256, 1024, 1024),
+       # bf16 fast-path shapes: partial 128-tiles, split-K over 4096 rows
+       (384, 192, 256), (136, 64, 64), (4096, 64, 64), (1024, 320, 192)]
 
 
 @pytest.mark.parametrize("dt", DTYPES)

@@ -312,3 +312,194 @@ int run(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64
 
 }  // namespace gemm
 }  // namespace nott
+
+// ===========================================================================
+// Fast bf16 path: plain strided operands (no gathers), K a multiple of 64.
+//
+//   A(m, k) = A[m·lda + k]   (AT = false)   or   A[k·lda + m]   (AT = true)
+//   B(n, k) = B[n·ldb + k]   (BT = false)   or   B[k·ldb + n]   (BT = true)
+//
+// 128×128 tile per 256-thread workgroup (4 waves as 2×2, each 64×64 = 4×4
+// tiles of v_mfma_f32_16x16x32_bf16); a k-stage is 64 deep (two 32-wide
+// MFMA slices) and the LDS stages are double-buffered, so a wave runs 32
+// MFMAs per barrier and the next stage's global loads are in flight while it
+// does.  Both operands sit in LDS as [row][k] 16-byte chunks (row = m or n);
+// a transposed operand is transposed in registers on its way in (8×8 bf16
+// blocks).  Chunk (row, c) of slice s is at
+//   s·8 KiB + (row/16)·1 KiB + c·256 + ((row%16) ^ ((row/16)%8))·16,
+// which keeps every 16-row MFMA fragment read, every plain fill (16 rows per
+// quarter-wave) and every transposed fill (rows 8j+i of 16 consecutive j)
+// on 16 distinct 16-byte slots.
+// ===========================================================================
+namespace nott {
+namespace gemm {
+namespace fast {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int kThreads = 256;
+constexpr int kStageBytes = 2 * BM * BK * 2;   // A and B, one stage (32 KiB)
+
+__device__ __forceinline__ int off(int row, int c) {
+    const int s = c >> 2, sub = c & 3;
+    return (s << 13) + ((row >> 4) << 10) + (sub << 8) + ((((row & 15) ^ ((row >> 4) & 7))) << 4);
+}
+
+// One operand tile (128 rows × 64 k) of stage `k0`, staged through registers.
+template <bool TR>
+struct Fill {
+    u32x4 r[TR ? 8 : 4];
+    // Plain: chunk c = j·256 + tid -> row = 16·(c / 128) + c % 16, k-chunk (c / 16) % 8.
+    // Transposed: threads 0..127 each own an 8k × 8row block
+    // (k-block kb = t % 8, row block rb = t / 8).
+    __device__ __forceinline__ void load(const bf16_t* __restrict__ p, int64_t ld, int64_t row0, int64_t rows,
+                                         int64_t k0, int tid, bool active) {
+        if constexpr (!TR) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = j * kThreads + tid;
+                const int64_t row = row0 + 16 * (c >> 7) + (c & 15);
+                const int kc = (c >> 4) & 7;
+                const int64_t rr = row < rows ? row : rows - 1;
+                r[j] = *reinterpret_cast<const u32x4*>(p + rr * ld + k0 + kc * 8);
+            }
+        } else {
+            if (!active) return;
+            const int kb = tid & 7, rb = tid >> 3;
+            int64_t col = row0 + rb * 8;
+            col = col + 8 <= rows ? col : (rows >= 8 ? rows - 8 : 0);   // clamped reads; masked at the store
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r[e] = *reinterpret_cast<const u32x4*>(p + (k0 + kb * 8 + e) * ld + col);
+        }
+    }
+    __device__ __forceinline__ void store(char* lds, int tid, bool active) const {
+        if constexpr (!TR) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = j * kThreads + tid;
+                *reinterpret_cast<u32x4*>(lds + off(16 * (c >> 7) + (c & 15), (c >> 4) & 7)) = r[j];
+            }
+        } else {
+            if (!active) return;
+            const int kb = tid & 7, rb = tid >> 3;
+            // r[e] holds rows rb·8 + 0..7 of k = kb·8 + e; out[i] holds k = kb·8 + 0..7 of row rb·8 + i.
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                u32x4 o0, o1;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t a = r[2 * e][i >> 1], b = r[2 * e + 1][i >> 1];
+                    o0[e] = (a & 0xffffu) | (b << 16);
+                    o1[e] = (a >> 16) | (b & 0xffff0000u);
+                }
+                *reinterpret_cast<u32x4*>(lds + off(rb * 8 + i, kb)) = o0;
+                *reinterpret_cast<u32x4*>(lds + off(rb * 8 + i + 1, kb)) = o1;
+            }
+        }
+    }
+};
+
+template <bool AT, bool BT, class EP>
+__global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const bf16_t* __restrict__ A, int64_t lda,
+                                                                const bf16_t* __restrict__ B, int64_t ldb, EP ep,
+                                                                int64_t M, int64_t N, int64_t K, int64_t k_per_split) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+    const int64_t kb0 = (int64_t)blockIdx.z * k_per_split;
+    const int nk = (int)((std::min<int64_t>(K, kb0 + k_per_split) - kb0) / BK);
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int wm = wid >> 1, wn = wid & 1, r16 = lane & 15, kq = lane >> 4;
+    // Transposed fills: A on threads 0..127, B on 128..255 (one 8×8 block each).
+    const bool act_a = !AT || tid < 128, act_b = !BT || tid >= 128;
+    const int tid_a = AT ? (tid & 127) : tid, tid_b = BT ? (tid & 127) : tid;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    Fill<AT> fa;
+    Fill<BT> fb;
+    fa.load(A, lda, m0, M, kb0, tid_a, act_a);
+    fb.load(B, ldb, n0, N, kb0, tid_b, act_b);
+    fa.store(smem, tid_a, act_a);
+    fb.store(smem + kStageBytes / 2, tid_b, act_b);
+    __syncthreads();
+    for (int t = 0; t < nk; ++t) {
+        const char* la = smem + (t & 1) * kStageBytes;
+        const char* lb = la + kStageBytes / 2;
+        const bool more = t + 1 < nk;
+        if (more) {
+            fa.load(A, lda, m0, M, kb0 + (t + 1) * BK, tid_a, act_a);
+            fb.load(B, ldb, n0, N, kb0 + (t + 1) * BK, tid_b, act_b);
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            u32x4 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const u32x4*>(la + off(wm * 64 + i * 16 + r16, 4 * s + kq));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const u32x4*>(lb + off(wn * 64 + j * 16 + r16, 4 * s + kq));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[i]),
+                                                                        __builtin_bit_cast(bf16x8, b[j]), acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            char* na = smem + ((t + 1) & 1) * kStageBytes;
+            fa.store(na, tid_a, act_a);
+            fb.store(na + kStageBytes / 2, tid_b, act_b);
+        }
+        __syncthreads();
+    }
+    const int col = lane & 15, rq = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ep.store(m0 + wm * 64 + i * 16 + rq + e, n0 + wn * 64 + j * 16 + col, acc[i][j][e]);
+}
+
+// C = A·B through the fast path, or NOTT_ERR_UNSUPPORTED when the operands do
+// not qualify (then the caller uses the generic engine).
+template <bool AT, bool BT, class EP>
+int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep, int64_t M, int64_t N,
+        int64_t K, int64_t splits = 0) {
+    if (M <= 0 || N <= 0) return NOTT_OK;
+    auto ok16 = [](const void* p, int64_t ld) { return ((uintptr_t)p % 16) == 0 && (ld % 8) == 0; };
+    if (K <= 0 || K % BK != 0 || !ok16(A, lda) || !ok16(B, ldb)) return NOTT_ERR_UNSUPPORTED;
+    // transposed operands are read in whole 8-row blocks
+    if ((AT && M % 8 != 0) || (BT && N % 8 != 0)) return NOTT_ERR_UNSUPPORTED;
+    const int64_t tn = ceil_div(N, BN), tm = ceil_div(M, BM);
+    if (tn > 0x7fffffff || tm > 65535) return NOTT_ERR_UNSUPPORTED;
+    const int64_t nkb = K / BK;
+    if (splits <= 0) {
+        splits = std::max<int64_t>(1, (2 * (int64_t)ctx->num_cu + tn * tm - 1) / (tn * tm));
+        splits = std::min<int64_t>(splits, std::max<int64_t>(1, nkb / 4));   // at least 4 stages per split
+    }
+    splits = std::max<int64_t>(1, std::min<int64_t>(splits, std::min<int64_t>(nkb, 65535)));
+    const int64_t kps = ceil_div(nkb, splits) * BK;
+    splits = ceil_div(K, kps);
+    const size_t lds = 2 * kStageBytes;
+    if (splits == 1) {
+        hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EP>), dim3((unsigned)tn, (unsigned)tm, 1), dim3(kThreads), lds,
+                           ctx->stream, A, lda, B, ldb, ep, M, N, K, K);
+        return launch_status(ctx, "gemm_bf16");
+    }
+    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(splits * M * N)));
+    if (!ws) return NOTT_ERR_ALLOC;
+    PartialStore ps{ws, M, N};
+    hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
+                       dim3(kThreads), lds, ctx->stream, A, lda, B, ldb, ps, M, N, K, kps);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, ctx->stream,
+                       ws, splits, M, N, ep);
+    return launch_status(ctx, "gemm_bf16_splitk");
+}
+
+}  // namespace fast
+}  // namespace gemm
+}  // namespace nott

@@ -7,12 +7,18 @@
 //   y  = x·wᵀ + b         (NT: both operands k-contiguous)
 //   dx = dy·w             (NN: w is k-strided)
 //   dw = dyᵀ·x            (TN: both k-strided; split-K over rows)
-//   db = Σ_rows dy        (folded into the dw GEMM as an extra all-ones column)
+//   db = Σ_rows dy        (folded into the dw GEMM as an extra all-ones column;
+//                          bf16 fast path: a two-phase column sum)
+// bf16 operands whose k extent is a multiple of 64 take the fast GEMM path
+// (gemm.hpp, namespace fast); everything else the generic engine.
 #include "gemm.hpp"
 
 namespace {
 
 using namespace nott::gemm;
+using nott::ceil_div;
+using nott::launch_status;
+using nott::workspace;
 
 template <typename T>
 bool vec16(const void* p, int64_t ld) {
@@ -59,8 +65,45 @@ struct DwDbStore {
     }
 };
 
+// db[o] (+)= Σ_r dy[r·nout + o] in two deterministic phases: kColSumSlabs
+// row slabs each write a partial row (lane = column, 4 waves split the
+// slab's rows), then one pass adds the partials in slab order.
+constexpr int kColSumSlabs = 32;
+
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_partial_kernel(const T* __restrict__ dy, int64_t rows, int64_t nout,
+                                                             float* __restrict__ partial) {
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int64_t col = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t per = (rows + kColSumSlabs - 1) / kColSumSlabs;
+    const int64_t r0 = (int64_t)blockIdx.y * per, r1 = r0 + per < rows ? r0 + per : rows;
+    float s = 0.f;
+    if (col < nout)
+        for (int64_t r = r0 + wid; r < r1; r += 4) s += Io<T>::ld(dy, r * nout + col);
+    red[wid][lane] = s;
+    __syncthreads();
+    if (wid == 0 && col < nout) partial[(int64_t)blockIdx.y * nout + col] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+}
+
+__global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restrict__ partial, int64_t nout,
+                                                            float* __restrict__ db, int accumulate) {
+    const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (col >= nout) return;
+    float s = 0.f;
+#pragma unroll 8
+    for (int z = 0; z < kColSumSlabs; ++z) s += partial[(int64_t)z * nout + col];
+    db[col] = accumulate ? db[col] + s : s;
+}
+
 template <typename T>
 int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
+    if constexpr (sizeof(T) == 2) {
+        RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
+        const int st = fast::run<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
+                                               m, nout, kin);
+        if (st != NOTT_ERR_UNSUPPORTED) return st;
+    }
     const T* xp = static_cast<const T*>(x);
     const T* wp = static_cast<const T*>(w);
     RowKLoader<T> la{xp, kin, m, kin, vec16<T>(x, kin)};
@@ -73,6 +116,41 @@ template <typename T>
 int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, const void* x, const void* w, void* dx,
         float* dw, float* db, int accumulate) {
     const T* dyp = static_cast<const T*>(dy);
+    if constexpr (sizeof(T) == 2) {
+        // dx = dy·w: A = dy (k = o contiguous), B(i, o) = w[o·kin + i] (transposed)
+        // dw = dyᵀ·x: A(o, r) = dy[r·nout + o], B(i, r) = x[r·kin + i] (both transposed)
+        const bool fx = !dx || (nout % fast::BK == 0 && kin % 8 == 0);
+        const bool fw = !dw || (m % fast::BK == 0 && nout % 8 == 0 && kin % 8 == 0);
+        if (fx && fw) {
+            if (dx) {
+                RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
+                const int st = fast::run<false, true>(ctx, dyp, nout, static_cast<const T*>(w), kin, ep, m, kin, nout);
+                if (st != NOTT_ERR_UNSUPPORTED) {
+                    if (st != NOTT_OK) return st;
+                    dx = nullptr;
+                }
+            }
+            if (dw) {
+                DwDbStore ep{dw, nullptr, nout, kin, accumulate};
+                const int st = fast::run<true, true>(ctx, dyp, nout, static_cast<const T*>(x), kin, ep, nout, kin, m);
+                if (st != NOTT_ERR_UNSUPPORTED) {
+                    if (st != NOTT_OK) return st;
+                    dw = nullptr;
+                    if (db) {
+                        float* part = static_cast<float*>(workspace(ctx, sizeof(float) * kColSumSlabs * (size_t)nout));
+                        if (!part) return NOTT_ERR_ALLOC;
+                        hipLaunchKernelGGL(colsum_partial_kernel<T>, dim3((unsigned)ceil_div(nout, 64), kColSumSlabs),
+                                           dim3(256), 0, ctx->stream, dyp, m, nout, part);
+                        hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)ceil_div(nout, 256)), dim3(256), 0,
+                                           ctx->stream, part, nout, db, accumulate);
+                        db = nullptr;
+                        const int st2 = launch_status(ctx, "linear db");
+                        if (st2 != NOTT_OK) return st2;
+                    }
+                }
+            }
+        }
+    }
     if (dx) {
         RowKLoader<T> la{dyp, nout, m, nout, vec16<T>(dy, nout)};
         ColKLoader<T> lb{static_cast<const T*>(w), kin, kin, nout};
