@@ -46,9 +46,7 @@ __device__ __forceinline__ int toff(int row, int ch, int nch) {
     return (row >> 4) * (nch << 8) + (ch << 8) + (((row ^ ch) & 15) << 4);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-    return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-}
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) { return pack_bf16x2(a, b); }
 
 template <typename T>
 __device__ __forceinline__ void mma(const u32x4& a, const u32x4& b, f32x4& acc) {
@@ -64,46 +62,54 @@ __device__ __forceinline__ void mma(const u32x4& a, const u32x4& b, f32x4& acc) 
     }
 }
 
-// MFMA whose A operand is the 64-byte k-slice `s` of register tiles v[t][e]
-// (t = 16-wide tile of the k dimension, e = its 4 slots per lane).  For fp32
-// the float vector goes to the MFMA directly: building a u32x4 from
-// bit-cast floats and casting it back makes hipcc (ROCm 7.2) feed the first
-// component to all four v_mfma_f32_16x16x4_f32 issues.
-template <typename T>
-__device__ __forceinline__ void mma_rf(const f32x4 (&v)[4], int s, const u32x4& b, f32x4& acc) {
-    if constexpr (sizeof(T) == 2) {
-        const f32x4 x = v[2 * s], y = v[2 * s + 1];
-        const u32x4 a = u32x4{pack_bf16(x.x, x.y), pack_bf16(x.z, x.w), pack_bf16(y.x, y.y), pack_bf16(y.z, y.w)};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
-                                                      0, 0, 0);
-    } else {
-        const f32x4 af = v[s];
-        const f32x4 bf = __builtin_bit_cast(f32x4, b);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], acc, 0, 0, 0);
-    }
-}
-
-// As mma_rf, but for bf16 the A values are split into a bf16 head and a bf16
-// remainder (two MFMAs), so the product carries ~16 mantissa bits of ds.
-// Used for ds, whose entries are differences (p∘(dp − rowsum)) and lose the
-// most to a single bf16 rounding.
-template <typename T>
-__device__ __forceinline__ void mma_rf2(const f32x4 (&v)[4], int s, const u32x4& b, f32x4& acc) {
-    if constexpr (sizeof(T) == 2) {
-        f32x4 lo[4];
+// Register tiles v[4] (4 × 16 k-slots) as MFMA A operands, packed once per
+// block.  bf16: hi[s] is the 64-byte k-slice s rounded to bf16, tiles 2s and
+// 2s+1 interleaved as k-slots {4q..4q+3, 16+4q..16+4q+3}; with LO, lo[s] is
+// the bf16 remainder v − hi, so the two MFMAs carry ~16 mantissa bits (used
+// for ds, whose entries are differences p∘(dp − rowsum) and lose the most to
+// one bf16 rounding, and for p in the dk/dv pass).  fp32 passes the float
+// vectors straight to the MFMA: building a u32x4 from bit-cast floats and
+// casting it back makes hipcc (ROCm 7.2) feed the first component to all four
+// v_mfma_f32_16x16x4_f32 issues.
+template <typename T, bool LO>
+struct RegA {
+    u32x4 hi[2], lo[2];
+    const f32x4* v;
+    __device__ __forceinline__ explicit RegA(const f32x4 (&t)[4]) : v(t) {
+        if constexpr (sizeof(T) == 2) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) lo[t][e] = v[t][e] - bf16_to_f32(f32_to_bf16(v[t][e]));
-        mma_rf<T>(v, s, b, acc);
-        mma_rf<T>(lo, s, b, acc);
-    } else {
-        mma_rf<T>(v, s, b, acc);
+            for (int s = 0; s < 2; ++s) {
+                const f32x4 x = t[2 * s], y = t[2 * s + 1];
+                hi[s] = u32x4{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w), pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w)};
+                if constexpr (LO) {
+                    auto lo_of = [](uint32_t h, float a, float b) {
+                        return pack_bf16x2(a - __builtin_bit_cast(float, h << 16),
+                                           b - __builtin_bit_cast(float, h & 0xffff0000u));
+                    };
+                    lo[s] = u32x4{lo_of(hi[s].x, x.x, x.y), lo_of(hi[s].y, x.z, x.w), lo_of(hi[s].z, y.x, y.y),
+                                  lo_of(hi[s].w, y.z, y.w)};
+                }
+            }
+        }
     }
-}
+    // acc += A(slice s) · b
+    __device__ __forceinline__ void mma(int s, const u32x4& b, f32x4& acc) const {
+        if constexpr (sizeof(T) == 2) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, hi[s]), __builtin_bit_cast(bf16x8, b),
+                                                          acc, 0, 0, 0);
+            if constexpr (LO)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, lo[s]),
+                                                              __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+        } else {
+            const f32x4 af = v[s];
+            const f32x4 bf = __builtin_bit_cast(f32x4, b);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], acc, 0, 0, 0);
+        }
+    }
+};
 
 // Loads 16 bytes (E elements) of row `row` starting at column c0 of a
 // [rows × dh] matrix, zero outside; vec = rows are 16-byte aligned.
@@ -134,6 +140,49 @@ __device__ __forceinline__ void fill_nat(char* tile, const T* base, int r0, int 
         *reinterpret_cast<u32x4*>(tile + toff(row, ch, NCHD)) = load_chunk<T>(base, r0 + row, nrows, ch * E, dh, vec);
     }
 }
+
+// A natural tile staged through registers, so that the next block's loads
+// are in flight while the current block is computed: load() issues them,
+// store() writes the tile after the barrier.  With 16-byte aligned rows and
+// dh a multiple of the chunk width, every load is unconditional (rows past
+// the end re-read a valid row and are zeroed at the store).
+template <typename T, int NCHD>
+struct TileRegs {
+    static constexpr int E = AT<T>::E;
+    static constexpr int N = (BR * NCHD + kThreads - 1) / kThreads;
+    u32x4 r[N];
+    uint32_t ok = 0;
+    __device__ __forceinline__ void load(const T* base, int r0, int nrows, int dh, bool vec) {
+        if (vec && dh % E == 0) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const int t = threadIdx.x + j * kThreads;
+                const int ch = t % NCHD, row = r0 + t / NCHD;
+                const bool good = t < BR * NCHD && row < nrows && ch * E < dh;
+                const int rr = row < nrows ? row : nrows - 1;
+                r[j] = *reinterpret_cast<const u32x4*>(base + (int64_t)rr * dh + (ch * E < dh ? ch * E : 0));
+                ok = good ? (ok | (1u << j)) : (ok & ~(1u << j));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const int t = threadIdx.x + j * kThreads;
+                const int ch = t % NCHD, row = t / NCHD;
+                r[j] = t < BR * NCHD ? load_chunk<T>(base, r0 + row, nrows, ch * E, dh, vec) : u32x4{0u, 0u, 0u, 0u};
+            }
+            ok = ~0u;
+        }
+    }
+    __device__ __forceinline__ void store(char* tile) const {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            const int t = threadIdx.x + j * kThreads;
+            if (t < BR * NCHD)
+                *reinterpret_cast<u32x4*>(tile + toff(t / NCHD, t % NCHD, NCHD)) =
+                    (ok >> j) & 1u ? r[j] : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+};
 
 // Row (within a 64-row block) stored at k-slot position `pos` of the
 // transposed tile (the bf16 interleave described above; identity for fp32).
@@ -184,6 +233,40 @@ __device__ __forceinline__ u32x4 frag(const char* tile, int r0, int s, int nch) 
     return *reinterpret_cast<const u32x4*>(tile + toff(r0 + (lane & 15), 4 * s + (lane >> 4), nch));
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// bf16 B fragment for columns d0..d0+15 whose 8 k-slots are rows ra+0..3 and
+// rb+0..3 of a natural [row][d] tile (ra, rb per 16-lane group), read with
+// two transposing LDS reads (ds_read_b64_tr_b16: within each 16-lane group,
+// result lane j, element e comes from lane 4e + j/4, element j % 4; so lane
+// s reads the 4 columns d0 + 4·(s%4).. of row ra + s/4).
+__device__ __forceinline__ u32x4 frag_tr(const char* tile, int nch, int ra, int rb, int d0) {
+    const int s = threadIdx.x & 15;
+    const int d = d0 + 4 * (s & 3);
+    const int ch = d >> 3, byte = (d & 7) * 2;
+    const v4i16 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(tile + toff(ra + (s >> 2), ch, nch) + byte));
+    const v4i16 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(tile + toff(rb + (s >> 2), ch, nch) + byte));
+    const u32x2 xu = __builtin_bit_cast(u32x2, x), yu = __builtin_bit_cast(u32x2, y);
+    return u32x4{xu.x, xu.y, yu.x, yu.y};
+}
+
+// B operand of the second-stage MFMAs (p·v, pᵀ·do, dsᵀ·q, ds·k): columns
+// d0 = 16·dt, k-slice s of the register-resident tiles.  bf16 reads the
+// natural tile with transposing reads, in the key interleave of RegA
+// (k-slots 0..3 = rows 32s + 4·kq + e, 4..7 = rows 32s + 16 + 4·kq + e); fp32
+// reads the transposed tile.
+template <typename T, int NCHD, int NCHT>
+__device__ __forceinline__ u32x4 frag2(const char* nat, const char* trans, int dt, int s) {
+    if constexpr (sizeof(T) == 2) {
+        const int kq = (threadIdx.x & 63) >> 4;
+        return frag_tr(nat, NCHD, 32 * s + 4 * kq, 32 * s + 16 + 4 * kq, dt * 16);
+    } else {
+        return frag(trans, dt * 16, s, NCHT);
+    }
+}
+
 struct AttnParams {
     int32_t t, s, dh;
     int32_t causal;
@@ -209,8 +292,8 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
     char* lk = smem + X;
     char* lvt = smem + 2 * X;
 
-    const int bh = blockIdx.y;
-    const int qb = p.nqb - 1 - (int)blockIdx.x;      // heaviest (causal) blocks first
+    const int bh = blockIdx.x;
+    const int qb = p.nqb - 1 - (int)blockIdx.y;      // heaviest (causal) blocks dispatched first
     const int q0 = qb * BR;
     const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -226,12 +309,20 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
 
     int kb_end = p.nkb;
     if (p.causal) kb_end = min(kb_end, (q0 + BR - 1) / BR + 1);
+    TileRegs<T, NCHD> rk, rv;
+    rk.load(k + koff, 0, p.s, p.dh, p.vec);
+    if constexpr (sizeof(T) == 2) rv.load(v + koff, 0, p.s, p.dh, p.vec);
     for (int kb = 0; kb < kb_end; ++kb) {
         const int k0 = kb * BR;
         __syncthreads();
-        fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
-        fill_trans<T, DP>(lvt, v + koff, k0, p.s, p.dh, p.vec);
+        rk.store(lk);
+        if constexpr (sizeof(T) == 2) rv.store(lvt);   // natural v
+        else fill_trans<T, DP>(lvt, v + koff, k0, p.s, p.dh, p.vec);
         __syncthreads();
+        if (kb + 1 < kb_end) {
+            rk.load(k + koff, k0 + BR, p.s, p.dh, p.vec);
+            if constexpr (sizeof(T) == 2) rv.load(v + koff, k0 + BR, p.s, p.dh, p.vec);
+        }
         // scores in transposed form: lane holds s[my_q][k0 + 16·kt + 4·kq + e]
         f32x4 sc[4];
 #pragma unroll
@@ -241,25 +332,27 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
             for (int s = 0; s < NS; ++s) mma<T>(frag(lk, kt * 16, s, NCHD), frag(lq, wid * 16, s, NCHD), sc[kt]);
         }
         float mx = -INFINITY;
+        // masking only where the block touches the diagonal or the end
+        const bool full = k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int key = k0 + kt * 16 + kq * 4 + e;
-                const bool ok = key < p.s && !(p.causal && key > my_q);
+                const bool ok = full || (key < p.s && !(p.causal && key > my_q));
                 sc[kt][e] = ok ? sc[kt][e] * sl2 : -INFINITY;   // log2 domain
                 mx = fmaxf(mx, sc[kt][e]);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(m, mx);
-        const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m - m_new);
+        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m - m_new);
         float rs = 0.f;
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float pe = (m_new == -INFINITY) ? 0.f : exp2f(sc[kt][e] - m_new);
+                const float pe = (m_new == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sc[kt][e] - m_new);
                 sc[kt][e] = pe;
                 rs += pe;
             }
@@ -275,10 +368,11 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
         for (int dt = 0; dt < ND; ++dt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[dt][e] *= al[e];
+        const RegA<T, false> pa(sc);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
 #pragma unroll
-            for (int dt = 0; dt < ND; ++dt) mma_rf<T>(sc, s, frag(lvt, dt * 16, s, NCHT), acc[dt]);
+            for (int dt = 0; dt < ND; ++dt) pa.mma(s, frag2<T, NCHD, NCHT>(lvt, lvt, dt, s), acc[dt]);
     }
     // o = acc / l (rows 4·kq + e of this wave's 16), lse = m + ln l (in natural log).
     float li[4];
@@ -334,8 +428,8 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
     float* llse = reinterpret_cast<float*>(smem + 6 * X);
     float* lds_ = llse + BR;
 
-    const int bh = blockIdx.y;
-    const int kb = blockIdx.x;
+    const int bh = blockIdx.x;
+    const int kb = blockIdx.y;       // key blocks outermost: the longest (causal) ones are dispatched first
     const int k0 = kb * BR;
     const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -350,19 +444,41 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
     for (int i = 0; i < ND; ++i) adk[i] = adv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int qb_begin = p.causal ? k0 / BR : 0;
+    TileRegs<T, NCHD> rq, rdo;
+    // lse (log2 domain) and rowsum(p∘dp) of the next query block, one per thread < BR
+    float nxt_lse = 0.f, nxt_ds = 0.f;
+    auto load_stats = [&](int r0) {
+        const int row = r0 + (int)threadIdx.x;
+        const bool in = threadIdx.x < BR && row < p.t;
+        const int64_t i = (int64_t)bh * p.t + (in ? row : 0);
+        nxt_lse = in ? lse[i] * 1.4426950408889634f : 0.f;
+        nxt_ds = in ? dsum[i] : 0.f;
+    };
+    if (qb_begin < p.nqb) {
+        rq.load(q + qoff, qb_begin * BR, p.t, p.dh, p.vec);
+        rdo.load(dO + qoff, qb_begin * BR, p.t, p.dh, p.vec);
+        load_stats(qb_begin * BR);
+    }
     for (int qb = qb_begin; qb < p.nqb; ++qb) {
         const int q0 = qb * BR;
         __syncthreads();
-        fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
-        fill_nat<T, NCHD>(ldo, dO + qoff, q0, p.t, p.dh, p.vec);
-        fill_trans<T, DP>(lqt, q + qoff, q0, p.t, p.dh, p.vec);
-        fill_trans<T, DP>(ldot, dO + qoff, q0, p.t, p.dh, p.vec);
+        rq.store(lq);
+        rdo.store(ldo);
+        if constexpr (sizeof(T) == 4) {
+            fill_trans<T, DP>(lqt, q + qoff, q0, p.t, p.dh, p.vec);
+            fill_trans<T, DP>(ldot, dO + qoff, q0, p.t, p.dh, p.vec);
+        }
         if (threadIdx.x < BR) {
-            const int row = q0 + threadIdx.x;
-            llse[threadIdx.x] = row < p.t ? lse[(int64_t)bh * p.t + row] * 1.4426950408889634f : 0.f;
-            lds_[threadIdx.x] = row < p.t ? dsum[(int64_t)bh * p.t + row] : 0.f;
+            llse[threadIdx.x] = nxt_lse;
+            lds_[threadIdx.x] = nxt_ds;
         }
         __syncthreads();
+        if (qb + 1 < p.nqb) {
+            rq.load(q + qoff, q0 + BR, p.t, p.dh, p.vec);
+            rdo.load(dO + qoff, q0 + BR, p.t, p.dh, p.vec);
+            load_stats(q0 + BR);
+        }
+        const bool full = q0 + BR <= p.t && k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
         // s and dp in transposed form: lane holds [q0 + 16·qt + 4·kq + e][my_k]
         f32x4 pt[4], dpt[4];
 #pragma unroll
@@ -380,17 +496,18 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
             for (int e = 0; e < 4; ++e) {
                 const int ql = qt * 16 + kq * 4 + e;
                 const int qrow = q0 + ql;
-                const bool ok = qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow);
-                const float pe = ok ? exp2f(pt[qt][e] * sl2 - llse[ql]) : 0.f;
+                const bool ok = full || (qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow));
+                const float pe = __builtin_amdgcn_exp2f(ok ? pt[qt][e] * sl2 - llse[ql] : -INFINITY);
                 pt[qt][e] = pe;
                 dpt[qt][e] = pe * (dpt[qt][e] - lds_[ql]);   // ds
             }
+        const RegA<T, true> pa(pt), pds(dpt);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
 #pragma unroll
             for (int dt = 0; dt < ND; ++dt) {
-                mma_rf2<T>(pt, s, frag(ldot, dt * 16, s, NCHT), adv[dt]);
-                mma_rf2<T>(dpt, s, frag(lqt, dt * 16, s, NCHT), adk[dt]);
+                pa.mma(s, frag2<T, NCHD, NCHT>(ldo, ldot, dt, s), adv[dt]);
+                pds.mma(s, frag2<T, NCHD, NCHT>(lq, lqt, dt, s), adk[dt]);
             }
     }
 #pragma unroll
@@ -433,8 +550,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
     char* lv = smem + 3 * X;
     char* lkt = smem + 4 * X;
 
-    const int bh = blockIdx.y;
-    const int qb = p.nqb - 1 - (int)blockIdx.x;
+    const int bh = blockIdx.x;
+    const int qb = p.nqb - 1 - (int)blockIdx.y;      // heaviest (causal) blocks dispatched first
     const int q0 = qb * BR;
     const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -452,14 +569,22 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
     int kb_end = p.nkb;
     if (p.causal) kb_end = min(kb_end, (q0 + BR - 1) / BR + 1);
     float my_ds;
+    TileRegs<T, NCHD> rk, rv;
     if constexpr (EXACT_DSUM) {
         float part = 0.f;
+        rk.load(k + koff, 0, p.s, p.dh, p.vec);
+        rv.load(v + koff, 0, p.s, p.dh, p.vec);
         for (int kb = 0; kb < kb_end; ++kb) {
             const int k0 = kb * BR;
+            const bool full = q0 + BR <= p.t && k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
             __syncthreads();
-            fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
-            fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
+            rk.store(lk);
+            rv.store(lv);
             __syncthreads();
+            // next block (or, after the last, block 0 for the main pass)
+            const int nk0 = kb + 1 < kb_end ? k0 + BR : 0;
+            rk.load(k + koff, nk0, p.s, p.dh, p.vec);
+            rv.load(v + koff, nk0, p.s, p.dh, p.vec);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -471,8 +596,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int key = k0 + kt * 16 + kq * 4 + e;
-                    const bool ok = my_q < p.t && key < p.s && !(p.causal && key > my_q);
-                    part += ok ? exp2f(sc[e] * sl2 - my_lse) * dp[e] : 0.f;
+                    const bool ok = full || (my_q < p.t && key < p.s && !(p.causal && key > my_q));
+                    part += __builtin_amdgcn_exp2f(ok ? sc[e] * sl2 - my_lse : -INFINITY) * (ok ? dp[e] : 0.f);
                 }
             }
         }
@@ -482,14 +607,21 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
         if (kq == 0 && my_q < p.t) dsum[(int64_t)bh * p.t + my_q] = my_ds;
     } else {
         my_ds = my_q < p.t ? dsum[(int64_t)bh * p.t + my_q] : 0.f;
+        rk.load(k + koff, 0, p.s, p.dh, p.vec);
+        rv.load(v + koff, 0, p.s, p.dh, p.vec);
     }
     for (int kb = 0; kb < kb_end; ++kb) {
         const int k0 = kb * BR;
+        const bool full = q0 + BR <= p.t && k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
         __syncthreads();
-        fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
-        fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
-        fill_trans<T, DP>(lkt, k + koff, k0, p.s, p.dh, p.vec);
+        rk.store(lk);
+        rv.store(lv);
+        if constexpr (sizeof(T) == 4) fill_trans<T, DP>(lkt, k + koff, k0, p.s, p.dh, p.vec);
         __syncthreads();
+        if (kb + 1 < kb_end) {
+            rk.load(k + koff, k0 + BR, p.s, p.dh, p.vec);
+            rv.load(v + koff, k0 + BR, p.s, p.dh, p.vec);
+        }
         // lane holds s / dp at [my_q][k0 + 16·kt + 4·kq + e]
         f32x4 sc[4], dp[4];
 #pragma unroll
@@ -506,14 +638,15 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int key = k0 + kt * 16 + kq * 4 + e;
-                const bool ok = my_q < p.t && key < p.s && !(p.causal && key > my_q);
-                const float pe = ok ? exp2f(sc[kt][e] * sl2 - my_lse) : 0.f;
+                const bool ok = full || (my_q < p.t && key < p.s && !(p.causal && key > my_q));
+                const float pe = __builtin_amdgcn_exp2f(ok ? sc[kt][e] * sl2 - my_lse : -INFINITY);
                 dp[kt][e] = pe * (dp[kt][e] - my_ds);
             }
+        const RegA<T, true> pds(dp);
 #pragma unroll
         for (int s = 0; s < KS; ++s)
 #pragma unroll
-            for (int dt = 0; dt < ND; ++dt) mma_rf2<T>(dp, s, frag(lkt, dt * 16, s, NCHT), acc[dt]);
+            for (int dt = 0; dt < ND; ++dt) pds.mma(s, frag2<T, NCHD, NCHT>(lk, lkt, dt, s), acc[dt]);
     }
 #pragma unroll
     for (int dt = 0; dt < ND; ++dt) {
@@ -532,7 +665,9 @@ int check(nott_ctx ctx, const nott_attn_desc* d, AttnParams* p, int elem) {
     NOTT_REQUIRE(ctx, d->b >= 0 && d->h >= 0 && d->t >= 0 && d->s >= 0 && d->dh > 0, "attention: bad shape");
     // LDS holds six 64-row tiles of the padded head dim in the dk/dv pass.
     NOTT_REQUIRE(ctx, d->dh <= (elem == 2 ? 128 : 64), "attention: head dim above 128 (bf16) / 64 (fp32) is not supported");
-    NOTT_REQUIRE(ctx, d->b * d->h <= 65535, "attention: too many (batch, head) pairs");
+    // grid: x = (batch, head) pairs, y = 64-row blocks
+    NOTT_REQUIRE(ctx, d->b * d->h <= 0x7fffffff, "attention: too many (batch, head) pairs");
+    NOTT_REQUIRE(ctx, ceil_div(d->t, BR) <= 65535 && ceil_div(d->s, BR) <= 65535, "attention: sequence too long");
     NOTT_REQUIRE(ctx, d->t * d->dh < (int64_t(1) << 31) && d->s * d->dh < (int64_t(1) << 31),
                  "attention: sequence too long");
     NOTT_REQUIRE(ctx, !d->causal || d->s > 0, "attention: causal needs keys");
@@ -564,7 +699,7 @@ int fwd_ns(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const voi
     if (lds > 64 * 1024)
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, NS>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((attn_fwd_kernel<T, NS>), dim3((unsigned)p.nqb, (unsigned)(d->b * d->h)), dim3(kThreads), lds,
+    hipLaunchKernelGGL((attn_fwd_kernel<T, NS>), dim3((unsigned)(d->b * d->h), (unsigned)p.nqb), dim3(kThreads), lds,
                        ctx->stream, static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                        static_cast<T*>(o), lse, p);
     return launch_status(ctx, "attention_fwd");
@@ -590,10 +725,10 @@ int bwd_ns(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const voi
     if (!EXACT)
         hipLaunchKernelGGL(attn_dsum_kernel<T>, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, ctx->stream,
                            static_cast<const T*>(o), static_cast<const T*>(dO), dsum, rows, (int)d->dh);
-    hipLaunchKernelGGL((attn_dq_kernel<T, NS, EXACT>), dim3((unsigned)p.nqb, bh), dim3(kThreads), lds_q, ctx->stream,
+    hipLaunchKernelGGL((attn_dq_kernel<T, NS, EXACT>), dim3(bh, (unsigned)p.nqb), dim3(kThreads), lds_q, ctx->stream,
                        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                        static_cast<const T*>(dO), lse, dsum, static_cast<T*>(dq), p);
-    hipLaunchKernelGGL((attn_dkdv_kernel<T, NS>), dim3((unsigned)p.nkb, bh), dim3(kThreads), lds_kv, ctx->stream,
+    hipLaunchKernelGGL((attn_dkdv_kernel<T, NS>), dim3(bh, (unsigned)p.nkb), dim3(kThreads), lds_kv, ctx->stream,
                        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                        static_cast<const T*>(dO), lse, dsum, static_cast<T*>(dk), static_cast<T*>(dv), p);
     return launch_status(ctx, "attention_bwd");

@@ -84,12 +84,17 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t h) {
     return __builtin_bit_cast(float, (uint32_t)h << 16);
 }
 
-// Round to nearest even; NaN maps to a quiet NaN of the same sign.
+// Round to nearest even; NaN maps to a quiet NaN of the same sign (gfx950's
+// v_cvt_pk_bf16_f32).
 __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x0040u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+    return __builtin_bit_cast(bf16_t, (__bf16)f);
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// Two floats -> packed bf16 pair (a in the low half), one instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
 template <typename T> struct Io;
