@@ -100,6 +100,14 @@ CONV = [
     (3, 64, 5, 13, 64, 3, 3, 1, 1, 1),         # 3x3 tile spanning three images
     (2, 32, 60, 60, 128, 3, 3, 1, 1, 1),       # widest row the 3x3 kernel takes
     (5, 128, 7, 7, 192, 3, 3, 1, 1, 1),        # ragged last pixel tile
+    # bf16 column path (n·p·q a multiple of 64): strided 3x3, 1x1 projection,
+    # 7x7 stem, small-width 3x3 wgrad, odd channel counts
+    (4, 64, 56, 56, 128, 3, 3, 2, 1, 1),
+    (4, 64, 56, 56, 128, 1, 1, 2, 0, 1),
+    (1, 3, 64, 64, 64, 7, 7, 2, 3, 1),
+    (16, 64, 14, 14, 64, 3, 3, 1, 1, 1),
+    (64, 32, 7, 7, 64, 3, 3, 1, 1, 1),
+    (2, 5, 16, 16, 64, 3, 3, 1, 1, 2),
 ]
 
 

@@ -21,6 +21,7 @@ namespace {
 
 using namespace nott::gemm;
 using ::FastDiv;
+using nott::ceil_div;
 
 struct Geom {
     int32_t n, c, h, w, k, r, s, p, q;
@@ -274,6 +275,213 @@ __global__ __launch_bounds__(256) void conv_db_kernel(const T* __restrict__ dy, 
     if (threadIdx.x == 0) db[ko] = accumulate ? db[ko] + s : s;
 }
 
+// ---------------------------------------------------------------------------
+// Column path (bf16, NCHW) for the shapes the 3×3 stride-1 kernels do not
+// take (strided, 1×1, 7×7 stem, small image widths): explicit column buffers
+// and the fast bf16 GEMM, instead of element gathers inside the GEMM loads.
+// With CRS = c·r·s padded to CRSp (a multiple of 64) and NPQ = n·p·q:
+//   col[crs][npq]   = x[n, c, p·sh−ph+r·dh, q·sw−pw+s·dw]   (im2col, 0 outside)
+//   dyt[k][npq]     = dy[n, k, p, q]                        (channel-major dy)
+//   wp[k][crs]      = w[k, c, r, s]                          (zero-padded rows)
+//   fwd  : y[n,k,pq]   = Σ_crs wp[k][crs]·col[crs][npq]      (GEMM M=k, N=npq)
+//   wgrad: dw[k][crs]  = Σ_npq dyt[k][npq]·col[crs][npq]     (GEMM M=k, N=crs, K=npq)
+//   dgrad: dcol[crs][npq] = Σ_k wp[k][crs]·dyt[k][npq], then
+//          dx[n,c,h,w] = Σ_{r,s} dcol[(c,r,s)][(n, (h+ph−r·dh)/sh, (w+pw−s·dw)/sw)]
+//          over the exact, in-range quotients (col2im as a gather: no atomics).
+// ---------------------------------------------------------------------------
+constexpr int64_t kColAlign = 256;
+inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void pack_w_kernel(const T* __restrict__ w, int32_t K, int32_t CRS, int32_t CRSp,
+                                                     T* __restrict__ wp) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)K * CRSp) return;
+    const int32_t k = (int32_t)(i / CRSp), j = (int32_t)(i % CRSp);
+    wp[i] = j < CRS ? w[(int64_t)k * CRS + j] : T(0);
+}
+
+// One thread: 8 consecutive npq of one crs row (one 16-byte store).
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_kernel(const T* __restrict__ x, Geom g, int32_t CRS, int32_t CRSp,
+                                                     int32_t NPQ, T* __restrict__ col) {
+    constexpr int E = 16 / (int)sizeof(T);
+    const int32_t per_row = NPQ / E;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)CRSp * per_row) return;
+    const int32_t crs = (int32_t)(t / per_row), m0 = (int32_t)(t % per_row) * E;
+    T v[E];
+    if (crs < CRS) {
+        uint32_t c, rs, r, s;
+        g.fd_rs.divmod((uint32_t)crs, c, rs);
+        g.fd_s.divmod(rs, r, s);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            uint32_t n, pq, pp, qq;
+            g.fd_pq.divmod((uint32_t)(m0 + e), n, pq);
+            g.fd_q.divmod(pq, pp, qq);
+            const int32_t h = (int32_t)pp * g.sh - g.ph + (int32_t)r * g.dh;
+            const int32_t w = (int32_t)qq * g.sw - g.pw + (int32_t)s * g.dw;
+            v[e] = (h >= 0 && h < g.h && w >= 0 && w < g.w) ? x[(((int64_t)n * g.c + c) * g.h + h) * g.w + w] : T(0);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = T(0);
+    }
+    *reinterpret_cast<u32x4*>(col + (int64_t)crs * NPQ + m0) = Pack<T>::make(v);
+}
+
+// dyt[k][n·PQ + pq] = dy[n][k][pq]; one thread per 8 consecutive npq.
+template <typename T>
+__global__ __launch_bounds__(256) void to_kn_kernel(const T* __restrict__ dy, Geom g, int32_t NPQ, T* __restrict__ dyt) {
+    constexpr int E = 16 / (int)sizeof(T);
+    const int32_t per_row = NPQ / E;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)g.k * per_row) return;
+    const int32_t k = (int32_t)(t / per_row), m0 = (int32_t)(t % per_row) * E;
+    const int32_t PQ = g.p * g.q;
+    T v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        uint32_t n, pq;
+        g.fd_pq.divmod((uint32_t)(m0 + e), n, pq);
+        v[e] = dy[((int64_t)n * g.k + k) * PQ + pq];
+    }
+    *reinterpret_cast<u32x4*>(dyt + (int64_t)k * NPQ + m0) = Pack<T>::make(v);
+}
+
+// dx[n,c,h,w] = Σ over (r, s) whose source output position is exact and in range.
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_kernel(const T* __restrict__ dcol, Geom g, int32_t NPQ, T* __restrict__ dx) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)g.n * g.c * g.h * g.w;
+    if (i >= total) return;
+    uint32_t nc, hw, h, w, n, c;
+    g.fd_hw.divmod((uint32_t)i, nc, hw);
+    g.fd_w.divmod(hw, h, w);
+    n = nc / (uint32_t)g.c;
+    c = nc - n * (uint32_t)g.c;
+    float acc = 0.f;
+    for (int32_t r = 0; r < g.r; ++r) {
+        const int32_t ph = (int32_t)h + g.ph - r * g.dh;
+        if (ph < 0) break;
+        uint32_t pp, remh;
+        g.fd_sh.divmod((uint32_t)ph, pp, remh);
+        if (remh != 0 || (int32_t)pp >= g.p) continue;
+        for (int32_t s = 0; s < g.s; ++s) {
+            const int32_t pw = (int32_t)w + g.pw - s * g.dw;
+            if (pw < 0) break;
+            uint32_t qq, remw;
+            g.fd_sw.divmod((uint32_t)pw, qq, remw);
+            if (remw != 0 || (int32_t)qq >= g.q) continue;
+            const int64_t crs = ((int64_t)c * g.r + r) * g.s + s;
+            acc += Io<T>::ld(dcol, crs * NPQ + ((int64_t)n * g.p + pp) * g.q + qq);
+        }
+    }
+    Io<T>::st(dx, i, acc);
+}
+
+// y[n, k, pq] = acc + b[k] for GEMM (m = k, n = npq).
+template <typename T>
+struct ColFwdStore {
+    T* y;
+    const float* b;
+    Geom g;
+    int64_t NPQ;
+    __device__ __forceinline__ void store(int64_t k, int64_t m, float v) const {
+        if (k >= g.k || m >= NPQ) return;
+        uint32_t n, pq;
+        g.fd_pq.divmod((uint32_t)m, n, pq);
+        if (b) v += b[k];
+        Io<T>::st(y, ((int64_t)n * g.k + k) * ((int64_t)g.p * g.q) + pq, v);
+    }
+};
+
+struct ColPlan {
+    int64_t CRS, CRSp, NPQ;
+};
+
+bool col_applies(const nott_conv2d_desc* d, int64_t p, int64_t q, bool need_k64) {
+    const int64_t npq = d->n * p * q;
+    return d->layout == NOTT_NCHW && npq % 64 == 0 && (!need_k64 || d->k % 64 == 0) &&
+           d->c * d->r * d->s <= (int64_t(1) << 20);
+}
+
+// Carves aligned pieces out of one workspace request.
+struct Carve {
+    int64_t off = 0;
+    int64_t take(int64_t bytes) {
+        const int64_t o = off;
+        off = align_up(off + bytes, kColAlign);
+        return o;
+    }
+};
+
+int col_fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const bf16_t* x, const bf16_t* w,
+            const float* b, bf16_t* y) {
+    const Geom g = make_geom(d, p, q);
+    const int64_t CRS = d->c * d->r * d->s, CRSp = align_up(CRS, 64), NPQ = d->n * p * q;
+    Carve cv;
+    const int64_t o_wp = cv.take(2 * d->k * CRSp), o_col = cv.take(2 * CRSp * NPQ);
+    const int64_t o_part = cv.take(4 * (int64_t)fast::partial_floats(ctx, d->k, NPQ, CRSp));
+    char* ws = static_cast<char*>(nott::workspace(ctx, (size_t)cv.off));
+    if (!ws) return NOTT_ERR_ALLOC;
+    bf16_t* wp = reinterpret_cast<bf16_t*>(ws + o_wp);
+    bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
+    hipLaunchKernelGGL(pack_w_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * CRSp, 256)), dim3(256), 0, ctx->stream, w,
+                       (int32_t)d->k, (int32_t)CRS, (int32_t)CRSp, wp);
+    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(CRSp * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
+                       x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+    ColFwdStore<bf16_t> ep{y, b, g, NPQ};
+    return fast::run<false, true>(ctx, wp, CRSp, col, NPQ, ep, d->k, NPQ, CRSp, 0,
+                                  reinterpret_cast<float*>(ws + o_part));
+}
+
+int col_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const bf16_t* x, const bf16_t* dy,
+              float* dw, int accumulate) {
+    const Geom g = make_geom(d, p, q);
+    const int64_t CRS = d->c * d->r * d->s, CRSp = align_up(CRS, 64), NPQ = d->n * p * q;
+    Carve cv;
+    const int64_t o_dyt = cv.take(2 * d->k * NPQ), o_col = cv.take(2 * CRSp * NPQ);
+    const int64_t o_part = cv.take(4 * (int64_t)fast::partial_floats(ctx, d->k, CRSp, NPQ));
+    char* ws = static_cast<char*>(nott::workspace(ctx, (size_t)cv.off));
+    if (!ws) return NOTT_ERR_ALLOC;
+    bf16_t* dyt = reinterpret_cast<bf16_t*>(ws + o_dyt);
+    bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
+    hipLaunchKernelGGL(to_kn_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
+                       dy, g, (int32_t)NPQ, dyt);
+    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(CRSp * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
+                       x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+    WgradStore ep{dw, d->k, CRS, accumulate};
+    return fast::run<false, false>(ctx, dyt, NPQ, col, NPQ, ep, d->k, CRSp, NPQ, 0,
+                                   reinterpret_cast<float*>(ws + o_part));
+}
+
+int col_dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const bf16_t* dy, const bf16_t* w,
+              bf16_t* dx) {
+    const Geom g = make_geom(d, p, q);
+    const int64_t CRS = d->c * d->r * d->s, CRSp = align_up(CRS, 64), NPQ = d->n * p * q;
+    Carve cv;
+    const int64_t o_wp = cv.take(2 * d->k * CRSp), o_dyt = cv.take(2 * d->k * NPQ), o_dcol = cv.take(2 * CRSp * NPQ);
+    const int64_t o_part = cv.take(4 * (int64_t)fast::partial_floats(ctx, CRSp, NPQ, d->k));
+    char* ws = static_cast<char*>(nott::workspace(ctx, (size_t)cv.off));
+    if (!ws) return NOTT_ERR_ALLOC;
+    bf16_t* wp = reinterpret_cast<bf16_t*>(ws + o_wp);
+    bf16_t* dyt = reinterpret_cast<bf16_t*>(ws + o_dyt);
+    bf16_t* dcol = reinterpret_cast<bf16_t*>(ws + o_dcol);
+    hipLaunchKernelGGL(pack_w_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * CRSp, 256)), dim3(256), 0, ctx->stream, w,
+                       (int32_t)d->k, (int32_t)CRS, (int32_t)CRSp, wp);
+    hipLaunchKernelGGL(to_kn_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
+                       dy, g, (int32_t)NPQ, dyt);
+    RowMajorStore<bf16_t> ep{dcol, NPQ, CRSp, NPQ, nullptr, 0};
+    const int st = fast::run<true, true>(ctx, wp, CRSp, dyt, NPQ, ep, CRSp, NPQ, d->k, 0,
+                                         reinterpret_cast<float*>(ws + o_part));
+    if (st != NOTT_OK) return st;
+    hipLaunchKernelGGL(col2im_kernel<bf16_t>, dim3((unsigned)ceil_div(d->n * d->c * d->h * d->w, 256)), dim3(256), 0,
+                       ctx->stream, dcol, g, (int32_t)NPQ, dx);
+    return nott::launch_status(ctx, "conv col2im");
+}
+
 int64_t out_size(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d) { return (in + 2 * p - d * (k - 1) - 1) / s + 1; }
 
 int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) {
@@ -302,6 +510,10 @@ int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const voi
     const int64_t M = d->n * p * q, K = d->c * d->r * d->s;
     if (nott::conv_fast::fwd_applies(d, sizeof(T)))
         return nott::conv_fast::fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
+    if constexpr (sizeof(T) == 2) {
+        if (col_applies(d, p, q, false))
+            return col_fwd(ctx, d, p, q, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
+    }
     FwdALoader<T> la{static_cast<const T*>(x), g, M, K};
     const bool v = ((uintptr_t)w % 16) == 0 && ((K * (int64_t)sizeof(T)) % 16) == 0;
     RowKLoader<T> lb{static_cast<const T*>(w), K, d->k, K, v};
@@ -313,6 +525,10 @@ template <typename T>
 int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* dy, const void* w, void* dx) {
     if (nott::conv_fast::dgrad_applies(d, sizeof(T)))
         return nott::conv_fast::dgrad<T>(ctx, d, static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx));
+    if constexpr (sizeof(T) == 2) {
+        if (col_applies(d, p, q, true))
+            return col_dgrad(ctx, d, p, q, static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx));
+    }
     const Geom g = make_geom(d, p, q);
     const int64_t M = d->n * d->h * d->w, K = d->k * d->r * d->s;
     DgradALoader<T> la{static_cast<const T*>(dy), g, M, K};
@@ -330,6 +546,9 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         const bool aligned = ((uintptr_t)x % 16) == 0 && ((uintptr_t)dy % 16) == 0;
         if (aligned && nott::conv_fast::wgrad_applies(d, sizeof(T))) {
             st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
+        } else if (sizeof(T) == 2 && col_applies(d, p, q, false)) {
+            st = col_wgrad(ctx, d, p, q, reinterpret_cast<const bf16_t*>(x), reinterpret_cast<const bf16_t*>(dy), dw,
+                           accumulate);
         } else {
             const int64_t M = d->k, N = d->c * d->r * d->s, K = d->n * p * q;
             WgradALoader<T> la{static_cast<const T*>(dy), g, M, K};

@@ -464,11 +464,32 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(const bf16_t* __
                 ep.store(m0 + wm * 64 + i * 16 + rq + e, n0 + wn * 64 + j * 16 + col, acc[i][j][e]);
 }
 
+// Split-K plan: `splits` k-ranges of `kps` (a multiple of BK) each.
+inline void plan(nott_ctx ctx, int64_t M, int64_t N, int64_t K, int64_t& splits, int64_t& kps) {
+    const int64_t tn = ceil_div(N, BN), tm = ceil_div(M, BM);
+    const int64_t nkb = K / BK;
+    if (splits <= 0) {
+        splits = std::max<int64_t>(1, (2 * (int64_t)ctx->num_cu + tn * tm - 1) / (tn * tm));
+        splits = std::min<int64_t>(splits, std::max<int64_t>(1, nkb / 4));   // at least 4 stages per split
+    }
+    splits = std::max<int64_t>(1, std::min<int64_t>(splits, std::min<int64_t>(nkb, 65535)));
+    kps = ceil_div(nkb, splits) * BK;
+    splits = ceil_div(K, kps);
+}
+
+// fp32 scratch the split-K partials of an M×N product need (0 if unsplit).
+inline size_t partial_floats(nott_ctx ctx, int64_t M, int64_t N, int64_t K) {
+    int64_t splits = 0, kps = 0;
+    plan(ctx, M, N, K, splits, kps);
+    return splits > 1 ? (size_t)(splits * M * N) : 0;
+}
+
 // C = A·B through the fast path, or NOTT_ERR_UNSUPPORTED when the operands do
-// not qualify (then the caller uses the generic engine).
+// not qualify (then the caller uses the generic engine).  Split-K partials go
+// to `partial` when given (partial_floats() of them), else to the workspace.
 template <bool AT, bool BT, class EP>
 int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep, int64_t M, int64_t N,
-        int64_t K, int64_t splits = 0) {
+        int64_t K, int64_t splits = 0, float* partial = nullptr) {
     if (M <= 0 || N <= 0) return NOTT_OK;
     auto ok16 = [](const void* p, int64_t ld) { return ((uintptr_t)p % 16) == 0 && (ld % 8) == 0; };
     if (K <= 0 || K % BK != 0 || !ok16(A, lda) || !ok16(B, ldb)) return NOTT_ERR_UNSUPPORTED;
@@ -476,21 +497,15 @@ int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
     if ((AT && M % 8 != 0) || (BT && N % 8 != 0)) return NOTT_ERR_UNSUPPORTED;
     const int64_t tn = ceil_div(N, BN), tm = ceil_div(M, BM);
     if (tn > 0x7fffffff || tm > 65535) return NOTT_ERR_UNSUPPORTED;
-    const int64_t nkb = K / BK;
-    if (splits <= 0) {
-        splits = std::max<int64_t>(1, (2 * (int64_t)ctx->num_cu + tn * tm - 1) / (tn * tm));
-        splits = std::min<int64_t>(splits, std::max<int64_t>(1, nkb / 4));   // at least 4 stages per split
-    }
-    splits = std::max<int64_t>(1, std::min<int64_t>(splits, std::min<int64_t>(nkb, 65535)));
-    const int64_t kps = ceil_div(nkb, splits) * BK;
-    splits = ceil_div(K, kps);
+    int64_t kps = 0;
+    plan(ctx, M, N, K, splits, kps);
     const size_t lds = 2 * kStageBytes;
     if (splits == 1) {
         hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EP>), dim3((unsigned)tn, (unsigned)tm, 1), dim3(kThreads), lds,
                            ctx->stream, A, lda, B, ldb, ep, M, N, K, K);
         return launch_status(ctx, "gemm_bf16");
     }
-    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(splits * M * N)));
+    float* ws = partial ? partial : static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(splits * M * N)));
     if (!ws) return NOTT_ERR_ALLOC;
     PartialStore ps{ws, M, N};
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
