@@ -109,9 +109,12 @@ __global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t total,
                                                              int64_t c, int64_t hw, const float* __restrict__ coef) {
-    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * (VEC ? 4 : 1);
-    if (i >= total) return;
-    const int64_t ch = (i / hw) % c;
+    // grid: x over the n·c planes, y over each plane's hw: no per-element division
+    const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
+    if (j >= hw) return;
+    const int64_t plane = blockIdx.x;
+    const int64_t i = plane * hw + j;
+    const int64_t ch = plane % c;
     const float a = coef[2 * ch], b = coef[2 * ch + 1];
     if (VEC) {
         f32x4 v = Vec4<T>::ld(x + i);
@@ -186,9 +189,11 @@ template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                 T* __restrict__ dx, int64_t total, int64_t c,
                                                                 int64_t hw, const float* __restrict__ coef) {
-    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * (VEC ? 4 : 1);
-    if (i >= total) return;
-    const int64_t ch = (i / hw) % c;
+    const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
+    if (j >= hw) return;
+    const int64_t plane = blockIdx.x;
+    const int64_t i = plane * hw + j;
+    const int64_t ch = plane % c;
     const float A = coef[3 * ch], B = coef[3 * ch + 1], C = coef[3 * ch + 2];
     if (VEC) {
         f32x4 g = Vec4<T>::ld(dy + i), v = Vec4<T>::ld(x + i);
@@ -228,10 +233,10 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
                        c, splits, hw, n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
     const int64_t total = n * c * hw;
     if (vec)
-        hipLaunchKernelGGL((bn_affine_kernel<T, true>), dim3((unsigned)nott::ceil_div(total / 4, kThreads)),
+        hipLaunchKernelGGL((bn_affine_kernel<T, true>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)),
                            dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
     else
-        hipLaunchKernelGGL((bn_affine_kernel<T, false>), dim3((unsigned)nott::ceil_div(total, kThreads)),
+        hipLaunchKernelGGL((bn_affine_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
                            dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
     return nott::launch_status(ctx, "batchnorm_fwd");
 }
@@ -263,10 +268,11 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     if (dx) {
         const int64_t total = n * c * hw;
         if (vec)
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>), dim3((unsigned)nott::ceil_div(total / 4, kThreads)),
-                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef);
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>),
+                               dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)), dim3(kThreads), 0,
+                               ctx->stream, x, dy, dx, total, c, hw, coef);
         else
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), dim3((unsigned)nott::ceil_div(total, kThreads)),
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
                                dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef);
     }
     return nott::launch_status(ctx, "batchnorm_bwd");
@@ -282,7 +288,7 @@ extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, i
     NOTT_REQUIRE(ctx, (running_mean == nullptr) == (running_var == nullptr),
                  "nott_batchnorm2d_fwd: running_mean and running_var go together");
     NOTT_REQUIRE(ctx, x && y && mean && rstd, "nott_batchnorm2d_fwd: null buffer");
-    NOTT_REQUIRE(ctx, c <= 65535, "nott_batchnorm2d_fwd: too many channels");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_fwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
     return dtype == NOTT_F32 ? fwd<float>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
                                           running_var, y, mean, rstd)
@@ -296,7 +302,7 @@ extern "C" int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, i
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_bwd: bad shape");
     NOTT_REQUIRE(ctx, x && dy && mean && rstd, "nott_batchnorm2d_bwd: null buffer");
-    NOTT_REQUIRE(ctx, c <= 65535, "nott_batchnorm2d_bwd: too many channels");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_bwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
     return dtype == NOTT_F32 ? bwd<float>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate)
                              : bwd<bf16_t>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate);

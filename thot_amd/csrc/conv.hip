@@ -301,39 +301,46 @@ __global__ __launch_bounds__(256) void pack_w_kernel(const T* __restrict__ w, in
     wp[i] = j < CRS ? w[(int64_t)k * CRS + j] : T(0);
 }
 
-// One thread: 8 consecutive npq of one crs row (one 16-byte store).
+// One thread: one npq column position for kColRows consecutive crs rows, so
+// that each load and each store of a wave covers 64 consecutive pixels.
+constexpr int kColRows = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void im2col_kernel(const T* __restrict__ x, Geom g, int32_t CRS, int32_t CRSp,
                                                      int32_t NPQ, T* __restrict__ col) {
-    constexpr int E = 16 / (int)sizeof(T);
-    const int32_t per_row = NPQ / E;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (int64_t)CRSp * per_row) return;
-    const int32_t crs = (int32_t)(t / per_row), m0 = (int32_t)(t % per_row) * E;
-    T v[E];
-    if (crs < CRS) {
-        uint32_t c, rs, r, s;
-        g.fd_rs.divmod((uint32_t)crs, c, rs);
-        g.fd_s.divmod(rs, r, s);
+    const int32_t m = (int32_t)((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (m >= NPQ) return;
+    const int32_t crs0 = (int32_t)blockIdx.y * kColRows;
+    uint32_t n, pq, pp, qq;
+    g.fd_pq.divmod((uint32_t)m, n, pq);
+    g.fd_q.divmod(pq, pp, qq);
+    const int32_t hb = (int32_t)pp * g.sh - g.ph, wb = (int32_t)qq * g.sw - g.pw;
+    uint32_t c, rs, r, s;
+    g.fd_rs.divmod((uint32_t)(crs0 < CRS ? crs0 : 0), c, rs);
+    g.fd_s.divmod(rs, r, s);
+    int32_t ci = (int32_t)c, ri = (int32_t)r, si = (int32_t)s;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            uint32_t n, pq, pp, qq;
-            g.fd_pq.divmod((uint32_t)(m0 + e), n, pq);
-            g.fd_q.divmod(pq, pp, qq);
-            const int32_t h = (int32_t)pp * g.sh - g.ph + (int32_t)r * g.dh;
-            const int32_t w = (int32_t)qq * g.sw - g.pw + (int32_t)s * g.dw;
-            v[e] = (h >= 0 && h < g.h && w >= 0 && w < g.w) ? x[(((int64_t)n * g.c + c) * g.h + h) * g.w + w] : T(0);
+    for (int e = 0; e < kColRows; ++e) {
+        const int32_t crs = crs0 + e;
+        T v = T(0);
+        if (crs < CRS) {
+            const int32_t h = hb + ri * g.dh, w = wb + si * g.dw;
+            if (h >= 0 && h < g.h && w >= 0 && w < g.w) v = x[(((int64_t)n * g.c + ci) * g.h + h) * g.w + w];
         }
-    } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = T(0);
+        col[(int64_t)crs * NPQ + m] = v;
+        if (++si == g.s) {
+            si = 0;
+            if (++ri == g.r) {
+                ri = 0;
+                ++ci;
+            }
+        }
     }
-    *reinterpret_cast<u32x4*>(col + (int64_t)crs * NPQ + m0) = Pack<T>::make(v);
 }
 
 // dyt[k][n·PQ + pq] = dy[n][k][pq]; one thread per 8 consecutive npq.
 template <typename T>
-__global__ __launch_bounds__(256) void to_kn_kernel(const T* __restrict__ dy, Geom g, int32_t NPQ, T* __restrict__ dyt) {
+__global__ __launch_bounds__(256) void to_kn_kernel(const T* __restrict__ dy, Geom g, int32_t NPQ, int vec,
+                                                    T* __restrict__ dyt) {
     constexpr int E = 16 / (int)sizeof(T);
     const int32_t per_row = NPQ / E;
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -341,11 +348,21 @@ __global__ __launch_bounds__(256) void to_kn_kernel(const T* __restrict__ dy, Ge
     const int32_t k = (int32_t)(t / per_row), m0 = (int32_t)(t % per_row) * E;
     const int32_t PQ = g.p * g.q;
     T v[E];
+    uint32_t n, pq;
+    g.fd_pq.divmod((uint32_t)m0, n, pq);
+    if (vec) {   // PQ % E == 0, 16-byte aligned dy: the E positions are one aligned run of one plane
+        *reinterpret_cast<u32x4*>(dyt + (int64_t)k * NPQ + m0) =
+            *reinterpret_cast<const u32x4*>(dy + ((int64_t)n * g.k + k) * PQ + pq);
+        return;
+    }
+    int32_t ni = (int32_t)n, pqi = (int32_t)pq;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        uint32_t n, pq;
-        g.fd_pq.divmod((uint32_t)(m0 + e), n, pq);
-        v[e] = dy[((int64_t)n * g.k + k) * PQ + pq];
+        v[e] = dy[((int64_t)ni * g.k + k) * PQ + pqi];
+        if (++pqi == PQ) {
+            pqi = 0;
+            ++ni;
+        }
     }
     *reinterpret_cast<u32x4*>(dyt + (int64_t)k * NPQ + m0) = Pack<T>::make(v);
 }
@@ -404,7 +421,7 @@ struct ColPlan {
 bool col_applies(const nott_conv2d_desc* d, int64_t p, int64_t q, bool need_k64) {
     const int64_t npq = d->n * p * q;
     return d->layout == NOTT_NCHW && npq % 64 == 0 && (!need_k64 || d->k % 64 == 0) &&
-           d->c * d->r * d->s <= (int64_t(1) << 20);
+           d->c * d->r * d->s <= 65535 * 8 - 64;   // col rows per launch: grid.y = CRSp / 8
 }
 
 // Carves aligned pieces out of one workspace request.
@@ -430,8 +447,8 @@ int col_fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const
     bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
     hipLaunchKernelGGL(pack_w_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * CRSp, 256)), dim3(256), 0, ctx->stream, w,
                        (int32_t)d->k, (int32_t)CRS, (int32_t)CRSp, wp);
-    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(CRSp * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
-                       x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(NPQ, 256), (unsigned)(CRSp / kColRows)), dim3(256),
+                       0, ctx->stream, x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
     ColFwdStore<bf16_t> ep{y, b, g, NPQ};
     return fast::run<false, true>(ctx, wp, CRSp, col, NPQ, ep, d->k, NPQ, CRSp, 0,
                                   reinterpret_cast<float*>(ws + o_part));
@@ -449,9 +466,9 @@ int col_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, con
     bf16_t* dyt = reinterpret_cast<bf16_t*>(ws + o_dyt);
     bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
     hipLaunchKernelGGL(to_kn_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
-                       dy, g, (int32_t)NPQ, dyt);
-    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(CRSp * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
-                       x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+                       dy, g, (int32_t)NPQ, (int)((p * q) % 8 == 0 && ((uintptr_t)dy % 16) == 0), dyt);
+    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(NPQ, 256), (unsigned)(CRSp / kColRows)), dim3(256),
+                       0, ctx->stream, x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
     WgradStore ep{dw, d->k, CRS, accumulate};
     return fast::run<false, false>(ctx, dyt, NPQ, col, NPQ, ep, d->k, CRSp, NPQ, 0,
                                    reinterpret_cast<float*>(ws + o_part));
@@ -472,7 +489,7 @@ int col_dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, con
     hipLaunchKernelGGL(pack_w_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * CRSp, 256)), dim3(256), 0, ctx->stream, w,
                        (int32_t)d->k, (int32_t)CRS, (int32_t)CRSp, wp);
     hipLaunchKernelGGL(to_kn_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
-                       dy, g, (int32_t)NPQ, dyt);
+                       dy, g, (int32_t)NPQ, (int)((p * q) % 8 == 0 && ((uintptr_t)dy % 16) == 0), dyt);
     RowMajorStore<bf16_t> ep{dcol, NPQ, CRSp, NPQ, nullptr, 0};
     const int st = fast::run<true, true>(ctx, wp, CRSp, dyt, NPQ, ep, CRSp, NPQ, d->k, 0,
                                          reinterpret_cast<float*>(ws + o_part));

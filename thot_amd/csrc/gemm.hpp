@@ -256,16 +256,33 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(LA la, LB lb, EP ep, int
                 ep.store(m0 + wm * 64 + i * 16 + rq + e, n0 + wn * 64 + j * 16 + col, acc[i][j][e]);
 }
 
-// Sums split-K partials ws[s][m][n] in split order and hands each total to
-// the epilogue (deterministic).
+// Sums split-K partials ws[s][m][n] and hands each total to the epilogue.  A
+// block owns 64 consecutive outputs (lane = output, coalesced); its 4 waves
+// take the splits round-robin with 8 loads in flight each and combine in LDS
+// in wave order, so the summation order is fixed (deterministic).
 template <class EP>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t splits, int64_t M,
                                                             int64_t N, EP ep) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= M * N) return;
+    __shared__ float red[4][64];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t MN = M * N;
     float s = 0.f;
-    for (int64_t z = 0; z < splits; ++z) s += ws[z * M * N + i];
-    ep.store(i / N, i % N, s);
+    if (i < MN) {
+        for (int64_t z = wid; z < splits; z += 32) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t zz = z + 4 * u;
+                t[u] = ws[(zz < splits ? zz : splits - 1) * MN + i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += (z + 4 * u < splits) ? t[u] : 0.f;
+        }
+    }
+    red[wid][lane] = s;
+    __syncthreads();
+    if (wid == 0 && i < MN) ep.store(i / N, i % N, (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]));
 }
 
 // Picks a split count that gives the grid at least ~2 workgroups per CU
@@ -305,7 +322,7 @@ int run(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64
     PartialStore ps{ws, M, N};
     hipLaunchKernelGGL((gemm_kernel<T, LA, LB, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
                        dim3(kThreads), 0, ctx->stream, la, lb, ps, M, N, K, kps);
-    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
                        ws, splits, M, N, ep);
     return launch_status(ctx, "gemm_splitk");
 }
@@ -510,7 +527,7 @@ int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
     PartialStore ps{ws, M, N};
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
                        dim3(kThreads), lds, ctx->stream, A, lda, B, ldb, ps, M, N, K, kps);
-    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
                        ws, splits, M, N, ep);
     return launch_status(ctx, "gemm_bf16_splitk");
 }
