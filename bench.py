@@ -41,11 +41,22 @@ MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
 METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HBM)"
 
 
-# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes
-# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each divided by the factor
-# the same counter reads for a plain device copy of known size.  Keyed by
-# (workload, dtype, kernel); None where no pass has been recorded.
-TRAFFIC = {}
+# HBM bytes per launch of the dominant kernel (all kernels of the bracketed
+# entry point), from two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE,
+# KiB per dispatch), each divided by what the same counter reads for a plain
+# 256 MiB device copy (FETCH_SIZE reads 0.5 x the bytes, WRITE_SIZE 1.0 x).
+# The passes and their commands are in profiles/.  Keyed by (workload, dtype,
+# kernel); None where no pass has been recorded.
+TRAFFIC = {
+    ("conv_bwd", "bf16", "dgrad"): 213.39e6,   # conv3x3_wprep + conv3x3_same
+    ("conv_bwd", "bf16", "wgrad"): 230.33e6,   # conv3x3_wgrad + conv3x3_wgrad_reduce
+    ("ln_bwd", "f32", None): 210.91e6,         # ln_bwd_kernel + col_reduce_kernel
+    ("ln_bwd", "bf16", None): 109.74e6,
+    ("adamw", "f32", None): 2799.94e6,
+    ("adamw", "bf16", None): 2200.00e6,
+    ("xent", "f32", None): 4206.80e6,          # xent_count_kernel + xent_row_kernel
+    ("xent", "bf16", None): 2101.70e6,
+}
 
 
 def traffic_for(workload, dtype, kernel):
@@ -468,7 +479,7 @@ def main():
         ach = wl.flop_one / (per[dom] * 1e-3) / 1e12
         peak = MFMA_PEAK_TFLOPS[dtype]
         roof = {"bound": "mfma", "kernel": f"conv2d_{dom}", "achieved": round(ach, 2), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic_for("conv_bwd", dtype, dom),
+                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic_for("conv_bwd", dtype, dom), "traffic_unit": "B",
                 "per_kernel_ms": {k: round(v, 4) for k, v in per.items()},
                 "per_kernel_tflops": {k: round(wl.flop_one / (v * 1e-3) / 1e12, 2) for k, v in per.items()}}
         metric_part = "conv-bwd TFLOP/s"
@@ -498,7 +509,7 @@ def main():
         value = wl.work_per_step() / (ms * 1e-3) / 1e9
         ach = wl.work_per_step() / (kms * 1e-3) / 1e9
         roof = {"bound": "hbm", "kernel": wl.name, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_for(wl.name, dtype, None),
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_for(wl.name, dtype, None), "traffic_unit": "B",
                 "launch_ms": round(kms, 4)}
         metric_part = {"ln_bwd": "LN-bwd GB/s", "xent": "CE-grad GB/s", "adamw": "AdamW GB/s"}[wl.name]
         cfg = {"workload": wl.name}
