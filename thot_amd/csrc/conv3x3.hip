@@ -60,7 +60,11 @@ struct SameParams {
     FastDiv fd_hw, fd_w, fd_w2, fd_h2;
 };
 
-// wt_prep[cb][cc][tap][co64][CC] from w (fwd) or from the flipped transpose (dgrad).
+// Weight slices from w (fwd) or from its flipped transpose (dgrad): slice
+// (cb, cc) holds rows (tap, co) = tap·64 + co of CC channels, stored in the
+// LDS order of lds_off(row, sub) (16-row groups, sub-chunk-major inside a
+// group), so the kernels copy a slice to LDS linearly: contiguous 16-byte
+// pieces per lane, bank-conflict-free writes.
 template <typename T, bool DGRAD>
 __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict__ w, T* __restrict__ wp, int32_t cout,
                                                             int32_t cin) {
@@ -84,7 +88,9 @@ __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict_
     // (in dgrad terms w is [k = cin][c = cout][3][3]).
     const int64_t src = DGRAD ? (((int64_t)ci * cout + co) * 9 + (2 - r) * 3 + (2 - s))
                               : (((int64_t)co * cin + ci) * 9 + r * 3 + s);
-    wp[i] = w[src];
+    constexpr int SUB = Chunk<T>::SUB;
+    const int64_t slice = ((int64_t)cb * ncc + cc) * 9 * kTileCo * CC;
+    wp[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = w[src];
 }
 
 template <typename T>
@@ -133,9 +139,13 @@ __device__ __forceinline__ void transpose_block(const u32x4 (&in)[4], u32x4 (&ou
     for (int j = 0; j < 4; ++j) out[j] = u32x4{in[0][j], in[1][j], in[2][j], in[3][j]};
 }
 
+// Fill tasks per thread whose global loads are issued one channel chunk ahead
+// and held in registers across the MFMA loop; a tile with more tasks (one
+// that spans more padded rows, e.g. across an image boundary) loads the rest
+// when it stores them.
 template <typename T> struct VecTasks;
-template <> struct VecTasks<bf16_t> { static constexpr int VT = 2; };
-template <> struct VecTasks<float> { static constexpr int VT = 3; };
+template <> struct VecTasks<bf16_t> { static constexpr int VT = 1; };
+template <> struct VecTasks<float> { static constexpr int VT = 2; };
 
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
@@ -223,9 +233,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         wc = (u2 - cig * wgroups) * WG + (t % WG);
     };
     u32x4 rin[VT][SUB];
-    // VEC fill task j of chunk cc: SUB global loads into rin[j] ...
-    auto fetch_task = [&](int j, int32_t cc) {
-        const int32_t t = threadIdx.x + j * kThreads;
+    // VEC fill task t of chunk cc: SUB global loads into r ...
+    auto fetch_task = [&](int32_t t, int32_t cc, u32x4 (&r)[SUB]) {
         int32_t wc, vr, cig;
         task_of(t, wc, vr, cig);
         uint32_t img, hh;
@@ -235,12 +244,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
             const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w + wc * SUB;
 #pragma unroll
             for (int i = 0; i < SUB; ++i)
-                rin[j][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw));
+                r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw));
         }
     };
     // ... and the transpose + SUB LDS row writes into buffer `dst`.
-    auto stash_task = [&](int j, char* dst) {
-        const int32_t t = threadIdx.x + j * kThreads;
+    auto stash_task = [&](int32_t t, const u32x4 (&r)[SUB], char* dst) {
         int32_t wc, vr, cig;
         task_of(t, wc, vr, cig);
         uint32_t img, hh;
@@ -248,7 +256,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         const int32_t h = (int32_t)hh - 1;
         if (t < ntask && wc < wchunks && h >= 0 && h < p.h) {
             u32x4 tr[SUB];
-            transpose_block(rin[j], tr);
+            transpose_block(r, tr);
             const int32_t row0 = vr * p.w2 + 1 + wc * SUB;
 #pragma unroll
             for (int i = 0; i < SUB; ++i) *reinterpret_cast<u32x4*>(dst + lds_off(row0 + i, cig)) = tr[i];
@@ -260,7 +268,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     auto stash = [&](int32_t cc) {
         if constexpr (VEC) {
 #pragma unroll
-            for (int j = 0; j < VT; ++j) stash_task(j, lds_in);
+            for (int j = 0; j < VT; ++j) stash_task(threadIdx.x + j * kThreads, rin[j], lds_in);
+            for (int32_t t = threadIdx.x + VT * kThreads; t < ntask; t += kThreads) {
+                u32x4 r[SUB];
+                fetch_task(t, cc, r);
+                stash_task(t, r, lds_in);
+            }
         } else {
             for (int32_t t = threadIdx.x; t < nrows * 4; t += kThreads) {
                 const int32_t sub = t / nrows;        // consecutive lanes -> consecutive pixels
@@ -282,17 +295,12 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
                 *reinterpret_cast<u32x4*>(lds_in + lds_off(row, sub)) = pack_sub<T>(v);
             }
         }
-        // Weights come from L2 (every workgroup reads the same slice): loaded
-        // here rather than held in registers across the MFMA loop.
         const u32x4* wsrc = reinterpret_cast<const u32x4*>(wblk + (int64_t)cc * 9 * kTileCo * CC);
         u32x4 rw[WT];
 #pragma unroll
         for (int j = 0; j < WT; ++j) rw[j] = wsrc[threadIdx.x + j * kThreads];
 #pragma unroll
-        for (int j = 0; j < WT; ++j) {
-            const int t = threadIdx.x + j * kThreads;
-            *reinterpret_cast<u32x4*>(lds_w + lds_off(t >> 2, t & 3)) = rw[j];
-        }
+        for (int j = 0; j < WT; ++j) *reinterpret_cast<u32x4*>(lds_w + (threadIdx.x + j * kThreads) * 16) = rw[j];
     };
 
     if constexpr (VEC) {
@@ -300,7 +308,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         for (int32_t t = threadIdx.x; t < ((nrows + 15) >> 4) * 64; t += kThreads)
             *reinterpret_cast<u32x4*>(lds_in + t * 16) = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int j = 0; j < VT; ++j) fetch_task(j, 0);
+        for (int j = 0; j < VT; ++j) fetch_task(threadIdx.x + j * kThreads, 0, rin[j]);
     }
     for (int32_t cc = 0; cc < nchunks; ++cc) {
         __syncthreads();     // previous chunk fully read (and, at cc = 0, the halo zeroing done)
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         if constexpr (VEC) {
             if (cc + 1 < nchunks) {
 #pragma unroll
-                for (int j = 0; j < VT; ++j) fetch_task(j, cc + 1);
+                for (int j = 0; j < VT; ++j) fetch_task(threadIdx.x + j * kThreads, cc + 1, rin[j]);
             }
         }
         // 9 taps × 16 MFMAs with the next tap's 8 operand fragments loaded
@@ -430,13 +438,10 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     const int64_t tiles = ceil_div((int64_t)p.npix, kTilePix);
     p.remap = (tiles % 8 == 0) ? 1 : 0;
     p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
-    // Vector fill when image rows are whole 16-byte chunks, the input is
-    // 16-byte aligned and the tile's fill tasks fit the per-thread registers.
+    // Vector fill when image rows are whole 16-byte chunks and the input is
+    // 16-byte aligned.
     const int32_t sub = Chunk<T>::SUB;
-    const int32_t max_vr = in_rows_bound(h, w) / row_pitch(w);
-    const int32_t wg = 16 / sub, wgroups = (w / sub + wg - 1) / wg;
-    const bool vec = (w % sub) == 0 && ((uintptr_t)in % 16) == 0 &&
-                     (int64_t)max_vr * wgroups * wg * 4 <= (int64_t)VecTasks<T>::VT * kThreads;
+    const bool vec = (w % sub) == 0 && ((uintptr_t)in % 16) == 0;
     const size_t lds = same_lds_bytes(h, w, sizeof(T));
     static bool attr_set[2][2] = {{false, false}, {false, false}};
     if (!attr_set[sizeof(T) == 2][vec]) {

@@ -29,7 +29,7 @@ __host__ __device__ constexpr int rows_in_flight(int elem_bytes, int dpl) {
 }
 constexpr int kReduceThreads = 1024;   // column reduction: 16 waves split the partial rows
 constexpr int kReduceWaves = kReduceThreads / 64;
-constexpr int kReduceUnroll = 8;
+constexpr int kReduceUnroll = 32;  // 16 waves x 32 loads cover 512 partial rows in one round
 
 // Element e of a lane's DPL row values is column col(g, e) with g = e / G:
 // group g of lane `lane` covers the 16 bytes at columns [(g*64 + lane)*G, +G),
