@@ -473,20 +473,29 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
 // Per band, LDS holds dy[64 k][TH·P slots] and x[64 c][(TH+2)·P slots] (one
 // halo row above and below) as 16-byte chunks of slots, stored chunk-major
 // in groups of 16 channels: chunk j of channel ch sits in the 256-byte block
-// (ch / 16, j) at slot (ch ^ j) % 16.  The 16 lanes that read one chunk of 16
-// channels, and the 16 lanes that fill 16 consecutive chunks of one channel,
-// both touch 16 distinct slots (conflict-free ds_read/ds_write_b128).  x has
+// (ch / 16, j) at slot (ch ^ 4·(j % 4)) % 16.  The 16 lanes that read one
+// chunk of 16 channels, and the 16 lanes that fill 4 consecutive chunks of 4
+// channels, both touch 16 distinct slots (conflict-free ds_read/ds_write_b128),
+// and a lane's read slots depend on j % 4 only, which its k-slice fixes, so
+// every read address is a per-lane base plus a compile-time offset.  x has
 // one zero guard block before and after each channel group, read by the
 // s = 0 / s = 2 shifts at the band edges.  A lane's
 // MFMA k-slice is 8 (bf16) / 4 (fp32) consecutive slots: s = 1 is an aligned
-// 16-byte LDS read, s = 0 and s = 2 realign the neighbouring aligned chunks by
-// one element in registers.  Wave w owns channels 16w..16w+15 for all 9 taps
-// and all 64 k: 36 accumulator tiles, 13 LDS reads per 36 MFMAs.
+// 16-byte LDS read, s = 0 and s = 2 realign it with one dword of each
+// neighbouring chunk in registers.  Wave w owns channels 16w..16w+15 for all
+// 9 taps and 32 of the 64 k: 18 accumulator tiles per 2 + 3 chunk reads
+// (+ 6 dword reads); the next k-step's operands are read while the current
+// one's 18 MFMAs run.
 //
 // The pixel range is split across workgroups (whole bands each); partial
 // sums go to ws[split][tap][k][c] and conv3x3_wgrad_reduce_kernel adds them
 // in split order (deterministic).
 // ---------------------------------------------------------------------------
+// 8 waves: wave w owns x channels 16·(w % 4)..+15 and dy channels
+// 32·(w / 4)..+31, i.e. 2 × 9 accumulator tiles, so a wave fits in 256
+// registers and two waves share each SIMD (one wave per SIMD cannot keep the
+// matrix core busy).
+constexpr int kWgThreads = 512;
 template <typename T> struct WgCfg;
 template <> struct WgCfg<bf16_t> { static constexpr int TH = 4, E = 8, KSTEP = 32; };
 template <> struct WgCfg<float> { static constexpr int TH = 2, E = 4, KSTEP = 16; };
@@ -499,7 +508,7 @@ struct WgradParams {
 
 // Chunk j (16 bytes) of channel ch in a region of nch chunks per channel.
 __device__ __forceinline__ int wg_off(int ch, int j, int nch) {
-    return (ch >> 4) * (nch << 8) + (j << 8) + (((ch ^ j) & 15) << 4);
+    return (ch >> 4) * (nch << 8) + (j << 8) + (((ch ^ ((j & 3) << 2)) & 15) << 4);
 }
 
 // Shift a 16-byte chunk by one element toward lower slots (s = 2: slots base+1..)
@@ -524,13 +533,12 @@ template <>
 __device__ __forceinline__ u32x4 shift_hi<float>(const u32x4& p, const u32x4& c) { return u32x4{p.w, c.x, c.y, c.z}; }
 
 template <typename T, int P>
-__global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+__global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                    float* __restrict__ ws, WgradParams p) {
     constexpr int TH = WgCfg<T>::TH, E = WgCfg<T>::E, KSTEP = WgCfg<T>::KSTEP;
     constexpr int CPR = P / E;                          // 16-byte chunks per slot row
     constexpr int A_TOTAL = 64 * TH * CPR, B_TOTAL = 64 * (TH + 2) * CPR;   // 16-byte chunks per band
-    constexpr int A_TASKS = (A_TOTAL + kThreads - 1) / kThreads;             // per thread
-    constexpr int B_TASKS = (B_TOTAL + kThreads - 1) / kThreads;
+    constexpr int A_TASKS = (A_TOTAL + kWgThreads - 1) / kWgThreads;             // per thread
     constexpr int RB = P * (int)sizeof(T);              // bytes per slot row
     constexpr int KSTEPS = TH * P / KSTEP;
     constexpr int NA = TH * CPR;                        // dy chunks per channel
@@ -544,105 +552,144 @@ __global__ __launch_bounds__(kThreads, 1) void conv3x3_wgrad_kernel(const T* __r
     const int32_t b1 = min(p.total_bands, b0 + p.bands_per_split);
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
+    const int cg = wid & 3, kh = wid >> 2;               // x channel group, dy channel half
     const int64_t plane = (int64_t)p.h * p.w;
 
     // Zero the guard chunks of x (never written by the fill).
-    for (int i = threadIdx.x; i < 64 * 2; i += kThreads) {
+    for (int i = threadIdx.x; i < 64 * 2; i += kWgThreads) {
         const int ch = i >> 1, j = (i & 1) ? NB - 1 : 0;
         *reinterpret_cast<u32x4*>(lds_b + wg_off(ch, j, NB)) = u32x4{0u, 0u, 0u, 0u};
     }
 
-    f32x4 acc[4][9];
+    f32x4 acc[2][9];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 ra[A_TASKS], rb[B_TASKS];
+    // Fill task t: chunk j = 4·jh + t%4 of channel ch = 4·chh + (t/4)%4, with
+    // (jh, chh) = t/16 split over the chunk quads of a channel: 16 lanes fill
+    // 4 consecutive chunks of 4 channels (64-byte global runs).
+    constexpr int NBF = (TH + 2) * CPR;                  // filled x chunks per channel
+    constexpr int QA = NA / 4, QB = (NBF + 3) / 4;       // chunk quads per channel
+    constexpr int A_TOTAL4 = 64 * QA * 16 / 4, B_TOTAL4 = 64 * QB * 16 / 4;
+    static_assert(NA % 4 == 0, "dy chunks per channel must be a multiple of 4");
+    static_assert(A_TOTAL4 == A_TOTAL, "task count");
+    auto task = [](int t, int nq, int& ch, int& j) {
+        const int rest = t >> 4;
+        j = (rest % nq) * 4 + (t & 3);
+        ch = (rest / nq) * 4 + ((t >> 2) & 3);
+    };
+    u32x4 ra[A_TASKS], rb[(B_TOTAL4 + kWgThreads - 1) / kWgThreads];
     auto fetch = [&](int32_t band) {
         const int32_t img = band / p.bands_per_img;
         const int32_t h0 = (band - img * p.bands_per_img) * TH;
         const T* dyb = dy + ((int64_t)img * p.k + kb * 64) * plane;
         const T* xb = x + ((int64_t)img * p.c + cb * 64) * plane;
 #pragma unroll
-        for (int j = 0; j < A_TASKS; ++j) {
-            const int t = threadIdx.x + j * kThreads;
-            const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
-            const int h = h0 + row;
+        for (int i = 0; i < A_TASKS; ++i) {
+            const int t = threadIdx.x + i * kWgThreads;
+            int kk, j;
+            task(t, QA, kk, j);
+            const int ch = j % CPR, h = h0 + j / CPR;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((A_TOTAL % kThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h)
+            if ((A_TOTAL % kWgThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h)
                 v = *reinterpret_cast<const u32x4*>(dyb + kk * plane + (int64_t)h * p.w + ch * E);
-            ra[j] = v;
+            ra[i] = v;
         }
 #pragma unroll
-        for (int j = 0; j < B_TASKS; ++j) {
-            const int t = threadIdx.x + j * kThreads;
-            const int ch = t % CPR, row = (t / CPR) % (TH + 2), cc = t / (CPR * (TH + 2));
-            const int h = h0 - 1 + row;
+        for (int i = 0; i < (B_TOTAL4 + kWgThreads - 1) / kWgThreads; ++i) {
+            const int t = threadIdx.x + i * kWgThreads;
+            int cc, j;
+            task(t, QB, cc, j);
+            const int ch = j % CPR, h = h0 - 1 + j / CPR;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((B_TOTAL % kThreads == 0 || t < B_TOTAL) && ch * E < p.w && h >= 0 && h < p.h)
+            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && h >= 0 && h < p.h)
                 v = *reinterpret_cast<const u32x4*>(xb + cc * plane + (int64_t)h * p.w + ch * E);
-            rb[j] = v;
+            rb[i] = v;
         }
     };
     auto stash = [&]() {
 #pragma unroll
-        for (int j = 0; j < A_TASKS; ++j) {
-            const int t = threadIdx.x + j * kThreads;
-            const int ch = t % CPR, row = (t / CPR) % TH, kk = t / (CPR * TH);
-            if (A_TOTAL % kThreads == 0 || t < A_TOTAL)
-                *reinterpret_cast<u32x4*>(lds_a + wg_off(kk, row * CPR + ch, NA)) = ra[j];
+        for (int i = 0; i < A_TASKS; ++i) {
+            const int t = threadIdx.x + i * kWgThreads;
+            int kk, j;
+            task(t, QA, kk, j);
+            if (A_TOTAL % kWgThreads == 0 || t < A_TOTAL)
+                *reinterpret_cast<u32x4*>(lds_a + wg_off(kk, j, NA)) = ra[i];
         }
 #pragma unroll
-        for (int j = 0; j < B_TASKS; ++j) {
-            const int t = threadIdx.x + j * kThreads;
-            const int ch = t % CPR, row = (t / CPR) % (TH + 2), cc = t / (CPR * (TH + 2));
-            if (B_TOTAL % kThreads == 0 || t < B_TOTAL)
-                *reinterpret_cast<u32x4*>(lds_b + wg_off(cc, 1 + row * CPR + ch, NB)) = rb[j];
+        for (int i = 0; i < (B_TOTAL4 + kWgThreads - 1) / kWgThreads; ++i) {
+            const int t = threadIdx.x + i * kWgThreads;
+            int cc, j;
+            task(t, QB, cc, j);
+            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF)
+                *reinterpret_cast<u32x4*>(lds_b + wg_off(cc, 1 + j, NB)) = rb[i];
         }
     };
 
+    // Per-lane LDS bases.  dy: chunk ja = 4·t + kq of channel (2·kh + mt)·16 + r16
+    // is at a_base + mt·NA·256 + t·1024.  x: chunk j = 1 + 4·t + kq + r·CPR + d of
+    // channel cl is at b_base[c] + (1 + 4·t + r·CPR + d)·256 with
+    // c = (1 + r·CPR + d) % 4 (the slot depends on j % 4 = (kq + c) % 4).
+    const int cl = cg * 16 + r16;                               // this lane's x channel
+    const int a_base = kh * 2 * NA * 256 + kq * 256 + ((r16 ^ (kq << 2)) & 15) * 16;
+    int b_base[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        b_base[c] = (cl >> 4) * (NB << 8) + kq * 256 + (((cl ^ (((kq + c) & 3) << 2)) & 15) << 4);
+    struct Ops {
+        u32x4 a[2], cur[3];
+        uint32_t prev_w[3], next_x[3];
+    };
+    auto load_ops = [&](int t, Ops& o) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+            o.a[mt] = *reinterpret_cast<const u32x4*>(lds_a + a_base + mt * NA * 256 + t * 1024);
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+            const int jc = 1 + 4 * t + r * CPR;                 // chunk of s = 1, less kq
+            o.cur[r] = *reinterpret_cast<const u32x4*>(lds_b + b_base[(jc) & 3] + jc * 256);
+            o.prev_w[r] = *reinterpret_cast<const uint32_t*>(lds_b + b_base[(jc + 3) & 3] + (jc - 1) * 256 + 12);
+            o.next_x[r] = *reinterpret_cast<const uint32_t*>(lds_b + b_base[(jc + 1) & 3] + (jc + 1) * 256);
+        }
+    };
     if (b0 < b1) fetch(b0);
-    const int cl = wid * 16 + r16;                              // this lane's x channel
     for (int32_t band = b0; band < b1; ++band) {
         __syncthreads();
         stash();
         __syncthreads();
         if (band + 1 < b1) fetch(band + 1);
-#pragma unroll 2
-        for (int t = 0; t < KSTEPS; ++t) {
-            const int ja = t * (KSTEP / E) + kq;                // dy chunk of this lane's k-slice
-            u32x4 a[4];
+        Ops ops[2];
+        load_ops(0, ops[0]);
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                a[mt] = *reinterpret_cast<const u32x4*>(lds_a + wg_off(mt * 16 + r16, ja, NA));
+        for (int t = 0; t < KSTEPS; ++t) {
+            Ops& o = ops[t & 1];
+            if (t + 1 < KSTEPS) load_ops(t + 1, ops[(t + 1) & 1]);
 #pragma unroll
             for (int r = 0; r < 3; ++r) {
-                const int jb = 1 + ja + r * CPR;                // x chunk for s = 1 (guard-shifted)
-                const u32x4 prev = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb - 1, NB));
-                const u32x4 cur = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb, NB));
-                const u32x4 next = *reinterpret_cast<const u32x4*>(lds_b + wg_off(cl, jb + 1, NB));
-                const u32x4 b_s0 = shift_hi<T>(prev, cur);
-                const u32x4 b_s2 = shift_lo<T>(cur, next);
+                const u32x4 pv = u32x4{0u, 0u, 0u, o.prev_w[r]}, nx = u32x4{o.next_x[r], 0u, 0u, 0u};
+                const u32x4 b_s0 = shift_hi<T>(pv, o.cur[r]);
+                const u32x4 b_s2 = shift_lo<T>(o.cur[r], nx);
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    mfma_chunk<T>(a[mt], b_s0, acc[mt][r * 3 + 0]);
-                    mfma_chunk<T>(a[mt], cur, acc[mt][r * 3 + 1]);
-                    mfma_chunk<T>(a[mt], b_s2, acc[mt][r * 3 + 2]);
+                for (int mt = 0; mt < 2; ++mt) {
+                    mfma_chunk<T>(o.a[mt], b_s0, acc[mt][r * 3 + 0]);
+                    mfma_chunk<T>(o.a[mt], o.cur[r], acc[mt][r * 3 + 1]);
+                    mfma_chunk<T>(o.a[mt], b_s2, acc[mt][r * 3 + 2]);
                 }
             }
         }
     }
     // Partials: ws[split][tap][k][c]; lane column = channel, rows = k.
-    const int32_t c = cb * 64 + wid * 16 + r16;
+    const int32_t c = cb * 64 + cg * 16 + r16;
     float* wsp = ws + (int64_t)blockIdx.x * 9 * p.k * p.c;
 #pragma unroll
     for (int tap = 0; tap < 9; ++tap)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int32_t k = kb * 64 + mt * 16 + kq * 4 + e;
+                const int32_t k = kb * 64 + (kh * 2 + mt) * 16 + kq * 4 + e;
                 wsp[((int64_t)tap * p.k + k) * p.c + c] = acc[mt][tap][e];
             }
 }
@@ -713,7 +760,7 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P>), dim3((unsigned)splits, (unsigned)tiles), dim3(kThreads), lds,
+    hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P>), dim3((unsigned)splits, (unsigned)tiles), dim3(kWgThreads), lds,
                        ctx->stream, x, dy, ws, p);
     const int64_t per = (int64_t)9 * p.k * p.c;
     hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256), 0, ctx->stream, ws,
