@@ -256,23 +256,35 @@ struct WgradStore {
     }
 };
 
-// db[k] = Σ_{n,p,q} dy[n,k,p,q]; one workgroup per output channel,
-// deterministic order.
+// db[k] = Σ_{n,p,q} dy[n,k,p,q] in two deterministic passes: workgroup
+// (k, z) sums images [z·npb, (z+1)·npb) of channel k into part[z][k], then
+// conv_db_finish_kernel adds the kDbSlabs partials of a channel in slab order.
+constexpr int kDbSlabs = 32;
 template <typename T>
-__global__ __launch_bounds__(256) void conv_db_kernel(const T* __restrict__ dy, Geom g, float* __restrict__ db,
-                                                      int accumulate) {
+__global__ __launch_bounds__(256) void conv_db_partial_kernel(const T* __restrict__ dy, Geom g, int32_t npb,
+                                                              float* __restrict__ part) {
     __shared__ float red[4];
-    const int32_t ko = blockIdx.x;
+    const int32_t ko = blockIdx.x, z = blockIdx.y;
     const int64_t pq = (int64_t)g.p * g.q;
+    const int32_t n0 = z * npb, n1 = min(g.n, n0 + npb);
     float s = 0.f;
-    for (int32_t n = 0; n < g.n; ++n) {
+    for (int32_t n = n0; n < n1; ++n) {
         for (int64_t i = threadIdx.x; i < pq; i += 256) {
             const int64_t idx = g.nhwc ? ((int64_t)n * pq + i) * g.k + ko : ((int64_t)n * g.k + ko) * pq + i;
             s += Io<T>::ld(dy, idx);
         }
     }
     s = block_sum<4>(s, red);
-    if (threadIdx.x == 0) db[ko] = accumulate ? db[ko] + s : s;
+    if (threadIdx.x == 0) part[(int64_t)z * g.k + ko] = s;
+}
+
+__global__ __launch_bounds__(256) void conv_db_finish_kernel(const float* __restrict__ part, int32_t k,
+                                                             float* __restrict__ db, int accumulate) {
+    const int32_t ko = blockIdx.x * 256 + threadIdx.x;
+    if (ko >= k) return;
+    float s = 0.f;
+    for (int z = 0; z < kDbSlabs; ++z) s += part[(int64_t)z * k + ko];
+    db[ko] = accumulate ? db[ko] + s : s;
 }
 
 // ---------------------------------------------------------------------------
@@ -576,8 +588,13 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         if (st != NOTT_OK) return st;
     }
     if (db) {
-        hipLaunchKernelGGL(conv_db_kernel<T>, dim3((unsigned)d->k), dim3(256), 0, ctx->stream,
-                           static_cast<const T*>(dy), g, db, accumulate);
+        float* part = static_cast<float*>(nott::workspace(ctx, sizeof(float) * kDbSlabs * (size_t)d->k));
+        if (!part) return NOTT_ERR_ALLOC;
+        const int32_t npb = (int32_t)nott::ceil_div((int64_t)d->n, (int64_t)kDbSlabs);
+        hipLaunchKernelGGL(conv_db_partial_kernel<T>, dim3((unsigned)d->k, kDbSlabs), dim3(256), 0, ctx->stream,
+                           static_cast<const T*>(dy), g, npb, part);
+        hipLaunchKernelGGL(conv_db_finish_kernel, dim3((unsigned)nott::ceil_div((int64_t)d->k, (int64_t)256)), dim3(256),
+                           0, ctx->stream, part, (int32_t)d->k, db, accumulate);
         return nott::launch_status(ctx, "conv_db");
     }
     return NOTT_OK;

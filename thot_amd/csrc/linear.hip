@@ -109,7 +109,7 @@ int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const
     RowKLoader<T> la{xp, kin, m, kin, vec16<T>(x, kin)};
     RowKLoader<T> lb{wp, kin, nout, kin, vec16<T>(w, kin)};
     RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
-    return run<T>(ctx, la, lb, ep, m, nout, kin, 1);
+    return run<T>(ctx, la, lb, ep, m, nout, kin);
 }
 
 template <typename T>
@@ -155,7 +155,7 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
         RowKLoader<T> la{dyp, nout, m, nout, vec16<T>(dy, nout)};
         ColKLoader<T> lb{static_cast<const T*>(w), kin, kin, nout};
         RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
-        const int st = run<T>(ctx, la, lb, ep, m, kin, nout, 1);
+        const int st = run<T>(ctx, la, lb, ep, m, kin, nout);
         if (st != NOTT_OK) return st;
     }
     if (dw || db) {
