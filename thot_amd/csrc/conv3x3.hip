@@ -57,6 +57,8 @@ struct SameParams {
     int32_t in_rows;           // LDS rows reserved for the input tile
     int32_t remap;             // XCD-aware block remap active
     int32_t vec_store;         // 16-byte output runs stay inside one image plane
+    int32_t cc_per_split;      // channel chunks per blockIdx.z split
+    float* partial;            // split partials [split][cout][npix] (fp32, no bias), or null
     FastDiv fd_hw, fd_w, fd_w2, fd_h2;
 };
 
@@ -212,8 +214,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int32_t nchunks = p.cin / CC;
-    const T* wblk = wp + (int64_t)cb * nchunks * 9 * kTileCo * CC;
+    // Channel chunks [cc0, cc1) of this split (all of them without split-K).
+    const int32_t cc0 = blockIdx.z * p.cc_per_split;
+    const int32_t cc1 = min(p.cin / CC, cc0 + p.cc_per_split);
+    const T* wblk = wp + (int64_t)cb * (p.cin / CC) * 9 * kTileCo * CC;
 
     // Vector fill: task = (w-chunk of SUB pixels, padded row, channel group of
     // SUB): SUB 16-byte loads (one per channel), a register transpose, SUB
@@ -308,14 +312,14 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         for (int32_t t = threadIdx.x; t < ((nrows + 15) >> 4) * 64; t += kThreads)
             *reinterpret_cast<u32x4*>(lds_in + t * 16) = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int j = 0; j < VT; ++j) fetch_task(threadIdx.x + j * kThreads, 0, rin[j]);
+        for (int j = 0; j < VT; ++j) fetch_task(threadIdx.x + j * kThreads, cc0, rin[j]);
     }
-    for (int32_t cc = 0; cc < nchunks; ++cc) {
+    for (int32_t cc = cc0; cc < cc1; ++cc) {
         __syncthreads();     // previous chunk fully read (and, at cc = 0, the halo zeroing done)
         stash(cc);
         __syncthreads();
         if constexpr (VEC) {
-            if (cc + 1 < nchunks) {
+            if (cc + 1 < cc1) {
 #pragma unroll
                 for (int j = 0; j < VT; ++j) fetch_task(threadIdx.x + j * kThreads, cc + 1, rin[j]);
             }
@@ -345,6 +349,28 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
                 for (int nt = 0; nt < 4; ++nt) mfma_chunk<T>(a[cur][mt], b[cur][nt], acc[mt][nt]);
         }
+    }
+
+    if (p.partial) {
+        // Split-K: fp32 partial sums straight from the accumulators; lane holds
+        // pixels 4·(lane/16) + e (consecutive, 16-byte aligned) of column co.
+        float* dst = p.partial + (int64_t)blockIdx.z * p.cout * p.npix;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const int32_t co = cb * kTileCo + nt * 16 + r16;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int32_t m = m0 + wid * 64 + mt * 16 + kq * 4;
+                if (m + 3 <= m_last) {
+                    *reinterpret_cast<f32x4*>(dst + (int64_t)co * p.npix + m) = acc[mt][nt];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (m + e <= m_last) dst[(int64_t)co * p.npix + m + e] = acc[mt][nt][e];
+                }
+            }
+        }
+        return;
     }
 
     // ---- epilogue: the 256-pixel × 64-channel tile goes through LDS as
@@ -390,6 +416,30 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     }
 }
 
+// out[n][co][hw] = bias[co] + Σ_split partial[split][co][m] (m = n·hw + hw),
+// splits added in order.  Thread = 4 consecutive pixels of one channel.
+template <typename T>
+__global__ __launch_bounds__(256) void conv3x3_split_reduce_kernel(const float* __restrict__ partial, int32_t splits,
+                                                                   int32_t cout, int32_t npix, FastDiv fd_hw,
+                                                                   int32_t hw, const float* __restrict__ bias,
+                                                                   T* __restrict__ out) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;     // group of 4 pixels
+    const int32_t groups = npix >> 2;
+    if (q >= (int64_t)groups * cout) return;
+    const int32_t co = (int32_t)(q / groups), m = (int32_t)(q - (int64_t)co * groups) * 4;
+    const int64_t stride = (int64_t)cout * npix;
+    const float* src = partial + (int64_t)co * npix + m;
+    f32x4 s = *reinterpret_cast<const f32x4*>(src);
+    for (int32_t z = 1; z < splits; ++z) s += *reinterpret_cast<const f32x4*>(src + z * stride);
+    const float bv = bias ? bias[co] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        uint32_t n, pix;
+        fd_hw.divmod((uint32_t)(m + e), n, pix);
+        Io<T>::st(out, ((int64_t)n * cout + co) * hw + pix, s[e] + bv);
+    }
+}
+
 bool same_shape(const nott_conv2d_desc* d) {
     return d->layout == NOTT_NCHW && d->groups == 1 && d->r == 3 && d->s == 3 && d->stride_h == 1 &&
            d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1 && d->dil_h == 1 && d->dil_w == 1 && d->w <= 64;
@@ -423,8 +473,22 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
     if (same_lds_bytes(h, w, sizeof(T)) > kSameLdsMax)
         return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
-    T* wp = static_cast<T*>(workspace(ctx, wbytes));
-    if (!wp) return NOTT_ERR_ALLOC;
+    // Split the channel chunks over blockIdx.z when the grid would not give
+    // every CU two workgroups (small images, many channels).
+    const int64_t tiles = ceil_div((int64_t)n * h * w, kTilePix);
+    const int64_t blocks = tiles * (cout / kTileCo);
+    const int32_t nchunks = cin / CC;
+    int32_t splits = 1;
+    const int64_t npix64 = (int64_t)n * h * w;
+    if (blocks < 2 * (int64_t)ctx->num_cu && nchunks > 1 && npix64 % 4 == 0)
+        splits = (int32_t)std::min<int64_t>(std::min<int64_t>(nchunks, 8), ceil_div(2 * (int64_t)ctx->num_cu, blocks));
+    const int32_t cc_per_split = (int32_t)ceil_div(nchunks, splits);
+    splits = (int32_t)ceil_div(nchunks, cc_per_split);
+    const size_t wbytes_al = (wbytes + 255) & ~(size_t)255;
+    const size_t pbytes = splits > 1 ? sizeof(float) * (size_t)splits * cout * (size_t)npix64 : 0;
+    char* ws = static_cast<char*>(workspace(ctx, wbytes_al + pbytes));
+    if (!ws) return NOTT_ERR_ALLOC;
+    T* wp = reinterpret_cast<T*>(ws);
     const int64_t welems = (int64_t)cout * cin * 9;
     hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(welems, 256)), dim3(256), 0,
                        ctx->stream, wsrc, wp, cout, cin);
@@ -435,7 +499,8 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     p.fd_w = FastDiv((uint32_t)w);
     p.fd_w2 = FastDiv((uint32_t)row_pitch(w));
     p.fd_h2 = FastDiv((uint32_t)(h + 2));
-    const int64_t tiles = ceil_div((int64_t)p.npix, kTilePix);
+    p.cc_per_split = cc_per_split;
+    p.partial = splits > 1 ? reinterpret_cast<float*>(ws + wbytes_al) : nullptr;
     p.remap = (tiles % 8 == 0) ? 1 : 0;
     p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
     // Vector fill when image rows are whole 16-byte chunks and the input is
@@ -450,11 +515,14 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
         (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
         attr_set[sizeof(T) == 2][vec] = true;
     }
-    const dim3 grid((unsigned)tiles, (unsigned)(cout / kTileCo));
+    const dim3 grid((unsigned)tiles, (unsigned)(cout / kTileCo), (unsigned)splits);
     if (vec)
         hipLaunchKernelGGL((conv3x3_same_kernel<T, true>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
     else
         hipLaunchKernelGGL((conv3x3_same_kernel<T, false>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    if (splits > 1)
+        hipLaunchKernelGGL(conv3x3_split_reduce_kernel<T>, dim3((unsigned)ceil_div(npix64 / 4 * cout, 256)), dim3(256), 0,
+                           ctx->stream, p.partial, splits, cout, p.npix, p.fd_hw, p.hw, bias, out);
     return launch_status(ctx, "conv3x3_same");
 }
 
