@@ -117,6 +117,9 @@ POOLS = [
     (4, 64, 112, 112, (3, 3), (2, 2), (1, 1), (1, 1), False),  # ResNet-18 stem pool (batch slice)
     (2, 3, 9, 8, (3, 3), (2, 2), (0, 0), (1, 1), True),
     (2, 3, 9, 9, (2, 2), (1, 1), (0, 0), (2, 2), False),
+    (2, 3, 17, 23, (3, 3), (2, 2), (1, 1), (1, 1), True),     # row bands cut mid-window, ceil mode
+    (1, 2, 40, 33, (5, 4), (3, 2), (2, 1), (1, 2), False),    # dilation with padding
+    (3, 5, 70, 19, (3, 3), (1, 1), (1, 1), (1, 1), False),    # stride 1: several bands per plane
 ]
 
 

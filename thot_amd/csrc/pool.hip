@@ -141,6 +141,105 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* 
     Io<T>::st(dx, i, acc);
 }
 
+// Row-tiled versions for the common case of whole planes of moderate width.
+// Forward: workgroup (band of kPoolRows output rows, plane) stages the input
+// rows its windows touch in LDS (one coalesced read of each row, converted to
+// float), then every output scans its window from LDS in the same order and
+// with the same NaN / first-maximum rule as the untiled kernel.
+constexpr int kPoolRows = 8;
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                                     int64_t* __restrict__ argmax, PoolGeom32 g) {
+    extern __shared__ float rows[];
+    const int32_t pl = blockIdx.y;
+    const int32_t oh0 = blockIdx.x * kPoolRows, oh1 = min(oh0 + kPoolRows, g.oh);
+    const int32_t ih_lo = max(0, oh0 * g.sh - g.ph);
+    const int32_t ih_hi = min(g.h, (oh1 - 1) * g.sh - g.ph + (g.kh - 1) * g.dh + 1);   // exclusive
+    const T* xp = x + (int64_t)pl * g.h * g.w;
+    const int32_t nin = (ih_hi - ih_lo) * g.w;
+    for (int32_t i = threadIdx.x; i < nin; i += kThreads) rows[i] = Io<T>::ld(xp, (int64_t)ih_lo * g.w + i);
+    __syncthreads();
+    const int32_t nout = (oh1 - oh0) * g.ow;
+    for (int32_t j = threadIdx.x; j < nout; j += kThreads) {
+        const int32_t oh = oh0 + j / g.ow, ow = j % g.ow;
+        int32_t ih0 = oh * g.sh - g.ph, iw0 = ow * g.sw - g.pw;
+        const int32_t ih1 = min(ih0 + (g.kh - 1) * g.dh + 1, g.h);
+        const int32_t iw1 = min(iw0 + (g.kw - 1) * g.dw + 1, g.w);
+        while (ih0 < 0) ih0 += g.dh;
+        while (iw0 < 0) iw0 += g.dw;
+        int32_t best = ih0 * g.w + iw0;
+        float bv = -INFINITY;
+        for (int32_t ih = ih0; ih < ih1; ih += g.dh)
+            for (int32_t iw = iw0; iw < iw1; iw += g.dw) {
+                const float v = rows[(ih - ih_lo) * g.w + iw];
+                if (v > bv || v != v) {
+                    bv = v;
+                    best = ih * g.w + iw;
+                }
+            }
+        const int64_t o = ((int64_t)pl * g.oh + oh) * g.ow + ow;
+        Io<T>::st(y, o, bv);
+        argmax[o] = best;
+    }
+}
+
+// Backward: workgroup (band of kPoolRows·sh input rows, plane) stages the
+// argmax (as 32-bit in-plane indices) and dy of every output row whose window
+// reaches the band in LDS, then each input gathers from the outputs that can
+// cover it, in the untiled kernel's order (oh, then ow, ascending): the same
+// sums, bit for bit, with each argmax read from HBM about once.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64_t* __restrict__ argmax,
+                                                                     const T* __restrict__ dy, T* __restrict__ dx,
+                                                                     PoolGeom32 g, int32_t band_rows) {
+    extern __shared__ char sm[];
+    const int32_t pl = blockIdx.y;
+    const int32_t ih_lo = blockIdx.x * band_rows, ih_hi = min(ih_lo + band_rows, g.h);
+    const int32_t num = ih_lo + g.ph - (g.kh - 1) * g.dh;
+    const int32_t oh_lo = num <= 0 ? 0 : (num + g.sh - 1) / g.sh;
+    const int32_t oh_hi = min((ih_hi - 1 + g.ph) / g.sh, g.oh - 1);
+    const int32_t nout = oh_hi >= oh_lo ? (oh_hi - oh_lo + 1) * g.ow : 0;
+    int32_t* code = reinterpret_cast<int32_t*>(sm);
+    float* gv = reinterpret_cast<float*>(sm) + nout;
+    const int64_t obase = (int64_t)pl * g.oh * g.ow + (int64_t)oh_lo * g.ow;
+    for (int32_t i = threadIdx.x; i < nout; i += kThreads) {
+        code[i] = (int32_t)argmax[obase + i];
+        gv[i] = Io<T>::ld(dy, obase + i);
+    }
+    __syncthreads();
+    const int32_t nin = (ih_hi - ih_lo) * g.w;
+    for (int32_t j = threadIdx.x; j < nin; j += kThreads) {
+        const int32_t ih = ih_lo + j / g.w, iw = j % g.w;
+        const int32_t idx = ih * g.w + iw;
+        const int32_t num_h = ih + g.ph - (g.kh - 1) * g.dh;
+        const int32_t oh0 = num_h <= 0 ? 0 : (num_h + g.sh - 1) / g.sh;
+        const int32_t oh1 = min((ih + g.ph) / g.sh, g.oh - 1);
+        const int32_t num_w = iw + g.pw - (g.kw - 1) * g.dw;
+        const int32_t ow0 = num_w <= 0 ? 0 : (num_w + g.sw - 1) / g.sw;
+        const int32_t ow1 = min((iw + g.pw) / g.sw, g.ow - 1);
+        float acc = 0.f;
+        for (int32_t oh = oh0; oh <= oh1; ++oh)
+            for (int32_t ow = ow0; ow <= ow1; ++ow) {
+                const int32_t o = (oh - oh_lo) * g.ow + ow;
+                if (code[o] == idx) acc += gv[o];
+            }
+        Io<T>::st(dx, (int64_t)pl * g.h * g.w + idx, acc);
+    }
+}
+
+// LDS bytes of the tiled kernels (0 when a band does not fit).
+constexpr size_t kPoolLdsMax = 48 * 1024;
+size_t pool_fwd_lds(const PoolGeom& g) {
+    const int64_t rows = (int64_t)(kPoolRows - 1) * g.sh + (g.kh - 1) * g.dh + 1;
+    const size_t b = sizeof(float) * (size_t)(std::min<int64_t>(rows, g.h) * g.w);
+    return b <= kPoolLdsMax ? b : 0;
+}
+size_t pool_bwd_lds(const PoolGeom& g, int32_t band_rows) {
+    const int64_t orows = (band_rows - 1 + (g.kh - 1) * g.dh) / g.sh + 2;
+    const size_t b = 8 * (size_t)(std::min<int64_t>(orows, g.oh) * g.ow);
+    return b <= kPoolLdsMax ? b : 0;
+}
+
 PoolGeom32 geom32(const PoolGeom& g) {
     PoolGeom32 r;
     r.h = (int32_t)g.h; r.w = (int32_t)g.w; r.oh = (int32_t)g.oh; r.ow = (int32_t)g.ow;
@@ -200,7 +299,17 @@ extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     NOTT_REQUIRE(ctx, x && y && argmax, "nott_maxpool2d_fwd: null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
-    if (fits32(planes, g)) {
+    const size_t flds = pool_fwd_lds(g);
+    if (fits32(planes, g) && flds > 0 && planes <= 65535) {
+        const PoolGeom32 g32 = geom32(g);
+        const dim3 tgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kPoolRows), (unsigned)planes);
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL(maxpool_fwd_tiled_kernel<float>, tgrid, dim3(kThreads), flds, ctx->stream,
+                               static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
+        else
+            hipLaunchKernelGGL(maxpool_fwd_tiled_kernel<bf16_t>, tgrid, dim3(kThreads), flds, ctx->stream,
+                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, g32);
+    } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
         if (dtype == NOTT_F32)
             hipLaunchKernelGGL(maxpool_fwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream,
@@ -229,7 +338,18 @@ extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     NOTT_REQUIRE(ctx, argmax && dy && dx, "nott_maxpool2d_bwd: null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
-    if (fits32(planes, g)) {
+    const int32_t band_rows = (int32_t)(kPoolRows * g.sh);
+    const size_t blds = pool_bwd_lds(g, band_rows);
+    if (fits32(planes, g) && blds > 0 && planes <= 65535) {
+        const PoolGeom32 g32 = geom32(g);
+        const dim3 tgrid((unsigned)nott::ceil_div(g.h, (int64_t)band_rows), (unsigned)planes);
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<float>, tgrid, dim3(kThreads), blds, ctx->stream, argmax,
+                               static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+        else
+            hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<bf16_t>, tgrid, dim3(kThreads), blds, ctx->stream, argmax,
+                               static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
+    } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
         if (dtype == NOTT_F32)
             hipLaunchKernelGGL(maxpool_bwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
