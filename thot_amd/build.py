@@ -20,6 +20,7 @@ INCLUDE = os.path.join(REPO_DIR, "include")
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM_LIB = "/opt/rocm/lib"
 
 # Packed-fp32 VALU ops are disabled for every HIP translation unit.
 HIP_FLAGS = [
@@ -56,7 +57,8 @@ def build_library(jobs: int | None = None, verbose: bool = True) -> str:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs, "-Wl,-soname,libnott_hip.so"]
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-o", tmp, *objs, "-Wl,-soname,libnott_hip.so",
+           f"-L{ROCM_LIB}", "-lhipblaslt", f"-Wl,-rpath,{ROCM_LIB}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

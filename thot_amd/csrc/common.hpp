@@ -19,6 +19,7 @@ struct nott_ctx_s {
     size_t ws_bytes = 0;
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;
+    void* blas = nullptr;          // hipBLASLt handle, workspace and plans (created on first use)
     std::string last_error;
 };
 

@@ -1,5 +1,6 @@
 // Context, errors and workspace of libnott_hip.
 #include "common.hpp"
+#include "blaslt.hpp"
 
 #include <new>
 
@@ -94,6 +95,7 @@ int nott_destroy(nott_ctx ctx) {
     {
         nott::DeviceScope scope(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
+        nott::blas::release(ctx);
         if (ctx->ws) (void)hipFree(ctx->ws);
         if (ctx->err_word) (void)hipFree(ctx->err_word);
     }

@@ -12,6 +12,7 @@
 // bf16 operands whose k extent is a multiple of 64 take the fast GEMM path
 // (gemm.hpp, namespace fast); everything else the generic engine.
 #include "gemm.hpp"
+#include "blaslt.hpp"
 
 namespace {
 
@@ -19,6 +20,7 @@ using namespace nott::gemm;
 using nott::ceil_div;
 using nott::launch_status;
 using nott::workspace;
+namespace blas = nott::blas;
 
 template <typename T>
 bool vec16(const void* p, int64_t ld) {
@@ -97,7 +99,16 @@ __global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restr
 }
 
 template <typename T>
+constexpr hipDataType lib_type() { return sizeof(T) == 2 ? HIP_R_16BF : HIP_R_32F; }
+
+template <typename T>
 int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
+    // Library GEMM, column-major: Yᵀ (nout×m) = Wᵀᵀ·Xᵀ, bias per row of Yᵀ.
+    {
+        const int st = blas::gemm(ctx, true, false, nout, m, kin, w, kin, x, kin, lib_type<T>(), y, nout, lib_type<T>(),
+                                  0.f, b);
+        if (st != NOTT_ERR_UNSUPPORTED) return st;
+    }
     if constexpr (sizeof(T) == 2) {
         RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
         const int st = fast::run<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
@@ -116,6 +127,35 @@ template <typename T>
 int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, const void* x, const void* w, void* dx,
         float* dw, float* db, int accumulate) {
     const T* dyp = static_cast<const T*>(dy);
+    // Library GEMMs, column-major: dXᵀ (kin×m) = Wᵀ(kin×nout)·dYᵀ(nout×m);
+    // dWᵀ (kin×nout, fp32) = Xᵀ(kin×m)·dY(m×nout) (+ dWᵀ when accumulating).
+    if (dx) {
+        const int st = blas::gemm(ctx, false, false, kin, m, nout, w, kin, dy, nout, lib_type<T>(), dx, kin,
+                                  lib_type<T>(), 0.f, nullptr);
+        if (st == NOTT_OK) dx = nullptr;
+        else if (st != NOTT_ERR_UNSUPPORTED) return st;
+    }
+    if (dw) {
+        const int st = blas::gemm(ctx, false, true, kin, nout, m, x, kin, dy, nout, lib_type<T>(), dw, kin, HIP_R_32F,
+                                  accumulate ? 1.f : 0.f, nullptr);
+        if (st == NOTT_OK) {
+            dw = nullptr;
+            if (db) {
+                float* part = static_cast<float*>(workspace(ctx, sizeof(float) * kColSumSlabs * (size_t)nout));
+                if (!part) return NOTT_ERR_ALLOC;
+                hipLaunchKernelGGL(colsum_partial_kernel<T>, dim3((unsigned)ceil_div(nout, 64), kColSumSlabs),
+                                   dim3(256), 0, ctx->stream, dyp, m, nout, part);
+                hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)ceil_div(nout, 256)), dim3(256), 0,
+                                   ctx->stream, part, nout, db, accumulate);
+                db = nullptr;
+                const int st2 = launch_status(ctx, "linear db");
+                if (st2 != NOTT_OK) return st2;
+            }
+        } else if (st != NOTT_ERR_UNSUPPORTED) {
+            return st;
+        }
+    }
+    if (!dx && !dw && !db) return NOTT_OK;
     if constexpr (sizeof(T) == 2) {
         // dx = dy·w: A = dy (k = o contiguous), B(i, o) = w[o·kin + i] (transposed)
         // dw = dyᵀ·x: A(o, r) = dy[r·nout + o], B(i, r) = x[r·kin + i] (both transposed)
