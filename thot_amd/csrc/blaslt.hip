@@ -19,7 +19,8 @@ namespace {
 
 constexpr size_t kWsBytes = 32u << 20;
 
-using Key = std::tuple<int, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int>;
+using Key = std::tuple<int, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int, int64_t, int64_t,
+                       int64_t, int64_t>;
 
 struct Plan {
     hipblasLtMatmulDesc_t op = nullptr;
@@ -54,7 +55,7 @@ void destroy_plan(Plan& p) {
 }
 
 Plan make_plan(State* s, bool ta, bool tb, int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldd,
-               hipDataType ab, hipDataType dt, bool bias) {
+               hipDataType ab, hipDataType dt, bool bias, int64_t batch, int64_t sa, int64_t sb, int64_t sd) {
     Plan p;
     if (hipblasLtMatmulDescCreate(&p.op, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
     const int32_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
@@ -71,6 +72,16 @@ Plan make_plan(State* s, bool ta, bool tb, int64_t m, int64_t n, int64_t k, int6
         hipblasLtMatrixLayoutCreate(&p.b, ab, tb ? n : k, tb ? k : n, ldb) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&p.d, dt, m, n, ldd) != HIPBLAS_STATUS_SUCCESS)
         return p;
+    if (batch > 1) {
+        const int32_t bc = (int32_t)batch;
+        const int64_t strides[3] = {sa, sb, sd};
+        hipblasLtMatrixLayout_t ls[3] = {p.a, p.b, p.d};
+        for (int i = 0; i < 3; ++i) {
+            hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc));
+            hipblasLtMatrixLayoutSetAttribute(ls[i], HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &strides[i],
+                                              sizeof(strides[i]));
+        }
+    }
     hipblasLtMatmulPreference_t pref = nullptr;
     if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
     const uint64_t wsb = kWsBytes;
@@ -89,14 +100,16 @@ Plan make_plan(State* s, bool ta, bool tb, int64_t m, int64_t n, int64_t k, int6
 }  // namespace
 
 int gemm(nott_ctx ctx, bool ta, bool tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda, const void* B,
-         int64_t ldb, hipDataType ab, void* D, int64_t ldd, hipDataType dt, float beta, const float* bias) {
-    if (m <= 0 || n <= 0 || k <= 0) return NOTT_ERR_UNSUPPORTED;
+         int64_t ldb, hipDataType ab, void* D, int64_t ldd, hipDataType dt, float beta, const float* bias, int64_t batch,
+         int64_t sa, int64_t sb, int64_t sd) {
+    if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || batch > 0x7fffffff) return NOTT_ERR_UNSUPPORTED;
     State* s = state(ctx);
     if (s->broken) return NOTT_ERR_UNSUPPORTED;
-    const Key key{ta, tb, m, n, k, lda, ldb, ldd, (int)ab, (int)dt, bias != nullptr};
+    const Key key{ta, tb, m, n, k, lda, ldb, ldd, (int)ab, (int)dt, bias != nullptr, batch, sa, sb, sd};
     auto it = s->plans.find(key);
     if (it == s->plans.end())
-        it = s->plans.emplace(key, make_plan(s, ta, tb, m, n, k, lda, ldb, ldd, ab, dt, bias != nullptr)).first;
+        it = s->plans.emplace(key, make_plan(s, ta, tb, m, n, k, lda, ldb, ldd, ab, dt, bias != nullptr, batch, sa, sb,
+                                             sd)).first;
     Plan& p = it->second;
     if (!p.ok) return NOTT_ERR_UNSUPPORTED;
     if (bias) hipblasLtMatmulDescSetAttribute(p.op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
