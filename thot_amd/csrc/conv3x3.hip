@@ -600,7 +600,38 @@ __device__ __forceinline__ u32x4 shift_lo<float>(const u32x4& c, const u32x4& n)
 template <>
 __device__ __forceinline__ u32x4 shift_hi<float>(const u32x4& p, const u32x4& c) { return u32x4{p.w, c.x, c.y, c.z}; }
 
-template <typename T, int P>
+// Chunk ch (E elements, 16 bytes) of an image row of w elements, read with
+// LW-byte loads (LW = 16 when rows are whole 16-byte chunks; 8, 4 or 2 when
+// w is only a multiple of 4, 2 or 1 bf16 / of 2 or 1 fp32): pieces past the
+// row end read as zero.
+template <typename T, int LW>
+__device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, int w) {
+    constexpr int E = 16 / (int)sizeof(T), PE = LW / (int)sizeof(T);   // elements per chunk / per piece
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (LW == 16) {
+        if (ch * E < w) v = *reinterpret_cast<const u32x4*>(row + ch * E);
+    } else if constexpr (LW == 8) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            if (ch * E + q * PE < w) {
+                const uint2 t = *reinterpret_cast<const uint2*>(row + ch * E + q * PE);
+                v[2 * q] = t.x;
+                v[2 * q + 1] = t.y;
+            }
+    } else if constexpr (LW == 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (ch * E + q * PE < w) v[q] = *reinterpret_cast<const uint32_t*>(row + ch * E + q * PE);
+    } else {
+        static_assert(LW == 2 && sizeof(T) == 2, "2-byte pieces are bf16 elements");
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (ch * E + q < w) v[q >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[ch * E + q] << (16 * (q & 1));
+    }
+    return v;
+}
+
+template <typename T, int P, int LW>
 __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                    float* __restrict__ ws, WgradParams p) {
     constexpr int TH = WgCfg<T>::TH, E = WgCfg<T>::E, KSTEP = WgCfg<T>::KSTEP;
@@ -662,7 +693,7 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
             const int ch = j % CPR, h = h0 + j / CPR;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
             if ((A_TOTAL % kWgThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h)
-                v = *reinterpret_cast<const u32x4*>(dyb + kk * plane + (int64_t)h * p.w + ch * E);
+                v = load_chunk<T, LW>(dyb + kk * plane + (int64_t)h * p.w, ch, p.w);
             ra[i] = v;
         }
 #pragma unroll
@@ -673,7 +704,7 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
             const int ch = j % CPR, h = h0 - 1 + j / CPR;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
             if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && h >= 0 && h < p.h)
-                v = *reinterpret_cast<const u32x4*>(xb + cc * plane + (int64_t)h * p.w + ch * E);
+                v = load_chunk<T, LW>(xb + cc * plane + (int64_t)h * p.w, ch, p.w);
             rb[i] = v;
         }
     };
@@ -803,7 +834,7 @@ __global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* 
 }
 
 
-template <typename T, int P>
+template <typename T, int P, int LW>
 int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
     constexpr int TH = WgCfg<T>::TH;
     constexpr int RB = P * (int)sizeof(T);
@@ -824,11 +855,11 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     if (!ws) return NOTT_ERR_ALLOC;
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3x3_wgrad_kernel<T, P>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3x3_wgrad_kernel<T, P, LW>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr_set = true;
     }
-    hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P>), dim3((unsigned)splits, (unsigned)tiles), dim3(kWgThreads), lds,
+    hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P, LW>), dim3((unsigned)splits, (unsigned)tiles), dim3(kWgThreads), lds,
                        ctx->stream, x, dy, ws, p);
     const int64_t per = (int64_t)9 * p.k * p.c;
     hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256), 0, ctx->stream, ws,
@@ -858,9 +889,17 @@ bool dgrad_applies(const nott_conv2d_desc* d, size_t elem) {
 }
 
 bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {
-    // 16-byte aligned image rows, a slot row of at most 64, whole 64-channel blocks.
-    const int e = elem == 2 ? 8 : 4;
-    return same_shape(d) && d->w % e == 0 && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 64 == 0;
+    // A slot row of at most 64, whole 64-channel blocks (image rows of any
+    // width: narrower loads when rows are not whole 16-byte chunks).
+    (void)elem;
+    return same_shape(d) && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 64 == 0;
+}
+
+// Widest load (bytes) that keeps every image row's pieces aligned.
+int wgrad_load_width(int64_t w, size_t elem) {
+    for (int lw = 16; lw > (int)elem; lw >>= 1)
+        if ((w * (int64_t)elem) % lw == 0) return lw;
+    return (int)elem;
 }
 
 template <typename T>
@@ -874,13 +913,25 @@ int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* d
                              nullptr, dx);
 }
 
+template <typename T, int LW>
+int wgrad_p(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
+    switch (wgrad_slot_pitch(d->w)) {
+        case 8: return run_wgrad<T, 8, LW>(ctx, d, x, dy, dw, accumulate);
+        case 16: return run_wgrad<T, 16, LW>(ctx, d, x, dy, dw, accumulate);
+        case 32: return run_wgrad<T, 32, LW>(ctx, d, x, dy, dw, accumulate);
+        default: return run_wgrad<T, 64, LW>(ctx, d, x, dy, dw, accumulate);
+    }
+}
+
 template <typename T>
 int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
-    switch (wgrad_slot_pitch(d->w)) {
-        case 8: return run_wgrad<T, 8>(ctx, d, x, dy, dw, accumulate);
-        case 16: return run_wgrad<T, 16>(ctx, d, x, dy, dw, accumulate);
-        case 32: return run_wgrad<T, 32>(ctx, d, x, dy, dw, accumulate);
-        default: return run_wgrad<T, 64>(ctx, d, x, dy, dw, accumulate);
+    switch (wgrad_load_width(d->w, sizeof(T))) {
+        case 16: return wgrad_p<T, 16>(ctx, d, x, dy, dw, accumulate);
+        case 8: return wgrad_p<T, 8>(ctx, d, x, dy, dw, accumulate);
+        case 4: return wgrad_p<T, 4>(ctx, d, x, dy, dw, accumulate);
+        default:
+            if constexpr (sizeof(T) == 2) return wgrad_p<T, 2>(ctx, d, x, dy, dw, accumulate);
+            else return wgrad_p<T, 4>(ctx, d, x, dy, dw, accumulate);
     }
 }
 
