@@ -149,7 +149,41 @@ template <typename T> struct VecTasks;
 template <> struct VecTasks<bf16_t> { static constexpr int VT = 1; };
 template <> struct VecTasks<float> { static constexpr int VT = 2; };
 
-template <typename T, bool VEC>
+// Chunk ch (E elements, 16 bytes) of an image row of w elements, read with
+// LW-byte loads (LW = 16 when rows are whole 16-byte chunks; 8, 4 or 2 when
+// w is only a multiple of 4, 2 or 1 bf16 / of 2 or 1 fp32): pieces past the
+// row end read as zero.
+template <typename T, int LW, bool NT = false>
+__device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, int w) {
+    constexpr int E = 16 / (int)sizeof(T), PE = LW / (int)sizeof(T);   // elements per chunk / per piece
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (LW == 16) {
+        if (ch * E < w) {
+            const u32x4* q = reinterpret_cast<const u32x4*>(row + ch * E);
+            v = NT ? __builtin_nontemporal_load(q) : *q;
+        }
+    } else if constexpr (LW == 8) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            if (ch * E + q * PE < w) {
+                const uint2 t = *reinterpret_cast<const uint2*>(row + ch * E + q * PE);
+                v[2 * q] = t.x;
+                v[2 * q + 1] = t.y;
+            }
+    } else if constexpr (LW == 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (ch * E + q * PE < w) v[q] = *reinterpret_cast<const uint32_t*>(row + ch * E + q * PE);
+    } else {
+        static_assert(LW == 2 && sizeof(T) == 2, "2-byte pieces are bf16 elements");
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (ch * E + q < w) v[q >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[ch * E + q] << (16 * (q & 1));
+    }
+    return v;
+}
+
+template <typename T, bool VEC, int LW>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
                                                                   const float* __restrict__ bias, T* __restrict__ out,
                                                                   SameParams p) {
@@ -227,7 +261,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     // quarter-wave then start their SUB-row runs at 16 distinct rows mod 16,
     // so each of the SUB transposed writes is conflict-free.
     constexpr int WG = 16 / SUB;
-    const int32_t wchunks = p.w / SUB;
+    const int32_t wchunks = (p.w + SUB - 1) / SUB;      // the last chunk of a row may be partial
     const int32_t wgroups = (wchunks + WG - 1) / WG;
     const int32_t ntask = nvr * wgroups * WG * 4;
     auto task_of = [&](int32_t t, int32_t& wc, int32_t& vr, int32_t& cig) {
@@ -245,10 +279,9 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         p.fd_h2.divmod((uint32_t)(v_lo + vr), img, hh);
         const int32_t h = (int32_t)hh - 1;
         if (t < ntask && wc < wchunks && h >= 0 && h < p.h) {
-            const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w + wc * SUB;
+            const T* src = in + (((int64_t)img * p.cin + cc * CC + cig * SUB) * p.h + h) * p.w;
 #pragma unroll
-            for (int i = 0; i < SUB; ++i)
-                r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)i * p.hw));
+            for (int i = 0; i < SUB; ++i) r[i] = load_chunk<T, LW, true>(src + (int64_t)i * p.hw, wc, p.w);
         }
     };
     // ... and the transpose + SUB LDS row writes into buffer `dst`.
@@ -263,7 +296,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
             transpose_block(r, tr);
             const int32_t row0 = vr * p.w2 + 1 + wc * SUB;
 #pragma unroll
-            for (int i = 0; i < SUB; ++i) *reinterpret_cast<u32x4*>(dst + lds_off(row0 + i, cig)) = tr[i];
+            for (int i = 0; i < SUB; ++i)     // pixels past the row end stay zero (right halo)
+                if (LW == 16 || wc * SUB + i < p.w) *reinterpret_cast<u32x4*>(dst + lds_off(row0 + i, cig)) = tr[i];
         }
     };
     // Fill of chunk cc: VEC tasks from the registers loaded by fetch_task, or
@@ -465,6 +499,13 @@ size_t same_lds_bytes(int32_t h, int32_t w, size_t elem) {
 }
 constexpr size_t kSameLdsMax = 80 * 1024;   // two workgroups per CU
 
+// Widest load (bytes) that keeps every image row's pieces aligned.
+int wgrad_load_width(int64_t w, size_t elem) {
+    for (int lw = 16; lw > (int)elem; lw >>= 1)
+        if ((w * (int64_t)elem) % lw == 0) return lw;
+    return (int)elem;
+}
+
 template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
              const float* bias, T* out) {
@@ -503,23 +544,30 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     p.partial = splits > 1 ? reinterpret_cast<float*>(ws + wbytes_al) : nullptr;
     p.remap = (tiles % 8 == 0) ? 1 : 0;
     p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
-    // Vector fill when image rows are whole 16-byte chunks and the input is
-    // 16-byte aligned.
-    const int32_t sub = Chunk<T>::SUB;
-    const bool vec = (w % sub) == 0 && ((uintptr_t)in % 16) == 0;
+    // Vector fill when the input is 16-byte aligned and image rows split into
+    // 16- or 8-byte pieces (narrower pieces measured slower than the element
+    // fill).
+    const int lw = wgrad_load_width(w, sizeof(T));
+    const bool vec = ((uintptr_t)in % 16) == 0 && lw >= 8;
     const size_t lds = same_lds_bytes(h, w, sizeof(T));
-    static bool attr_set[2][2] = {{false, false}, {false, false}};
-    if (!attr_set[sizeof(T) == 2][vec]) {
-        const void* fn = vec ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true>)
-                             : reinterpret_cast<const void*>(&conv3x3_same_kernel<T, false>);
-        (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
-        attr_set[sizeof(T) == 2][vec] = true;
-    }
+    const void* fn = !vec      ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, false, 16>)
+                     : lw == 16 ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, 16>)
+                     : lw == 8  ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, 8>)
+                     : lw == 4  ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, 4>)
+                                : reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, sizeof(T) == 2 ? 2 : 4>);
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
     const dim3 grid((unsigned)tiles, (unsigned)(cout / kTileCo), (unsigned)splits);
-    if (vec)
-        hipLaunchKernelGGL((conv3x3_same_kernel<T, true>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    if (!vec)
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, false, 16>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    else if (lw == 16)
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, true, 16>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    else if (lw == 8)
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, true, 8>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+    else if (lw == 4)
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, true, 4>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
     else
-        hipLaunchKernelGGL((conv3x3_same_kernel<T, false>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
+        hipLaunchKernelGGL((conv3x3_same_kernel<T, true, sizeof(T) == 2 ? 2 : 4>), grid, dim3(kThreads), lds, ctx->stream,
+                           in, wp, bias, out, p);
     if (splits > 1)
         hipLaunchKernelGGL(conv3x3_split_reduce_kernel<T>, dim3((unsigned)ceil_div(npix64 / 4 * cout, 256)), dim3(256), 0,
                            ctx->stream, p.partial, splits, cout, p.npix, p.fd_hw, p.hw, bias, out);
@@ -599,37 +647,6 @@ template <>
 __device__ __forceinline__ u32x4 shift_lo<float>(const u32x4& c, const u32x4& n) { return u32x4{c.y, c.z, c.w, n.x}; }
 template <>
 __device__ __forceinline__ u32x4 shift_hi<float>(const u32x4& p, const u32x4& c) { return u32x4{p.w, c.x, c.y, c.z}; }
-
-// Chunk ch (E elements, 16 bytes) of an image row of w elements, read with
-// LW-byte loads (LW = 16 when rows are whole 16-byte chunks; 8, 4 or 2 when
-// w is only a multiple of 4, 2 or 1 bf16 / of 2 or 1 fp32): pieces past the
-// row end read as zero.
-template <typename T, int LW>
-__device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, int w) {
-    constexpr int E = 16 / (int)sizeof(T), PE = LW / (int)sizeof(T);   // elements per chunk / per piece
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (LW == 16) {
-        if (ch * E < w) v = *reinterpret_cast<const u32x4*>(row + ch * E);
-    } else if constexpr (LW == 8) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-            if (ch * E + q * PE < w) {
-                const uint2 t = *reinterpret_cast<const uint2*>(row + ch * E + q * PE);
-                v[2 * q] = t.x;
-                v[2 * q + 1] = t.y;
-            }
-    } else if constexpr (LW == 4) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (ch * E + q * PE < w) v[q] = *reinterpret_cast<const uint32_t*>(row + ch * E + q * PE);
-    } else {
-        static_assert(LW == 2 && sizeof(T) == 2, "2-byte pieces are bf16 elements");
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            if (ch * E + q < w) v[q >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[ch * E + q] << (16 * (q & 1));
-    }
-    return v;
-}
 
 template <typename T, int P, int LW>
 __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
@@ -895,12 +912,6 @@ bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {
     return same_shape(d) && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 64 == 0;
 }
 
-// Widest load (bytes) that keeps every image row's pieces aligned.
-int wgrad_load_width(int64_t w, size_t elem) {
-    for (int lw = 16; lw > (int)elem; lw >>= 1)
-        if ((w * (int64_t)elem) % lw == 0) return lw;
-    return (int)elem;
-}
 
 template <typename T>
 int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
