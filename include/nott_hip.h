@@ -158,6 +158,22 @@ int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, i
                          const void* x, const void* dy, const float* mean, const float* rstd,
                          const float* gamma, void* dx, float* dgamma, float* dbeta,
                          int accumulate);
+/* BatchNorm2d fused with what Nott applies right after it: the layer's own
+ * activation (ReLU; block/details/blocks/residual.hpp:94-96, the BN layer
+ * then Activation::Details::apply) and, for the second BN of a residual
+ * branch, the skip addition and the block's final activation (residual.hpp:
+ * 130-132).  Forward: y = act(BN(x) [+ residual]), act = ReLU when relu != 0
+ * (residual nullable).  Backward with relu != 0: dy is the gradient w.r.t.
+ * relu(BN(x)) (no residual), the ReLU mask is recomputed from x, gamma, beta,
+ * mean and rstd; with relu == 0 it is nott_batchnorm2d_bwd. */
+int nott_batchnorm2d_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                             const void* x, const float* gamma, const float* beta,
+                             double eps, double momentum, float* running_mean, float* running_var,
+                             const void* residual, int relu, void* y, float* mean, float* rstd);
+int nott_batchnorm2d_bwd_act(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                             const void* x, const void* dy, const float* mean, const float* rstd,
+                             const float* gamma, const float* beta, int relu, void* dx,
+                             float* dgamma, float* dbeta, int accumulate);
 
 /* ---- layer norm ---------------------------------------------------------
  * Replaces torch::nn::LayerNorm of TransformerEncoderLayerImpl

@@ -292,6 +292,80 @@ struct BatchNorm2dFn : torch::autograd::Function<BatchNorm2dFn> {
     }
 };
 
+// BatchNorm2d followed by the layer's ReLU (block/details/blocks/residual.hpp:
+// 94-96: the layer, then Activation::Details::apply): one apply pass forward;
+// the backward recomputes the ReLU mask from x inside the BN backward.
+struct BatchNorm2dReluFn : torch::autograd::Function<BatchNorm2dReluFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor gamma, Tensor beta, Tensor running_mean,
+                          Tensor running_var, double eps, double momentum) {
+        x = contig(x);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor y = torch::empty_like(x);
+        auto fo = x.options().dtype(torch::kFloat32);
+        Tensor mean = torch::empty({ch}, fo), rstd = torch::empty({ch}, fo);
+        nott_ctx c = bind(x);
+        check(nott_batchnorm2d_fwd_act(c, dtype_of(x), n, ch, hw, ptr(x), fptr(gamma), fptr(beta), eps, momentum,
+                                       fptr(running_mean), fptr(running_var), nullptr, 1, ptr(y), fptr(mean),
+                                       fptr(rstd)),
+              c, "batchnorm+relu forward");
+        ctx->save_for_backward({x, gamma, beta, mean, rstd});
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4];
+        Tensor dy = contig(grads[0]);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
+        Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
+        nott_ctx c = bind(dy);
+        check(nott_batchnorm2d_bwd_act(c, dtype_of(dy), n, ch, hw, ptr(x), ptr(dy), fptr(mean), fptr(rstd),
+                                       fptr(gamma), fptr(beta), 1, ptr(dx), fptr(gg), fptr(gbt), 1),
+              c, "batchnorm+relu backward");
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+// The second BatchNorm2d of a residual branch with the skip addition and the
+// block's final ReLU (residual.hpp:130-132): y = relu(BN(x) + skip) in one
+// apply pass.  Backward: dz = dy·[y > 0] feeds both the BN backward and the
+// skip.
+struct BatchNorm2dAddReluFn : torch::autograd::Function<BatchNorm2dAddReluFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor skip, Tensor gamma, Tensor beta,
+                          Tensor running_mean, Tensor running_var, double eps, double momentum) {
+        x = contig(x);
+        skip = contig(skip);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor y = torch::empty_like(x);
+        auto fo = x.options().dtype(torch::kFloat32);
+        Tensor mean = torch::empty({ch}, fo), rstd = torch::empty({ch}, fo);
+        nott_ctx c = bind(x);
+        check(nott_batchnorm2d_fwd_act(c, dtype_of(x), n, ch, hw, ptr(x), fptr(gamma), fptr(beta), eps, momentum,
+                                       fptr(running_mean), fptr(running_var), ptr(skip), 1, ptr(y), fptr(mean),
+                                       fptr(rstd)),
+              c, "batchnorm+add+relu forward");
+        ctx->save_for_backward({x, gamma, beta, mean, rstd, y});
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4], y = s[5];
+        Tensor dy = contig(grads[0]);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        Tensor dz = torch::empty_like(dy);
+        nott_ctx c = bind(dy);
+        check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "block relu backward");
+        Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
+        Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
+        check(nott_batchnorm2d_bwd(c, dtype_of(dz), n, ch, hw, ptr(x), ptr(dz), fptr(mean), fptr(rstd), fptr(gamma),
+                                   ptr(dx), fptr(gg), fptr(gbt), 1),
+              c, "batchnorm backward");
+        return {dx, dz, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
 // ------------------------------------------------------------ LayerNorm
 struct LayerNormFn : torch::autograd::Function<LayerNormFn> {
     static Tensor forward(AutogradContext* ctx, Tensor x, Tensor gamma, Tensor beta, Tensor gamma_c, Tensor beta_c,
@@ -469,6 +543,17 @@ public:
     Tensor forward(const Tensor& x) {
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
         return BatchNorm2dFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
+    }
+    // relu(BN(x)): the layer with its ReLU activation, fused.
+    Tensor forward_relu(const Tensor& x) {
+        if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        return BatchNorm2dReluFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
+    }
+    // relu(BN(x) + skip): the residual branch's last layer, skip addition and
+    // final ReLU, fused.
+    Tensor forward_add_relu(const Tensor& x, const Tensor& skip) {
+        if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        return BatchNorm2dAddReluFn::apply(x, skip, weight, bias, running_mean, running_var, eps_, momentum_);
     }
     Tensor weight, bias, running_mean, running_var;
 private:

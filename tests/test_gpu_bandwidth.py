@@ -154,8 +154,11 @@ def test_avgpool_global(ops, oracle, dt):
 
 
 # -------------------------------------------------------------- batchnorm
+BN_SHAPES = [(64, 64, 56, 56), (64, 512, 7, 7), (3, 5, 4, 3)]
+
+
 @pytest.mark.parametrize("dt", DTYPES)
-@pytest.mark.parametrize("shape", [(64, 64, 56, 56), (64, 512, 7, 7), (3, 5, 4, 3)])
+@pytest.mark.parametrize("shape", BN_SHAPES)
 def test_batchnorm(ops, oracle, dt, shape):
     n, c, h, w = shape
     g = rng(n * c + h)
@@ -177,6 +180,40 @@ def test_batchnorm(ops, oracle, dt, shape):
     check(host(dx), dxe, dt, "bn dx")
     check(host(dg), dge, "f32", "bn dgamma")
     check(host(db), dbe, "f32", "bn dbeta")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("shape", BN_SHAPES)
+@pytest.mark.parametrize("with_res", [False, True])
+def test_batchnorm_act(ops, oracle, dt, shape, with_res):
+    """nott_batchnorm2d_fwd_act / _bwd_act against the composition the
+    reference runs: BatchNorm2d, then (+ skip) ReLU (residual.hpp:94-96,
+    130-132); the backward through the ReLU masks dy where BN(x) <= 0."""
+    n, c, h, w = shape
+    g = rng(n * c + h + 7)
+    x = host_input(g.standard_normal(shape) * 1.5 + 0.3, dt)
+    gamma = f32(1 + 0.1 * g.standard_normal(c))
+    beta = f32(0.1 * g.standard_normal(c))
+    res = host_input(g.standard_normal(shape), dt) if with_res else None
+    y, mean, rstd = ops.batchnorm2d_fwd(dev(x, dt), dev(gamma), dev(beta), 1e-5, 0.1,
+                                        residual=dev(res, dt) if with_res else None, relu=True)
+    ye, me, re_, _, _ = oracle.batchnorm2d_fwd(x, gamma, beta, 1e-5, 0.1, f32(np.zeros(c)), f32(np.ones(c)))
+    check(host(mean), me, "f32", "bn mean", atol=1e-5)
+    ya = ye + (res if with_res else 0.0)
+    check(host(y), np.maximum(ya, 0.0), dt, "bn+relu y")
+    if with_res:
+        return                       # the residual block's backward goes through relu_bwd + BN backward
+    dy = host_input(g.standard_normal(shape), dt)
+    dx, dg, db = ops.batchnorm2d_bwd(dev(x, dt), dev(dy, dt), mean, rstd, dev(gamma), beta=dev(beta), relu=True)
+    # mask from this run's statistics (a flip needs |BN(x)| below fp32 rounding)
+    mh, rh = host(mean).astype(np.float64), host(rstd).astype(np.float64)
+    z = (x.astype(np.float64) - mh[None, :, None, None]) * rh[None, :, None, None] * gamma[None, :, None, None] \
+        + beta[None, :, None, None]
+    dym = np.where(z > 0, dy, 0.0).astype(np.float32)
+    dxe, dge, dbe = oracle.batchnorm2d_bwd(x, dym, host(mean), host(rstd), gamma)
+    check(host(dx), dxe, dt, "bn+relu dx")
+    check(host(dg), dge, "f32", "bn+relu dgamma")
+    check(host(db), dbe, "f32", "bn+relu dbeta")
 
 
 # -------------------------------------------------------------- layernorm

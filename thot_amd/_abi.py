@@ -71,6 +71,8 @@ SIGNATURES: dict[str, list] = {
     "nott_avgpool_global_bwd": [vp, i32, i64, i64, vp, vp],
     "nott_batchnorm2d_fwd": [vp, i32, i64, i64, i64, vp, fp, fp, f64, f64, fp, fp, vp, fp, fp],
     "nott_batchnorm2d_bwd": [vp, i32, i64, i64, i64, vp, vp, fp, fp, fp, vp, fp, fp, i32],
+    "nott_batchnorm2d_fwd_act": [vp, i32, i64, i64, i64, vp, fp, fp, f64, f64, fp, fp, vp, i32, vp, fp, fp],
+    "nott_batchnorm2d_bwd_act": [vp, i32, i64, i64, i64, vp, vp, fp, fp, fp, fp, i32, vp, fp, fp, i32],
     "nott_layernorm_fwd": [vp, i32, i64, i64, vp, vp, vp, f64, vp, fp, fp],
     "nott_layernorm_bwd": [vp, i32, i64, i64, vp, vp, fp, fp, vp, vp, fp, fp, i32],
     "nott_softmax_xent_bwd": [vp, i32, i64, i64, vp, vp, f64, f64, vp, fp],

@@ -73,7 +73,28 @@ __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict_
 }
 
 // Per channel: mean, rstd, running stats and the affine coefficients
-// y = a·x + b used by the apply pass.
+// Per-channel affine form of the normalisation, z = a·x + c, shared by the
+// forward apply and by the backward's recomputation of the ReLU mask, so both
+// see the same z bit for bit.
+__device__ __forceinline__ void bn_coef(float g, float b, float mu, float rs, float& a, float& c) {
+#pragma clang fp contract(off)
+    a = g * rs;
+    c = b - mu * a;
+}
+__device__ __forceinline__ float bn_z(float x, float a, float c) { return __builtin_fmaf(x, a, c); }
+// ReLU forward (a NaN passes) and its gradient mask (zero where y <= 0).
+__device__ __forceinline__ float relu_f(float v) { return (v > 0.f || v != v) ? v : 0.f; }
+
+// Backward through a fused ReLU: the incoming gradient is w.r.t.
+// relu(a·x + c); the mask is recomputed from x, γ, β, μ and rstd.
+struct BnAct {
+    int relu;
+    const float* gamma;
+    const float* beta;
+    const float* rstd;
+};
+
+// y = a·x + c used by the apply pass.
 template <typename T>
 __global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict__ partial, int64_t c, int64_t splits,
                                 int64_t hw, int64_t m, const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -96,8 +117,7 @@ __global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict
     mean[ch] = mu;
     rstd[ch] = rs;
     const float g = gamma ? gamma[ch] : 1.f, b = beta ? beta[ch] : 0.f;
-    coef[2 * ch + 0] = g * rs;
-    coef[2 * ch + 1] = b - mu * g * rs;
+    bn_coef(g, b, mu, rs, coef[2 * ch + 0], coef[2 * ch + 1]);
     if (running_mean) {
         const double unbiased = m > 1 ? var * (double)m / (double)(m - 1) : var;
         running_mean[ch] = (1.f - momentum) * running_mean[ch] + momentum * mu;
@@ -105,10 +125,11 @@ __global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict
     }
 }
 
-// y = a_c·x + b_c over the whole tensor.
+// y = act(a_c·x + c_c [+ res]) over the whole tensor (act = ReLU or identity).
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t total,
-                                                             int64_t c, int64_t hw, const float* __restrict__ coef) {
+                                                             int64_t c, int64_t hw, const float* __restrict__ coef,
+                                                             const T* __restrict__ res, int relu) {
     // grid: x over the n·c planes, y over each plane's hw: no per-element division
     const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
     if (j >= hw) return;
@@ -118,10 +139,15 @@ __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict
     const float a = coef[2 * ch], b = coef[2 * ch + 1];
     if (VEC) {
         f32x4 v = Vec4<T>::ld(x + i);
-        v.x = v.x * a + b; v.y = v.y * a + b; v.z = v.z * a + b; v.w = v.w * a + b;
+        v.x = bn_z(v.x, a, b); v.y = bn_z(v.y, a, b); v.z = bn_z(v.z, a, b); v.w = bn_z(v.w, a, b);
+        if (res) v += Vec4<T>::ld(res + i);
+        if (relu) { v.x = relu_f(v.x); v.y = relu_f(v.y); v.z = relu_f(v.z); v.w = relu_f(v.w); }
         Vec4<T>::st(y + i, v);
     } else {
-        Io<T>::st(y, i, Io<T>::ld(x, i) * a + b);
+        float v = bn_z(Io<T>::ld(x, i), a, b);
+        if (res) v += Io<T>::ld(res, i);
+        if (relu) v = relu_f(v);
+        Io<T>::st(y, i, v);
     }
 }
 
@@ -130,26 +156,36 @@ template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                  const float* __restrict__ mean, int64_t n, int64_t c,
                                                                  int64_t hw, int64_t per_split,
-                                                                 float* __restrict__ partial) {
+                                                                 float* __restrict__ partial, BnAct act) {
     __shared__ float red[2 * kWaves];
     const int64_t ch = blockIdx.x;
     const int64_t n0 = (int64_t)blockIdx.y * per_split;
     const int64_t n1 = std::min<int64_t>(n, n0 + per_split);
     const float mu = mean[ch];
+    float za = 0.f, zc = 0.f;   // z = za·x + zc when the gradient comes through a ReLU
+    if (act.relu) bn_coef(act.gamma ? act.gamma[ch] : 1.f, act.beta ? act.beta[ch] : 0.f, mu, act.rstd[ch], za, zc);
     float s1 = 0.f, s2 = 0.f;
     for (int64_t i = n0; i < n1; ++i) {
         const int64_t base = (i * c + ch) * hw;
         if (VEC) {
             for (int64_t j = (int64_t)threadIdx.x * 4; j < hw; j += kThreads * 4) {
                 f32x4 g = Vec4<T>::ld(dy + base + j), v = Vec4<T>::ld(x + base + j);
+                if (act.relu) {
+                    if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
+                    if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
+                    if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
+                    if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
+                }
                 s1 += (g.x + g.y) + (g.z + g.w);
                 s2 += (g.x * (v.x - mu) + g.y * (v.y - mu)) + (g.z * (v.z - mu) + g.w * (v.w - mu));
             }
         } else {
             for (int64_t j = threadIdx.x; j < hw; j += kThreads) {
-                const float g = Io<T>::ld(dy, base + j);
+                const float xv = Io<T>::ld(x, base + j);
+                float g = Io<T>::ld(dy, base + j);
+                if (act.relu && bn_z(xv, za, zc) <= 0.f) g = 0.f;
                 s1 += g;
-                s2 += g * (Io<T>::ld(x, base + j) - mu);
+                s2 += g * (xv - mu);
             }
         }
     }
@@ -188,21 +224,34 @@ __global__ void bn_bwd_finalize(const float* __restrict__ partial, int64_t c, in
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                 T* __restrict__ dx, int64_t total, int64_t c,
-                                                                int64_t hw, const float* __restrict__ coef) {
+                                                                int64_t hw, const float* __restrict__ coef,
+                                                                const float* __restrict__ mean, BnAct act) {
     const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
     if (j >= hw) return;
     const int64_t plane = blockIdx.x;
     const int64_t i = plane * hw + j;
     const int64_t ch = plane % c;
     const float A = coef[3 * ch], B = coef[3 * ch + 1], C = coef[3 * ch + 2];
+    float za = 0.f, zc = 0.f;
+    if (act.relu)
+        bn_coef(act.gamma ? act.gamma[ch] : 1.f, act.beta ? act.beta[ch] : 0.f, mean[ch], act.rstd[ch], za, zc);
     if (VEC) {
         f32x4 g = Vec4<T>::ld(dy + i), v = Vec4<T>::ld(x + i);
+        if (act.relu) {
+            if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
+            if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
+            if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
+            if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
+        }
         f32x4 r;
         r.x = A * g.x + B * v.x + C; r.y = A * g.y + B * v.y + C;
         r.z = A * g.z + B * v.z + C; r.w = A * g.w + B * v.w + C;
         Vec4<T>::st(dx + i, r);
     } else {
-        Io<T>::st(dx, i, A * Io<T>::ld(dy, i) + B * Io<T>::ld(x, i) + C);
+        const float xv = Io<T>::ld(x, i);
+        float g = Io<T>::ld(dy, i);
+        if (act.relu && bn_z(xv, za, zc) <= 0.f) g = 0.f;
+        Io<T>::st(dx, i, A * g + B * xv + C);
     }
 }
 
@@ -213,8 +262,9 @@ int64_t pick_splits(int64_t n, int64_t c) {
 
 template <typename T>
 int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const float* gamma, const float* beta,
-        float eps, float momentum, float* rm, float* rv, void* yv, float* mean, float* rstd) {
+        float eps, float momentum, float* rm, float* rv, void* yv, float* mean, float* rstd, const void* resv, int relu) {
     const T* x = static_cast<const T*>(xv);
+    const T* res = static_cast<const T*>(resv);
     T* y = static_cast<T*>(yv);
     const int64_t splits0 = pick_splits(n, c);
     const int64_t per = nott::ceil_div(n, splits0);
@@ -223,7 +273,8 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
     if (!ws) return NOTT_ERR_ALLOC;
     float* partial = ws;
     float* coef = ws + 2 * c * splits;
-    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 && ((uintptr_t)yv % (4 * sizeof(T))) == 0;
+    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 && ((uintptr_t)yv % (4 * sizeof(T))) == 0 &&
+                     ((uintptr_t)resv % (4 * sizeof(T))) == 0;
     const dim3 g1((unsigned)c, (unsigned)splits);
     if (vec)
         hipLaunchKernelGGL((bn_stats_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
@@ -234,16 +285,16 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
     const int64_t total = n * c * hw;
     if (vec)
         hipLaunchKernelGGL((bn_affine_kernel<T, true>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)),
-                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
+                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef, res, relu);
     else
         hipLaunchKernelGGL((bn_affine_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
-                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef);
+                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef, res, relu);
     return nott::launch_status(ctx, "batchnorm_fwd");
 }
 
 template <typename T>
 int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const void* dyv, const float* mean,
-        const float* rstd, const float* gamma, void* dxv, float* dgamma, float* dbeta, int accumulate) {
+        const float* rstd, const float* gamma, void* dxv, float* dgamma, float* dbeta, int accumulate, BnAct act) {
     const T* x = static_cast<const T*>(xv);
     const T* dy = static_cast<const T*>(dyv);
     T* dx = static_cast<T*>(dxv);
@@ -259,10 +310,10 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     const dim3 g1((unsigned)c, (unsigned)splits);
     if (vec)
         hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
-                           per, partial);
+                           per, partial, act);
     else
         hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
-                           per, partial);
+                           per, partial, act);
     hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, partial, c,
                        splits, n * hw, mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
     if (dx) {
@@ -270,19 +321,20 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
         if (vec)
             hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>),
                                dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)), dim3(kThreads), 0,
-                               ctx->stream, x, dy, dx, total, c, hw, coef);
+                               ctx->stream, x, dy, dx, total, c, hw, coef, mean, act);
         else
             hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
-                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef);
+                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef, mean, act);
     }
     return nott::launch_status(ctx, "batchnorm_bwd");
 }
 
 }  // namespace
 
-extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
-                                    const float* gamma, const float* beta, double eps, double momentum,
-                                    float* running_mean, float* running_var, void* y, float* mean, float* rstd) {
+extern "C" int nott_batchnorm2d_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                                        const void* x, const float* gamma, const float* beta, double eps,
+                                        double momentum, float* running_mean, float* running_var,
+                                        const void* residual, int relu, void* y, float* mean, float* rstd) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_fwd: bad shape");
     NOTT_REQUIRE(ctx, (running_mean == nullptr) == (running_var == nullptr),
@@ -291,19 +343,35 @@ extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, i
     NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_fwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
     return dtype == NOTT_F32 ? fwd<float>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
-                                          running_var, y, mean, rstd)
+                                          running_var, y, mean, rstd, residual, relu != 0)
                              : fwd<bf16_t>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
-                                           running_var, y, mean, rstd);
+                                           running_var, y, mean, rstd, residual, relu != 0);
 }
 
-extern "C" int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
-                                    const void* dy, const float* mean, const float* rstd, const float* gamma, void* dx,
-                                    float* dgamma, float* dbeta, int accumulate) {
+extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
+                                    const float* gamma, const float* beta, double eps, double momentum,
+                                    float* running_mean, float* running_var, void* y, float* mean, float* rstd) {
+    return nott_batchnorm2d_fwd_act(ctx, dtype, n, c, hw, x, gamma, beta, eps, momentum, running_mean, running_var,
+                                    nullptr, 0, y, mean, rstd);
+}
+
+extern "C" int nott_batchnorm2d_bwd_act(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                                        const void* x, const void* dy, const float* mean, const float* rstd,
+                                        const float* gamma, const float* beta, int relu, void* dx, float* dgamma,
+                                        float* dbeta, int accumulate) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_bwd: bad shape");
     NOTT_REQUIRE(ctx, x && dy && mean && rstd, "nott_batchnorm2d_bwd: null buffer");
     NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_bwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
-    return dtype == NOTT_F32 ? bwd<float>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate)
-                             : bwd<bf16_t>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate);
+    const BnAct act{relu != 0, gamma, beta, rstd};
+    return dtype == NOTT_F32 ? bwd<float>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, act)
+                             : bwd<bf16_t>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, act);
+}
+
+extern "C" int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,
+                                    const void* dy, const float* mean, const float* rstd, const float* gamma, void* dx,
+                                    float* dgamma, float* dbeta, int accumulate) {
+    return nott_batchnorm2d_bwd_act(ctx, dtype, n, c, hw, x, dy, mean, rstd, gamma, nullptr, 0, dx, dgamma, dbeta,
+                                    accumulate);
 }

@@ -161,7 +161,9 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
     __syncthreads();
     const int32_t nout = (oh1 - oh0) * g.ow;
     for (int32_t j = threadIdx.x; j < nout; j += kThreads) {
-        const int32_t oh = oh0 + j / g.ow, ow = j % g.ow;
+        uint32_t ohl, owu;
+        g.fd_ow.divmod((uint32_t)j, ohl, owu);
+        const int32_t oh = oh0 + (int32_t)ohl, ow = (int32_t)owu;
         int32_t ih0 = oh * g.sh - g.ph, iw0 = ow * g.sw - g.pw;
         const int32_t ih1 = min(ih0 + (g.kh - 1) * g.dh + 1, g.h);
         const int32_t iw1 = min(iw0 + (g.kw - 1) * g.dw + 1, g.w);
@@ -209,14 +211,16 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
     __syncthreads();
     const int32_t nin = (ih_hi - ih_lo) * g.w;
     for (int32_t j = threadIdx.x; j < nin; j += kThreads) {
-        const int32_t ih = ih_lo + j / g.w, iw = j % g.w;
+        uint32_t ihl, iwu;
+        g.fd_w.divmod((uint32_t)j, ihl, iwu);
+        const int32_t ih = ih_lo + (int32_t)ihl, iw = (int32_t)iwu;
         const int32_t idx = ih * g.w + iw;
         const int32_t num_h = ih + g.ph - (g.kh - 1) * g.dh;
-        const int32_t oh0 = num_h <= 0 ? 0 : (num_h + g.sh - 1) / g.sh;
-        const int32_t oh1 = min((ih + g.ph) / g.sh, g.oh - 1);
+        const int32_t oh0 = num_h <= 0 ? 0 : (int32_t)g.fd_sh.div((uint32_t)(num_h + g.sh - 1));
+        const int32_t oh1 = min((int32_t)g.fd_sh.div((uint32_t)(ih + g.ph)), g.oh - 1);
         const int32_t num_w = iw + g.pw - (g.kw - 1) * g.dw;
-        const int32_t ow0 = num_w <= 0 ? 0 : (num_w + g.sw - 1) / g.sw;
-        const int32_t ow1 = min((iw + g.pw) / g.sw, g.ow - 1);
+        const int32_t ow0 = num_w <= 0 ? 0 : (int32_t)g.fd_sw.div((uint32_t)(num_w + g.sw - 1));
+        const int32_t ow1 = min((int32_t)g.fd_sw.div((uint32_t)(iw + g.pw)), g.ow - 1);
         float acc = 0.f;
         for (int32_t oh = oh0; oh <= oh1; ++oh)
             for (int32_t ow = ow0; ow <= ow1; ++ow) {

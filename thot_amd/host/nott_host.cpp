@@ -50,6 +50,13 @@ struct BasicBlockImpl : torch::nn::Module {
     }
     Tensor forward(const Tensor& x) {
         auto f = NH::ForkFn::apply(x);     // x feeds the branch and the skip
+        if (!keep) {
+            // BN + ReLU and BN + skip + ReLU fused (same values; the probe
+            // below keeps every intermediate as its own tensor).
+            Tensor h = b1->forward_relu(c1(f[0]));
+            Tensor skip = proj ? proj(f[1]) : f[1];
+            return b2->forward_add_relu(c2(h), skip);
+        }
         Tensor c0 = c1(f[0]);
         Tensor h = NH::relu(b1(c0));
         Tensor c1o = c2(h);
@@ -87,7 +94,7 @@ struct ResNet18Impl : torch::nn::Module {
         fc = register_module("fc", NH::Linear(512, classes));
     }
     Tensor forward(Tensor x) {
-        x = NH::max_pool2d(NH::relu(stem_bn(stem(x))), 3, 2, 1);
+        x = NH::max_pool2d(keep_grads ? NH::relu(stem_bn(stem(x))) : stem_bn->forward_relu(stem(x)), 3, 2, 1);
         if (keep_grads) mark(x, "stem_out");
         for (size_t i = 0; i < blocks.size(); ++i) {
             x = blocks[i](x);

@@ -207,7 +207,10 @@ def layernorm_bwd(x: torch.Tensor, dy: torch.Tensor, mean: torch.Tensor, rstd: t
 # ------------------------------------------------------------------ batchnorm
 def batchnorm2d_fwd(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5,
                     momentum: float = 0.1, running_mean: Optional[torch.Tensor] = None,
-                    running_var: Optional[torch.Tensor] = None):
+                    running_var: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None,
+                    relu: bool = False):
+    """Training-mode BatchNorm2d; with `residual` / `relu` the fused
+    y = act(BN(x) [+ residual]) of nott_batchnorm2d_fwd_act."""
     _check(x, "x")
     if x.dim() != 4:
         raise ValueError("x must be [n, c, h, w]")
@@ -222,15 +225,24 @@ def batchnorm2d_fwd(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, ep
     y = torch.empty_like(x)
     mean = torch.empty(c, dtype=torch.float32, device=x.device)
     rstd = torch.empty(c, dtype=torch.float32, device=x.device)
-    _ctx_for(x).call("nott_batchnorm2d_fwd", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta),
-                     float(eps), float(momentum), _ptr(running_mean), _ptr(running_var), _ptr(y), _ptr(mean),
-                     _ptr(rstd))
+    if residual is None and not relu:
+        _ctx_for(x).call("nott_batchnorm2d_fwd", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta),
+                         float(eps), float(momentum), _ptr(running_mean), _ptr(running_var), _ptr(y), _ptr(mean),
+                         _ptr(rstd))
+    else:
+        if residual is not None:
+            _check(residual, "residual", shape=x.shape, dtype=x.dtype, device=x.device)
+        _ctx_for(x).call("nott_batchnorm2d_fwd_act", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(gamma),
+                         _ptr(beta), float(eps), float(momentum), _ptr(running_mean), _ptr(running_var),
+                         _ptr(residual), int(relu), _ptr(y), _ptr(mean), _ptr(rstd))
     return y, mean, rstd
 
 
 def batchnorm2d_bwd(x: torch.Tensor, dy: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor, gamma: torch.Tensor,
                     dgamma: Optional[torch.Tensor] = None, dbeta: Optional[torch.Tensor] = None,
-                    accumulate: bool = False):
+                    accumulate: bool = False, beta: Optional[torch.Tensor] = None, relu: bool = False):
+    """BatchNorm2d backward; with relu=True, dy is the gradient w.r.t.
+    relu(BN(x)) and `beta` is required (nott_batchnorm2d_bwd_act)."""
     _check(x, "x")
     if x.dim() != 4:
         raise ValueError("x must be [n, c, h, w]")
@@ -243,8 +255,16 @@ def batchnorm2d_bwd(x: torch.Tensor, dy: torch.Tensor, mean: torch.Tensor, rstd:
     dbeta = torch.empty(c, dtype=torch.float32, device=x.device) if dbeta is None else dbeta
     _check(dgamma, "dgamma", shape=(c,), dtype=torch.float32, device=x.device)
     _check(dbeta, "dbeta", shape=(c,), dtype=torch.float32, device=x.device)
-    _ctx_for(x).call("nott_batchnorm2d_bwd", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(dy), _ptr(mean),
-                     _ptr(rstd), _ptr(gamma), _ptr(dx), _ptr(dgamma), _ptr(dbeta), int(accumulate))
+    if not relu:
+        _ctx_for(x).call("nott_batchnorm2d_bwd", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(dy), _ptr(mean),
+                         _ptr(rstd), _ptr(gamma), _ptr(dx), _ptr(dgamma), _ptr(dbeta), int(accumulate))
+    else:
+        if beta is None:
+            raise ValueError("relu=True needs beta")
+        _check(beta, "beta", shape=(c,), dtype=torch.float32, device=x.device)
+        _ctx_for(x).call("nott_batchnorm2d_bwd_act", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(dy), _ptr(mean),
+                         _ptr(rstd), _ptr(gamma), _ptr(beta), 1, _ptr(dx), _ptr(dgamma), _ptr(dbeta),
+                         int(accumulate))
     return dx, dgamma, dbeta
 
 
