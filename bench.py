@@ -269,6 +269,8 @@ class TrainStep(Workload):
     bound = "mfma"
     BATCH = 64
 
+    graph = True   # forward + loss + backward replayed from a captured HIP graph (AdamW eager)
+
     def __init__(self, dtype, model):
         self.dtype = dtype
         self.name = model
@@ -289,9 +291,18 @@ class TrainStep(Workload):
             self.y = torch.randint(0, 1000, (self.BATCH,), generator=g, device="cuda")
             self.flop_sample = 3 * 2 * 1.814e9   # ResNet-18 at 224^2: 1.814 GMAC forward
         self.tr.step(self.x, self.y)
+        if self.graph:
+            try:
+                self.tr.capture(self.x, self.y, 2)
+            except RuntimeError as e:   # reported in the JSON line via hip_graph = false
+                print(f"bench: HIP graph capture failed, stepping eagerly: {e}", file=sys.stderr)
+                self.graph = False
 
     def step(self):
-        self.tr.step(self.x, self.y)
+        if self.graph:
+            self.tr.step_graph(self.x, self.y)
+        else:
+            self.tr.step(self.x, self.y)
 
     def work_per_step(self):
         return self.BATCH
@@ -439,6 +450,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for cpu_baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="training-step workloads: run every step eagerly instead of replaying a captured HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run 3 plain 256 MiB device copies (the known-size kernel that calibrates "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes)")
@@ -465,6 +478,7 @@ def main():
         del src, dst
 
     dtype = args.dtype or ("f32" if args.workload in ("ln_bwd", "xent", "adamw", "small_cnn") else "bf16")
+    TrainStep.graph = not args.eager
     wl = WORKLOADS[args.workload](dtype)
     wl.setup(torch, ops)
     wl.ev0 = wl.ev1 = None
@@ -503,7 +517,8 @@ def main():
                 "peak": peak, "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None}
         metric_part = "train samples/s"
         cfg = {"workload": f"{wl.name} training step (BASELINE configs[{0 if wl.name == 'small_cnn' else 4}])",
-               "batch": wl.BATCH, "optimizer": "Adam" if wl.name == "small_cnn" else "AdamW"}
+               "batch": wl.BATCH, "optimizer": "Adam" if wl.name == "small_cnn" else "AdamW",
+               "hip_graph": wl.graph}
     else:
         kms = simple_kernel_ms(torch, wl, args.steps)
         value = wl.work_per_step() / (ms * 1e-3) / 1e9
@@ -544,7 +559,7 @@ def main():
             leg = TrainStep(dt, model)
             leg.setup(torch, ops)
             lms = time_workload(torch, leg, args.steps, args.warmup)
-            rec = {"samples/s": round(leg.BATCH / (lms * 1e-3), 1), "ms_per_step": round(lms, 3),
+            rec = {"samples/s": round(leg.BATCH / (lms * 1e-3), 1), "ms_per_step": round(lms, 3), "hip_graph": leg.graph,
                    "batch": leg.BATCH}
             if not args.no_cpu and dt == "f32":
                 try:

@@ -10,6 +10,9 @@
 
 #include "nott_hip/host.hpp"
 
+#include <ATen/hip/HIPGraph.h>
+#include <c10/hip/HIPGuard.h>
+
 namespace NH = Nott::HIP;
 using torch::Tensor;
 
@@ -163,6 +166,46 @@ struct Trainer {
         opt->step();   // fused AdamW + zero_grad (+ bf16 copies)
         return loss;
     }
+
+    // Step orchestration on device (the reference's CUDA-graph step path,
+    // src/core.hpp:3829-3945): forward + loss + backward are captured once
+    // into a HIP graph over static input buffers, so a step is two input
+    // copies, one graph launch and the fused AdamW launch.  The optimizer
+    // step stays outside the graph because its step count and bias
+    // corrections change every step.  `warmup` forward/backward passes run
+    // first on the capture stream (workspace, library plans and allocator
+    // pools reach their steady state; their gradients are zeroed again).
+    std::unique_ptr<at::cuda::CUDAGraph> graph;
+    Tensor gx, gy, gloss;
+    void warmup(const Tensor& x, const Tensor& y, int passes) {
+        for (int i = 0; i < passes; ++i) forward_backward(x, y);
+        opt->zero_grad();
+    }
+    void capture(const Tensor& x, const Tensor& y, int passes) {
+        gx = x.clone();
+        gy = y.clone();
+        if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("capture: device synchronize failed");
+        auto s = c10::hip::getStreamFromPool();
+        {
+            c10::hip::HIPStreamGuard guard(s);
+            warmup(gx, gy, passes);
+            if (hipStreamSynchronize(s.stream()) != hipSuccess) throw std::runtime_error("capture: stream sync failed");
+            auto g = std::make_unique<at::cuda::CUDAGraph>();
+            g->capture_begin();
+            gloss = forward_backward(gx, gy);
+            g->capture_end();
+            graph = std::move(g);
+        }
+        if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("capture: device synchronize failed");
+    }
+    Tensor step_graph(const Tensor& x, const Tensor& y) {
+        if (!graph) throw std::logic_error("step_graph: call capture() first");
+        gx.copy_(x);
+        gy.copy_(y);
+        graph->replay();
+        opt->step();
+        return gloss.clone();
+    }
     Tensor forward(const Tensor& x) {
         torch::NoGradGuard ng;
         return model->forward(input(x));
@@ -213,6 +256,11 @@ PYBIND11_MODULE(_nott_host, m) {
              }),
              py::arg("device") = 0, py::arg("seed") = 0, py::arg("lr") = 1e-3)
         .def("step", &SmallT::step, py::call_guard<py::gil_scoped_release>())
+        .def("warmup", &SmallT::warmup, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
+             py::call_guard<py::gil_scoped_release>())
+        .def("capture", &SmallT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
+             py::call_guard<py::gil_scoped_release>())
+        .def("step_graph", &SmallT::step_graph, py::call_guard<py::gil_scoped_release>())
         .def("forward_backward", &SmallT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", [](SmallT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
         .def("forward", &SmallT::forward, py::call_guard<py::gil_scoped_release>())
@@ -232,6 +280,11 @@ PYBIND11_MODULE(_nott_host, m) {
              py::arg("device") = 0, py::arg("seed") = 0, py::arg("bf16") = false, py::arg("lr") = 1e-3,
              py::arg("weight_decay") = 1e-2, py::arg("classes") = 1000)
         .def("step", &ResT::step, py::call_guard<py::gil_scoped_release>())
+        .def("warmup", &ResT::warmup, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
+             py::call_guard<py::gil_scoped_release>())
+        .def("capture", &ResT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
+             py::call_guard<py::gil_scoped_release>())
+        .def("step_graph", &ResT::step_graph, py::call_guard<py::gil_scoped_release>())
         .def("forward_backward", &ResT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", [](ResT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
         .def("forward", &ResT::forward, py::call_guard<py::gil_scoped_release>())
