@@ -563,7 +563,7 @@ int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
     DgradALoader<T> la{static_cast<const T*>(dy), g, M, K};
     DgradBLoader<T> lb{static_cast<const T*>(w), g, d->c, K};
     DgradStore<T> ep{static_cast<T*>(dx), g, M};
-    return run<T>(ctx, la, lb, ep, M, d->c, K, 1);
+    return run<T>(ctx, la, lb, ep, M, d->c, K);
 }
 
 template <typename T>
