@@ -27,7 +27,7 @@ struct Geom {
     int32_t n, c, h, w, k, r, s, p, q;
     int32_t sh, sw, ph, pw, dh, dw;
     int32_t nhwc;
-    FastDiv fd_pq, fd_q, fd_rs, fd_s, fd_hw, fd_w, fd_sh, fd_sw;
+    FastDiv fd_pq, fd_q, fd_rs, fd_s, fd_hw, fd_w, fd_sh, fd_sw, fd_c;
 };
 
 Geom make_geom(const nott_conv2d_desc* d, int64_t p, int64_t q) {
@@ -45,6 +45,7 @@ Geom make_geom(const nott_conv2d_desc* d, int64_t p, int64_t q) {
     g.fd_w = FastDiv((uint32_t)d->w);
     g.fd_sh = FastDiv((uint32_t)d->stride_h);
     g.fd_sw = FastDiv((uint32_t)d->stride_w);
+    g.fd_c = FastDiv((uint32_t)d->c);
     return g;
 }
 
@@ -388,8 +389,7 @@ __global__ __launch_bounds__(256) void col2im_kernel(const T* __restrict__ dcol,
     uint32_t nc, hw, h, w, n, c;
     g.fd_hw.divmod((uint32_t)i, nc, hw);
     g.fd_w.divmod(hw, h, w);
-    n = nc / (uint32_t)g.c;
-    c = nc - n * (uint32_t)g.c;
+    g.fd_c.divmod(nc, n, c);
     float acc = 0.f;
     for (int32_t r = 0; r < g.r; ++r) {
         const int32_t ph = (int32_t)h + g.ph - r * g.dh;
@@ -446,6 +446,13 @@ struct Carve {
     }
 };
 
+// col[CRSp][NPQ]: consecutive lanes take consecutive columns (coalesced
+// gathers from x), each thread kColRows rows.
+void launch_im2col(nott_ctx ctx, const bf16_t* x, const Geom& g, int64_t CRS, int64_t CRSp, int64_t NPQ, bf16_t* col) {
+    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(NPQ, 256), (unsigned)(CRSp / kColRows)), dim3(256),
+                       0, ctx->stream, x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+}
+
 int col_fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const bf16_t* x, const bf16_t* w,
             const float* b, bf16_t* y) {
     const Geom g = make_geom(d, p, q);
@@ -459,8 +466,7 @@ int col_fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const
     bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
     hipLaunchKernelGGL(pack_w_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * CRSp, 256)), dim3(256), 0, ctx->stream, w,
                        (int32_t)d->k, (int32_t)CRS, (int32_t)CRSp, wp);
-    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(NPQ, 256), (unsigned)(CRSp / kColRows)), dim3(256),
-                       0, ctx->stream, x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+    launch_im2col(ctx, x, g, CRS, CRSp, NPQ, col);
     ColFwdStore<bf16_t> ep{y, b, g, NPQ};
     return fast::run<false, true>(ctx, wp, CRSp, col, NPQ, ep, d->k, NPQ, CRSp, 0,
                                   reinterpret_cast<float*>(ws + o_part));
@@ -479,8 +485,7 @@ int col_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, con
     bf16_t* col = reinterpret_cast<bf16_t*>(ws + o_col);
     hipLaunchKernelGGL(to_kn_kernel<bf16_t>, dim3((unsigned)ceil_div(d->k * (NPQ / 8), 256)), dim3(256), 0, ctx->stream,
                        dy, g, (int32_t)NPQ, (int)((p * q) % 8 == 0 && ((uintptr_t)dy % 16) == 0), dyt);
-    hipLaunchKernelGGL(im2col_kernel<bf16_t>, dim3((unsigned)ceil_div(NPQ, 256), (unsigned)(CRSp / kColRows)), dim3(256),
-                       0, ctx->stream, x, g, (int32_t)CRS, (int32_t)CRSp, (int32_t)NPQ, col);
+    launch_im2col(ctx, x, g, CRS, CRSp, NPQ, col);
     WgradStore ep{dw, d->k, CRS, accumulate};
     return fast::run<false, false>(ctx, dyt, NPQ, col, NPQ, ep, d->k, CRSp, NPQ, 0,
                                    reinterpret_cast<float*>(ws + o_part));
