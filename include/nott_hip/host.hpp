@@ -563,9 +563,54 @@ TORCH_MODULE(BatchNorm2d);
 
 inline Tensor relu(const Tensor& x) { return ReluFn::apply(x); }
 
+// Writes `m` in the archive layout torch::nn::Module::save produces (its own
+// parameters, then buffers, then one child archive per submodule), with every
+// tensor copied to the host first, so a CPU model built from the reference's
+// descriptors loads it directly.  Nott's Model::save writes the same archive
+// as parameters.binary (src/core.hpp:2131-2135) and Model::load reads it back
+// by the registration keys (`conv2d_0.weight`, `fc_5.bias`, ...,
+// src/core.hpp:2188-2236).
+inline void save_module_host(const torch::nn::Module& m, torch::serialize::OutputArchive& ar) {
+    for (const auto& p : m.named_parameters(/*recurse=*/false)) ar.write(p.key(), p.value().detach().cpu());
+    for (const auto& b : m.named_buffers(/*recurse=*/false))
+        if (b.value().defined()) ar.write(b.key(), b.value().detach().cpu(), /*is_buffer=*/true);
+    for (const auto& c : m.named_children()) {
+        torch::serialize::OutputArchive child(ar.compilation_unit());
+        save_module_host(*c.value(), child);
+        ar.write(c.key(), child);
+    }
+}
+inline void save_parameters(const torch::nn::Module& m, const std::string& path) {
+    torch::serialize::OutputArchive ar;
+    save_module_host(m, ar);
+    ar.save_to(path);
+}
+
 inline Tensor max_pool2d(const Tensor& x, int64_t k, int64_t stride, int64_t pad = 0, bool ceil_mode = false) {
     return MaxPool2dFn::apply(x, std::vector<int64_t>{k, k, stride, stride, pad, pad, 1, 1, ceil_mode ? 1 : 0});
 }
+
+// Parameter-less layers as modules, so that a model registers every layer of
+// its descriptor list under Nott's `<kind>_<index>` key (pooling.hpp:132-149,
+// flatten.hpp:19-41) and its checkpoint archive has the same child entries.
+class MaxPool2dImpl : public torch::nn::Module {
+public:
+    MaxPool2dImpl(int64_t k, int64_t stride, int64_t pad = 0, bool ceil_mode = false)
+        : k_(k), stride_(stride), pad_(pad), ceil_(ceil_mode) {}
+    Tensor forward(const Tensor& x) { return max_pool2d(x, k_, stride_, pad_, ceil_); }
+private:
+    int64_t k_, stride_, pad_;
+    bool ceil_;
+};
+TORCH_MODULE(MaxPool2d);
+class FlattenImpl : public torch::nn::Module {
+public:
+    // Nott's Flatten wraps a torch::nn::Flatten registered as "flatten"
+    // (flatten.hpp:34): an empty child entry in the archive.
+    FlattenImpl() { register_module("flatten", std::make_shared<torch::nn::Module>()); }
+    Tensor forward(const Tensor& x) { return x.flatten(1); }
+};
+TORCH_MODULE(Flatten);
 
 inline Tensor cross_entropy(const Tensor& logits, const Tensor& labels, double label_smoothing = 0.0) {
     return CrossEntropyFn::apply(logits, labels, label_smoothing);

@@ -575,6 +575,23 @@ int ref_mha(int64_t b, int64_t t, int64_t e, int64_t heads, int causal, int with
     });
 }
 
+// Loads a parameters.binary archive (torch::nn::Module::save layout, keys by
+// Nott's registration names) into the configs[0] model built from the
+// reference's descriptors and runs its forward on x[batch,1,28,28]; logits
+// [batch,10].  Checks that a checkpoint written by another implementation
+// loads into the reference (core.hpp:2188-2236 reads the same archive).
+int ref_small_cnn_forward_archive(const char* path, int64_t batch, const float* x, float* logits) {
+    return guarded([&] {
+        SmallCnnRef net;
+        torch::serialize::InputArchive ar;
+        ar.load_from(std::string(path));
+        net.c.owner.load(ar);
+        torch::NoGradGuard ng;
+        auto y = net.forward(in(x, {batch, 1, 28, 28}));
+        out(y, logits);
+    });
+}
+
 // Times `iters` full fp32 training steps on the CPU (forward, CE mean,
 // backward, Adam (model 0, configs[0]) or AdamW (model 1, configs[4]) step,
 // zero_grad) at the given batch; seconds per step in *sec.  Inputs

@@ -326,6 +326,14 @@ class Ref:
         self._ok(self.lib.ref_adamw_time(i64(n), C.c_int(iters), C.byref(sec)))
         return sec.value
 
+    def small_cnn_forward_archive(self, path: str, x):
+        """configs[0] logits of the reference-built model after loading the
+        parameters.binary archive at `path`."""
+        x = f32(x)
+        logits = np.empty((x.shape[0], 10), np.float32)
+        self._ok(self.lib.ref_small_cnn_forward_archive(C.c_char_p(path.encode()), i64(x.shape[0]), _p(x), _p(logits)))
+        return logits
+
     def train_step_time(self, model: str, batch: int, iters: int) -> float:
         """Seconds per fp32 CPU training step of "small_cnn" or
         "resnet18" built from the reference's layer descriptors."""

@@ -247,3 +247,23 @@ def test_graph_step_matches_eager(host_mod, model):
     torch.cuda.synchronize()
     for k in pe:
         assert torch.equal(pe[k], pg[k]), k
+
+
+def test_checkpoint_loads_into_reference(host_mod, oracle, tmp_path):
+    """parameters.binary written by the HIP trainer (torch::nn::Module::save
+    layout, Nott's registration keys) loads into the configs[0] model built
+    from the reference's own layer descriptors, whose CPU forward then
+    matches the GPU forward (fp32)."""
+    from oracle_lib import Ref
+    if not Ref.available():
+        pytest.skip("oracle/_ref not built")
+    tr = host_mod.SmallCNNTrainer(0, 21, 1e-3)
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.rand((8, 1, 28, 28), generator=gen, device="cuda")
+    y = torch.randint(0, 10, (8,), generator=gen, device="cuda")
+    tr.step(x, y)
+    path = str(tmp_path / "parameters.binary")
+    tr.save(path)
+    got = tr.forward(x).float().cpu().numpy()
+    want = Ref().small_cnn_forward_archive(path, x.cpu().numpy())
+    check(got, want, "f32", "logits after checkpoint round trip")

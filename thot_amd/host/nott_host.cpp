@@ -21,17 +21,23 @@ namespace {
 // ------------------------------------------------------------- configs[0]
 struct SmallCNNImpl : torch::nn::Module {
     NH::Conv2d conv0{nullptr}, conv1{nullptr};
+    NH::MaxPool2d pool0{nullptr}, pool1{nullptr};
+    NH::Flatten flat{nullptr};
     NH::Linear fc0{nullptr}, fc1{nullptr};
     SmallCNNImpl() {
+        // every layer under its Nott registration key (<kind>_<index>)
         conv0 = register_module("conv2d_0", NH::Conv2d(NH::Conv2dOptions{1, 32, {3, 3}, {1, 1}, {1, 1}}));
+        pool0 = register_module("maxpool2d_1", NH::MaxPool2d(2, 2));
         conv1 = register_module("conv2d_2", NH::Conv2d(NH::Conv2dOptions{32, 64, {3, 3}, {1, 1}, {1, 1}}));
+        pool1 = register_module("maxpool2d_3", NH::MaxPool2d(2, 2));
+        flat = register_module("flatten_4", NH::Flatten());
         fc0 = register_module("fc_5", NH::Linear(3136, 128));
         fc1 = register_module("fc_6", NH::Linear(128, 10));
     }
     Tensor forward(Tensor x) {
-        x = NH::max_pool2d(NH::relu(conv0(x)), 2, 2);   // Conv + ReLU, MaxPool2
-        x = NH::max_pool2d(NH::relu(conv1(x)), 2, 2);
-        x = x.flatten(1);                               // Flatten (a view)
+        x = pool0(NH::relu(conv0(x)));   // Conv + ReLU, MaxPool2
+        x = pool1(NH::relu(conv1(x)));
+        x = flat(x);                     // Flatten (a view)
         x = NH::relu(fc0(x));
         return fc1(x);
     }
@@ -198,6 +204,8 @@ struct Trainer {
         }
         if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("capture: device synchronize failed");
     }
+    // parameters.binary in Nott's archive layout (src/core.hpp:2131-2135).
+    void save(const std::string& path) { NH::save_parameters(*model, path); }
     Tensor step_graph(const Tensor& x, const Tensor& y) {
         if (!graph) throw std::logic_error("step_graph: call capture() first");
         gx.copy_(x);
@@ -261,6 +269,7 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("capture", &SmallT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
              py::call_guard<py::gil_scoped_release>())
         .def("step_graph", &SmallT::step_graph, py::call_guard<py::gil_scoped_release>())
+        .def("save", &SmallT::save, py::arg("path"))
         .def("forward_backward", &SmallT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", [](SmallT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
         .def("forward", &SmallT::forward, py::call_guard<py::gil_scoped_release>())
@@ -285,6 +294,7 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("capture", &ResT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
              py::call_guard<py::gil_scoped_release>())
         .def("step_graph", &ResT::step_graph, py::call_guard<py::gil_scoped_release>())
+        .def("save", &ResT::save, py::arg("path"))
         .def("forward_backward", &ResT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", [](ResT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
         .def("forward", &ResT::forward, py::call_guard<py::gil_scoped_release>())
