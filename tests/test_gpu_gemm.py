@@ -245,3 +245,43 @@ def test_conv_bwd_full_size_config(ops, oracle, dt):
     tol = 1e-6 if dt == "f32" else 2e-3
     assert abs(via_w - lhs) <= tol * scale, (via_w, lhs)
     assert abs(via_x - lhs) <= tol * scale, (via_x, lhs)
+    # every image of dx, and the forward, against torch's fp32 convolution
+    ref_dx = torch.nn.grad.conv2d_input((N, C, H, H), w.float(), dyf, padding=1)
+    check(host(dx), host(ref_dx), dt, "dx vs torch fp32")
+    b = torch.randn((K,), generator=gen, device="cuda")
+    yk = ops.conv2d_fwd(x, w, b, d)
+    check(host(yk), host(torch.nn.functional.conv2d(xf, w.float(), b, padding=1)), dt, "y vs torch fp32")
+
+
+# Large bf16 3x3 grids: several rounds of workgroups, pixel tiles across
+# image boundaries, row widths 8..64, 1..8 output-channel blocks.
+# (n, c, h, w, k)
+BIG3X3 = [
+    (42, 64, 56, 56, 64),
+    (33, 64, 32, 32, 256),     # tiles spanning images
+    (5, 64, 64, 64, 512),      # widest row, 8 channel blocks
+    (1030, 32, 8, 8, 256),     # 4 images per tile, one channel chunk
+    (130, 64, 16, 16, 256),
+    (34, 256, 32, 32, 64),     # dgrad: cin 64 -> 256 output channels
+]
+
+
+@pytest.mark.parametrize("case", BIG3X3)
+def test_conv3x3_large_grids(ops, case):
+    """bf16 forward and dgrad of 3x3 s1 p1 convs at sizes the CPU oracle is
+    too slow for, against torch's fp32 convolution on the same rounded inputs
+    (the same kernels meet the oracle at the small sizes above)."""
+    n, c, h, w_, k = case
+    d = ops.conv_desc((n, c, h, w_), (k, c, 3, 3), padding=(1, 1))
+    gen = torch.Generator(device="cuda").manual_seed(sum(case))
+    x = torch.randn((n, c, h, w_), generator=gen, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((k, c, 3, 3), generator=gen, device="cuda") / math.sqrt(c * 9)).to(torch.bfloat16)
+    b = torch.randn((k,), generator=gen, device="cuda")
+    dy = torch.randn((n, k, h, w_), generator=gen, device="cuda").to(torch.bfloat16)
+    y = ops.conv2d_fwd(x, w, b, d)
+    dx = ops.conv2d_bwd_data(dy, w, d)
+    torch.cuda.synchronize()
+    ref_y = torch.nn.functional.conv2d(x.float(), w.float(), b, padding=1)
+    ref_dx = torch.nn.grad.conv2d_input((n, c, h, w_), w.float(), dy.float(), padding=1)
+    check(host(y), host(ref_y), "bf16", "y vs torch fp32")
+    check(host(dx), host(ref_dx), "bf16", "dx vs torch fp32")

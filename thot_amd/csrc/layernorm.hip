@@ -62,6 +62,34 @@ __device__ __forceinline__ void load_row(const T* __restrict__ p, int64_t d, int
     }
 }
 
+// load_row split in two: the raw 16-byte loads, and their conversion to
+// floats (columns past d read column 0 and become zero).
+template <typename T>
+__host__ __device__ constexpr int raw_groups(int dpl) { return dpl / Pack16<T>::N > 0 ? dpl / Pack16<T>::N : 1; }
+template <typename T, int DPL, bool NT>
+__device__ __forceinline__ void load_raw(const T* __restrict__ p, int64_t d, int lane,
+                                         typename Pack16<T>::Raw (&raw)[raw_groups<T>(DPL)]) {
+    constexpr int G = Pack16<T>::N;
+#pragma unroll
+    for (int g = 0; g < DPL / G; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * G;
+        raw[g] = Pack16<T>::template raw<NT>(p + (c0 < d ? c0 : 0));
+    }
+}
+template <typename T, int DPL>
+__device__ __forceinline__ void unpack_row(const typename Pack16<T>::Raw (&raw)[raw_groups<T>(DPL)], int64_t d,
+                                           int lane, float (&v)[DPL]) {
+    constexpr int G = Pack16<T>::N;
+#pragma unroll
+    for (int g = 0; g < DPL / G; ++g) {
+        const int64_t c0 = ((int64_t)g * 64 + lane) * G;
+        float t[G];
+        Pack16<T>::unpack(raw[g], t);
+#pragma unroll
+        for (int e = 0; e < G; ++e) v[G * g + e] = c0 < d ? t[e] : 0.f;
+    }
+}
+
 template <typename T, int DPL, bool NT>
 __device__ __forceinline__ void store_row(T* __restrict__ p, int64_t d, int lane, const float (&v)[DPL]) {
     constexpr int G = Pack16<T>::N;
@@ -123,20 +151,37 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     for (int e = 0; e < DPL; ++e) dg[e] = db[e] = 0.f;
     const float inv_d = 1.f / (float)d;
     constexpr int kRowsInFlight = rows_in_flight((int)sizeof(T), DPL);
+    constexpr int NG = raw_groups<T>(DPL);
     const int64_t stride = (int64_t)gridDim.x * kWaves * kRowsInFlight;
-    for (int64_t r0 = ((int64_t)blockIdx.x * kWaves + wid) * kRowsInFlight; r0 < rows; r0 += stride) {
-        float xv[kRowsInFlight][DPL], gv[kRowsInFlight][DPL];
-        float mu[kRowsInFlight], rs[kRowsInFlight];
+    // The next group of rows is loaded (raw) while the current one is
+    // reduced and stored: two groups' loads per wave stay in flight.
+    typename Pack16<T>::Raw rx[kRowsInFlight][NG], rd[kRowsInFlight][NG];
+    float nmu[kRowsInFlight], nrs[kRowsInFlight];
+    auto fetch = [&](int64_t r0) {
 #pragma unroll
         for (int i = 0; i < kRowsInFlight; ++i) {
             // Rows past the end re-read the last row (unconditional loads keep
             // every row's loads in flight together); they are not stored.
             const int64_t r = r0 + i < rows ? r0 + i : rows - 1;
-            load_row<T, DPL, true>(x + r * d, d, lane, xv[i]);
-            load_row<T, DPL, true>(dy + r * d, d, lane, gv[i]);
-            mu[i] = mean[r];
-            rs[i] = rstd[r];
+            load_raw<T, DPL, true>(x + r * d, d, lane, rx[i]);
+            load_raw<T, DPL, true>(dy + r * d, d, lane, rd[i]);
+            nmu[i] = mean[r];
+            nrs[i] = rstd[r];
         }
+    };
+    const int64_t first = ((int64_t)blockIdx.x * kWaves + wid) * kRowsInFlight;
+    if (first < rows) fetch(first);
+    for (int64_t r0 = first; r0 < rows; r0 += stride) {
+        float xv[kRowsInFlight][DPL], gv[kRowsInFlight][DPL];
+        float mu[kRowsInFlight], rs[kRowsInFlight];
+#pragma unroll
+        for (int i = 0; i < kRowsInFlight; ++i) {
+            unpack_row<T, DPL>(rx[i], d, lane, xv[i]);
+            unpack_row<T, DPL>(rd[i], d, lane, gv[i]);
+            mu[i] = nmu[i];
+            rs[i] = nrs[i];
+        }
+        if (r0 + stride < rows) fetch(r0 + stride);
 #pragma unroll
         for (int i = 0; i < kRowsInFlight; ++i) {
             const int64_t r = r0 + i;
@@ -171,13 +216,61 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
         }
     }
     __syncthreads();
+    // Partial layout [which][16-column group][block][16]: the reduction reads
+    // each group's partials as one contiguous run.
+    const int64_t ngroups = (d + 15) / 16;
     for (int64_t j = threadIdx.x; j < 2 * d; j += kThreads) {
         const int which = j >= d;
         const int64_t col = j - which * d;
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) s += lds[(w * 2 + which) * d + col];
-        partial[((int64_t)blockIdx.x * 2 + which) * d + col] = s;
+        partial[((which * ngroups + col / 16) * gridDim.x + blockIdx.x) * 16 + col % 16] = s;
+    }
+}
+
+// dgamma / dbeta from ln_bwd_kernel's grouped partials.  One wave per
+// 16-column group of one output: lane = (block row b = lane / 4 mod 16,
+// column quad lane % 4), 16-byte loads, kGroupUnroll of them in flight, so
+// each load instruction reads 1 KB of consecutive partials.  Each lane adds
+// its blocks in order, then the 16 lanes of a quad combine by a fixed
+// butterfly: the summation order does not depend on timing.
+constexpr int kGroupUnroll = 16;
+__global__ __launch_bounds__(64) void col_reduce_grouped_kernel(const float* __restrict__ partial, int64_t nparts,
+                                                                int64_t d, float* __restrict__ dgamma,
+                                                                float* __restrict__ dbeta, int accumulate) {
+    const int lane = threadIdx.x;
+    const int64_t ngroups = (d + 15) / 16;
+    const int64_t gi = blockIdx.x;                  // which · ngroups + group
+    const int which = gi >= ngroups;
+    const int64_t cg = gi - which * ngroups;
+    const int q = lane & 3, br = lane >> 2;
+    const f32x4* src = reinterpret_cast<const f32x4*>(partial + gi * nparts * 16) + q;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t b0 = 0; b0 < nparts; b0 += 16 * kGroupUnroll) {
+        f32x4 t[kGroupUnroll];
+#pragma unroll
+        for (int u = 0; u < kGroupUnroll; ++u) {
+            const int64_t b = b0 + u * 16 + br;
+            t[u] = b < nparts ? src[b * 4] : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < kGroupUnroll; ++u) s += t[u];
+    }
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+        s.x += __shfl_xor(s.x, off);
+        s.y += __shfl_xor(s.y, off);
+        s.z += __shfl_xor(s.z, off);
+        s.w += __shfl_xor(s.w, off);
+    }
+    float* out = which ? dbeta : dgamma;
+    if (br == 0 && out) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t col = cg * 16 + q * 4 + e;
+            if (col < d) out[col] = accumulate ? out[col] + s[e] : s[e];
+        }
     }
 }
 
@@ -332,7 +425,8 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
     } else {
         nparts = rows;
     }
-    float* partial = static_cast<float*>(nott::workspace(ctx, sizeof(float) * 2 * (size_t)d * (size_t)nparts));
+    const size_t pcols = vec ? (size_t)nott::ceil_div(d, 16) * 16 : (size_t)d;
+    float* partial = static_cast<float*>(nott::workspace(ctx, sizeof(float) * 2 * pcols * (size_t)nparts));
     if (!partial) return NOTT_ERR_ALLOC;
     const dim3 grid((unsigned)nparts);
     const size_t lds = sizeof(float) * kWaves * 2 * (size_t)d;
@@ -346,7 +440,10 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
         hipLaunchKernelGGL((ln_bwd_kernel<T, 32>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else
         hipLaunchKernelGGL(ln_bwd_generic<T>, grid, dim3(kThreads), 0, ctx->stream, xx, dd, mean, rstd, gg, out, partial, d);
-    if (dgamma || dbeta)
+    if ((dgamma || dbeta) && vec)
+        hipLaunchKernelGGL(col_reduce_grouped_kernel, dim3((unsigned)(2 * nott::ceil_div(d, 16))), dim3(64), 0,
+                           ctx->stream, partial, nparts, d, dgamma, dbeta, accumulate);
+    else if (dgamma || dbeta)
         hipLaunchKernelGGL(col_reduce_kernel, dim3((unsigned)nott::ceil_div(d, 64), 2), dim3(kReduceThreads), 0, ctx->stream,
                            partial, nparts, d, dgamma, dbeta, accumulate);
     return nott::launch_status(ctx, "layernorm_bwd");
