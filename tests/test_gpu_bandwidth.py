@@ -262,7 +262,9 @@ def test_layernorm_full_size_invariants(ops):
 # ---------------------------------------------------------- cross-entropy
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("n,c,eps,ignore", [(64, 10, 0.0, False), (64, 1000, 0.0, False), (33, 1001, 0.1, True),
-                                            (256, 32000, 0.0, False), (8, 40000, 0.05, True), (5, 7, 0.0, False)])
+                                            (256, 32000, 0.0, False), (8, 40000, 0.05, True), (5, 7, 0.0, False),
+                                            # more rows than resident workgroups: each takes several rows
+                                            (2000, 5000, 0.1, True), (600, 32000, 0.0, True), (5000, 1000, 0.0, True)])
 def test_softmax_xent(ops, oracle, dt, n, c, eps, ignore):
     g = rng(n + c)
     z = host_input(g.standard_normal((n, c)) * 2.0, dt)

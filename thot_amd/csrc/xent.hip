@@ -11,6 +11,8 @@
 // Each row lives in registers of one workgroup: one HBM read, one write.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace {
 
 constexpr int64_t kIgnoreIndex = -100;
@@ -64,55 +66,23 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
     b = tb;
 }
 
-// One workgroup of NT threads per row; each thread holds EPT elements of the
-// row in registers.  VEC: 16-byte groups of G = 4 (fp32) or 8 (bf16)
-// elements, strided by NT·G, loaded unconditionally (past-the-end groups
-// re-read group 0 and count as −inf) so all of a thread's loads are in flight
-// together; otherwise single elements strided by NT.
+// Row body: v holds this thread's EPT elements of row `row` (element e of
+// group g is column (g·NT + tid)·G + e; −inf past the end).  Writes the
+// gradient row and the row's loss.  Every thread calls it (block reductions).
 template <typename T, int NT, int EPT, bool VEC>
-__global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logits, const int64_t* __restrict__ labels,
-                                                      int64_t c, float smoothing, float grad_scale,
-                                                      const int* __restrict__ nvalid, T* __restrict__ dlogits,
-                                                      float* __restrict__ row_loss) {
+__device__ __forceinline__ void xent_row_body(const float (&v)[EPT], int64_t row, int64_t y, const T* __restrict__ z,
+                                              int64_t c, float smoothing, float grad_scale, int nv,
+                                              T* __restrict__ dz, float* __restrict__ row_loss, float* red) {
     constexpr int NWAVES = NT / 64;
     constexpr int G = VEC ? Pack16<T>::N : 1;
     constexpr int NG = EPT / G;
-    __shared__ float red[2 * NWAVES];
-    const int64_t row = blockIdx.x;
-    const T* z = logits + row * c;
-    T* dz = dlogits + row * c;
-    const int64_t y = labels[row];
-    const bool valid = (y >= 0 && y < c);
-
-    float v[EPT];
-    if constexpr (VEC) {
-        typename Pack16<T>::Raw raw[NG];
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
-            raw[g] = Pack16<T>::template raw<true>(z + (j0 < c ? j0 : 0));
-        }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
-            float t[G];
-            Pack16<T>::unpack(raw[g], t);
-#pragma unroll
-            for (int e = 0; e < G; ++e) v[g * G + e] = j0 < c ? t[e] : -INFINITY;
-        }
-    } else {
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            const int64_t j0 = (int64_t)g * NT + threadIdx.x;
-            v[g] = j0 < c ? Io<T>::ld(z, j0) : -INFINITY;
-        }
-    }
-    if (!valid) {
+    const int ci = (int)c;
+    if (!(y >= 0 && y < c)) {
         // Ignored (or out-of-range) row: zero gradient, no loss.
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
-            if (j0 >= c) continue;
+            const int j0 = (g * NT + (int)threadIdx.x) * G;
+            if (j0 >= ci) continue;
             if constexpr (VEC) {
                 float t[G];
 #pragma unroll
@@ -137,17 +107,18 @@ __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logi
     }
     block_sum2<NWAVES>(se, sz, red);
     const float lse = mx + __logf(se);
-    const float scale = grad_scale / (float)(*nvalid);
+    const float scale = grad_scale / (float)nv;
     const float off = smoothing / (float)c;
     const float hit = 1.f - smoothing;
+    const int yi = (int)y;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-        const int64_t j0 = ((int64_t)g * NT + threadIdx.x) * G;
-        if (j0 >= c) continue;
+        const int j0 = (g * NT + (int)threadIdx.x) * G;
+        if (j0 >= ci) continue;
         float t[G];
 #pragma unroll
         for (int e = 0; e < G; ++e)
-            t[e] = scale * (__expf(v[g * G + e] - lse) - off - (j0 + e == y ? hit : 0.f));
+            t[e] = scale * (__expf(v[g * G + e] - lse) - off - (j0 + e == yi ? hit : 0.f));
         if constexpr (VEC) Pack16<T>::template st<true>(dz + j0, t);
         else Io<T>::st(dz, j0, t[0]);
     }
@@ -155,6 +126,71 @@ __global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logi
         const float zy = Io<T>::ld(z, y);
         row_loss[row] = hit * (lse - zy) + off * ((float)c * lse - sz);
     }
+}
+
+// Vector path: 16-byte groups of G = 4 (fp32) or 8 (bf16) elements, strided
+// by NT·G, loaded unconditionally (past-the-end groups re-read group 0 and
+// count as −inf) so all of a thread's loads are in flight together.  The
+// grid is persistent (rows blockIdx.x, + gridDim.x, ...) and the next row's
+// loads are issued before the current row is reduced and written, so a CU's
+// loads stay in flight through the block reductions and the stores.
+template <typename T, int NT, int EPT>
+__global__ __launch_bounds__(NT) void xent_rows_vec_kernel(const T* __restrict__ logits,
+                                                           const int64_t* __restrict__ labels, int64_t n, int64_t c,
+                                                           float smoothing, float grad_scale,
+                                                           const int* __restrict__ nvalid, T* __restrict__ dlogits,
+                                                           float* __restrict__ row_loss) {
+    constexpr int G = Pack16<T>::N;
+    constexpr int NG = EPT / G;
+    __shared__ float red[2 * (NT / 64)];
+    typename Pack16<T>::Raw raw[NG];
+    int64_t ny = 0;
+    auto fetch = [&](int64_t row) {
+        const T* z = logits + row * c;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int j0 = (g * NT + (int)threadIdx.x) * G;
+            raw[g] = Pack16<T>::template raw<true>(z + (j0 < (int)c ? j0 : 0));
+        }
+        ny = labels[row];
+    };
+    const int nv = *nvalid;
+    if ((int64_t)blockIdx.x < n) fetch(blockIdx.x);
+    for (int64_t row = blockIdx.x; row < n; row += gridDim.x) {
+        float v[EPT];
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int j0 = (g * NT + (int)threadIdx.x) * G;
+            float t[G];
+            Pack16<T>::unpack(raw[g], t);
+#pragma unroll
+            for (int e = 0; e < G; ++e) v[g * G + e] = j0 < (int)c ? t[e] : -INFINITY;
+        }
+        const int64_t y = ny;
+        if (row + gridDim.x < n) fetch(row + gridDim.x);
+        xent_row_body<T, NT, EPT, true>(v, row, y, logits + row * c, c, smoothing, grad_scale, nv,
+                                        dlogits + row * c, row_loss, red);
+    }
+}
+
+// Element path (unaligned rows or c not a multiple of G): one workgroup per
+// row, single elements strided by NT.
+template <typename T, int NT, int EPT>
+__global__ __launch_bounds__(NT) void xent_row_kernel(const T* __restrict__ logits, const int64_t* __restrict__ labels,
+                                                      int64_t c, float smoothing, float grad_scale,
+                                                      const int* __restrict__ nvalid, T* __restrict__ dlogits,
+                                                      float* __restrict__ row_loss) {
+    __shared__ float red[2 * (NT / 64)];
+    const int64_t row = blockIdx.x;
+    const T* z = logits + row * c;
+    float v[EPT];
+#pragma unroll
+    for (int g = 0; g < EPT; ++g) {
+        const int64_t j0 = (int64_t)g * NT + threadIdx.x;
+        v[g] = j0 < c ? Io<T>::ld(z, j0) : -INFINITY;
+    }
+    xent_row_body<T, NT, EPT, false>(v, row, labels[row], z, c, smoothing, grad_scale, *nvalid, dlogits + row * c,
+                                     row_loss, red);
 }
 
 // Rows too long for registers: three passes over the row (the re-reads are
@@ -206,8 +242,23 @@ __global__ void xent_nan_kernel(float* __restrict__ loss) { *loss = __builtin_na
 template <typename T, int NT, int EPT, bool VEC>
 void launch_rows(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int64_t* labels, float eps,
                  float scale, const int* nvalid, void* dl, float* row_loss) {
-    hipLaunchKernelGGL((xent_row_kernel<T, NT, EPT, VEC>), dim3((unsigned)n), dim3(NT), 0, ctx->stream,
-                       static_cast<const T*>(logits), labels, c, eps, scale, nvalid, static_cast<T*>(dl), row_loss);
+    if constexpr (VEC) {
+        // Persistent grid: as many workgroups as are resident at once, at
+        // most one per row.
+        static int per_cu = 0;
+        if (per_cu == 0 &&
+            (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, xent_rows_vec_kernel<T, NT, EPT>, NT, 0) !=
+                 hipSuccess ||
+             per_cu < 1))
+            per_cu = 1;
+        const int64_t grid = std::min<int64_t>(n, (int64_t)ctx->num_cu * per_cu);
+        hipLaunchKernelGGL((xent_rows_vec_kernel<T, NT, EPT>), dim3((unsigned)grid), dim3(NT), 0, ctx->stream,
+                           static_cast<const T*>(logits), labels, n, c, eps, scale, nvalid, static_cast<T*>(dl),
+                           row_loss);
+    } else {
+        hipLaunchKernelGGL((xent_row_kernel<T, NT, EPT>), dim3((unsigned)n), dim3(NT), 0, ctx->stream,
+                           static_cast<const T*>(logits), labels, c, eps, scale, nvalid, static_cast<T*>(dl), row_loss);
+    }
 }
 
 template <typename T>
@@ -218,8 +269,8 @@ void dispatch(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int6
         launch_rows<T, 64, 16, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (vec && c <= 256 * 32)
         launch_rows<T, 256, 32, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
-    else if (vec && c <= 512 * 64)
-        launch_rows<T, 512, 64, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+    else if (vec && c <= 1024 * 32)
+        launch_rows<T, 1024, 32, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (c <= 64 * 16)
         launch_rows<T, 64, 16, false>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (c <= 512 * 32)
