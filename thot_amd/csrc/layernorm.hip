@@ -229,29 +229,31 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     }
 }
 
-// dgamma / dbeta from ln_bwd_kernel's grouped partials.  One wave per
-// 16-column group of one output: lane = (block row b = lane / 4 mod 16,
-// column quad lane % 4), 16-byte loads, kGroupUnroll of them in flight, so
-// each load instruction reads 1 KB of consecutive partials.  Each lane adds
-// its blocks in order, then the 16 lanes of a quad combine by a fixed
-// butterfly: the summation order does not depend on timing.
-constexpr int kGroupUnroll = 16;
-__global__ __launch_bounds__(64) void col_reduce_grouped_kernel(const float* __restrict__ partial, int64_t nparts,
-                                                                int64_t d, float* __restrict__ dgamma,
-                                                                float* __restrict__ dbeta, int accumulate) {
-    const int lane = threadIdx.x;
+// dgamma / dbeta from ln_bwd_kernel's grouped partials.  One 4-wave block
+// per 16-column group of one output: thread = (block row b = tid / 4 mod 64,
+// column quad tid % 4), 16-byte loads, kGroupUnroll of them in flight (512
+// partial rows in one round), so each wave load reads 1 KB of consecutive
+// partials.  Each thread adds its rows in order, the 16 row slots of a wave
+// combine by a fixed butterfly and the 4 waves in wave order: the summation
+// order does not depend on timing.
+constexpr int kGroupUnroll = 8;
+__global__ __launch_bounds__(256) void col_reduce_grouped_kernel(const float* __restrict__ partial, int64_t nparts,
+                                                                 int64_t d, float* __restrict__ dgamma,
+                                                                 float* __restrict__ dbeta, int accumulate) {
+    __shared__ f32x4 red[4][4];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int64_t ngroups = (d + 15) / 16;
     const int64_t gi = blockIdx.x;                  // which · ngroups + group
     const int which = gi >= ngroups;
     const int64_t cg = gi - which * ngroups;
-    const int q = lane & 3, br = lane >> 2;
+    const int q = tid & 3, br = tid >> 2;
     const f32x4* src = reinterpret_cast<const f32x4*>(partial + gi * nparts * 16) + q;
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t b0 = 0; b0 < nparts; b0 += 16 * kGroupUnroll) {
+    for (int64_t b0 = 0; b0 < nparts; b0 += 64 * kGroupUnroll) {
         f32x4 t[kGroupUnroll];
 #pragma unroll
         for (int u = 0; u < kGroupUnroll; ++u) {
-            const int64_t b = b0 + u * 16 + br;
+            const int64_t b = b0 + u * 64 + br;
             t[u] = b < nparts ? src[b * 4] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
@@ -264,8 +266,12 @@ __global__ __launch_bounds__(64) void col_reduce_grouped_kernel(const float* __r
         s.z += __shfl_xor(s.z, off);
         s.w += __shfl_xor(s.w, off);
     }
+    if (lane < 4) red[wid][lane] = s;
+    __syncthreads();
+    if (tid >= 4) return;
+    s = red[0][q] + red[1][q] + red[2][q] + red[3][q];
     float* out = which ? dbeta : dgamma;
-    if (br == 0 && out) {
+    if (out) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int64_t col = cg * 16 + q * 4 + e;
@@ -441,7 +447,7 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
     else
         hipLaunchKernelGGL(ln_bwd_generic<T>, grid, dim3(kThreads), 0, ctx->stream, xx, dd, mean, rstd, gg, out, partial, d);
     if ((dgamma || dbeta) && vec)
-        hipLaunchKernelGGL(col_reduce_grouped_kernel, dim3((unsigned)(2 * nott::ceil_div(d, 16))), dim3(64), 0,
+        hipLaunchKernelGGL(col_reduce_grouped_kernel, dim3((unsigned)(2 * nott::ceil_div(d, 16))), dim3(256), 0,
                            ctx->stream, partial, nparts, d, dgamma, dbeta, accumulate);
     else if (dgamma || dbeta)
         hipLaunchKernelGGL(col_reduce_kernel, dim3((unsigned)nott::ceil_div(d, 64), 2), dim3(kReduceThreads), 0, ctx->stream,
