@@ -120,6 +120,10 @@ POOLS = [
     (2, 3, 17, 23, (3, 3), (2, 2), (1, 1), (1, 1), True),     # row bands cut mid-window, ceil mode
     (1, 2, 40, 33, (5, 4), (3, 2), (2, 1), (1, 2), False),    # dilation with padding
     (3, 5, 70, 19, (3, 3), (1, 1), (1, 1), (1, 1), False),    # stride 1: several bands per plane
+    # rows of whole 4-element groups (the 4-wide path)
+    (2, 3, 24, 16, (3, 3), (1, 1), (1, 1), (1, 1), False),
+    (3, 4, 16, 16, (2, 2), (2, 2), (0, 0), (1, 1), False),
+    (2, 5, 40, 64, (3, 3), (2, 2), (1, 1), (1, 1), False),
 ]
 
 

@@ -12,9 +12,12 @@
 //             the fp32 sum order equals the reference's scatter order.
 #include "common.hpp"
 
+#include <initializer_list>
+
 namespace {
 
 constexpr int kThreads = 256;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 struct PoolGeom {
     int64_t h, w, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
@@ -147,20 +150,33 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* 
 // float), then every output scans its window from LDS in the same order and
 // with the same NaN / first-maximum rule as the untiled kernel.
 constexpr int kPoolRows = 8;
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                                      int64_t* __restrict__ argmax, PoolGeom32 g) {
+    // VEC (w and ow multiples of 4, aligned buffers): 4 consecutive elements
+    // per thread for the staging loads and for the y / argmax stores.
+    constexpr int V = VEC ? 4 : 1;
     extern __shared__ float rows[];
     const int32_t pl = blockIdx.y;
     const int32_t oh0 = blockIdx.x * kPoolRows, oh1 = min(oh0 + kPoolRows, g.oh);
     const int32_t ih_lo = max(0, oh0 * g.sh - g.ph);
     const int32_t ih_hi = min(g.h, (oh1 - 1) * g.sh - g.ph + (g.kh - 1) * g.dh + 1);   // exclusive
-    const T* xp = x + (int64_t)pl * g.h * g.w;
+    const T* xp = x + (int64_t)pl * g.h * g.w + (int64_t)ih_lo * g.w;
     const int32_t nin = (ih_hi - ih_lo) * g.w;
-    for (int32_t i = threadIdx.x; i < nin; i += kThreads) rows[i] = Io<T>::ld(xp, (int64_t)ih_lo * g.w + i);
+    if constexpr (VEC) {
+        for (int32_t i = threadIdx.x; i < nin / 4; i += kThreads)
+            reinterpret_cast<f32x4*>(rows)[i] = Vec4<T>::ld(xp + 4 * i);
+    } else {
+        for (int32_t i = threadIdx.x; i < nin; i += kThreads) rows[i] = Io<T>::ld(xp, i);
+    }
     __syncthreads();
     const int32_t nout = (oh1 - oh0) * g.ow;
-    for (int32_t j = threadIdx.x; j < nout; j += kThreads) {
+    for (int32_t j0 = threadIdx.x * V; j0 < nout; j0 += kThreads * V) {
+      f32x4 yv;
+      int64_t av[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const int32_t j = j0 + e;
         uint32_t ohl, owu;
         g.fd_ow.divmod((uint32_t)j, ohl, owu);
         const int32_t oh = oh0 + (int32_t)ohl, ow = (int32_t)owu;
@@ -179,9 +195,18 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
                     best = ih * g.w + iw;
                 }
             }
-        const int64_t o = ((int64_t)pl * g.oh + oh) * g.ow + ow;
-        Io<T>::st(y, o, bv);
-        argmax[o] = best;
+        yv[e] = bv;
+        av[e] = best;
+      }
+      const int64_t o = ((int64_t)pl * g.oh + oh0) * g.ow + j0;
+      if constexpr (VEC) {
+        Vec4<T>::st(y + o, yv);
+#pragma unroll
+        for (int e = 0; e < V; ++e) argmax[o + e] = av[e];
+      } else {
+        Io<T>::st(y, o, yv[0]);
+        argmax[o] = av[0];
+      }
     }
 }
 
@@ -190,10 +215,13 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
 // reaches the band in LDS, then each input gathers from the outputs that can
 // cover it, in the untiled kernel's order (oh, then ow, ascending): the same
 // sums, bit for bit, with each argmax read from HBM about once.
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64_t* __restrict__ argmax,
                                                                      const T* __restrict__ dy, T* __restrict__ dx,
                                                                      PoolGeom32 g, int32_t band_rows) {
+    // VEC (w and ow multiples of 4, aligned buffers): 4 consecutive elements
+    // per thread for the staging loads and for the dx stores.
+    constexpr int V = VEC ? 4 : 1;
     extern __shared__ char sm[];
     const int32_t pl = blockIdx.y;
     const int32_t ih_lo = blockIdx.x * band_rows, ih_hi = min(ih_lo + band_rows, g.h);
@@ -204,13 +232,28 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
     int32_t* code = reinterpret_cast<int32_t*>(sm);
     float* gv = reinterpret_cast<float*>(sm) + nout;
     const int64_t obase = (int64_t)pl * g.oh * g.ow + (int64_t)oh_lo * g.ow;
-    for (int32_t i = threadIdx.x; i < nout; i += kThreads) {
-        code[i] = (int32_t)argmax[obase + i];
-        gv[i] = Io<T>::ld(dy, obase + i);
+    if constexpr (VEC) {
+        for (int32_t i = threadIdx.x; i < nout / 4; i += kThreads) {
+            const f32x4 d4 = Vec4<T>::ld(dy + obase + 4 * i);
+            int32_t c4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c4[e] = (int32_t)argmax[obase + 4 * i + e];
+            reinterpret_cast<f32x4*>(gv)[i] = d4;
+            reinterpret_cast<i32x4*>(code)[i] = i32x4{c4[0], c4[1], c4[2], c4[3]};
+        }
+    } else {
+        for (int32_t i = threadIdx.x; i < nout; i += kThreads) {
+            code[i] = (int32_t)argmax[obase + i];
+            gv[i] = Io<T>::ld(dy, obase + i);
+        }
     }
     __syncthreads();
     const int32_t nin = (ih_hi - ih_lo) * g.w;
-    for (int32_t j = threadIdx.x; j < nin; j += kThreads) {
+    for (int32_t j0 = threadIdx.x * V; j0 < nin; j0 += kThreads * V) {
+      f32x4 out;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const int32_t j = j0 + e;
         uint32_t ihl, iwu;
         g.fd_w.divmod((uint32_t)j, ihl, iwu);
         const int32_t ih = ih_lo + (int32_t)ihl, iw = (int32_t)iwu;
@@ -227,8 +270,23 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
                 const int32_t o = (oh - oh_lo) * g.ow + ow;
                 if (code[o] == idx) acc += gv[o];
             }
-        Io<T>::st(dx, (int64_t)pl * g.h * g.w + idx, acc);
+        out[e] = acc;
+      }
+      const int64_t di = (int64_t)pl * g.h * g.w + (int64_t)ih_lo * g.w + j0;
+      if constexpr (VEC) Vec4<T>::st(dx + di, out);
+      else Io<T>::st(dx, di, out[0]);
     }
+}
+
+// The tiled kernels' 4-element path: image and output rows of whole 4-element
+// groups, and 4-element groups of the given buffers aligned (8 bytes bf16,
+// 16 bytes fp32).
+bool vec4_ok(const PoolGeom& g, nott_dtype dtype, std::initializer_list<const void*> ptrs) {
+    if (g.w % 4 != 0 || g.ow % 4 != 0) return false;
+    const uintptr_t al = dtype == NOTT_F32 ? 16 : 8;
+    for (const void* p : ptrs)
+        if ((uintptr_t)p % al != 0) return false;
+    return true;
 }
 
 // LDS bytes of the tiled kernels (0 when a band does not fit).
@@ -307,11 +365,18 @@ extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     if (fits32(planes, g) && flds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kPoolRows), (unsigned)planes);
-        if (dtype == NOTT_F32)
-            hipLaunchKernelGGL(maxpool_fwd_tiled_kernel<float>, tgrid, dim3(kThreads), flds, ctx->stream,
+        const bool vec = vec4_ok(g, dtype, {x, y});
+        if (dtype == NOTT_F32 && vec)
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), flds, ctx->stream,
                                static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
+        else if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, false>), tgrid, dim3(kThreads), flds, ctx->stream,
+                               static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
+        else if (vec)
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, true>), tgrid, dim3(kThreads), flds, ctx->stream,
+                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, g32);
         else
-            hipLaunchKernelGGL(maxpool_fwd_tiled_kernel<bf16_t>, tgrid, dim3(kThreads), flds, ctx->stream,
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, false>), tgrid, dim3(kThreads), flds, ctx->stream,
                                static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, g32);
     } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
@@ -347,12 +412,19 @@ extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     if (fits32(planes, g) && blds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.h, (int64_t)band_rows), (unsigned)planes);
-        if (dtype == NOTT_F32)
-            hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<float>, tgrid, dim3(kThreads), blds, ctx->stream, argmax,
-                               static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+        const bool vec = vec4_ok(g, dtype, {dy, dx});
+        if (dtype == NOTT_F32 && vec)
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+        else if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, false>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+        else if (vec)
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, true>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
         else
-            hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<bf16_t>, tgrid, dim3(kThreads), blds, ctx->stream, argmax,
-                               static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, false>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
     } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
         if (dtype == NOTT_F32)
