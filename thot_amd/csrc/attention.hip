@@ -781,6 +781,20 @@ extern "C" int nott_attention_bwd(nott_ctx ctx, const nott_attn_desc* d, nott_dt
     const int st = check(ctx, d, &p, (int)nott::dtype_size(dtype));
     if (st != NOTT_OK) return st;
     if (d->b * d->h == 0) return NOTT_OK;
+    if (d->t == 0 || d->s == 0) {
+        // No queries: dk = dv = 0 (sums over no rows); no keys: dq = 0.
+        nott::DeviceScope scope(ctx->device);
+        const int64_t es = (int64_t)nott::dtype_size(dtype), bh = d->b * d->h;
+        if (d->t == 0) {
+            NOTT_REQUIRE(ctx, dk && dv, "nott_attention_bwd: null buffer");
+            if (nott_zero(ctx, es * bh * d->s * d->dh, dk) != NOTT_OK) return NOTT_ERR_HIP;
+            if (nott_zero(ctx, es * bh * d->s * d->dh, dv) != NOTT_OK) return NOTT_ERR_HIP;
+        } else {
+            NOTT_REQUIRE(ctx, dq, "nott_attention_bwd: null buffer");
+            if (nott_zero(ctx, es * bh * d->t * d->dh, dq) != NOTT_OK) return NOTT_ERR_HIP;
+        }
+        return NOTT_OK;
+    }
     NOTT_REQUIRE(ctx, q && k && v && o && dO && lse && dq && dk && dv, "nott_attention_bwd: null buffer");
     if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dO))) p.vec = 0;
     nott::DeviceScope scope(ctx->device);
