@@ -50,12 +50,12 @@ METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HB
 TRAFFIC = {
     ("conv_bwd", "bf16", "dgrad"): 183.36e6,   # conv3x3_wprep + conv3x3_same
     ("conv_bwd", "bf16", "wgrad"): 230.21e6,   # conv3x3_wgrad + conv3x3_wgrad_reduce
-    ("ln_bwd", "f32", None): 210.96e6,         # ln_bwd_kernel + col_reduce_kernel
-    ("ln_bwd", "bf16", None): 109.79e6,
+    ("ln_bwd", "f32", None): 210.93e6,         # ln_bwd_kernel + col_reduce_grouped_kernel
+    ("ln_bwd", "bf16", None): 109.77e6,
     ("adamw", "f32", None): 2799.94e6,
     ("adamw", "bf16", None): 2200.00e6,
-    ("xent", "f32", None): 4207.84e6,          # xent_count_kernel + xent_row_kernel
-    ("xent", "bf16", None): 2101.75e6,
+    ("xent", "f32", None): 4199.32e6,          # xent_count_kernel + xent_rows_vec_kernel
+    ("xent", "bf16", None): 2101.43e6,
 }
 
 
