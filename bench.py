@@ -327,9 +327,12 @@ class MhaBwd(Workload):
     """causal multi-head attention backward, bf16, B=8, H=16,
     T=1024, dh=64, with the projection-weight gradients of the 1024->3x1024
     input and 1024->1024 output projections.  One step: output-projection
-    backward, head split of dO, attention backward, head merge of dq/dk/dv,
-    input-projection backward.  Work: 34.36 GFLOP causal core (dV, dP, dQ, dK
-    GEMMs) + 137.44 GFLOP projections."""
+    backward, attention backward, input-projection backward.  The attention
+    reads q, k, v as token-major views of the packed [B·T, 3·E] projection
+    output and dO as a view of the output projection's dX, and writes dq, dk,
+    dv into the packed [B·T, 3·E] gradient the input projection consumes, so
+    no head split or merge copies run.  Work: 34.36 GFLOP causal core (dV,
+    dP, dQ, dK GEMMs) + 137.44 GFLOP projections."""
     name = "mha_bwd"
     unit = "TFLOP/s"
     bound = "mfma"
@@ -347,12 +350,15 @@ class MhaBwd(Workload):
         self.x = torch.randn((B * T, E), generator=g, device="cuda").to(dt)
         self.w_in = (0.02 * torch.randn((3 * E, E), generator=g, device="cuda")).to(dt)
         self.w_out = (0.02 * torch.randn((E, E), generator=g, device="cuda")).to(dt)
-        self.d = ops.attn_desc(B, H, T, T, DH, True)
-        qkv = torch.randn((3, B, H, T, DH), generator=g, device="cuda").to(dt)
-        self.q, self.k, self.v = qkv[0].contiguous(), qkv[1].contiguous(), qkv[2].contiguous()
+        self.d = ops.attn_desc(B, H, T, T, DH, True, token_major=True, ld_qkv=3 * E)
+        qkv = torch.randn((B, T, 3 * E), generator=g, device="cuda").to(dt)
+        self.q, self.k, self.v = (qkv[:, :, i * E:(i + 1) * E].view(B, T, H, DH) for i in range(3))
+        self.qkv = qkv
         self.o, self.lse = ops.attention_fwd(self.q, self.k, self.v, self.d)
-        self.attn_out = self.o.permute(0, 2, 1, 3).reshape(B * T, E).contiguous()
+        self.attn_out = self.o.view(B * T, E)
         self.dy = torch.randn((B * T, E), generator=g, device="cuda").to(dt)
+        self.dqkv = torch.empty((B, T, 3 * E), dtype=dt, device="cuda")
+        self.dqkv_views = tuple(self.dqkv[:, :, i * E:(i + 1) * E].view(B, T, H, DH) for i in range(3))
         self.dw_in = torch.empty((3 * E, E), device="cuda")
         self.db_in = torch.empty((3 * E,), device="cuda")
         self.dw_out = torch.empty((E, E), device="cuda")
@@ -362,17 +368,16 @@ class MhaBwd(Workload):
         self.ev_a = [None, None]
 
     def step(self):
-        torch, ops = self.torch, self.ops
+        ops = self.ops
         B, H, T, DH = self.B, self.H, self.T, self.DH
         dattn, _, _ = ops.linear_bwd(self.dy, self.attn_out, self.w_out, dw=self.dw_out, db=self.db_out)
-        dO = dattn.view(B, T, H, DH).permute(0, 2, 1, 3).contiguous()
+        dO = dattn.view(B, T, H, DH)
         if self.ev_a[0] is not None:
             self.ev_a[0].record()
-        dq, dk, dv = ops.attention_bwd(self.q, self.k, self.v, self.o, dO, self.lse, self.d)
+        ops.attention_bwd(self.q, self.k, self.v, self.o, dO, self.lse, self.d, out=self.dqkv_views)
         if self.ev_a[1] is not None:
             self.ev_a[1].record()
-        dqkv = torch.stack((dq, dk, dv), 0).permute(1, 3, 0, 2, 4).reshape(B * T, 3 * H * DH)
-        ops.linear_bwd(dqkv, self.x, self.w_in, dw=self.dw_in, db=self.db_in)
+        ops.linear_bwd(self.dqkv.view(B * T, 3 * H * DH), self.x, self.w_in, dw=self.dw_in, db=self.db_in)
 
     def work_per_step(self):
         return self.core_flop + self.proj_flop

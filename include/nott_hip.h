@@ -203,13 +203,23 @@ int nott_softmax_xent_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c,
 /* ---- scaled dot-product attention -----------------------------------------
  * Replaces ScaledDotProductKernelImpl::forward (attention/details/kernel.hpp:20-96):
  * s = q·kᵀ·scale, causal mask triu(1) -> -inf, p = softmax(s), o = p·v.
- * q, o, dO, dq [b, h, t, dh]; k, v, dk, dv [b, h, s, dh] (dtype);
- * lse [b, h, t] fp32 = log Σ exp(s).  Dropout must be 0. */
+ * lse [b, h, t] fp32 = log Σ exp(s).  Dropout must be 0.
+ * Layouts (dtype elements):
+ *   NOTT_ATTN_HEAD_MAJOR: q, o, dO, dq [b, h, t, dh]; k, v, dk, dv [b, h, s, dh],
+ *     contiguous (the tensors after head.hpp:70-75's view + transpose);
+ *   NOTT_ATTN_TOKEN_MAJOR: q, dq [b, t, h, dh] and k, v, dk, dv [b, s, h, dh]
+ *     with row stride ld_qkv between consecutive tokens, o, dO [b, t, h, dh]
+ *     with row stride ld_o (0 = h·dh): the projections' outputs as they are,
+ *     e.g. q, k, v = qkv, qkv + h·dh, qkv + 2·h·dh of a packed [b·t, 3·h·dh]
+ *     buffer with ld_qkv = 3·h·dh, so no head split or merge copies. */
+#define NOTT_ATTN_HEAD_MAJOR 0
+#define NOTT_ATTN_TOKEN_MAJOR 1
 typedef struct nott_attn_desc {
     int64_t b, h, t, s, dh;
     int32_t causal;
-    int32_t reserved;
+    int32_t layout;            /* NOTT_ATTN_HEAD_MAJOR or NOTT_ATTN_TOKEN_MAJOR */
     double scale;              /* reference: 1/sqrt(dh) */
+    int64_t ld_qkv, ld_o;      /* token-major row strides (elements); 0 = h·dh */
 } nott_attn_desc;
 int nott_attention_fwd(nott_ctx ctx, const nott_attn_desc* d, nott_dtype dtype,
                        const void* q, const void* k, const void* v, void* o, float* lse);

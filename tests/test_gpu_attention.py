@@ -116,3 +116,33 @@ def test_attention_rejects_bad_descriptors(ops):
     d = ops.attn_desc(1, 1, 4, 4, 200, False)
     with pytest.raises(NottInvalidArgument):
         ops.attention_fwd(q, q, q, d)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("b,h,t,dh,causal", [(2, 3, 100, 64, True), (1, 4, 77, 40, False), (2, 2, 130, 32, True)])
+def test_attention_token_major(ops, dt, b, h, t, dh, causal):
+    """Token-major views (q, k, v packed per token as a [b·t, 3·h·dh]
+    projection output, o / dO as [b·t, h·dh]; dq, dk, dv written into a packed
+    buffer) give the head-major results bit for bit."""
+    g = torch.Generator(device="cuda").manual_seed(b * 100 + t + dh)
+    E = h * dh
+    qkv = torch.randn((b, t, 3, h, dh), generator=g, device="cuda").to(dt)
+    dO_tm = torch.randn((b, t, h, dh), generator=g, device="cuda").to(dt)
+    hm = lambda x: x.permute(0, 2, 1, 3).contiguous()
+    q, k, v = (hm(qkv[:, :, i]) for i in range(3))
+    d = ops.attn_desc(b, h, t, t, dh, causal)
+    o, lse = ops.attention_fwd(q, k, v, d)
+    dq, dk, dv = ops.attention_bwd(q, k, v, o, hm(dO_tm), lse, d)
+
+    flat = qkv.view(b, t, 3 * E)
+    qt, kt, vt = (flat[:, :, i * E:(i + 1) * E].view(b, t, h, dh) for i in range(3))
+    dtm = ops.attn_desc(b, h, t, t, dh, causal, token_major=True, ld_qkv=3 * E)
+    o_tm, lse_tm = ops.attention_fwd(qt, kt, vt, dtm)
+    dqkv = torch.full((b, t, 3 * E), 5.0, device="cuda").to(dt)
+    outs = tuple(dqkv[:, :, i * E:(i + 1) * E].view(b, t, h, dh) for i in range(3))
+    ops.attention_bwd(qt, kt, vt, o_tm, dO_tm, lse_tm, dtm, out=outs)
+    torch.cuda.synchronize()
+    assert torch.equal(o_tm.permute(0, 2, 1, 3), o)
+    assert torch.equal(lse_tm, lse)
+    for got, want in zip(outs, (dq, dk, dv)):
+        assert torch.equal(got.permute(0, 2, 1, 3), want)

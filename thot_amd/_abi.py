@@ -42,9 +42,12 @@ class Pool2dDesc(C.Structure):
                [("ceil_mode", C.c_int32), ("layout", C.c_int32)]
 
 
+NOTT_ATTN_HEAD_MAJOR, NOTT_ATTN_TOKEN_MAJOR = 0, 1
+
+
 class AttnDesc(C.Structure):
     _fields_ = [(n, i64) for n in ("b", "h", "t", "s", "dh")] + \
-               [("causal", C.c_int32), ("reserved", C.c_int32), ("scale", f64)]
+               [("causal", C.c_int32), ("layout", C.c_int32), ("scale", f64), ("ld_qkv", i64), ("ld_o", i64)]
 
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)

@@ -26,6 +26,8 @@
 // it is still one 16-byte read per lane.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace {
 
 using nott::ceil_div;
@@ -114,10 +116,10 @@ struct RegA {
 // Loads 16 bytes (E elements) of row `row` starting at column c0 of a
 // [rows × dh] matrix, zero outside; vec = rows are 16-byte aligned.
 template <typename T>
-__device__ __forceinline__ u32x4 load_chunk(const T* base, int row, int nrows, int c0, int dh, bool vec) {
+__device__ __forceinline__ u32x4 load_chunk(const T* base, int row, int nrows, int c0, int dh, int ld, bool vec) {
     constexpr int E = AT<T>::E;
     if (row >= nrows || c0 >= dh) return u32x4{0u, 0u, 0u, 0u};
-    const T* p = base + (int64_t)row * dh + c0;
+    const T* p = base + (int64_t)row * ld + c0;
     if (vec && c0 + E <= dh) return *reinterpret_cast<const u32x4*>(p);
     T v[E];
 #pragma unroll
@@ -133,11 +135,11 @@ __device__ __forceinline__ u32x4 load_chunk(const T* base, int row, int nrows, i
 
 // Natural tile: rows r0..r0+63 of the matrix, [row][d], NCHD chunks per row.
 template <typename T, int NCHD>
-__device__ __forceinline__ void fill_nat(char* tile, const T* base, int r0, int nrows, int dh, bool vec) {
+__device__ __forceinline__ void fill_nat(char* tile, const T* base, int r0, int nrows, int dh, int ld, bool vec) {
     constexpr int E = AT<T>::E;
     for (int t = threadIdx.x; t < BR * NCHD; t += kThreads) {
         const int ch = t % NCHD, row = t / NCHD;
-        *reinterpret_cast<u32x4*>(tile + toff(row, ch, NCHD)) = load_chunk<T>(base, r0 + row, nrows, ch * E, dh, vec);
+        *reinterpret_cast<u32x4*>(tile + toff(row, ch, NCHD)) = load_chunk<T>(base, r0 + row, nrows, ch * E, dh, ld, vec);
     }
 }
 
@@ -152,7 +154,7 @@ struct TileRegs {
     static constexpr int N = (BR * NCHD + kThreads - 1) / kThreads;
     u32x4 r[N];
     uint32_t ok = 0;
-    __device__ __forceinline__ void load(const T* base, int r0, int nrows, int dh, bool vec) {
+    __device__ __forceinline__ void load(const T* base, int r0, int nrows, int dh, int ld, bool vec) {
         if (vec && dh % E == 0) {
 #pragma unroll
             for (int j = 0; j < N; ++j) {
@@ -160,7 +162,7 @@ struct TileRegs {
                 const int ch = t % NCHD, row = r0 + t / NCHD;
                 const bool good = t < BR * NCHD && row < nrows && ch * E < dh;
                 const int rr = row < nrows ? row : nrows - 1;
-                r[j] = *reinterpret_cast<const u32x4*>(base + (int64_t)rr * dh + (ch * E < dh ? ch * E : 0));
+                r[j] = *reinterpret_cast<const u32x4*>(base + (int64_t)rr * ld + (ch * E < dh ? ch * E : 0));
                 ok = good ? (ok | (1u << j)) : (ok & ~(1u << j));
             }
         } else {
@@ -168,7 +170,7 @@ struct TileRegs {
             for (int j = 0; j < N; ++j) {
                 const int t = threadIdx.x + j * kThreads;
                 const int ch = t % NCHD, row = t / NCHD;
-                r[j] = t < BR * NCHD ? load_chunk<T>(base, r0 + row, nrows, ch * E, dh, vec) : u32x4{0u, 0u, 0u, 0u};
+                r[j] = t < BR * NCHD ? load_chunk<T>(base, r0 + row, nrows, ch * E, dh, ld, vec) : u32x4{0u, 0u, 0u, 0u};
             }
             ok = ~0u;
         }
@@ -200,7 +202,7 @@ __device__ __forceinline__ int perm_row(int pos) {
 // chunks per d-row; DP rows (padded head dim).  One task moves an E×E block:
 // E rows (at E consecutive positions) × E columns, transposed in registers.
 template <typename T, int DP>
-__device__ __forceinline__ void fill_trans(char* tile, const T* base, int r0, int nrows, int dh, bool vec) {
+__device__ __forceinline__ void fill_trans(char* tile, const T* base, int r0, int nrows, int dh, int ld, bool vec) {
     constexpr int E = AT<T>::E;
     constexpr int NCHT = BR / E;
     constexpr int TASKS = NCHT * (DP / E);
@@ -208,7 +210,7 @@ __device__ __forceinline__ void fill_trans(char* tile, const T* base, int r0, in
         const int pc = t % NCHT, dc = t / NCHT;     // position chunk, d chunk
         u32x4 in[E], out[E];
 #pragma unroll
-        for (int i = 0; i < E; ++i) in[i] = load_chunk<T>(base, r0 + perm_row<T>(pc * E + i), nrows, dc * E, dh, vec);
+        for (int i = 0; i < E; ++i) in[i] = load_chunk<T>(base, r0 + perm_row<T>(pc * E + i), nrows, dc * E, dh, ld, vec);
         if constexpr (E == 8) {
 #pragma unroll
             for (int d = 0; d < 4; ++d)
@@ -273,7 +275,19 @@ struct AttnParams {
     float scale;
     int32_t nqb, nkb;     // query / key blocks
     int32_t vec;          // rows are 16-byte aligned (vector loads)
+    int32_t nh;           // heads
+    // Element strides: row, batch and head of q/dq (q), k/v/dk/dv (k) and
+    // o/dO (o).  Head-major [b, h, rows, dh]: row dh, head rows·dh; token-major
+    // [b, rows, h, ·]: row ld, head dh.
+    int32_t ldq, ldk, ldo;
+    int64_t sbq, shq, sbk, shk, sbo, sho;
 };
+
+// Element offset of (batch, head) pair bh in a tensor with batch / head
+// strides sb / sh.
+__device__ __forceinline__ int64_t bh_off(int bh, int nh, int64_t sb, int64_t sh) {
+    return (int64_t)(bh / nh) * sb + (int64_t)(bh % nh) * sh;
+}
 
 // ---------------------------------------------------------------- forward
 template <typename T, int NS>
@@ -295,13 +309,14 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
     const int bh = blockIdx.x;
     const int qb = p.nqb - 1 - (int)blockIdx.y;      // heaviest (causal) blocks dispatched first
     const int q0 = qb * BR;
-    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
+    const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
     const int my_q = q0 + wid * 16 + r16;            // this lane's query row (score layout)
     const float sl2 = p.scale * 1.4426950408889634f;  // scale·log2(e)
 
-    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
+    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.ldq, p.vec);
     float m = -INFINITY, l = 0.f;
     f32x4 acc[ND];
 #pragma unroll
@@ -310,18 +325,18 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
     int kb_end = p.nkb;
     if (p.causal) kb_end = min(kb_end, (q0 + BR - 1) / BR + 1);
     TileRegs<T, NCHD> rk, rv;
-    rk.load(k + koff, 0, p.s, p.dh, p.vec);
-    if constexpr (sizeof(T) == 2) rv.load(v + koff, 0, p.s, p.dh, p.vec);
+    rk.load(k + koff, 0, p.s, p.dh, p.ldk, p.vec);
+    if constexpr (sizeof(T) == 2) rv.load(v + koff, 0, p.s, p.dh, p.ldk, p.vec);
     for (int kb = 0; kb < kb_end; ++kb) {
         const int k0 = kb * BR;
         __syncthreads();
         rk.store(lk);
         if constexpr (sizeof(T) == 2) rv.store(lvt);   // natural v
-        else fill_trans<T, DP>(lvt, v + koff, k0, p.s, p.dh, p.vec);
+        else fill_trans<T, DP>(lvt, v + koff, k0, p.s, p.dh, p.ldk, p.vec);
         __syncthreads();
         if (kb + 1 < kb_end) {
-            rk.load(k + koff, k0 + BR, p.s, p.dh, p.vec);
-            if constexpr (sizeof(T) == 2) rv.load(v + koff, k0 + BR, p.s, p.dh, p.vec);
+            rk.load(k + koff, k0 + BR, p.s, p.dh, p.ldk, p.vec);
+            if constexpr (sizeof(T) == 2) rv.load(v + koff, k0 + BR, p.s, p.dh, p.ldk, p.vec);
         }
         // scores in transposed form: lane holds s[my_q][k0 + 16·kt + 4·kq + e]
         f32x4 sc[4];
@@ -385,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int row = q0 + wid * 16 + kq * 4 + e;
-            if (row < p.t) Io<T>::st(o + qoff, (int64_t)row * p.dh + d, acc[dt][e] / li[e]);
+            if (row < p.t) Io<T>::st(o + ooff, (int64_t)row * p.ldo + d, acc[dt][e] / li[e]);
         }
     }
     if (kq == 0 && my_q < p.t) lse[(int64_t)bh * p.t + my_q] = (m + log2f(l)) * 0.6931471805599453f;
@@ -394,12 +409,14 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
 // ------------------------------------------------------- rowsum(do ∘ o)
 template <typename T>
 __global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ o, const T* __restrict__ dO,
-                                                        float* __restrict__ dsum, int64_t rows, int dh) {
-    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+                                                        float* __restrict__ dsum, int64_t rows, AttnParams p) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);   // (batch·head)·t + query
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;
+    const int bh = (int)(r / p.t), qi = (int)(r - (int64_t)bh * p.t);
+    const int64_t base = bh_off(bh, p.nh, p.sbo, p.sho) + (int64_t)qi * p.ldo;
     float s = 0.f;
-    for (int d = lane; d < dh; d += 64) s += Io<T>::ld(o, r * dh + d) * Io<T>::ld(dO, r * dh + d);
+    for (int d = lane; d < p.dh; d += 64) s += Io<T>::ld(o, base + d) * Io<T>::ld(dO, base + d);
     s = wave_sum(s);
     if (lane == 0) dsum[r] = s;
 }
@@ -431,14 +448,15 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
     const int bh = blockIdx.x;
     const int kb = blockIdx.y;       // key blocks outermost: the longest (causal) ones are dispatched first
     const int k0 = kb * BR;
-    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
+    const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
     const int my_k = k0 + wid * 16 + r16;   // this lane's key (score layout column)
     const float sl2 = p.scale * 1.4426950408889634f;
 
-    fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.vec);
-    fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.vec);
+    fill_nat<T, NCHD>(lk, k + koff, k0, p.s, p.dh, p.ldk, p.vec);
+    fill_nat<T, NCHD>(lv, v + koff, k0, p.s, p.dh, p.ldk, p.vec);
     f32x4 adk[ND], adv[ND];
 #pragma unroll
     for (int i = 0; i < ND; ++i) adk[i] = adv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -455,8 +473,8 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
         nxt_ds = in ? dsum[i] : 0.f;
     };
     if (qb_begin < p.nqb) {
-        rq.load(q + qoff, qb_begin * BR, p.t, p.dh, p.vec);
-        rdo.load(dO + qoff, qb_begin * BR, p.t, p.dh, p.vec);
+        rq.load(q + qoff, qb_begin * BR, p.t, p.dh, p.ldq, p.vec);
+        rdo.load(dO + ooff, qb_begin * BR, p.t, p.dh, p.ldo, p.vec);
         load_stats(qb_begin * BR);
     }
     for (int qb = qb_begin; qb < p.nqb; ++qb) {
@@ -465,8 +483,8 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
         rq.store(lq);
         rdo.store(ldo);
         if constexpr (sizeof(T) == 4) {
-            fill_trans<T, DP>(lqt, q + qoff, q0, p.t, p.dh, p.vec);
-            fill_trans<T, DP>(ldot, dO + qoff, q0, p.t, p.dh, p.vec);
+            fill_trans<T, DP>(lqt, q + qoff, q0, p.t, p.dh, p.ldq, p.vec);
+            fill_trans<T, DP>(ldot, dO + ooff, q0, p.t, p.dh, p.ldo, p.vec);
         }
         if (threadIdx.x < BR) {
             llse[threadIdx.x] = nxt_lse;
@@ -474,8 +492,8 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
         }
         __syncthreads();
         if (qb + 1 < p.nqb) {
-            rq.load(q + qoff, q0 + BR, p.t, p.dh, p.vec);
-            rdo.load(dO + qoff, q0 + BR, p.t, p.dh, p.vec);
+            rq.load(q + qoff, q0 + BR, p.t, p.dh, p.ldq, p.vec);
+            rdo.load(dO + ooff, q0 + BR, p.t, p.dh, p.ldo, p.vec);
             load_stats(q0 + BR);
         }
         const bool full = q0 + BR <= p.t && k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
@@ -518,8 +536,8 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
         for (int e = 0; e < 4; ++e) {
             const int key = k0 + wid * 16 + kq * 4 + e;
             if (key < p.s) {
-                Io<T>::st(dk + koff, (int64_t)key * p.dh + d, adk[dt][e] * p.scale);
-                Io<T>::st(dv + koff, (int64_t)key * p.dh + d, adv[dt][e]);
+                Io<T>::st(dk + koff, (int64_t)key * p.ldk + d, adk[dt][e] * p.scale);
+                Io<T>::st(dv + koff, (int64_t)key * p.ldk + d, adv[dt][e]);
             }
         }
     }
@@ -553,15 +571,16 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
     const int bh = blockIdx.x;
     const int qb = p.nqb - 1 - (int)blockIdx.y;      // heaviest (causal) blocks dispatched first
     const int q0 = qb * BR;
-    const int64_t qoff = (int64_t)bh * p.t * p.dh, koff = (int64_t)bh * p.s * p.dh;
+    const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
+    const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, kq = lane >> 4;
     const int my_q = q0 + wid * 16 + r16;
     const float sl2 = p.scale * 1.4426950408889634f;
     const float my_lse = my_q < p.t ? lse[(int64_t)bh * p.t + my_q] * 1.4426950408889634f : 0.f;
 
-    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.vec);
-    fill_nat<T, NCHD>(ldo, dO + qoff, q0, p.t, p.dh, p.vec);
+    fill_nat<T, NCHD>(lq, q + qoff, q0, p.t, p.dh, p.ldq, p.vec);
+    fill_nat<T, NCHD>(ldo, dO + ooff, q0, p.t, p.dh, p.ldo, p.vec);
     f32x4 acc[ND];
 #pragma unroll
     for (int i = 0; i < ND; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -572,8 +591,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
     TileRegs<T, NCHD> rk, rv;
     if constexpr (EXACT_DSUM) {
         float part = 0.f;
-        rk.load(k + koff, 0, p.s, p.dh, p.vec);
-        rv.load(v + koff, 0, p.s, p.dh, p.vec);
+        rk.load(k + koff, 0, p.s, p.dh, p.ldk, p.vec);
+        rv.load(v + koff, 0, p.s, p.dh, p.ldk, p.vec);
         for (int kb = 0; kb < kb_end; ++kb) {
             const int k0 = kb * BR;
             const bool full = q0 + BR <= p.t && k0 + BR <= p.s && (!p.causal || k0 + BR - 1 <= q0);
@@ -583,8 +602,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
             __syncthreads();
             // next block (or, after the last, block 0 for the main pass)
             const int nk0 = kb + 1 < kb_end ? k0 + BR : 0;
-            rk.load(k + koff, nk0, p.s, p.dh, p.vec);
-            rv.load(v + koff, nk0, p.s, p.dh, p.vec);
+            rk.load(k + koff, nk0, p.s, p.dh, p.ldk, p.vec);
+            rv.load(v + koff, nk0, p.s, p.dh, p.ldk, p.vec);
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
                 f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -607,8 +626,8 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
         if (kq == 0 && my_q < p.t) dsum[(int64_t)bh * p.t + my_q] = my_ds;
     } else {
         my_ds = my_q < p.t ? dsum[(int64_t)bh * p.t + my_q] : 0.f;
-        rk.load(k + koff, 0, p.s, p.dh, p.vec);
-        rv.load(v + koff, 0, p.s, p.dh, p.vec);
+        rk.load(k + koff, 0, p.s, p.dh, p.ldk, p.vec);
+        rv.load(v + koff, 0, p.s, p.dh, p.ldk, p.vec);
     }
     for (int kb = 0; kb < kb_end; ++kb) {
         const int k0 = kb * BR;
@@ -616,11 +635,11 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
         __syncthreads();
         rk.store(lk);
         rv.store(lv);
-        if constexpr (sizeof(T) == 4) fill_trans<T, DP>(lkt, k + koff, k0, p.s, p.dh, p.vec);
+        if constexpr (sizeof(T) == 4) fill_trans<T, DP>(lkt, k + koff, k0, p.s, p.dh, p.ldk, p.vec);
         __syncthreads();
         if (kb + 1 < kb_end) {
-            rk.load(k + koff, k0 + BR, p.s, p.dh, p.vec);
-            rv.load(v + koff, k0 + BR, p.s, p.dh, p.vec);
+            rk.load(k + koff, k0 + BR, p.s, p.dh, p.ldk, p.vec);
+            rv.load(v + koff, k0 + BR, p.s, p.dh, p.ldk, p.vec);
         }
         // lane holds s / dp at [my_q][k0 + 16·kt + 4·kq + e]
         f32x4 sc[4], dp[4];
@@ -655,7 +674,7 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int row = q0 + wid * 16 + kq * 4 + e;
-            if (row < p.t) Io<T>::st(dq + qoff, (int64_t)row * p.dh + d, acc[dt][e] * p.scale);
+            if (row < p.t) Io<T>::st(dq + qoff, (int64_t)row * p.ldq + d, acc[dt][e] * p.scale);
         }
     }
 }
@@ -671,13 +690,61 @@ int check(nott_ctx ctx, const nott_attn_desc* d, AttnParams* p, int elem) {
     NOTT_REQUIRE(ctx, d->t * d->dh < (int64_t(1) << 31) && d->s * d->dh < (int64_t(1) << 31),
                  "attention: sequence too long");
     NOTT_REQUIRE(ctx, !d->causal || d->s > 0, "attention: causal needs keys");
+    NOTT_REQUIRE(ctx, d->layout == NOTT_ATTN_HEAD_MAJOR || d->layout == NOTT_ATTN_TOKEN_MAJOR, "attention: bad layout");
     p->t = (int32_t)d->t; p->s = (int32_t)d->s; p->dh = (int32_t)d->dh;
     p->causal = d->causal != 0;
     p->scale = (float)d->scale;
     p->nqb = (int32_t)ceil_div(d->t, BR);
     p->nkb = (int32_t)ceil_div(d->s, BR);
-    p->vec = ((d->dh * elem) % 16) == 0;
+    p->nh = (int32_t)std::max<int64_t>(d->h, 1);
+    if (d->layout == NOTT_ATTN_HEAD_MAJOR) {
+        p->ldq = p->ldk = p->ldo = p->dh;
+        p->shq = p->sho = d->t * d->dh;
+        p->sbq = p->sbo = d->h * d->t * d->dh;
+        p->shk = d->s * d->dh;
+        p->sbk = d->h * d->s * d->dh;
+    } else {
+        const int64_t ldqkv = d->ld_qkv ? d->ld_qkv : d->h * d->dh, ldo = d->ld_o ? d->ld_o : d->h * d->dh;
+        NOTT_REQUIRE(ctx, ldqkv >= d->h * d->dh && ldo >= d->h * d->dh, "attention: row stride below h·dh");
+        NOTT_REQUIRE(ctx, std::max(d->t, d->s) * std::max(ldqkv, ldo) < (int64_t(1) << 31),
+                     "attention: sequence too long");
+        p->ldq = p->ldk = (int32_t)ldqkv;
+        p->ldo = (int32_t)ldo;
+        p->shq = p->shk = p->sho = d->dh;
+        p->sbq = d->t * ldqkv;
+        p->sbk = d->s * ldqkv;
+        p->sbo = d->t * ldo;
+    }
+    p->vec = ((d->dh * elem) % 16) == 0 && ((int64_t)p->ldq * elem) % 16 == 0 && ((int64_t)p->ldo * elem) % 16 == 0;
     return NOTT_OK;
+}
+
+// Zeroes `rows` rows of `cols` elements at row stride ld (strided outputs of
+// the empty cases).
+__global__ __launch_bounds__(256) void zero_rows_kernel(uint16_t* __restrict__ p16, float* __restrict__ p32,
+                                                        int64_t rows, int64_t cols, int64_t ld) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols, c = i - r * cols;
+    if (p16) p16[r * ld + c] = 0;
+    else p32[r * ld + c] = 0.f;
+}
+
+// Zero the (b, h, rows, dh) view of a q-side (kq = 0) or k-side (kq = 1)
+// tensor in the descriptor's layout.
+int zero_view(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, int elem, int64_t rows, bool kside,
+              void* dst) {
+    if (d->b * d->h * rows == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, dst != nullptr, "nott_attention_bwd: null buffer");
+    // head-major: b·h·rows contiguous rows of dh; token-major: b·rows rows of h·dh at stride ld.
+    const bool hm = d->layout == NOTT_ATTN_HEAD_MAJOR;
+    const int64_t nrows = hm ? d->b * d->h * rows : d->b * rows;
+    const int64_t cols = hm ? d->dh : d->h * d->dh;
+    const int64_t ld = hm ? d->dh : (kside ? p.ldk : p.ldq);
+    hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)ceil_div(nrows * cols, 256)), dim3(256), 0, ctx->stream,
+                       elem == 2 ? static_cast<uint16_t*>(dst) : nullptr, elem == 2 ? nullptr : static_cast<float*>(dst),
+                       nrows, cols, ld);
+    return launch_status(ctx, "attention zero");
 }
 
 template <typename T>
@@ -724,7 +791,7 @@ int bwd_ns(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const voi
     // fp32: rowsum(do∘o) from o; bf16: the dq pass forms it exactly and runs first.
     if (!EXACT)
         hipLaunchKernelGGL(attn_dsum_kernel<T>, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, ctx->stream,
-                           static_cast<const T*>(o), static_cast<const T*>(dO), dsum, rows, (int)d->dh);
+                           static_cast<const T*>(o), static_cast<const T*>(dO), dsum, rows, p);
     hipLaunchKernelGGL((attn_dq_kernel<T, NS, EXACT>), dim3(bh, (unsigned)p.nqb), dim3(kThreads), lds_q, ctx->stream,
                        static_cast<const T*>(q), static_cast<const T*>(k), static_cast<const T*>(v),
                        static_cast<const T*>(dO), lse, dsum, static_cast<T*>(dq), p);
@@ -784,16 +851,12 @@ extern "C" int nott_attention_bwd(nott_ctx ctx, const nott_attn_desc* d, nott_dt
     if (d->t == 0 || d->s == 0) {
         // No queries: dk = dv = 0 (sums over no rows); no keys: dq = 0.
         nott::DeviceScope scope(ctx->device);
-        const int64_t es = (int64_t)nott::dtype_size(dtype), bh = d->b * d->h;
+        const int elem = (int)nott::dtype_size(dtype);
         if (d->t == 0) {
-            NOTT_REQUIRE(ctx, dk && dv, "nott_attention_bwd: null buffer");
-            if (nott_zero(ctx, es * bh * d->s * d->dh, dk) != NOTT_OK) return NOTT_ERR_HIP;
-            if (nott_zero(ctx, es * bh * d->s * d->dh, dv) != NOTT_OK) return NOTT_ERR_HIP;
-        } else {
-            NOTT_REQUIRE(ctx, dq, "nott_attention_bwd: null buffer");
-            if (nott_zero(ctx, es * bh * d->t * d->dh, dq) != NOTT_OK) return NOTT_ERR_HIP;
+            const int st1 = zero_view(ctx, d, p, elem, d->s, true, dk);
+            return st1 != NOTT_OK ? st1 : zero_view(ctx, d, p, elem, d->s, true, dv);
         }
-        return NOTT_OK;
+        return zero_view(ctx, d, p, elem, d->t, false, dq);
     }
     NOTT_REQUIRE(ctx, q && k && v && o && dO && lse && dq && dk && dv, "nott_attention_bwd: null buffer");
     if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dO))) p.vec = 0;

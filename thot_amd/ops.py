@@ -421,28 +421,74 @@ def conv2d_bwd_weight(x: torch.Tensor, dy: torch.Tensor, d: Conv2dDesc, *, need_
 
 
 # ------------------------------------------------------------------- attention
-def attn_desc(b: int, h: int, t: int, s: int, dh: int, causal: bool, scale: Optional[float] = None) -> AttnDesc:
-    return AttnDesc(b, h, t, s, dh, int(causal), 0, 1.0 / math.sqrt(dh) if scale is None else float(scale))
+def attn_desc(b: int, h: int, t: int, s: int, dh: int, causal: bool, scale: Optional[float] = None, *,
+              token_major: bool = False, ld_qkv: int = 0, ld_o: int = 0) -> AttnDesc:
+    """Head-major ([b, h, rows, dh] contiguous) or token-major ([b, rows, h, dh]
+    views with row strides ld_qkv for q/k/v and their gradients, ld_o for o/dO;
+    0 = h·dh) attention descriptor."""
+    layout = _abi.NOTT_ATTN_TOKEN_MAJOR if token_major else _abi.NOTT_ATTN_HEAD_MAJOR
+    return AttnDesc(b, h, t, s, dh, int(causal), layout, 1.0 / math.sqrt(dh) if scale is None else float(scale),
+                    int(ld_qkv), int(ld_o))
 
 
-def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, d: AttnDesc):
-    _check(q, "q", shape=(d.b, d.h, d.t, d.dh))
-    _check(k, "k", shape=(d.b, d.h, d.s, d.dh), dtype=q.dtype, device=q.device)
-    _check(v, "v", shape=(d.b, d.h, d.s, d.dh), dtype=q.dtype, device=q.device)
-    o = torch.empty_like(q)
+def _attn_ld(d: AttnDesc, which: str) -> int:
+    ld = d.ld_qkv if which == "qkv" else d.ld_o
+    return ld if ld else d.h * d.dh
+
+
+def _check_attn(t: torch.Tensor, name: str, d: AttnDesc, rows: int, which: str, ref: Optional[torch.Tensor] = None):
+    """Head-major: contiguous [b, h, rows, dh].  Token-major: [b, rows, h, dh]
+    with strides (rows·ld, ld, dh, 1)."""
+    if d.layout == _abi.NOTT_ATTN_HEAD_MAJOR:
+        _check(t, name, shape=(d.b, d.h, rows, d.dh), dtype=None if ref is None else ref.dtype,
+               device=None if ref is None else ref.device)
+        return
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if tuple(t.shape) != (d.b, rows, d.h, d.dh):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {(d.b, rows, d.h, d.dh)}")
+    ld = _attn_ld(d, which)
+    want = (rows * ld, ld, d.dh, 1)
+    if t.numel() and any(sz > 1 and st != w for sz, st, w in zip(t.shape, t.stride(), want)):
+        raise ValueError(f"{name} has strides {t.stride()}, expected {want}")
+    if ref is not None and (t.dtype != ref.dtype or t.device != ref.device):
+        raise TypeError(f"{name} must match q's dtype and device")
+
+
+def _attn_empty(d: AttnDesc, rows: int, which: str, like: torch.Tensor) -> torch.Tensor:
+    if d.layout == _abi.NOTT_ATTN_HEAD_MAJOR:
+        return torch.empty((d.b, d.h, rows, d.dh), dtype=like.dtype, device=like.device)
+    if _attn_ld(d, which) != d.h * d.dh:
+        raise ValueError("token-major outputs with a row stride other than h·dh must be passed in")
+    return torch.empty((d.b, rows, d.h, d.dh), dtype=like.dtype, device=like.device)
+
+
+def attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, d: AttnDesc, out: Optional[torch.Tensor] = None):
+    _check_attn(q, "q", d, d.t, "qkv")
+    _check_attn(k, "k", d, d.s, "qkv", q)
+    _check_attn(v, "v", d, d.s, "qkv", q)
+    o = _attn_empty(d, d.t, "o", q) if out is None else out
+    _check_attn(o, "o", d, d.t, "o", q)
     lse = torch.empty((d.b, d.h, d.t), dtype=torch.float32, device=q.device)
     _ctx_for(q).call("nott_attention_fwd", C.byref(d), nott_dtype(q.dtype), _ptr(q), _ptr(k), _ptr(v), _ptr(o),
                      _ptr(lse))
     return o, lse
 
 
-def attention_bwd(q, k, v, o, dO, lse, d: AttnDesc):
-    _check(q, "q", shape=(d.b, d.h, d.t, d.dh))
-    for t, nm, shp in ((k, "k", (d.b, d.h, d.s, d.dh)), (v, "v", (d.b, d.h, d.s, d.dh)),
-                       (o, "o", (d.b, d.h, d.t, d.dh)), (dO, "dO", (d.b, d.h, d.t, d.dh))):
-        _check(t, nm, shape=shp, dtype=q.dtype, device=q.device)
+def attention_bwd(q, k, v, o, dO, lse, d: AttnDesc, out=None):
+    """Returns (dq, dk, dv) in the descriptor's layout; `out` = three tensors
+    to write them into (required for token-major row strides other than h·dh)."""
+    _check_attn(q, "q", d, d.t, "qkv")
+    for t, nm, rows, which in ((k, "k", d.s, "qkv"), (v, "v", d.s, "qkv"), (o, "o", d.t, "o"),
+                               (dO, "dO", d.t, "o")):
+        _check_attn(t, nm, d, rows, which, q)
     _check(lse, "lse", shape=(d.b, d.h, d.t), dtype=torch.float32, device=q.device)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if out is None:
+        dq, dk, dv = _attn_empty(d, d.t, "qkv", q), _attn_empty(d, d.s, "qkv", q), _attn_empty(d, d.s, "qkv", q)
+    else:
+        dq, dk, dv = out
+    for t, nm, rows in ((dq, "dq", d.t), (dk, "dk", d.s), (dv, "dv", d.s)):
+        _check_attn(t, nm, d, rows, "qkv", q)
     _ctx_for(q).call("nott_attention_bwd", C.byref(d), nott_dtype(q.dtype), _ptr(q), _ptr(k), _ptr(v), _ptr(o),
                      _ptr(dO), _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv))
     return dq, dk, dv
