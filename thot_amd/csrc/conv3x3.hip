@@ -70,8 +70,10 @@ struct SameParams {
 template <typename T, bool DGRAD>
 __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict__ w, T* __restrict__ wp, int32_t cout,
                                                             int32_t cin) {
+    // Slices cover whole 64-channel blocks; channels from cout up to the
+    // block end are zero weights.
     constexpr int CC = Chunk<T>::CC;
-    const int64_t total = (int64_t)cout * cin * 9;
+    const int64_t total = (int64_t)((cout + kTileCo - 1) / kTileCo) * kTileCo * cin * 9;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
     // decompose destination index
@@ -92,7 +94,9 @@ __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict_
                               : (((int64_t)co * cin + ci) * 9 + r * 3 + s);
     constexpr int SUB = Chunk<T>::SUB;
     const int64_t slice = ((int64_t)cb * ncc + cc) * 9 * kTileCo * CC;
-    wp[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = w[src];
+    T val = T(0);
+    if (co < cout) val = w[src];
+    wp[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = val;
 }
 
 template <typename T>
@@ -392,6 +396,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             const int32_t co = cb * kTileCo + nt * 16 + r16;
+            if (co >= p.cout) continue;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
                 const int32_t m = m0 + wid * 64 + mt * 16 + kq * 4;
@@ -417,7 +422,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
         const int32_t col = nt * 16 + r16;
-        const float bv = bias ? bias[cb * kTileCo + col] : 0.f;
+        const float bv = bias && cb * kTileCo + col < p.cout ? bias[cb * kTileCo + col] : 0.f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const int px = wid * 64 + mt * 16 + kq * 4;
@@ -432,8 +437,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     for (int t = threadIdx.x; t < kTileCo * RUNS; t += kThreads) {
         const int col = t / RUNS, j = t % RUNS;
         const int32_t m = m0 + j * E16;
-        if (m > m_last) continue;
         const int32_t co = cb * kTileCo + col;
+        if (m > m_last || co >= p.cout) continue;
         const char* src = lds_o + col * OP + j * 16;
         uint32_t n, hw;
         p.fd_hw.divmod((uint32_t)m, n, hw);
@@ -510,14 +515,15 @@ template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
              const float* bias, T* out) {
     constexpr int CC = Chunk<T>::CC;
-    const size_t wbytes = sizeof(T) * (size_t)cout * cin * 9;
+    const int64_t cbc = ceil_div(cout, kTileCo);                 // 64-channel blocks (the last may be partial)
+    const size_t wbytes = sizeof(T) * (size_t)cbc * kTileCo * cin * 9;
     const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
     if (same_lds_bytes(h, w, sizeof(T)) > kSameLdsMax)
         return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
     // Split the channel chunks over blockIdx.z when the grid would not give
     // every CU two workgroups (small images, many channels).
     const int64_t tiles = ceil_div((int64_t)n * h * w, kTilePix);
-    const int64_t blocks = tiles * (cout / kTileCo);
+    const int64_t blocks = tiles * cbc;
     const int32_t nchunks = cin / CC;
     int32_t splits = 1;
     const int64_t npix64 = (int64_t)n * h * w;
@@ -530,7 +536,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     char* ws = static_cast<char*>(workspace(ctx, wbytes_al + pbytes));
     if (!ws) return NOTT_ERR_ALLOC;
     T* wp = reinterpret_cast<T*>(ws);
-    const int64_t welems = (int64_t)cout * cin * 9;
+    const int64_t welems = cbc * kTileCo * cin * 9;
     hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(welems, 256)), dim3(256), 0,
                        ctx->stream, wsrc, wp, cout, cin);
     SameParams p;
@@ -556,7 +562,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
                      : lw == 4  ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, 4>)
                                 : reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, sizeof(T) == 2 ? 2 : 4>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
-    const dim3 grid((unsigned)tiles, (unsigned)(cout / kTileCo), (unsigned)splits);
+    const dim3 grid((unsigned)tiles, (unsigned)cbc, (unsigned)splits);
     if (!vec)
         hipLaunchKernelGGL((conv3x3_same_kernel<T, false, 16>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
     else if (lw == 16)
@@ -720,7 +726,8 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
             task(t, QB, cc, j);
             const int ch = j % CPR, h = h0 - 1 + j / CPR;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && h >= 0 && h < p.h)
+            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && h >= 0 && h < p.h &&
+                cb * 64 + cc < p.c)
                 v = load_chunk<T, LW>(xb + cc * plane + (int64_t)h * p.w, ch, p.w);
             rb[i] = v;
         }
@@ -798,6 +805,7 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
     }
     // Partials: ws[split][tap][k][c]; lane column = channel, rows = k.
     const int32_t c = cb * 64 + cg * 16 + r16;
+    if (c >= p.c) return;                        // padding channels of a partial 64-channel block
     float* wsp = ws + (int64_t)blockIdx.x * 9 * p.k * p.c;
 #pragma unroll
     for (int tap = 0; tap < 9; ++tap)
@@ -861,7 +869,7 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     p.total_bands = p.n * p.bands_per_img;
     p.kblocks = p.k / 64;
     constexpr int CPR = P * (int)sizeof(T) / 16;
-    const int tiles = p.kblocks * (p.c / 64);
+    const int tiles = p.kblocks * (int)ceil_div(p.c, 64);
     // About one workgroup per CU in total.
     int64_t splits = std::max<int64_t>(1, std::min<int64_t>(p.total_bands, ceil_div((int64_t)ctx->num_cu, tiles)));
     p.bands_per_split = (int32_t)ceil_div(p.total_bands, splits);
@@ -894,22 +902,25 @@ int wgrad_slot_pitch(int64_t w) {
 
 bool fwd_applies(const nott_conv2d_desc* d, size_t elem) {
     const int cc = elem == 2 ? Chunk<bf16_t>::CC : Chunk<float>::CC;
-    return same_shape(d) && d->c % cc == 0 && d->k % kTileCo == 0 &&
+    // Output channels: whole 16-channel MFMA columns (the last 64-channel
+    // block may be partial; its missing channels are zero weights).
+    return same_shape(d) && d->c % cc == 0 && d->k % 16 == 0 &&
            same_lds_bytes((int32_t)d->h, (int32_t)d->w, elem) <= kSameLdsMax;
 }
 
 bool dgrad_applies(const nott_conv2d_desc* d, size_t elem) {
     const int cc = elem == 2 ? Chunk<bf16_t>::CC : Chunk<float>::CC;
     // dgrad's input channels are the conv's outputs (k), its outputs the conv's inputs (c).
-    return same_shape(d) && d->k % cc == 0 && d->c % kTileCo == 0 &&
+    return same_shape(d) && d->k % cc == 0 && d->c % 16 == 0 &&
            same_lds_bytes((int32_t)d->h, (int32_t)d->w, elem) <= kSameLdsMax;
 }
 
 bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {
-    // A slot row of at most 64, whole 64-channel blocks (image rows of any
-    // width: narrower loads when rows are not whole 16-byte chunks).
+    // A slot row of at most 64, whole 64-channel blocks of dy and 16-channel
+    // groups of x (a partial last x block loads zeros past c), image rows of
+    // any width (narrower loads when rows are not whole 16-byte chunks).
     (void)elem;
-    return same_shape(d) && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 64 == 0;
+    return same_shape(d) && wgrad_slot_pitch(d->w) <= 64 && d->k % 64 == 0 && d->c % 16 == 0;
 }
 
 
