@@ -102,6 +102,7 @@ CONV = [
     (5, 128, 7, 7, 192, 3, 3, 1, 1, 1),        # ragged last pixel tile
     (3, 16, 12, 12, 48, 3, 3, 1, 1, 1),        # partial 64-channel output blocks (48; dgrad 16)
     (2, 80, 8, 8, 64, 3, 3, 1, 1, 1),          # partial last x-channel block in wgrad, dgrad 80 outputs
+    (3, 1, 9, 7, 40, 3, 3, 1, 1, 1),           # one input channel (direct kernels), odd sizes
     # bf16 column path (n·p·q a multiple of 64): strided 3x3, 1x1 projection,
     # 7x7 stem, small-width 3x3 wgrad, odd channel counts
     (4, 64, 56, 56, 128, 3, 3, 2, 1, 1),

@@ -537,6 +537,128 @@ int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) 
     return NOTT_OK;
 }
 
+// ---------------------------------------------------------------------------
+// One input channel, 3×3, stride 1, pad 1, NCHW (the first conv of the
+// configs[0] small CNN, conv.hpp:177 on a [n, 1, 28, 28] image): a GEMM with
+// K = 9 is all overhead, so these are direct kernels.
+//   fwd  : y[n, co, h, w] = b[co] + Σ_{r,s} x[n, 0, h+r−1, w+s−1] · wt[co, 0, r, s]
+//   wgrad: dw[co, 0, r, s] = Σ_{n,h,w} dy[n, co, h, w] · x[n, 0, h+r−1, w+s−1]
+// (db keeps its own two-pass kernels).  wgrad is deterministic: workgroup
+// (co, slab of images) writes 9 partial sums, and a second pass adds the
+// slabs in order.
+// ---------------------------------------------------------------------------
+bool cin1_applies(const nott_conv2d_desc* d) {
+    return d->layout == NOTT_NCHW && d->groups == 1 && d->c == 1 && d->r == 3 && d->s == 3 && d->stride_h == 1 &&
+           d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1 && d->dil_h == 1 && d->dil_w == 1 && d->k <= 256;
+}
+
+// The 9 taps of x around pixel (h, w) of image plane xp (zero outside).
+template <typename T>
+__device__ __forceinline__ void cin1_taps(const T* __restrict__ xp, int32_t h, int32_t w, int32_t H, int32_t W,
+                                          float (&t)[9]) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const int32_t hh = h + r - 1, ww = w + s - 1;
+            t[r * 3 + s] = (hh >= 0 && hh < H && ww >= 0 && ww < W) ? Io<T>::ld(xp, (int64_t)hh * W + ww) : 0.f;
+        }
+}
+
+// Thread = one pixel for all k output channels (weights and bias in LDS).
+template <typename T>
+__global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, const T* __restrict__ wt,
+                                                       const float* __restrict__ b, T* __restrict__ y, int32_t n,
+                                                       int32_t H, int32_t W, int32_t k) {
+    __shared__ float lw[256 * 9], lb[256];
+    for (int i = threadIdx.x; i < k * 9; i += 256) lw[i] = Io<T>::ld(wt, i);
+    for (int i = threadIdx.x; i < k; i += 256) lb[i] = b ? b[i] : 0.f;
+    __syncthreads();
+    const int64_t hw = (int64_t)H * W;
+    const int64_t pix = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (pix >= (int64_t)n * hw) return;
+    const int64_t img = pix / hw, in = pix - img * hw;
+    const int32_t h = (int32_t)(in / W), w = (int32_t)(in - (int64_t)h * W);
+    float t[9];
+    cin1_taps<T>(x + img * hw, h, w, H, W, t);
+    T* yp = y + img * k * hw + in;
+    for (int co = 0; co < k; ++co) {
+        float a = lb[co];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) a = __builtin_fmaf(t[j], lw[co * 9 + j], a);
+        Io<T>::st(yp, (int64_t)co * hw, a);
+    }
+}
+
+constexpr int kCin1Slabs = 16;
+
+// Workgroup (co, slab): 9 partial sums over the slab's images.
+template <typename T>
+__global__ __launch_bounds__(256) void cin1_wgrad_partial_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                                 int32_t n, int32_t H, int32_t W, int32_t k,
+                                                                 float* __restrict__ part) {
+    __shared__ float red[4][9];
+    const int co = blockIdx.x, slab = blockIdx.y;
+    const int64_t hw = (int64_t)H * W;
+    const int32_t per = (n + kCin1Slabs - 1) / kCin1Slabs;
+    const int32_t n0 = slab * per, n1 = min(n, n0 + per);
+    float acc[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) acc[j] = 0.f;
+    for (int32_t img = n0; img < n1; ++img) {
+        const T* xp = x + (int64_t)img * hw;
+        const T* dp = dy + ((int64_t)img * k + co) * hw;
+        for (int64_t in = threadIdx.x; in < hw; in += 256) {
+            const int32_t h = (int32_t)(in / W), w = (int32_t)(in - (int64_t)h * W);
+            float t[9];
+            cin1_taps<T>(xp, h, w, H, W, t);
+            const float g = Io<T>::ld(dp, in);
+#pragma unroll
+            for (int j = 0; j < 9; ++j) acc[j] = __builtin_fmaf(g, t[j], acc[j]);
+        }
+    }
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+        const float v = wave_sum(acc[j]);
+        if (lane == 0) red[wid][j] = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 9) {
+        const int j = threadIdx.x;
+        part[((int64_t)co * kCin1Slabs + slab) * 9 + j] = (red[0][j] + red[1][j]) + (red[2][j] + red[3][j]);
+    }
+}
+
+__global__ __launch_bounds__(256) void cin1_wgrad_finish_kernel(const float* __restrict__ part, int32_t k,
+                                                                float* __restrict__ dw, int accumulate) {
+    const int i = blockIdx.x * 256 + threadIdx.x;     // co·9 + tap
+    if (i >= k * 9) return;
+    const int co = i / 9, j = i - co * 9;
+    float s = 0.f;
+    for (int z = 0; z < kCin1Slabs; ++z) s += part[((int64_t)co * kCin1Slabs + z) * 9 + j];
+    dw[i] = accumulate ? dw[i] + s : s;
+}
+
+template <typename T>
+int cin1_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
+    const int64_t pix = d->n * d->h * d->w;
+    hipLaunchKernelGGL(cin1_fwd_kernel<T>, dim3((unsigned)nott::ceil_div(pix, 256)), dim3(256), 0, ctx->stream, x, w,
+                       b, y, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k);
+    return nott::launch_status(ctx, "conv2d_fwd (1 input channel)");
+}
+
+template <typename T>
+int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
+    float* part = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)d->k * kCin1Slabs * 9));
+    if (!part) return NOTT_ERR_ALLOC;
+    hipLaunchKernelGGL(cin1_wgrad_partial_kernel<T>, dim3((unsigned)d->k, kCin1Slabs), dim3(256), 0, ctx->stream, x,
+                       dy, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, part);
+    hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 9, (int64_t)256)), dim3(256), 0,
+                       ctx->stream, part, (int32_t)d->k, dw, accumulate);
+    return nott::launch_status(ctx, "conv2d_bwd_weight (1 input channel)");
+}
+
 template <typename T>
 int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* w, const float* b,
         void* y) {
@@ -544,6 +666,8 @@ int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const voi
     const int64_t M = d->n * p * q, K = d->c * d->r * d->s;
     if (nott::conv_fast::fwd_applies(d, sizeof(T)))
         return nott::conv_fast::fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
+    if (cin1_applies(d))
+        return cin1_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
     if constexpr (sizeof(T) == 2) {
         if (col_applies(d, p, q, false))
             return col_fwd(ctx, d, p, q, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
@@ -580,6 +704,8 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         const bool aligned = ((uintptr_t)x % 16) == 0 && ((uintptr_t)dy % 16) == 0;
         if (aligned && nott::conv_fast::wgrad_applies(d, sizeof(T))) {
             st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
+        } else if (cin1_applies(d)) {
+            st = cin1_wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
         } else if (sizeof(T) == 2 && col_applies(d, p, q, false)) {
             st = col_wgrad(ctx, d, p, q, reinterpret_cast<const bf16_t*>(x), reinterpret_cast<const bf16_t*>(dy), dw,
                            accumulate);
