@@ -565,7 +565,9 @@ __device__ __forceinline__ void cin1_taps(const T* __restrict__ xp, int32_t h, i
         }
 }
 
-// Thread = one pixel for all k output channels (weights and bias in LDS).
+// Thread = one pixel for kCin1Co output channels (grid.y = channel group;
+// weights and bias in LDS).
+constexpr int kCin1Co = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, const T* __restrict__ wt,
                                                        const float* __restrict__ b, T* __restrict__ y, int32_t n,
@@ -582,7 +584,8 @@ __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, 
     float t[9];
     cin1_taps<T>(x + img * hw, h, w, H, W, t);
     T* yp = y + img * k * hw + in;
-    for (int co = 0; co < k; ++co) {
+    const int co1 = min(k, (int)(blockIdx.y + 1) * kCin1Co);
+    for (int co = blockIdx.y * kCin1Co; co < co1; ++co) {
         float a = lb[co];
 #pragma unroll
         for (int j = 0; j < 9; ++j) a = __builtin_fmaf(t[j], lw[co * 9 + j], a);
@@ -590,7 +593,7 @@ __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, 
     }
 }
 
-constexpr int kCin1Slabs = 16;
+constexpr int kCin1Slabs = 64;
 
 // Workgroup (co, slab): 9 partial sums over the slab's images.
 template <typename T>
@@ -643,8 +646,9 @@ __global__ __launch_bounds__(256) void cin1_wgrad_finish_kernel(const float* __r
 template <typename T>
 int cin1_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
     const int64_t pix = d->n * d->h * d->w;
-    hipLaunchKernelGGL(cin1_fwd_kernel<T>, dim3((unsigned)nott::ceil_div(pix, 256)), dim3(256), 0, ctx->stream, x, w,
-                       b, y, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k);
+    hipLaunchKernelGGL(cin1_fwd_kernel<T>, dim3((unsigned)nott::ceil_div(pix, 256), (unsigned)nott::ceil_div(d->k, (int64_t)kCin1Co)),
+                       dim3(256), 0, ctx->stream, x, w, b, y, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w,
+                       (int32_t)d->k);
     return nott::launch_status(ctx, "conv2d_fwd (1 input channel)");
 }
 
