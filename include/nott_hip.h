@@ -90,6 +90,11 @@ typedef struct nott_conv2d_desc {
  * backward (conv.hpp:177 forward). */
 int nott_conv2d_fwd(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
                     const void* x, const void* w, const float* b, void* y);
+/* y = relu(conv(x, w) + b) when relu = 1 (0: as nott_conv2d_fwd): the layer
+ * with the activation Nott applies after it (apply.hpp:24-57, relu.hpp:13;
+ * src/core.hpp:1933), fused into the convolution's epilogue where it has one. */
+int nott_conv2d_fwd_act(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                        const void* x, const void* w, const float* b, int relu, void* y);
 /* dgrad: dx = conv_transpose(dy, w).  (ATen convolution_backward, input grad) */
 int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
                          const void* dy, const void* w, void* dx);

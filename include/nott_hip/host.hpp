@@ -145,6 +145,45 @@ struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
     }
 };
 
+// Conv2d followed by ReLU, the activation fused into the convolution's
+// forward (nott_conv2d_fwd_act); backward = ReLU mask from the saved output,
+// then the convolution's gradients.
+struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b, std::vector<int64_t> geom) {
+        x = contig(x);
+        const nott_conv2d_desc d = Conv2dFn::desc(x, wc, geom);
+        const int64_t p = (d.h + 2 * d.pad_h - d.dil_h * (d.r - 1) - 1) / d.stride_h + 1;
+        const int64_t q = (d.w + 2 * d.pad_w - d.dil_w * (d.s - 1) - 1) / d.stride_w + 1;
+        Tensor y = torch::empty({d.n, d.k, p, q}, x.options());
+        nott_ctx c = bind(x);
+        check(nott_conv2d_fwd_act(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), 1, ptr(y)), c, "conv2d+relu forward");
+        ctx->save_for_backward({x, w, wc, b, y});
+        ctx->saved_data["geom"] = geom;
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3], y = s[4];
+        Tensor dy = contig(grads[0]);
+        const auto geom = ctx->saved_data["geom"].toIntVector();
+        const nott_conv2d_desc d = Conv2dFn::desc(x, wc, geom);
+        nott_ctx c = bind(dy);
+        Tensor dz = torch::empty_like(dy);
+        check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "relu backward");
+        Tensor dx;
+        if (ctx->saved_data["needs_dx"].toBool()) {
+            dx = torch::empty_like(x);
+            check(nott_conv2d_bwd_data(c, &d, dtype_of(dz), ptr(dz), ptr(wc), ptr(dx)), c, "conv2d dgrad");
+        }
+        Tensor gw = grad_buffer(w), gb = grad_buffer(b);
+        if (gw.defined() || gb.defined())
+            check(nott_conv2d_bwd_weight(c, &d, dtype_of(dz), ptr(x), ptr(dz), fptr(gw), fptr(gb), 1), c,
+                  "conv2d wgrad");
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
 // --------------------------------------------------------------- Linear
 struct LinearFn : torch::autograd::Function<LinearFn> {
     static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b) {
@@ -511,6 +550,11 @@ public:
     Tensor forward(const Tensor& x) {
         const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
         return Conv2dFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
+    }
+    // relu(forward(x)) with the activation fused into the convolution.
+    Tensor forward_relu(const Tensor& x) {
+        const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
+        return Conv2dReluFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
     }
     Tensor weight, bias, weight_compute;
 private:

@@ -288,3 +288,19 @@ def test_conv3x3_large_grids(ops, case):
     ref_dx = torch.nn.grad.conv2d_input((n, c, h, w_), w.float(), dy.float(), padding=1)
     check(host(y), host(ref_y), "bf16", "y vs torch fp32")
     check(host(dx), host(ref_dx), "bf16", "dx vs torch fp32")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", [CONV[5], CONV[6], CONV[2], CONV[3], (2, 32, 10, 10, 64, 3, 3, 1, 1, 1)],
+                         ids=lambda c: "n{}c{}h{}w{}k{}r{}s{}st{}".format(*c[:8]))
+def test_conv_fwd_relu_fused(ops, dt, case):
+    """nott_conv2d_fwd_act(relu=1) equals the ReLU of the plain forward, bit
+    for bit, on every forward path (single channel, 3×3 MFMA with and without
+    split-K, column path, generic GEMM + separate ReLU)."""
+    d = _desc(ops, case)
+    x, w, b, _ = _inputs(case, dt, 3 + sum(case))
+    xd, wd, bd = dev(x, dt), dev(w, dt), dev(b)
+    y = ops.conv2d_fwd(xd, wd, bd, d)
+    yr = ops.conv2d_fwd(xd, wd, bd, d, relu=True)
+    torch.cuda.synchronize()
+    assert torch.equal(yr, torch.relu(y))

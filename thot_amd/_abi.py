@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
     "nott_device_errors": [vp, C.POINTER(i64)],
     "nott_workspace_bytes": [vp, C.POINTER(i64)],
     "nott_conv2d_fwd": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, vp],
+    "nott_conv2d_fwd_act": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, i32, vp],
     "nott_conv2d_bwd_data": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, vp],
     "nott_conv2d_bwd_weight": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, fp, i32],
     "nott_linear_fwd": [vp, i32, i64, i64, i64, vp, vp, fp, vp],

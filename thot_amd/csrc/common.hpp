@@ -216,6 +216,9 @@ __device__ __forceinline__ float lane_f32(float v) {
 
 // Full 64-lane sum; every lane receives the result.  Within a row of 16
 // lanes: DPP quad_perm / half-mirror / mirror; across rows: lane reads.
+// ReLU as torch::relu computes it (reference relu.hpp:13): a NaN passes.
+__device__ __forceinline__ float relu_out(float x) { return (x > 0.f || x != x) ? x : 0.f; }
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]

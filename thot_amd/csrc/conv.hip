@@ -571,7 +571,7 @@ constexpr int kCin1Co = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, const T* __restrict__ wt,
                                                        const float* __restrict__ b, T* __restrict__ y, int32_t n,
-                                                       int32_t H, int32_t W, int32_t k) {
+                                                       int32_t H, int32_t W, int32_t k, int relu) {
     __shared__ float lw[256 * 9], lb[256];
     for (int i = threadIdx.x; i < k * 9; i += 256) lw[i] = Io<T>::ld(wt, i);
     for (int i = threadIdx.x; i < k; i += 256) lb[i] = b ? b[i] : 0.f;
@@ -589,7 +589,7 @@ __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, 
         float a = lb[co];
 #pragma unroll
         for (int j = 0; j < 9; ++j) a = __builtin_fmaf(t[j], lw[co * 9 + j], a);
-        Io<T>::st(yp, (int64_t)co * hw, a);
+        Io<T>::st(yp, (int64_t)co * hw, relu ? relu_out(a) : a);
     }
 }
 
@@ -644,11 +644,11 @@ __global__ __launch_bounds__(256) void cin1_wgrad_finish_kernel(const float* __r
 }
 
 template <typename T>
-int cin1_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
+int cin1_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu) {
     const int64_t pix = d->n * d->h * d->w;
     hipLaunchKernelGGL(cin1_fwd_kernel<T>, dim3((unsigned)nott::ceil_div(pix, 256), (unsigned)nott::ceil_div(d->k, (int64_t)kCin1Co)),
                        dim3(256), 0, ctx->stream, x, w, b, y, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w,
-                       (int32_t)d->k);
+                       (int32_t)d->k, relu);
     return nott::launch_status(ctx, "conv2d_fwd (1 input channel)");
 }
 
@@ -663,15 +663,12 @@ int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy,
     return nott::launch_status(ctx, "conv2d_bwd_weight (1 input channel)");
 }
 
+// Convolution without a fused activation (the paths whose epilogue has none).
 template <typename T>
-int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* w, const float* b,
-        void* y) {
+int fwd_plain(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* w,
+              const float* b, void* y) {
     const Geom g = make_geom(d, p, q);
     const int64_t M = d->n * p * q, K = d->c * d->r * d->s;
-    if (nott::conv_fast::fwd_applies(d, sizeof(T)))
-        return nott::conv_fast::fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
-    if (cin1_applies(d))
-        return cin1_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
     if constexpr (sizeof(T) == 2) {
         if (col_applies(d, p, q, false))
             return col_fwd(ctx, d, p, q, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y));
@@ -681,6 +678,21 @@ int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const voi
     RowKLoader<T> lb{static_cast<const T*>(w), K, d->k, K, v};
     FwdStore<T> ep{static_cast<T*>(y), b, g, M};
     return run<T>(ctx, la, lb, ep, M, d->k, K, 1);
+}
+
+// relu = 1: y = relu(conv(x) + b), fused into the 3×3 and single-channel
+// epilogues, a separate in-place ReLU pass after the other paths.
+template <typename T>
+int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* x, const void* w, const float* b,
+        void* y, int relu) {
+    if (nott::conv_fast::fwd_applies(d, sizeof(T)))
+        return nott::conv_fast::fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b,
+                                       static_cast<T*>(y), relu);
+    if (cin1_applies(d))
+        return cin1_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y), relu);
+    const int st = fwd_plain<T>(ctx, d, p, q, x, w, b, y);
+    if (st != NOTT_OK || !relu) return st;
+    return nott_relu_fwd(ctx, sizeof(T) == 2 ? NOTT_BF16 : NOTT_F32, d->n * d->k * p * q, y, y);
 }
 
 template <typename T>
@@ -737,17 +749,23 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
 
 }  // namespace
 
-extern "C" int nott_conv2d_fwd(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x, const void* w,
-                               const float* b, void* y) {
+extern "C" int nott_conv2d_fwd_act(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x,
+                                   const void* w, const float* b, int relu, void* y) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_fwd: bad dtype");
+    NOTT_REQUIRE(ctx, relu == 0 || relu == 1, "nott_conv2d_fwd_act: relu must be 0 or 1");
     int64_t p, q;
     int st = check_desc(ctx, d, &p, &q);
     if (st != NOTT_OK) return st;
     if (d->n == 0) return NOTT_OK;
     NOTT_REQUIRE(ctx, x && w && y, "nott_conv2d_fwd: null buffer");
     nott::DeviceScope scope(ctx->device);
-    return dtype == NOTT_F32 ? fwd<float>(ctx, d, p, q, x, w, b, y) : fwd<bf16_t>(ctx, d, p, q, x, w, b, y);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, d, p, q, x, w, b, y, relu) : fwd<bf16_t>(ctx, d, p, q, x, w, b, y, relu);
+}
+
+extern "C" int nott_conv2d_fwd(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x, const void* w,
+                               const float* b, void* y) {
+    return nott_conv2d_fwd_act(ctx, d, dtype, x, w, b, 0, y);
 }
 
 extern "C" int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* dy,

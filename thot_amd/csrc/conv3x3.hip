@@ -57,6 +57,7 @@ struct SameParams {
     int32_t in_rows;           // LDS rows reserved for the input tile
     int32_t remap;             // XCD-aware block remap active
     int32_t vec_store;         // 16-byte output runs stay inside one image plane
+    int32_t relu;              // ReLU on the output (forward with a fused activation)
     int32_t cc_per_split;      // channel chunks per blockIdx.z split
     float* partial;            // split partials [split][cout][npix] (fp32, no bias), or null
     FastDiv fd_hw, fd_w, fd_w2, fd_h2;
@@ -426,7 +427,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const int px = wid * 64 + mt * 16 + kq * 4;
-            const f32x4 v = acc[mt][nt] + bv;
+            f32x4 v = acc[mt][nt] + bv;
+            if (p.relu) {
+                v.x = relu_out(v.x); v.y = relu_out(v.y); v.z = relu_out(v.z); v.w = relu_out(v.w);
+            }
             Vec4<T>::st(reinterpret_cast<T*>(lds_o + col * OP + px * (int)sizeof(T)), v);
         }
     }
@@ -461,7 +465,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void conv3x3_split_reduce_kernel(const float* __restrict__ partial, int32_t splits,
                                                                    int32_t cout, int32_t npix, FastDiv fd_hw,
                                                                    int32_t hw, const float* __restrict__ bias,
-                                                                   T* __restrict__ out) {
+                                                                   T* __restrict__ out, int relu) {
     const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;     // group of 4 pixels
     const int32_t groups = npix >> 2;
     if (q >= (int64_t)groups * cout) return;
@@ -475,7 +479,8 @@ __global__ __launch_bounds__(256) void conv3x3_split_reduce_kernel(const float* 
     for (int e = 0; e < 4; ++e) {
         uint32_t n, pix;
         fd_hw.divmod((uint32_t)(m + e), n, pix);
-        Io<T>::st(out, ((int64_t)n * cout + co) * hw + pix, s[e] + bv);
+        const float v = s[e] + bv;
+        Io<T>::st(out, ((int64_t)n * cout + co) * hw + pix, relu ? relu_out(v) : v);
     }
 }
 
@@ -513,7 +518,7 @@ int wgrad_load_width(int64_t w, size_t elem) {
 
 template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
-             const float* bias, T* out) {
+             const float* bias, T* out, int relu = 0) {
     constexpr int CC = Chunk<T>::CC;
     const int64_t cbc = ceil_div(cout, kTileCo);                 // 64-channel blocks (the last may be partial)
     const size_t wbytes = sizeof(T) * (size_t)cbc * kTileCo * cin * 9;
@@ -547,6 +552,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     p.fd_w2 = FastDiv((uint32_t)row_pitch(w));
     p.fd_h2 = FastDiv((uint32_t)(h + 2));
     p.cc_per_split = cc_per_split;
+    p.relu = relu;
     p.partial = splits > 1 ? reinterpret_cast<float*>(ws + wbytes_al) : nullptr;
     p.remap = (tiles % 8 == 0) ? 1 : 0;
     p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
@@ -576,7 +582,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
                            in, wp, bias, out, p);
     if (splits > 1)
         hipLaunchKernelGGL(conv3x3_split_reduce_kernel<T>, dim3((unsigned)ceil_div(npix64 / 4 * cout, 256)), dim3(256), 0,
-                           ctx->stream, p.partial, splits, cout, p.npix, p.fd_hw, p.hw, bias, out);
+                           ctx->stream, p.partial, splits, cout, p.npix, p.fd_hw, p.hw, bias, out, p.relu);
     return launch_status(ctx, "conv3x3_same");
 }
 
@@ -925,8 +931,9 @@ bool wgrad_applies(const nott_conv2d_desc* d, size_t elem) {
 
 
 template <typename T>
-int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y) {
-    return run_same<T, false>(ctx, (int32_t)d->n, (int32_t)d->c, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, x, w, b, y);
+int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu) {
+    return run_same<T, false>(ctx, (int32_t)d->n, (int32_t)d->c, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, x, w, b, y,
+                              relu);
 }
 
 template <typename T>
@@ -957,8 +964,8 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, floa
     }
 }
 
-template int fwd<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, const float*, float*);
-template int fwd<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, const float*, bf16_t*);
+template int fwd<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, const float*, float*, int);
+template int fwd<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, const float*, bf16_t*, int);
 template int dgrad<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, float*);
 template int dgrad<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, bf16_t*);
 template int wgrad<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, float*, int);

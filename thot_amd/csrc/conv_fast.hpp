@@ -11,7 +11,7 @@ bool dgrad_applies(const nott_conv2d_desc* d, size_t elem);
 bool wgrad_applies(const nott_conv2d_desc* d, size_t elem);
 
 template <typename T>
-int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y);
+int fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu = 0);
 template <typename T>
 int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* dx);
 template <typename T>

@@ -35,8 +35,8 @@ struct SmallCNNImpl : torch::nn::Module {
         fc1 = register_module("fc_6", NH::Linear(128, 10));
     }
     Tensor forward(Tensor x) {
-        x = pool0(NH::relu(conv0(x)));   // Conv + ReLU, MaxPool2
-        x = pool1(NH::relu(conv1(x)));
+        x = pool0(conv0->forward_relu(x));   // Conv + ReLU (fused), MaxPool2
+        x = pool1(conv1->forward_relu(x));
         x = flat(x);                     // Flatten (a view)
         x = NH::relu(fc0(x));
         return fc1(x);

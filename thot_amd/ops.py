@@ -381,14 +381,17 @@ def _conv_shapes(d: Conv2dDesc):
     return (d.n, d.h, d.w, d.c), (d.n, p, q, d.k)
 
 
-def conv2d_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor], d: Conv2dDesc) -> torch.Tensor:
+def conv2d_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor], d: Conv2dDesc,
+               relu: bool = False) -> torch.Tensor:
+    """y = conv(x, w) + b, or relu of it with relu=True (fused where the kernel allows)."""
     xs, ys = _conv_shapes(d)
     _check(x, "x", shape=xs)
     _check(w, "w", shape=(d.k, d.c, d.r, d.s), dtype=x.dtype, device=x.device)
     if b is not None:
         _check(b, "b", shape=(d.k,), dtype=torch.float32, device=x.device)
     y = torch.empty(ys, dtype=x.dtype, device=x.device)
-    _ctx_for(x).call("nott_conv2d_fwd", C.byref(d), nott_dtype(x.dtype), _ptr(x), _ptr(w), _ptr(b), _ptr(y))
+    _ctx_for(x).call("nott_conv2d_fwd_act", C.byref(d), nott_dtype(x.dtype), _ptr(x), _ptr(w), _ptr(b), int(relu),
+                     _ptr(y))
     return y
 
 
