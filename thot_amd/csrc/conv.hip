@@ -543,9 +543,9 @@ int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) 
 // K = 9 is all overhead, so these are direct kernels.
 //   fwd  : y[n, co, h, w] = b[co] + Σ_{r,s} x[n, 0, h+r−1, w+s−1] · wt[co, 0, r, s]
 //   wgrad: dw[co, 0, r, s] = Σ_{n,h,w} dy[n, co, h, w] · x[n, 0, h+r−1, w+s−1]
-// (db keeps its own two-pass kernels).  wgrad is deterministic: workgroup
-// (co, slab of images) writes 9 partial sums, and a second pass adds the
-// slabs in order.
+//   db   : db[co] = Σ_{n,h,w} dy[n, co, h, w]  (a tenth sum of the same pass)
+// wgrad is deterministic: workgroup (co, slab of images) writes 10 partial
+// sums, and a second pass adds the slabs in order.
 // ---------------------------------------------------------------------------
 bool cin1_applies(const nott_conv2d_desc* d) {
     return d->layout == NOTT_NCHW && d->groups == 1 && d->c == 1 && d->r == 3 && d->s == 3 && d->stride_h == 1 &&
@@ -600,14 +600,14 @@ template <typename T>
 __global__ __launch_bounds__(256) void cin1_wgrad_partial_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                  int32_t n, int32_t H, int32_t W, int32_t k,
                                                                  float* __restrict__ part) {
-    __shared__ float red[4][9];
+    __shared__ float red[4][10];
     const int co = blockIdx.x, slab = blockIdx.y;
     const int64_t hw = (int64_t)H * W;
     const int32_t per = (n + kCin1Slabs - 1) / kCin1Slabs;
     const int32_t n0 = slab * per, n1 = min(n, n0 + per);
-    float acc[9];
+    float acc[10];       // 9 taps, then Σ dy
 #pragma unroll
-    for (int j = 0; j < 9; ++j) acc[j] = 0.f;
+    for (int j = 0; j < 10; ++j) acc[j] = 0.f;
     for (int32_t img = n0; img < n1; ++img) {
         const T* xp = x + (int64_t)img * hw;
         const T* dp = dy + ((int64_t)img * k + co) * hw;
@@ -618,29 +618,33 @@ __global__ __launch_bounds__(256) void cin1_wgrad_partial_kernel(const T* __rest
             const float g = Io<T>::ld(dp, in);
 #pragma unroll
             for (int j = 0; j < 9; ++j) acc[j] = __builtin_fmaf(g, t[j], acc[j]);
+            acc[9] += g;
         }
     }
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 9; ++j) {
+    for (int j = 0; j < 10; ++j) {
         const float v = wave_sum(acc[j]);
         if (lane == 0) red[wid][j] = v;
     }
     __syncthreads();
-    if (threadIdx.x < 9) {
+    if (threadIdx.x < 10) {
         const int j = threadIdx.x;
-        part[((int64_t)co * kCin1Slabs + slab) * 9 + j] = (red[0][j] + red[1][j]) + (red[2][j] + red[3][j]);
+        part[((int64_t)co * kCin1Slabs + slab) * 10 + j] = (red[0][j] + red[1][j]) + (red[2][j] + red[3][j]);
     }
 }
 
 __global__ __launch_bounds__(256) void cin1_wgrad_finish_kernel(const float* __restrict__ part, int32_t k,
-                                                                float* __restrict__ dw, int accumulate) {
-    const int i = blockIdx.x * 256 + threadIdx.x;     // co·9 + tap
-    if (i >= k * 9) return;
-    const int co = i / 9, j = i - co * 9;
+                                                                float* __restrict__ dw, float* __restrict__ db,
+                                                                int accumulate) {
+    const int i = blockIdx.x * 256 + threadIdx.x;     // co·10 + j (j = tap, or 9 for the bias)
+    if (i >= k * 10) return;
+    const int co = i / 10, j = i - co * 10;
+    float* out = j < 9 ? (dw ? dw + co * 9 + j : nullptr) : (db ? db + co : nullptr);
+    if (!out) return;
     float s = 0.f;
-    for (int z = 0; z < kCin1Slabs; ++z) s += part[((int64_t)co * kCin1Slabs + z) * 9 + j];
-    dw[i] = accumulate ? dw[i] + s : s;
+    for (int z = 0; z < kCin1Slabs; ++z) s += part[((int64_t)co * kCin1Slabs + z) * 10 + j];
+    *out = accumulate ? *out + s : s;
 }
 
 template <typename T>
@@ -653,13 +657,14 @@ int cin1_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, co
 }
 
 template <typename T>
-int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
-    float* part = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)d->k * kCin1Slabs * 9));
+int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, float* db,
+               int accumulate) {
+    float* part = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)d->k * kCin1Slabs * 10));
     if (!part) return NOTT_ERR_ALLOC;
     hipLaunchKernelGGL(cin1_wgrad_partial_kernel<T>, dim3((unsigned)d->k, kCin1Slabs), dim3(256), 0, ctx->stream, x,
                        dy, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, part);
-    hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 9, (int64_t)256)), dim3(256), 0,
-                       ctx->stream, part, (int32_t)d->k, dw, accumulate);
+    hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 10, (int64_t)256)), dim3(256), 0,
+                       ctx->stream, part, (int32_t)d->k, dw, db, accumulate);
     return nott::launch_status(ctx, "conv2d_bwd_weight (1 input channel)");
 }
 
@@ -721,7 +726,9 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         if (aligned && nott::conv_fast::wgrad_applies(d, sizeof(T))) {
             st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
         } else if (cin1_applies(d)) {
-            st = cin1_wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
+            // the bias gradient comes out of the same pass
+            st = cin1_wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, db, accumulate);
+            db = nullptr;
         } else if (sizeof(T) == 2 && col_applies(d, p, q, false)) {
             st = col_wgrad(ctx, d, p, q, reinterpret_cast<const bf16_t*>(x), reinterpret_cast<const bf16_t*>(dy), dw,
                            accumulate);
