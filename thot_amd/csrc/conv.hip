@@ -382,10 +382,7 @@ __global__ __launch_bounds__(256) void to_kn_kernel(const T* __restrict__ dy, Ge
 
 // dx[n,c,h,w] = Σ over (r, s) whose source output position is exact and in range.
 template <typename T>
-__global__ __launch_bounds__(256) void col2im_kernel(const T* __restrict__ dcol, Geom g, int32_t NPQ, T* __restrict__ dx) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)g.n * g.c * g.h * g.w;
-    if (i >= total) return;
+__device__ __forceinline__ float col2im_at(const T* __restrict__ dcol, const Geom& g, int32_t NPQ, int64_t i) {
     uint32_t nc, hw, h, w, n, c;
     g.fd_hw.divmod((uint32_t)i, nc, hw);
     g.fd_w.divmod(hw, h, w);
@@ -407,7 +404,32 @@ __global__ __launch_bounds__(256) void col2im_kernel(const T* __restrict__ dcol,
             acc += Io<T>::ld(dcol, crs * NPQ + ((int64_t)n * g.p + pp) * g.q + qq);
         }
     }
-    Io<T>::st(dx, i, acc);
+    return acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_kernel(const T* __restrict__ dcol, Geom g, int32_t NPQ, T* __restrict__ dx) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)g.n * g.c * g.h * g.w;
+    if (i >= total) return;
+    Io<T>::st(dx, i, col2im_at<T>(dcol, g, NPQ, i));
+}
+
+// Two horizontally adjacent outputs per thread (even image width): at stride
+// 2 the two gather from neighbouring output columns, so consecutive lanes
+// read consecutive columns of dcol; one 2-element store.
+template <typename T>
+__global__ __launch_bounds__(256) void col2im2_kernel(const T* __restrict__ dcol, Geom g, int32_t NPQ,
+                                                      T* __restrict__ dx) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;
+    const int64_t total = (int64_t)g.n * g.c * g.h * g.w;
+    if (i >= total) return;
+    const float a = col2im_at<T>(dcol, g, NPQ, i), b = col2im_at<T>(dcol, g, NPQ, i + 1);
+    if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint32_t*>(dx + i) = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    } else {
+        *reinterpret_cast<float2*>(dx + i) = make_float2(a, b);
+    }
 }
 
 // y[n, k, pq] = acc + b[k] for GEMM (m = k, n = npq).
@@ -511,8 +533,12 @@ int col_dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, con
     const int st = fast::run<true, true>(ctx, wp, CRSp, dyt, NPQ, ep, CRSp, NPQ, d->k, 0,
                                          reinterpret_cast<float*>(ws + o_part));
     if (st != NOTT_OK) return st;
-    hipLaunchKernelGGL(col2im_kernel<bf16_t>, dim3((unsigned)ceil_div(d->n * d->c * d->h * d->w, 256)), dim3(256), 0,
-                       ctx->stream, dcol, g, (int32_t)NPQ, dx);
+    if (d->w % 2 == 0 && ((uintptr_t)dx % 4) == 0)
+        hipLaunchKernelGGL(col2im2_kernel<bf16_t>, dim3((unsigned)ceil_div(d->n * d->c * d->h * d->w / 2, 256)), dim3(256),
+                           0, ctx->stream, dcol, g, (int32_t)NPQ, dx);
+    else
+        hipLaunchKernelGGL(col2im_kernel<bf16_t>, dim3((unsigned)ceil_div(d->n * d->c * d->h * d->w, 256)), dim3(256), 0,
+                           ctx->stream, dcol, g, (int32_t)NPQ, dx);
     return nott::launch_status(ctx, "conv col2im");
 }
 
