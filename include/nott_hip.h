@@ -51,9 +51,14 @@ typedef enum { NOTT_NCHW = 0, NOTT_NHWC = 1 } nott_layout;
 typedef struct nott_ctx_s* nott_ctx;
 
 /* ---- context --------------------------------------------------------- */
-/* Owns: device id, the launch stream, a grow-only workspace arena and a
- * device error word.  Replaces nothing in the reference (libtorch keeps
- * this state in its caching allocator and per-device stream pool). */
+/* Owns: device id, the launch stream, a workspace arena and a device error
+ * word.  When a call needs more workspace, a new arena (at least twice the
+ * size) is allocated and the old one is kept, not freed, until nott_destroy:
+ * a HIP graph captured earlier keeps its workspace pointer valid, and no
+ * stream is synchronised for growth.  The workspace is shared by every call
+ * on the context, so calls on different streams that overlap race on it.
+ * Replaces nothing in the reference (libtorch keeps this state in its
+ * caching allocator and per-device stream pool). */
 int nott_create(int device, nott_ctx* out);
 int nott_destroy(nott_ctx ctx);
 int nott_set_stream(nott_ctx ctx, void* hip_stream);   /* NULL = legacy default stream */

@@ -31,6 +31,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "nott_hip.h"
@@ -89,12 +90,50 @@ inline float* fptr(const Tensor& t) { return present(t) ? t.data_ptr<float>() : 
 
 inline Tensor contig(const Tensor& t) { return t.is_contiguous() ? t : t.contiguous(); }
 
+// Gradient buffers a fused optimizer keeps in its flat arena, by parameter.
+// A parameter whose .grad() was reset to none (Optimizer::zero_grad(true))
+// gets its arena slice back, zeroed, the next time a backward writes it, so
+// one fused launch still sees every gradient.
+namespace detail {
+inline std::mutex& arena_mutex() {
+    static std::mutex mu;
+    return mu;
+}
+inline std::unordered_map<const c10::TensorImpl*, Tensor>& arena_grads() {
+    static std::unordered_map<const c10::TensorImpl*, Tensor> m;
+    return m;
+}
+inline Tensor arena_grad(const Tensor& p) {
+    std::lock_guard<std::mutex> g(arena_mutex());
+    auto it = arena_grads().find(p.unsafeGetTensorImpl());
+    return it == arena_grads().end() ? Tensor() : it->second;
+}
+// A tensor over `arena`'s storage at element offset `off` with the given
+// shape (contiguous).  It shares memory with the arena but is not an
+// autograd view, so libtorch's Optimizer::zero_grad may detach_ it.
+inline Tensor alias(const Tensor& arena, int64_t off, at::IntArrayRef sizes) {
+    torch::NoGradGuard ng;
+    std::vector<int64_t> strides(sizes.size(), 1);
+    for (int64_t i = (int64_t)sizes.size() - 2; i >= 0; --i) strides[i] = strides[i + 1] * sizes[i + 1];
+    Tensor t = torch::empty({0}, arena.options());
+    t.set_(arena.storage(), arena.storage_offset() + off, sizes, strides);
+    return t;
+}
+}  // namespace detail
+
 // Ensures p.grad() exists (zeros) so that backward can accumulate into it.
 inline Tensor grad_buffer(const Tensor& p) {
     if (!present(p) || !p.requires_grad()) return Tensor();
     if (!p.grad().defined()) {
         torch::NoGradGuard ng;
-        const_cast<Tensor&>(p).mutable_grad() = torch::zeros_like(p);
+        Tensor g = detail::arena_grad(p);
+        if (g.defined()) {
+            nott_ctx c = bind(g);
+            check(nott_zero(c, g.numel() * (int64_t)g.element_size(), g.data_ptr()), c, "gradient re-attach");
+        } else {
+            g = torch::zeros_like(p);
+        }
+        const_cast<Tensor&>(p).mutable_grad() = g;
     }
     return p.grad();
 }
@@ -583,25 +622,42 @@ public:
         bias = register_parameter("bias", torch::zeros({c}));
         running_mean = register_buffer("running_mean", torch::zeros({c}));
         running_var = register_buffer("running_var", torch::ones({c}));
+        // torch::nn::BatchNorm2d's third buffer, kept for the checkpoint
+        // layout.  With a fixed momentum it only counts training forwards;
+        // the count is kept on the host (count_batch) and written into the
+        // buffer by sync_counter() before a save.
+        num_batches_tracked = register_buffer("num_batches_tracked", torch::zeros({}, torch::kLong));
     }
     Tensor forward(const Tensor& x) {
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        ++batches_;
         return BatchNorm2dFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
     }
     // relu(BN(x)): the layer with its ReLU activation, fused.
     Tensor forward_relu(const Tensor& x) {
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        ++batches_;
         return BatchNorm2dReluFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
     }
     // relu(BN(x) + skip): the residual branch's last layer, skip addition and
     // final ReLU, fused.
     Tensor forward_add_relu(const Tensor& x, const Tensor& skip) {
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        ++batches_;
         return BatchNorm2dAddReluFn::apply(x, skip, weight, bias, running_mean, running_var, eps_, momentum_);
     }
-    Tensor weight, bias, running_mean, running_var;
+    // A forward replayed from a captured graph (no host code ran), or one
+    // recorded during capture / undone by a warm-up (not run as a step).
+    void count_batch() { ++batches_; }
+    void uncount(int64_t n) { batches_ -= n; }
+    void sync_counter() {
+        torch::NoGradGuard ng;
+        num_batches_tracked.fill_(batches_);
+    }
+    Tensor weight, bias, running_mean, running_var, num_batches_tracked;
 private:
     double eps_, momentum_;
+    int64_t batches_ = 0;
 };
 TORCH_MODULE(BatchNorm2d);
 
@@ -624,7 +680,9 @@ inline void save_module_host(const torch::nn::Module& m, torch::serialize::Outpu
         ar.write(c.key(), child);
     }
 }
-inline void save_parameters(const torch::nn::Module& m, const std::string& path) {
+inline void save_parameters(torch::nn::Module& m, const std::string& path) {
+    for (auto& child : m.modules(/*include_self=*/true))
+        if (auto* bn = child->as<BatchNorm2dImpl>()) bn->sync_counter();
     torch::serialize::OutputArchive ar;
     save_module_host(m, ar);
     ar.save_to(path);
@@ -655,6 +713,45 @@ public:
     Tensor forward(const Tensor& x) { return x.flatten(1); }
 };
 TORCH_MODULE(Flatten);
+// AdaptiveAvgPool2d({1, 1}) (pooling.hpp:164-167): no parameters or buffers.
+class AdaptiveAvgPool2dImpl : public torch::nn::Module {
+public:
+    Tensor forward(const Tensor& x) { return AvgPoolGlobalFn::apply(x); }
+};
+TORCH_MODULE(AdaptiveAvgPool2d);
+
+// The residual block Nott builds from
+//   Block::Residual({Conv2d(in→out, 3×3, stride s, pad 1, no bias),
+//                    BatchNorm2d(out) + ReLU, Conv2d(out→out, 3×3, pad 1, no bias),
+//                    BatchNorm2d(out)},
+//                   1, {projection: Conv2d(in→out, 1×1, stride s, no bias)},
+//                   {final_activation: ReLU})
+// (block/details/blocks/residual.hpp:37-141): the layers registered as
+// conv2d_0, batchnorm2d_1, conv2d_2, batchnorm2d_3 and the projection as
+// conv2d_4 (residual.hpp:49-62), so checkpoint keys match the reference's.
+// forward = relu(bn3(conv2(relu(bn1(conv0(x))))) + skip(x)) with skip the
+// projection or the identity (residual.hpp:87-132); the layer ReLU and the
+// skip addition + final ReLU run fused into the BatchNorm apply passes.
+class ResidualBasicBlockImpl : public torch::nn::Module {
+public:
+    ResidualBasicBlockImpl(int64_t in, int64_t out, int64_t stride, bool projection) {
+        conv0 = register_module("conv2d_0", Conv2d(Conv2dOptions{in, out, {3, 3}, {stride, stride}, {1, 1}, {1, 1}, false}));
+        bn1 = register_module("batchnorm2d_1", BatchNorm2d(out));
+        conv2 = register_module("conv2d_2", Conv2d(Conv2dOptions{out, out, {3, 3}, {1, 1}, {1, 1}, {1, 1}, false}));
+        bn3 = register_module("batchnorm2d_3", BatchNorm2d(out));
+        if (projection)
+            proj = register_module("conv2d_4", Conv2d(Conv2dOptions{in, out, {1, 1}, {stride, stride}, {0, 0}, {1, 1}, false}));
+    }
+    Tensor forward(const Tensor& x) {
+        auto f = ForkFn::apply(x);   // x feeds the branch and the skip
+        Tensor h = bn1->forward_relu(conv0(f[0]));
+        Tensor skip = proj ? proj(f[1]) : f[1];
+        return bn3->forward_add_relu(conv2(h), skip);
+    }
+    Conv2d conv0{nullptr}, conv2{nullptr}, proj{nullptr};
+    BatchNorm2d bn1{nullptr}, bn3{nullptr};
+};
+TORCH_MODULE(ResidualBasicBlock);
 
 inline Tensor cross_entropy(const Tensor& logits, const Tensor& labels, double label_smoothing = 0.0) {
     return CrossEntropyFn::apply(logits, labels, label_smoothing);
@@ -672,85 +769,222 @@ inline void he_uniform_(Tensor& w, torch::Generator& gen) {
 }
 
 // ============================================================ optimizer
-// Fused Adam / AdamW over one flat arena (reference optimizer/details/adam.hpp:
-// 63-154, 159-250; stepped at core.hpp:3820, zero_grad(false) at :3823).
-// Every parameter and its gradient are re-pointed into flat fp32 buffers,
-// so one nott_adam_step launch updates all of them, then zeroes the grads.
-// Mixed precision: bf16 working copies of the given weights live in a flat
-// bf16 arena and are refreshed with one nott_cast after each step.
-class FusedAdam {
+// Fused Adam / AdamW behind libtorch's optimizer interface: a drop-in for
+// Nott::Optimizer::Details::Adam / AdamW (reference optimizer/details/adam.hpp:
+// 63-154, 159-250), which Model::set_optimizer holds as a
+// std::unique_ptr<torch::optim::Optimizer> (core.hpp:170-181, 1364-1381) and
+// Model::step_optimizers steps through the virtual step() (core.hpp:
+// 5049-5057).  Same constructors (parameters or parameter groups, the torch
+// options, warm-up buckets), same param_groups() whose options() a scheduler
+// rewrites with set_lr (lrscheduler/details/cosineannealing.hpp:52-63), and a
+// state() with one AdamParamState / AdamWParamState per parameter.
+//
+// Layout: at construction every parameter and its gradient are moved into
+// flat fp32 arenas (P, G, M, V), one contiguous range per param group with
+// 256-byte aligned segments.  A parameter keeps its identity (set_data onto
+// its arena slice); its .grad() and its state's exp_avg / exp_avg_sq are
+// tensors over the arenas' storage, so step() is one nott_adam_step launch
+// per group, reading the group's options at call time.  libtorch's own
+// Optimizer::zero_grad(false) (what Nott's Model::zero_grad calls, core.hpp:
+// 2425-2442) zeroes the arena slices in place; after zero_grad(true) the
+// host modules re-attach each parameter's arena slice when a backward next
+// writes it (grad_buffer).
+//
+// set_fused_zero_grad(true) makes step() also clear the gradients in the same
+// pass, for callers that always follow step() with zero_grad() as
+// Model::run_training_step does (core.hpp:3819-3823).
+//
+// Mixed precision: bf16 working copies of chosen weights live in a flat bf16
+// arena aligned like the masters and are refreshed with one nott_cast after
+// each step.  amsgrad is not supported (std::invalid_argument), nor is
+// serialising the optimizer state (Nott's checkpoint stores parameters only).
+template <bool Decoupled>
+class FusedAdamImpl : public torch::optim::Optimizer {
 public:
-    struct Options {
-        double lr = 1e-3, beta1 = 0.9, beta2 = 0.999, eps = 1e-8, weight_decay = 0.0;
-        bool decoupled = false;   // false: Adam (L2), true: AdamW
-    };
-    FusedAdam(std::vector<Tensor> params, Options o, std::vector<Tensor*> bf16_copies = {},
-              std::vector<Tensor> bf16_masters = {})
-        : o_(o) {
-        torch::NoGradGuard ng;
-        if (params.empty()) throw std::invalid_argument("FusedAdam: no parameters");
-        const auto dev = params[0].device();
-        int64_t total = 0;
-        std::vector<int64_t> off;
-        for (auto& p : params) {
-            off.push_back(total);
-            total += (p.numel() + 63) / 64 * 64;   // 256-byte aligned segments
+    using TorchOptions = std::conditional_t<Decoupled, torch::optim::AdamWOptions, torch::optim::AdamOptions>;
+    using ParamState = std::conditional_t<Decoupled, torch::optim::AdamWParamState, torch::optim::AdamParamState>;
+
+    FusedAdamImpl(std::vector<Tensor> params, const TorchOptions& options,
+                  std::vector<std::vector<Tensor>> warmup_buckets = {})
+        : torch::optim::Optimizer(std::move(params), std::make_unique<TorchOptions>(options)) {
+        (void)warmup_buckets;   // state is created eagerly; the buckets only order warm-up in the reference
+        build();
+    }
+    FusedAdamImpl(const std::vector<torch::optim::OptimizerParamGroup>& groups, const TorchOptions& options,
+                  std::vector<std::vector<Tensor>> warmup_buckets = {})
+        : torch::optim::Optimizer(groups, std::make_unique<TorchOptions>(options)) {
+        (void)warmup_buckets;
+        build();
+    }
+    ~FusedAdamImpl() override {
+        std::lock_guard<std::mutex> g(detail::arena_mutex());
+        for (auto* impl : registered_) detail::arena_grads().erase(impl);
+    }
+
+    // Updates every parameter whose gradient is defined, as
+    // torch::optim::Adam[W]::step does (a parameter whose .grad() is none is
+    // skipped and keeps its step count).  Consecutive parameters with a
+    // gradient and the same step count form one segment of the arena, and
+    // each segment is one nott_adam_step launch with its group's options at
+    // call time: one launch per group in the usual case.  A gradient tensor
+    // assigned from outside is copied into the arena first.
+    Tensor step(LossClosure closure = nullptr) override {
+        Tensor loss;
+        if (closure) {
+            torch::AutoGradMode enable(true);
+            loss = closure();
         }
-        auto fo = torch::TensorOptions().dtype(torch::kFloat32).device(dev);
+        if (param_groups_.size() != group_count_)
+            throw std::logic_error("FusedAdam: parameter groups were added after construction");
+        if (!P_.defined()) return loss;
+        torch::NoGradGuard ng;
+        nott_ctx c = bind(P_);
+        struct Seg { int64_t off, end, step; };
+        for (auto& group : param_groups_) {
+            const auto& o = static_cast<const TorchOptions&>(group.options());
+            std::vector<Seg> segs;
+            for (auto& p : group.params()) {
+                auto it = offsets_.find(p.unsafeGetTensorImpl());
+                if (it == offsets_.end()) continue;   // does not require grad
+                const int64_t off = it->second, len = (p.numel() + 63) / 64 * 64;
+                Tensor gv = p.grad();
+                if (!gv.defined()) continue;
+                float* slot = G_.data_ptr<float>() + off;
+                if (gv.data_ptr() != (void*)slot) {
+                    Tensor a = detail::alias(G_, off, p.sizes());
+                    a.copy_(gv);
+                    p.mutable_grad() = a;
+                }
+                auto& st = static_cast<ParamState&>(*state_.at(p.unsafeGetTensorImpl()));
+                const int64_t t = st.step() + 1;
+                st.step(t);
+                if (!segs.empty() && segs.back().end == off && segs.back().step == t) segs.back().end = off + len;
+                else segs.push_back({off, off + len, t});
+            }
+            for (const auto& sg : segs)
+                check(nott_adam_step(c, Decoupled ? 1 : 0, sg.end - sg.off, P_.data_ptr<float>() + sg.off, NOTT_F32,
+                                     G_.data_ptr<float>() + sg.off, NOTT_F32, M_.data_ptr<float>() + sg.off,
+                                     V_.data_ptr<float>() + sg.off, o.lr(), std::get<0>(o.betas()),
+                                     std::get<1>(o.betas()), o.eps(), o.weight_decay(), sg.step, fuse_zero_ ? 1 : 0),
+                      c, "adam step");
+        }
+        if (Pb_.defined()) refresh();
+        return loss;
+    }
+
+    // The reference's warm-up hook (adam.hpp:98-150, called through
+    // OptimizerBinding::warmup): the state already exists, nothing to do.
+    void ensure_state_initialized() {}
+
+    void set_fused_zero_grad(bool on) { fuse_zero_ = on; }
+
+    // Clears every gradient with one kernel (what Optimizer::zero_grad(false)
+    // does with one fill per parameter).
+    void zero_flat_grads() {
+        if (!G_.defined()) return;
+        nott_ctx c = bind(G_);
+        check(nott_zero(c, G_.numel() * 4, G_.data_ptr()), c, "zero_grad");
+    }
+
+    // bf16 working copies: *copies[j] becomes a bf16 view of masters[j]'s
+    // values, refreshed after every step (and by refresh()).
+    void attach_bf16_copies(const std::vector<Tensor*>& copies, const std::vector<Tensor>& masters) {
+        if (copies.size() != masters.size()) throw std::invalid_argument("FusedAdam: copy/master mismatch");
+        if (copies.empty()) return;
+        torch::NoGradGuard ng;
+        Pb_ = torch::zeros({P_.numel()}, P_.options().dtype(torch::kBFloat16));
+        for (size_t j = 0; j < masters.size(); ++j) {
+            auto it = offsets_.find(masters[j].unsafeGetTensorImpl());
+            if (it == offsets_.end()) throw std::invalid_argument("FusedAdam: bf16 master not among params");
+            *copies[j] = detail::alias(Pb_, it->second, masters[j].sizes());
+        }
+        refresh();
+    }
+    // Re-casts the bf16 working copies (after parameters were overwritten).
+    void refresh() {
+        if (!Pb_.defined()) return;
+        nott_ctx c = bind(P_);
+        check(nott_cast(c, P_.numel(), P_.data_ptr(), NOTT_F32, Pb_.data_ptr(), NOTT_BF16), c, "bf16 copy");
+    }
+    // Step count of a parameter's state (0 before its first update).
+    int64_t step_count(const Tensor& p) const {
+        auto it = state_.find(p.unsafeGetTensorImpl());
+        return it == state_.end() ? 0 : static_cast<const ParamState&>(*it->second).step();
+    }
+    const Tensor& flat_params() const { return P_; }
+    const Tensor& flat_grads() const { return G_; }
+
+    void save(torch::serialize::OutputArchive&) const override {
+        throw std::logic_error("FusedAdam: optimizer state serialisation is not supported");
+    }
+    void load(torch::serialize::InputArchive&) override {
+        throw std::logic_error("FusedAdam: optimizer state serialisation is not supported");
+    }
+
+private:
+    void build() {
+        torch::NoGradGuard ng;
+        int64_t total = 0;
+        c10::optional<torch::Device> dev;
+        std::vector<std::vector<int64_t>> offs(param_groups_.size());
+        for (size_t gi = 0; gi < param_groups_.size(); ++gi) {
+            const auto& o = static_cast<const TorchOptions&>(param_groups_[gi].options());
+            if (o.amsgrad()) throw std::invalid_argument("FusedAdam: amsgrad is not supported");
+            for (const auto& p : param_groups_[gi].params()) {
+                offs[gi].push_back(-1);
+                if (!p.defined() || !p.requires_grad()) continue;
+                if (p.scalar_type() != torch::kFloat32) throw std::invalid_argument("FusedAdam: parameters must be float32");
+                if (!p.is_cuda()) throw std::invalid_argument("FusedAdam: parameters must live on a HIP device");
+                if (dev && *dev != p.device()) throw std::invalid_argument("FusedAdam: parameters on several devices");
+                dev = p.device();
+                offs[gi].back() = total;
+                total += (p.numel() + 63) / 64 * 64;   // 256-byte aligned segments
+            }
+        }
+        group_count_ = param_groups_.size();
+        if (total == 0) return;
+        auto fo = torch::TensorOptions().dtype(torch::kFloat32).device(*dev);
         P_ = torch::zeros({total}, fo);
         G_ = torch::zeros({total}, fo);
         M_ = torch::zeros({total}, fo);
         V_ = torch::zeros({total}, fo);
-        for (size_t i = 0; i < params.size(); ++i) {
-            auto& p = params[i];
-            Tensor pv = P_.narrow(0, off[i], p.numel()).view(p.sizes());
-            pv.copy_(p.detach());
-            p.set_data(pv);
-            p.mutable_grad() = G_.narrow(0, off[i], p.numel()).view(p.sizes());
-        }
-        params_ = params;
-        // bf16 working copies: one arena aligned like the masters.
-        if (!bf16_copies.empty()) {
-            if (bf16_copies.size() != bf16_masters.size()) throw std::invalid_argument("FusedAdam: copy/master mismatch");
-            Pb_ = torch::zeros({total}, fo.dtype(torch::kBFloat16));
-            for (size_t j = 0; j < bf16_masters.size(); ++j) {
-                size_t i = 0;
-                while (i < params.size() && !params[i].is_same(bf16_masters[j])) ++i;
-                if (i == params.size()) throw std::invalid_argument("FusedAdam: bf16 master not among params");
-                *bf16_copies[j] = Pb_.narrow(0, off[i], params[i].numel()).view(params[i].sizes());
+        std::lock_guard<std::mutex> g(detail::arena_mutex());
+        for (size_t gi = 0; gi < param_groups_.size(); ++gi) {
+            auto& params = param_groups_[gi].params();
+            for (size_t k = 0; k < params.size(); ++k) {
+                const int64_t off = offs[gi][k];
+                if (off < 0) continue;
+                auto& p = params[k];
+                Tensor pv = detail::alias(P_, off, p.sizes());
+                pv.copy_(p.detach());
+                p.set_data(pv);
+                // A gradient that exists moves into the arena; one that does
+                // not is attached (zeroed) by the first backward that writes it.
+                Tensor gv = detail::alias(G_, off, p.sizes());
+                if (p.grad().defined()) {
+                    gv.copy_(p.grad());
+                    p.mutable_grad() = gv;
+                }
+                auto st = std::make_unique<ParamState>();
+                st->step(0);
+                st->exp_avg(detail::alias(M_, off, p.sizes()));
+                st->exp_avg_sq(detail::alias(V_, off, p.sizes()));
+                state_[p.unsafeGetTensorImpl()] = std::move(st);
+                detail::arena_grads()[p.unsafeGetTensorImpl()] = gv;
+                registered_.push_back(p.unsafeGetTensorImpl());
+                offsets_[p.unsafeGetTensorImpl()] = off;
             }
-            refresh_copies();
         }
     }
-    void step() {
-        ++t_;
-        nott_ctx c = bind(P_);
-        check(nott_adam_step(c, o_.decoupled ? 1 : 0, P_.numel(), ptr(P_), NOTT_F32, ptr(G_), NOTT_F32, fptr(M_),
-                             fptr(V_), o_.lr, o_.beta1, o_.beta2, o_.eps, o_.weight_decay, t_, 1),
-              c, "adam step");
-        if (Pb_.defined()) refresh_copies();
-    }
-    void zero_grad() {
-        nott_ctx c = bind(G_);
-        check(nott_zero(c, G_.numel() * 4, ptr(G_)), c, "zero_grad");
-    }
-    // Re-casts the bf16 working copies (after parameters were overwritten).
-    void refresh() {
-        if (Pb_.defined()) refresh_copies();
-    }
-    int64_t step_count() const { return t_; }
-    void set_lr(double lr) { o_.lr = lr; }
-    const Tensor& flat_params() const { return P_; }
-private:
-    void refresh_copies() {
-        nott_ctx c = bind(P_);
-        check(nott_cast(c, P_.numel(), ptr(P_), NOTT_F32, ptr(Pb_), NOTT_BF16), c, "bf16 copy");
-    }
-    Options o_;
-    std::vector<Tensor> params_;
+
+    size_t group_count_ = 0;
+    std::vector<const c10::TensorImpl*> registered_;
+    std::unordered_map<const c10::TensorImpl*, int64_t> offsets_;
     Tensor P_, G_, M_, V_, Pb_;
-    int64_t t_ = 0;
+    bool fuse_zero_ = false;
 };
+using FusedAdam = FusedAdamImpl<false>;    // Nott::Optimizer::Details::Adam
+using FusedAdamW = FusedAdamImpl<true>;    // Nott::Optimizer::Details::AdamW
 
 }  // namespace HIP
 }  // namespace Nott

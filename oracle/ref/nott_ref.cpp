@@ -28,6 +28,7 @@
 #include "attention/details/head.hpp"
 
 #include <chrono>
+#include <optional>
 #include <cstring>
 #include <stdexcept>
 
@@ -163,58 +164,120 @@ struct SmallCnnRef {
     }
 };
 
-// ResNet-18 (7x7/2 stem + BN + ReLU + 3x3/2 max-pool, 4 stages of
-// 2 basic blocks, global average pool, FC 512->1000) from the same layer
-// descriptors; the residual add and the post-add ReLU are what Nott's
-// residual block applies (block/details/blocks/residual.hpp:131-132).
-struct ResNet18Ref {
-    Chain c;
-    struct Block { size_t c0, b0, c1, b1; long sc = -1, sb = -1; };
-    size_t stem, stem_bn, pool, gap, flat, fc;
-    std::vector<Block> blocks;
-    ResNet18Ref() {
-        stem = c.add(conv_d(3, 64, 7, 2, 3, false, false));
-        stem_bn = c.add(bn_d(64, true));
-        pool = c.add(maxpool_d(3, 2, 1));
-        int64_t in = 64;
-        const int64_t widths[4] = {64, 128, 256, 512};
-        for (int st = 0; st < 4; ++st) {
-            for (int j = 0; j < 2; ++j) {
-                const int64_t out = widths[st], stride = (st > 0 && j == 0) ? 2 : 1;
-                Block b;
-                b.c0 = c.add(conv_d(in, out, 3, stride, 1, false, false));
-                b.b0 = c.add(bn_d(out, true));
-                b.c1 = c.add(conv_d(out, out, 3, 1, 1, false, false));
-                b.b1 = c.add(bn_d(out, false));
-                if (stride != 1 || in != out) {
-                    b.sc = (long)c.add(conv_d(in, out, 1, stride, 0, false, false));
-                    b.sb = (long)c.add(bn_d(out, false));
-                }
-                blocks.push_back(b);
-                in = out;
-            }
-        }
-        Nott::Layer::Details::AdaptiveAvgPool2dOptions ao;
-        ao.output_size = {1, 1};
-        gap = c.add(Nott::Layer::Details::PoolingDescriptor{ao});
-        flat = c.add(Nott::Layer::Details::FlattenDescriptor{});
-        fc = c.add(fc_d(512, 1000, false));
+// Rounds a tensor to bf16 and back in the forward, and its gradient the same
+// way in the backward: placed where a bf16 mixed-precision implementation
+// stores activations (and, in the backward, the gradients of those
+// activations), it turns the fp32 reference into the same computation with
+// bf16 storage.
+struct RoundBF16 : torch::autograd::Function<RoundBF16> {
+    static torch::Tensor forward(torch::autograd::AutogradContext*, torch::Tensor x) {
+        return x.to(torch::kBFloat16).to(x.scalar_type());
     }
-    torch::Tensor forward(torch::Tensor x) {
-        x = c.run(pool, c.run(stem_bn, c.run(stem, x)));
-        for (auto& b : blocks) {
-            auto y = c.run(b.b1, c.run(b.c1, c.run(b.b0, c.run(b.c0, x))));
-            auto s = b.sc >= 0 ? c.run((size_t)b.sb, c.run((size_t)b.sc, x)) : x;
-            x = torch::relu(y + s);
+    static torch::autograd::variable_list backward(torch::autograd::AutogradContext*,
+                                                   torch::autograd::variable_list g) {
+        return {g[0].to(torch::kBFloat16).to(g[0].scalar_type())};
+    }
+};
+inline torch::Tensor store(torch::Tensor t, bool bf16) { return bf16 ? RoundBF16::apply(t) : t; }
+
+// Nott's residual block (block/details/blocks/residual.hpp:37-141) cannot be
+// compiled here: residual.hpp includes layer/layer.hpp, whose
+// details/recurrent.hpp:14 includes <ATen/cuda/CUDAContext.h>, which needs
+// the CUDA runtime headers this ROCm image does not have.  ResidualRef
+// restates the block over the reference's own layer factories, which do
+// compile: one repeat of its layers registered by build_registered_layer on
+// the block with running indices, then the projection (residual.hpp:49-62),
+// and the forward of residual.hpp:87-132 — the branch through every layer
+// and its activation, the skip through the projection and its activation,
+// their sum, then the final activation (dropout 0 registers nothing).
+struct ResidualRef : torch::nn::Module {
+    std::vector<Nott::Layer::Details::RegisteredLayer> layers;
+    std::optional<Nott::Layer::Details::RegisteredLayer> projection;
+    Nott::Activation::Type final_activation;
+    template <class... D>
+    ResidualRef(Nott::Activation::Type final_act, const std::optional<Nott::Layer::Details::Conv2dDescriptor>& proj,
+                const D&... ds)
+        : final_activation(final_act) {
+        size_t index = 0;
+        (layers.push_back(Nott::Layer::Details::build_registered_layer(*this, ds, index++)), ...);
+        if (proj) projection = Nott::Layer::Details::build_registered_layer(*this, *proj, index++);
+    }
+    // bf16: activations stored in bf16 after each layer but the last (whose
+    // output is summed with the skip before one rounding), after the
+    // projection and after the final activation.
+    torch::Tensor forward(torch::Tensor input, bool bf16 = false) {
+        auto branch = input;
+        for (size_t i = 0; i < layers.size(); ++i) {
+            branch = Nott::Activation::Details::apply(layers[i].activation, layers[i].forward(branch));
+            if (i + 1 < layers.size()) branch = store(branch, bf16);
         }
-        return c.run(fc, c.run(flat, c.run(gap, x)));
+        auto skip = input;
+        if (projection)
+            skip = store(Nott::Activation::Details::apply(projection->activation, projection->forward(skip)), bf16);
+        return store(Nott::Activation::Details::apply(final_activation, branch + skip), bf16);
     }
 };
 
+// ResNet-18 assembled the way a Nott model registers it
+// (core.hpp:516-523 layers, 576-592 residual blocks): the stem Conv2d,
+// BatchNorm2d with ReLU and MaxPool2d under conv2d_0 / batchnorm2d_1 /
+// maxpool2d_2, eight residual blocks under residual_block_3 ..
+// residual_block_10 ({Conv2d, BatchNorm2d+ReLU, Conv2d, BatchNorm2d}, a 1×1
+// stride-2 Conv2d projection on each down-sampling block, final ReLU), then
+// adaptive_avgpool2d_11, flatten_12 and fc_13.
+struct ResNet18Ref {
+    Owner owner;
+    std::vector<Nott::Layer::Details::RegisteredLayer> head, tail;
+    std::vector<std::shared_ptr<ResidualRef>> blocks;
+    size_t index = 0;
+    ResNet18Ref() {
+        head.push_back(Nott::Layer::Details::build_registered_layer(owner, conv_d(3, 64, 7, 2, 3, false, false), index++));
+        head.push_back(Nott::Layer::Details::build_registered_layer(owner, bn_d(64, true), index++));
+        head.push_back(Nott::Layer::Details::build_registered_layer(owner, maxpool_d(3, 2, 1), index++));
+        int64_t in = 64;
+        const int64_t widths[4] = {64, 128, 256, 512};
+        for (int st = 0; st < 4; ++st)
+            for (int j = 0; j < 2; ++j) {
+                const int64_t out = widths[st], stride = (st > 0 && j == 0) ? 2 : 1;
+                std::optional<Nott::Layer::Details::Conv2dDescriptor> proj;
+                if (stride != 1 || in != out) proj = conv_d(in, out, 1, stride, 0, false, false);
+                auto block = std::make_shared<ResidualRef>(Nott::Activation::Type::ReLU, proj,
+                                                           conv_d(in, out, 3, stride, 1, false, false), bn_d(out, true),
+                                                           conv_d(out, out, 3, 1, 1, false, false), bn_d(out, false));
+                blocks.push_back(owner.register_module("residual_block_" + std::to_string(index++), block));
+                in = out;
+            }
+        Nott::Layer::Details::AdaptiveAvgPool2dOptions ao;
+        ao.output_size = {1, 1};
+        tail.push_back(Nott::Layer::Details::build_registered_layer(owner, Nott::Layer::Details::PoolingDescriptor{ao}, index++));
+        tail.push_back(Nott::Layer::Details::build_registered_layer(owner, Nott::Layer::Details::FlattenDescriptor{}, index++));
+        tail.push_back(Nott::Layer::Details::build_registered_layer(owner, fc_d(512, 1000, false), index++));
+    }
+    static torch::Tensor run(const Nott::Layer::Details::RegisteredLayer& l, torch::Tensor x) {
+        return Nott::Activation::Details::apply(l.activation, l.forward(std::move(x)));
+    }
+    // Model::forward over the registered layers (core.hpp:1926-1936); the
+    // stem output and every block output go to `outs` when given.
+    // bf16: every layer's output stored in bf16 (the flatten is a view).
+    torch::Tensor forward(torch::Tensor x, std::vector<torch::Tensor>* outs = nullptr, bool bf16 = false) {
+        for (auto& l : head) x = store(run(l, x), bf16);
+        if (outs) outs->push_back(x);
+        for (auto& b : blocks) {
+            x = b->forward(x, bf16);
+            if (outs) outs->push_back(x);
+        }
+        for (auto& l : tail) x = store(run(l, x), bf16);
+        return x;
+    }
+};
+
+torch::nn::Module& owner_of(SmallCnnRef& n) { return n.c.owner; }
+torch::nn::Module& owner_of(ResNet18Ref& n) { return n.owner; }
+
 template <class Net>
 double time_train_steps(Net& net, torch::Tensor x, torch::Tensor y, bool decoupled, int iters) {
-    net.c.owner.train();
-    std::vector<torch::Tensor> params = net.c.owner.parameters();
+    owner_of(net).train();
+    std::vector<torch::Tensor> params = owner_of(net).parameters();
     Nott::Loss::Details::CrossEntropyDescriptor ce;
     auto run = [&](auto& opt) {
         auto step = [&] {   // core.hpp:3757-3823: forward, loss, backward, step, zero_grad
@@ -589,6 +652,85 @@ int ref_small_cnn_forward_archive(const char* path, int64_t batch, const float* 
         torch::NoGradGuard ng;
         auto y = net.forward(in(x, {batch, 1, 28, 28}));
         out(y, logits);
+    });
+}
+
+// One configs[4] training step of the reference's ResNet-18 (ResNet18Ref) on
+// the CPU, in the order of Model::run_training_step (core.hpp:3757-3823):
+// forward in training mode, CrossEntropy mean (ce.hpp:21-37), backward,
+// AdamW(lr, weight_decay) step (adam.hpp:159-250).  Tensors are exchanged by
+// their registration keys: for each of the `count` names, init[i] (nullable)
+// sets the parameter or float buffer before the step, grads_out[i]
+// (nullable) receives the parameter's gradient, after_out[i] (nullable) its
+// value after the step (buffers: after the forward).  block_outs (nullable)
+// receives the stem output and the 8 block outputs, in that order.
+//
+// precision 1 runs the same step with the model, input, loss and optimizer
+// in double precision (the exact-arithmetic yardstick both fp32 paths are
+// measured against); results are still returned as fp32.  precision 2 runs
+// it in fp32 with every activation and activation gradient rounded to bf16
+// where a bf16 mixed-precision step stores them (RoundBF16).
+int ref_resnet18_step(int64_t batch, const float* x, const int64_t* labels, double lr, double weight_decay,
+                      int64_t count, const char* const* names, const float* const* init, float* const* grads_out,
+                      float* const* after_out, float* loss, float* logits, float* const* block_outs, int precision) {
+    return guarded([&] {
+        ResNet18Ref net;
+        net.owner.train();
+        auto params = net.owner.named_parameters(true);
+        auto bufs = net.owner.named_buffers(true);
+        auto find = [&](const char* name) -> torch::Tensor* {
+            if (auto* p = params.find(name)) return p;
+            if (auto* b = bufs.find(name)) return b;
+            throw std::runtime_error(std::string("no parameter or buffer ") + name);
+        };
+        {
+            torch::NoGradGuard ng;
+            for (int64_t i = 0; i < count; ++i)
+                if (init && init[i]) {
+                    torch::Tensor* t = find(names[i]);
+                    t->copy_(in(init[i], t->sizes().vec()));
+                }
+        }
+        auto xt = in(x, {batch, 3, 224, 224});
+        if (precision == 1) {
+            net.owner.to(torch::kDouble);
+            xt = xt.to(torch::kDouble);
+            params = net.owner.named_parameters(true);
+            bufs = net.owner.named_buffers(true);
+        }
+        std::vector<torch::Tensor> outs;
+        auto z = net.forward(xt, block_outs ? &outs : nullptr, precision == 2);
+        out(z, logits);
+        Nott::Loss::Details::CrossEntropyDescriptor ce;
+        auto l = Nott::Loss::Details::compute(ce, z, in64(labels, {batch}));
+        if (loss) *loss = (float)l.item<double>();
+        l.backward();
+        for (int64_t i = 0; i < count; ++i)
+            if (grads_out && grads_out[i]) out(find(names[i])->grad(), grads_out[i]);
+        if (block_outs)
+            for (size_t j = 0; j < outs.size(); ++j) out(outs[j], block_outs[j]);
+        Nott::Optimizer::Details::AdamWOptions o;
+        o.learning_rate = lr;
+        o.weight_decay = weight_decay;
+        Nott::Optimizer::Details::AdamW opt(net.owner.parameters(), Nott::Optimizer::Details::to_torch_options(o));
+        opt.step();
+        opt.zero_grad(false);
+        for (int64_t i = 0; i < count; ++i)
+            if (after_out && after_out[i]) out(*find(names[i]), after_out[i]);
+    });
+}
+
+// Loads a parameters.binary archive into the reference's ResNet-18 and runs
+// its training-mode forward on x[batch,3,224,224]; logits [batch,1000].
+int ref_resnet18_forward_archive(const char* path, int64_t batch, const float* x, float* logits) {
+    return guarded([&] {
+        ResNet18Ref net;
+        torch::serialize::InputArchive ar;
+        ar.load_from(std::string(path));
+        net.owner.load(ar);
+        net.owner.train();
+        torch::NoGradGuard ng;
+        out(net.forward(in(x, {batch, 3, 224, 224})), logits);
     });
 }
 

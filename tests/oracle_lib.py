@@ -210,6 +210,12 @@ class Oracle:
         return dq, dk, dv
 
     # adam -------------------------------------------------------------------
+    def round_bf16(self, x):
+        """oracle_round_bf16: fp32 -> nearest bf16 (RNE) -> fp32, elementwise."""
+        x = f32(x).copy()
+        self.lib.oracle_round_bf16(i64(x.size), _p(x))
+        return x
+
     def adam_step(self, decoupled, p, g, m, v, lr, beta1, beta2, eps, weight_decay, step):
         p, m, v = f32(p).copy(), f32(m).copy(), f32(v).copy()
         self.lib.oracle_adam_step(C.c_int(int(decoupled)), i64(p.size), _p(p), _p(f32(g)), _p(m), _p(v), f64(lr),
@@ -332,6 +338,46 @@ class Ref:
         x = f32(x)
         logits = np.empty((x.shape[0], 10), np.float32)
         self._ok(self.lib.ref_small_cnn_forward_archive(C.c_char_p(path.encode()), i64(x.shape[0]), _p(x), _p(logits)))
+        return logits
+
+    def resnet18_step(self, x, labels, values: dict, lr: float, weight_decay: float, want_blocks: bool = False,
+                      precision: str = "f32"):
+        """One configs[4] step of the reference's ResNet-18 on the CPU
+        (forward, CE mean, backward, AdamW).  `values` maps registration keys
+        (parameters and float buffers) to their initial arrays.  Returns
+        (loss, logits, grads, after, blocks): grads of the parameters, every
+        tensor after the step, and the 9 stem/block outputs when asked.
+        precision "f64": the same step in double precision (results as fp32);
+        "bf16_storage": fp32 arithmetic with every activation and activation
+        gradient rounded to bf16 where the mixed-precision path stores them."""
+        x = f32(x)
+        batch = x.shape[0]
+        names = sorted(values)
+        init = [f32(values[k]) for k in names]
+        is_param = [not (k.endswith("running_mean") or k.endswith("running_var")) for k in names]
+        grads = [np.empty_like(a) if ip else None for a, ip in zip(init, is_param)]
+        after = [np.empty_like(a) for a in init]
+        arr = lambda items: (C.c_void_p * len(items))(*[None if a is None else a.ctypes.data for a in items])
+        cname = (C.c_char_p * len(names))(*[k.encode() for k in names])
+        sizes = [(64, 56), (64, 56), (64, 56), (128, 28), (128, 28), (256, 14), (256, 14), (512, 7), (512, 7)]
+        blocks = [np.empty((batch, c, h, h), np.float32) for c, h in sizes] if want_blocks else None
+        loss = C.c_float()
+        logits = np.empty((batch, 1000), np.float32)
+        self._ok(self.lib.ref_resnet18_step(i64(batch), _p(x), _p(np.ascontiguousarray(labels, np.int64)), f64(lr),
+                                            f64(weight_decay), i64(len(names)), cname, arr(init), arr(grads),
+                                            arr(after), C.byref(loss), _p(logits),
+                                            arr(blocks) if want_blocks else None,
+                                            C.c_int({"f32": 0, "f64": 1, "bf16_storage": 2}[precision])))
+        return (loss.value, logits, {k: g for k, g in zip(names, grads) if g is not None},
+                dict(zip(names, after)), blocks)
+
+    def resnet18_forward_archive(self, path: str, x):
+        """configs[4] training-mode logits of the reference's ResNet-18 after
+        loading the parameters.binary archive at `path`."""
+        x = f32(x)
+        logits = np.empty((x.shape[0], 1000), np.float32)
+        self._ok(self.lib.ref_resnet18_forward_archive(C.c_char_p(path.encode()), i64(x.shape[0]), _p(x),
+                                                       _p(logits)))
         return logits
 
     def train_step_time(self, model: str, batch: int, iters: int) -> float:

@@ -146,3 +146,79 @@ def test_attention_token_major(ops, dt, b, h, t, dh, causal):
     assert torch.equal(lse_tm, lse)
     for got, want in zip(outs, (dq, dk, dv)):
         assert torch.equal(got.permute(0, 2, 1, 3), want)
+
+
+# ------------------------------------------------ composed MultiHeadAttention
+def _mha_composed(ops, x2, w_in, b_in, wo, bo, dy2, b, t, heads, causal=True):
+    """MultiHeadAttentionImpl (reference attention/details/head.hpp:47-83 +
+    kernel.hpp:20-96) as the bench composes it: one packed q/k/v projection,
+    token-major attention on views of its output (no head split or merge
+    copies), the output projection; then the backward in reverse, with dq,
+    dk, dv written into the packed gradient the input projection reads."""
+    e = x2.shape[1]
+    dh = e // heads
+    qkv = ops.linear_fwd(x2, w_in, b_in)
+    d = ops.attn_desc(b, heads, t, t, dh, causal, token_major=True, ld_qkv=3 * e)
+    q, k, v = (qkv.view(b, t, 3 * e)[:, :, i * e:(i + 1) * e].view(b, t, heads, dh) for i in range(3))
+    o, lse = ops.attention_fwd(q, k, v, d)
+    a = o.view(b * t, e)
+    y = ops.linear_fwd(a, wo, bo)
+    da, dwo, dbo = ops.linear_bwd(dy2, a, wo)
+    dqkv = torch.empty((b, t, 3 * e), dtype=x2.dtype, device="cuda")
+    views = tuple(dqkv[:, :, i * e:(i + 1) * e].view(b, t, heads, dh) for i in range(3))
+    ops.attention_bwd(q, k, v, o, da.view(b, t, heads, dh), lse, d, out=views)
+    dx, dw_in, db_in = ops.linear_bwd(dqkv.view(b * t, 3 * e), x2, w_in)
+    return y, dx, dw_in, db_in, dwo, dbo
+
+
+def test_mha_module_golden(ops):
+    """The composed module against the reference MultiHeadAttention's own
+    output and gradients (tests/golden/mha_causal.npz, written by head.hpp's
+    module through libtorch): fp32, causal, with biases."""
+    z = np.load(os.path.join(GOLD, "mha_causal.npz"))
+    x = f32(z["x"])
+    b, t, e = x.shape
+    heads = int(z["heads"])
+    w_in = np.concatenate([z["wq"], z["wk"], z["wv"]], 0)
+    b_in = np.concatenate([z["bq"], z["bk"], z["bv"]], 0)
+    y, dx, dw_in, db_in, dwo, dbo = _mha_composed(ops, dev(x.reshape(b * t, e)), dev(w_in), dev(b_in), dev(z["wo"]),
+                                                  dev(z["bo"]), dev(f32(z["dy"]).reshape(b * t, e)), b, t, heads)
+    torch.cuda.synchronize()
+    check(host(y).reshape(b, t, e), z["y"], what="mha y")
+    check(host(dx).reshape(b, t, e), z["dx"], what="mha dx")
+    dw = host(dw_in)
+    db = host(db_in)
+    for i, n in enumerate("qkv"):
+        check(dw[i * e:(i + 1) * e], z["dw" + n], what=f"mha dw{n}")
+        check(db[i * e:(i + 1) * e], z["db" + n], what=f"mha db{n}")
+    check(host(dwo), z["dwo"], what="mha dwo")
+    check(host(dbo), z["dbo"], what="mha dbo")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_mha_projection_shapes_config3(ops, oracle, dt):
+    """configs[3]'s projection GEMMs at full size (8192 tokens, E = 1024: the
+    packed 1024→3072 input projection and the 1024→1024 output projection),
+    forward and backward, on the hand-written GEMMs.  Checked against the
+    oracle on slices: 64 rows of y and dx (all columns), and 16 output rows
+    of dW / db (sums over all 8192 tokens)."""
+    g = rng(31)
+    m, kin = 8192, 1024
+    for nout in (3072, 1024):
+        print(f"projection {m}x{kin}->{nout} {dt}", flush=True)
+        x = host_input(g.standard_normal((m, kin)), dt)
+        w = host_input(g.standard_normal((nout, kin)) * 0.02, dt)
+        bias = f32(g.standard_normal(nout) * 0.1)
+        dy = host_input(g.standard_normal((m, nout)), dt)
+        xd, wd, dyd = dev(x, dt), dev(w, dt), dev(dy, dt)
+        y = ops.linear_fwd(xd, wd, dev(bias))
+        dx, dw, db = ops.linear_bwd(dyd, xd, wd)
+        torch.cuda.synchronize()
+        rows = np.r_[0:32, m - 32:m]
+        check(host(y)[rows], oracle.linear_fwd(x[rows], w, bias), dt, "proj y rows")
+        rdx, _, _ = oracle.linear_bwd(dy[rows], x[rows], w)
+        check(host(dx)[rows], rdx, dt, "proj dx rows")
+        outs = np.r_[0:8, nout - 8:nout]
+        _, rdw, rdb = oracle.linear_bwd(np.ascontiguousarray(dy[:, outs]), x, np.ascontiguousarray(w[outs]))
+        check(host(dw)[outs], rdw, "f32" if dt == "f32" else dt, "proj dw rows")
+        check(host(db)[outs], rdb, "f32" if dt == "f32" else dt, "proj db rows")

@@ -292,3 +292,18 @@ def test_softmax_xent_bad_label_is_reported(ops):
     dl, _ = ops.softmax_xent_bwd(z, y)
     assert ctx.device_errors() == 2
     assert torch.count_nonzero(dl[2:]).item() == 0
+
+
+def test_cast_matches_torch_bf16_conversion(ops):
+    """nott_cast fp32 -> bf16 (the mixed-precision weight copies and input
+    cast) against torch's CPU conversion, bit for bit, on random values over
+    the whole range, exact ties, ±0, ±inf, NaNs, subnormals and overflow to
+    inf; NaN stays NaN with its sign."""
+    from test_oracle import _bf16_specials
+    x = _bf16_specials()
+    got = host(ops.cast(torch.from_numpy(x.copy()).cuda(), torch.bfloat16))
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).to(torch.float32).numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.array_equal(np.signbit(got[nan]), np.signbit(x[nan]))

@@ -5,14 +5,13 @@ Adam/AdamW update all run on libnott_hip.
 configs[0] (small CNN + Adam) is checked step by step against the CPU oracle
 composed layer by layer in the reference's order (core.hpp:3735-3827): loss,
 every parameter gradient, and the updated parameters after two steps.
-configs[4] (ResNet-18 + AdamW) is checked against a float64 torch reference
-of the same network on identical weights and inputs."""
+configs[4] (ResNet-18 + AdamW) is checked at batch 64 against the reference's
+ResNet-18 on the CPU (oracle/_ref) on identical weights and inputs."""
 import math
 
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 from gpu_util import check, host
 from oracle_lib import f32, rng
@@ -110,49 +109,27 @@ def test_small_cnn_two_steps_vs_oracle(host_mod, oracle):
 
 
 # ------------------------------------------------------------- ResNet-18
-class _RoundBF16(torch.autograd.Function):
-    """Rounds to bf16 in both directions: where the bf16 path stores a tensor."""
-
-    @staticmethod
-    def forward(ctx, t):
-        return t.to(torch.bfloat16).to(t.dtype)
-
-    @staticmethod
-    def backward(ctx, g):
-        return g.to(torch.bfloat16).to(g.dtype)
+def _strict(got, want, rtol, atol):
+    """Elements of `got` outside |got − want| <= atol + rtol·|want| (count, worst excess ratio)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bound = atol + rtol * np.abs(want)
+    err = np.abs(got - want)
+    return int((err > bound).sum()), float((err / bound).max()) if err.size else 0.0
 
 
-def resnet18_ref64(params, buffers, x, y, bf16_storage=False):
-    """float64 CPU reference of the host layer's ResNet-18 (same parameter names).
-    bf16_storage: round every op output (forward) and every activation
-    gradient (backward) to bf16, where the mixed-precision path stores them."""
-    P = {k: v.detach().double().cpu().requires_grad_(True) for k, v in params.items()}
-    B = {k: v.detach().double().cpu() for k, v in buffers.items()}
-    q = _RoundBF16.apply if bf16_storage else (lambda t: t)
-
-    def bn(t, name):
-        return q(F.batch_norm(t, B[name + ".running_mean"], B[name + ".running_var"], P[name + ".weight"],
-                              P[name + ".bias"], training=True, momentum=0.1, eps=1e-5))
-
-    def conv(t, name, **kw):
-        return q(F.conv2d(t, P[name], **kw))
-
-    h = conv(q(x.double().cpu()), "stem.weight", stride=2, padding=3)
-    h = q(F.relu(bn(h, "stem_bn")))
-    h = q(F.max_pool2d(h, 3, 2, 1))
-    for s in range(4):
-        for b in range(2):
-            pre = f"block{s}_{b}"
-            stride = 2 if (s > 0 and b == 0) else 1
-            t = q(F.relu(bn(conv(h, pre + ".conv0.weight", stride=stride, padding=1), pre + ".bn0")))
-            t = bn(conv(t, pre + ".conv1.weight", padding=1), pre + ".bn1")
-            skip = conv(h, pre + ".proj.weight", stride=stride) if (pre + ".proj.weight") in P else h
-            h = q(F.relu(q(t + skip)))
-    h = q(F.adaptive_avg_pool2d(h, 1)).flatten(1)
-    z = q(F.linear(h, P["fc.weight"], P["fc.bias"]))
-    loss = F.cross_entropy(z, y.cpu())
-    loss.backward()
-    return loss.item(), {k: v.grad for k, v in P.items()}
+def _ref_inputs(tr, bf16):
+    """The reference's initial tensors: the HIP model's parameters and float
+    buffers by registration key (bf16: conv/linear weights as the bf16
+    working copies the mixed-precision path computes with)."""
+    vals = {k: host(v) for k, v in tr.params().items()}
+    if bf16:
+        from oracle_lib import round_bf16
+        vals = {k: (round_bf16(v) if v.ndim > 1 else v) for k, v in vals.items()}
+    for k, v in tr.buffers().items():
+        if not k.endswith("num_batches_tracked"):
+            vals[k] = host(v)
+    return vals
 
 
 def _rel(a, b):
@@ -161,51 +138,171 @@ def _rel(a, b):
 
 
 @pytest.mark.parametrize("bf16", [False, True], ids=["fp32", "bf16"])
-def test_resnet18_step_vs_float64(host_mod, bf16):
-    """configs[4] architecture, batch 4 at 224x224 (11,687,720 params), against a
-    float64 reference on the same weights and input.
+def test_resnet18_step_batch64_vs_reference(host_mod, bf16):
+    """configs[4] at its size: one full training step (forward, CE mean,
+    backward, AdamW lr 1e-3 wd 1e-2) at batch 64 × 3×224×224 against the
+    reference's ResNet-18 assembled from Nott's own layer factories and
+    residual-block semantics (oracle/_ref, libtorch CPU), on identical weights
+    (loaded by registration key) and inputs.
 
-    Through 20 ReLU layers an activation within rounding of zero can take the
-    other branch in any fp32 implementation and reroute one upstream gradient
-    element, so whole-network gradients are judged per tensor by relative
-    norm (fp32: every tensor within 1e-2, most within 1e-5); the bf16
-    mixed-precision step is judged by direction and scale (cosine > 0.95
-    for every gradient, median > 0.97 at this batch of 4, where batch-norm
-    backward over few samples amplifies bf16 rounding; norms within 10%),
-    while every op is held to elementwise rel 1e-4 in
-    test_gpu_gemm / test_gpu_bandwidth and configs[0] in
-    test_small_cnn_two_steps_vs_oracle."""
-    tr = host_mod.ResNet18Trainer(0, 7, bf16, 1e-3, 1e-2, 1000)
+    fp32.  The loss, the logits, every parameter after AdamW and every
+    BatchNorm running statistic must agree with the reference's fp32 step
+    elementwise at |got − want| <= 1e-5 + 1e-4·|want|.  The gradients are
+    judged against the exact result: the same reference step in float64.
+    Through 20 ReLUs and 20 training-mode BatchNorms at batch 64, the
+    reference's own fp32 gradients are not within that bound of the float64
+    ones (BatchNorm's backward subtracts per-channel sums from each element,
+    and an activation within rounding of zero takes the other ReLU branch in
+    one precision and not the other), so for every one of the 56 gradient
+    tensors the HIP result must be at least as close to float64 as the
+    reference's fp32 result, within a factor 2 (relative norm), and the
+    number of elements outside the bound against float64 must be no larger
+    than the reference's within a factor 2.  All counts, and the ReLU flips
+    at the nine observable ReLU outputs (stem, eight blocks), are printed.
+    Parameters after AdamW are bit-exact against the oracle's AdamW on the
+    step's own gradients, and every element that differs from the
+    reference's updated parameter beyond the bound is one whose gradient has
+    the other sign (step 1 moves a weight by about lr·sign(g)).
+    bf16 mixed precision: the reference runs on the bf16-rounded weights and
+    input, once in plain fp32 and once with every activation and activation
+    gradient rounded to bf16 where this path stores them.  Loss within rel
+    2e-2 of both.  Two bf16-storage computations that differ only in fp32
+    summation order already diverge through 20 layers (values on either side
+    of a bf16 rounding boundary, thousands of ReLU flips per block), so the
+    gradients are judged by what bf16 storage costs: for every tensor the
+    relative-norm distance of the HIP gradient from the fp32 reference must
+    be within 1.5× that of the bf16-storage reference (+1e-3); elementwise
+    counts at rel 2e-2 are printed.  The AdamW update is bit-exact against
+    the oracle on the step's own gradients."""
+    from oracle_lib import Ref, round_bf16
+    if not Ref.available():
+        pytest.skip("oracle/_ref not built")
+    ref = Ref()
+    n = 64
+    g = rng(4242)
+    x = f32(g.uniform(0, 1, (n, 3, 224, 224)))
+    y = g.integers(0, 1000, n).astype(np.int64)
+    tr = host_mod.ResNet18Trainer(0, 17, bf16, 1e-3, 1e-2, 1000)
     assert tr.num_params() == 11687720
-    gen = torch.Generator(device="cuda").manual_seed(11)
-    x = torch.rand((4, 3, 224, 224), generator=gen, device="cuda")
-    y = torch.randint(0, 1000, (4,), generator=gen, device="cuda")
-    params = {k: v.clone() for k, v in tr.params().items()}
-    buffers = {k: v.clone() for k, v in tr.buffers().items()}
-    if bf16:   # the reference sees the rounded weights and input the bf16 path computes with
-        params = {k: (v.to(torch.bfloat16).float() if v.dim() > 1 else v) for k, v in params.items()}
-        x_ref = x.to(torch.bfloat16).float()
-    else:
-        x_ref = x
-    loss = tr.forward_backward(x, y).item()
+    vals = _ref_inputs(tr, bf16)
+    p0 = {k: host(v) for k, v in tr.params().items()}
+    loss_t, outs = tr.forward_backward_recording(torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda())
+    loss = loss_t.item()
     grads = {k: host(v) for k, v in tr.grads().items()}
-    rloss, rgrads = resnet18_ref64(params, buffers, x_ref, y)
-    errs = {k: _rel(grads[k], g.numpy()) for k, g in rgrads.items()}
-    if bf16:
-        # bf16 activations and activation gradients through 20 layers: judge the
-        # direction and scale of every gradient, and the typical one tightly.
-        assert abs(loss - rloss) <= 2e-2 * abs(rloss), (loss, rloss)
-        cos = {}
-        for k, g in rgrads.items():
-            got, want = grads[k].ravel().astype(np.float64), g.numpy().ravel()
-            cos[k] = float(np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want) + 1e-300))
-            assert abs(np.linalg.norm(got) / np.linalg.norm(want) - 1) < 0.1, k
-        assert min(cos.values()) > 0.95, sorted(cos.items(), key=lambda kv: kv[1])[:5]
-        assert float(np.median(list(cos.values()))) > 0.97, sorted(cos.items(), key=lambda kv: kv[1])[:5]
+    outs = [host(o) for o in outs]
+    logits = outs.pop()
+    tr.optimizer_step()
+    after = {k: host(v) for k, v in tr.params().items()}
+    bufs = {k: host(v) for k, v in tr.buffers().items()}
+    assert all(float(torch.count_nonzero(v)) == 0 for v in tr.grads().values())
+    xr = round_bf16(x) if bf16 else x
+    rloss, rlogits, rgrads, rafter, rblocks = ref.resnet18_step(xr, y, vals, 1e-3, 1e-2, want_blocks=True)
+    assert set(rgrads) == set(grads), sorted(set(rgrads) ^ set(grads))
+    flips = [int(((a > 0) != (b > 0)).sum()) for a, b in zip(outs, rblocks)]
+    report = {"loss": (loss, rloss), "relu_flips_vs_ref32": flips}
+    if not bf16:
+        dloss, _, dgrads, _, dblocks = ref.resnet18_step(x, y, vals, 1e-3, 1e-2, want_blocks=True, precision="f64")
+        report["loss_f64"] = dloss
+        report["relu_flips_hip_vs_f64"] = [int(((a > 0) != (b > 0)).sum()) for a, b in zip(outs, dblocks)]
+        report["relu_flips_ref32_vs_f64"] = [int(((a > 0) != (b > 0)).sum()) for a, b in zip(rblocks, dblocks)]
+        assert abs(loss - rloss) <= 1e-5 + 1e-4 * abs(rloss), report
+        report["logits_out_of_tol"] = _strict(logits, rlogits, 1e-4, 1e-5)
+        assert report["logits_out_of_tol"][0] == 0, report
+        rows = {}
+        for k in sorted(rgrads):
+            rows[k] = {"hip_vs_ref32": _strict(grads[k], rgrads[k], 1e-4, 1e-5)[0],
+                       "hip_vs_f64": _strict(grads[k], dgrads[k], 1e-4, 1e-5)[0],
+                       "ref32_vs_f64": _strict(rgrads[k], dgrads[k], 1e-4, 1e-5)[0],
+                       "relnorm_hip_f64": _rel(grads[k], dgrads[k]), "relnorm_ref32_f64": _rel(rgrads[k], dgrads[k])}
+        tot = {c: sum(r[c] for r in rows.values()) for c in ("hip_vs_ref32", "hip_vs_f64", "ref32_vs_f64")}
+        report["grad_elements"] = int(sum(v.size for v in grads.values()))
+        report["out_of_tol_totals"] = tot
+        # Parameters after AdamW: the update is bit-exact on the step's own
+        # gradients.  Against the reference's step, step 1 moves each weight
+        # by lr·g/(|g| + eps) ≈ lr·sign(g), so an element whose gradient is
+        # within the fp32 noise of zero moves differently in the two steps;
+        # every element out of tolerance must be explained by its two
+        # gradients: |Δp| <= lr·|u(g_hip) − u(g_ref)| + tolerance.
+        lr, eps = 1e-3, 1e-8
+        unexplained, out_tol = 0, 0
+        for k in p0:
+            pe, _, _ = oracle_adam(p0[k], grads[k], 1)
+            assert np.array_equal(after[k], pe), k
+            gh, gr = grads[k].astype(np.float64), rgrads[k].astype(np.float64)
+            tol = 1e-5 + 1e-4 * np.abs(rafter[k])
+            dp = np.abs(after[k].astype(np.float64) - rafter[k])
+            du = lr * np.abs(gh / (np.abs(gh) + eps) - gr / (np.abs(gr) + eps))
+            out_tol += int((dp > tol).sum())
+            unexplained += int((dp > du + tol).sum())
+        report["params_out_of_tol"] = out_tol
+        assert unexplained == 0, (unexplained, report)
+        print("resnet18 fp32 batch 64:", report)
+        for k, r in rows.items():
+            print(f"  {k:42s} hip-ref32 {r['hip_vs_ref32']:7d}  hip-f64 {r['hip_vs_f64']:7d}  ref32-f64 "
+                  f"{r['ref32_vs_f64']:7d}  |hip-f64| {r['relnorm_hip_f64']:.2e}  |ref32-f64| {r['relnorm_ref32_f64']:.2e}")
+        for k, r in rows.items():
+            assert r["relnorm_hip_f64"] <= 2 * r["relnorm_ref32_f64"] + 1e-7, (k, r)
+        assert tot["hip_vs_f64"] <= 2 * tot["ref32_vs_f64"] + 100, tot
+        for k, v in bufs.items():
+            if k.endswith("num_batches_tracked"):
+                assert int(v) == 1, (k, v)
+            else:
+                c, w = _strict(v, rafter[k], 1e-4, 1e-5)
+                assert c == 0, (k, c, w)
     else:
-        assert abs(loss - rloss) <= 1e-5 * abs(rloss), (loss, rloss)
-        assert max(errs.values()) < 1e-2, sorted(errs.items(), key=lambda kv: -kv[1])[:5]
-        assert float(np.median(list(errs.values()))) < 1e-5, sorted(errs.items(), key=lambda kv: -kv[1])[:5]
+        # The same reference computation with bf16 storage where this path
+        # stores bf16 (activations and activation gradients), fp32 arithmetic.
+        eloss, _, egrads, _, eblocks = ref.resnet18_step(xr, y, vals, 1e-3, 1e-2, want_blocks=True,
+                                                         precision="bf16_storage")
+        report["loss_bf16_storage_ref"] = eloss
+        report["relu_flips_vs_bf16_storage_ref"] = [int(((a > 0) != (b > 0)).sum()) for a, b in zip(outs, eblocks)]
+        report["grad_relnorm_vs_ref32_max"] = max(_rel(grads[k], rgrads[k]) for k in rgrads)
+        report["grad_relnorm_bf16ref_vs_ref32_max"] = max(_rel(egrads[k], rgrads[k]) for k in rgrads)
+        report["grad_relnorm_vs_bf16_storage_ref"] = {k: round(_rel(grads[k], egrads[k]), 5) for k in sorted(egrads)}
+        rows = {}
+        for k in sorted(rgrads):
+            rows[k] = (_rel(grads[k], rgrads[k]), _rel(egrads[k], rgrads[k]))
+        report["grad_elements_out_of_rel2e-2_vs_ref32"] = int(sum(
+            _strict(grads[k], rgrads[k], 2e-2, 2e-2 * float(np.sqrt(np.mean(rgrads[k].astype(np.float64) ** 2))))[0]
+            for k in rgrads))
+        print("resnet18 bf16 batch 64:", report)
+        for k, (a, b) in rows.items():
+            print(f"  {k:42s} |hip-ref32| {a:.3e}  |bf16ref-ref32| {b:.3e}")
+        assert abs(loss - eloss) <= 2e-2 * abs(eloss), report
+        assert abs(loss - rloss) <= 2e-2 * abs(rloss), report
+        # What bf16 storage itself costs: the reference computation with the
+        # same bf16 storage is as far from the fp32 reference.  The HIP path
+        # may not add more than half as much again on any tensor.
+        for k, (a, b) in rows.items():
+            assert a <= 1.5 * b + 1e-3, (k, a, b)
+        for k in p0:
+            pe, _, _ = oracle_adam(p0[k], grads[k], 1)
+            assert np.array_equal(after[k], pe), k
+
+
+def oracle_adam(p, gr, step):
+    from oracle_lib import Oracle
+    z = np.zeros_like(p)
+    return Oracle().adam_step(1, p, gr, z, z, 1e-3, 0.9, 0.999, 1e-8, 1e-2, step)
+
+
+def test_resnet18_checkpoint_loads_into_reference(host_mod, tmp_path):
+    """parameters.binary of the HIP ResNet-18 (every tensor under Nott's
+    registration keys, residual_block_<i>.conv2d_0.weight ...) loads into the
+    reference's ResNet-18, whose CPU forward then matches the GPU forward."""
+    from oracle_lib import Ref
+    if not Ref.available():
+        pytest.skip("oracle/_ref not built")
+    tr = host_mod.ResNet18Trainer(0, 23, False, 1e-3, 1e-2, 1000)
+    g = rng(77)
+    x = f32(g.uniform(0, 1, (4, 3, 224, 224)))
+    y = g.integers(0, 1000, 4).astype(np.int64)
+    tr.step(torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda())
+    path = str(tmp_path / "parameters.binary")
+    tr.save(path)
+    got = host(tr.forward(torch.from_numpy(x).cuda()))
+    want = Ref().resnet18_forward_archive(path, x)
+    check(got, want, "f32", "ResNet-18 logits after checkpoint round trip")
 
 
 def test_resnet18_loss_decreases(host_mod):
@@ -222,9 +319,11 @@ def test_resnet18_loss_decreases(host_mod):
 @pytest.mark.parametrize("model", ["small_cnn", "resnet18_bf16"])
 def test_graph_step_matches_eager(host_mod, model):
     """The HIP-graph step (forward + loss + backward captured once, replayed
-    per step; fused AdamW eager) against the eager step on a twin trainer:
-    every replay, with eager work and synchronisations between replays, must
-    give the same loss and, at the end, the same parameters bit for bit."""
+    per step; fused AdamW eager) against the eager step on a twin trainer
+    that does no warm-up: every replay, with eager work and synchronisations
+    between replays, must give the same loss and, at the end, the same
+    parameters and buffers (BatchNorm running statistics, batch counters) bit
+    for bit — the capture's warm-up passes leave no trace in the model."""
     def make():
         if model == "small_cnn":
             return host_mod.SmallCNNTrainer(0, 11, 1e-3)
@@ -235,7 +334,6 @@ def test_graph_step_matches_eager(host_mod, model):
     batches = [(torch.rand(shape, generator=gen, device="cuda"),
                 torch.randint(0, classes, (shape[0],), generator=gen, device="cuda")) for _ in range(4)]
     x0, y0 = batches[0]
-    eager.warmup(x0, y0, 2)
     graphed.capture(x0, y0, 2)
     for i, (x, y) in enumerate(batches):
         le = eager.step(x, y)
@@ -244,7 +342,41 @@ def test_graph_step_matches_eager(host_mod, model):
         assert torch.equal(le, lg), (i, le.item(), lg.item())
         _ = (x * 2).sum().item()          # unrelated eager work between replays
     pe, pg = eager.params(), graphed.params()
+    be, bg = eager.buffers(), graphed.buffers()
     torch.cuda.synchronize()
+    for k in pe:
+        assert torch.equal(pe[k], pg[k]), k
+    for k in be:
+        assert torch.equal(be[k], bg[k]), k
+
+
+def test_graph_replay_after_workspace_growth(host_mod):
+    """A captured graph keeps the workspace pointer it was recorded with.  An
+    eager step at a larger batch on the same device afterwards must grow the
+    workspace without freeing the captured one, so later replays still match
+    an eager twin bit for bit."""
+    eager = host_mod.ResNet18Trainer(0, 13, True, 1e-3, 1e-2, 1000)
+    graphed = host_mod.ResNet18Trainer(0, 13, True, 1e-3, 1e-2, 1000)
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    batches = [(torch.rand((2, 3, 224, 224), generator=gen, device="cuda"),
+                torch.randint(0, 1000, (2,), generator=gen, device="cuda")) for _ in range(3)]
+    graphed.capture(*batches[0], 1)
+    before = host_mod.workspace_bytes(0)
+    other = host_mod.ResNet18Trainer(0, 5, True, 1e-3, 1e-2, 1000)
+    for b in (32, 64, 128, 256):   # the workspace is shared by the whole process: grow it past its current size
+        other.step(torch.rand((b, 3, 224, 224), generator=gen, device="cuda"),
+                   torch.randint(0, 1000, (b,), generator=gen, device="cuda"))
+        torch.cuda.synchronize()
+        if host_mod.workspace_bytes(0) > before:
+            break
+    assert host_mod.workspace_bytes(0) > before, (before, host_mod.workspace_bytes(0))
+    del other
+    for i, (x, y) in enumerate(batches):
+        le = eager.step(x, y)
+        lg = graphed.step_graph(x, y)
+        torch.cuda.synchronize()
+        assert torch.equal(le, lg), (i, le.item(), lg.item())
+    pe, pg = eager.params(), graphed.params()
     for k in pe:
         assert torch.equal(pe[k], pg[k]), k
 

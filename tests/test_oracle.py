@@ -13,7 +13,7 @@ import os
 import numpy as np
 import pytest
 
-from oracle_lib import conv_out, f32, rng
+from oracle_lib import conv_out, f32, rng, round_bf16
 from thot_amd._abi import AttnDesc, Conv2dDesc, Pool2dDesc
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -366,3 +366,38 @@ def test_random_cases_against_reference(oracle, ref):
     dl0, loss0 = oracle.softmax_xent(z, lab, 0.05)
     close(dl0, dl)
     close(loss0, loss)
+
+
+# ------------------------------------------------- bf16 rounding, pinned
+def _bf16_specials():
+    """Random values over the whole fp32 range plus the cases rounding gets
+    wrong: exact ties (even and odd lower halves), values just above and below
+    a tie, ±0, ±inf, quiet and signalling NaNs of both signs, fp32 subnormals,
+    the largest finite values (which round to inf) and carries into the
+    exponent."""
+    g = rng(404)
+    u = g.integers(0, 2 ** 32, 20000, dtype=np.uint64).astype(np.uint32)
+    base = g.integers(0, 2 ** 16, 2000, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([base | 0x8000, base | 0x7FFF, base | 0x8001, base | 0xFFFF, base | 0x0001])
+    special = np.array([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00000, 0x7F800001,
+                        0xFF800001, 0x7FBFFFFF, 0x00000001, 0x80000001, 0x007FFFFF, 0x807FFFFF, 0x00008000,
+                        0x00018000, 0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x3F7FFFFF, 0x3F7F8000,
+                        0x3F808000, 0x3F818000], np.uint32)
+    return np.concatenate([u, ties, special]).view(np.float32)
+
+
+def test_round_bf16_matches_torch(oracle):
+    """round_bf16 (tests) and oracle_round_bf16 (oracle.c), which give the
+    oracle the values a bf16 path computes with, agree bit for bit with
+    torch's CPU float32 -> bfloat16 conversion (round to nearest even) on
+    every finite value and infinity, and keep NaN as NaN of the same sign."""
+    import torch
+    x = _bf16_specials()
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).to(torch.float32).numpy()
+    got_py = round_bf16(x)
+    got_c = oracle.round_bf16(x)
+    for got in (got_py, got_c):
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+        assert np.array_equal(np.signbit(got[nan]), np.signbit(x[nan]))

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "nott_hip.h"
 
@@ -15,11 +16,11 @@
 struct nott_ctx_s {
     int device = 0;
     hipStream_t stream = nullptr;
-    void* ws = nullptr;            // grow-only device workspace
+    void* ws = nullptr;            // current device workspace
     size_t ws_bytes = 0;
+    std::vector<void*> retired;    // earlier, smaller workspaces: kept until nott_destroy
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;
-    void* blas = nullptr;          // hipBLASLt handle, workspace and plans (created on first use)
     std::string last_error;
 };
 
@@ -41,8 +42,11 @@ struct DeviceScope {
 
 int fail(nott_ctx ctx, int status, const std::string& msg);
 int hip_fail(nott_ctx ctx, hipError_t e, const char* what);
-// Returns a workspace pointer of at least `bytes` (grows by re-allocation
-// after synchronising the stream); nullptr on failure (error already set).
+// Returns a workspace pointer of at least `bytes`; nullptr on failure (error
+// already set).  Growth allocates a new arena (at least twice the old size)
+// and retires the old one without freeing it: kernels still in flight on any
+// stream, and HIP graphs captured with the old pointer, keep valid memory.
+// Retired arenas are freed by nott_destroy.
 void* workspace(nott_ctx ctx, size_t bytes);
 // Checks the last launch and records an error message.
 int launch_status(nott_ctx ctx, const char* kernel);

@@ -1,6 +1,5 @@
 // Context, errors and workspace of libnott_hip.
 #include "common.hpp"
-#include "blaslt.hpp"
 
 #include <new>
 
@@ -19,25 +18,18 @@ int hip_fail(nott_ctx ctx, hipError_t e, const char* what) {
 void* workspace(nott_ctx ctx, size_t bytes) {
     if (bytes == 0) bytes = 256;
     if (bytes <= ctx->ws_bytes) return ctx->ws;
-    // In-flight kernels may still read the old arena.
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) {
-        hip_fail(ctx, e, "hipStreamSynchronize (workspace growth)");
-        return nullptr;
-    }
-    if (ctx->ws) {
-        (void)hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-    }
+    // Geometric growth bounds the retired total by the current arena's size.
     size_t want = (bytes + (1u << 20) - 1) & ~size_t((1u << 20) - 1);
-    e = hipMalloc(&ctx->ws, want);
+    want = std::max(want, 2 * ctx->ws_bytes);
+    void* fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, want);
     if (e != hipSuccess) {
-        ctx->ws = nullptr;
         fail(ctx, NOTT_ERR_ALLOC, std::string("workspace hipMalloc of ") + std::to_string(want) +
                                       " bytes failed: " + hipGetErrorString(e));
         return nullptr;
     }
+    if (ctx->ws) ctx->retired.push_back(ctx->ws);
+    ctx->ws = fresh;
     ctx->ws_bytes = want;
     return ctx->ws;
 }
@@ -94,9 +86,9 @@ int nott_destroy(nott_ctx ctx) {
     if (!ctx) return NOTT_OK;
     {
         nott::DeviceScope scope(ctx->device);
-        (void)hipStreamSynchronize(ctx->stream);
-        nott::blas::release(ctx);
+        (void)hipDeviceSynchronize();
         if (ctx->ws) (void)hipFree(ctx->ws);
+        for (void* r : ctx->retired) (void)hipFree(r);
         if (ctx->err_word) (void)hipFree(ctx->err_word);
     }
     delete ctx;

@@ -10,9 +10,9 @@
 //   db = Σ_rows dy        (folded into the dw GEMM as an extra all-ones column;
 //                          bf16 fast path: a two-phase column sum)
 // bf16 operands whose k extent is a multiple of 64 take the fast GEMM path
-// (gemm.hpp, namespace fast); everything else the generic engine.
+// (gemm.hpp, namespace fast); everything else the generic engine.  Every
+// product runs on the kernels in this library; no vendor GEMM is called.
 #include "gemm.hpp"
-#include "blaslt.hpp"
 
 namespace {
 
@@ -20,7 +20,6 @@ using namespace nott::gemm;
 using nott::ceil_div;
 using nott::launch_status;
 using nott::workspace;
-namespace blas = nott::blas;
 
 template <typename T>
 bool vec16(const void* p, int64_t ld) {
@@ -154,17 +153,19 @@ __global__ __launch_bounds__(256) void colsum_finish_kernel(const float* __restr
     db[col] = accumulate ? db[col] + s : s;
 }
 
+// db (+)= Σ_rows dy through the two-phase column sum.
 template <typename T>
-constexpr hipDataType lib_type() { return sizeof(T) == 2 ? HIP_R_16BF : HIP_R_32F; }
+int launch_db(nott_ctx ctx, const T* dy, int64_t m, int64_t nout, float* db, int accumulate) {
+    float* part = static_cast<float*>(workspace(ctx, sizeof(float) * kColSumSlabs * (size_t)nout));
+    if (!part) return NOTT_ERR_ALLOC;
+    launch_colsum<T>(ctx, dy, m, nout, part);
+    hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)ceil_div(nout, 256)), dim3(256), 0, ctx->stream, part,
+                       nout, db, accumulate);
+    return launch_status(ctx, "linear db");
+}
 
 template <typename T>
 int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
-    // Library GEMM, column-major: Yᵀ (nout×m) = Wᵀᵀ·Xᵀ, bias per row of Yᵀ.
-    {
-        const int st = blas::gemm(ctx, true, false, nout, m, kin, w, kin, x, kin, lib_type<T>(), y, nout, lib_type<T>(),
-                                  0.f, b);
-        if (st != NOTT_ERR_UNSUPPORTED) return st;
-    }
     if constexpr (sizeof(T) == 2) {
         RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
         const int st = fast::run<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
@@ -183,32 +184,11 @@ template <typename T>
 int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, const void* x, const void* w, void* dx,
         float* dw, float* db, int accumulate) {
     const T* dyp = static_cast<const T*>(dy);
-    // Library GEMMs, column-major: dXᵀ (kin×m) = Wᵀ(kin×nout)·dYᵀ(nout×m);
-    // dWᵀ (kin×nout, fp32) = Xᵀ(kin×m)·dY(m×nout) (+ dWᵀ when accumulating).
-    if (dx) {
-        const int st = blas::gemm(ctx, false, false, kin, m, nout, w, kin, dy, nout, lib_type<T>(), dx, kin,
-                                  lib_type<T>(), 0.f, nullptr);
-        if (st == NOTT_OK) dx = nullptr;
-        else if (st != NOTT_ERR_UNSUPPORTED) return st;
-    }
-    if (dw) {
-        const int st = blas::gemm(ctx, false, true, kin, nout, m, x, kin, dy, nout, lib_type<T>(), dw, kin, HIP_R_32F,
-                                  accumulate ? 1.f : 0.f, nullptr);
-        if (st == NOTT_OK) {
-            dw = nullptr;
-            if (db) {
-                float* part = static_cast<float*>(workspace(ctx, sizeof(float) * kColSumSlabs * (size_t)nout));
-                if (!part) return NOTT_ERR_ALLOC;
-                launch_colsum<T>(ctx, dyp, m, nout, part);
-                hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)ceil_div(nout, 256)), dim3(256), 0,
-                                   ctx->stream, part, nout, db, accumulate);
-                db = nullptr;
-                const int st2 = launch_status(ctx, "linear db");
-                if (st2 != NOTT_OK) return st2;
-            }
-        } else if (st != NOTT_ERR_UNSUPPORTED) {
-            return st;
-        }
+    // A db-only request (no dw) is the column sum alone.
+    if (db && !dw) {
+        const int st = launch_db<T>(ctx, dyp, m, nout, db, accumulate);
+        if (st != NOTT_OK) return st;
+        db = nullptr;
     }
     if (!dx && !dw && !db) return NOTT_OK;
     if constexpr (sizeof(T) == 2) {
@@ -232,14 +212,9 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
                     if (st != NOTT_OK) return st;
                     dw = nullptr;
                     if (db) {
-                        float* part = static_cast<float*>(workspace(ctx, sizeof(float) * kColSumSlabs * (size_t)nout));
-                        if (!part) return NOTT_ERR_ALLOC;
-                        launch_colsum<T>(ctx, dyp, m, nout, part);
-                        hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)ceil_div(nout, 256)), dim3(256), 0,
-                                           ctx->stream, part, nout, db, accumulate);
-                        db = nullptr;
-                        const int st2 = launch_status(ctx, "linear db");
+                        const int st2 = launch_db<T>(ctx, dyp, m, nout, db, accumulate);
                         if (st2 != NOTT_OK) return st2;
+                        db = nullptr;
                     }
                 }
             }
@@ -282,7 +257,7 @@ extern "C" int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_
     NOTT_REQUIRE(ctx, m >= 0 && kin > 0 && nout > 0, "nott_linear_bwd: need m >= 0, kin > 0, nout > 0");
     NOTT_REQUIRE(ctx, dy != nullptr || m == 0, "nott_linear_bwd: null dy");
     NOTT_REQUIRE(ctx, !dx || w, "nott_linear_bwd: dx needs w");
-    NOTT_REQUIRE(ctx, !(dw || db) || x || m == 0, "nott_linear_bwd: dw needs x");
+    NOTT_REQUIRE(ctx, !dw || x || m == 0, "nott_linear_bwd: dw needs x");
     nott::DeviceScope scope(ctx->device);
     if (m == 0) {
         // Empty batch: dx is empty; the parameter gradients sum over nothing.

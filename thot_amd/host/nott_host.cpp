@@ -45,80 +45,56 @@ struct SmallCNNImpl : torch::nn::Module {
 TORCH_MODULE(SmallCNN);
 
 // ------------------------------------------------------------- configs[4]
-struct BasicBlockImpl : torch::nn::Module {
-    NH::Conv2d c1{nullptr}, c2{nullptr}, proj{nullptr};
-    NH::BatchNorm2d b1{nullptr}, b2{nullptr};
-    BasicBlockImpl(int64_t in, int64_t out, int64_t stride) {
-        c1 = register_module("conv0", NH::Conv2d(NH::Conv2dOptions{in, out, {3, 3}, {stride, stride}, {1, 1}, {1, 1}, false}));
-        b1 = register_module("bn0", NH::BatchNorm2d(out));
-        c2 = register_module("conv1", NH::Conv2d(NH::Conv2dOptions{out, out, {3, 3}, {1, 1}, {1, 1}, {1, 1}, false}));
-        b2 = register_module("bn1", NH::BatchNorm2d(out));
-        // Projection shortcut: a single 1×1 stride-2 conv, no BN (residual.hpp:18-20, 99-104).
-        if (stride != 1 || in != out)
-            proj = register_module("proj", NH::Conv2d(NH::Conv2dOptions{in, out, {1, 1}, {stride, stride}, {0, 0}, {1, 1}, false}));
-    }
-    Tensor forward(const Tensor& x) {
-        auto f = NH::ForkFn::apply(x);     // x feeds the branch and the skip
-        if (!keep) {
-            // BN + ReLU and BN + skip + ReLU fused (same values; the probe
-            // below keeps every intermediate as its own tensor).
-            Tensor h = b1->forward_relu(c1(f[0]));
-            Tensor skip = proj ? proj(f[1]) : f[1];
-            return b2->forward_add_relu(c2(h), skip);
-        }
-        Tensor c0 = c1(f[0]);
-        Tensor h = NH::relu(b1(c0));
-        Tensor c1o = c2(h);
-        Tensor h2 = b2(c1o);
-        Tensor skip = proj ? proj(f[1]) : f[1];
-        Tensor sum = NH::AddFn::apply(h2, skip);
-        if (keep) {
-            for (auto* t : {&c0, &h, &c1o, &h2, &sum, &f[0], &f[1]}) t->retain_grad();
-            kept = {{"c0", c0}, {"h", h}, {"c1", c1o}, {"h2", h2}, {"sum", sum}, {"f0", f[0]}, {"f1", f[1]}};
-        }
-        return NH::relu(sum);
-    }
-    bool keep = false;
-    std::vector<std::pair<std::string, Tensor>> kept;
-};
-TORCH_MODULE(BasicBlock);
-
+// ResNet-18 as a Nott model registers it (core.hpp:516-523, 576-592): the
+// stem Conv2d (identity activation), BatchNorm2d with ReLU and MaxPool2d,
+// eight Residual blocks (residual_block_<i>, each down-sampling block its
+// own descriptor with a 1×1 stride-2 projection; residual.hpp:18-20, 99-104),
+// AdaptiveAvgPool2d, Flatten and the FC layer, each under its
+// `<kind>_<index>` key, so parameter names match the reference's
+// (e.g. residual_block_3.conv2d_0.weight, fc_13.bias).
 struct ResNet18Impl : torch::nn::Module {
     NH::Conv2d stem{nullptr};
     NH::BatchNorm2d stem_bn{nullptr};
-    std::vector<BasicBlock> blocks;
+    NH::MaxPool2d pool{nullptr};
+    std::vector<NH::ResidualBasicBlock> blocks;
+    NH::AdaptiveAvgPool2d gap{nullptr};
+    NH::Flatten flat{nullptr};
     NH::Linear fc{nullptr};
     explicit ResNet18Impl(int64_t classes) {
-        stem = register_module("stem", NH::Conv2d(NH::Conv2dOptions{3, 64, {7, 7}, {2, 2}, {3, 3}, {1, 1}, false}));
-        stem_bn = register_module("stem_bn", NH::BatchNorm2d(64));
+        int64_t index = 0;
+        auto key = [&](const char* kind) { return std::string(kind) + "_" + std::to_string(index++); };
+        stem = register_module(key("conv2d"), NH::Conv2d(NH::Conv2dOptions{3, 64, {7, 7}, {2, 2}, {3, 3}, {1, 1}, false}));
+        stem_bn = register_module(key("batchnorm2d"), NH::BatchNorm2d(64));
+        pool = register_module(key("maxpool2d"), NH::MaxPool2d(3, 2, 1));
         const int64_t widths[4] = {64, 128, 256, 512};
         int64_t in = 64;
         for (int s = 0; s < 4; ++s)
             for (int b = 0; b < 2; ++b) {
                 const int64_t stride = (s > 0 && b == 0) ? 2 : 1;
-                blocks.push_back(register_module("block" + std::to_string(s) + "_" + std::to_string(b),
-                                                 BasicBlock(in, widths[s], stride)));
+                const bool projection = stride != 1 || in != widths[s];
+                blocks.push_back(register_module(key("residual_block"),
+                                                 NH::ResidualBasicBlock(in, widths[s], stride, projection)));
                 in = widths[s];
             }
-        fc = register_module("fc", NH::Linear(512, classes));
+        gap = register_module(key("adaptive_avgpool2d"), NH::AdaptiveAvgPool2d());
+        flat = register_module(key("flatten"), NH::Flatten());
+        fc = register_module(key("fc"), NH::Linear(512, classes));
     }
     Tensor forward(Tensor x) {
-        x = NH::max_pool2d(keep_grads ? NH::relu(stem_bn(stem(x))) : stem_bn->forward_relu(stem(x)), 3, 2, 1);
-        if (keep_grads) mark(x, "stem_out");
-        for (size_t i = 0; i < blocks.size(); ++i) {
-            x = blocks[i](x);
-            if (keep_grads) mark(x, "block_out" + std::to_string(i));
+        x = pool(stem_bn->forward_relu(stem(x)));
+        if (record) outputs.push_back(x);
+        for (auto& b : blocks) {
+            x = b(x);
+            if (record) outputs.push_back(x);
         }
-        x = NH::AvgPoolGlobalFn::apply(x).flatten(1);
-        return fc(x);
+        x = fc(flat(gap(x)));
+        if (record) outputs.push_back(x);
+        return x;
     }
-    // Intermediate activations whose gradients are kept (tests of the wiring).
-    bool keep_grads = false;
-    std::vector<std::pair<std::string, Tensor>> marked;
-    void mark(Tensor& t, const std::string& name) {
-        t.retain_grad();
-        marked.emplace_back(name, t);
-    }
+    // When set, forward keeps the stem output, every block output (the
+    // post-ReLU activations; tests compare their zero patterns) and the logits.
+    bool record = false;
+    std::vector<Tensor> outputs;
 };
 TORCH_MODULE(ResNet18);
 
@@ -135,13 +111,19 @@ void collect_weights(torch::nn::Module& m, std::vector<Tensor*>& copies, std::ve
     }
 }
 
-// A model + fused optimizer on one device; the Python side drives it.
-template <class Model>
+// A model and its optimizer on one device; the Python side drives it.  The
+// optimizer is held as Nott's OptimizerBinding holds it, a
+// std::unique_ptr<torch::optim::Optimizer> (core.hpp:170-181), and stepped
+// through the virtual step() (core.hpp:5049-5057).
+template <class Model, bool Decoupled>
 struct Trainer {
+    using Fused = NH::FusedAdamImpl<Decoupled>;
     Model model;
-    std::unique_ptr<NH::FusedAdam> opt;
+    std::unique_ptr<torch::optim::Optimizer> opt;
+    Fused* fused = nullptr;   // the same object, for the flat-arena extras
     bool bf16;
-    Trainer(Model m, bool bf16_, NH::FusedAdam::Options o, int device, uint64_t seed) : model(std::move(m)), bf16(bf16_) {
+    Trainer(Model m, bool bf16_, const typename Fused::TorchOptions& o, int device, uint64_t seed)
+        : model(std::move(m)), bf16(bf16_) {
         torch::NoGradGuard ng;
         auto gen = at::detail::createCPUGenerator(seed);
         torch::Generator g(gen);
@@ -150,16 +132,32 @@ struct Trainer {
             const auto& name = kv.key();
             if (name.size() >= 6 && name.compare(name.size() - 6, 6, "weight") == 0 && p.dim() >= 2) NH::he_uniform_(p, g);
         }
-        if (device >= 0) model->to(torch::Device(torch::kCUDA, device));   // device < 0: host only (tests of the wiring)
+        model->to(torch::Device(torch::kCUDA, device));
         model->train();
-        std::vector<Tensor*> copies;
-        std::vector<Tensor> masters;
-        if (bf16) collect_weights(*model, copies, masters);
         std::vector<Tensor> params;
         for (auto& p : model->parameters()) params.push_back(p);
-        opt = std::make_unique<NH::FusedAdam>(params, o, copies, masters);
+        auto f = std::make_unique<Fused>(params, o);
+        // Model::run_training_step always follows step() with zero_grad()
+        // (core.hpp:3819-3823): clear the gradients in the update pass.
+        f->set_fused_zero_grad(true);
+        if (bf16) {
+            std::vector<Tensor*> copies;
+            std::vector<Tensor> masters;
+            collect_weights(*model, copies, masters);
+            f->attach_bf16_copies(copies, masters);
+        }
+        fused = f.get();
+        opt = std::move(f);
     }
-    Tensor input(const Tensor& x) { return bf16 ? x.to(torch::kBFloat16) : x; }
+    // The model's input in the compute dtype (bf16: one nott_cast).
+    Tensor input(const Tensor& x) {
+        if (!bf16) return x;
+        Tensor xc = x.contiguous();
+        Tensor out = torch::empty(xc.sizes(), xc.options().dtype(torch::kBFloat16));
+        nott_ctx c = NH::bind(xc);
+        NH::check(nott_cast(c, xc.numel(), xc.data_ptr(), NOTT_F32, out.data_ptr(), NOTT_BF16), c, "input cast");
+        return out;
+    }
     // forward + loss + backward (grads land in the flat gradient arena)
     Tensor forward_backward(const Tensor& x, const Tensor& y) {
         Tensor logits = model->forward(input(x));
@@ -167,10 +165,18 @@ struct Trainer {
         loss.backward();
         return loss.detach();
     }
+    // One training step: forward, loss, backward, optimizer step with the
+    // gradients cleared in the same pass.
     Tensor step(const Tensor& x, const Tensor& y) {
         Tensor loss = forward_backward(x, y);
-        opt->step();   // fused AdamW + zero_grad (+ bf16 copies)
+        opt->step();
         return loss;
+    }
+    // Nott's sequence through the base-class interface only:
+    // step_optimizers() then zero_grad(false) (core.hpp:3820-3823).
+    void optimizer_step() {
+        opt->step();
+        opt->zero_grad(false);
     }
 
     // Step orchestration on device (the reference's CUDA-graph step path,
@@ -178,14 +184,23 @@ struct Trainer {
     // into a HIP graph over static input buffers, so a step is two input
     // copies, one graph launch and the fused AdamW launch.  The optimizer
     // step stays outside the graph because its step count and bias
-    // corrections change every step.  `warmup` forward/backward passes run
-    // first on the capture stream (workspace, library plans and allocator
-    // pools reach their steady state; their gradients are zeroed again).
+    // corrections change every step.  `passes` forward/backward passes run
+    // first on the capture stream so the workspace and the allocator pools
+    // reach their steady state; their gradients are cleared again and the
+    // model's buffers (BatchNorm running statistics) restored, so the warm-up
+    // leaves no trace in the model.
     std::unique_ptr<at::cuda::CUDAGraph> graph;
     Tensor gx, gy, gloss;
     void warmup(const Tensor& x, const Tensor& y, int passes) {
+        std::vector<Tensor> saved;
+        for (auto& b : model->buffers()) saved.push_back(b.clone());
         for (int i = 0; i < passes; ++i) forward_backward(x, y);
-        opt->zero_grad();
+        fused->zero_flat_grads();
+        torch::NoGradGuard ng;
+        auto bufs = model->buffers();
+        for (size_t i = 0; i < bufs.size(); ++i) bufs[i].copy_(saved[i]);
+        for (auto& child : model->modules(/*include_self=*/true))
+            if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->uncount(passes);
     }
     void capture(const Tensor& x, const Tensor& y, int passes) {
         gx = x.clone();
@@ -201,6 +216,9 @@ struct Trainer {
             gloss = forward_backward(gx, gy);
             g->capture_end();
             graph = std::move(g);
+            // The captured forward was recorded, not run.
+            for (auto& child : model->modules(/*include_self=*/true))
+                if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->uncount(1);
         }
         if (hipDeviceSynchronize() != hipSuccess) throw std::runtime_error("capture: device synchronize failed");
     }
@@ -211,6 +229,8 @@ struct Trainer {
         gx.copy_(x);
         gy.copy_(y);
         graph->replay();
+        for (auto& child : model->modules(/*include_self=*/true))
+            if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->count_batch();
         opt->step();
         return gloss.clone();
     }
@@ -229,21 +249,31 @@ struct Trainer {
         return out;
     }
     std::map<std::string, Tensor> buffers() {
+        for (auto& child : model->modules(/*include_self=*/true))
+            if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->sync_counter();
         std::map<std::string, Tensor> out;
         for (auto& kv : model->named_buffers()) out[kv.key()] = kv.value();
         return out;
     }
-    // Copies values into named parameters (then refreshes bf16 copies).
+    // Copies values into named parameters or buffers (then refreshes the
+    // bf16 copies).
     void load(const std::map<std::string, Tensor>& values) {
         torch::NoGradGuard ng;
         auto named = model->named_parameters();
+        auto bufs = model->named_buffers();
         for (auto& kv : values) {
-            auto* p = named.find(kv.first);
-            if (!p) throw std::invalid_argument("no parameter " + kv.first);
-            p->copy_(kv.second);
+            if (auto* p = named.find(kv.first)) p->copy_(kv.second);
+            else if (auto* b = bufs.find(kv.first)) b->copy_(kv.second);
+            else throw std::invalid_argument("no parameter or buffer " + kv.first);
         }
-        opt->refresh();
+        fused->refresh();
     }
+    // Scheduler-style learning-rate write into a param group's options
+    // (lrscheduler/details/cosineannealing.hpp:52-63).
+    void set_lr(double lr) {
+        for (auto& g : opt->param_groups()) g.options().set_lr(lr);
+    }
+    void set_fused_zero_grad(bool on) { fused->set_fused_zero_grad(on); }
     int64_t num_params() {
         int64_t n = 0;
         for (auto& p : model->parameters()) n += p.numel();
@@ -253,14 +283,46 @@ struct Trainer {
 
 }  // namespace
 
+// Parameter groups behind the fused optimizer, driven from Python through
+// the torch::optim::Optimizer interface only (tests of the drop-in: groups
+// with their own options, scheduler-style lr writes, zero_grad modes).
+struct OptimizerHandle {
+    std::unique_ptr<torch::optim::Optimizer> opt;
+    OptimizerHandle(const std::vector<std::vector<Tensor>>& groups, const std::vector<double>& lrs,
+                    const std::vector<double>& wds, bool decoupled, double beta1, double beta2, double eps) {
+        if (groups.size() != lrs.size() || groups.size() != wds.size())
+            throw std::invalid_argument("one lr and weight decay per group");
+        auto make = [&](auto defaults, auto tag) {
+            using Opts = decltype(defaults);
+            std::vector<torch::optim::OptimizerParamGroup> pg;
+            for (size_t i = 0; i < groups.size(); ++i) {
+                auto o = std::make_unique<Opts>(lrs[i]);
+                o->betas(std::make_tuple(beta1, beta2)).eps(eps).weight_decay(wds[i]);
+                pg.emplace_back(groups[i], std::move(o));
+            }
+            defaults.betas(std::make_tuple(beta1, beta2)).eps(eps);
+            using F = typename decltype(tag)::type;
+            return std::unique_ptr<torch::optim::Optimizer>(new F(pg, defaults));
+        };
+        struct W { using type = NH::FusedAdamW; };
+        struct A { using type = NH::FusedAdam; };
+        opt = decoupled ? make(torch::optim::AdamWOptions(1e-3), W{}) : make(torch::optim::AdamOptions(1e-3), A{});
+    }
+};
+
 PYBIND11_MODULE(_nott_host, m) {
     m.doc() = "C++ host layer (Nott::HIP) over libnott_hip: configs[0] and configs[4] training steps";
-    using SmallT = Trainer<SmallCNN>;
+    m.def("workspace_bytes", [](int device) {
+        int64_t b = 0;
+        nott_ctx c = NH::context(device);
+        NH::check(nott_workspace_bytes(c, &b), c, "workspace bytes");
+        return b;
+    }, py::arg("device") = 0);
+    using SmallT = Trainer<SmallCNN, false>;
     py::class_<SmallT>(m, "SmallCNNTrainer")
         .def(py::init([](int device, uint64_t seed, double lr) {
-                 NH::FusedAdam::Options o;
-                 o.lr = lr;   // Adam, betas (0.9, 0.999), eps 1e-8, no weight decay
-                 return new SmallT(SmallCNN(), false, o, device, seed);
+                 // Adam, betas (0.9, 0.999), eps 1e-8, no weight decay
+                 return new SmallT(SmallCNN(), false, torch::optim::AdamOptions(lr), device, seed);
              }),
              py::arg("device") = 0, py::arg("seed") = 0, py::arg("lr") = 1e-3)
         .def("step", &SmallT::step, py::call_guard<py::gil_scoped_release>())
@@ -271,19 +333,20 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("step_graph", &SmallT::step_graph, py::call_guard<py::gil_scoped_release>())
         .def("save", &SmallT::save, py::arg("path"))
         .def("forward_backward", &SmallT::forward_backward, py::call_guard<py::gil_scoped_release>())
-        .def("optimizer_step", [](SmallT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
+        .def("optimizer_step", &SmallT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &SmallT::forward, py::call_guard<py::gil_scoped_release>())
         .def("params", &SmallT::params)
         .def("grads", &SmallT::grads)
+        .def("buffers", &SmallT::buffers)
         .def("load", &SmallT::load)
+        .def("set_lr", &SmallT::set_lr)
+        .def("set_fused_zero_grad", &SmallT::set_fused_zero_grad)
         .def("num_params", &SmallT::num_params);
-    using ResT = Trainer<ResNet18>;
+    using ResT = Trainer<ResNet18, true>;
     py::class_<ResT>(m, "ResNet18Trainer")
         .def(py::init([](int device, uint64_t seed, bool bf16, double lr, double wd, int64_t classes) {
-                 NH::FusedAdam::Options o;
-                 o.lr = lr;
-                 o.weight_decay = wd;
-                 o.decoupled = true;   // AdamW
+                 torch::optim::AdamWOptions o(lr);   // AdamW, betas (0.9, 0.999), eps 1e-8
+                 o.weight_decay(wd);
                  return new ResT(ResNet18(classes), bf16, o, device, seed);
              }),
              py::arg("device") = 0, py::arg("seed") = 0, py::arg("bf16") = false, py::arg("lr") = 1e-3,
@@ -296,29 +359,54 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("step_graph", &ResT::step_graph, py::call_guard<py::gil_scoped_release>())
         .def("save", &ResT::save, py::arg("path"))
         .def("forward_backward", &ResT::forward_backward, py::call_guard<py::gil_scoped_release>())
-        .def("optimizer_step", [](ResT& t) { t.opt->step(); }, py::call_guard<py::gil_scoped_release>())
+        .def("optimizer_step", &ResT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &ResT::forward, py::call_guard<py::gil_scoped_release>())
         .def("params", &ResT::params)
         .def("grads", &ResT::grads)
         .def("buffers", &ResT::buffers)
-        .def("activation_grads",
+        .def("load", &ResT::load)
+        .def("set_lr", &ResT::set_lr)
+        .def("set_fused_zero_grad", &ResT::set_fused_zero_grad)
+        .def("forward_backward_recording",
              [](ResT& t, const Tensor& x, const Tensor& y) {
-                 t.model->keep_grads = true;
-                 t.model->marked.clear();
-                 t.model->blocks[0]->keep = true;
+                 // forward + loss + backward, keeping the stem and block outputs
+                 t.model->record = true;
+                 t.model->outputs.clear();
+                 Tensor loss;
                  {
                      py::gil_scoped_release nogil;
-                     t.forward_backward(x, y);
+                     loss = t.forward_backward(x, y);
                  }
-                 std::map<std::string, Tensor> out;
-                 for (auto& kv : t.model->marked) out[kv.first] = kv.second.grad();
-                 for (auto& kv : t.model->blocks[0]->kept) out["b0_" + kv.first] = kv.second.grad();
-                 t.model->blocks[0]->keep = false;
-                 t.model->blocks[0]->kept.clear();
-                 t.model->keep_grads = false;
-                 t.model->marked.clear();
-                 return out;
+                 std::vector<Tensor> outs;
+                 for (auto& o : t.model->outputs) outs.push_back(o.detach());
+                 t.model->record = false;
+                 t.model->outputs.clear();
+                 return std::make_pair(loss, outs);
              })
-        .def("load", &ResT::load)
         .def("num_params", &ResT::num_params);
+    py::class_<OptimizerHandle>(m, "FusedOptimizer")
+        .def(py::init<const std::vector<std::vector<Tensor>>&, const std::vector<double>&,
+                      const std::vector<double>&, bool, double, double, double>(),
+             py::arg("groups"), py::arg("lrs"), py::arg("weight_decays"), py::arg("decoupled"),
+             py::arg("beta1") = 0.9, py::arg("beta2") = 0.999, py::arg("eps") = 1e-8)
+        .def("step", [](OptimizerHandle& h) { h.opt->step(); }, py::call_guard<py::gil_scoped_release>())
+        .def("zero_grad", [](OptimizerHandle& h, bool set_to_none) { h.opt->zero_grad(set_to_none); },
+             py::arg("set_to_none") = false)
+        .def("set_lr", [](OptimizerHandle& h, size_t group, double lr) {
+                 h.opt->param_groups().at(group).options().set_lr(lr);
+             })
+        .def("num_groups", [](OptimizerHandle& h) { return h.opt->param_groups().size(); })
+        .def("state_step", [](OptimizerHandle& h, const Tensor& p) {
+                 auto it = h.opt->state().find(p.unsafeGetTensorImpl());
+                 if (it == h.opt->state().end()) throw std::invalid_argument("no state for this parameter");
+                 return dynamic_cast<torch::optim::AdamParamState*>(it->second.get())
+                            ? static_cast<torch::optim::AdamParamState&>(*it->second).step()
+                            : static_cast<torch::optim::AdamWParamState&>(*it->second).step();
+             })
+        .def("exp_avg", [](OptimizerHandle& h, const Tensor& p) {
+                 auto it = h.opt->state().find(p.unsafeGetTensorImpl());
+                 if (it == h.opt->state().end()) throw std::invalid_argument("no state for this parameter");
+                 if (auto* a = dynamic_cast<torch::optim::AdamParamState*>(it->second.get())) return a->exp_avg();
+                 return static_cast<torch::optim::AdamWParamState&>(*it->second).exp_avg();
+             });
 }
