@@ -197,6 +197,23 @@ int nott_layernorm_bwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d,
                        const void* x, const void* dy, const float* mean, const float* rstd,
                        const void* gamma, void* dx, float* dgamma, float* dbeta,
                        int accumulate);
+/* nott_layernorm_bwd without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as nott_layernorm_bwd (the same kernels); the
+ * dgamma/dbeta column partials live in a static 16 MiB device array, one per
+ * GPU, instead of the context workspace.  That bounds the problem: the
+ * partials take 2·16·ceil(d/16)·4 bytes per block for up to 2·(number of
+ * CUs) blocks (d <= 4096 on a 256-CU MI355X), or 8·d·rows bytes when
+ * d or the pointers do not allow 16-byte rows; larger problems return
+ * NOTT_ERR_UNSUPPORTED with the sizes in the message.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two
+ * contexts) race.  The partials are written in full before they are read,
+ * so no clearing is needed between calls. */
+int nott_layernorm_bwd_noalloc(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d,
+                               const void* x, const void* dy, const float* mean, const float* rstd,
+                               const void* gamma, void* dx, float* dgamma, float* dbeta,
+                               int accumulate);
 
 /* ---- softmax cross-entropy ------------------------------------------------
  * Replaces F::cross_entropy called by Nott::Loss::Details::compute(const

@@ -79,6 +79,7 @@ SIGNATURES: dict[str, list] = {
     "nott_batchnorm2d_bwd_act": [vp, i32, i64, i64, i64, vp, vp, fp, fp, fp, fp, i32, vp, fp, fp, i32],
     "nott_layernorm_fwd": [vp, i32, i64, i64, vp, vp, vp, f64, vp, fp, fp],
     "nott_layernorm_bwd": [vp, i32, i64, i64, vp, vp, fp, fp, vp, vp, fp, fp, i32],
+    "nott_layernorm_bwd_noalloc": [vp, i32, i64, i64, vp, vp, fp, fp, vp, vp, fp, fp, i32],
     "nott_softmax_xent_bwd": [vp, i32, i64, i64, vp, vp, f64, f64, vp, fp],
     "nott_attention_fwd": [vp, C.POINTER(AttnDesc), i32, vp, vp, vp, vp, fp],
     "nott_attention_bwd": [vp, C.POINTER(AttnDesc), i32, vp, vp, vp, vp, vp, fp, vp, vp, vp],

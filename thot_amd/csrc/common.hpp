@@ -19,6 +19,7 @@ struct nott_ctx_s {
     void* ws = nullptr;            // current device workspace
     size_t ws_bytes = 0;
     std::vector<void*> retired;    // earlier, smaller workspaces: kept until nott_destroy
+    void* ln_scratch = nullptr;    // this device's static LayerNorm scratch (nott_layernorm_bwd_noalloc)
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;
     std::string last_error;
@@ -48,6 +49,8 @@ int hip_fail(nott_ctx ctx, hipError_t e, const char* what);
 // stream, and HIP graphs captured with the old pointer, keep valid memory.
 // Retired arenas are freed by nott_destroy.
 void* workspace(nott_ctx ctx, size_t bytes);
+// Looks up this device's static LayerNorm scratch (layernorm.hip).
+int layernorm_scratch_setup(nott_ctx ctx);
 // Checks the last launch and records an error message.
 int launch_status(nott_ctx ctx, const char* kernel);
 

@@ -78,6 +78,12 @@ int nott_create(int device, nott_ctx* out) {
         delete c;
         return NOTT_ERR_HIP;
     }
+    const int st = nott::layernorm_scratch_setup(c);
+    if (st != NOTT_OK) {
+        (void)hipFree(c->err_word);
+        delete c;
+        return st;
+    }
     *out = c;
     return NOTT_OK;
 }

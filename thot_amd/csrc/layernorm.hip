@@ -13,6 +13,8 @@
 // kernel reduces them (deterministic order).
 #include "common.hpp"
 
+#include <mutex>
+
 #include <initializer_list>
 
 namespace {
@@ -414,16 +416,16 @@ int fwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* gamma,
     return nott::launch_status(ctx, "layernorm_fwd");
 }
 
+// Scratch for the column partials of the allocation-free entry point
+// (nott_layernorm_bwd_noalloc): one copy per GPU, alive until the process
+// ends.  Host code never passes `scratch` itself to a kernel; it uses the
+// device address hipGetSymbolAddress returns for the current device.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+// Partials need: 2 rows (dgamma, dbeta) of `pcols` columns per block.
 template <typename T>
-int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, const float* mean, const float* rstd,
-        const void* gamma, void* dx, float* dgamma, float* dbeta, int accumulate) {
-    const T* xx = static_cast<const T*>(x);
-    const T* dd = static_cast<const T*>(dy);
-    const T* gg = static_cast<const T*>(gamma);
-    T* out = static_cast<T*>(dx);
-    const bool vec = vec_ok<T>(d, {x, dy, gamma, dx});
-    const int dpl = vec ? dpl_for<T>(d) : 0;
-    int64_t nparts;
+void partial_plan(nott_ctx ctx, int64_t rows, int64_t d, bool vec, int dpl, int64_t& nparts, size_t& pcols) {
     if (vec) {
         nparts = std::min<int64_t>(nott::ceil_div(rows, kWaves * rows_in_flight((int)sizeof(T), dpl)),
                                    (int64_t)ctx->num_cu * 2);
@@ -431,9 +433,37 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
     } else {
         nparts = rows;
     }
-    const size_t pcols = vec ? (size_t)nott::ceil_div(d, 16) * 16 : (size_t)d;
-    float* partial = static_cast<float*>(nott::workspace(ctx, sizeof(float) * 2 * pcols * (size_t)nparts));
-    if (!partial) return NOTT_ERR_ALLOC;
+    pcols = vec ? (size_t)nott::ceil_div(d, 16) * 16 : (size_t)d;
+}
+
+// `fixed` (nullable) replaces the context workspace for the partials;
+// `fixed_bytes` is its size.
+template <typename T>
+int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, const float* mean, const float* rstd,
+        const void* gamma, void* dx, float* dgamma, float* dbeta, int accumulate, float* fixed = nullptr,
+        size_t fixed_bytes = 0) {
+    const T* xx = static_cast<const T*>(x);
+    const T* dd = static_cast<const T*>(dy);
+    const T* gg = static_cast<const T*>(gamma);
+    T* out = static_cast<T*>(dx);
+    const bool vec = vec_ok<T>(d, {x, dy, gamma, dx});
+    const int dpl = vec ? dpl_for<T>(d) : 0;
+    int64_t nparts;
+    size_t pcols;
+    partial_plan<T>(ctx, rows, d, vec, dpl, nparts, pcols);
+    const size_t need = sizeof(float) * 2 * pcols * (size_t)nparts;
+    float* partial;
+    if (fixed) {
+        if (need > fixed_bytes)
+            return nott::fail(ctx, NOTT_ERR_UNSUPPORTED,
+                              "nott_layernorm_bwd_noalloc: rows=" + std::to_string(rows) + ", d=" + std::to_string(d) +
+                                  " needs " + std::to_string(need) + " bytes of scratch; the static scratch holds " +
+                                  std::to_string(fixed_bytes));
+        partial = fixed;
+    } else {
+        partial = static_cast<float*>(nott::workspace(ctx, need));
+        if (!partial) return NOTT_ERR_ALLOC;
+    }
     const dim3 grid((unsigned)nparts);
     const size_t lds = sizeof(float) * kWaves * 2 * (size_t)d;
     if (dpl == 4)
@@ -456,6 +486,27 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
 }
 
 }  // namespace
+
+namespace nott {
+
+// Device address of `scratch` on each device, looked up once per device by
+// nott_create (the context's device is current there).
+int layernorm_scratch_setup(nott_ctx ctx) {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    std::lock_guard<std::mutex> g(mu);
+    if (ctx->device < 0 || ctx->device >= 64) return fail(ctx, NOTT_ERR_INVALID_ARG, "device index out of range");
+    if (!addr[ctx->device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return hip_fail(ctx, e, "hipGetSymbolAddress(layernorm scratch)");
+        addr[ctx->device] = p;
+    }
+    ctx->ln_scratch = addr[ctx->device];
+    return NOTT_OK;
+}
+
+}  // namespace nott
 
 extern "C" int nott_layernorm_fwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d, const void* x,
                                   const void* gamma, const void* beta, double eps, void* y, float* mean, float* rstd) {
@@ -485,4 +536,25 @@ extern "C" int nott_layernorm_bwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, 
     }
     return dtype == NOTT_F32 ? bwd<float>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate)
                              : bwd<bf16_t>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate);
+}
+
+extern "C" int nott_layernorm_bwd_noalloc(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d, const void* x,
+                                          const void* dy, const float* mean, const float* rstd, const void* gamma,
+                                          void* dx, float* dgamma, float* dbeta, int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && rows >= 0 && d > 0, "nott_layernorm_bwd_noalloc: bad arguments");
+    NOTT_REQUIRE(ctx, rows == 0 || (x && dy && mean && rstd && gamma && dx), "nott_layernorm_bwd_noalloc: null buffer");
+    NOTT_REQUIRE(ctx, ctx->ln_scratch != nullptr, "nott_layernorm_bwd_noalloc: scratch not set up");
+    nott::DeviceScope scope(ctx->device);
+    if (rows == 0) {
+        if (!accumulate) {
+            if (dgamma && nott_zero(ctx, sizeof(float) * d, dgamma) != NOTT_OK) return NOTT_ERR_HIP;
+            if (dbeta && nott_zero(ctx, sizeof(float) * d, dbeta) != NOTT_OK) return NOTT_ERR_HIP;
+        }
+        return NOTT_OK;
+    }
+    float* sp = static_cast<float*>(ctx->ln_scratch);
+    return dtype == NOTT_F32
+               ? bwd<float>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, sp, kScratchBytes)
+               : bwd<bf16_t>(ctx, rows, d, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, sp, kScratchBytes);
 }
