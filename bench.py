@@ -8,6 +8,8 @@ one batch of synthetic input already resident in HBM:
 
   conv_bwd  (default)  conv2d dgrad + wgrad, N=128,
             Cin=64, Cout=128, 56x56, 3x3 s1 p1, NCHW, no bias.  TFLOP/s.
+            The headline is fp32 (the reference's arithmetic); the bf16 leg
+            with its own roofline sits beside it in `legs`.
   ln_bwd    LayerNorm backward 16384x1024 (configs[2]a).  GB/s.
   xent      fused softmax-CE gradient 16384x32000 (configs[2]b).  GB/s.
   adamw     fused AdamW over a flat 1e8-parameter buffer (configs[2]c).  GB/s.
@@ -15,14 +17,11 @@ one batch of synthetic input already resident in HBM:
   small_cnn configs[0] training step, batch 64 (fp32).  samples/s.
   resnet18  configs[4] training step, batch 64 (bf16 or fp32).  samples/s.
 
-Besides `value`, the line carries `roofline` for the dominant kernel (its
-algorithmic work per launch over its HIP-event-timed launch duration on the
-launch stream) and `cpu_baseline`: the reference's own libtorch CPU path
-(oracle/_ref, kind "reference") or the plain-C oracle (kind "port"), timed on
-a bounded sample on this host's cores.  `extra` reports the other legs the
-metric names: LayerNorm-backward, AdamW and CE-gradient bandwidth (fp32 and
-bf16), conv backward in fp32, MHA backward, and the configs[0] / configs[4]
-training steps in samples/s (with their own CPU baselines).
+Every leg carries `roofline` for its dominant kernel (algorithmic work per
+launch over the HIP-event-timed launch duration on the launch stream) and
+`cpu_baseline`: the reference's own libtorch CPU path (oracle/_ref, kind
+"reference") timed on a bounded sample on this host's cores.  The default
+run (conv_bwd) reports every other BASELINE leg in `legs`.
 """
 from __future__ import annotations
 
@@ -46,70 +45,121 @@ METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HB
 # KiB per dispatch), each divided by what the same counter reads for a plain
 # 256 MiB device copy (FETCH_SIZE reads 0.5 x the bytes, WRITE_SIZE 1.0 x).
 # The passes and their commands are in profiles/.  Keyed by (workload, dtype,
-# kernel); None where no pass has been recorded.
+# kernel group); None where no pass has been recorded.
 TRAFFIC = {
     ("conv_bwd", "bf16", "dgrad"): 183.36e6,   # conv3x3_wprep + conv3x3_same
     ("conv_bwd", "bf16", "wgrad"): 230.21e6,   # conv3x3_wgrad + conv3x3_wgrad_reduce
-    ("ln_bwd", "f32", None): 210.93e6,         # ln_bwd_kernel + col_reduce_grouped_kernel
-    ("ln_bwd", "bf16", None): 109.77e6,
-    ("adamw", "f32", None): 2799.94e6,
-    ("adamw", "bf16", None): 2200.00e6,
-    ("xent", "f32", None): 4199.32e6,          # xent_count_kernel + xent_rows_vec_kernel
-    ("xent", "bf16", None): 2101.43e6,
+    ("ln_bwd", "f32", "all"): 210.93e6,        # ln_bwd_kernel + col_reduce_grouped_kernel
+    ("ln_bwd", "bf16", "all"): 109.77e6,
+    ("adamw", "f32", "all"): 2799.94e6,
+    ("adamw", "bf16", "all"): 2200.00e6,
+    ("xent", "f32", "all"): 4199.32e6,         # xent_count_kernel + xent_rows_vec_kernel
+    ("xent", "bf16", "all"): 2101.43e6,
 }
 
 
-def traffic_for(workload, dtype, kernel):
-    return TRAFFIC.get((workload, dtype, kernel))
-
-
-def host_cores() -> int:
+def host_info() -> dict:
+    """What the CPU baselines ran on: logical CPUs, the CPUs this process may
+    use, physical cores, the CPU model, and the thread count P used.  P is the
+    CPUs this process may use, capped by OMP_NUM_THREADS where it is set (the
+    GPU box's CPU share for one GPU is 16 and sets it to that)."""
     try:
-        n = len(os.sched_getaffinity(0))
+        aff = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        aff = os.cpu_count() or 1
+    model, phys = None, set()
+    try:
+        pid = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    pid = v
+                elif k == "core id":
+                    core = v
+                elif not k and pid is not None:
+                    phys.add((pid, core))
+                    pid = core = None
+        if pid is not None:
+            phys.add((pid, core))
+    except OSError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    p = aff if not (omp and omp.isdigit() and int(omp) > 0) else min(aff, int(omp))
+    return {"nproc": os.cpu_count(), "affinity_cpus": aff, "physical_cores": len(phys) or None,
+            "model": model, "threads": p, "omp_num_threads": omp}
+
+
+def cpu_threads() -> int:
+    return host_info()["threads"]
+
+
+def _ref():
+    from oracle_lib import Ref
+    if not Ref.available():
+        return None
+    ref = Ref()
+    ref.set_threads(cpu_threads())
+    return ref
+
+
+def _iters_for(sec_one: float, budget_s: float, cap: int = 20000) -> int:
+    return max(1, min(cap, int(budget_s / max(sec_one, 1e-6))))
 
 
 # ----------------------------------------------------------------- workloads
 class Workload:
+    """A BASELINE leg.  `groups` names the launch groups bracketed by HIP
+    events inside step(); `group_work` gives each group's algorithmic work per
+    launch (FLOP or bytes); `dominant` is the group the roofline is quoted on."""
     name = ""
     unit = ""
+    scale = 1.0          # value = work_per_step / seconds / scale
     bound = "hbm"
     dtype = "f32"
+    groups = ("all",)
+
+    def __init__(self, dtype):
+        self.dtype = dtype
+        self.ev = {}
+
+    def mark(self, group, i):
+        e = self.ev.get(group)
+        if e is not None:
+            e[i].record()
 
     def setup(self, torch, ops): ...
 
-    def step(self):
-        """Runs one pass; returns nothing.  The dominant kernel's launches are
-        bracketed by self.ev0 / self.ev1 when they are set."""
+    def step(self): ...
 
-    def work_per_step(self) -> float:
-        """Algorithmic FLOPs or bytes of one step (the unit of `value`)."""
+    def work_per_step(self) -> float: ...
 
-    def dominant(self):
-        """(name, algorithmic work per launch)."""
+    def group_work(self) -> dict:
+        return {"all": self.work_per_step()}
+
+    def dominant(self, per_ms: dict) -> str:
+        return max(per_ms, key=per_ms.get)
+
+    def peak(self):
+        return HBM_PEAK_GBS if self.bound == "hbm" else MFMA_PEAK_TFLOPS[self.dtype]
 
     def cpu_baseline(self, budget_s: float):
         return None
 
-
-def _timed(wl, fn):
-    if wl.ev0 is not None:
-        wl.ev0.record()
-    fn()
-    if wl.ev1 is not None:
-        wl.ev1.record()
+    def config(self) -> dict:
+        return {"workload": self.name}
 
 
 class ConvBwd(Workload):
     name = "conv_bwd"
     unit = "TFLOP/s"
+    scale = 1e12
     bound = "mfma"
+    groups = ("dgrad", "wgrad")
     N, C, K, H, W = 128, 64, 128, 56, 56
-
-    def __init__(self, dtype):
-        self.dtype = dtype
 
     def setup(self, torch, ops):
         self.ops = ops
@@ -122,54 +172,51 @@ class ConvBwd(Workload):
         self.dx = torch.empty_like(self.x)
         self.dw = torch.empty((self.K, self.C, 3, 3), dtype=torch.float32, device="cuda")
         self.flop_one = 2.0 * self.N * self.H * self.W * self.K * self.C * 9
-        self.ev_d = [None, None]
-        self.ev_w = [None, None]
 
     def step(self):
-        ops = self.ops
-        if self.ev_d[0] is not None:
-            self.ev_d[0].record()
-        ops.conv2d_bwd_data(self.dy, self.w, self.d, out=self.dx)
-        if self.ev_d[1] is not None:
-            self.ev_d[1].record()
-            self.ev_w[0].record()
-        ops.conv2d_bwd_weight(self.x, self.dy, self.d, dw=self.dw)
-        if self.ev_w[1] is not None:
-            self.ev_w[1].record()
+        self.mark("dgrad", 0)
+        self.ops.conv2d_bwd_data(self.dy, self.w, self.d, out=self.dx)
+        self.mark("dgrad", 1)
+        self.mark("wgrad", 0)
+        self.ops.conv2d_bwd_weight(self.x, self.dy, self.d, dw=self.dw)
+        self.mark("wgrad", 1)
 
     def work_per_step(self):
         return 2 * self.flop_one
 
+    def group_work(self):
+        return {"dgrad": self.flop_one, "wgrad": self.flop_one}
+
+    def config(self):
+        return {"workload": "conv2d_bwd (BASELINE configs[1])", "n": self.N, "c_in": self.C, "c_out": self.K,
+                "hw": self.H, "kernel": "3x3 s1 p1", "layout": "NCHW", "bias": False}
+
     def cpu_baseline(self, budget_s):
-        from oracle_lib import Ref, f32, rng
         import numpy as np
-        if not Ref.available():
+        from oracle_lib import f32, rng
+        ref = _ref()
+        if ref is None:
             return None
-        ref = Ref()
-        cores = host_cores()
-        ref.set_threads(cores)
         n = 8
         g = rng(0)
         d = self.ops.conv_desc((n, self.C, self.H, self.W), (self.K, self.C, 3, 3), padding=(1, 1))
         x = f32(g.standard_normal((n, self.C, self.H, self.W)))
         w = f32(g.standard_normal((self.K, self.C, 3, 3)) / math.sqrt(self.C * 9))
         dy = f32(g.standard_normal((n, self.K, self.H, self.W)))
-        sec = ref.conv2d_bwd_time(d, x, w, dy, 1)
-        iters = max(1, min(20000, int(budget_s / max(sec, 1e-6))))
+        iters = _iters_for(ref.conv2d_bwd_time(d, x, w, dy, 1), budget_s)
         sec = ref.conv2d_bwd_time(d, x, w, dy, iters)
         flop = 2 * 2.0 * n * self.H * self.W * self.K * self.C * 9
-        return {"value": flop / sec / 1e12, "unit": "TFLOP/s", "cores": ref.get_threads(), "kind": "reference",
-                "sample": f"Nott Conv2d (libtorch CPU autograd) dgrad+wgrad at N={n} of 128, fp32, "
-                          f"{iters} passes x {sec * 1e3:.1f} ms"}
+        return {"value": round(flop / sec / 1e12, 4), "unit": "TFLOP/s", "cores": ref.get_threads(),
+                "kind": "reference",
+                "sample": f"Nott Conv2d (libtorch CPU autograd) dgrad+wgrad, fp32, N={n} of 128 "
+                          f"(per-image work, scaled by FLOPs), {iters} passes x {sec * 1e3:.1f} ms"}
 
 
 class LnBwd(Workload):
     name = "ln_bwd"
     unit = "GB/s"
+    scale = 1e9
     R, D = 16384, 1024
-
-    def __init__(self, dtype):
-        self.dtype = dtype
 
     def setup(self, torch, ops):
         self.ops = ops
@@ -187,23 +234,35 @@ class LnBwd(Workload):
         self.bytes = 3 * self.R * self.D * s + self.D * s + 2 * self.R * 4 + 2 * self.D * 4
 
     def step(self):
+        self.mark("all", 0)
         self.ops.layernorm_bwd(self.x, self.dy, self.mean, self.rstd, self.gamma, dgamma=self.dg, dbeta=self.db,
                                out=self.dx)
+        self.mark("all", 1)
 
     def work_per_step(self):
         return self.bytes
 
+    def config(self):
+        return {"workload": "layernorm_bwd (BASELINE configs[2]a)", "rows": self.R, "d": self.D}
+
     def cpu_baseline(self, budget_s):
-        return None
+        ref = _ref()
+        if ref is None:
+            return None
+        iters = _iters_for(ref.layernorm_bwd_time(self.R, self.D, 1), budget_s, 1000)
+        sec = ref.layernorm_bwd_time(self.R, self.D, iters)
+        b32 = 3 * self.R * self.D * 4 + self.D * 4 + 2 * self.R * 4 + 2 * self.D * 4
+        return {"value": round(b32 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
+                "sample": f"at::native_layer_norm_backward (the op LayerNorm's autograd node runs), fp32, full "
+                          f"{self.R}x{self.D}, {iters} calls x {sec * 1e3:.2f} ms; GB/s on the fp32 algorithmic "
+                          f"bytes (the reference has no bf16 path)"}
 
 
 class Xent(Workload):
     name = "xent"
     unit = "GB/s"
+    scale = 1e9
     N, C = 16384, 32000
-
-    def __init__(self, dtype):
-        self.dtype = dtype
 
     def setup(self, torch, ops):
         self.ops = ops
@@ -216,19 +275,35 @@ class Xent(Workload):
         self.bytes = 2 * self.N * self.C * s + self.N * 8
 
     def step(self):
+        self.mark("all", 0)
         self.ops.softmax_xent_bwd(self.z, self.y, out=self.dz, with_loss=False)
+        self.mark("all", 1)
 
     def work_per_step(self):
         return self.bytes
+
+    def config(self):
+        return {"workload": "softmax_xent_grad (BASELINE configs[2]b)", "rows": self.N, "classes": self.C}
+
+    def cpu_baseline(self, budget_s):
+        ref = _ref()
+        if ref is None:
+            return None
+        rows = 512
+        iters = _iters_for(ref.cross_entropy_time(rows, self.C, 1), budget_s, 1000)
+        sec = ref.cross_entropy_time(rows, self.C, iters)
+        b32 = 2 * rows * self.C * 4 + rows * 8
+        return {"value": round(b32 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
+                "sample": f"Nott CrossEntropy forward + backward (log_softmax + nll_loss, libtorch CPU autograd), "
+                          f"fp32, {rows} of {self.N} rows x {self.C}, {iters} passes x {sec * 1e3:.2f} ms; GB/s on "
+                          f"the fp32 algorithmic bytes of those rows"}
 
 
 class AdamW(Workload):
     name = "adamw"
     unit = "GB/s"
+    scale = 1e9
     NP = 100_000_000
-
-    def __init__(self, dtype):
-        self.dtype = dtype
 
     def setup(self, torch, ops):
         self.ops = ops
@@ -241,86 +316,26 @@ class AdamW(Workload):
         self.bytes = self.NP * (22 if self.dtype == "bf16" else 28)
 
     def step(self):
+        self.mark("all", 0)
         self.ops.adam_step(self.p, self.g, self.m, self.v, lr=3e-4, weight_decay=0.01, step=10, decoupled=True)
+        self.mark("all", 1)
 
     def work_per_step(self):
         return self.bytes
 
+    def config(self):
+        return {"workload": "adamw_flat (BASELINE configs[2]c)", "params": self.NP, "step": 10}
+
     def cpu_baseline(self, budget_s):
-        from oracle_lib import Ref
-        if not Ref.available():
+        ref = _ref()
+        if ref is None:
             return None
-        ref = Ref()
-        ref.set_threads(host_cores())
         n = 10_000_000
-        sec = ref.adamw_time(n, 1)
-        iters = max(1, min(100, int(budget_s / max(sec, 1e-6))))
+        iters = _iters_for(ref.adamw_time(n, 1), budget_s, 200)
         sec = ref.adamw_time(n, iters)
-        return {"value": n * 28 / sec / 1e9, "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
+        return {"value": round(n * 28 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
                 "sample": f"Nott AdamW (torch::optim CPU) on a flat 1e7-param fp32 buffer, {iters} steps x "
                           f"{sec * 1e3:.1f} ms"}
-
-
-class TrainStep(Workload):
-    """One full training step (forward, CE mean, backward, fused Adam/AdamW,
-    zero_grad) through the C++ host layer: configs[0] small CNN (fp32, Adam)
-    or configs[4] ResNet-18 (AdamW; fp32 or bf16 mixed precision), batch 64."""
-    unit = "samples/s"
-    bound = "mfma"
-    BATCH = 64
-
-    graph = True   # forward + loss + backward replayed from a captured HIP graph (AdamW eager)
-
-    def __init__(self, dtype, model):
-        self.dtype = dtype
-        self.name = model
-
-    def setup(self, torch, ops):
-        import importlib
-        host = importlib.import_module("thot_amd._nott_host")
-        g = torch.Generator(device="cuda").manual_seed(4)
-        if self.name == "small_cnn":
-            self.tr = host.SmallCNNTrainer(0, 0, 1e-3)
-            self.x = torch.rand((self.BATCH, 1, 28, 28), generator=g, device="cuda")
-            self.y = torch.randint(0, 10, (self.BATCH,), generator=g, device="cuda")
-            # forward 2*MACs: conv1 1*32*9*784, conv2 32*64*9*196, fc 3136*128 + 128*10; training ~ 3x forward
-            self.flop_sample = 3 * 2.0 * (32 * 9 * 784 + 32 * 64 * 9 * 196 + 3136 * 128 + 128 * 10)
-        else:
-            self.tr = host.ResNet18Trainer(0, 0, self.dtype == "bf16", 1e-3, 1e-2, 1000)
-            self.x = torch.rand((self.BATCH, 3, 224, 224), generator=g, device="cuda")
-            self.y = torch.randint(0, 1000, (self.BATCH,), generator=g, device="cuda")
-            self.flop_sample = 3 * 2 * 1.814e9   # ResNet-18 at 224^2: 1.814 GMAC forward
-        self.tr.step(self.x, self.y)
-        if self.graph:
-            try:
-                self.tr.capture(self.x, self.y, 2)
-            except RuntimeError as e:   # reported in the JSON line via hip_graph = false
-                print(f"bench: HIP graph capture failed, stepping eagerly: {e}", file=sys.stderr)
-                self.graph = False
-
-    def step(self):
-        if self.graph:
-            self.tr.step_graph(self.x, self.y)
-        else:
-            self.tr.step(self.x, self.y)
-
-    def work_per_step(self):
-        return self.BATCH
-
-    def cpu_baseline(self, budget_s):
-        from oracle_lib import Ref
-        if not Ref.available():
-            return None
-        ref = Ref()
-        ref.set_threads(host_cores())
-        batch = 64 if self.name == "small_cnn" else 8
-        sec = ref.train_step_time(self.name, batch, 1)
-        iters = max(1, min(20000, int(budget_s / max(sec, 1e-6))))
-        sec = ref.train_step_time(self.name, batch, iters)
-        what = "configs[0] small CNN + Adam" if self.name == "small_cnn" else "configs[4] ResNet-18 + AdamW"
-        return {"value": batch / sec, "unit": "samples/s", "cores": ref.get_threads(), "kind": "reference",
-                "sample": f"{what}, fp32 libtorch CPU step built from Nott's layer descriptors, batch {batch}, "
-                          f"{iters} steps x {sec * 1e3:.1f} ms"}
 
 
 class MhaBwd(Workload):
@@ -335,11 +350,10 @@ class MhaBwd(Workload):
     dP, dQ, dK GEMMs) + 137.44 GFLOP projections."""
     name = "mha_bwd"
     unit = "TFLOP/s"
+    scale = 1e12
     bound = "mfma"
+    groups = ("out_proj", "attention", "in_proj")
     B, H, T, DH = 8, 16, 1024, 64
-
-    def __init__(self, dtype):
-        self.dtype = dtype
 
     def setup(self, torch, ops):
         self.torch, self.ops = torch, ops
@@ -357,34 +371,129 @@ class MhaBwd(Workload):
         self.o, self.lse = ops.attention_fwd(self.q, self.k, self.v, self.d)
         self.attn_out = self.o.view(B * T, E)
         self.dy = torch.randn((B * T, E), generator=g, device="cuda").to(dt)
+        self.dattn = torch.empty((B * T, E), dtype=dt, device="cuda")
         self.dqkv = torch.empty((B, T, 3 * E), dtype=dt, device="cuda")
         self.dqkv_views = tuple(self.dqkv[:, :, i * E:(i + 1) * E].view(B, T, H, DH) for i in range(3))
+        self.dx = torch.empty((B * T, E), dtype=dt, device="cuda")
         self.dw_in = torch.empty((3 * E, E), device="cuda")
         self.db_in = torch.empty((3 * E,), device="cuda")
         self.dw_out = torch.empty((E, E), device="cuda")
         self.db_out = torch.empty((E,), device="cuda")
         self.core_flop = 4 * 2.0 * B * H * DH * (T * (T + 1) / 2)
-        self.proj_flop = 2 * 2.0 * B * T * E * 3 * E + 2 * 2.0 * B * T * E * E
-        self.ev_a = [None, None]
+        self.out_flop = 2 * 2.0 * B * T * E * E
+        self.in_flop = 2 * 2.0 * B * T * E * 3 * E
 
     def step(self):
         ops = self.ops
         B, H, T, DH = self.B, self.H, self.T, self.DH
-        dattn, _, _ = ops.linear_bwd(self.dy, self.attn_out, self.w_out, dw=self.dw_out, db=self.db_out)
-        dO = dattn.view(B, T, H, DH)
-        if self.ev_a[0] is not None:
-            self.ev_a[0].record()
+        self.mark("out_proj", 0)
+        ops.linear_bwd(self.dy, self.attn_out, self.w_out, dx=self.dattn, dw=self.dw_out, db=self.db_out)
+        self.mark("out_proj", 1)
+        dO = self.dattn.view(B, T, H, DH)
+        self.mark("attention", 0)
         ops.attention_bwd(self.q, self.k, self.v, self.o, dO, self.lse, self.d, out=self.dqkv_views)
-        if self.ev_a[1] is not None:
-            self.ev_a[1].record()
-        ops.linear_bwd(self.dqkv.view(B * T, 3 * H * DH), self.x, self.w_in, dw=self.dw_in, db=self.db_in)
+        self.mark("attention", 1)
+        self.mark("in_proj", 0)
+        ops.linear_bwd(self.dqkv.view(B * T, 3 * H * DH), self.x, self.w_in, dx=self.dx, dw=self.dw_in,
+                       db=self.db_in)
+        self.mark("in_proj", 1)
 
     def work_per_step(self):
-        return self.core_flop + self.proj_flop
+        return self.core_flop + self.out_flop + self.in_flop
+
+    def group_work(self):
+        return {"out_proj": self.out_flop, "attention": self.core_flop, "in_proj": self.in_flop}
+
+    def config(self):
+        return {"workload": "mha_bwd (BASELINE configs[3])", "b": self.B, "heads": self.H, "t": self.T,
+                "dh": self.DH, "causal": True, "projections": "1024->3x1024 in, 1024->1024 out"}
+
+    def cpu_baseline(self, budget_s):
+        ref = _ref()
+        if ref is None:
+            return None
+        b = 1
+        E = self.H * self.DH
+        iters = _iters_for(ref.mha_bwd_time(b, self.T, E, self.H, True, 1), budget_s, 200)
+        sec = ref.mha_bwd_time(b, self.T, E, self.H, True, iters)
+        flop = self.work_per_step() * b / self.B
+        return {"value": round(flop / sec / 1e12, 4), "unit": "TFLOP/s", "cores": ref.get_threads(),
+                "kind": "reference",
+                "sample": f"Nott MultiHeadAttention backward (libtorch CPU autograd through the saved graph), fp32, "
+                          f"batch {b} of {self.B}, {iters} passes x {sec * 1e3:.1f} ms; TFLOP/s on the same "
+                          f"algorithmic FLOPs per sample"}
+
+
+class TrainStep(Workload):
+    """One full training step (forward, CE mean, backward, fused Adam/AdamW,
+    zero_grad) through the C++ host layer: configs[0] small CNN (fp32, Adam)
+    or configs[4] ResNet-18 (AdamW; fp32 or bf16 mixed precision), batch 64."""
+    unit = "samples/s"
+    bound = "mfma"
+    BATCH = 64
+    groups = ()
+
+    graph = True   # forward + loss + backward replayed from a captured HIP graph (AdamW eager)
+
+    def __init__(self, dtype, model):
+        super().__init__(dtype)
+        self.name = model
+
+    def setup(self, torch, ops):
+        import importlib
+        host = importlib.import_module("thot_amd._nott_host")
+        g = torch.Generator(device="cuda").manual_seed(4)
+        if self.name == "small_cnn":
+            self.tr = host.SmallCNNTrainer(0, 0, 1e-3)
+            self.x = torch.rand((self.BATCH, 1, 28, 28), generator=g, device="cuda")
+            self.y = torch.randint(0, 10, (self.BATCH,), generator=g, device="cuda")
+            # forward 2*MACs: conv1 1*32*9*784, conv2 32*64*9*196, fc 3136*128 + 128*10; training ~ 3x forward
+            self.flop_sample = 3 * 2.0 * (32 * 9 * 784 + 32 * 64 * 9 * 196 + 3136 * 128 + 128 * 10)
+        else:
+            self.tr = host.ResNet18Trainer(0, 0, self.dtype == "bf16", 1e-3, 1e-2, 1000)
+            self.x = torch.rand((self.BATCH, 3, 224, 224), generator=g, device="cuda")
+            self.y = torch.randint(0, 1000, (self.BATCH,), generator=g, device="cuda")
+            self.flop_sample = 681.5e9 / 64   # 3 x 1.814 GMAC forward - stem dgrad, per image
+        self.tr.step(self.x, self.y)
+        if self.graph:
+            try:
+                self.tr.capture(self.x, self.y, 2)
+            except RuntimeError as e:   # reported in the JSON line via hip_graph = false
+                print(f"bench: HIP graph capture failed, stepping eagerly: {e}", file=sys.stderr)
+                self.graph = False
+
+    def step(self):
+        if self.graph:
+            self.tr.step_graph(self.x, self.y)
+        else:
+            self.tr.step(self.x, self.y)
+
+    def work_per_step(self):
+        return self.BATCH
+
+    def config(self):
+        return {"workload": f"{self.name} training step (BASELINE configs[{0 if self.name == 'small_cnn' else 4}])",
+                "batch": self.BATCH, "optimizer": "Adam" if self.name == "small_cnn" else "AdamW",
+                "hip_graph": self.graph}
+
+    def cpu_baseline(self, budget_s):
+        ref = _ref()
+        if ref is None:
+            return None
+        batch = 64 if self.name == "small_cnn" else 8
+        iters = _iters_for(ref.train_step_time(self.name, batch, 1), budget_s)
+        sec = ref.train_step_time(self.name, batch, iters)
+        what = "configs[0] small CNN + Adam" if self.name == "small_cnn" else "configs[4] ResNet-18 + AdamW"
+        note = "" if self.dtype == "f32" else " (the reference has no bf16 path: its fp32 step)"
+        return {"value": round(batch / sec, 2), "unit": "samples/s", "cores": ref.get_threads(), "kind": "reference",
+                "sample": f"{what}, fp32 libtorch CPU step built from Nott's layer descriptors{note}, batch {batch}, "
+                          f"{iters} steps x {sec * 1e3:.1f} ms"}
 
 
 WORKLOADS = {"conv_bwd": ConvBwd, "ln_bwd": LnBwd, "xent": Xent, "adamw": AdamW, "mha_bwd": MhaBwd,
              "small_cnn": lambda dt: TrainStep(dt, "small_cnn"), "resnet18": lambda dt: TrainStep(dt, "resnet18")}
+DEFAULT_DTYPE = {"conv_bwd": "f32", "ln_bwd": "f32", "xent": "f32", "adamw": "f32", "mha_bwd": "bf16",
+                 "small_cnn": "f32", "resnet18": "bf16"}
 
 
 def time_workload(torch, wl, steps, warmup):
@@ -396,53 +505,60 @@ def time_workload(torch, wl, steps, warmup):
     for _ in range(steps):
         wl.step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    return ms
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def kernel_ms(torch, wl, steps, pairs_attr):
+def group_ms(torch, wl, steps):
     """Average duration of each bracketed launch group, from HIP events recorded
     on torch's current stream (the stream the C ABI launches on).  The steps
     are queued back to back with one synchronisation at the end, so a start
-    event fires when the previous step's work drains, not when the host gets
-    round to the next launch."""
+    event fires when the previous work drains, not when the host gets round
+    to the next launch."""
+    if not wl.groups:
+        return {}
     wl.step()
     pairs = []
     for _ in range(steps):
-        step_pairs = {}
-        for k in pairs_attr:
-            step_pairs[k] = [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-            getattr(wl, k)[0], getattr(wl, k)[1] = step_pairs[k]
+        wl.ev = {k: [torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for k in wl.groups}
         wl.step()
-        pairs.append(step_pairs)
+        pairs.append(wl.ev)
     torch.cuda.synchronize()
-    out = {}
-    for k in pairs_attr:
-        getattr(wl, k)[0] = getattr(wl, k)[1] = None
-        out[k] = sum(p[k][0].elapsed_time(p[k][1]) for p in pairs) / steps
-    return out
+    wl.ev = {}
+    return {k: sum(p[k][0].elapsed_time(p[k][1]) for p in pairs) / steps for k in wl.groups}
 
 
-def simple_kernel_ms(torch, wl, steps):
-    """Event-timed average of one whole step (for one-entry-point workloads),
-    steps queued back to back on the launch stream."""
-    wl.step()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        wl.step()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
-
-
-def run_bandwidth_leg(torch, ops, cls, dtype, steps, warmup):
-    wl = cls(dtype)
+def measure(torch, ops, wl, steps, warmup, cpu_budget):
+    """One leg: value from wall-clock steps, roofline from event-timed groups,
+    CPU baseline from the reference on a bounded sample."""
     wl.setup(torch, ops)
     ms = time_workload(torch, wl, steps, warmup)
-    kms = simple_kernel_ms(torch, wl, steps)
-    gbs = wl.work_per_step() / (kms * 1e-3) / 1e9
-    return wl, ms, kms, gbs
+    rec = {"value": round(wl.work_per_step() / (ms * 1e-3) / wl.scale, 3), "unit": wl.unit, "dtype": wl.dtype,
+           "ms_per_step": round(ms, 4), "config": wl.config()}
+    per = group_ms(torch, wl, steps)
+    if per:
+        work = wl.group_work()
+        dom = wl.dominant(per)
+        peak = wl.peak()
+        unit = "GB/s" if wl.bound == "hbm" else "TFLOP/s"
+        div = 1e9 if wl.bound == "hbm" else 1e12
+        ach = work[dom] / (per[dom] * 1e-3) / div
+        rec["roofline"] = {"bound": wl.bound, "kernel": f"{wl.name}:{dom}", "achieved": round(ach, 2), "peak": peak,
+                           "unit": unit, "frac": round(ach / peak, 4),
+                           "traffic": TRAFFIC.get((wl.name, wl.dtype, dom)), "traffic_unit": "B",
+                           "per_group_ms": {k: round(v, 4) for k, v in per.items()},
+                           "per_group_rate": {k: round(work[k] / (v * 1e-3) / div, 2) for k, v in per.items()}}
+    else:   # whole training steps: model FLOPs over the step
+        ach = wl.flop_sample * (wl.BATCH / (ms * 1e-3)) / 1e12
+        peak = wl.peak()
+        rec["roofline"] = {"bound": "mfma", "kernel": f"{wl.name}: whole training step (model FLOPs)",
+                           "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                           "traffic": None}
+    if cpu_budget > 0:
+        try:
+            rec["cpu_baseline"] = wl.cpu_baseline(cpu_budget)
+        except Exception as e:  # reported, never fatal for the GPU measurement
+            rec["cpu_baseline"] = {"error": repr(e)}
+    return rec
 
 
 def main():
@@ -452,9 +568,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="conv_bwd", choices=sorted(WORKLOADS))
     ap.add_argument("--dtype", default=None, choices=["bf16", "f32"])
-    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for cpu_baseline")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU work for the headline cpu_baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="headline leg only")
     ap.add_argument("--eager", action="store_true",
                     help="training-step workloads: run every step eagerly instead of replaying a captured HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
@@ -482,125 +598,55 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    dtype = args.dtype or ("f32" if args.workload in ("ln_bwd", "xent", "adamw", "small_cnn") else "bf16")
     TrainStep.graph = not args.eager
-    wl = WORKLOADS[args.workload](dtype)
-    wl.setup(torch, ops)
-    wl.ev0 = wl.ev1 = None
-    ms = time_workload(torch, wl, args.steps, args.warmup)
-    value_per_s = wl.work_per_step() / (ms * 1e-3)
+    dtype = args.dtype or DEFAULT_DTYPE[args.workload]
+    cpu_budget = 0.0 if args.no_cpu else args.cpu_budget
+    head = measure(torch, ops, WORKLOADS[args.workload](dtype), args.steps, args.warmup, cpu_budget)
+    torch.cuda.empty_cache()
 
-    if args.workload == "conv_bwd":
-        kms = kernel_ms(torch, wl, args.steps, ["ev_d", "ev_w"])
-        value = value_per_s / 1e12
-        per = {"dgrad": kms["ev_d"], "wgrad": kms["ev_w"]}
-        dom = max(per, key=per.get)
-        ach = wl.flop_one / (per[dom] * 1e-3) / 1e12
-        peak = MFMA_PEAK_TFLOPS[dtype]
-        roof = {"bound": "mfma", "kernel": f"conv2d_{dom}", "achieved": round(ach, 2), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": traffic_for("conv_bwd", dtype, dom), "traffic_unit": "B",
-                "per_kernel_ms": {k: round(v, 4) for k, v in per.items()},
-                "per_kernel_tflops": {k: round(wl.flop_one / (v * 1e-3) / 1e12, 2) for k, v in per.items()}}
-        metric_part = "conv-bwd TFLOP/s"
-        cfg = {"workload": "conv2d_bwd (BASELINE configs[1])", "n": wl.N, "c_in": wl.C, "c_out": wl.K,
-               "hw": wl.H, "kernel": "3x3 s1 p1", "layout": "NCHW", "bias": False}
-    elif args.workload == "mha_bwd":
-        kms = kernel_ms(torch, wl, args.steps, ["ev_a"])["ev_a"]
-        value = value_per_s / 1e12
-        ach = wl.core_flop / (kms * 1e-3) / 1e12
-        peak = MFMA_PEAK_TFLOPS[dtype]
-        roof = {"bound": "mfma", "kernel": "attention_bwd (dq + dkdv)", "achieved": round(ach, 2), "peak": peak,
-                "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None, "launch_ms": round(kms, 4)}
-        metric_part = "MHA-bwd TFLOP/s"
-        cfg = {"workload": "mha_bwd (BASELINE configs[3])", "b": wl.B, "heads": wl.H, "t": wl.T, "dh": wl.DH,
-               "causal": True, "projections": "1024->3x1024 in, 1024->1024 out"}
-    elif args.workload in ("small_cnn", "resnet18"):
-        value = value_per_s
-        ach = wl.flop_sample * value / 1e12
-        peak = MFMA_PEAK_TFLOPS[dtype]
-        roof = {"bound": "mfma", "kernel": "whole training step (model FLOPs, ~3x forward)", "achieved": round(ach, 2),
-                "peak": peak, "unit": "TFLOP/s", "frac": round(ach / peak, 4), "traffic": None}
-        metric_part = "train samples/s"
-        cfg = {"workload": f"{wl.name} training step (BASELINE configs[{0 if wl.name == 'small_cnn' else 4}])",
-               "batch": wl.BATCH, "optimizer": "Adam" if wl.name == "small_cnn" else "AdamW",
-               "hip_graph": wl.graph}
-    else:
-        kms = simple_kernel_ms(torch, wl, args.steps)
-        value = wl.work_per_step() / (ms * 1e-3) / 1e9
-        ach = wl.work_per_step() / (kms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "kernel": wl.name, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic_for(wl.name, dtype, None), "traffic_unit": "B",
-                "launch_ms": round(kms, 4)}
-        metric_part = {"ln_bwd": "LN-bwd GB/s", "xent": "CE-grad GB/s", "adamw": "AdamW GB/s"}[wl.name]
-        cfg = {"workload": wl.name}
-
-    extra = {}
+    legs = {}
     if not args.no_extra and args.workload == "conv_bwd":
-        del wl.x, wl.dy, wl.dx
-        torch.cuda.empty_cache()
-        for nm, cls in (("ln_bwd", LnBwd), ("adamw", AdamW), ("xent", Xent)):
-            for dt in ("f32", "bf16"):
-                leg, lms, lk, gbs = run_bandwidth_leg(torch, ops, cls, dt, args.steps, args.warmup)
-                extra[f"{nm}_{dt}"] = {"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                                       "kernel_ms": round(lk, 4)}
-                del leg
-                torch.cuda.empty_cache()
-        leg = ConvBwd("f32")
-        leg.setup(torch, ops)
-        lms = time_workload(torch, leg, max(3, args.steps // 4), 1)
-        extra["conv_bwd_f32"] = {"TFLOP/s": round(leg.work_per_step() / (lms * 1e-3) / 1e12, 2),
-                                 "frac_mfma": round(leg.work_per_step() / (lms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["f32"], 4)}
-        del leg
-        torch.cuda.empty_cache()
-        leg = MhaBwd("bf16")
-        leg.setup(torch, ops)
-        lms = time_workload(torch, leg, args.steps, args.warmup)
-        ams = kernel_ms(torch, leg, args.steps, ["ev_a"])["ev_a"]
-        extra["mha_bwd_bf16"] = {"TFLOP/s": round(leg.work_per_step() / (lms * 1e-3) / 1e12, 2), "ms": round(lms, 4),
-                                 "core_TFLOP/s": round(leg.core_flop / (ams * 1e-3) / 1e12, 2)}
-        del leg
-        torch.cuda.empty_cache()
-        for model, dt in (("small_cnn", "f32"), ("resnet18", "bf16"), ("resnet18", "f32")):
-            leg = TrainStep(dt, model)
-            leg.setup(torch, ops)
-            lms = time_workload(torch, leg, args.steps, args.warmup)
-            rec = {"samples/s": round(leg.BATCH / (lms * 1e-3), 1), "ms_per_step": round(lms, 3), "hip_graph": leg.graph,
-                   "batch": leg.BATCH}
-            if not args.no_cpu and dt == "f32":
-                try:
-                    rec["cpu_baseline"] = leg.cpu_baseline(args.cpu_budget / 2)
-                except Exception as e:
-                    rec["cpu_baseline"] = {"error": repr(e)}
-            extra[f"{model}_{dt}"] = rec
-            del leg
+        leg_budget = 0.0 if args.no_cpu else max(1.0, args.cpu_budget / 3)
+        plan = [("conv_bwd", "bf16" if dtype == "f32" else "f32"), ("ln_bwd", "f32"), ("ln_bwd", "bf16"),
+                ("adamw", "f32"), ("adamw", "bf16"), ("xent", "f32"), ("xent", "bf16"), ("mha_bwd", "bf16"),
+                ("small_cnn", "f32"), ("resnet18", "bf16"), ("resnet18", "f32")]
+        cpu_done = {}
+        for name, dt in plan:
+            wl = WORKLOADS[name](dt)
+            # One CPU baseline per workload (the reference computes in fp32 only).
+            key = name
+            rec = measure(torch, ops, wl, args.steps, args.warmup, 0.0 if key in cpu_done else leg_budget)
+            if key in cpu_done:
+                rec["cpu_baseline"] = cpu_done[key]
+            elif "cpu_baseline" in rec:
+                cpu_done[key] = rec["cpu_baseline"]
+            legs[f"{name}_{dt}"] = rec
+            del wl
             torch.cuda.empty_cache()
 
-    cpu = None
-    if not args.no_cpu:
-        try:
-            cpu = wl.cpu_baseline(args.cpu_budget)
-        except Exception as e:  # reported, never fatal for the GPU measurement
-            cpu = {"error": repr(e)}
-
+    metric_part = {"conv_bwd": "conv-bwd TFLOP/s", "ln_bwd": "LN-bwd GB/s", "xent": "CE-grad GB/s",
+                   "adamw": "AdamW GB/s", "mha_bwd": "MHA-bwd TFLOP/s", "small_cnn": "train samples/s",
+                   "resnet18": "train samples/s"}[args.workload]
     line = {
         "metric": f"{metric_part} (of: {METRIC})",
-        "value": round(value, 3),
-        "unit": wl.unit,
+        "value": head["value"],
+        "unit": head["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
         "data": "synthetic (seeded torch generator on device; inputs resident in HBM)",
-        "config": cfg,
-        "roofline": roof,
-        "cpu_baseline": cpu,
+        "config": head["config"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "host": host_info(),
     }
-    if extra:
-        line["extra"] = extra
+    if legs:
+        line["legs"] = legs
     print(json.dumps(line), flush=True)
 
 

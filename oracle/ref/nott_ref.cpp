@@ -573,6 +573,78 @@ int ref_adamw_time(int64_t n, int iters, double* sec) {
     });
 }
 
+// Seconds per call of the ATen op LayerNorm's autograd node runs backward
+// (native_layer_norm_backward, for the norms of classic.hpp:403-404) on
+// x ~ N(0,1) [rows, d], gamma ~ N(1, 0.1), beta = 0, dy ~ N(0,1).
+int ref_layernorm_bwd_time(int64_t rows, int64_t d, int iters, double* sec) {
+    return guarded([&] {
+        torch::manual_seed(1);
+        auto x = torch::randn({rows, d});
+        auto gamma = 1 + 0.1 * torch::randn({d});
+        auto beta = torch::zeros({d});
+        auto dy = torch::randn({rows, d});
+        auto fwd = at::native_layer_norm(x, {d}, gamma, beta, 1e-5);
+        const auto& mean = std::get<1>(fwd);
+        const auto& rstd = std::get<2>(fwd);
+        auto once = [&] { return at::native_layer_norm_backward(dy, x, {d}, mean, rstd, gamma, beta, {true, true, true}); };
+        once();
+        auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) once();
+        auto t1 = std::chrono::steady_clock::now();
+        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+    });
+}
+
+// Seconds per forward + backward of Nott's CrossEntropy loss (ce.hpp:21-37,
+// mean reduction; log_softmax + nll_loss and their backward, as
+// core.hpp:3777-3819 runs them) on logits ~ N(0, 2) [n, c], labels uniform.
+int ref_cross_entropy_time(int64_t n, int64_t c, int iters, double* sec) {
+    return guarded([&] {
+        torch::manual_seed(2);
+        auto z = (2 * torch::randn({n, c})).requires_grad_(true);
+        auto y = torch::randint(0, c, {n}, torch::kInt64);
+        Nott::Loss::Details::CrossEntropyDescriptor desc;
+        auto once = [&] {
+            auto l = Nott::Loss::Details::compute(desc, z, y);
+            l.backward();
+            z.mutable_grad().reset();
+        };
+        once();
+        auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) once();
+        auto t1 = std::chrono::steady_clock::now();
+        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+    });
+}
+
+// Seconds per backward pass of Nott's MultiHeadAttention (head.hpp:22-98,
+// self-attention, batch_first, with bias) through its saved graph: x ~ N(0,1)
+// [b, t, e], weights ~ N(0, 0.02), dy ~ N(0,1).  The graph is kept between
+// passes (retain_graph), so only the backward is timed.
+int ref_mha_bwd_time(int64_t b, int64_t t, int64_t e, int64_t heads, int causal, int iters, double* sec) {
+    return guarded([&] {
+        torch::manual_seed(5);
+        Nott::Attention::Details::MultiHeadAttentionOptions o;
+        o.embed_dim = e;
+        o.num_heads = heads;
+        o.dropout = 0.0;
+        o.bias = true;
+        o.batch_first = true;
+        o.variant = causal ? Nott::Attention::Variant::Causal : Nott::Attention::Variant::Full;
+        Nott::Attention::Details::MultiHeadAttention mha(o);
+        for (const char* w : {"q_proj.weight", "k_proj.weight", "v_proj.weight", "out_proj.weight"})
+            set_param(*mha, w, 0.02 * torch::randn({e, e}));
+        auto xt = torch::randn({b, t, e}).requires_grad_(true);
+        auto yt = mha->forward(xt, xt, xt);
+        auto dy = torch::randn({b, t, e});
+        yt.backward(dy, /*retain_graph=*/true);
+        auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) yt.backward(dy, /*retain_graph=*/true);
+        auto t1 = std::chrono::steady_clock::now();
+        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+    });
+}
+
 // kernel.hpp:20-96 (ScaledDotProductKernel; Variant::Causal when causal).
 int ref_attention(const nott_attn_desc* d, const float* q, const float* k, const float* v, const float* dO, float* o,
                   float* dq, float* dk, float* dv) {

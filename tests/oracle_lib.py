@@ -332,6 +332,22 @@ class Ref:
         self._ok(self.lib.ref_adamw_time(i64(n), C.c_int(iters), C.byref(sec)))
         return sec.value
 
+    def layernorm_bwd_time(self, rows: int, d: int, iters: int) -> float:
+        sec = C.c_double()
+        self._ok(self.lib.ref_layernorm_bwd_time(i64(rows), i64(d), C.c_int(iters), C.byref(sec)))
+        return sec.value
+
+    def cross_entropy_time(self, n: int, c: int, iters: int) -> float:
+        sec = C.c_double()
+        self._ok(self.lib.ref_cross_entropy_time(i64(n), i64(c), C.c_int(iters), C.byref(sec)))
+        return sec.value
+
+    def mha_bwd_time(self, b: int, t: int, e: int, heads: int, causal: bool, iters: int) -> float:
+        sec = C.c_double()
+        self._ok(self.lib.ref_mha_bwd_time(i64(b), i64(t), i64(e), i64(heads), C.c_int(int(causal)), C.c_int(iters),
+                                           C.byref(sec)))
+        return sec.value
+
     def small_cnn_forward_archive(self, path: str, x):
         """configs[0] logits of the reference-built model after loading the
         parameters.binary archive at `path`."""

@@ -9,10 +9,12 @@
 //   dw = dyᵀ·x            (TN: both k-strided; split-K over rows)
 //   db = Σ_rows dy        (folded into the dw GEMM as an extra all-ones column;
 //                          bf16 fast path: a two-phase column sum)
-// bf16 operands whose k extent is a multiple of 64 take the fast GEMM path
-// (gemm.hpp, namespace fast); everything else the generic engine.  Every
-// product runs on the kernels in this library; no vendor GEMM is called.
-#include "gemm.hpp"
+// bf16 operands whose k extent is a multiple of 64 take the direct-to-LDS
+// GEMM (gemm_dma.hpp) when both output extents are at least 128, else the
+// register-staged fast GEMM (gemm.hpp, namespace fast); everything else the
+// generic engine.  Every product runs on the kernels in this library; no
+// vendor GEMM is called.
+#include "gemm_dma.hpp"
 
 namespace {
 
@@ -164,11 +166,21 @@ int launch_db(nott_ctx ctx, const T* dy, int64_t m, int64_t nout, float* db, int
     return launch_status(ctx, "linear db");
 }
 
+// bf16 C = A·B on the direct-to-LDS engine, else the register-staged one;
+// NOTT_ERR_UNSUPPORTED when neither takes the operands.
+template <bool AT, bool BT, class EP>
+int bf16_gemm(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep, int64_t M,
+              int64_t N, int64_t K) {
+    const int st = dma::run<AT, BT>(ctx, A, lda, B, ldb, ep, M, N, K);
+    if (st != NOTT_ERR_UNSUPPORTED) return st;
+    return fast::run<AT, BT>(ctx, A, lda, B, ldb, ep, M, N, K);
+}
+
 template <typename T>
 int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
     if constexpr (sizeof(T) == 2) {
         RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
-        const int st = fast::run<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
+        const int st = bf16_gemm<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
                                                m, nout, kin);
         if (st != NOTT_ERR_UNSUPPORTED) return st;
     }
@@ -199,7 +211,7 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
         if (fx && fw) {
             if (dx) {
                 RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
-                const int st = fast::run<false, true>(ctx, dyp, nout, static_cast<const T*>(w), kin, ep, m, kin, nout);
+                const int st = bf16_gemm<false, true>(ctx, dyp, nout, static_cast<const T*>(w), kin, ep, m, kin, nout);
                 if (st != NOTT_ERR_UNSUPPORTED) {
                     if (st != NOTT_OK) return st;
                     dx = nullptr;
@@ -207,7 +219,7 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
             }
             if (dw) {
                 DwDbStore ep{dw, nullptr, nout, kin, accumulate};
-                const int st = fast::run<true, true>(ctx, dyp, nout, static_cast<const T*>(x), kin, ep, nout, kin, m);
+                const int st = bf16_gemm<true, true>(ctx, dyp, nout, static_cast<const T*>(x), kin, ep, nout, kin, m);
                 if (st != NOTT_ERR_UNSUPPORTED) {
                     if (st != NOTT_OK) return st;
                     dw = nullptr;

@@ -337,14 +337,19 @@ def linear_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = Non
 
 
 def linear_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, *, need_dx: bool = True, need_dw: bool = True,
-               need_db: bool = True, dw: Optional[torch.Tensor] = None, db: Optional[torch.Tensor] = None,
-               accumulate: bool = False):
+               need_db: bool = True, dx: Optional[torch.Tensor] = None, dw: Optional[torch.Tensor] = None,
+               db: Optional[torch.Tensor] = None, accumulate: bool = False):
     _check(x, "x")
     m, kin = x.reshape(-1, x.shape[-1]).shape
     nout = w.shape[0]
     _check(w, "w", shape=(nout, kin), dtype=x.dtype, device=x.device)
     _check(dy, "dy", shape=(*x.shape[:-1], nout), dtype=x.dtype, device=x.device)
-    dx = torch.empty_like(x) if need_dx else None
+    if need_dx and dx is None:
+        dx = torch.empty_like(x)
+    if need_dx:
+        _check(dx, "dx", shape=tuple(x.shape), dtype=x.dtype, device=x.device)
+    else:
+        dx = None
     if need_dw and dw is None:
         dw = torch.empty((nout, kin), dtype=torch.float32, device=x.device)
     if need_db and db is None:
