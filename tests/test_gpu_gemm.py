@@ -54,6 +54,46 @@ def test_linear(ops, oracle, dt, m, kin, nout):
     check(host(db), rdb, "f32" if dt == "f32" else dt, "linear db")
 
 
+# bf16 shapes chosen for the direct-to-LDS GEMM's tile plans, each with
+# partial tiles: (4104, 192, 2056) forward on 256x128 tiles; (2048, 1288,
+# 1544) dW on 256x256 tiles split over K with the fused bias gradient;
+# (1024, 200, 320) dX on unsplit 128x128 and dW split 4 ways; (256, 384, 256)
+# dW unsplit over three tile columns (the bias gradient is summed once).
+DMA_LIN = [(4104, 192, 2056), (2048, 1288, 1544), (1024, 200, 320), (256, 384, 256)]
+
+
+def _edge(idx, n):
+    return np.unique(np.clip(np.asarray(idx), 0, n - 1))
+
+
+@pytest.mark.parametrize("accumulate", [False, True], ids=["set", "accumulate"])
+@pytest.mark.parametrize("m,kin,nout", DMA_LIN)
+def test_linear_bf16_tile_shapes(ops, oracle, m, kin, nout, accumulate):
+    """Rows of y and dx, and output rows of dw and db (sums over every
+    token), at the tile edges, against the oracle; accumulate adds into
+    existing fp32 gradients."""
+    dt = "bf16"
+    g = rng(5 + m + kin + nout)
+    x = host_input(g.standard_normal((m, kin)), dt)
+    w = host_input(g.standard_normal((nout, kin)) / math.sqrt(kin), dt)
+    b = f32(g.standard_normal(nout) * 0.1)
+    dy = host_input(g.standard_normal((m, nout)), dt)
+    xd, wd, dyd = dev(x, dt), dev(w, dt), dev(dy, dt)
+    dw0 = f32(g.standard_normal((nout, kin))) if accumulate else np.zeros((nout, kin), np.float32)
+    db0 = f32(g.standard_normal(nout)) if accumulate else np.zeros(nout, np.float32)
+    y = ops.linear_fwd(xd, wd, dev(b))
+    dx, dw, db = ops.linear_bwd(dyd, xd, wd, dw=dev(dw0), db=dev(db0), accumulate=accumulate)
+    torch.cuda.synchronize()
+    rows = _edge(np.r_[0:4, 124:132, 252:260, m // 2:m // 2 + 4, m - 4:m], m)
+    check(host(y)[rows], oracle.linear_fwd(x[rows], w, b), dt, "y rows")
+    rdx, _, _ = oracle.linear_bwd(dy[rows], x[rows], w)
+    check(host(dx)[rows], rdx, dt, "dx rows")
+    outs = _edge(np.r_[0:4, 124:132, 252:260, nout - 4:nout], nout)
+    _, rdw, rdb = oracle.linear_bwd(np.ascontiguousarray(dy[:, outs]), x, np.ascontiguousarray(w[outs]))
+    check(host(dw)[outs], dw0[outs] + rdw, dt, "dw rows")
+    check(host(db)[outs], db0[outs] + rdb, dt, "db rows")
+
+
 def test_linear_golden(ops):
     z = np.load(os.path.join(GOLD, "linear.npz"))
     x, w, b, dy = (f32(z[k]) for k in ("x", "w", "b", "dy"))

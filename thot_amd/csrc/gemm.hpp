@@ -285,6 +285,42 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     if (wid == 0 && i < MN) ep.store(i / N, i % N, (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]));
 }
 
+// Vector form of splitk_reduce_kernel for N % 4 == 0: a thread owns 4
+// consecutive outputs of one row, loads them as one 16-byte word per split
+// (8 splits' loads in flight) and adds the splits in order 0, 1, 2, ...
+template <class EP>
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __restrict__ ws, int64_t splits, int64_t M,
+                                                             int64_t N, EP ep) {
+    const int64_t MN = M * N;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= MN) return;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    int64_t z = 0;
+    for (; z + 8 <= splits; z += 8) {
+        f32x4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + (z + u) * MN + i));
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += t[u];
+    }
+    for (; z < splits; ++z) s += __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(ws + z * MN + i));
+    const int64_t m = i / N, n = i - m * N;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ep.store(m, n + e, s[e]);
+}
+
+// Sums split-K partials ws[splits][M][N] (fp32, 16-byte aligned) through
+// the epilogue, in split order.
+template <class EP>
+void launch_splitk_reduce(nott_ctx ctx, const float* ws, int64_t splits, int64_t M, int64_t N, const EP& ep) {
+    if (N % 4 == 0 && ((uintptr_t)ws % 16) == 0)
+        hipLaunchKernelGGL((splitk_reduce4_kernel<EP>), dim3((unsigned)ceil_div(M * N, 1024)), dim3(256), 0,
+                           ctx->stream, ws, splits, M, N, ep);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
+                           ws, splits, M, N, ep);
+}
+
 // Picks a split count that gives the grid at least ~2 workgroups per CU
 // while keeping each split at least `min_k` long.
 inline int64_t pick_splits(int64_t tiles, int64_t K, int64_t num_cu, int64_t bk) {
@@ -322,8 +358,7 @@ int run(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64
     PartialStore ps{ws, M, N};
     hipLaunchKernelGGL((gemm_kernel<T, LA, LB, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
                        dim3(kThreads), 0, ctx->stream, la, lb, ps, M, N, K, kps);
-    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
-                       ws, splits, M, N, ep);
+    launch_splitk_reduce(ctx, ws, splits, M, N, ep);
     return launch_status(ctx, "gemm_splitk");
 }
 
@@ -527,8 +562,7 @@ int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
     PartialStore ps{ws, M, N};
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
                        dim3(kThreads), lds, ctx->stream, A, lda, B, ldb, ps, M, N, K, kps);
-    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
-                       ws, splits, M, N, ep);
+    launch_splitk_reduce(ctx, ws, splits, M, N, ep);
     return launch_status(ctx, "gemm_bf16_splitk");
 }
 

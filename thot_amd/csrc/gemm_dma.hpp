@@ -27,8 +27,9 @@
 // are in flight while one is multiplied.  Only s_waitcnt vmcnt (how many of
 // this wave's loads may still be outstanding) and s_barrier order the ring;
 // the compiler's workgroup fence (which would wait for every load) is not
-// used.  Within a stage the four 16-deep slices are software-pipelined: the
-// fragments of slice s+1 are read while slice s is multiplied.
+// used, and the DMA is issued as inline assembly (see dma16).  Within a
+// stage the four 16-deep slices are software-pipelined: the fragments of
+// slice s+1 are read while slice s is multiplied.
 //
 // Tile order.  Workgroups are dispatched round-robin over the 8 XCDs (each
 // with its own L2); the linear tile index is remapped so that each XCD gets
@@ -63,6 +64,18 @@ __device__ __forceinline__ void barrier() {
     asm volatile("" ::: "memory");
 }
 
+__device__ __forceinline__ uint32_t lds_addr(const char NOTT_LDS* p) { return (uint32_t)(uintptr_t)p; }
+
+// global_load_lds_dwordx4: 16 bytes per lane from `src` to LDS byte
+// lds + 16·lane (lds wave-uniform, through M0).  Issued as inline assembly
+// so that the compiler does not see an LDS DMA in flight: it would otherwise
+// make every later transposing LDS read wait for all outstanding loads
+// (vmcnt(0)), which serialises the ring.  The ring's own waits (vmcnt and
+// the barrier) order the DMA against the reads.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
+}
+
 // Issues this wave's share of one operand tile (R rows × 64 k) of stage k0.
 // Rows past `rows` are clamped to the last row (their results are never
 // stored); row-contiguous operands need rows % 8 == 0 and rows >= 8.
@@ -91,48 +104,30 @@ __device__ __forceinline__ void fill(const bf16_t* __restrict__ p, int64_t ld, i
             gc = gc <= rows - 8 ? gc : rows - 8;
             src = p + (k0 + k) * ld + gc;
         }
-        __builtin_amdgcn_global_load_lds(src, dst + 1024 * q, 16, 0, 0);
+        dma16(src, lds_addr(dst) + 1024 * q);
     }
 }
 
-// LDS fragment reads are issued as inline assembly so that this file, not
-// the compiler, owns their ordering: the compiler treats a transposing LDS
-// read as aliasing every LDS DMA still in flight and would wait for all of
-// them (vmcnt(0)) before each one, which serialises the ring.  A read's
-// result is used only after an explicit lgkmcnt wait tied to its registers.
-__device__ __forceinline__ uint32_t lds_addr(const char NOTT_LDS* p) { return (uint32_t)(uintptr_t)p; }
-
-template <int OFF>
-__device__ __forceinline__ void ds_b128(u32x4& d, uint32_t a) {
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(a), "i"(OFF));
-}
-template <int OFF>
-__device__ __forceinline__ void ds_tr(u32x2& d, uint32_t a) {
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(d) : "v"(a), "i"(OFF));
-}
-template <int N>
-__device__ __forceinline__ void wait_lgkm() {
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N));
-}
-
-// A 32×16 MFMA operand (lane l: row l % 32, k = 8·(l/32) + 0..7) as the
-// registers its reads fill: one 16-byte read from a [row][k] tile, or two
-// transposing 8-byte reads from a [k][row] tile.
+// A 32×16 MFMA operand (lane l: row l % 32, k = 8·(l/32) + 0..7): one
+// 16-byte read from a [row][k] tile, or two transposing 8-byte reads from a
+// [k][row] tile.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 template <bool TR> struct Frag;
 template <> struct Frag<false> {
     u32x4 v;
-    static constexpr int kReads = 1;
     __device__ __forceinline__ bf16x8 get() const { return __builtin_bit_cast(bf16x8, v); }
-    __device__ __forceinline__ void tie() { asm volatile("" : "+v"(v)); }
+    __device__ __forceinline__ void ld(const char NOTT_LDS* p) { v = *reinterpret_cast<const u32x4 NOTT_LDS*>(p); }
 };
 template <> struct Frag<true> {
-    u32x2 lo, hi;
-    static constexpr int kReads = 2;
+    v4i16 lo, hi;
     __device__ __forceinline__ bf16x8 get() const {
-        const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
+        const v4i16 w[2] = {lo, hi};
         return __builtin_bit_cast(bf16x8, w);
     }
-    __device__ __forceinline__ void tie() { asm volatile("" : "+v"(lo), "+v"(hi)); }
+    __device__ __forceinline__ void ld(const char NOTT_LDS* p, int hi_off) {
+        lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 NOTT_LDS*)p);
+        hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 NOTT_LDS*)(p + hi_off));
+    }
 };
 
 // Per-lane LDS byte offsets of one operand's fragments inside a stage tile
@@ -160,20 +155,16 @@ struct FragAddr {
             }
         }
     }
-    // Reads fragment FI of slice S of the tile at LDS address `base`.
+    // Reads fragment FI of slice S of the tile at `base`.
     template <int S, int FI>
-    __device__ __forceinline__ void read(Frag<TR>& d, uint32_t base) const {
-        if constexpr (!TR) {
-            ds_b128<4096 * FI>(d.v, base + off[S]);
-        } else {
-            ds_tr<16 * S * 2 * R>(d.lo, base + off[FI]);
-            ds_tr<(16 * S + 4) * 2 * R>(d.hi, base + off[FI]);
-        }
+    __device__ __forceinline__ void read(Frag<TR>& d, const char NOTT_LDS* base) const {
+        if constexpr (!TR) d.ld(base + off[S] + 4096 * FI);
+        else d.ld(base + off[FI] + 16 * S * 2 * R, 4 * 2 * R);
     }
 };
 
 template <int S, bool TR, int R, int F, int I = 0>
-__device__ __forceinline__ void read_all(Frag<TR> (&d)[F], const FragAddr<TR, R, F>& a, uint32_t base) {
+__device__ __forceinline__ void read_all(Frag<TR> (&d)[F], const FragAddr<TR, R, F>& a, const char NOTT_LDS* base) {
     if constexpr (I < F) {
         a.template read<S, I>(d[I], base);
         read_all<S, TR, R, F, I + 1>(d, a, base);
@@ -194,8 +185,33 @@ __device__ __forceinline__ void tile_of(int id, int tm, int tn, int gm, int& pm,
     pn = in / gsz;
 }
 
+// Sum of the 8 bf16 values of an operand fragment, in k order.
+__device__ __forceinline__ void add_bf16x2(float& s, uint32_t w) {
+    s += __builtin_bit_cast(float, w << 16);
+    s += __builtin_bit_cast(float, w & 0xffff0000u);
+}
+__device__ __forceinline__ void add_frag(float& s, const Frag<false>& f) {
+    add_bf16x2(s, f.v.x);
+    add_bf16x2(s, f.v.y);
+    add_bf16x2(s, f.v.z);
+    add_bf16x2(s, f.v.w);
+}
+__device__ __forceinline__ void add_frag(float& s, const Frag<true>& f) {
+    const u32x4 w = __builtin_bit_cast(u32x4, f.get());
+    add_bf16x2(s, w.x);
+    add_bf16x2(s, w.y);
+    add_bf16x2(s, w.z);
+    add_bf16x2(s, w.w);
+}
+
 // grid: x = tiles (tm·tn), z = k splits of kps (a multiple of BK) each.
-template <bool AT, bool BT, int BM, int BN, int WM, int WN, int S, class EP>
+// ROWSUM: also Σ_k A(m, k) for every row m of the tile (the bias gradient
+// when A is the output gradient of a Linear), summed in fp32 from the A
+// fragments already in registers: only the tiles of tile column 0 sum, and
+// there fragment f's sum is kept by wave column f % WN, so each row is
+// summed once; the two k-halves of a row are held by lanes l and l+32 and
+// combined at the end; the epilogue receives it via ep.rowsum(m, v).
+template <bool AT, bool BT, int BM, int BN, int WM, int WN, int S, bool ROWSUM, class EP>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const bf16_t* __restrict__ A, int64_t lda,
                                                              const bf16_t* __restrict__ B, int64_t ldb, EP ep,
                                                              int64_t M, int64_t N, int64_t K, int64_t kps, int gm) {
@@ -204,10 +220,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const bf16_t* __rest
     constexpr int FM = TM / 32, FN = TN / 32;
     constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128, STAGE = A_BYTES + B_BYTES;
     constexpr int LOADS = (BM / 8 + BN / 8) / NW;   // global_load_lds per wave per stage
-    constexpr int RA = FM * Frag<AT>::kReads, RB = FN * Frag<BT>::kReads;   // LDS reads per slice
     static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tiles are whole 32x32 blocks");
     static_assert(S >= 2 && (S - 2) * LOADS < 64, "ring depth");
-    static_assert(RA + RB < 16, "lgkmcnt range");
     extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
     char NOTT_LDS* smem = (char NOTT_LDS*)smem_raw;
 
@@ -239,15 +253,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const bf16_t* __rest
     FragAddr<BT, BN, FN> fb;
     fa.init(wm * TM, lane);
     fb.init(wn * TN, lane);
-    const uint32_t lds0 = lds_addr(smem);
 
     Frag<AT> a[2][FM];
     Frag<BT> b[2][FN];
+    float rs[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) rs[i] = 0.f;
     auto mma = [&](int p) {
+        if constexpr (ROWSUM) {
+            if (pn == 0) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) a[p][i].tie();
-#pragma unroll
-        for (int j = 0; j < FN; ++j) b[p][j].tie();
+                for (int i = 0; i < FM; ++i)
+                    if (i % WN == wn) add_frag(rs[i], a[p][i]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -266,23 +285,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const bf16_t* __rest
         else wait_vm_lgkm0<0>();
         barrier();
         if (S - 1 < nk) issue(S - 1, S - 1);
-        read_all<0>(a[0], fa, lds0);
-        read_all<0>(b[0], fb, lds0 + A_BYTES);
+        read_all<0>(a[0], fa, smem);
+        read_all<0>(b[0], fb, smem + A_BYTES);
     }
     int slot = 0;   // ring slot of stage t
     for (int t = 0; t < nk; ++t) {
-        const uint32_t sa = lds0 + slot * STAGE, sb = sa + A_BYTES;
+        const char NOTT_LDS* sa = smem + slot * STAGE;
+        const char NOTT_LDS* sb = sa + A_BYTES;
         read_all<1>(a[1], fa, sa);
         read_all<1>(b[1], fb, sb);
-        wait_lgkm<RA + RB>();
         mma(0);
         read_all<2>(a[0], fa, sa);
         read_all<2>(b[0], fb, sb);
-        wait_lgkm<RA + RB>();
         mma(1);
         read_all<3>(a[1], fa, sa);
         read_all<3>(b[1], fb, sb);
-        wait_lgkm<RA + RB>();
         mma(0);
         const int nslot = slot + 1 == S ? 0 : slot + 1;
         if (t + 1 < nk) {
@@ -291,15 +308,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(const bf16_t* __rest
             else wait_vm_lgkm0<0>();
             barrier();
             if (t + S < nk) issue(t + S, slot);
-            const uint32_t na = lds0 + nslot * STAGE;
+            const char NOTT_LDS* na = smem + nslot * STAGE;
             read_all<0>(a[0], fa, na);
             read_all<0>(b[0], fb, na + A_BYTES);
-            wait_lgkm<RA + RB>();
-        } else {
-            wait_lgkm<0>();
         }
         mma(1);
         slot = nslot;
+    }
+    if constexpr (ROWSUM) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            if (pn != 0 || i % WN != wn) continue;
+            const float v = rs[i] + __shfl_xor(rs[i], 32);
+            if (lane < 32) ep.rowsum(m0 + wm * TM + 32 * i + lane, v);
+        }
     }
     // Accumulator layout of a 32×32 block: lane l holds column l % 32 and,
     // in register 4q + e, row 8q + 4·(l/32) + e.
@@ -375,10 +397,10 @@ inline size_t partial_floats(nott_ctx ctx, int64_t M, int64_t N, int64_t K) {
     return p.splits > 1 ? (size_t)(p.splits * M * N) : 0;
 }
 
-template <class Cfg, class EP>
+template <class Cfg, bool ROWSUM, class EP>
 int launch(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep, int64_t M,
            int64_t N, int64_t K, int64_t splits, int64_t kps) {
-    auto fn = gemm_kernel<Cfg::kAT, Cfg::kBT, Cfg::kBM, Cfg::kBN, Cfg::kWM, Cfg::kWN, Cfg::kS, EP>;
+    auto fn = gemm_kernel<Cfg::kAT, Cfg::kBT, Cfg::kBM, Cfg::kBN, Cfg::kWM, Cfg::kWN, Cfg::kS, ROWSUM, EP>;
     static bool attr = false;   // one setting per kernel instantiation
     if (!attr) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -392,36 +414,71 @@ int launch(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t 
     return launch_status(ctx, "gemm_dma");
 }
 
-template <bool AT, bool BT, class EP>
+template <bool AT, bool BT, bool ROWSUM, class EP>
 int launch_shape(nott_ctx ctx, Shape sh, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep,
                  int64_t M, int64_t N, int64_t K, int64_t splits, int64_t kps) {
     switch (sh) {
         case Shape::T256x128:
-            return launch<Config<AT, BT, 256, 128, 4, 2, 3>>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
+            return launch<Config<AT, BT, 256, 128, 4, 2, 3>, ROWSUM>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
         case Shape::T256x256:
-            return launch<Config<AT, BT, 256, 256, 2, 4, 2>>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
+            return launch<Config<AT, BT, 256, 256, 2, 4, 2>, ROWSUM>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
         default:
-            return launch<Config<AT, BT, 128, 128, 2, 2, 3>>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
+            return launch<Config<AT, BT, 128, 128, 2, 2, 3>, ROWSUM>(ctx, A, lda, B, ldb, ep, M, N, K, splits, kps);
     }
+}
+
+// Split-K partial store with per-split row sums: ws[split][m][n] and
+// rows[split][m].
+struct PartialRowStore {
+    float* ws;
+    float* rows;
+    int64_t M, N;
+    __device__ __forceinline__ void store(int64_t m, int64_t n, float v) const {
+        if (m < M && n < N) ws[((int64_t)blockIdx.z * M + m) * N + n] = v;
+    }
+    __device__ __forceinline__ void rowsum(int64_t m, float v) const {
+        if (m < M) rows[(int64_t)blockIdx.z * M + m] = v;
+    }
+};
+
+// ep.rowsum(m, Σ_z rows[z][m]) in split order.
+template <class EP>
+__global__ __launch_bounds__(256) void rowsum_reduce_kernel(const float* __restrict__ rows, int64_t splits, int64_t M,
+                                                            EP ep) {
+    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (m >= M) return;
+    float s = 0.f;
+    for (int64_t z = 0; z < splits; ++z) s += rows[z * M + m];
+    ep.rowsum(m, s);
 }
 
 // C = A·B, or NOTT_ERR_UNSUPPORTED when the operands do not qualify (the
 // caller then uses another engine).  Split-K partials go to `partial` when
 // given (partial_floats() of them), else to the workspace, and are summed in
-// split order by the reduce kernel, which applies the epilogue.
-template <bool AT, bool BT, class EP>
+// split order by the reduce kernel, which applies the epilogue.  ROWSUM also
+// hands ep.rowsum(m, Σ_k A(m, k)) for every row (see gemm_kernel).
+template <bool AT, bool BT, bool ROWSUM = false, class EP>
 int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb, const EP& ep, int64_t M, int64_t N,
         int64_t K, int64_t splits = 0, float* partial = nullptr) {
     if (M <= 0 || N <= 0) return NOTT_OK;
     if (!applies<AT, BT>(A, lda, B, ldb, M, N, K)) return NOTT_ERR_UNSUPPORTED;
     const Plan p = plan(ctx, M, N, K, splits);
-    if (p.splits == 1) return launch_shape<AT, BT>(ctx, p.shape, A, lda, B, ldb, ep, M, N, K, 1, p.kps);
-    float* ws = partial ? partial : static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(p.splits * M * N)));
+    if (p.splits == 1) return launch_shape<AT, BT, ROWSUM>(ctx, p.shape, A, lda, B, ldb, ep, M, N, K, 1, p.kps);
+    const size_t body = (size_t)(p.splits * M * N), rows = ROWSUM ? (size_t)(p.splits * M) : 0;
+    float* ws = partial && !ROWSUM ? partial : static_cast<float*>(workspace(ctx, sizeof(float) * (body + rows)));
     if (!ws) return NOTT_ERR_ALLOC;
-    const int st = launch_shape<AT, BT>(ctx, p.shape, A, lda, B, ldb, PartialStore{ws, M, N}, M, N, K, p.splits, p.kps);
+    int st;
+    if constexpr (ROWSUM)
+        st = launch_shape<AT, BT, true>(ctx, p.shape, A, lda, B, ldb, PartialRowStore{ws, ws + body, M, N}, M, N, K,
+                                        p.splits, p.kps);
+    else
+        st = launch_shape<AT, BT, false>(ctx, p.shape, A, lda, B, ldb, PartialStore{ws, M, N}, M, N, K, p.splits,
+                                         p.kps);
     if (st != NOTT_OK) return st;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream, ws,
-                       p.splits, M, N, ep);
+    launch_splitk_reduce(ctx, ws, p.splits, M, N, ep);
+    if constexpr (ROWSUM)
+        hipLaunchKernelGGL((rowsum_reduce_kernel<EP>), dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, ctx->stream,
+                           ws + body, p.splits, M, ep);
     return launch_status(ctx, "gemm_dma_splitk");
 }
 

@@ -68,6 +68,23 @@ struct DwDbStore {
     }
 };
 
+// dw[o][i] for i < kin (columns past kin are tile padding), db[o] from the
+// GEMM's row sums of dy.
+struct DwRowsumStore {
+    float* dw;
+    float* db;
+    int64_t nout, kin;
+    int accumulate;
+    __device__ __forceinline__ void store(int64_t o, int64_t i, float v) const {
+        if (o >= nout || i >= kin) return;
+        float* p = dw + o * kin + i;
+        *p = accumulate ? *p + v : v;
+    }
+    __device__ __forceinline__ void rowsum(int64_t o, float v) const {
+        if (o < nout) db[o] = accumulate ? db[o] + v : v;
+    }
+};
+
 // db[o] (+)= Σ_r dy[r·nout + o] in two deterministic phases: kColSumSlabs
 // row slabs each write a partial row (lane = column, 4 waves split the
 // slab's rows), then one pass adds the partials in slab order.
@@ -215,6 +232,17 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
                 if (st != NOTT_ERR_UNSUPPORTED) {
                     if (st != NOTT_OK) return st;
                     dx = nullptr;
+                }
+            }
+            if (dw && db) {
+                // db = Σ_rows dy summed from the dw GEMM's dy fragments.
+                DwRowsumStore ep{dw, db, nout, kin, accumulate};
+                const int st = dma::run<true, true, true>(ctx, dyp, nout, static_cast<const T*>(x), kin, ep, nout, kin,
+                                                          m);
+                if (st != NOTT_ERR_UNSUPPORTED) {
+                    if (st != NOTT_OK) return st;
+                    dw = nullptr;
+                    db = nullptr;
                 }
             }
             if (dw) {
