@@ -25,6 +25,7 @@
 // MFMA is stored in LDS transposed with its keys permuted the same way, so
 // it is still one 16-byte read per lane.
 #include "common.hpp"
+#include "lds_dma.hpp"
 
 #include <algorithm>
 
@@ -679,6 +680,437 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
     }
 }
 
+// ===========================================================================
+// bf16 backward for head dim 64 on 32×32×16 MFMAs.
+//
+// Two deterministic passes, each streaming 64-row tiles of the other side
+// through an LDS ring filled by direct-to-LDS loads:
+//   attn_dq64:   one workgroup per 128 query rows (4 waves × 32); forms
+//                D = rowsum(dO∘O) for its rows (written for the next pass),
+//                then per 64-key block: sᵀ = k·qᵀ, dpᵀ = v·dOᵀ, dsᵀ, and
+//                dq += ds·k.
+//   attn_dkdv64: one workgroup per 128 keys (4 waves × 32); per 64-query
+//                block: s = q·kᵀ, dp = dO·vᵀ, p, ds, dv += pᵀ·dO and
+//                dk += dsᵀ·q.
+// Each wave keeps its own 32 rows of the fixed side (q and dO, or k and v) as
+// MFMA B operands in registers for the whole pass.
+//
+// Precision.  p and ds enter the second-stage MFMAs as bf16.  Where a wave's
+// tile holds a probability of at least kLoTau (rows with few effective keys,
+// whose few large terms dominate their sums), the bf16 remainder
+// (x − bf16(x), rounded again) is multiplied as well, which carries ~16
+// mantissa bits; elsewhere a rounding error of 2^-9 relative on terms that
+// small stays far inside the bf16 tolerance.  D must be exact: D taken from
+// the bf16-rounded o is off by dO·δo, which shifts every ds of the row.  The
+// dq pass therefore uses D~ = rowsum(dO∘o_bf16) during its sweep, while it
+// accumulates the exact D = Σ_j p·dp and b = Σ_j p·k, and at the end sets
+// dq = scale·(Σ_j p(dp − D~)k − (D − D~)·b); the exact D is what it writes
+// for the dk/dv pass.  Score tiles are computed with
+// the fixed side as the B operand, so a lane's accumulator column is its own
+// row of the fixed side and its 16 registers are rows 8j + 4·(l/32) + e of
+// the streamed side; 8 consecutive registers are then exactly a 32×16 A
+// operand whose k-slots are streamed rows {4h..4h+3, 8+4h..8+4h+3} of a
+// 16-row slice, and the matching B operand is read from the streamed tile
+// with two transposing LDS reads (ds_read_b64_tr_b16, 4 rows each).
+// Tiles are [row][64] bf16 with 128-byte rows and 16-byte chunks swizzled by
+// (row>>1)&7, as in the direct-to-LDS GEMM.
+namespace a64 {
+
+using nott::lds::barrier;
+using nott::lds::dma16;
+using nott::lds::dma4;
+using nott::lds::lds_addr;
+using nott::lds::wait_vm_lgkm0;
+
+constexpr int NW = 4;                    // waves per workgroup, 32 fixed rows each
+constexpr int FIXED = 32 * NW;           // fixed rows per workgroup
+constexpr int TR = 64;                   // streamed rows per stage
+constexpr int TILE = TR * 128;           // one [64][64] bf16 tile
+constexpr int RING = 3;                  // stages in flight + 1
+constexpr float kLoTau = 1.f / 16;       // tile max of p above which the bf16 remainder is multiplied too
+
+__device__ __forceinline__ int toff64(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
+// Fills a [64][64] tile with rows row0.. of `base` (row stride ld, rows past
+// nrows clamped to the last one): 8 blocks of 1 KB, two per wave.
+__device__ __forceinline__ void fill_tile(const bf16_t* base, int row0, int nrows, int ld, char NOTT_LDS* tile,
+                                          int wid, int lane) {
+#pragma unroll
+    for (int qq = 0; qq < 8 / NW; ++qq) {
+        const int q = wid + NW * qq;
+        const int r = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        int gr = row0 + r;
+        gr = gr < nrows ? gr : nrows - 1;
+        dma16(base + (int64_t)gr * ld + 8 * c, lds_addr(tile) + 1024 * q);
+    }
+}
+
+// 32×16 operand of tile rows r0..r0+31, d slice s: lane l gets row r0 + l%32,
+// d = 16s + 8·(l/32) + 0..7.
+__device__ __forceinline__ bf16x8 frag_rows(const char NOTT_LDS* tile, int r0, int s, int lane) {
+    const int r = r0 + (lane & 31);
+    return __builtin_bit_cast(bf16x8,
+                              *reinterpret_cast<const u32x4 NOTT_LDS*>(tile + toff64(r, 2 * s + (lane >> 5))));
+}
+
+typedef short v4i16s __attribute__((ext_vector_type(4)));
+
+// B operand over a 16-row slice starting at tile row rs: lane l gets column
+// d0 + l%32 and rows rs + 4h + 0..3, rs + 8 + 4h + 0..3 (h = l/32).
+__device__ __forceinline__ bf16x8 frag_cols(const char NOTT_LDS* tile, int rs, int d0, int lane) {
+    const int j = lane & 15, g = lane >> 4;
+    const int col = d0 + 16 * (g & 1) + 4 * (j & 3);
+    const int r1 = rs + 4 * (g >> 1) + (j >> 2);
+    const int byte = (col & 7) * 2;
+    const v4i16s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16s NOTT_LDS*)(tile + toff64(r1, col >> 3) + byte));
+    const v4i16s hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16s NOTT_LDS*)(tile + toff64(r1 + 8, col >> 3) + byte));
+    const v4i16s w[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+// Registers base..base+7 of an accumulator tile as a bf16 A operand.
+__device__ __forceinline__ bf16x8 pack8(const f32x16& t, int base) {
+    const u32x4 w = {pack_bf16x2(t[base], t[base + 1]), pack_bf16x2(t[base + 2], t[base + 3]),
+                     pack_bf16x2(t[base + 4], t[base + 5]), pack_bf16x2(t[base + 6], t[base + 7])};
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+// The remainder x − bf16(x) of the same 8 registers, rounded to bf16.
+__device__ __forceinline__ bf16x8 pack8_lo(const f32x16& t, int base, const bf16x8& hi) {
+    const u32x4 h = __builtin_bit_cast(u32x4, hi);
+    auto lo2 = [&](int i, uint32_t w) {
+        return pack_bf16x2(t[base + i] - __builtin_bit_cast(float, w << 16),
+                           t[base + i + 1] - __builtin_bit_cast(float, w & 0xffff0000u));
+    };
+    const u32x4 w = {lo2(0, h.x), lo2(2, h.y), lo2(4, h.z), lo2(6, h.w)};
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+// Wave-wide maximum (uniform result).
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+    return x;
+}
+
+__device__ __forceinline__ f32x16 mfma(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// A row's 64 values as 4 B-operand slices: lane l holds d = 16s + 8·(l/32) + 0..7.
+__device__ __forceinline__ void load_fixed(const bf16_t* base, int row, int nrows, int ld, int lane, u32x4 (&r)[4]) {
+    const int rr = row < nrows ? row : nrows - 1;
+    const bf16_t* pr = base + (int64_t)rr * ld + 8 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) r[s] = *reinterpret_cast<const u32x4*>(pr + 16 * s);
+}
+
+__device__ __forceinline__ float dot_bf16x8(const u32x4& a, const u32x4& b) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s += __builtin_bit_cast(float, a[i] << 16) * __builtin_bit_cast(float, b[i] << 16);
+        s += __builtin_bit_cast(float, a[i] & 0xffff0000u) * __builtin_bit_cast(float, b[i] & 0xffff0000u);
+    }
+    return s;
+}
+
+__global__ __launch_bounds__(64 * NW, 2) void attn_dq64_kernel(const bf16_t* __restrict__ q,
+                                                                 const bf16_t* __restrict__ k,
+                                                                 const bf16_t* __restrict__ v,
+                                                                 const bf16_t* __restrict__ o,
+                                                                 const bf16_t* __restrict__ dO,
+                                                                 const float* __restrict__ lse,
+                                                                 float* __restrict__ dsum, bf16_t* __restrict__ dq,
+                                                                 AttnParams p) {
+    constexpr int STAGE = 2 * TILE;
+    extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+    char NOTT_LDS* smem = (char NOTT_LDS*)smem_raw;
+    const int bh = blockIdx.x;
+    const int nqb = (p.t + FIXED - 1) / FIXED;
+    const int q0 = (nqb - 1 - (int)blockIdx.y) * FIXED;   // heaviest (causal) blocks first
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int h = lane >> 5;
+    const int qw0 = q0 + 32 * wid;
+    const int my_q = qw0 + (lane & 31);
+    const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
+    const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
+    const float sl2 = p.scale * 1.4426950408889634f;
+
+    u32x4 qr[4], dr[4];
+    load_fixed(q + qoff, my_q, p.t, p.ldq, lane, qr);
+    load_fixed(dO + ooff, my_q, p.t, p.ldo, lane, dr);
+    float my_d;
+    {
+        u32x4 orr[4];
+        load_fixed(o + ooff, my_q, p.t, p.ldo, lane, orr);
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += dot_bf16x8(dr[i], orr[i]);
+        my_d = s + __shfl_xor(s, 32, 64);
+    }
+    const bool q_in = my_q < p.t;
+    const float my_lse2 = lse[(int64_t)bh * p.t + (q_in ? my_q : p.t - 1)] * 1.4426950408889634f;
+
+    int nk = p.nkb;   // 64-key blocks
+    if (p.causal) nk = min(nk, (q0 + FIXED - 1) / TR + 1);
+    auto issue = [&](int i, int slot) {
+        char NOTT_LDS* st = smem + slot * STAGE;
+        fill_tile(k + koff, i * TR, p.s, p.ldk, st, wid, lane);
+        fill_tile(v + koff, i * TR, p.s, p.ldk, st + TILE, wid, lane);
+    };
+#pragma unroll
+    for (int i = 0; i < RING - 1; ++i)
+        if (i < nk) issue(i, i);
+
+    f32x16 adq[2], abv[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) adq[f][e] = abv[f][e] = 0.f;
+    float d_exact = 0.f;   // Σ p·dp over this lane's keys (its half of the row)
+    int slot = 0, next = RING - 1;
+    for (int i = 0; i < nk; ++i) {
+        if (i + RING - 2 < nk) wait_vm_lgkm0<(RING - 2) * 2 * (8 / NW)>();
+        else wait_vm_lgkm0<0>();
+        barrier();
+        if (i + RING - 1 < nk) issue(i + RING - 1, next);
+        const char NOTT_LDS* tk = smem + slot * STAGE;
+        const char NOTT_LDS* tv = tk + TILE;
+        slot = slot + 1 == RING ? 0 : slot + 1;
+        next = next + 1 == RING ? 0 : next + 1;
+        const int k0 = i * TR;
+        if ((p.causal && k0 > qw0 + 31) || qw0 >= p.t) continue;   // every key of the block masked for this wave
+        f32x16 st[2], dpt[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) st[f][e] = dpt[f][e] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                st[f] = mfma(frag_rows(tk, 32 * f, s, lane), __builtin_bit_cast(bf16x8, qr[s]), st[f]);
+                dpt[f] = mfma(frag_rows(tv, 32 * f, s, lane), __builtin_bit_cast(bf16x8, dr[s]), dpt[f]);
+            }
+        }
+        const bool full = qw0 + 32 <= p.t && k0 + TR <= p.s && (!p.causal || k0 + TR - 1 <= qw0);
+        float pmax = 0.f;
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 32 * f + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = full || (q_in && key < p.s && !(p.causal && key > my_q));
+                const float pe = ok ? __builtin_amdgcn_exp2f(st[f][r] * sl2 - my_lse2) : 0.f;
+                d_exact += pe * dpt[f][r];
+                pmax = fmaxf(pmax, pe);
+                st[f][r] = pe;
+                dpt[f][r] = pe * (dpt[f][r] - my_d);
+            }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const bf16x8 a = pack8(dpt[s >> 1], 8 * (s & 1));
+            const bf16x8 pa = pack8(st[s >> 1], 8 * (s & 1));
+#pragma unroll
+            for (int df = 0; df < 2; ++df) {
+                const bf16x8 b = frag_cols(tk, 16 * s, 32 * df, lane);
+                adq[df] = mfma(a, b, adq[df]);
+                abv[df] = mfma(pa, b, abv[df]);
+            }
+        }
+        if (wave_max(pmax) >= kLoTau) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const bf16x8 al = pack8_lo(dpt[s >> 1], 8 * (s & 1), pack8(dpt[s >> 1], 8 * (s & 1)));
+#pragma unroll
+                for (int df = 0; df < 2; ++df) adq[df] = mfma(al, frag_cols(tk, 16 * s, 32 * df, lane), adq[df]);
+            }
+        }
+    }
+    // Exact D of this lane's row (lanes l and l^32 hold the two key halves);
+    // the dk/dv pass reads it.
+    d_exact += __shfl_xor(d_exact, 32, 64);
+    if (h == 0 && q_in) dsum[(int64_t)bh * p.t + my_q] = d_exact;
+    const float corr = d_exact - my_d;
+    // adq, abv: lane holds column d = 32·df + l%32, rows 8j + 4h + e of this
+    // wave's 32 (row r's correction lives in lane r's column).
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int rl = 8 * (r >> 2) + 4 * h + (r & 3);
+        const float c = __shfl(corr, rl, 64);
+        const int row = qw0 + rl;
+#pragma unroll
+        for (int df = 0; df < 2; ++df)
+            if (row < p.t)
+                dq[qoff + (int64_t)row * p.ldq + 32 * df + (lane & 31)] =
+                    f32_to_bf16((adq[df][r] - c * abv[df][r]) * p.scale);
+    }
+}
+
+__global__ __launch_bounds__(64 * NW, 2) void attn_dkdv64_kernel(const bf16_t* __restrict__ q,
+                                                                   const bf16_t* __restrict__ k,
+                                                                   const bf16_t* __restrict__ v,
+                                                                   const bf16_t* __restrict__ dO,
+                                                                   const float* __restrict__ lse,
+                                                                   const float* __restrict__ dsum,
+                                                                   bf16_t* __restrict__ dk, bf16_t* __restrict__ dv,
+                                                                   AttnParams p) {
+    constexpr int STAGE = 2 * TILE + 2 * TR * 4;   // q tile, dO tile, lse and D of its rows
+    extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+    char NOTT_LDS* smem = (char NOTT_LDS*)smem_raw;
+    const int bh = blockIdx.x;
+    const int k0 = (int)blockIdx.y * FIXED;   // causal: the longest (first) key blocks are dispatched first
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int h = lane >> 5;
+    const int kw0 = k0 + 32 * wid;
+    const int my_k = kw0 + (lane & 31);
+    const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
+    const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
+    const float sl2 = p.scale * 1.4426950408889634f;
+    const float* lse_bh = lse + (int64_t)bh * p.t;
+    const float* d_bh = dsum + (int64_t)bh * p.t;
+
+    u32x4 kr[4], vr[4];
+    load_fixed(k + koff, my_k, p.s, p.ldk, lane, kr);
+    load_fixed(v + koff, my_k, p.s, p.ldk, lane, vr);
+
+    const int qb0 = p.causal ? k0 / TR : 0;
+    const int nq = p.nqb - qb0;   // 64-query blocks
+    auto issue = [&](int i, int slot) {
+        char NOTT_LDS* st = smem + slot * STAGE;
+        const int q0 = (qb0 + i) * TR;
+        fill_tile(q + qoff, q0, p.t, p.ldq, st, wid, lane);
+        fill_tile(dO + ooff, q0, p.t, p.ldo, st + TILE, wid, lane);
+        if (wid < 2) {
+            const int row = q0 + lane < p.t ? q0 + lane : p.t - 1;
+            dma4((wid == 0 ? lse_bh : d_bh) + row, lds_addr(st + 2 * TILE) + 256 * wid);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < RING - 1; ++i)
+        if (i < nq) issue(i, i);
+
+    f32x16 adk[2], adv[2];
+#pragma unroll
+    for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) adk[f][e] = adv[f][e] = 0.f;
+    int slot = 0, next = RING - 1;
+    for (int i = 0; i < nq; ++i) {
+        // Waves 0 and 1 issue one more load per stage than 2 and 3; the count
+        // of the latter is a safe bound for both.
+        if (i + RING - 2 < nq) wait_vm_lgkm0<(RING - 2) * 2 * (8 / NW)>();
+        else wait_vm_lgkm0<0>();
+        barrier();
+        if (i + RING - 1 < nq) issue(i + RING - 1, next);
+        const char NOTT_LDS* tq = smem + slot * STAGE;
+        const char NOTT_LDS* tdo = tq + TILE;
+        const float NOTT_LDS* slse = reinterpret_cast<const float NOTT_LDS*>(tq + 2 * TILE);
+        const float NOTT_LDS* sd = slse + TR;
+        slot = slot + 1 == RING ? 0 : slot + 1;
+        next = next + 1 == RING ? 0 : next + 1;
+        const int q0 = (qb0 + i) * TR;
+        if ((p.causal && kw0 > q0 + TR - 1) || kw0 >= p.s) continue;   // every query of the block masked
+        f32x16 sc[2], dp[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) sc[f][e] = dp[f][e] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                sc[f] = mfma(frag_rows(tq, 32 * f, s, lane), __builtin_bit_cast(bf16x8, kr[s]), sc[f]);
+                dp[f] = mfma(frag_rows(tdo, 32 * f, s, lane), __builtin_bit_cast(bf16x8, vr[s]), dp[f]);
+            }
+        }
+        const bool full = q0 + TR <= p.t && kw0 + 32 <= p.s && (!p.causal || kw0 + 31 <= q0);
+        float pmax = 0.f;
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int ql = 32 * f + 8 * j + 4 * h;   // rows ql..ql+3 of the block
+                const f32x4 l4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(slse + ql);
+                const f32x4 d4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(sd + ql);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int qrow = q0 + ql + e;
+                    const bool ok = full || (qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow));
+                    const int r = 4 * j + e;
+                    const float pe = ok ? __builtin_amdgcn_exp2f(sc[f][r] * sl2 - l4[e] * 1.4426950408889634f) : 0.f;
+                    pmax = fmaxf(pmax, pe);
+                    sc[f][r] = pe;
+                    dp[f][r] = pe * (dp[f][r] - d4[e]);
+                }
+            }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const bf16x8 pa = pack8(sc[s >> 1], 8 * (s & 1));
+            const bf16x8 da = pack8(dp[s >> 1], 8 * (s & 1));
+#pragma unroll
+            for (int df = 0; df < 2; ++df) {
+                adv[df] = mfma(pa, frag_cols(tdo, 16 * s, 32 * df, lane), adv[df]);
+                adk[df] = mfma(da, frag_cols(tq, 16 * s, 32 * df, lane), adk[df]);
+            }
+        }
+        if (wave_max(pmax) >= kLoTau) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const bf16x8 pl = pack8_lo(sc[s >> 1], 8 * (s & 1), pack8(sc[s >> 1], 8 * (s & 1)));
+                const bf16x8 dl = pack8_lo(dp[s >> 1], 8 * (s & 1), pack8(dp[s >> 1], 8 * (s & 1)));
+#pragma unroll
+                for (int df = 0; df < 2; ++df) {
+                    adv[df] = mfma(pl, frag_cols(tdo, 16 * s, 32 * df, lane), adv[df]);
+                    adk[df] = mfma(dl, frag_cols(tq, 16 * s, 32 * df, lane), adk[df]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int df = 0; df < 2; ++df)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kw0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (key < p.s) {
+                const int64_t i = koff + (int64_t)key * p.ldk + 32 * df + (lane & 31);
+                dk[i] = f32_to_bf16(adk[df][r] * p.scale);
+                dv[i] = f32_to_bf16(adv[df][r]);
+            }
+        }
+}
+
+// Whether the head-dim-64 kernels take this problem: bf16, dh = 64, 16-byte
+// aligned rows (the fills move 16-byte chunks).
+bool applies(const nott_attn_desc* d, const AttnParams& p, int elem) { return elem == 2 && d->dh == 64 && p.vec; }
+
+int bwd(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
+        const void* o, const void* dO, const float* lse, void* dq, void* dk, void* dv) {
+    const int64_t rows = d->b * d->h * d->t;
+    float* dsum = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)std::max<int64_t>(rows, 1)));
+    if (!dsum) return NOTT_ERR_ALLOC;
+    const unsigned bh = (unsigned)(d->b * d->h);
+    const size_t lds_q = RING * 2 * TILE, lds_kv = RING * (2 * TILE + 2 * TR * 4);
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dq64_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_q);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dkdv64_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_kv);
+        attr = true;
+    }
+    const auto* qb = static_cast<const bf16_t*>(q);
+    const auto* kb = static_cast<const bf16_t*>(k);
+    const auto* vb = static_cast<const bf16_t*>(v);
+    const auto* dob = static_cast<const bf16_t*>(dO);
+    hipLaunchKernelGGL(attn_dq64_kernel, dim3(bh, (unsigned)ceil_div(d->t, FIXED)), dim3(64 * NW), lds_q, ctx->stream,
+                       qb, kb, vb, static_cast<const bf16_t*>(o), dob, lse, dsum, static_cast<bf16_t*>(dq), p);
+    hipLaunchKernelGGL(attn_dkdv64_kernel, dim3(bh, (unsigned)ceil_div(d->s, FIXED)), dim3(64 * NW), lds_kv,
+                       ctx->stream, qb, kb, vb, dob, lse, dsum, static_cast<bf16_t*>(dk), static_cast<bf16_t*>(dv), p);
+    return launch_status(ctx, "attention_bwd");
+}
+
+}  // namespace a64
+
 int check(nott_ctx ctx, const nott_attn_desc* d, AttnParams* p, int elem) {
     NOTT_REQUIRE(ctx, d != nullptr, "attention: null descriptor");
     NOTT_REQUIRE(ctx, d->b >= 0 && d->h >= 0 && d->t >= 0 && d->s >= 0 && d->dh > 0, "attention: bad shape");
@@ -859,8 +1291,9 @@ extern "C" int nott_attention_bwd(nott_ctx ctx, const nott_attn_desc* d, nott_dt
         return zero_view(ctx, d, p, elem, d->t, false, dq);
     }
     NOTT_REQUIRE(ctx, q && k && v && o && dO && lse && dq && dk && dv, "nott_attention_bwd: null buffer");
-    if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dO))) p.vec = 0;
+    if (!(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(dO) && aligned16(o))) p.vec = 0;
     nott::DeviceScope scope(ctx->device);
+    if (a64::applies(d, p, (int)nott::dtype_size(dtype))) return a64::bwd(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
     return dtype == NOTT_F32 ? bwd<float>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv)
                              : bwd<bf16_t>(ctx, d, p, q, k, v, o, dO, lse, dq, dk, dv);
 }

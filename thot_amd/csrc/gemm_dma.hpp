@@ -38,8 +38,7 @@
 #pragma once
 
 #include "gemm.hpp"
-
-#define NOTT_LDS __attribute__((address_space(3)))
+#include "lds_dma.hpp"
 
 namespace nott {
 namespace gemm {
@@ -47,34 +46,10 @@ namespace dma {
 
 constexpr int BK = 64;
 
-// s_waitcnt vmcnt(n) and lgkmcnt(0) (gfx9 encoding: vmcnt[3:0] and [15:14],
-// expcnt[6:4], lgkmcnt[11:8]).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0x0 << 8));
-}
-
-// Workgroup barrier without a memory fence: the ring's ordering comes from
-// the explicit waits; the empty asm statements keep the compiler from moving
-// memory accesses across the barrier.
-__device__ __forceinline__ void barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const char NOTT_LDS* p) { return (uint32_t)(uintptr_t)p; }
-
-// global_load_lds_dwordx4: 16 bytes per lane from `src` to LDS byte
-// lds + 16·lane (lds wave-uniform, through M0).  Issued as inline assembly
-// so that the compiler does not see an LDS DMA in flight: it would otherwise
-// make every later transposing LDS read wait for all outstanding loads
-// (vmcnt(0)), which serialises the ring.  The ring's own waits (vmcnt and
-// the barrier) order the DMA against the reads.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
-}
+using lds::barrier;
+using lds::dma16;
+using lds::lds_addr;
+using lds::wait_vm_lgkm0;
 
 // Issues this wave's share of one operand tile (R rows × 64 k) of stage k0.
 // Rows past `rows` are clamped to the last row (their results are never
