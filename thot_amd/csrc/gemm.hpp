@@ -288,12 +288,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // Vector form of splitk_reduce_kernel for N % 4 == 0: a thread owns 4
 // consecutive outputs of one row, loads them as one 16-byte word per split
 // (8 splits' loads in flight) and adds the splits in order 0, 1, 2, ...
-template <class EP>
+// With `rows` (per-split row sums rows[z][m], the bias gradient of a Linear),
+// the thread that owns column 0 of row m also hands ep.rowsum(m, Σ_z rows).
+template <class EP, bool ROWS>
 __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __restrict__ ws, int64_t splits, int64_t M,
-                                                             int64_t N, EP ep) {
+                                                             int64_t N, EP ep, const float* __restrict__ rows) {
     const int64_t MN = M * N;
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= MN) return;
+    if constexpr (ROWS) {
+        if (i % N == 0) {
+            const int64_t m = i / N;
+            float r = 0.f;
+            for (int64_t z = 0; z < splits; ++z) r += rows[z * M + m];
+            ep.rowsum(m, r);
+        }
+    }
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     int64_t z = 0;
     for (; z + 8 <= splits; z += 8) {
@@ -314,11 +324,20 @@ __global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float* __rest
 template <class EP>
 void launch_splitk_reduce(nott_ctx ctx, const float* ws, int64_t splits, int64_t M, int64_t N, const EP& ep) {
     if (N % 4 == 0 && ((uintptr_t)ws % 16) == 0)
-        hipLaunchKernelGGL((splitk_reduce4_kernel<EP>), dim3((unsigned)ceil_div(M * N, 1024)), dim3(256), 0,
-                           ctx->stream, ws, splits, M, N, ep);
+        hipLaunchKernelGGL((splitk_reduce4_kernel<EP, false>), dim3((unsigned)ceil_div(M * N, 1024)), dim3(256), 0,
+                           ctx->stream, ws, splits, M, N, ep, nullptr);
     else
         hipLaunchKernelGGL((splitk_reduce_kernel<EP>), dim3((unsigned)ceil_div(M * N, 64)), dim3(256), 0, ctx->stream,
                            ws, splits, M, N, ep);
+}
+
+// The same, also reducing per-split row sums rows[splits][M] into
+// ep.rowsum (N % 4 == 0 and a 16-byte aligned ws required).
+template <class EP>
+void launch_splitk_reduce(nott_ctx ctx, const float* ws, int64_t splits, int64_t M, int64_t N, const EP& ep,
+                          const float* rows) {
+    hipLaunchKernelGGL((splitk_reduce4_kernel<EP, true>), dim3((unsigned)ceil_div(M * N, 1024)), dim3(256), 0,
+                       ctx->stream, ws, splits, M, N, ep, rows);
 }
 
 // Picks a split count that gives the grid at least ~2 workgroups per CU

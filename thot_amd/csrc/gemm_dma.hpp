@@ -338,14 +338,17 @@ inline Plan plan(nott_ctx ctx, int64_t M, int64_t N, int64_t K, int64_t splits) 
     auto tiles = [&](int bm, int bn) { return ceil_div(M, bm) * ceil_div(N, bn); };
     Plan p{Shape::T128x128, 1, K};
     int64_t want = 1, min_stages = 4;
+    // Split counts keep the grid within one round of workgroups (one per CU:
+    // the 256x256 and 128x128 shapes hold 128 and 96 KB of LDS), so that a
+    // few leftover splits do not cost a second round.
     if (tiles(256, 128) >= cu) {
         p.shape = Shape::T256x128;
     } else if (tiles(256, 256) >= cu / 8 && nkb >= 16) {
         p.shape = Shape::T256x256;
-        want = ceil_div(cu, tiles(256, 256));
+        want = std::max<int64_t>(1, cu / tiles(256, 256));
         min_stages = 8;
     } else {
-        want = ceil_div(cu, tiles(128, 128));
+        want = std::max<int64_t>(1, cu / tiles(128, 128));
     }
     if (splits <= 0) splits = std::min<int64_t>(want, std::max<int64_t>(1, nkb / min_stages));
     splits = std::max<int64_t>(1, std::min<int64_t>(splits, std::min<int64_t>(nkb, 65535)));
@@ -416,16 +419,6 @@ struct PartialRowStore {
     }
 };
 
-// ep.rowsum(m, Σ_z rows[z][m]) in split order.
-template <class EP>
-__global__ __launch_bounds__(256) void rowsum_reduce_kernel(const float* __restrict__ rows, int64_t splits, int64_t M,
-                                                            EP ep) {
-    const int64_t m = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (m >= M) return;
-    float s = 0.f;
-    for (int64_t z = 0; z < splits; ++z) s += rows[z * M + m];
-    ep.rowsum(m, s);
-}
 
 // C = A·B, or NOTT_ERR_UNSUPPORTED when the operands do not qualify (the
 // caller then uses another engine).  Split-K partials go to `partial` when
@@ -437,6 +430,8 @@ int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
         int64_t K, int64_t splits = 0, float* partial = nullptr) {
     if (M <= 0 || N <= 0) return NOTT_OK;
     if (!applies<AT, BT>(A, lda, B, ldb, M, N, K)) return NOTT_ERR_UNSUPPORTED;
+    // The split reduce that also sums rows works on 4-column groups.
+    if (ROWSUM && N % 4 != 0) splits = 1;
     const Plan p = plan(ctx, M, N, K, splits);
     if (p.splits == 1) return launch_shape<AT, BT, ROWSUM>(ctx, p.shape, A, lda, B, ldb, ep, M, N, K, 1, p.kps);
     const size_t body = (size_t)(p.splits * M * N), rows = ROWSUM ? (size_t)(p.splits * M) : 0;
@@ -450,10 +445,8 @@ int run(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64_t ldb
         st = launch_shape<AT, BT, false>(ctx, p.shape, A, lda, B, ldb, PartialStore{ws, M, N}, M, N, K, p.splits,
                                          p.kps);
     if (st != NOTT_OK) return st;
-    launch_splitk_reduce(ctx, ws, p.splits, M, N, ep);
-    if constexpr (ROWSUM)
-        hipLaunchKernelGGL((rowsum_reduce_kernel<EP>), dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, ctx->stream,
-                           ws + body, p.splits, M, ep);
+    if constexpr (ROWSUM) launch_splitk_reduce(ctx, ws, p.splits, M, N, ep, ws + body);
+    else launch_splitk_reduce(ctx, ws, p.splits, M, N, ep);
     return launch_status(ctx, "gemm_dma_splitk");
 }
 
