@@ -21,14 +21,6 @@ namespace {
 
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kWaves = kThreads / 64;
-// Rows a wave loads before it reduces: as many as fit 32 (fp32) or 64 (bf16)
-// VGPRs of row data per lane, at most 8 (d = 1024: 1 row fp32, 2 rows bf16,
-// i.e. 8 KB of x and dy in flight per wave; measured best at two 4-wave
-// blocks per CU).
-__host__ __device__ constexpr int rows_in_flight(int elem_bytes, int dpl) {
-    const int r = (elem_bytes == 2 ? 64 : 32) / (2 * dpl);
-    return r < 1 ? 1 : (r > 8 ? 8 : r);
-}
 constexpr int kReduceThreads = 1024;   // column reduction: 16 waves split the partial rows
 constexpr int kReduceWaves = kReduceThreads / 64;
 constexpr int kReduceUnroll = 32;  // 16 waves x 32 loads cover 512 partial rows in one round
@@ -139,12 +131,16 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const T* __restrict__ 
     }
 }
 
-template <typename T, int DPL>
-__global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
-                                                          const float* __restrict__ mean, const float* __restrict__ rstd,
-                                                          const T* __restrict__ gamma, T* __restrict__ dx,
-                                                          float* __restrict__ partial, int64_t rows, int64_t d) {
-    extern __shared__ float lds[];  // [kWaves][2][d]
+// WAVES waves per block, one block per CU (measured best for configs[2]a:
+// 8 waves of one row each, ordinary loads and stores, with the next row's
+// loads in flight while the current row is reduced).
+template <typename T, int DPL, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void ln_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                            const float* __restrict__ mean,
+                                                            const float* __restrict__ rstd,
+                                                            const T* __restrict__ gamma, T* __restrict__ dx,
+                                                            float* __restrict__ partial, int64_t rows, int64_t d) {
+    extern __shared__ float lds[];  // [WAVES][2][d]
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     float gm[DPL];
     load_row<T, DPL, false>(gamma, d, lane, gm);
@@ -152,9 +148,9 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
 #pragma unroll
     for (int e = 0; e < DPL; ++e) dg[e] = db[e] = 0.f;
     const float inv_d = 1.f / (float)d;
-    constexpr int kRowsInFlight = rows_in_flight((int)sizeof(T), DPL);
+    constexpr int kRowsInFlight = 1;
     constexpr int NG = raw_groups<T>(DPL);
-    const int64_t stride = (int64_t)gridDim.x * kWaves * kRowsInFlight;
+    const int64_t stride = (int64_t)gridDim.x * WAVES * kRowsInFlight;
     // The next group of rows is loaded (raw) while the current one is
     // reduced and stored: two groups' loads per wave stay in flight.
     typename Pack16<T>::Raw rx[kRowsInFlight][NG], rd[kRowsInFlight][NG];
@@ -165,13 +161,13 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
             // Rows past the end re-read the last row (unconditional loads keep
             // every row's loads in flight together); they are not stored.
             const int64_t r = r0 + i < rows ? r0 + i : rows - 1;
-            load_raw<T, DPL, true>(x + r * d, d, lane, rx[i]);
-            load_raw<T, DPL, true>(dy + r * d, d, lane, rd[i]);
+            load_raw<T, DPL, false>(x + r * d, d, lane, rx[i]);
+            load_raw<T, DPL, false>(dy + r * d, d, lane, rd[i]);
             nmu[i] = mean[r];
             nrs[i] = rstd[r];
         }
     };
-    const int64_t first = ((int64_t)blockIdx.x * kWaves + wid) * kRowsInFlight;
+    const int64_t first = ((int64_t)blockIdx.x * WAVES + wid) * kRowsInFlight;
     if (first < rows) fetch(first);
     for (int64_t r0 = first; r0 < rows; r0 += stride) {
         float xv[kRowsInFlight][DPL], gv[kRowsInFlight][DPL];
@@ -205,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
             sgx = wave_sum(sgx) * inv_d;
 #pragma unroll
             for (int e = 0; e < DPL; ++e) xv[i][e] = rs[i] * (gv[i][e] - sg - xv[i][e] * sgx);
-            store_row<T, DPL, true>(dx + r * d, d, lane, xv[i]);
+            store_row<T, DPL, false>(dx + r * d, d, lane, xv[i]);
         }
     }
     // Combine the waves' column sums and write this block's partial row.
@@ -221,12 +217,12 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const T* __restrict__ 
     // Partial layout [which][16-column group][block][16]: the reduction reads
     // each group's partials as one contiguous run.
     const int64_t ngroups = (d + 15) / 16;
-    for (int64_t j = threadIdx.x; j < 2 * d; j += kThreads) {
+    for (int64_t j = threadIdx.x; j < 2 * d; j += 64 * WAVES) {
         const int which = j >= d;
         const int64_t col = j - which * d;
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) s += lds[(w * 2 + which) * d + col];
+        for (int w = 0; w < WAVES; ++w) s += lds[(w * 2 + which) * d + col];
         partial[((which * ngroups + col / 16) * gridDim.x + blockIdx.x) * 16 + col % 16] = s;
     }
 }
@@ -423,17 +419,32 @@ int fwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* gamma,
 constexpr size_t kScratchBytes = size_t(16) << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
+// Waves per block of the vector backward kernel: 8 while the block's LDS
+// column sums (waves × 2 × d floats) fit 64 KB, else 4.
+inline int bwd_waves(int64_t d) { return d <= 1024 ? 8 : 4; }
+
 // Partials need: 2 rows (dgamma, dbeta) of `pcols` columns per block.
 template <typename T>
 void partial_plan(nott_ctx ctx, int64_t rows, int64_t d, bool vec, int dpl, int64_t& nparts, size_t& pcols) {
+    (void)dpl;
     if (vec) {
-        nparts = std::min<int64_t>(nott::ceil_div(rows, kWaves * rows_in_flight((int)sizeof(T), dpl)),
-                                   (int64_t)ctx->num_cu * 2);
+        nparts = std::min<int64_t>(nott::ceil_div(rows, bwd_waves(d)), (int64_t)ctx->num_cu);
         nparts = std::max<int64_t>(nparts, 1);
     } else {
         nparts = rows;
     }
     pcols = vec ? (size_t)nott::ceil_div(d, 16) * 16 : (size_t)d;
+}
+
+template <typename T, int DPL>
+void launch_bwd_vec(nott_ctx ctx, dim3 grid, const T* x, const T* dy, const float* mean, const float* rstd,
+                    const T* gamma, T* dx, float* partial, int64_t rows, int64_t d) {
+    if (bwd_waves(d) == 8)
+        hipLaunchKernelGGL((ln_bwd_kernel<T, DPL, 8>), grid, dim3(512), sizeof(float) * 8 * 2 * (size_t)d, ctx->stream,
+                           x, dy, mean, rstd, gamma, dx, partial, rows, d);
+    else
+        hipLaunchKernelGGL((ln_bwd_kernel<T, DPL, 4>), grid, dim3(256), sizeof(float) * 4 * 2 * (size_t)d, ctx->stream,
+                           x, dy, mean, rstd, gamma, dx, partial, rows, d);
 }
 
 // `fixed` (nullable) replaces the context workspace for the partials;
@@ -465,15 +476,14 @@ int bwd(nott_ctx ctx, int64_t rows, int64_t d, const void* x, const void* dy, co
         if (!partial) return NOTT_ERR_ALLOC;
     }
     const dim3 grid((unsigned)nparts);
-    const size_t lds = sizeof(float) * kWaves * 2 * (size_t)d;
     if (dpl == 4)
-        hipLaunchKernelGGL((ln_bwd_kernel<T, 4>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+        launch_bwd_vec<T, 4>(ctx, grid, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else if (dpl == 8)
-        hipLaunchKernelGGL((ln_bwd_kernel<T, 8>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+        launch_bwd_vec<T, 8>(ctx, grid, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else if (dpl == 16)
-        hipLaunchKernelGGL((ln_bwd_kernel<T, 16>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+        launch_bwd_vec<T, 16>(ctx, grid, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else if (dpl == 32)
-        hipLaunchKernelGGL((ln_bwd_kernel<T, 32>), grid, dim3(kThreads), lds, ctx->stream, xx, dd, mean, rstd, gg, out, partial, rows, d);
+        launch_bwd_vec<T, 32>(ctx, grid, xx, dd, mean, rstd, gg, out, partial, rows, d);
     else
         hipLaunchKernelGGL(ln_bwd_generic<T>, grid, dim3(kThreads), 0, ctx->stream, xx, dd, mean, rstd, gg, out, partial, d);
     if ((dgamma || dbeta) && vec)

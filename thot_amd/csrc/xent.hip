@@ -269,6 +269,10 @@ void dispatch(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int6
         launch_rows<T, 64, 16, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (vec && c <= 256 * 32)
         launch_rows<T, 256, 32, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
+    else if (vec && sizeof(T) == 2 && c <= 512 * 64)
+        // bf16 rows of up to 32768: two 512-thread workgroups per CU, so that
+        // two rows (plus the two prefetched ones) are in flight per CU.
+        launch_rows<T, 512, 64, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (vec && c <= 1024 * 32)
         launch_rows<T, 1024, 32, true>(ctx, n, c, logits, labels, eps, scale, nvalid, dl, row_loss);
     else if (c <= 64 * 16)
