@@ -269,6 +269,29 @@ int nott_adam_step(nott_ctx ctx, int decoupled, int64_t n,
                    double lr, double beta1, double beta2, double eps, double weight_decay,
                    int64_t step, int zero_grad_after);
 
+/* The same update as nott_adam_step with its scalars taken from memory at
+ * launch time, so that the launch can be captured once into a HIP graph
+ * that is replayed every step (the reference's CUDA-graph step path,
+ * core.hpp:3829-3945, with the optimizer inside the graph).  Each launch
+ * first increments state->step (device memory, the per-tensor step count of
+ * torch::optim::Adam[W]; 0 before the first update) and forms the bias
+ * corrections from the new count, in the same double arithmetic as
+ * nott_adam_step, then runs the update.  hparams = {lr, beta1, beta2, eps,
+ * weight_decay} (5 doubles) is read by the device at launch time: device
+ * memory, or pinned host memory (hipHostMalloc) that the host rewrites
+ * between replays, e.g. after a scheduler writes a new lr
+ * (lrscheduler/details/cosineannealing.hpp:52-63).  Whether the weight
+ * decay term runs is fixed by weight_decay_nonzero at the call (libtorch
+ * skips it when weight_decay == 0). */
+typedef struct nott_adam_device_state {
+    int64_t step;
+    int64_t reserved[7];       /* the launch's scalar block; written by the library */
+} nott_adam_device_state;
+int nott_adam_step_graph(nott_ctx ctx, int decoupled, int64_t n,
+                         void* p, nott_dtype p_dtype, void* g, nott_dtype g_dtype,
+                         float* m, float* v, const double* hparams, nott_adam_device_state* state,
+                         int weight_decay_nonzero, int zero_grad_after);
+
 /* ---- utilities used by the host modules ---------------------------------- */
 /* dst = a + b elementwise (residual gradient fan-in, block/details/blocks/residual.hpp:131). */
 int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, void* dst);
@@ -280,6 +303,11 @@ int nott_zero(nott_ctx ctx, int64_t bytes, void* dst);
  * of a loss gradient with the upstream gradient of the scalar loss, which
  * libtorch's engine hands over as a device tensor. */
 int nott_scale(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* x, const float* scale, void* y);
+/* acc[0] += (double)loss[0] · weight, in double on the device: the epoch
+ * loss accumulation of Model::run_epochs (core.hpp:4481-4487: the step's
+ * detached loss in float64, times the batch size, added to a device
+ * accumulator), so a training loop needs no host read per step. */
+int nott_loss_accumulate(nott_ctx ctx, const float* loss, double weight, double* acc);
 
 #ifdef __cplusplus
 }

@@ -654,6 +654,8 @@ public:
         torch::NoGradGuard ng;
         num_batches_tracked.fill_(batches_);
     }
+    // After the buffer was loaded from a checkpoint: continue counting from it.
+    void reload_counter() { batches_ = num_batches_tracked.item<int64_t>(); }
     Tensor weight, bias, running_mean, running_var, num_batches_tracked;
 private:
     double eps_, momentum_;
@@ -858,6 +860,7 @@ public:
                 auto& st = static_cast<ParamState&>(*state_.at(p.unsafeGetTensorImpl()));
                 const int64_t t = st.step() + 1;
                 st.step(t);
+                device_steps_stale_ = true;
                 if (!segs.empty() && segs.back().end == off && segs.back().step == t) segs.back().end = off + len;
                 else segs.push_back({off, off + len, t});
             }
@@ -875,6 +878,100 @@ public:
     // The reference's warm-up hook (adam.hpp:98-150, called through
     // OptimizerBinding::warmup): the state already exists, nothing to do.
     void ensure_state_initialized() {}
+
+    // ---- Graph mode: the optimizer step inside a captured HIP graph
+    // (OptimizerBinding::capture_safe, core.hpp:170-181, 3829-3945).
+    // graph_prepare() runs before capture: each group gets a device state
+    // (nott_adam_device_state: its step count and the launch's scalar
+    // block) and a pinned block of hyper-parameters the device reads at
+    // launch time.  graph_step() is called while capturing and records one
+    // nott_adam_step_graph launch per group (and the bf16 refresh).  Before
+    // every replay graph_sync() writes the groups' current options (a
+    // scheduler's set_lr included) into the pinned blocks and, if an eager
+    // step() ran since, the host step count into the device state; after
+    // it, graph_after_replay() advances the per-parameter step counts the
+    // device advanced.  Every parameter of a group must have a gradient and
+    // the group's step counts must be equal at capture.
+    void graph_prepare() {
+        if (!P_.defined()) return;
+        torch::NoGradGuard ng;
+        const int64_t ng_ = (int64_t)param_groups_.size();
+        dev_state_ = torch::zeros({ng_, 8}, P_.options().dtype(torch::kInt64));
+        hparams_ = torch::empty({ng_, 5}, torch::TensorOptions().dtype(torch::kFloat64)).pin_memory();
+        ranges_.assign(param_groups_.size(), {0, 0});
+        wd_nonzero_.assign(param_groups_.size(), 0);
+        for (size_t gi = 0; gi < param_groups_.size(); ++gi) {
+            int64_t lo = -1, hi = -1, t = -1;
+            for (auto& p : param_groups_[gi].params()) {
+                auto it = offsets_.find(p.unsafeGetTensorImpl());
+                if (it == offsets_.end()) continue;
+                if (!p.grad().defined() || p.grad().data_ptr() != (void*)(G_.data_ptr<float>() + it->second))
+                    throw std::logic_error("FusedAdam graph mode: every parameter needs its arena gradient");
+                const int64_t st = static_cast<ParamState&>(*state_.at(p.unsafeGetTensorImpl())).step();
+                if (t >= 0 && st != t) throw std::logic_error("FusedAdam graph mode: unequal step counts in a group");
+                t = st;
+                const int64_t off = it->second, end = off + (p.numel() + 63) / 64 * 64;
+                lo = lo < 0 ? off : std::min(lo, off);
+                hi = std::max(hi, end);
+            }
+            if (lo >= 0) ranges_[gi] = {lo, hi};
+            const auto& o = static_cast<const TorchOptions&>(param_groups_[gi].options());
+            wd_nonzero_[gi] = o.weight_decay() != 0.0;
+        }
+        device_steps_stale_ = true;
+        graph_sync();
+    }
+    void graph_step() {
+        if (!P_.defined()) return;
+        nott_ctx c = bind(P_);
+        auto* st = reinterpret_cast<nott_adam_device_state*>(dev_state_.data_ptr<int64_t>());
+        const double* hp = hparams_.data_ptr<double>();
+        for (size_t gi = 0; gi < ranges_.size(); ++gi) {
+            const int64_t lo = ranges_[gi].first, hi = ranges_[gi].second;
+            if (hi <= lo) continue;
+            check(nott_adam_step_graph(c, Decoupled ? 1 : 0, hi - lo, P_.data_ptr<float>() + lo, NOTT_F32,
+                                       G_.data_ptr<float>() + lo, NOTT_F32, M_.data_ptr<float>() + lo,
+                                       V_.data_ptr<float>() + lo, hp + 5 * gi, st + gi, wd_nonzero_[gi],
+                                       fuse_zero_ ? 1 : 0),
+                  c, "adam step (graph)");
+        }
+        if (Pb_.defined()) refresh();
+    }
+    void graph_sync() {
+        if (!hparams_.defined()) return;
+        double* hp = hparams_.data_ptr<double>();
+        for (size_t gi = 0; gi < param_groups_.size(); ++gi) {
+            const auto& o = static_cast<const TorchOptions&>(param_groups_[gi].options());
+            if ((o.weight_decay() != 0.0) != (wd_nonzero_[gi] != 0))
+                throw std::logic_error("FusedAdam graph mode: weight decay switched on or off after capture");
+            hp[5 * gi + 0] = o.lr();
+            hp[5 * gi + 1] = std::get<0>(o.betas());
+            hp[5 * gi + 2] = std::get<1>(o.betas());
+            hp[5 * gi + 3] = o.eps();
+            hp[5 * gi + 4] = o.weight_decay();
+        }
+        if (device_steps_stale_) {
+            Tensor host = torch::zeros({(int64_t)param_groups_.size(), 8}, torch::kInt64);
+            for (size_t gi = 0; gi < param_groups_.size(); ++gi)
+                for (auto& p : param_groups_[gi].params()) {
+                    auto it = state_.find(p.unsafeGetTensorImpl());
+                    if (it != state_.end()) host[gi][0] = static_cast<ParamState&>(*it->second).step();
+                }
+            dev_state_.copy_(host);
+            device_steps_stale_ = false;
+        }
+    }
+    void graph_after_replay() {
+        for (size_t gi = 0; gi < ranges_.size(); ++gi) {
+            if (ranges_[gi].second <= ranges_[gi].first) continue;
+            for (auto& p : param_groups_[gi].params()) {
+                auto it = state_.find(p.unsafeGetTensorImpl());
+                if (it == state_.end()) continue;
+                auto& st = static_cast<ParamState&>(*it->second);
+                st.step(st.step() + 1);
+            }
+        }
+    }
 
     void set_fused_zero_grad(bool on) { fuse_zero_ = on; }
 
@@ -978,6 +1075,11 @@ private:
     }
 
     size_t group_count_ = 0;
+    // graph mode: per-group device state, pinned hyper-parameters, arena ranges
+    Tensor dev_state_, hparams_;
+    std::vector<std::pair<int64_t, int64_t>> ranges_;
+    std::vector<int> wd_nonzero_;
+    bool device_steps_stale_ = true;
     std::vector<const c10::TensorImpl*> registered_;
     std::unordered_map<const c10::TensorImpl*, int64_t> offsets_;
     Tensor P_, G_, M_, V_, Pb_;

@@ -806,6 +806,35 @@ int ref_resnet18_forward_archive(const char* path, int64_t batch, const float* x
     });
 }
 
+// Writes parameters.binary (torch::nn::Module::save, the archive
+// Model::save stores, core.hpp:2131-2135) of the reference's configs[0]
+// (model 0) or configs[4] (model 1) model: weights as its layer factories
+// initialise them from torch's CPU generator seeded with `seed`, then one
+// training-mode forward on uniform inputs so that the BatchNorm running
+// statistics and batch counters are not at their initial values.
+int ref_save_archive(int model, uint64_t seed, int64_t batch, const char* path) {
+    return guarded([&] {
+        torch::manual_seed(seed);
+        torch::serialize::OutputArchive ar;
+        if (model == 0) {
+            SmallCnnRef net;
+            torch::NoGradGuard ng;
+            net.c.owner.train();
+            (void)net.forward(torch::rand({batch, 1, 28, 28}));
+            net.c.owner.save(ar);
+        } else if (model == 1) {
+            ResNet18Ref net;
+            torch::NoGradGuard ng;
+            net.owner.train();
+            (void)net.forward(torch::rand({batch, 3, 224, 224}));
+            net.owner.save(ar);
+        } else {
+            throw std::invalid_argument("model must be 0 (small CNN) or 1 (ResNet-18)");
+        }
+        ar.save_to(std::string(path));
+    });
+}
+
 // Times `iters` full fp32 training steps on the CPU (forward, CE mean,
 // backward, Adam (model 0, configs[0]) or AdamW (model 1, configs[4]) step,
 // zero_grad) at the given batch; seconds per step in *sec.  Inputs

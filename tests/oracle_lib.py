@@ -396,6 +396,13 @@ class Ref:
                                                        _p(logits)))
         return logits
 
+    def save_archive(self, model: str, seed: int, batch: int, path: str):
+        """parameters.binary of the reference's "small_cnn" or
+        "resnet18" model, seeded weights and BatchNorm statistics
+        after one training-mode forward at `batch`."""
+        which = {"small_cnn": 0, "resnet18": 1}[model]
+        self._ok(self.lib.ref_save_archive(C.c_int(which), C.c_uint64(seed), i64(batch), C.c_char_p(path.encode())))
+
     def train_step_time(self, model: str, batch: int, iters: int) -> float:
         """Seconds per fp32 CPU training step of "small_cnn" or
         "resnet18" built from the reference's layer descriptors."""

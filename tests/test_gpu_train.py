@@ -399,3 +399,102 @@ def test_checkpoint_loads_into_reference(host_mod, oracle, tmp_path):
     got = tr.forward(x).float().cpu().numpy()
     want = Ref().small_cnn_forward_archive(path, x.cpu().numpy())
     check(got, want, "f32", "logits after checkpoint round trip")
+
+
+def test_graph_optimizer_follows_scheduler(host_mod):
+    """The optimizer step inside the captured graph reads its learning rate
+    at replay time: a scheduler-style set_lr between replays (cosine-like
+    sequence) gives the same parameters, bit for bit, as the eager twin that
+    steps through torch::optim::Optimizer::step with the same writes; the
+    per-parameter step counts advance with the replays."""
+    eager = host_mod.SmallCNNTrainer(0, 41, 1e-3)
+    graphed = host_mod.SmallCNNTrainer(0, 41, 1e-3)
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    batches = [(torch.rand((32, 1, 28, 28), generator=gen, device="cuda"),
+                torch.randint(0, 10, (32,), generator=gen, device="cuda")) for _ in range(5)]
+    graphed.capture(*batches[0], 1)
+    lrs = [1e-3, 8e-4, 5e-4, 2e-4, 5e-5]
+    for (x, y), lr in zip(batches, lrs):
+        eager.set_lr(lr)
+        graphed.set_lr(lr)
+        le = eager.step(x, y)
+        lg = graphed.step_graph(x, y)
+        torch.cuda.synchronize()
+        assert torch.equal(le, lg), (lr, le.item(), lg.item())
+    pe, pg = eager.params(), graphed.params()
+    for k in pe:
+        assert torch.equal(pe[k], pg[k]), k
+    # an eager step after the replays continues the same step count
+    x, y = batches[0]
+    eager.step(x, y)
+    graphed.step(x, y)
+    lg = graphed.step_graph(x, y)
+    le = eager.step(x, y)
+    torch.cuda.synchronize()
+    assert torch.equal(le, lg)
+    pe, pg = eager.params(), graphed.params()
+    for k in pe:
+        assert torch.equal(pe[k], pg[k]), k
+
+
+@pytest.mark.parametrize("model", ["small_cnn", "resnet18_bf16"])
+def test_train_epoch_prefetch_matches_steps(host_mod, model):
+    """One epoch from pinned host memory (batch i+1 copied on a copy stream
+    while step i replays; the loss summed on the device in float64 as
+    Model::run_epochs accumulates it) against eager steps over the same
+    batches: the same parameters bit for bit and the same mean loss."""
+    def make():
+        if model == "small_cnn":
+            return host_mod.SmallCNNTrainer(0, 17, 1e-3)
+        return host_mod.ResNet18Trainer(0, 17, True, 1e-3, 1e-2, 1000)
+    eager, graphed = make(), make()
+    b, nb = (32, 6) if model == "small_cnn" else (4, 3)
+    shape, classes = ((1, 28, 28), 10) if model == "small_cnn" else ((3, 224, 224), 1000)
+    g = torch.Generator().manual_seed(23)
+    xs = torch.rand((b * nb, *shape), generator=g).pin_memory()
+    ys = torch.randint(0, classes, (b * nb,), generator=g).pin_memory()
+    graphed.capture(xs[:b].cuda(), ys[:b].cuda(), 1)
+    mean = graphed.train_epoch(xs, ys)
+    total = 0.0
+    for i in range(nb):
+        loss = eager.step(xs[i * b:(i + 1) * b].cuda(), ys[i * b:(i + 1) * b].cuda())
+        total += float(loss.item()) * b
+    torch.cuda.synchronize()
+    assert mean == total / (b * nb), (mean, total / (b * nb))
+    pe, pg = eager.params(), graphed.params()
+    for k in pe:
+        assert torch.equal(pe[k], pg[k]), k
+
+
+@pytest.mark.parametrize("model", ["small_cnn", "resnet18"])
+def test_reference_checkpoint_loads_into_hip_model(host_mod, tmp_path, model):
+    """parameters.binary written by the reference's own model (its layer
+    factories' initialisation, BatchNorm statistics after a training-mode
+    forward) loads into the HIP model by registration key (Model::load,
+    core.hpp:2140-2244): the HIP forward (fp32, training mode) matches the
+    reference's forward on the same archive, and the BatchNorm buffers and
+    batch counters come through unchanged."""
+    from oracle_lib import Ref
+    if not Ref.available():
+        pytest.skip("oracle/_ref not built")
+    ref = Ref()
+    path = str(tmp_path / "parameters.binary")
+    ref.save_archive(model, 99, 4, path)
+    if model == "small_cnn":
+        tr = host_mod.SmallCNNTrainer(0, 1, 1e-3)
+        x = f32(rng(8).uniform(0, 1, (4, 1, 28, 28)))
+        want = ref.small_cnn_forward_archive(path, x)
+    else:
+        tr = host_mod.ResNet18Trainer(0, 1, False, 1e-3, 1e-2, 1000)
+        x = f32(rng(8).uniform(0, 1, (4, 3, 224, 224)))
+        want = ref.resnet18_forward_archive(path, x)
+    tr.load_archive(path)
+    if model == "resnet18":
+        # Read before the forward: a training-mode forward counts one more batch.
+        bufs = tr.buffers()
+        assert int(bufs["batchnorm2d_1.num_batches_tracked"]) == 1
+        assert float(bufs["batchnorm2d_1.running_var"].float().std()) > 0
+    got = host(tr.forward(torch.from_numpy(x).cuda()))
+    check(got, want, "f32", f"{model} logits from a reference checkpoint")
+    if model == "resnet18":
+        assert int(tr.buffers()["batchnorm2d_1.num_batches_tracked"]) == 2

@@ -84,6 +84,8 @@ SIGNATURES: dict[str, list] = {
     "nott_attention_fwd": [vp, C.POINTER(AttnDesc), i32, vp, vp, vp, vp, fp],
     "nott_attention_bwd": [vp, C.POINTER(AttnDesc), i32, vp, vp, vp, vp, vp, fp, vp, vp, vp],
     "nott_adam_step": [vp, i32, i64, vp, i32, vp, i32, fp, fp, f64, f64, f64, f64, f64, i64, i32],
+    "nott_adam_step_graph": [vp, i32, i64, vp, i32, vp, i32, fp, fp, vp, vp, i32, i32],
+    "nott_loss_accumulate": [vp, fp, f64, vp],
     "nott_add": [vp, i32, i64, vp, vp, vp],
     "nott_cast": [vp, i64, vp, i32, vp, i32],
     "nott_zero": [vp, i64, vp],

@@ -79,7 +79,9 @@ template <> struct Stream4<bf16_t> {
 template <typename TP, typename TG, int MODE, bool ZERO>
 __global__ __launch_bounds__(kThreads) void adam_vec_kernel(TP* __restrict__ p, TG* __restrict__ g,
                                                             float* __restrict__ m, float* __restrict__ v,
-                                                            int64_t nvec, AdamScalars s) {
+                                                            int64_t nvec, AdamScalars s,
+                                                            const AdamScalars* __restrict__ sdev) {
+    if (sdev) s = *sdev;
     const int64_t base = ((int64_t)blockIdx.x * kThreads * kUnroll) + threadIdx.x;
     f32x4 pv[kUnroll], gv[kUnroll], mv[kUnroll], vv[kUnroll];
 #pragma unroll
@@ -116,7 +118,9 @@ __global__ __launch_bounds__(kThreads) void adam_vec_kernel(TP* __restrict__ p, 
 template <typename TP, typename TG, int MODE, bool ZERO>
 __global__ __launch_bounds__(kThreads) void adam_scalar_kernel(TP* __restrict__ p, TG* __restrict__ g,
                                                                float* __restrict__ m, float* __restrict__ v,
-                                                               int64_t begin, int64_t n, AdamScalars s) {
+                                                               int64_t begin, int64_t n, AdamScalars s,
+                                                               const AdamScalars* __restrict__ sdev) {
+    if (sdev) s = *sdev;
     const int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     float pe = Io<TP>::ld(p, i), me = m[i], ve = v[i];
@@ -128,7 +132,8 @@ __global__ __launch_bounds__(kThreads) void adam_scalar_kernel(TP* __restrict__ 
 }
 
 template <typename TP, typename TG, int MODE, bool ZERO>
-int launch(nott_ctx ctx, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s) {
+int launch(nott_ctx ctx, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s,
+           const AdamScalars* sdev) {
     TP* pp = static_cast<TP*>(p);
     TG* gg = static_cast<TG*>(g);
     const bool aligned = (((uintptr_t)p % (4 * sizeof(TP))) == 0) && (((uintptr_t)g % (4 * sizeof(TG))) == 0) &&
@@ -139,29 +144,69 @@ int launch(nott_ctx ctx, int64_t n, void* p, void* g, float* m, float* v, const 
         if (nvec > 0) {
             const int64_t blocks = nott::ceil_div(nvec, (int64_t)kThreads * kUnroll);
             hipLaunchKernelGGL((adam_vec_kernel<TP, TG, MODE, ZERO>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                               ctx->stream, pp, gg, m, v, nvec, s);
+                               ctx->stream, pp, gg, m, v, nvec, s, sdev);
         }
         done = nvec * 4;
     }
     if (done < n) {
         const int64_t blocks = nott::ceil_div(n - done, (int64_t)kThreads);
         hipLaunchKernelGGL((adam_scalar_kernel<TP, TG, MODE, ZERO>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                           ctx->stream, pp, gg, m, v, done, n, s);
+                           ctx->stream, pp, gg, m, v, done, n, s, sdev);
     }
     return nott::launch_status(ctx, "adam_kernel");
 }
 
 template <typename TP, typename TG, int MODE>
-int dispatch_zero(nott_ctx ctx, int zero, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s) {
-    return zero ? launch<TP, TG, MODE, true>(ctx, n, p, g, m, v, s) : launch<TP, TG, MODE, false>(ctx, n, p, g, m, v, s);
+int dispatch_zero(nott_ctx ctx, int zero, int64_t n, void* p, void* g, float* m, float* v, const AdamScalars& s,
+                  const AdamScalars* sdev) {
+    return zero ? launch<TP, TG, MODE, true>(ctx, n, p, g, m, v, s, sdev)
+                : launch<TP, TG, MODE, false>(ctx, n, p, g, m, v, s, sdev);
 }
 
 template <typename TP, typename TG>
 int dispatch_flags(nott_ctx ctx, int mode, int zero, int64_t n, void* p, void* g, float* m, float* v,
-                   const AdamScalars& s) {
-    if (mode == 2) return dispatch_zero<TP, TG, 2>(ctx, zero, n, p, g, m, v, s);
-    if (mode == 1) return dispatch_zero<TP, TG, 1>(ctx, zero, n, p, g, m, v, s);
-    return dispatch_zero<TP, TG, 0>(ctx, zero, n, p, g, m, v, s);
+                   const AdamScalars& s, const AdamScalars* sdev = nullptr) {
+    if (mode == 2) return dispatch_zero<TP, TG, 2>(ctx, zero, n, p, g, m, v, s, sdev);
+    if (mode == 1) return dispatch_zero<TP, TG, 1>(ctx, zero, n, p, g, m, v, s, sdev);
+    return dispatch_zero<TP, TG, 0>(ctx, zero, n, p, g, m, v, s, sdev);
+}
+
+int dispatch_types(nott_ctx ctx, int mode, int zero, int64_t n, void* p, nott_dtype p_dtype, void* g,
+                   nott_dtype g_dtype, float* m, float* v, const AdamScalars& s, const AdamScalars* sdev) {
+    if (p_dtype == NOTT_F32 && g_dtype == NOTT_F32) return dispatch_flags<float, float>(ctx, mode, zero, n, p, g, m, v, s, sdev);
+    if (p_dtype == NOTT_BF16 && g_dtype == NOTT_BF16) return dispatch_flags<bf16_t, bf16_t>(ctx, mode, zero, n, p, g, m, v, s, sdev);
+    if (p_dtype == NOTT_F32 && g_dtype == NOTT_BF16) return dispatch_flags<float, bf16_t>(ctx, mode, zero, n, p, g, m, v, s, sdev);
+    return dispatch_flags<bf16_t, float>(ctx, mode, zero, n, p, g, m, v, s, sdev);
+}
+
+// The host's scalar set, written once for the device form: the same double
+// arithmetic as nott_adam_step, rounded to float at the same places.
+__host__ __device__ inline AdamScalars make_scalars(double lr, double beta1, double beta2, double eps, double wd,
+                                                    int64_t step) {
+    const double bc1 = 1.0 - pow(beta1, (double)step);
+    const double bc2 = 1.0 - pow(beta2, (double)step);
+    AdamScalars s;
+    s.beta1 = (float)beta1;
+    s.beta2 = (float)beta2;
+    s.one_m_b1 = (float)(1.0 - beta1);
+    s.one_m_b2 = (float)(1.0 - beta2);
+    s.wd = (float)wd;
+    s.decay = (float)(1.0 - lr * wd);
+    s.neg_step = (float)(-(lr / bc1));
+    s.bc2_sqrt = (float)sqrt(bc2);
+    s.eps = (float)eps;
+    return s;
+}
+
+// Device form of the host's scalar set: advances the step count held in
+// device memory and forms the bias corrections from it and from the
+// hyper-parameters {lr, beta1, beta2, eps, weight_decay} read at launch time.
+__global__ void adam_prep_kernel(const double* __restrict__ hp, nott_adam_device_state* __restrict__ st) {
+    const int64_t t = st->step + 1;
+    st->step = t;
+    const AdamScalars s = make_scalars(hp[0], hp[1], hp[2], hp[3], hp[4], t);
+    static_assert(sizeof(AdamScalars) <= sizeof(st->reserved), "scalar block size");
+    *reinterpret_cast<AdamScalars*>(st->reserved) = s;
 }
 
 }  // namespace
@@ -179,23 +224,25 @@ extern "C" int nott_adam_step(nott_ctx ctx, int decoupled, int64_t n, void* p, n
     NOTT_REQUIRE(ctx, p && g && m && v, "nott_adam_step: null buffer");
     nott::DeviceScope scope(ctx->device);
 
-    const double bc1 = 1.0 - std::pow(beta1, (double)step);
-    const double bc2 = 1.0 - std::pow(beta2, (double)step);
-    AdamScalars s;
-    s.beta1 = (float)beta1;
-    s.beta2 = (float)beta2;
-    s.one_m_b1 = (float)(1.0 - beta1);
-    s.one_m_b2 = (float)(1.0 - beta2);
-    s.wd = (float)weight_decay;
-    s.decay = (float)(1.0 - lr * weight_decay);
-    s.neg_step = (float)(-(lr / bc1));
-    s.bc2_sqrt = (float)std::sqrt(bc2);
-    s.eps = (float)eps;
+    const AdamScalars s = make_scalars(lr, beta1, beta2, eps, weight_decay, step);
     // libtorch skips the weight-decay term entirely when wd == 0.
     const int mode = weight_decay == 0.0 ? 0 : (decoupled ? 2 : 1);
 
-    if (p_dtype == NOTT_F32 && g_dtype == NOTT_F32) return dispatch_flags<float, float>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
-    if (p_dtype == NOTT_BF16 && g_dtype == NOTT_BF16) return dispatch_flags<bf16_t, bf16_t>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
-    if (p_dtype == NOTT_F32 && g_dtype == NOTT_BF16) return dispatch_flags<float, bf16_t>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
-    return dispatch_flags<bf16_t, float>(ctx, mode, zero_grad_after, n, p, g, m, v, s);
+    return dispatch_types(ctx, mode, zero_grad_after, n, p, p_dtype, g, g_dtype, m, v, s, nullptr);
+}
+
+extern "C" int nott_adam_step_graph(nott_ctx ctx, int decoupled, int64_t n, void* p, nott_dtype p_dtype, void* g,
+                                    nott_dtype g_dtype, float* m, float* v, const double* hparams,
+                                    nott_adam_device_state* state, int weight_decay_nonzero, int zero_grad_after) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, n >= 0, "nott_adam_step_graph: n must be >= 0");
+    NOTT_REQUIRE(ctx, nott::valid_dtype(p_dtype) && nott::valid_dtype(g_dtype), "nott_adam_step_graph: bad dtype");
+    NOTT_REQUIRE(ctx, hparams && state, "nott_adam_step_graph: null hyper-parameters or state");
+    if (n == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, p && g && m && v, "nott_adam_step_graph: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    hipLaunchKernelGGL(adam_prep_kernel, dim3(1), dim3(1), 0, ctx->stream, hparams, state);
+    const int mode = !weight_decay_nonzero ? 0 : (decoupled ? 2 : 1);
+    const auto* sdev = reinterpret_cast<const AdamScalars*>(state->reserved);
+    return dispatch_types(ctx, mode, zero_grad_after, n, p, p_dtype, g, g_dtype, m, v, AdamScalars{}, sdev);
 }

@@ -256,3 +256,17 @@ int nott_avgpool_global_bwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t 
 }
 
 }  // extern "C"
+
+namespace {
+__global__ void loss_accumulate_kernel(const float* __restrict__ loss, double weight, double* __restrict__ acc) {
+    acc[0] += (double)loss[0] * weight;
+}
+}  // namespace
+
+extern "C" int nott_loss_accumulate(nott_ctx ctx, const float* loss, double weight, double* acc) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, loss && acc, "nott_loss_accumulate: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    hipLaunchKernelGGL(loss_accumulate_kernel, dim3(1), dim3(1), 0, ctx->stream, loss, weight, acc);
+    return nott::launch_status(ctx, "loss_accumulate");
+}

@@ -180,17 +180,20 @@ struct Trainer {
     }
 
     // Step orchestration on device (the reference's CUDA-graph step path,
-    // src/core.hpp:3829-3945): forward + loss + backward are captured once
-    // into a HIP graph over static input buffers, so a step is two input
-    // copies, one graph launch and the fused AdamW launch.  The optimizer
-    // step stays outside the graph because its step count and bias
-    // corrections change every step.  `passes` forward/backward passes run
-    // first on the capture stream so the workspace and the allocator pools
-    // reach their steady state; their gradients are cleared again and the
-    // model's buffers (BatchNorm running statistics) restored, so the warm-up
-    // leaves no trace in the model.
+    // src/core.hpp:3829-3945): forward, loss, backward, the fused optimizer
+    // step (its step count and bias corrections in device memory, its
+    // hyper-parameters read at launch time) and the device-side loss
+    // accumulation (core.hpp:4481-4487) are captured once into a HIP graph
+    // over static input buffers, so a step is two input copies and one
+    // graph launch.  `passes` forward/backward passes run first on the
+    // capture stream so the workspace and the allocator pools reach their
+    // steady state; their gradients are cleared again and the model's buffers
+    // (BatchNorm running statistics) restored, so the warm-up leaves no trace
+    // in the model.
     std::unique_ptr<at::cuda::CUDAGraph> graph;
     Tensor gx, gy, gloss;
+    Tensor loss_acc;     // float64 device scalar: Σ loss·batch since the last reset
+    int64_t batch_rows = 0;
     void warmup(const Tensor& x, const Tensor& y, int passes) {
         std::vector<Tensor> saved;
         for (auto& b : model->buffers()) saved.push_back(b.clone());
@@ -211,9 +214,19 @@ struct Trainer {
             c10::hip::HIPStreamGuard guard(s);
             warmup(gx, gy, passes);
             if (hipStreamSynchronize(s.stream()) != hipSuccess) throw std::runtime_error("capture: stream sync failed");
+            fused->graph_prepare();
+            loss_acc = torch::zeros({1}, gx.options().dtype(torch::kFloat64));
+            batch_rows = gx.size(0);
             auto g = std::make_unique<at::cuda::CUDAGraph>();
             g->capture_begin();
             gloss = forward_backward(gx, gy);
+            fused->graph_step();
+            {
+                nott_ctx c = NH::bind(gloss);
+                NH::check(nott_loss_accumulate(c, gloss.data_ptr<float>(), (double)batch_rows,
+                                               loss_acc.data_ptr<double>()),
+                          c, "loss accumulation");
+            }
             g->capture_end();
             graph = std::move(g);
             // The captured forward was recorded, not run.
@@ -224,15 +237,115 @@ struct Trainer {
     }
     // parameters.binary in Nott's archive layout (src/core.hpp:2131-2135).
     void save(const std::string& path) { NH::save_parameters(*model, path); }
+    // Loads a parameters.binary written by Model::save (core.hpp:2188-2236
+    // reads the same archive): every parameter and buffer by its
+    // registration key, with the reference's checks (a missing key or a
+    // shape mismatch throws), copied into this model's tensors (which are
+    // views into the optimizer's flat arena) and the bf16 copies refreshed.
+    // torch::nn::Module::save nests one archive per child module, so a key
+    // a.b.weight is read through the archives a and b.
+    static bool read_nested(torch::serialize::InputArchive& ar, const std::string& key, Tensor& t) {
+        const auto dot = key.find('.');
+        if (dot == std::string::npos) return ar.try_read(key, t);
+        torch::serialize::InputArchive sub;
+        if (!ar.try_read(key.substr(0, dot), sub)) return false;
+        return read_nested(sub, key.substr(dot + 1), t);
+    }
+    void load_archive(const std::string& path) {
+        torch::serialize::InputArchive ar;
+        ar.load_from(path);
+        std::map<std::string, Tensor> vals;
+        auto take = [&](const std::string& key, const Tensor& dst) {
+            Tensor t;
+            if (!read_nested(ar, key, t)) throw std::runtime_error("checkpoint is missing '" + key + "'");
+            if (t.sizes() != dst.sizes()) throw std::runtime_error("checkpoint tensor '" + key + "' has another shape");
+            vals[key] = t.to(dst.device(), dst.scalar_type());
+        };
+        for (auto& kv : model->named_parameters()) take(kv.key(), kv.value());
+        for (auto& kv : model->named_buffers()) take(kv.key(), kv.value());
+        load(vals);
+        for (auto& child : model->modules(/*include_self=*/true))
+            if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->reload_counter();
+    }
+    // One replayed step: the batch goes into the graph's input buffers, the
+    // optimizer's current options into its pinned hyper-parameter block.
     Tensor step_graph(const Tensor& x, const Tensor& y) {
         if (!graph) throw std::logic_error("step_graph: call capture() first");
         gx.copy_(x);
         gy.copy_(y);
+        replay();
+        return gloss.clone();
+    }
+    void replay() {
+        fused->graph_sync();
         graph->replay();
+        fused->graph_after_replay();
         for (auto& child : model->modules(/*include_self=*/true))
             if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->count_batch();
-        opt->step();
-        return gloss.clone();
+    }
+    // Σ loss·batch accumulated on the device by the replayed steps since the
+    // last reset (core.hpp:4481-4487), read back (one synchronisation).
+    double loss_sum() {
+        if (!loss_acc.defined()) throw std::logic_error("loss_sum: call capture() first");
+        return loss_acc.item<double>();
+    }
+    void reset_loss_sum() {
+        if (loss_acc.defined()) loss_acc.zero_();
+    }
+    // One epoch over host tensors as Model::run_epochs stages it
+    // (core.hpp:4165-4305, 4481-4487): xs / ys hold whole batches in pinned
+    // host memory; batch i+1 is copied to the device on a copy stream into
+    // the other of two buffers while step i runs, each step is one graph
+    // replay (optimizer and loss accumulation included), and the mean loss
+    // of the epoch is read back once at the end.
+    double train_epoch(const Tensor& xs, const Tensor& ys) {
+        if (!graph) throw std::logic_error("train_epoch: call capture() first");
+        if (!xs.is_pinned() || !ys.is_pinned()) throw std::invalid_argument("train_epoch: inputs must be pinned host tensors");
+        const int64_t b = batch_rows, n = xs.size(0) / b;
+        if (n * b != xs.size(0) || ys.size(0) != xs.size(0))
+            throw std::invalid_argument("train_epoch: sample count must be a multiple of the captured batch");
+        const auto dev = gx.device();
+        const int di = dev.index();
+        auto main = c10::hip::getCurrentHIPStream(di);
+        auto copy = c10::hip::getStreamFromPool(false, di);
+        std::array<Tensor, 2> bx{torch::empty_like(gx), torch::empty_like(gx)};
+        std::array<Tensor, 2> by{torch::empty_like(gy), torch::empty_like(gy)};
+        struct Events {
+            hipEvent_t e[4] = {};
+            Events() {
+                for (auto& x : e)
+                    if (hipEventCreateWithFlags(&x, hipEventDisableTiming) != hipSuccess)
+                        throw std::runtime_error("train_epoch: hipEventCreate failed");
+            }
+            ~Events() {
+                for (auto& x : e) (void)hipEventDestroy(x);
+            }
+        } ev;
+        hipEvent_t* landed = ev.e;        // batch in buffer k is on the device
+        hipEvent_t* consumed = ev.e + 2;  // buffer k was copied into the graph's inputs
+        auto hip_ok = [](hipError_t e, const char* what) {
+            if (e != hipSuccess) throw std::runtime_error(std::string("train_epoch: ") + what);
+        };
+        auto stage = [&](int64_t i) {
+            const int k = (int)(i & 1);
+            c10::hip::HIPStreamGuard g(copy);
+            if (i >= 2) hip_ok(hipStreamWaitEvent(copy.stream(), consumed[k], 0), "wait");
+            bx[k].copy_(xs.narrow(0, i * b, b).view(gx.sizes()), /*non_blocking=*/true);
+            by[k].copy_(ys.narrow(0, i * b, b).view(gy.sizes()), /*non_blocking=*/true);
+            hip_ok(hipEventRecord(landed[k], copy.stream()), "record");
+        };
+        reset_loss_sum();
+        stage(0);
+        for (int64_t i = 0; i < n; ++i) {
+            const int k = (int)(i & 1);
+            if (i + 1 < n) stage(i + 1);
+            hip_ok(hipStreamWaitEvent(main.stream(), landed[k], 0), "wait");
+            gx.copy_(bx[k], /*non_blocking=*/true);
+            gy.copy_(by[k], /*non_blocking=*/true);
+            hip_ok(hipEventRecord(consumed[k], main.stream()), "record");
+            replay();
+        }
+        return loss_sum() / (double)(n * b);
     }
     Tensor forward(const Tensor& x) {
         torch::NoGradGuard ng;
@@ -331,7 +444,11 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("capture", &SmallT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
              py::call_guard<py::gil_scoped_release>())
         .def("step_graph", &SmallT::step_graph, py::call_guard<py::gil_scoped_release>())
+        .def("train_epoch", &SmallT::train_epoch, py::call_guard<py::gil_scoped_release>())
+        .def("loss_sum", &SmallT::loss_sum)
+        .def("reset_loss_sum", &SmallT::reset_loss_sum)
         .def("save", &SmallT::save, py::arg("path"))
+        .def("load_archive", &SmallT::load_archive, py::arg("path"))
         .def("forward_backward", &SmallT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", &SmallT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &SmallT::forward, py::call_guard<py::gil_scoped_release>())
@@ -357,7 +474,11 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("capture", &ResT::capture, py::arg("x"), py::arg("y"), py::arg("passes") = 2,
              py::call_guard<py::gil_scoped_release>())
         .def("step_graph", &ResT::step_graph, py::call_guard<py::gil_scoped_release>())
+        .def("train_epoch", &ResT::train_epoch, py::call_guard<py::gil_scoped_release>())
+        .def("loss_sum", &ResT::loss_sum)
+        .def("reset_loss_sum", &ResT::reset_loss_sum)
         .def("save", &ResT::save, py::arg("path"))
+        .def("load_archive", &ResT::load_archive, py::arg("path"))
         .def("forward_backward", &ResT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", &ResT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &ResT::forward, py::call_guard<py::gil_scoped_release>())
