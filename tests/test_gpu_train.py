@@ -498,3 +498,43 @@ def test_reference_checkpoint_loads_into_hip_model(host_mod, tmp_path, model):
     check(got, want, "f32", f"{model} logits from a reference checkpoint")
     if model == "resnet18":
         assert int(tr.buffers()["batchnorm2d_1.num_batches_tracked"]) == 2
+
+
+@pytest.mark.parametrize("model", ["small_cnn", "resnet18"])
+def test_model_directory_round_trip(host_mod, tmp_path, model):
+    """Model::save's directory (core.hpp:2088-2137: <dir>/<name>/ with
+    architecture.json and parameters.binary; an existing directory leads to
+    <name>_1, the reference's default answer) loads back through
+    Model::load's checks (core.hpp:2140-2244) into a fresh model: same
+    parameters and buffers, same name; an architecture.json of another
+    model is refused."""
+    def make(seed):
+        if model == "small_cnn":
+            return host_mod.SmallCNNTrainer(0, seed, 1e-3)
+        return host_mod.ResNet18Trainer(0, seed, False, 1e-3, 1e-2, 1000)
+    a = make(3)
+    if model == "small_cnn":
+        x, y = torch.rand(8, 1, 28, 28).cuda(), torch.randint(0, 10, (8,)).cuda()
+    else:
+        x, y = torch.rand(2, 3, 224, 224).cuda(), torch.randint(0, 1000, (2,)).cuda()
+    a.step(x, y)
+    a.set_model_name("net")
+    d1 = a.save_model(str(tmp_path))
+    d2 = a.save_model(str(tmp_path))
+    assert d1.endswith("/net") and d2.endswith("/net_1")
+    with open(f"{d1}/architecture.json") as f:
+        assert f.read() == a.architecture_json()
+    b = make(4)
+    b.load_model(d2)
+    assert b.model_name() == "net"
+    pa, pb = a.params(), b.params()
+    for k in pa:
+        assert torch.equal(pa[k], pb[k]), k
+    ba, bb = a.buffers(), b.buffers()
+    for k in ba:
+        assert torch.equal(ba[k].cpu(), bb[k].cpu()), k
+    other = "resnet18" if model == "small_cnn" else "small_cnn"
+    with open(f"{d1}/architecture.json", "w") as f:
+        f.write(host_mod.architecture_json(other))
+    with pytest.raises(RuntimeError, match="describes another model"):
+        b.load_model(d1)

@@ -8,12 +8,16 @@
 // forward, mean cross-entropy, loss.backward(), optimizer step, zero_grad.
 #include <torch/extension.h>
 
+#include "nott_hip/architecture.hpp"
 #include "nott_hip/host.hpp"
+
+#include <filesystem>
 
 #include <ATen/hip/HIPGraph.h>
 #include <c10/hip/HIPGuard.h>
 
 namespace NH = Nott::HIP;
+namespace NA = Nott::HIP::arch;
 using torch::Tensor;
 
 namespace {
@@ -33,6 +37,18 @@ struct SmallCNNImpl : torch::nn::Module {
         flat = register_module("flatten_4", NH::Flatten());
         fc0 = register_module("fc_5", NH::Linear(3136, 128));
         fc1 = register_module("fc_6", NH::Linear(128, 10));
+    }
+    // The descriptor list a Nott model of this architecture records, in
+    // add() order (core.hpp:490-817): the layer factories' descriptors with
+    // ReLU on both convolutions and the first FC, Kaiming-uniform weights.
+    static std::vector<NA::Node> descriptors() {
+        return {NA::module("layer", NA::conv2d(1, 32, 3, 1, 1, true, "relu", "he_uniform")),
+                NA::module("layer", NA::max_pool2d(2, 2, 0)),
+                NA::module("layer", NA::conv2d(32, 64, 3, 1, 1, true, "relu", "he_uniform")),
+                NA::module("layer", NA::max_pool2d(2, 2, 0)),
+                NA::module("layer", NA::flatten()),
+                NA::module("layer", NA::fc(3136, 128, true, "relu", "he_uniform")),
+                NA::module("layer", NA::fc(128, 10, true, "identity", "he_uniform"))};
     }
     Tensor forward(Tensor x) {
         x = pool0(conv0->forward_relu(x));   // Conv + ReLU (fused), MaxPool2
@@ -60,7 +76,8 @@ struct ResNet18Impl : torch::nn::Module {
     NH::AdaptiveAvgPool2d gap{nullptr};
     NH::Flatten flat{nullptr};
     NH::Linear fc{nullptr};
-    explicit ResNet18Impl(int64_t classes) {
+    int64_t classes;
+    explicit ResNet18Impl(int64_t classes_) : classes(classes_) {
         int64_t index = 0;
         auto key = [&](const char* kind) { return std::string(kind) + "_" + std::to_string(index++); };
         stem = register_module(key("conv2d"), NH::Conv2d(NH::Conv2dOptions{3, 64, {7, 7}, {2, 2}, {3, 3}, {1, 1}, false}));
@@ -79,6 +96,37 @@ struct ResNet18Impl : torch::nn::Module {
         gap = register_module(key("adaptive_avgpool2d"), NH::AdaptiveAvgPool2d());
         flat = register_module(key("flatten"), NH::Flatten());
         fc = register_module(key("fc"), NH::Linear(512, classes));
+    }
+    // The descriptor list a Nott model of this architecture records: stem
+    // conv (identity), BatchNorm2d + ReLU, MaxPool2d 3/2/1, eight residual
+    // block descriptors ({conv 3×3, BN + ReLU, conv 3×3, BN}, final ReLU, a
+    // 1×1 projection conv on the down-sampling ones), AdaptiveAvgPool2d,
+    // Flatten, FC; Kaiming-uniform conv and FC weights.
+    std::vector<NA::Node> descriptors() const { return descriptors_for(classes); }
+    static std::vector<NA::Node> descriptors_for(int64_t classes) {
+        std::vector<NA::Node> mods;
+        mods.push_back(NA::module("layer", NA::conv2d(3, 64, 7, 2, 3, false, "identity", "he_uniform")));
+        mods.push_back(NA::module("layer", NA::batch_norm2d(64, "relu")));
+        mods.push_back(NA::module("layer", NA::max_pool2d(3, 2, 1)));
+        const int64_t widths[4] = {64, 128, 256, 512};
+        int64_t in = 64;
+        for (int s = 0; s < 4; ++s)
+            for (int b = 0; b < 2; ++b) {
+                const int64_t out = widths[s], stride = (s > 0 && b == 0) ? 2 : 1;
+                std::vector<NA::Node> layers;
+                layers.push_back(NA::conv2d(in, out, 3, stride, 1, false, "identity", "he_uniform"));
+                layers.push_back(NA::batch_norm2d(out, "relu"));
+                layers.push_back(NA::conv2d(out, out, 3, 1, 1, false, "identity", "he_uniform"));
+                layers.push_back(NA::batch_norm2d(out, "identity"));
+                const NA::Node proj = NA::conv2d(in, out, 1, stride, 0, false, "identity", "he_uniform");
+                const bool projection = stride != 1 || in != out;
+                mods.push_back(NA::module("block", NA::residual(std::move(layers), projection ? &proj : nullptr, "relu")));
+                in = out;
+            }
+        mods.push_back(NA::module("layer", NA::adaptive_avg_pool2d(1, 1)));
+        mods.push_back(NA::module("layer", NA::flatten()));
+        mods.push_back(NA::module("layer", NA::fc(512, classes, true, "identity", "he_uniform")));
+        return mods;
     }
     Tensor forward(Tensor x) {
         x = pool(stem_bn->forward_relu(stem(x)));
@@ -267,6 +315,75 @@ struct Trainer {
         for (auto& child : model->modules(/*include_self=*/true))
             if (auto* bn = child->template as<NH::BatchNorm2dImpl>()) bn->reload_counter();
     }
+    // Model::model_name (core.hpp:2078-2086): the set name, else the
+    // module's own ("Nott::Model" for a model constructed without one).
+    std::string model_name_;
+    void set_model_name(const std::string& n) { model_name_ = n; }
+    std::string model_name() const { return model_name_.empty() ? std::string("Nott::Model") : model_name_; }
+    NA::Node architecture() const { return NA::architecture(model_name(), model->descriptors()); }
+    std::string architecture_json() const { return NA::to_json(architecture()); }
+    // Model::save (core.hpp:2088-2137): <directory>/<model name>/ holding
+    // architecture.json and parameters.binary.  The reference asks on stdin
+    // whether to overwrite an existing directory and, on an empty or
+    // negative answer, picks <name>_<k> with the first free k; this host
+    // never reads stdin and always takes that default.  Returns the
+    // directory written.
+    std::string save_model(const std::string& directory) {
+        namespace fs = std::filesystem;
+        if (directory.empty()) throw std::invalid_argument("Model::save requires a non-empty directory path.");
+        fs::path target = fs::path(directory) / model_name();
+        if (fs::exists(target))
+            for (int k = 1;; ++k) {
+                auto candidate = fs::path(directory) / (model_name() + "_" + std::to_string(k));
+                if (!fs::exists(candidate)) { target = candidate; break; }
+            }
+        fs::create_directories(target);
+        const auto arch_path = target / "architecture.json";
+        try {
+            NA::write_file(arch_path.string(), architecture());
+        } catch (const std::exception& e) {
+            throw std::runtime_error("Failed to write architecture description to '" + arch_path.string() + "': " +
+                                     e.what());
+        }
+        save((target / "parameters.binary").string());
+        return target.string();
+    }
+    // Model::load (core.hpp:2140-2244) for a model whose layers are fixed:
+    // the directory's architecture.json must describe this model's
+    // descriptor list (the reference replays add() from it instead), then
+    // every parameter and buffer is read from parameters.binary with the
+    // key and shape checks of load_archive.  The file's name becomes the
+    // model's name.
+    void load_model(const std::string& directory) {
+        namespace fs = std::filesystem;
+        if (directory.empty()) throw std::invalid_argument("Model::load requires a non-empty directory path.");
+        const auto arch_path = fs::path(directory) / "architecture.json";
+        const auto params_path = fs::path(directory) / "parameters.binary";
+        if (!fs::exists(arch_path))
+            throw std::runtime_error("Architecture file not found at '" + arch_path.string() + "'.");
+        if (!fs::exists(params_path))
+            throw std::runtime_error("Parameter archive not found at '" + params_path.string() + "'.");
+        NA::Node file;
+        try {
+            file = NA::read_file(arch_path.string());
+        } catch (const std::exception& e) {
+            throw std::runtime_error("Failed to read architecture description from '" + arch_path.string() + "': " +
+                                     e.what());
+        }
+        const NA::Node* modules = file.find("modules");
+        if (!modules)
+            throw std::runtime_error("Architecture description '" + arch_path.string() +
+                                     "' is missing the 'modules' entry.");
+        NA::Node want;
+        for (auto& m : model->descriptors()) want.push_back(std::move(m));
+        std::string where;
+        if (!NA::matches(want, *modules, where))
+            throw std::runtime_error("Architecture description '" + arch_path.string() +
+                                     "' describes another model (first difference at modules" + where + ").");
+        const NA::Node* name = file.find("name");
+        model_name_ = name ? name->data : std::string();
+        load_archive(params_path.string());
+    }
     // One replayed step: the batch goes into the graph's input buffers, the
     // optimizer's current options into its pinned hyper-parameter block.
     Tensor step_graph(const Tensor& x, const Tensor& y) {
@@ -431,6 +548,13 @@ PYBIND11_MODULE(_nott_host, m) {
         NH::check(nott_workspace_bytes(c, &b), c, "workspace bytes");
         return b;
     }, py::arg("device") = 0);
+    // architecture.json text of a model (no device needed): "small_cnn" or
+    // "resnet18" with `classes` outputs.
+    m.def("architecture_json", [](const std::string& model, int64_t classes, const std::string& name) {
+        if (model == "small_cnn") return NA::to_json(NA::architecture(name, SmallCNNImpl::descriptors()));
+        if (model == "resnet18") return NA::to_json(NA::architecture(name, ResNet18Impl::descriptors_for(classes)));
+        throw std::invalid_argument("unknown model '" + model + "'");
+    }, py::arg("model"), py::arg("classes") = 1000, py::arg("name") = "Nott::Model");
     using SmallT = Trainer<SmallCNN, false>;
     py::class_<SmallT>(m, "SmallCNNTrainer")
         .def(py::init([](int device, uint64_t seed, double lr) {
@@ -449,6 +573,11 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("reset_loss_sum", &SmallT::reset_loss_sum)
         .def("save", &SmallT::save, py::arg("path"))
         .def("load_archive", &SmallT::load_archive, py::arg("path"))
+        .def("save_model", &SmallT::save_model, py::arg("directory"))
+        .def("load_model", &SmallT::load_model, py::arg("directory"))
+        .def("architecture_json", &SmallT::architecture_json)
+        .def("set_model_name", &SmallT::set_model_name)
+        .def("model_name", &SmallT::model_name)
         .def("forward_backward", &SmallT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", &SmallT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &SmallT::forward, py::call_guard<py::gil_scoped_release>())
@@ -479,6 +608,11 @@ PYBIND11_MODULE(_nott_host, m) {
         .def("reset_loss_sum", &ResT::reset_loss_sum)
         .def("save", &ResT::save, py::arg("path"))
         .def("load_archive", &ResT::load_archive, py::arg("path"))
+        .def("save_model", &ResT::save_model, py::arg("directory"))
+        .def("load_model", &ResT::load_model, py::arg("directory"))
+        .def("architecture_json", &ResT::architecture_json)
+        .def("set_model_name", &ResT::set_model_name)
+        .def("model_name", &ResT::model_name)
         .def("forward_backward", &ResT::forward_backward, py::call_guard<py::gil_scoped_release>())
         .def("optimizer_step", &ResT::optimizer_step, py::call_guard<py::gil_scoped_release>())
         .def("forward", &ResT::forward, py::call_guard<py::gil_scoped_release>())
