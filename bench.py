@@ -47,14 +47,19 @@ METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HB
 # The passes and their commands are in profiles/.  Keyed by (workload, dtype,
 # kernel group); None where no pass has been recorded.
 TRAFFIC = {
-    ("conv_bwd", "bf16", "dgrad"): 183.36e6,   # conv3x3_wprep + conv3x3_same
-    ("conv_bwd", "bf16", "wgrad"): 230.21e6,   # conv3x3_wgrad + conv3x3_wgrad_reduce
-    ("ln_bwd", "f32", "all"): 210.93e6,        # ln_bwd_kernel + col_reduce_grouped_kernel
-    ("ln_bwd", "bf16", "all"): 109.77e6,
-    ("adamw", "f32", "all"): 2799.94e6,
+    ("conv_bwd", "f32", "dgrad"): 416.03e6,    # conv3x3_wprep + conv3x3_same
+    ("conv_bwd", "f32", "wgrad"): 385.08e6,    # conv3x3_wgrad + conv3x3_wgrad_reduce
+    ("conv_bwd", "bf16", "dgrad"): 182.82e6,
+    ("conv_bwd", "bf16", "wgrad"): 230.20e6,
+    ("ln_bwd", "f32", "all"): 206.31e6,        # ln_bwd_kernel + col_reduce_grouped_kernel
+    ("ln_bwd", "bf16", "all"): 105.54e6,
+    ("adamw", "f32", "all"): 2799.95e6,
     ("adamw", "bf16", "all"): 2200.00e6,
-    ("xent", "f32", "all"): 4199.32e6,         # xent_count_kernel + xent_rows_vec_kernel
-    ("xent", "bf16", "all"): 2101.43e6,
+    ("xent", "f32", "all"): 4199.41e6,         # xent_count_kernel + xent_rows_vec_kernel
+    ("xent", "bf16", "all"): 2101.29e6,
+    ("mha_bwd", "bf16", "out_proj"): 194.04e6,   # dA GEMM + dW_o split GEMM + reduce
+    ("mha_bwd", "bf16", "attention"): 241.85e6,  # attn_dq64 + attn_dkdv64
+    ("mha_bwd", "bf16", "in_proj"): 480.57e6,    # dX GEMM + dW_qkv split GEMM + reduce
 }
 
 

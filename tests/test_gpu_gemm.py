@@ -151,6 +151,7 @@ CONV = [
     (16, 64, 14, 14, 64, 3, 3, 1, 1, 1),
     (64, 32, 7, 7, 64, 3, 3, 1, 1, 1),
     (2, 5, 16, 16, 64, 3, 3, 1, 1, 2),
+    (4, 64, 15, 15, 64, 3, 3, 2, 1, 1),        # odd input width: one-output-per-thread col2im
 ]
 
 
