@@ -151,7 +151,19 @@ CONV = [
     (16, 64, 14, 14, 64, 3, 3, 1, 1, 1),
     (64, 32, 7, 7, 64, 3, 3, 1, 1, 1),
     (2, 5, 16, 16, 64, 3, 3, 1, 1, 2),
-    (4, 64, 15, 15, 64, 3, 3, 2, 1, 1),        # odd input width: one-output-per-thread col2im
+    (2, 3, 15, 15, 64, 7, 7, 2, 3, 1),         # column-path dgrad at an odd width: one-output-per-thread col2im
+    # LDS-staged tap kernels (conv_tap.hip): strided 3x3 with odd sizes and a
+    # partial 64-channel block (parity classes of different sizes in dgrad),
+    # 1x1 stride 2 at odd sizes (dgrad classes no tap reaches stay zero),
+    # 3x3 stride 1 wider than the 3x3 kernels take, 1x1 stride 1, and a
+    # stride-2 pass small enough to split its channel chunks
+    (4, 64, 15, 15, 64, 3, 3, 2, 1, 1),
+    (3, 64, 13, 11, 96, 3, 3, 2, 1, 1),
+    (2, 64, 9, 9, 64, 1, 1, 2, 0, 1),
+    (2, 32, 70, 70, 32, 3, 3, 1, 1, 1),
+    (4, 32, 8, 8, 32, 1, 1, 1, 0, 1),
+    (1, 128, 8, 8, 64, 3, 3, 2, 1, 1),
+    (2, 32, 40, 40, 256, 3, 3, 2, 1, 1),       # one channel chunk: the bf16 forward takes the tap kernel unsplit
 ]
 
 

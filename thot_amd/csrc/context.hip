@@ -1,6 +1,8 @@
 // Context, errors and workspace of libnott_hip.
 #include "common.hpp"
 
+#include <cstdlib>
+
 #include <new>
 
 namespace nott {
@@ -69,6 +71,10 @@ int nott_create(int device, nott_ctx* out) {
     nott::DeviceScope scope(device);
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cu = prop.multiProcessorCount;
+    // NOTT_CONV_TAP=0 keeps convolutions off the conv_tap kernels (their
+    // column / generic paths run instead), so both implementations can be
+    // checked and timed against each other.
+    if (const char* e = std::getenv("NOTT_CONV_TAP")) c->conv_tap = (e[0] != '0');
     if (hipMalloc(&c->err_word, sizeof(unsigned long long)) != hipSuccess) {
         delete c;
         return NOTT_ERR_ALLOC;

@@ -721,6 +721,9 @@ int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const voi
                                        static_cast<T*>(y), relu);
     if (cin1_applies(d))
         return cin1_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y), relu);
+    if (nott::conv_fast::tap_fwd_applies(ctx, d, sizeof(T)))
+        return nott::conv_fast::tap_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b,
+                                           static_cast<T*>(y), relu);
     const int st = fwd_plain<T>(ctx, d, p, q, x, w, b, y);
     if (st != NOTT_OK || !relu) return st;
     return nott_relu_fwd(ctx, sizeof(T) == 2 ? NOTT_BF16 : NOTT_F32, d->n * d->k * p * q, y, y);
@@ -730,6 +733,9 @@ template <typename T>
 int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const void* dy, const void* w, void* dx) {
     if (nott::conv_fast::dgrad_applies(d, sizeof(T)))
         return nott::conv_fast::dgrad<T>(ctx, d, static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx));
+    if (nott::conv_fast::tap_dgrad_applies(ctx, d, sizeof(T)))
+        return nott::conv_fast::tap_dgrad<T>(ctx, d, static_cast<const T*>(dy), static_cast<const T*>(w),
+                                             static_cast<T*>(dx));
     if constexpr (sizeof(T) == 2) {
         if (col_applies(d, p, q, true))
             return col_dgrad(ctx, d, p, q, static_cast<const T*>(dy), static_cast<const T*>(w), static_cast<T*>(dx));

@@ -26,7 +26,7 @@
 //
 // conv3x3_wgrad_kernel computes dw[k, c, r, s] = Σ_{n,h,w} dy[n,k,h,w] ·
 // x[n, c, h−1+r, w−1+s] (ATen convolution_backward, weight grad).
-#include "conv_fast.hpp"
+#include "conv_tile.hpp"
 
 #include <algorithm>
 
@@ -34,21 +34,6 @@ namespace nott {
 namespace conv_fast {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTilePix = 256;       // pixels per workgroup (4 waves × 64)
-constexpr int kTileCo = 64;         // output channels per workgroup
-constexpr int kRowB = 64;           // bytes per LDS row (one channel chunk)
-
-template <typename T> struct Chunk;
-template <> struct Chunk<float> { static constexpr int CC = 16, SUB = 4; };   // channels per chunk / per 16 B
-template <> struct Chunk<bf16_t> { static constexpr int CC = 32, SUB = 8; };
-
-// LDS layout of [row][4 × 16-byte sub-chunks] tiles: rows are grouped by 16
-// and stored sub-chunk-major inside a group, so the 16 lanes of a quarter-wave
-// that read 16 consecutive rows at the same sub-chunk touch 16 distinct
-// 16-byte slots of 256-byte blocks (4 LDS cycles per ds_read_b128, measured
-// with SQ_LDS_BANK_CONFLICT = 0), whatever row the run starts at.
-__device__ __forceinline__ int lds_off(int row, int sub) { return ((row >> 4) << 10) + (sub << 8) + ((row & 15) << 4); }
 
 struct SameParams {
     int32_t n, cin, h, w, cout;
@@ -100,93 +85,6 @@ __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict_
     wp[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = val;
 }
 
-template <typename T>
-__device__ __forceinline__ u32x4 pack_sub(const T (&v)[Chunk<T>::SUB]);
-template <>
-__device__ __forceinline__ u32x4 pack_sub<float>(const float (&v)[4]) {
-    return u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                 __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
-}
-template <>
-__device__ __forceinline__ u32x4 pack_sub<bf16_t>(const bf16_t (&v)[8]) {
-    return u32x4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
-                 (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)};
-}
-
-template <typename T>
-__device__ __forceinline__ void mfma_chunk(const u32x4& a, const u32x4& b, f32x4& acc) {
-    if constexpr (sizeof(T) == 2) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                      acc, 0, 0, 0);
-    } else {
-        const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
-    }
-}
-
-// Register transpose of a SUB×SUB block: in[i] holds SUB pixels of channel i,
-// out[j] holds SUB channels of pixel j.
-__device__ __forceinline__ void transpose_block(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-    // bf16: dword d of in[i] = pixels (2d, 2d+1); dword e of out[j] = channels (2e, 2e+1).
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t a = in[2 * e][d], b = in[2 * e + 1][d];
-            out[2 * d][e] = (a & 0xffffu) | (b << 16);
-            out[2 * d + 1][e] = (a >> 16) | (b & 0xffff0000u);
-        }
-    }
-}
-__device__ __forceinline__ void transpose_block(const u32x4 (&in)[4], u32x4 (&out)[4]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = u32x4{in[0][j], in[1][j], in[2][j], in[3][j]};
-}
-
-// Fill tasks per thread whose global loads are issued one channel chunk ahead
-// and held in registers across the MFMA loop; a tile with more tasks (one
-// that spans more padded rows, e.g. across an image boundary) loads the rest
-// when it stores them.
-template <typename T> struct VecTasks;
-template <> struct VecTasks<bf16_t> { static constexpr int VT = 1; };
-template <> struct VecTasks<float> { static constexpr int VT = 2; };
-
-// Chunk ch (E elements, 16 bytes) of an image row of w elements, read with
-// LW-byte loads (LW = 16 when rows are whole 16-byte chunks; 8, 4 or 2 when
-// w is only a multiple of 4, 2 or 1 bf16 / of 2 or 1 fp32): pieces past the
-// row end read as zero.
-template <typename T, int LW, bool NT = false>
-__device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, int w) {
-    constexpr int E = 16 / (int)sizeof(T), PE = LW / (int)sizeof(T);   // elements per chunk / per piece
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (LW == 16) {
-        if (ch * E < w) {
-            const u32x4* q = reinterpret_cast<const u32x4*>(row + ch * E);
-            v = NT ? __builtin_nontemporal_load(q) : *q;
-        }
-    } else if constexpr (LW == 8) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-            if (ch * E + q * PE < w) {
-                const uint2 t = *reinterpret_cast<const uint2*>(row + ch * E + q * PE);
-                v[2 * q] = t.x;
-                v[2 * q + 1] = t.y;
-            }
-    } else if constexpr (LW == 4) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (ch * E + q * PE < w) v[q] = *reinterpret_cast<const uint32_t*>(row + ch * E + q * PE);
-    } else {
-        static_assert(LW == 2 && sizeof(T) == 2, "2-byte pieces are bf16 elements");
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            if (ch * E + q < w) v[q >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[ch * E + q] << (16 * (q & 1));
-    }
-    return v;
-}
 
 template <typename T, bool VEC, int LW>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
@@ -509,12 +407,6 @@ size_t same_lds_bytes(int32_t h, int32_t w, size_t elem) {
 }
 constexpr size_t kSameLdsMax = 80 * 1024;   // two workgroups per CU
 
-// Widest load (bytes) that keeps every image row's pieces aligned.
-int wgrad_load_width(int64_t w, size_t elem) {
-    for (int lw = 16; lw > (int)elem; lw >>= 1)
-        if ((w * (int64_t)elem) % lw == 0) return lw;
-    return (int)elem;
-}
 
 template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
@@ -905,6 +797,13 @@ int wgrad_slot_pitch(int64_t w) {
 }
 
 }  // namespace
+
+// Widest load (bytes) that keeps every image row's pieces aligned.
+int wgrad_load_width(int64_t w, size_t elem) {
+    for (int lw = 16; lw > (int)elem; lw >>= 1)
+        if ((w * (int64_t)elem) % lw == 0) return lw;
+    return (int)elem;
+}
 
 bool fwd_applies(const nott_conv2d_desc* d, size_t elem) {
     const int cc = elem == 2 ? Chunk<bf16_t>::CC : Chunk<float>::CC;

@@ -17,5 +17,17 @@ int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* d
 template <typename T>
 int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate);
 
+// LDS-staged implicit GEMM for other NCHW shapes (stride 1 or 2, up to 9
+// taps; conv_tap.hip).
+bool tap_fwd_applies(nott_ctx ctx, const nott_conv2d_desc* d, size_t elem);
+bool tap_dgrad_applies(nott_ctx ctx, const nott_conv2d_desc* d, size_t elem);
+template <typename T>
+int tap_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu);
+template <typename T>
+int tap_dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* dx);
+
+// Widest load (bytes) that keeps every image row's pieces aligned.
+int wgrad_load_width(int64_t w, size_t elem);
+
 }  // namespace conv_fast
 }  // namespace nott

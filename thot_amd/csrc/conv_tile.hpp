@@ -1,0 +1,117 @@
+// Building blocks shared by the LDS-staged convolution kernels (conv3x3.hip,
+// conv_tap.hip): tile constants, the 16-row-grouped LDS row layout, channel
+// chunks, the register transpose of the NCHW fill and the MFMA step on one
+// 16-byte operand pair.
+#pragma once
+
+#include "conv_fast.hpp"
+
+namespace nott {
+namespace conv_fast {
+
+constexpr int kThreads = 256;
+constexpr int kTilePix = 256;       // pixels per workgroup (4 waves × 64)
+constexpr int kTileCo = 64;         // output channels per workgroup
+constexpr int kRowB = 64;           // bytes per LDS row (one channel chunk)
+
+template <typename T> struct Chunk;
+template <> struct Chunk<float> { static constexpr int CC = 16, SUB = 4; };   // channels per chunk / per 16 B
+template <> struct Chunk<bf16_t> { static constexpr int CC = 32, SUB = 8; };
+
+// LDS layout of [row][4 × 16-byte sub-chunks] tiles: rows are grouped by 16
+// and stored sub-chunk-major inside a group, so the 16 lanes of a quarter-wave
+// that read 16 consecutive rows at the same sub-chunk touch 16 distinct
+// 16-byte slots of 256-byte blocks (4 LDS cycles per ds_read_b128, measured
+// with SQ_LDS_BANK_CONFLICT = 0), whatever row the run starts at.
+__device__ __forceinline__ int lds_off(int row, int sub) { return ((row >> 4) << 10) + (sub << 8) + ((row & 15) << 4); }
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack_sub(const T (&v)[Chunk<T>::SUB]);
+template <>
+__device__ __forceinline__ u32x4 pack_sub<float>(const float (&v)[4]) {
+    return u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                 __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])};
+}
+template <>
+__device__ __forceinline__ u32x4 pack_sub<bf16_t>(const bf16_t (&v)[8]) {
+    return u32x4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                 (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)};
+}
+
+template <typename T>
+__device__ __forceinline__ void mfma_chunk(const u32x4& a, const u32x4& b, f32x4& acc) {
+    if constexpr (sizeof(T) == 2) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                      acc, 0, 0, 0);
+    } else {
+        const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
+    }
+}
+
+// Register transpose of a SUB×SUB block: in[i] holds SUB pixels of channel i,
+// out[j] holds SUB channels of pixel j.
+__device__ __forceinline__ void transpose_block(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+    // bf16: dword d of in[i] = pixels (2d, 2d+1); dword e of out[j] = channels (2e, 2e+1).
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t a = in[2 * e][d], b = in[2 * e + 1][d];
+            out[2 * d][e] = (a & 0xffffu) | (b << 16);
+            out[2 * d + 1][e] = (a >> 16) | (b & 0xffff0000u);
+        }
+    }
+}
+__device__ __forceinline__ void transpose_block(const u32x4 (&in)[4], u32x4 (&out)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = u32x4{in[0][j], in[1][j], in[2][j], in[3][j]};
+}
+
+// Fill tasks per thread whose global loads are issued one channel chunk ahead
+// and held in registers across the MFMA loop; a tile with more tasks (one
+// that spans more padded rows, e.g. across an image boundary) loads the rest
+// when it stores them.
+template <typename T> struct VecTasks;
+template <> struct VecTasks<bf16_t> { static constexpr int VT = 1; };
+template <> struct VecTasks<float> { static constexpr int VT = 2; };
+
+// Chunk ch (E elements, 16 bytes) of an image row of w elements, read with
+// LW-byte loads (LW = 16 when rows are whole 16-byte chunks; 8, 4 or 2 when
+// w is only a multiple of 4, 2 or 1 bf16 / of 2 or 1 fp32): pieces past the
+// row end read as zero.
+template <typename T, int LW, bool NT = false>
+__device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, int w) {
+    constexpr int E = 16 / (int)sizeof(T), PE = LW / (int)sizeof(T);   // elements per chunk / per piece
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (LW == 16) {
+        if (ch * E < w) {
+            const u32x4* q = reinterpret_cast<const u32x4*>(row + ch * E);
+            v = NT ? __builtin_nontemporal_load(q) : *q;
+        }
+    } else if constexpr (LW == 8) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            if (ch * E + q * PE < w) {
+                const uint2 t = *reinterpret_cast<const uint2*>(row + ch * E + q * PE);
+                v[2 * q] = t.x;
+                v[2 * q + 1] = t.y;
+            }
+    } else if constexpr (LW == 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (ch * E + q * PE < w) v[q] = *reinterpret_cast<const uint32_t*>(row + ch * E + q * PE);
+    } else {
+        static_assert(LW == 2 && sizeof(T) == 2, "2-byte pieces are bf16 elements");
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (ch * E + q < w) v[q >> 1] |= (uint32_t)reinterpret_cast<const uint16_t*>(row)[ch * E + q] << (16 * (q & 1));
+    }
+    return v;
+}
+
+}  // namespace conv_fast
+}  // namespace nott
