@@ -164,6 +164,7 @@ CONV = [
     (4, 32, 8, 8, 32, 1, 1, 1, 0, 1),
     (1, 128, 8, 8, 64, 3, 3, 2, 1, 1),
     (2, 32, 40, 40, 256, 3, 3, 2, 1, 1),       # one channel chunk: the bf16 forward takes the tap kernel unsplit
+    (3, 3, 30, 26, 64, 7, 7, 2, 3, 1),         # stem forward kernel: odd output sizes, tiles across images
 ]
 
 

@@ -22,7 +22,7 @@ struct nott_ctx_s {
     void* ln_scratch = nullptr;    // this device's static LayerNorm scratch (nott_layernorm_bwd_noalloc)
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;
-    int conv_tap = 1;              // 0: NOTT_CONV_TAP=0 in the environment at nott_create (conv_tap.hip kernels off)
+    int conv_tap = 1;              // 0: NOTT_CONV_TAP=0 in the environment at nott_create (conv_tap.hip / conv_stem.hip kernels off)
     std::string last_error;
 };
 

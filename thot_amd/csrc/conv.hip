@@ -721,6 +721,9 @@ int fwd(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const voi
                                        static_cast<T*>(y), relu);
     if (cin1_applies(d))
         return cin1_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b, static_cast<T*>(y), relu);
+    if (nott::conv_fast::stem_fwd_applies(ctx, d))
+        return nott::conv_fast::stem_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b,
+                                            static_cast<T*>(y), relu);
     if (nott::conv_fast::tap_fwd_applies(ctx, d, sizeof(T)))
         return nott::conv_fast::tap_fwd<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(w), b,
                                            static_cast<T*>(y), relu);
@@ -757,6 +760,9 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         const bool aligned = ((uintptr_t)x % 16) == 0 && ((uintptr_t)dy % 16) == 0;
         if (aligned && nott::conv_fast::wgrad_applies(d, sizeof(T))) {
             st = nott::conv_fast::wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, accumulate);
+        } else if (nott::conv_fast::stem_wgrad_applies(ctx, d)) {
+            st = nott::conv_fast::stem_wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw,
+                                                accumulate);
         } else if (cin1_applies(d)) {
             // the bias gradient comes out of the same pass
             st = cin1_wgrad<T>(ctx, d, static_cast<const T*>(x), static_cast<const T*>(dy), dw, db, accumulate);

@@ -26,6 +26,15 @@ int tap_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, con
 template <typename T>
 int tap_dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* dx);
 
+// Forward of the 3-channel 7x7 column-stride-2 stem (conv_stem.hip).
+bool stem_fwd_applies(nott_ctx ctx, const nott_conv2d_desc* d);
+template <typename T>
+int stem_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu);
+
+bool stem_wgrad_applies(nott_ctx ctx, const nott_conv2d_desc* d);
+template <typename T>
+int stem_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate);
+
 // Widest load (bytes) that keeps every image row's pieces aligned.
 int wgrad_load_width(int64_t w, size_t elem);
 
