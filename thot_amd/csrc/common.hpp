@@ -200,10 +200,10 @@ template <> struct Pack16<bf16_t> {
     template <bool NT = false>
     static __device__ __forceinline__ void st(bf16_t* p, const float (&v)[8]) {
         u32x4 u;
-        u.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-        u.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
-        u.z = (uint32_t)f32_to_bf16(v[4]) | ((uint32_t)f32_to_bf16(v[5]) << 16);
-        u.w = (uint32_t)f32_to_bf16(v[6]) | ((uint32_t)f32_to_bf16(v[7]) << 16);
+        u.x = pack_bf16x2(v[0], v[1]);
+        u.y = pack_bf16x2(v[2], v[3]);
+        u.z = pack_bf16x2(v[4], v[5]);
+        u.w = pack_bf16x2(v[6], v[7]);
         u32x4* q = reinterpret_cast<u32x4*>(p);
         if (NT) __builtin_nontemporal_store(u, q);
         else *q = u;

@@ -69,13 +69,18 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
 // Row body: v holds this thread's EPT elements of row `row` (element e of
 // group g is column (g·NT + tid)·G + e; −inf past the end).  Writes the
 // gradient row and the row's loss.  Every thread calls it (block reductions).
+// One exponential per element: p = 2^(v·log2 e − max·log2 e) = e^(v − max)
+// is kept in v, and the gradient is scale·(p/Σp − ε/C − (1 − ε)·[j = y])
+// (the label's term applied once, by the thread that holds it); the row sum
+// of the logits is formed only when label smoothing needs it.
 template <typename T, int NT, int EPT, bool VEC>
-__device__ __forceinline__ void xent_row_body(const float (&v)[EPT], int64_t row, int64_t y, const T* __restrict__ z,
+__device__ __forceinline__ void xent_row_body(float (&v)[EPT], int64_t row, int64_t y, const T* __restrict__ z,
                                               int64_t c, float smoothing, float grad_scale, int nv,
                                               T* __restrict__ dz, float* __restrict__ row_loss, float* red) {
     constexpr int NWAVES = NT / 64;
     constexpr int G = VEC ? Pack16<T>::N : 1;
     constexpr int NG = EPT / G;
+    constexpr float kLog2e = 1.4426950408889634f;
     const int ci = (int)c;
     if (!(y >= 0 && y < c)) {
         // Ignored (or out-of-range) row: zero gradient, no loss.
@@ -99,17 +104,24 @@ __device__ __forceinline__ void xent_row_body(const float (&v)[EPT], int64_t row
 #pragma unroll
     for (int e = 0; e < EPT; ++e) mx = fmaxf(mx, v[e]);
     mx = block_max<NWAVES>(mx, red);
+    const float mxl = mx * kLog2e;
     float se = 0.f, sz = 0.f;
+    if (smoothing != 0.f) {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) sz += (v[e] == -INFINITY) ? 0.f : v[e];
+    }
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        se += __expf(v[e] - mx);
-        sz += (v[e] == -INFINITY) ? 0.f : v[e];
+        const float pe = __builtin_amdgcn_exp2f(fmaf(v[e], kLog2e, -mxl));
+        se += pe;
+        v[e] = pe;
     }
     block_sum2<NWAVES>(se, sz, red);
     const float lse = mx + __logf(se);
     const float scale = grad_scale / (float)nv;
     const float off = smoothing / (float)c;
     const float hit = 1.f - smoothing;
+    const float ga = scale / se, gb = -scale * off;
     const int yi = (int)y;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -117,8 +129,12 @@ __device__ __forceinline__ void xent_row_body(const float (&v)[EPT], int64_t row
         if (j0 >= ci) continue;
         float t[G];
 #pragma unroll
-        for (int e = 0; e < G; ++e)
-            t[e] = scale * (__expf(v[g * G + e] - lse) - off - (j0 + e == yi ? hit : 0.f));
+        for (int e = 0; e < G; ++e) t[e] = fmaf(v[g * G + e], ga, gb);
+        if ((unsigned)(yi - j0) < (unsigned)G) {
+#pragma unroll
+            for (int e = 0; e < G; ++e)
+                if (j0 + e == yi) t[e] -= scale * hit;
+        }
         if constexpr (VEC) Pack16<T>::template st<true>(dz + j0, t);
         else Io<T>::st(dz, j0, t[0]);
     }
