@@ -94,21 +94,38 @@ struct BnAct {
     const float* rstd;
 };
 
-// y = a·x + c used by the apply pass.
-template <typename T>
-__global__ void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict__ partial, int64_t c, int64_t splits,
-                                int64_t hw, int64_t m, const float* __restrict__ gamma, const float* __restrict__ beta,
-                                float eps, float momentum, float* __restrict__ running_mean,
-                                float* __restrict__ running_var, float* __restrict__ mean, float* __restrict__ rstd,
-                                float* __restrict__ coef) {
-    const int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (ch >= c) return;
-    const float pivot = Io<T>::ld(x, ch * hw);
-    double s1 = 0.0, s2 = 0.0;
-    for (int64_t s = 0; s < splits; ++s) {
+// Sum of the channel's split partials (pairs), one wave per channel: lanes
+// take splits s ≡ lane (mod 64) in order, then a fixed xor butterfly, so the
+// result does not depend on timing.
+__device__ __forceinline__ void wave_sum_partials(const float* __restrict__ partial, int64_t ch, int64_t splits,
+                                                  double& s1, double& s2) {
+    const int lane = threadIdx.x & 63;
+    s1 = 0.0;
+    s2 = 0.0;
+    for (int64_t s = lane; s < splits; s += 64) {
         s1 += partial[(ch * splits + s) * 2 + 0];
         s2 += partial[(ch * splits + s) * 2 + 1];
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        s1 += __shfl_xor(s1, o);
+        s2 += __shfl_xor(s2, o);
+    }
+}
+
+// y = a·x + c used by the apply pass.  One wave per channel.
+template <typename T>
+__global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict__ partial, int64_t c,
+                                                      int64_t splits, int64_t hw, int64_t m,
+                                                      const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                      float eps, float momentum, float* __restrict__ running_mean,
+                                                      float* __restrict__ running_var, float* __restrict__ mean,
+                                                      float* __restrict__ rstd, float* __restrict__ coef) {
+    const int64_t ch = blockIdx.x;
+    double s1, s2;
+    wave_sum_partials(partial, ch, splits, s1, s2);
+    if (threadIdx.x != 0) return;
+    const float pivot = Io<T>::ld(x, ch * hw);
     const double md = s1 / (double)m;
     double var = s2 / (double)m - md * md;
     if (var < 0.0) var = 0.0;
@@ -196,18 +213,16 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
     }
 }
 
-// dγ, dβ and the coefficients of dx = A·dy + B·x + C.
-__global__ void bn_bwd_finalize(const float* __restrict__ partial, int64_t c, int64_t splits, int64_t m,
-                                const float* __restrict__ mean, const float* __restrict__ rstd,
-                                const float* __restrict__ gamma, float* __restrict__ dgamma,
-                                float* __restrict__ dbeta, int accumulate, float* __restrict__ coef) {
-    const int64_t ch = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (ch >= c) return;
-    double sdy = 0.0, sdyxc = 0.0;
-    for (int64_t s = 0; s < splits; ++s) {
-        sdy += partial[(ch * splits + s) * 2 + 0];
-        sdyxc += partial[(ch * splits + s) * 2 + 1];
-    }
+// dγ, dβ and the coefficients of dx = A·dy + B·x + C.  One wave per channel.
+__global__ __launch_bounds__(64) void bn_bwd_finalize(const float* __restrict__ partial, int64_t c, int64_t splits,
+                                                      int64_t m, const float* __restrict__ mean,
+                                                      const float* __restrict__ rstd, const float* __restrict__ gamma,
+                                                      float* __restrict__ dgamma, float* __restrict__ dbeta,
+                                                      int accumulate, float* __restrict__ coef) {
+    const int64_t ch = blockIdx.x;
+    double sdy, sdyxc;
+    wave_sum_partials(partial, ch, splits, sdy, sdyxc);
+    if (threadIdx.x != 0) return;
     const double rs = rstd[ch], mu = mean[ch];
     const double sdyx = sdyxc * rs;  // Σ dy·x̂
     if (dgamma) dgamma[ch] = accumulate ? dgamma[ch] + (float)sdyx : (float)sdyx;
@@ -280,7 +295,7 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
         hipLaunchKernelGGL((bn_stats_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
     else
         hipLaunchKernelGGL((bn_stats_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
-    hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, x, partial,
+    hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial,
                        c, splits, hw, n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
     const int64_t total = n * c * hw;
     if (vec)
@@ -314,7 +329,7 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     else
         hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
                            per, partial, act);
-    hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, partial, c,
+    hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c,
                        splits, n * hw, mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
     if (dx) {
         const int64_t total = n * c * hw;
