@@ -165,6 +165,7 @@ CONV = [
     (1, 128, 8, 8, 64, 3, 3, 2, 1, 1),
     (2, 32, 40, 40, 256, 3, 3, 2, 1, 1),       # one channel chunk: the bf16 forward takes the tap kernel unsplit
     (3, 3, 30, 26, 64, 7, 7, 2, 3, 1),         # stem forward kernel: odd output sizes, tiles across images
+    (1, 16, 66, 70, 64, 3, 3, 1, 1, 1),        # tap weight gradient at stride 1 (rows wider than the 3x3 kernel's)
 ]
 
 
