@@ -16,6 +16,8 @@
 
 namespace {
 
+typedef long long i64x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 256;
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
@@ -201,8 +203,10 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
       const int64_t o = ((int64_t)pl * g.oh + oh0) * g.ow + j0;
       if constexpr (VEC) {
         Vec4<T>::st(y + o, yv);
-#pragma unroll
-        for (int e = 0; e < V; ++e) argmax[o + e] = av[e];
+        // o is a multiple of 4: two 16-byte index stores
+        i64x2* ap = reinterpret_cast<i64x2*>(argmax + o);
+        ap[0] = i64x2{av[0], av[1]};
+        ap[1] = i64x2{av[2], av[3]};
       } else {
         Io<T>::st(y, o, yv[0]);
         argmax[o] = av[0];
@@ -235,11 +239,10 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
     if constexpr (VEC) {
         for (int32_t i = threadIdx.x; i < nout / 4; i += kThreads) {
             const f32x4 d4 = Vec4<T>::ld(dy + obase + 4 * i);
-            int32_t c4[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) c4[e] = (int32_t)argmax[obase + 4 * i + e];
+            const i64x2* ap = reinterpret_cast<const i64x2*>(argmax + obase + 4 * i);   // 16-byte index loads
+            const i64x2 a01 = ap[0], a23 = ap[1];
             reinterpret_cast<f32x4*>(gv)[i] = d4;
-            reinterpret_cast<i32x4*>(code)[i] = i32x4{c4[0], c4[1], c4[2], c4[3]};
+            reinterpret_cast<i32x4*>(code)[i] = i32x4{(int32_t)a01.x, (int32_t)a01.y, (int32_t)a23.x, (int32_t)a23.y};
         }
     } else {
         for (int32_t i = threadIdx.x; i < nout; i += kThreads) {
@@ -365,7 +368,7 @@ extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     if (fits32(planes, g) && flds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kPoolRows), (unsigned)planes);
-        const bool vec = vec4_ok(g, dtype, {x, y});
+        const bool vec = vec4_ok(g, dtype, {x, y}) && ((uintptr_t)argmax % 16) == 0;
         if (dtype == NOTT_F32 && vec)
             hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), flds, ctx->stream,
                                static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
@@ -412,7 +415,7 @@ extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
     if (fits32(planes, g) && blds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.h, (int64_t)band_rows), (unsigned)planes);
-        const bool vec = vec4_ok(g, dtype, {dy, dx});
+        const bool vec = vec4_ok(g, dtype, {dy, dx}) && ((uintptr_t)argmax % 16) == 0;
         if (dtype == NOTT_F32 && vec)
             hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), blds, ctx->stream,
                                argmax, static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
