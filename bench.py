@@ -55,8 +55,8 @@ TRAFFIC = {
     ("ln_bwd", "bf16", "all"): 105.54e6,
     ("adamw", "f32", "all"): 2799.95e6,
     ("adamw", "bf16", "all"): 2200.00e6,
-    ("xent", "f32", "all"): 4199.41e6,         # xent_count_kernel + xent_rows_vec_kernel
-    ("xent", "bf16", "all"): 2101.29e6,
+    ("xent", "f32", "all"): 4200.27e6,         # xent_count_kernel + xent_rows_vec_kernel
+    ("xent", "bf16", "all"): 2101.67e6,
     ("mha_bwd", "bf16", "out_proj"): 194.04e6,   # dA GEMM + dW_o split GEMM + reduce
     ("mha_bwd", "bf16", "attention"): 241.85e6,  # attn_dq64 + attn_dkdv64
     ("mha_bwd", "bf16", "in_proj"): 480.57e6,    # dX GEMM + dW_qkv split GEMM + reduce
