@@ -823,8 +823,8 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dq64_kernel(const bf16_t* __r
                                                                  const bf16_t* __restrict__ o,
                                                                  const bf16_t* __restrict__ dO,
                                                                  const float* __restrict__ lse,
-                                                                 float* __restrict__ dsum, bf16_t* __restrict__ dq,
-                                                                 AttnParams p) {
+                                                                 float* __restrict__ dsum, float* __restrict__ lse2,
+                                                                 bf16_t* __restrict__ dq, AttnParams p) {
     constexpr int STAGE = 2 * TILE;
     extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
     char NOTT_LDS* smem = (char NOTT_LDS*)smem_raw;
@@ -894,15 +894,29 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dq64_kernel(const bf16_t* __r
                 dpt[f] = mfma(frag_rows(tv, 32 * f, s, lane), __builtin_bit_cast(bf16x8, dr[s]), dpt[f]);
             }
         }
-        const bool full = qw0 + 32 <= p.t && k0 + TR <= p.s && (!p.causal || k0 + TR - 1 <= qw0);
+        // exponent arguments (log2 domain) in place
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st[f][r] = fmaf(st[f][r], sl2, -my_lse2);
+        // Masking only on blocks that touch the diagonal or the end (a
+        // wave-uniform test).  Element (f, r) is key k0 + 4h + c with
+        // c = 32f + 8(r/4) + r%4 (0..59), kept iff c < rel: one compare against
+        // a constant, no per-element branches.
+        if (!(qw0 + 32 <= p.t && k0 + TR <= p.s && (!p.causal || k0 + TR - 1 <= qw0))) {
+            const int rel = q_in ? min(p.s, p.causal ? my_q + 1 : p.s) - k0 - 4 * h : -1;
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    if (!(32 * f + 8 * (r >> 2) + (r & 3) < rel)) st[f][r] = -INFINITY;
+        }
         float pmax = 0.f;
 #pragma unroll
         for (int f = 0; f < 2; ++f)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 32 * f + 8 * (r >> 2) + 4 * h + (r & 3);
-                const bool ok = full || (q_in && key < p.s && !(p.causal && key > my_q));
-                const float pe = ok ? __builtin_amdgcn_exp2f(st[f][r] * sl2 - my_lse2) : 0.f;
+                const float pe = __builtin_amdgcn_exp2f(st[f][r]);
                 d_exact += pe * dpt[f][r];
                 pmax = fmaxf(pmax, pe);
                 st[f][r] = pe;
@@ -931,7 +945,10 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dq64_kernel(const bf16_t* __r
     // Exact D of this lane's row (lanes l and l^32 hold the two key halves);
     // the dk/dv pass reads it.
     d_exact += __shfl_xor(d_exact, 32, 64);
-    if (h == 0 && q_in) dsum[(int64_t)bh * p.t + my_q] = d_exact;
+    if (h == 0 && q_in) {
+        dsum[(int64_t)bh * p.t + my_q] = d_exact;
+        lse2[(int64_t)bh * p.t + my_q] = my_lse2;
+    }
     const float corr = d_exact - my_d;
     // adq, abv: lane holds column d = 32·df + l%32, rows 8j + 4h + e of this
     // wave's 32 (row r's correction lives in lane r's column).
@@ -952,7 +969,7 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dkdv64_kernel(const bf16_t* _
                                                                    const bf16_t* __restrict__ k,
                                                                    const bf16_t* __restrict__ v,
                                                                    const bf16_t* __restrict__ dO,
-                                                                   const float* __restrict__ lse,
+                                                                   const float* __restrict__ lse2,
                                                                    const float* __restrict__ dsum,
                                                                    bf16_t* __restrict__ dk, bf16_t* __restrict__ dv,
                                                                    AttnParams p) {
@@ -968,7 +985,7 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dkdv64_kernel(const bf16_t* _
     const int64_t qoff = bh_off(bh, p.nh, p.sbq, p.shq), koff = bh_off(bh, p.nh, p.sbk, p.shk);
     const int64_t ooff = bh_off(bh, p.nh, p.sbo, p.sho);
     const float sl2 = p.scale * 1.4426950408889634f;
-    const float* lse_bh = lse + (int64_t)bh * p.t;
+    const float* lse_bh = lse2 + (int64_t)bh * p.t;   // lse·log2(e), written by the dq pass
     const float* d_bh = dsum + (int64_t)bh * p.t;
 
     u32x4 kr[4], vr[4];
@@ -1023,21 +1040,41 @@ __global__ __launch_bounds__(64 * NW, 2) void attn_dkdv64_kernel(const bf16_t* _
                 dp[f] = mfma(frag_rows(tdo, 32 * f, s, lane), __builtin_bit_cast(bf16x8, vr[s]), dp[f]);
             }
         }
-        const bool full = q0 + TR <= p.t && kw0 + 32 <= p.s && (!p.causal || kw0 + 31 <= q0);
+        // exponent arguments (log2 domain; the ring holds lse·log2(e)) in place
+#pragma unroll
+        for (int f = 0; f < 2; ++f)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 l4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(slse + 32 * f + 8 * j + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sc[f][4 * j + e] = fmaf(sc[f][4 * j + e], sl2, -l4[e]);
+            }
+        // Masking only on blocks that touch the diagonal or the end (a
+        // wave-uniform test).  Element (f, 4j + e) is query q0 + 4h + c with
+        // c = 32f + 8j + e (0..59), kept iff lo <= c < hi.
+        if (!(q0 + TR <= p.t && kw0 + 32 <= p.s && (!p.causal || kw0 + 31 <= q0))) {
+            const int hi = my_k < p.s ? p.t - q0 - 4 * h : -1;
+            const int lo = p.causal ? my_k - q0 - 4 * h : 0;
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int c = 32 * f + 8 * j + e;
+                        if (!((c >= lo) & (c < hi))) sc[f][4 * j + e] = -INFINITY;
+                    }
+        }
         float pmax = 0.f;
 #pragma unroll
         for (int f = 0; f < 2; ++f)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int ql = 32 * f + 8 * j + 4 * h;   // rows ql..ql+3 of the block
-                const f32x4 l4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(slse + ql);
-                const f32x4 d4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(sd + ql);
+                const f32x4 d4 = *reinterpret_cast<const f32x4 NOTT_LDS*>(sd + 32 * f + 8 * j + 4 * h);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int qrow = q0 + ql + e;
-                    const bool ok = full || (qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow));
                     const int r = 4 * j + e;
-                    const float pe = ok ? __builtin_amdgcn_exp2f(sc[f][r] * sl2 - l4[e] * 1.4426950408889634f) : 0.f;
+                    const float pe = __builtin_amdgcn_exp2f(sc[f][r]);
                     pmax = fmaxf(pmax, pe);
                     sc[f][r] = pe;
                     dp[f][r] = pe * (dp[f][r] - d4[e]);
@@ -1086,8 +1123,11 @@ bool applies(const nott_attn_desc* d, const AttnParams& p, int elem) { return el
 int bwd(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* q, const void* k, const void* v,
         const void* o, const void* dO, const float* lse, void* dq, void* dk, void* dv) {
     const int64_t rows = d->b * d->h * d->t;
-    float* dsum = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)std::max<int64_t>(rows, 1)));
+    // dsum (the exact rowsum(P∘dP)) and lse2 (lse·log2 e), both [b, h, t],
+    // handed from the dq pass to the dk/dv pass
+    float* dsum = static_cast<float*>(workspace(ctx, 2 * sizeof(float) * (size_t)std::max<int64_t>(rows, 1)));
     if (!dsum) return NOTT_ERR_ALLOC;
+    float* lse2 = dsum + std::max<int64_t>(rows, 1);
     const unsigned bh = (unsigned)(d->b * d->h);
     const size_t lds_q = RING * 2 * TILE, lds_kv = RING * (2 * TILE + 2 * TR * 4);
     static bool attr = false;
@@ -1103,9 +1143,9 @@ int bwd(nott_ctx ctx, const nott_attn_desc* d, const AttnParams& p, const void* 
     const auto* vb = static_cast<const bf16_t*>(v);
     const auto* dob = static_cast<const bf16_t*>(dO);
     hipLaunchKernelGGL(attn_dq64_kernel, dim3(bh, (unsigned)ceil_div(d->t, FIXED)), dim3(64 * NW), lds_q, ctx->stream,
-                       qb, kb, vb, static_cast<const bf16_t*>(o), dob, lse, dsum, static_cast<bf16_t*>(dq), p);
+                       qb, kb, vb, static_cast<const bf16_t*>(o), dob, lse, dsum, lse2, static_cast<bf16_t*>(dq), p);
     hipLaunchKernelGGL(attn_dkdv64_kernel, dim3(bh, (unsigned)ceil_div(d->s, FIXED)), dim3(64 * NW), lds_kv,
-                       ctx->stream, qb, kb, vb, dob, lse, dsum, static_cast<bf16_t*>(dk), static_cast<bf16_t*>(dv), p);
+                       ctx->stream, qb, kb, vb, dob, lse2, dsum, static_cast<bf16_t*>(dk), static_cast<bf16_t*>(dv), p);
     return launch_status(ctx, "attention_bwd");
 }
 
