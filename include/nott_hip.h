@@ -148,6 +148,16 @@ int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype
 /* dx[argmax] += dy, summed in output scan order for overlapping windows. */
 int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
                        const int64_t* argmax, const void* dy, void* dx);
+/* The same pair (the same torch::nn::MaxPool2d, pooling.hpp:132-149) with the
+ * argmax kept as the window tap, one byte per output:
+ *   tap = ((ih - oh*stride_h + pad_h) / dil_h) * kw + (iw - ow*stride_w + pad_w) / dil_w,
+ * for callers that keep the indices to themselves (the host models' MaxPool2d
+ * layers); 1/8 of the index traffic.  y and dx are bit-identical to the int64
+ * pair's.  Requires kh*kw <= 256. */
+int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                           const void* x, void* y, uint8_t* tap);
+int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                           const uint8_t* tap, const void* dy, void* dx);
 /* y[nc] = mean over hw; dx[nc, i] = dy[nc] / hw. */
 int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
                             const void* x, void* y);

@@ -293,9 +293,20 @@ struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
         const int64_t oh = out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, d.ceil_mode),
                       ow = out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, d.ceil_mode);
         Tensor y = torch::empty({d.n, d.c, oh, ow}, x.options());
-        Tensor idx = torch::empty({d.n, d.c, oh, ow}, x.options().dtype(torch::kInt64));
         nott_ctx c = bind(x);
-        check(nott_maxpool2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(y), idx.data_ptr<int64_t>()), c, "maxpool forward");
+        // The indices stay inside the layer, so windows of up to 256 taps keep
+        // them as one-byte window taps rather than ATen's int64 flat indices
+        // (the same routing, 1/8 of the index traffic).
+        Tensor idx;
+        if (d.kh * d.kw <= 256) {
+            idx = torch::empty({d.n, d.c, oh, ow}, x.options().dtype(torch::kUInt8));
+            check(nott_maxpool2d_fwd_tap(c, &d, dtype_of(x), ptr(x), ptr(y), idx.data_ptr<uint8_t>()), c,
+                  "maxpool forward");
+        } else {
+            idx = torch::empty({d.n, d.c, oh, ow}, x.options().dtype(torch::kInt64));
+            check(nott_maxpool2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(y), idx.data_ptr<int64_t>()), c,
+                  "maxpool forward");
+        }
         ctx->save_for_backward({idx});
         ctx->saved_data["geom"] = geom;
         ctx->saved_data["xshape"] = x.sizes().vec();
@@ -309,8 +320,12 @@ struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
         Tensor dx = torch::empty(xs, dy.options());
         const nott_pool2d_desc d = desc(dx, ctx->saved_data["geom"].toIntVector());
         nott_ctx c = bind(dy);
-        check(nott_maxpool2d_bwd(c, &d, dtype_of(dy), idx.data_ptr<int64_t>(), ptr(dy), ptr(dx)), c,
-              "maxpool backward");
+        if (idx.scalar_type() == torch::kUInt8)
+            check(nott_maxpool2d_bwd_tap(c, &d, dtype_of(dy), idx.data_ptr<uint8_t>(), ptr(dy), ptr(dx)), c,
+                  "maxpool backward");
+        else
+            check(nott_maxpool2d_bwd(c, &d, dtype_of(dy), idx.data_ptr<int64_t>(), ptr(dy), ptr(dx)), c,
+                  "maxpool backward");
         return {dx, Tensor()};
     }
 };

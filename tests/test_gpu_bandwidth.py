@@ -124,6 +124,11 @@ POOLS = [
     (2, 3, 24, 16, (3, 3), (1, 1), (1, 1), (1, 1), False),
     (3, 4, 16, 16, (2, 2), (2, 2), (0, 0), (1, 1), False),
     (2, 5, 40, 64, (3, 3), (2, 2), (1, 1), (1, 1), False),
+    # stride-2 kernels: odd height (last window cut by the image edge), several
+    # 32-row bands, 2x2 windows over several bands, wide rows
+    (2, 3, 35, 8, (3, 3), (2, 2), (1, 1), (1, 1), False),
+    (1, 2, 66, 24, (2, 2), (2, 2), (0, 0), (1, 1), False),
+    (1, 3, 23, 256, (3, 3), (2, 2), (1, 1), (1, 1), False),
 ]
 
 
@@ -144,6 +149,48 @@ def test_maxpool(ops, oracle, dt, case):
     dy = host_input(g.standard_normal(ye.shape), dt)
     dx = ops.maxpool2d_bwd(idx, dev(dy, dt), d)
     check(host(dx), oracle.maxpool2d_bwd(d, idxe, dy), dt, "maxpool dx")
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", POOLS)
+def test_maxpool_tap(ops, oracle, dt, case):
+    """The one-byte window-tap argmax (nott_maxpool2d_*_tap) names the same
+    inputs as the int64 flat index, and y / dx are bit-identical to the int64
+    pair's, NaN and -inf windows included."""
+    n, c, h, w, k, st, pd, dl, ceil = case
+    g = rng(h * w + c + 1)
+    x = np.maximum(g.standard_normal((n, c, h, w)), 0.0)
+    flat = x.reshape(-1)
+    flat[g.integers(0, flat.size, max(1, flat.size // 97))] = np.nan
+    flat[g.integers(0, flat.size, max(1, flat.size // 89))] = -np.inf
+    x = host_input(x, dt)
+    d = ops.pool_desc((n, c, h, w), k, st, pd, dl, ceil)
+    y, idx = ops.maxpool2d_fwd(dev(x, dt), d)
+    yt, tap = ops.maxpool2d_fwd_tap(dev(x, dt), d)
+    assert tap.dtype == torch.uint8
+    ye, idxe = oracle.maxpool2d_fwd(d, x)
+    assert np.array_equal(idx.cpu().numpy(), idxe), "argmax routing must be bit-exact (NaN / -inf windows)"
+    assert np.array_equal(host(y), ye, equal_nan=True)
+    assert torch.equal(y.view(torch.int16 if dt == "bf16" else torch.int32),
+                       yt.view(torch.int16 if dt == "bf16" else torch.int32))
+    oh, ow = y.shape[2], y.shape[3]
+    t = tap.cpu().numpy().astype(np.int64)
+    ohg = np.arange(oh).reshape(1, 1, oh, 1)
+    owg = np.arange(ow).reshape(1, 1, 1, ow)
+    decoded = (ohg * st[0] - pd[0] + (t // k[1]) * dl[0]) * w + (owg * st[1] - pd[1] + (t % k[1]) * dl[1])
+    assert np.array_equal(decoded, idx.cpu().numpy()), "tap and flat index must name the same input"
+    dy = dev(host_input(g.standard_normal(y.shape), dt), dt)
+    dx = ops.maxpool2d_bwd(idx, dy, d)
+    dxt = ops.maxpool2d_bwd_tap(tap, dy, d)
+    check(host(dx), oracle.maxpool2d_bwd(d, idxe, host(dy)), dt, "maxpool dx")
+    assert torch.equal(dx.view(torch.int16 if dt == "bf16" else torch.int32),
+                       dxt.view(torch.int16 if dt == "bf16" else torch.int32))
+
+
+def test_maxpool_tap_rejects_large_windows(ops):
+    d = ops.pool_desc((1, 1, 40, 40), (17, 17), (1, 1), (0, 0), (1, 1), False)
+    with pytest.raises(RuntimeError, match="256 taps"):
+        ops.maxpool2d_fwd_tap(torch.zeros((1, 1, 40, 40), device="cuda"), d)
 
 
 @pytest.mark.parametrize("dt", DTYPES)

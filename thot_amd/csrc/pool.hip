@@ -1,11 +1,15 @@
-// MaxPool2d forward (values + int64 argmax) and backward (argmax routing), NCHW.
+// MaxPool2d forward (values + argmax) and backward (argmax routing), NCHW.
 //
 // Replaces torch::nn::MaxPool2d built by build_registered_layer(Owner&, const
 // PoolingDescriptor&, size_t) (reference layer/details/pooling.hpp:132-149),
 // i.e. ATen max_pool2d_with_indices and its backward.
 //   forward : window scan rows-then-columns from the first in-bounds tap; the
 //             index moves on a strictly greater value or on a NaN; argmax is
-//             the flat index ih·w + iw inside the (n, c) plane.
+//             the flat index ih·w + iw inside the (n, c) plane (int64, ATen's
+//             form), or the window tap ((ih − oh·sh + ph)/dh)·kw +
+//             (iw − ow·sw + pw)/dw as one byte (the _tap entry points, for
+//             callers that keep the indices to themselves; the backward turns
+//             a tap back into the flat index, so both forms route identically).
 //   backward: dx[argmax] += dy.  Computed as a gather: each input element
 //             sums the dy of the windows that cover it and chose it, in
 //             output scan order, so overlapping windows need no atomics and
@@ -25,9 +29,31 @@ struct PoolGeom {
     int64_t h, w, oh, ow, kh, kw, sh, sw, ph, pw, dh, dw;
 };
 
-template <typename T>
+// Argmax of output (oh, ow) whose maximum is input (bh, bw), stored as IX:
+// int64_t = the flat index, uint8_t = the window tap.
+template <typename IX, typename I, typename G>
+__device__ __forceinline__ IX encode_ix(I bh, I bw, I oh, I ow, const G& g) {
+    if constexpr (sizeof(IX) == 8) {
+        return (IX)(bh * g.w + bw);
+    } else {
+        const I th = bh - (oh * g.sh - g.ph), tw = bw - (ow * g.sw - g.pw);
+        return (IX)((g.dh == 1 ? th : th / g.dh) * g.kw + (g.dw == 1 ? tw : tw / g.dw));
+    }
+}
+// The flat in-plane index a stored argmax of output (oh, ow) names.
+template <typename I, typename IX, typename G>
+__device__ __forceinline__ I decode_ix(IX code, I oh, I ow, const G& g) {
+    if constexpr (sizeof(IX) == 8) {
+        return (I)code;
+    } else {
+        const I t = (I)code, th = t / g.kw, tw = t - th * g.kw;
+        return (oh * g.sh - g.ph + th * g.dh) * g.w + (ow * g.sw - g.pw + tw * g.dw);
+    }
+}
+
+template <typename T, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(const T* __restrict__ x, T* __restrict__ y,
-                                                               int64_t* __restrict__ argmax, int64_t planes,
+                                                               IX* __restrict__ argmax, int64_t planes,
                                                                PoolGeom g) {
     const int64_t o = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     const int64_t per_plane = g.oh * g.ow;
@@ -41,22 +67,23 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel(const T* __restri
     const int64_t iw1 = std::min<int64_t>(iw0 + (g.kw - 1) * g.dw + 1, g.w);
     while (ih0 < 0) ih0 += g.dh;
     while (iw0 < 0) iw0 += g.dw;
-    int64_t best = ih0 * g.w + iw0;
+    int64_t bh = ih0, bw = iw0;
     float bv = -INFINITY;
     for (int64_t ih = ih0; ih < ih1; ih += g.dh)
         for (int64_t iw = iw0; iw < iw1; iw += g.dw) {
             const float v = Io<T>::ld(xp, ih * g.w + iw);
             if (v > bv || v != v) {
                 bv = v;
-                best = ih * g.w + iw;
+                bh = ih;
+                bw = iw;
             }
         }
     Io<T>::st(y, o, bv);
-    argmax[o] = best;
+    argmax[o] = encode_ix<IX>(bh, bw, oh, ow, g);
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(const int64_t* __restrict__ argmax,
+template <typename T, typename IX>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(const IX* __restrict__ argmax,
                                                                const T* __restrict__ dy, T* __restrict__ dx,
                                                                int64_t planes, PoolGeom g) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -72,13 +99,13 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel(const int64_t* __
     const int64_t num_w = iw + g.pw - (g.kw - 1) * g.dw;
     int64_t ow0 = num_w <= 0 ? 0 : (num_w + g.sw - 1) / g.sw;
     int64_t ow1 = std::min<int64_t>((iw + g.pw) / g.sw, g.ow - 1);
-    const int64_t* ap = argmax + pl * g.oh * g.ow;
+    const IX* ap = argmax + pl * g.oh * g.ow;
     const T* gp = dy + pl * g.oh * g.ow;
     float acc = 0.f;
     for (int64_t oh = oh0; oh <= oh1; ++oh)
         for (int64_t ow = ow0; ow <= ow1; ++ow) {
             const int64_t o = oh * g.ow + ow;
-            if (ap[o] == idx) acc += Io<T>::ld(gp, o);
+            if (decode_ix<int64_t>(ap[o], oh, ow, g) == idx) acc += Io<T>::ld(gp, o);
         }
     Io<T>::st(dx, i, acc);
 }
@@ -90,9 +117,9 @@ struct PoolGeom32 {
     FastDiv fd_out_plane, fd_ow, fd_in_plane, fd_w, fd_sh, fd_sw;
 };
 
-template <typename T>
+template <typename T, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel32(const T* __restrict__ x, T* __restrict__ y,
-                                                                 int64_t* __restrict__ argmax, uint32_t total,
+                                                                 IX* __restrict__ argmax, uint32_t total,
                                                                  PoolGeom32 g) {
     const uint32_t o = blockIdx.x * kThreads + threadIdx.x;
     if (o >= total) return;
@@ -105,22 +132,23 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_kernel32(const T* __rest
     const int32_t iw1 = min(iw0 + (g.kw - 1) * g.dw + 1, g.w);
     while (ih0 < 0) ih0 += g.dh;
     while (iw0 < 0) iw0 += g.dw;
-    int32_t best = ih0 * g.w + iw0;
+    int32_t bh = ih0, bw = iw0;
     float bv = -INFINITY;
     for (int32_t ih = ih0; ih < ih1; ih += g.dh)
         for (int32_t iw = iw0; iw < iw1; iw += g.dw) {
             const float v = Io<T>::ld(xp, ih * g.w + iw);
             if (v > bv || v != v) {
                 bv = v;
-                best = ih * g.w + iw;
+                bh = ih;
+                bw = iw;
             }
         }
     Io<T>::st(y, o, bv);
-    argmax[o] = best;
+    argmax[o] = encode_ix<IX>(bh, bw, (int32_t)oh, (int32_t)ow, g);
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* __restrict__ argmax,
+template <typename T, typename IX>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const IX* __restrict__ argmax,
                                                                  const T* __restrict__ dy, T* __restrict__ dx,
                                                                  uint32_t total, PoolGeom32 g) {
     const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
@@ -135,13 +163,13 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* 
     const int32_t num_w = (int32_t)iw + g.pw - (g.kw - 1) * g.dw;
     const int32_t ow0 = num_w <= 0 ? 0 : (int32_t)g.fd_sw.div((uint32_t)(num_w + g.sw - 1));
     const int32_t ow1 = min((int32_t)g.fd_sw.div(iw + (uint32_t)g.pw), g.ow - 1);
-    const int64_t* ap = argmax + (int64_t)pl * g.oh * g.ow;
+    const IX* ap = argmax + (int64_t)pl * g.oh * g.ow;
     const T* gp = dy + (int64_t)pl * g.oh * g.ow;
     float acc = 0.f;
     for (int32_t oh = oh0; oh <= oh1; ++oh)
         for (int32_t ow = ow0; ow <= ow1; ++ow) {
             const int32_t o = oh * g.ow + ow;
-            if (ap[o] == (int64_t)idx) acc += Io<T>::ld(gp, o);
+            if (decode_ix<int64_t>(ap[o], (int64_t)oh, (int64_t)ow, g) == (int64_t)idx) acc += Io<T>::ld(gp, o);
         }
     Io<T>::st(dx, i, acc);
 }
@@ -152,9 +180,9 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_kernel32(const int64_t* 
 // float), then every output scans its window from LDS in the same order and
 // with the same NaN / first-maximum rule as the untiled kernel.
 constexpr int kPoolRows = 8;
-template <typename T, bool VEC>
+template <typename T, bool VEC, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __restrict__ x, T* __restrict__ y,
-                                                                     int64_t* __restrict__ argmax, PoolGeom32 g) {
+                                                                     IX* __restrict__ argmax, PoolGeom32 g) {
     // VEC (w and ow multiples of 4, aligned buffers): 4 consecutive elements
     // per thread for the staging loads and for the y / argmax stores.
     constexpr int V = VEC ? 4 : 1;
@@ -175,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
     const int32_t nout = (oh1 - oh0) * g.ow;
     for (int32_t j0 = threadIdx.x * V; j0 < nout; j0 += kThreads * V) {
       f32x4 yv;
-      int64_t av[V];
+      IX av[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) {
         const int32_t j = j0 + e;
@@ -187,26 +215,33 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
         const int32_t iw1 = min(iw0 + (g.kw - 1) * g.dw + 1, g.w);
         while (ih0 < 0) ih0 += g.dh;
         while (iw0 < 0) iw0 += g.dw;
-        int32_t best = ih0 * g.w + iw0;
+        int32_t bh = ih0, bw = iw0;
         float bv = -INFINITY;
         for (int32_t ih = ih0; ih < ih1; ih += g.dh)
             for (int32_t iw = iw0; iw < iw1; iw += g.dw) {
                 const float v = rows[(ih - ih_lo) * g.w + iw];
                 if (v > bv || v != v) {
                     bv = v;
-                    best = ih * g.w + iw;
+                    bh = ih;
+                    bw = iw;
                 }
             }
         yv[e] = bv;
-        av[e] = best;
+        av[e] = encode_ix<IX>(bh, bw, oh, ow, g);
       }
       const int64_t o = ((int64_t)pl * g.oh + oh0) * g.ow + j0;
       if constexpr (VEC) {
         Vec4<T>::st(y + o, yv);
-        // o is a multiple of 4: two 16-byte index stores
-        i64x2* ap = reinterpret_cast<i64x2*>(argmax + o);
-        ap[0] = i64x2{av[0], av[1]};
-        ap[1] = i64x2{av[2], av[3]};
+        if constexpr (sizeof(IX) == 8) {
+            // o is a multiple of 4: two 16-byte index stores
+            i64x2* ap = reinterpret_cast<i64x2*>(argmax + o);
+            ap[0] = i64x2{av[0], av[1]};
+            ap[1] = i64x2{av[2], av[3]};
+        } else {
+            // four taps in one 4-byte store
+            *reinterpret_cast<uint32_t*>(argmax + o) =
+                (uint32_t)av[0] | ((uint32_t)av[1] << 8) | ((uint32_t)av[2] << 16) | ((uint32_t)av[3] << 24);
+        }
       } else {
         Io<T>::st(y, o, yv[0]);
         argmax[o] = av[0];
@@ -219,8 +254,8 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
 // reaches the band in LDS, then each input gathers from the outputs that can
 // cover it, in the untiled kernel's order (oh, then ow, ascending): the same
 // sums, bit for bit, with each argmax read from HBM about once.
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64_t* __restrict__ argmax,
+template <typename T, bool VEC, typename IX>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const IX* __restrict__ argmax,
                                                                      const T* __restrict__ dy, T* __restrict__ dx,
                                                                      PoolGeom32 g, int32_t band_rows) {
     // VEC (w and ow multiples of 4, aligned buffers): 4 consecutive elements
@@ -236,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
     int32_t* code = reinterpret_cast<int32_t*>(sm);
     float* gv = reinterpret_cast<float*>(sm) + nout;
     const int64_t obase = (int64_t)pl * g.oh * g.ow + (int64_t)oh_lo * g.ow;
-    if constexpr (VEC) {
+    if constexpr (VEC && sizeof(IX) == 8) {
         for (int32_t i = threadIdx.x; i < nout / 4; i += kThreads) {
             const f32x4 d4 = Vec4<T>::ld(dy + obase + 4 * i);
             const i64x2* ap = reinterpret_cast<const i64x2*>(argmax + obase + 4 * i);   // 16-byte index loads
@@ -244,9 +279,25 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
             reinterpret_cast<f32x4*>(gv)[i] = d4;
             reinterpret_cast<i32x4*>(code)[i] = i32x4{(int32_t)a01.x, (int32_t)a01.y, (int32_t)a23.x, (int32_t)a23.y};
         }
+    } else if constexpr (VEC) {
+        // four taps per 4-byte load, staged as flat indices
+        for (int32_t i = threadIdx.x; i < nout / 4; i += kThreads) {
+            const f32x4 d4 = Vec4<T>::ld(dy + obase + 4 * i);
+            const uint32_t t4 = *reinterpret_cast<const uint32_t*>(argmax + obase + 4 * i);
+            uint32_t ohl, owu;
+            g.fd_ow.divmod((uint32_t)(4 * i), ohl, owu);   // ow is a multiple of 4: one output row
+            const int32_t oh = oh_lo + (int32_t)ohl, ow = (int32_t)owu;
+            reinterpret_cast<f32x4*>(gv)[i] = d4;
+            reinterpret_cast<i32x4*>(code)[i] =
+                i32x4{decode_ix<int32_t>((uint8_t)t4, oh, ow, g), decode_ix<int32_t>((uint8_t)(t4 >> 8), oh, ow + 1, g),
+                      decode_ix<int32_t>((uint8_t)(t4 >> 16), oh, ow + 2, g),
+                      decode_ix<int32_t>((uint8_t)(t4 >> 24), oh, ow + 3, g)};
+        }
     } else {
         for (int32_t i = threadIdx.x; i < nout; i += kThreads) {
-            code[i] = (int32_t)argmax[obase + i];
+            uint32_t ohl, owu;
+            g.fd_ow.divmod((uint32_t)i, ohl, owu);
+            code[i] = decode_ix<int32_t>(argmax[obase + i], oh_lo + (int32_t)ohl, (int32_t)owu, g);
             gv[i] = Io<T>::ld(dy, obase + i);
         }
     }
@@ -278,6 +329,173 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const int64
       const int64_t di = (int64_t)pl * g.h * g.w + (int64_t)ih_lo * g.w + j0;
       if constexpr (VEC) Vec4<T>::st(dx + di, out);
       else Io<T>::st(dx, di, out[0]);
+    }
+}
+
+// Stride-2, dilation-1, K×K windows with pad P ((K, P) = (3, 1), the
+// ResNet-18 stem pool, or (2, 0)), image and output rows of whole 4-element
+// groups.  The window geometry is compile-time: the scans unroll, and every
+// division by the stride is a shift.
+//
+// Forward: workgroup = band of kS2Rows output rows of one plane.  The input
+// rows the band's windows touch are staged in LDS as fp32 split by column
+// parity (even columns, then odd columns, each half 16-byte aligned), so a
+// thread's 4 consecutive outputs read each window row as one 16-byte run of
+// even and one of odd columns (conflict-free), plus the odd column before
+// them when K = 3.  Windows are scanned rows then columns from the first
+// in-bounds tap with the generic kernels' rule (strictly greater, or NaN).
+constexpr int kS2Rows = 16;
+template <typename T, int K, int P, typename IX>
+__global__ __launch_bounds__(kThreads) void maxpool_fwd_s2_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                                  IX* __restrict__ argmax, PoolGeom32 g,
+                                                                  int32_t half_pitch) {
+    static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "window");
+    extern __shared__ float rows[];   // [row][even columns | odd columns], 2·half_pitch floats a row
+    const int32_t pl = blockIdx.y;
+    const int32_t oh0 = blockIdx.x * kS2Rows, oh1 = min(oh0 + kS2Rows, g.oh);
+    const int32_t ih_lo = max(0, 2 * oh0 - P);
+    const int32_t ih_hi = min(g.h, 2 * (oh1 - 1) - P + K);   // exclusive
+    const T* xp = x + (int64_t)pl * g.h * g.w;
+    const int32_t nq = (ih_hi - ih_lo) * (g.w >> 2);
+    for (int32_t i = threadIdx.x; i < nq; i += kThreads) {
+        uint32_t r, c;
+        g.fd_w.divmod((uint32_t)(4 * i), r, c);
+        const f32x4 v = Vec4<T>::ld(xp + (int64_t)(ih_lo + (int32_t)r) * g.w + c);
+        float* row = rows + r * 2 * half_pitch + (c >> 1);
+        *reinterpret_cast<f32x2*>(row) = f32x2{v.x, v.z};
+        *reinterpret_cast<f32x2*>(row + half_pitch) = f32x2{v.y, v.w};
+    }
+    __syncthreads();
+    const int32_t ntask = (oh1 - oh0) * (g.ow >> 2);
+    for (int32_t i = threadIdx.x; i < ntask; i += kThreads) {
+        uint32_t orow, owu;
+        g.fd_ow.divmod((uint32_t)(4 * i), orow, owu);
+        const int32_t oh = oh0 + (int32_t)orow, ow0 = (int32_t)owu;
+        float bv[4];
+        int32_t bh[4], bw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            bv[e] = -INFINITY;
+            bh[e] = max(2 * oh - P, 0);
+            bw[e] = max(2 * (ow0 + e) - P, 0);
+        }
+#pragma unroll
+        for (int ky = 0; ky < K; ++ky) {
+            const int32_t ih = 2 * oh - P + ky;
+            if (ih < 0 || ih >= g.h) continue;
+            const float* er = rows + (ih - ih_lo) * 2 * half_pitch;
+            const f32x4 ev = *reinterpret_cast<const f32x4*>(er + ow0);
+            const f32x4 od = *reinterpret_cast<const f32x4*>(er + half_pitch + ow0);
+            const float od_m1 = (K == 3 && ow0 > 0) ? er[half_pitch + ow0 - 1] : -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int kx = 0; kx < K; ++kx) {
+                    // iw = 2·ow − P + kx: K = 3: odd[ow−1], even[ow], odd[ow]; K = 2: even[ow], odd[ow]
+                    const int32_t iw = 2 * (ow0 + e) - P + kx;
+                    if (iw < 0 || iw >= g.w) continue;
+                    float v;
+                    if constexpr (K == 3)
+                        v = kx == 1 ? ev[e] : kx == 2 ? od[e] : (e == 0 ? od_m1 : od[e - 1]);
+                    else
+                        v = kx == 0 ? ev[e] : od[e];
+                    if (v > bv[e] || v != v) {
+                        bv[e] = v;
+                        bh[e] = ih;
+                        bw[e] = iw;
+                    }
+                }
+        }
+        const int64_t o = ((int64_t)pl * g.oh + oh) * g.ow + ow0;
+        Vec4<T>::st(y + o, f32x4{bv[0], bv[1], bv[2], bv[3]});
+        IX av[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) av[e] = encode_ix<IX>(bh[e], bw[e], oh, ow0 + e, g);
+        if constexpr (sizeof(IX) == 8) {
+            i64x2* ap = reinterpret_cast<i64x2*>(argmax + o);
+            ap[0] = i64x2{av[0], av[1]};
+            ap[1] = i64x2{av[2], av[3]};
+        } else {
+            *reinterpret_cast<uint32_t*>(argmax + o) =
+                (uint32_t)av[0] | ((uint32_t)av[1] << 8) | ((uint32_t)av[2] << 16) | ((uint32_t)av[3] << 24);
+        }
+    }
+}
+
+// Backward of the same windows: workgroup = band of 2·kS2Rows input rows of
+// one plane.  The dy and the argmax (as flat in-plane indices) of the output
+// rows whose windows reach the band are staged in LDS.  Inputs 4q..4q+3 of
+// row ih can only have been chosen by outputs 2q .. 2q+K−1 (fewer at the
+// right edge) of output rows ceil((ih+P−K+1)/2) .. floor((ih+P)/2); a thread
+// reads those as short runs and adds the matching dy in (oh, ow) order, the
+// generic kernels' order, so the sums are the same bit for bit.
+template <typename T, int K, int P, typename IX>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_s2_kernel(const IX* __restrict__ argmax,
+                                                                  const T* __restrict__ dy, T* __restrict__ dx,
+                                                                  PoolGeom32 g) {
+    static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "window");
+    constexpr int NC = K;   // candidate output columns of a 4-input group: 2q .. 2q + K − 1 (K ≤ 3)
+    extern __shared__ char sm[];
+    const int32_t pl = blockIdx.y;
+    const int32_t ih_lo = blockIdx.x * 2 * kS2Rows, ih_hi = min(ih_lo + 2 * kS2Rows, g.h);
+    const int32_t oh_lo = max(0, (ih_lo + P - K + 2) >> 1);          // ceil((ih_lo + P − K + 1) / 2)
+    const int32_t oh_hi = min(g.oh - 1, (ih_hi - 1 + P) >> 1);       // floor((ih_hi − 1 + P) / 2)
+    const int32_t nor = oh_hi - oh_lo + 1;
+    int32_t* code = reinterpret_cast<int32_t*>(sm);
+    float* gv = reinterpret_cast<float*>(sm) + (nor > 0 ? nor : 0) * g.ow;
+    const int64_t obase = (int64_t)pl * g.oh * g.ow + (int64_t)oh_lo * g.ow;
+    const int32_t nout4 = nor > 0 ? nor * (g.ow >> 2) : 0;
+    for (int32_t i = threadIdx.x; i < nout4; i += kThreads) {
+        uint32_t orow, owu;
+        g.fd_ow.divmod((uint32_t)(4 * i), orow, owu);
+        const int32_t oh = oh_lo + (int32_t)orow, ow = (int32_t)owu;
+        const f32x4 d4 = Vec4<T>::ld(dy + obase + 4 * i);
+        i32x4 c4;
+        if constexpr (sizeof(IX) == 8) {
+            const i64x2* ap = reinterpret_cast<const i64x2*>(argmax + obase + 4 * i);
+            const i64x2 a01 = ap[0], a23 = ap[1];
+            c4 = i32x4{(int32_t)a01.x, (int32_t)a01.y, (int32_t)a23.x, (int32_t)a23.y};
+        } else {
+            const uint32_t t4 = *reinterpret_cast<const uint32_t*>(argmax + obase + 4 * i);
+            c4 = i32x4{decode_ix<int32_t>((uint8_t)t4, oh, ow, g), decode_ix<int32_t>((uint8_t)(t4 >> 8), oh, ow + 1, g),
+                       decode_ix<int32_t>((uint8_t)(t4 >> 16), oh, ow + 2, g),
+                       decode_ix<int32_t>((uint8_t)(t4 >> 24), oh, ow + 3, g)};
+        }
+        reinterpret_cast<f32x4*>(gv)[i] = d4;
+        reinterpret_cast<i32x4*>(code)[i] = c4;
+    }
+    __syncthreads();
+    const int32_t ntask = (ih_hi - ih_lo) * (g.w >> 2);
+    for (int32_t i = threadIdx.x; i < ntask; i += kThreads) {
+        uint32_t rr, iwu;
+        g.fd_w.divmod((uint32_t)(4 * i), rr, iwu);
+        const int32_t ih = ih_lo + (int32_t)rr, iw0 = (int32_t)iwu, q2 = iw0 >> 1;
+        const int32_t oa = max(0, (ih + P - K + 2) >> 1), ob = min(g.oh - 1, (ih + P) >> 1);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dr = 0; dr < 2; ++dr) {
+            const int32_t oh = oa + dr;
+            if (oh > ob) break;
+            const int32_t* cr = code + (oh - oh_lo) * g.ow + q2;
+            const float* gr = gv + (oh - oh_lo) * g.ow + q2;
+            int32_t cc[NC];
+            float gg[NC];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const bool in = q2 + j < g.ow;
+                cc[j] = in ? cr[j] : -1;
+                gg[j] = in ? gr[j] : 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int32_t idx = ih * g.w + iw0 + e;
+#pragma unroll
+                for (int j = 0; j < NC; ++j)
+                    // output 2q + j's window columns are 4q + 2j − P .. 4q + 2j − P + K − 1
+                    if (2 * j - P <= e && e <= 2 * j - P + K - 1 && cc[j] == idx) acc[e] += gg[j];
+            }
+        }
+        Vec4<T>::st(dx + (int64_t)pl * g.h * g.w + (int64_t)ih * g.w + iw0, f32x4{acc[0], acc[1], acc[2], acc[3]});
     }
 }
 
@@ -352,95 +570,188 @@ int check_desc(nott_ctx ctx, const nott_pool2d_desc* d, PoolGeom* g) {
 
 }  // namespace
 
-extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x, void* y,
-                                  int64_t* argmax) {
+namespace {
+
+// Index alignment the 4-element tiled paths need: two 16-byte stores / loads
+// of int64 indices, or one 4-byte word of taps.
+template <typename IX>
+constexpr uintptr_t ix_align() { return sizeof(IX) == 8 ? 16 : 4; }
+
+// The stride-2 kernels' windows: 3×3 pad 1 or 2×2 pad 0, stride 2, dilation 1.
+bool s2_geom(const PoolGeom& g) {
+    return g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 && g.kh == g.kw && g.ph == g.pw &&
+           ((g.kh == 3 && g.ph == 1) || (g.kh == 2 && g.ph == 0));
+}
+// Half row pitch (floats) of the forward's parity-split rows, and the LDS
+// bytes of the two kernels (4 floats of slack past the last row).
+int32_t s2_half_pitch(const PoolGeom& g) { return (int32_t)((g.w / 2 + 3) / 4 * 4); }
+size_t s2_fwd_lds(const PoolGeom& g) {
+    return sizeof(float) * ((size_t)std::min<int64_t>(g.h, 2 * kS2Rows + g.kh - 2) * 2 * s2_half_pitch(g) + 4);
+}
+size_t s2_bwd_lds(const PoolGeom& g) {
+    return 2 * sizeof(float) * ((size_t)std::min<int64_t>(g.oh, kS2Rows + 2) * g.ow + 4);
+}
+
+template <typename IX>
+int maxpool_fwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x, void* y, IX* argmax,
+                     const char* name) {
     NOTT_CHECK_CTX(ctx);
-    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_maxpool2d_fwd: bad dtype");
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), std::string(name) + ": bad dtype");
     PoolGeom g;
     int st = check_desc(ctx, d, &g);
     if (st != NOTT_OK) return st;
+    if (sizeof(IX) == 1)
+        NOTT_REQUIRE(ctx, g.kh * g.kw <= 256, std::string(name) + ": a window of more than 256 taps needs int64 indices");
     const int64_t planes = d->n * d->c, total = planes * g.oh * g.ow;
     if (total == 0) return NOTT_OK;
-    NOTT_REQUIRE(ctx, x && y && argmax, "nott_maxpool2d_fwd: null buffer");
+    NOTT_REQUIRE(ctx, x && y && argmax, std::string(name) + ": null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
     const size_t flds = pool_fwd_lds(g);
-    if (fits32(planes, g) && flds > 0 && planes <= 65535) {
+    const auto* xf = static_cast<const float*>(x);
+    const auto* xb = static_cast<const bf16_t*>(x);
+    auto* yf = static_cast<float*>(y);
+    auto* yb = static_cast<bf16_t*>(y);
+    if (fits32(planes, g) && planes <= 65535 && s2_geom(g) && vec4_ok(g, dtype, {x, y}) &&
+        ((uintptr_t)argmax % ix_align<IX>()) == 0 && s2_fwd_lds(g) <= kPoolLdsMax) {
+        const PoolGeom32 g32 = geom32(g);
+        const dim3 sgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kS2Rows), (unsigned)planes);
+        const size_t lds = s2_fwd_lds(g);
+        const int32_t hp = s2_half_pitch(g);
+        if (g.kh == 3 && dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_fwd_s2_kernel<float, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xf, yf,
+                               argmax, g32, hp);
+        else if (g.kh == 3)
+            hipLaunchKernelGGL((maxpool_fwd_s2_kernel<bf16_t, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xb,
+                               yb, argmax, g32, hp);
+        else if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_fwd_s2_kernel<float, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xf, yf,
+                               argmax, g32, hp);
+        else
+            hipLaunchKernelGGL((maxpool_fwd_s2_kernel<bf16_t, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xb,
+                               yb, argmax, g32, hp);
+    } else if (fits32(planes, g) && flds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kPoolRows), (unsigned)planes);
-        const bool vec = vec4_ok(g, dtype, {x, y}) && ((uintptr_t)argmax % 16) == 0;
+        const bool vec = vec4_ok(g, dtype, {x, y}) && ((uintptr_t)argmax % ix_align<IX>()) == 0;
         if (dtype == NOTT_F32 && vec)
-            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), flds, ctx->stream,
-                               static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, true, IX>), tgrid, dim3(kThreads), flds, ctx->stream, xf,
+                               yf, argmax, g32);
         else if (dtype == NOTT_F32)
-            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, false>), tgrid, dim3(kThreads), flds, ctx->stream,
-                               static_cast<const float*>(x), static_cast<float*>(y), argmax, g32);
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<float, false, IX>), tgrid, dim3(kThreads), flds, ctx->stream,
+                               xf, yf, argmax, g32);
         else if (vec)
-            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, true>), tgrid, dim3(kThreads), flds, ctx->stream,
-                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, g32);
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, true, IX>), tgrid, dim3(kThreads), flds, ctx->stream,
+                               xb, yb, argmax, g32);
         else
-            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, false>), tgrid, dim3(kThreads), flds, ctx->stream,
-                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, g32);
+            hipLaunchKernelGGL((maxpool_fwd_tiled_kernel<bf16_t, false, IX>), tgrid, dim3(kThreads), flds, ctx->stream,
+                               xb, yb, argmax, g32);
     } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
         if (dtype == NOTT_F32)
-            hipLaunchKernelGGL(maxpool_fwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream,
-                               static_cast<const float*>(x), static_cast<float*>(y), argmax, (uint32_t)total, g32);
+            hipLaunchKernelGGL((maxpool_fwd_kernel32<float, IX>), grid, dim3(kThreads), 0, ctx->stream, xf, yf, argmax,
+                               (uint32_t)total, g32);
         else
-            hipLaunchKernelGGL(maxpool_fwd_kernel32<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
-                               static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, (uint32_t)total, g32);
+            hipLaunchKernelGGL((maxpool_fwd_kernel32<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, xb, yb, argmax,
+                               (uint32_t)total, g32);
     } else if (dtype == NOTT_F32)
-        hipLaunchKernelGGL(maxpool_fwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream,
-                           static_cast<const float*>(x), static_cast<float*>(y), argmax, planes, g);
+        hipLaunchKernelGGL((maxpool_fwd_kernel<float, IX>), grid, dim3(kThreads), 0, ctx->stream, xf, yf, argmax, planes,
+                           g);
     else
-        hipLaunchKernelGGL(maxpool_fwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream,
-                           static_cast<const bf16_t*>(x), static_cast<bf16_t*>(y), argmax, planes, g);
-    return nott::launch_status(ctx, "maxpool_fwd");
+        hipLaunchKernelGGL((maxpool_fwd_kernel<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, xb, yb, argmax,
+                           planes, g);
+    return nott::launch_status(ctx, name);
 }
 
-extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const int64_t* argmax,
-                                  const void* dy, void* dx) {
+template <typename IX>
+int maxpool_bwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const IX* argmax, const void* dy,
+                     void* dx, const char* name) {
     NOTT_CHECK_CTX(ctx);
-    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_maxpool2d_bwd: bad dtype");
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), std::string(name) + ": bad dtype");
     PoolGeom g;
     int st = check_desc(ctx, d, &g);
     if (st != NOTT_OK) return st;
+    if (sizeof(IX) == 1)
+        NOTT_REQUIRE(ctx, g.kh * g.kw <= 256, std::string(name) + ": a window of more than 256 taps needs int64 indices");
     const int64_t planes = d->n * d->c, total = planes * g.h * g.w;
     if (total == 0) return NOTT_OK;
-    NOTT_REQUIRE(ctx, argmax && dy && dx, "nott_maxpool2d_bwd: null buffer");
+    NOTT_REQUIRE(ctx, argmax && dy && dx, std::string(name) + ": null buffer");
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(total, kThreads));
     const int32_t band_rows = (int32_t)(kPoolRows * g.sh);
     const size_t blds = pool_bwd_lds(g, band_rows);
-    if (fits32(planes, g) && blds > 0 && planes <= 65535) {
+    const auto* df = static_cast<const float*>(dy);
+    const auto* db = static_cast<const bf16_t*>(dy);
+    auto* xf = static_cast<float*>(dx);
+    auto* xb = static_cast<bf16_t*>(dx);
+    if (fits32(planes, g) && planes <= 65535 && s2_geom(g) && vec4_ok(g, dtype, {dy, dx}) &&
+        ((uintptr_t)argmax % ix_align<IX>()) == 0 && s2_bwd_lds(g) <= kPoolLdsMax) {
+        const PoolGeom32 g32 = geom32(g);
+        const dim3 sgrid((unsigned)nott::ceil_div(g.h, (int64_t)(2 * kS2Rows)), (unsigned)planes);
+        const size_t lds = s2_bwd_lds(g);
+        if (g.kh == 3 && dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_bwd_s2_kernel<float, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, argmax,
+                               df, xf, g32);
+        else if (g.kh == 3)
+            hipLaunchKernelGGL((maxpool_bwd_s2_kernel<bf16_t, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream,
+                               argmax, db, xb, g32);
+        else if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_bwd_s2_kernel<float, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, argmax,
+                               df, xf, g32);
+        else
+            hipLaunchKernelGGL((maxpool_bwd_s2_kernel<bf16_t, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream,
+                               argmax, db, xb, g32);
+    } else if (fits32(planes, g) && blds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.h, (int64_t)band_rows), (unsigned)planes);
-        const bool vec = vec4_ok(g, dtype, {dy, dx}) && ((uintptr_t)argmax % 16) == 0;
+        const bool vec = vec4_ok(g, dtype, {dy, dx}) && ((uintptr_t)argmax % ix_align<IX>()) == 0;
         if (dtype == NOTT_F32 && vec)
-            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, true>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, true, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, df, xf, g32, band_rows);
         else if (dtype == NOTT_F32)
-            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, false>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, static_cast<const float*>(dy), static_cast<float*>(dx), g32, band_rows);
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, false, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, df, xf, g32, band_rows);
         else if (vec)
-            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, true>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, true, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, db, xb, g32, band_rows);
         else
-            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, false>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), g32, band_rows);
+            hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, false, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
+                               argmax, db, xb, g32, band_rows);
     } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
         if (dtype == NOTT_F32)
-            hipLaunchKernelGGL(maxpool_bwd_kernel32<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
-                               static_cast<const float*>(dy), static_cast<float*>(dx), (uint32_t)total, g32);
+            hipLaunchKernelGGL((maxpool_bwd_kernel32<float, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, df, xf,
+                               (uint32_t)total, g32);
         else
-            hipLaunchKernelGGL(maxpool_bwd_kernel32<bf16_t>, grid, dim3(kThreads), 0, ctx->stream, argmax,
-                               static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), (uint32_t)total, g32);
+            hipLaunchKernelGGL((maxpool_bwd_kernel32<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, db, xb,
+                               (uint32_t)total, g32);
     } else if (dtype == NOTT_F32)
-        hipLaunchKernelGGL(maxpool_bwd_kernel<float>, grid, dim3(kThreads), 0, ctx->stream, argmax,
-                           static_cast<const float*>(dy), static_cast<float*>(dx), planes, g);
+        hipLaunchKernelGGL((maxpool_bwd_kernel<float, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, df, xf, planes,
+                           g);
     else
-        hipLaunchKernelGGL(maxpool_bwd_kernel<bf16_t>, grid, dim3(kThreads), 0, ctx->stream, argmax,
-                           static_cast<const bf16_t*>(dy), static_cast<bf16_t*>(dx), planes, g);
-    return nott::launch_status(ctx, "maxpool_bwd");
+        hipLaunchKernelGGL((maxpool_bwd_kernel<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, db, xb,
+                           planes, g);
+    return nott::launch_status(ctx, name);
+}
+
+}  // namespace
+
+extern "C" int nott_maxpool2d_fwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x, void* y,
+                                  int64_t* argmax) {
+    return maxpool_fwd_impl<int64_t>(ctx, d, dtype, x, y, argmax, "nott_maxpool2d_fwd");
+}
+
+extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const int64_t* argmax,
+                                  const void* dy, void* dx) {
+    return maxpool_bwd_impl<int64_t>(ctx, d, dtype, argmax, dy, dx, "nott_maxpool2d_bwd");
+}
+
+extern "C" int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x,
+                                      void* y, uint8_t* tap) {
+    return maxpool_fwd_impl<uint8_t>(ctx, d, dtype, x, y, tap, "nott_maxpool2d_fwd_tap");
+}
+
+extern "C" int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
+                                      const void* dy, void* dx) {
+    return maxpool_bwd_impl<uint8_t>(ctx, d, dtype, tap, dy, dx, "nott_maxpool2d_bwd_tap");
 }

@@ -304,6 +304,28 @@ def maxpool2d_bwd(argmax: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc) -> torc
     return dx
 
 
+def maxpool2d_fwd_tap(x: torch.Tensor, d: Pool2dDesc):
+    """MaxPool2d forward keeping the argmax as the uint8 window tap
+    ((ih − oh·sh + ph)/dh)·kw + (iw − ow·sw + pw)/dw (nott_maxpool2d_fwd_tap)."""
+    _check(x, "x", shape=(d.n, d.c, d.h, d.w))
+    oh = pool_out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, bool(d.ceil_mode))
+    ow = pool_out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, bool(d.ceil_mode))
+    y = torch.empty((d.n, d.c, oh, ow), dtype=x.dtype, device=x.device)
+    tap = torch.empty((d.n, d.c, oh, ow), dtype=torch.uint8, device=x.device)
+    _ctx_for(x).call("nott_maxpool2d_fwd_tap", C.byref(d), nott_dtype(x.dtype), _ptr(x), _ptr(y), _ptr(tap))
+    return y, tap
+
+
+def maxpool2d_bwd_tap(tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc) -> torch.Tensor:
+    oh = pool_out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, bool(d.ceil_mode))
+    ow = pool_out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, bool(d.ceil_mode))
+    _check(dy, "dy", shape=(d.n, d.c, oh, ow))
+    _check(tap, "tap", shape=(d.n, d.c, oh, ow), dtype=torch.uint8, device=dy.device)
+    dx = torch.empty((d.n, d.c, d.h, d.w), dtype=dy.dtype, device=dy.device)
+    _ctx_for(dy).call("nott_maxpool2d_bwd_tap", C.byref(d), nott_dtype(dy.dtype), _ptr(tap), _ptr(dy), _ptr(dx))
+    return dx
+
+
 def avgpool_global_fwd(x: torch.Tensor) -> torch.Tensor:
     _check(x, "x")
     n, c, h, w = x.shape
