@@ -234,6 +234,25 @@ def test_batchnorm(ops, oracle, dt, shape):
 
 
 @pytest.mark.parametrize("dt", DTYPES)
+def test_batchnorm_bwd_params_only(ops, dt):
+    """With no dx requested the backward still writes dgamma / dbeta (its own
+    finalize pass), bit-identical to the full backward's, and accumulates."""
+    from thot_amd.ops import _ctx_for, _ptr, nott_dtype
+    n, c, h, w = 8, 24, 9, 12
+    g = rng(321)
+    x = dev(host_input(g.standard_normal((n, c, h, w)), dt), dt)
+    dy = dev(host_input(g.standard_normal((n, c, h, w)), dt), dt)
+    gamma = dev(f32(1 + 0.1 * g.standard_normal(c)))
+    _, mean, rstd = ops.batchnorm2d_fwd(x, gamma, dev(f32(np.zeros(c))), 1e-5, 0.1)
+    _, dg, db = ops.batchnorm2d_bwd(x, dy, mean, rstd, gamma)
+    dg2 = torch.full((c,), 0.5, device="cuda")
+    db2 = torch.full((c,), -0.25, device="cuda")
+    _ctx_for(x).call("nott_batchnorm2d_bwd", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(dy), _ptr(mean),
+                     _ptr(rstd), _ptr(gamma), None, _ptr(dg2), _ptr(db2), 1)
+    assert torch.equal(dg2, dg + 0.5) and torch.equal(db2, db - 0.25)
+
+
+@pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("shape", BN_SHAPES)
 @pytest.mark.parametrize("with_res", [False, True])
 def test_batchnorm_act(ops, oracle, dt, shape, with_res):

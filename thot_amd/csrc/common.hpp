@@ -222,11 +222,40 @@ __device__ __forceinline__ float lane_f32(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), L));
 }
 
-// Full 64-lane sum; every lane receives the result.  Within a row of 16
-// lanes: DPP quad_perm / half-mirror / mirror; across rows: lane reads.
 // ReLU as torch::relu computes it (reference relu.hpp:13): a NaN passes.
 __device__ __forceinline__ float relu_out(float x) { return (x > 0.f || x != x) ? x : 0.f; }
 
+// Σ_{z<n} p[z·stride] (n ≥ 1) as 4 floats, added in z order, with the loads
+// of 8 consecutive z in flight together (a loop over a run-time count
+// otherwise waits for each load before issuing the next).  Loads past n
+// re-read the last term and are not added.
+__device__ __forceinline__ f32x4 ordered_sum4(const float* __restrict__ p, int64_t stride, int32_t n) {
+    f32x4 s = *reinterpret_cast<const f32x4*>(p);
+    for (int32_t z = 1; z < n; z += 8) {
+        f32x4 t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = *reinterpret_cast<const f32x4*>(p + (int64_t)min(z + u, n - 1) * stride);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z + u < n) s += t[u];
+    }
+    return s;
+}
+__device__ __forceinline__ float ordered_sum1(const float* __restrict__ p, int64_t stride, int32_t n) {
+    float s = p[0];
+    for (int32_t z = 1; z < n; z += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = p[(int64_t)min(z + u, n - 1) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (z + u < n) s += t[u];
+    }
+    return s;
+}
+
+// Full 64-lane sum; every lane receives the result.  Within a row of 16
+// lanes: DPP quad_perm / half-mirror / mirror; across rows: lane reads.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
     v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]

@@ -369,16 +369,23 @@ __global__ __launch_bounds__(256) void conv3x3_split_reduce_kernel(const float* 
     if (q >= (int64_t)groups * cout) return;
     const int32_t co = (int32_t)(q / groups), m = (int32_t)(q - (int64_t)co * groups) * 4;
     const int64_t stride = (int64_t)cout * npix;
-    const float* src = partial + (int64_t)co * npix + m;
-    f32x4 s = *reinterpret_cast<const f32x4*>(src);
-    for (int32_t z = 1; z < splits; ++z) s += *reinterpret_cast<const f32x4*>(src + z * stride);
+    const f32x4 s = ordered_sum4(partial + (int64_t)co * npix + m, stride, splits);
     const float bv = bias ? bias[co] : 0.f;
+    f32x4 v;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 4; ++e) v[e] = relu ? relu_out(s[e] + bv) : s[e] + bv;
+    if ((hw & 3) == 0) {
+        // the 4 pixels lie in one image plane: one 4-element store
         uint32_t n, pix;
-        fd_hw.divmod((uint32_t)(m + e), n, pix);
-        const float v = s[e] + bv;
-        Io<T>::st(out, ((int64_t)n * cout + co) * hw + pix, relu ? relu_out(v) : v);
+        fd_hw.divmod((uint32_t)m, n, pix);
+        Vec4<T>::st(out + ((int64_t)n * cout + co) * hw + pix, v);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t n, pix;
+            fd_hw.divmod((uint32_t)(m + e), n, pix);
+            Io<T>::st(out, ((int64_t)n * cout + co) * hw + pix, v[e]);
+        }
     }
 }
 
@@ -701,59 +708,72 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
             }
         }
     }
-    // Partials: ws[split][tap][k][c]; lane column = channel, rows = k.
-    const int32_t c = cb * 64 + cg * 16 + r16;
-    if (c >= p.c) return;                        // padding channels of a partial 64-channel block
+    // Partials in dw's own layout, ws[split][k][c][tap].  For each (mt, e) a
+    // wave holds 4 k rows (one per 16-lane group) × its 16 channels × 9 taps,
+    // i.e. 4 runs of 144 consecutive floats; they pass through the wave's own
+    // LDS slice so that the global stores are whole 16-byte pieces.
+    const int32_t c0 = cb * 64 + cg * 16;        // this wave's first channel
     float* wsp = ws + (int64_t)blockIdx.x * 9 * p.k * p.c;
+    float* slice = reinterpret_cast<float*>(smem) + wid * (4 * 16 * 9);
+    __syncthreads();                             // every wave is done with the band operands
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap)
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int e = 0; e < 4; ++e) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int32_t k = kb * 64 + (kh * 2 + mt) * 16 + kq * 4 + e;
-                wsp[((int64_t)tap * p.k + k) * p.c + c] = acc[mt][tap][e];
+            for (int tap = 0; tap < 9; ++tap) slice[(kq * 16 + r16) * 9 + tap] = acc[mt][tap][e];
+            // the slice is this wave's own: wave-scope ordering suffices
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            // float4 piece i of run g (k = kb·64 + (kh·2 + mt)·16 + 4g + e): 36 per run
+            for (int i = lane; i < 4 * 36; i += 64) {
+                const int g = i / 36, j = i - g * 36;
+                const int32_t k = kb * 64 + (kh * 2 + mt) * 16 + g * 4 + e;
+                const int32_t cw = min(16, p.c - c0);   // channels of this wave inside c (whole groups of 16 or fewer)
+                if (4 * j < cw * 9)
+                    *reinterpret_cast<f32x4*>(wsp + ((int64_t)k * p.c + c0) * 9 + 4 * j) =
+                        *reinterpret_cast<const f32x4*>(slice + g * 144 + 4 * j);
             }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
 }
 
-// dw[k][c][tap] (+)= Σ_split ws[split][tap][k][c].  A block owns 64 float4
-// groups of the partial layout (lane = group, so each wave load is a 1 KB
-// coalesced run); its 4 waves take the splits round-robin with 8 loads in
-// flight each and combine in LDS in wave order, so the summation order is
-// fixed.  Requires c % 4 == 0 (the four floats of a group share kk and tap).
-constexpr int kWgReduceUnroll = 8;
+// dw[k][c][tap] (+)= Σ_split ws[split][k][c][tap] (the partials share dw's
+// layout, so reads and writes are contiguous float4 runs).  A block owns
+// 256 / ZL float4 groups; thread t takes group t % G and the splits
+// z ≡ t / G (mod ZL) in order, 8 loads in flight, and the ZL lane sums of a
+// group combine in LDS in lane order, so the summation order is fixed.
+// ZL = 4 (1 KB coalesced runs) for few splits, 16 for many (more loads in
+// flight per group, four times the workgroups).  Requires 9·k·c % 4 == 0.
+template <int ZL>
 __global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* __restrict__ ws, int32_t splits,
                                                                    int32_t k, int32_t c, float* __restrict__ dw,
                                                                    int accumulate) {
-    __shared__ f32x4 red[4][64];
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    constexpr int G = 256 / ZL;
+    __shared__ f32x4 red[ZL][G];
+    const int gl = threadIdx.x % G, zl = threadIdx.x / G;
     const int64_t per = (int64_t)9 * k * c;
-    const int64_t q = (int64_t)blockIdx.x * 64 + lane;   // float4 group: i = 4q = (tap·k + kk)·c + cc
+    const int64_t q = (int64_t)blockIdx.x * G + gl;   // float4 group: i = 4q = (tap·k + kk)·c + cc
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    if (4 * q < per) {
-        const f32x4* src = reinterpret_cast<const f32x4*>(ws) + q;
-        const int64_t zstride = per / 4;
-        int32_t z = wid;
-        for (; z + (kWgReduceUnroll - 1) * 4 < splits; z += kWgReduceUnroll * 4) {
-            f32x4 t[kWgReduceUnroll];
-#pragma unroll
-            for (int u = 0; u < kWgReduceUnroll; ++u) t[u] = src[(int64_t)(z + 4 * u) * zstride];
-#pragma unroll
-            for (int u = 0; u < kWgReduceUnroll; ++u) s += t[u];
-        }
-        for (; z < splits; z += 4) s += src[(int64_t)z * zstride];
+    if (4 * q < per && zl < splits) {
+        const int32_t n = (splits - zl + ZL - 1) / ZL;   // splits zl, zl + ZL, ...
+        s = ordered_sum4(ws + 4 * q + (int64_t)zl * per, (int64_t)ZL * per, n);
     }
-    red[wid][lane] = s;
+    red[zl][gl] = s;
     __syncthreads();
-    if (wid != 0 || 4 * q >= per) return;
-    const f32x4 t = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
-    const int64_t i = 4 * q;
-    const int32_t cc = (int32_t)(i % c);
-    const int64_t rest = i / c;
-    const int32_t kk = (int32_t)(rest % k), tap = (int32_t)(rest / k);
-    float* o = dw + ((int64_t)kk * c + cc) * 9 + tap;
+    if (zl != 0 || 4 * q >= per) return;
+    f32x4 t = red[0][gl];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[9 * e] = accumulate ? o[9 * e] + t[e] : t[e];
+    for (int u = 1; u < ZL; ++u) t += red[u][gl];
+    float* o = dw + 4 * q;
+    if (((uintptr_t)dw & 15) == 0) {
+        f32x4* o4 = reinterpret_cast<f32x4*>(o);
+        *o4 = accumulate ? *o4 + t : t;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = accumulate ? o[e] + t[e] : t[e];
+    }
 }
 
 
@@ -772,7 +792,8 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     int64_t splits = std::max<int64_t>(1, std::min<int64_t>(p.total_bands, ceil_div((int64_t)ctx->num_cu, tiles)));
     p.bands_per_split = (int32_t)ceil_div(p.total_bands, splits);
     splits = ceil_div(p.total_bands, p.bands_per_split);
-    const size_t lds = (size_t)64 * 16 * (TH * CPR + (TH + 2) * CPR + 2);
+    // band operands, or the epilogue's 8 wave slices of 4·16·9 floats if larger
+    const size_t lds = std::max<size_t>((size_t)64 * 16 * (TH * CPR + (TH + 2) * CPR + 2), 8 * 4 * 16 * 9 * sizeof(float));
     if (lds > 160 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad: band does not fit in LDS");
     float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)splits * 9 * p.k * p.c));
     if (!ws) return NOTT_ERR_ALLOC;
@@ -785,8 +806,12 @@ int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, 
     hipLaunchKernelGGL((conv3x3_wgrad_kernel<T, P, LW>), dim3((unsigned)splits, (unsigned)tiles), dim3(kWgThreads), lds,
                        ctx->stream, x, dy, ws, p);
     const int64_t per = (int64_t)9 * p.k * p.c;
-    hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256), 0, ctx->stream, ws,
-                       (int32_t)splits, p.k, p.c, dw, accumulate);
+    if (splits >= 32)
+        hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel<16>, dim3((unsigned)ceil_div(per / 4, 16)), dim3(256), 0,
+                           ctx->stream, ws, (int32_t)splits, p.k, p.c, dw, accumulate);
+    else
+        hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel<4>, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256), 0,
+                           ctx->stream, ws, (int32_t)splits, p.k, p.c, dw, accumulate);
     return launch_status(ctx, "conv3x3_wgrad");
 }
 

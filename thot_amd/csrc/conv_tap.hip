@@ -410,15 +410,10 @@ __global__ __launch_bounds__(256) void conv_tap_reduce_kernel(TapParams p, int32
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     const int ne = min(4, C.npix - m);
     if (ne == 4 && (p.npix_max & 3) == 0) {
-        f32x4 a = *reinterpret_cast<const f32x4*>(src);
-        for (int32_t z = 1; z < p.splits; ++z) a += *reinterpret_cast<const f32x4*>(src + (int64_t)z * per);
+        const f32x4 a = ordered_sum4(src, per, p.splits);
         s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w;
     } else {
-        for (int e = 0; e < ne; ++e) {
-            float a = src[e];
-            for (int32_t z = 1; z < p.splits; ++z) a += src[(int64_t)z * per + e];
-            s[e] = a;
-        }
+        for (int e = 0; e < ne; ++e) s[e] = ordered_sum1(src + e, per, p.splits);
     }
     const float bv = bias ? bias[co] : 0.f;
     for (int e = 0; e < ne; ++e) {
