@@ -50,6 +50,11 @@ CASES = [
     (1, 1, 100, 77, 8, False),
     (1, 2, 33, 100, 64, True),
     (1, 1, 192, 192, 24, True),
+    # head dim 64 (the bf16 a64 kernels): ragged ends over several 128-row
+    # blocks, causal and full, t < s and t > s
+    (1, 2, 300, 300, 64, True),
+    (1, 2, 200, 330, 64, False),
+    (2, 1, 257, 129, 64, True),
 ]
 
 
