@@ -355,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void attn_fwd_kernel(const T* __restrict_
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int key = k0 + kt * 16 + kq * 4 + e;
-                const bool ok = full || (key < p.s && !(p.causal && key > my_q));
+                const bool ok = full | ((key < p.s) & !(p.causal & (key > my_q)));   // bitwise: no per-element branches
                 sc[kt][e] = ok ? sc[kt][e] * sl2 : -INFINITY;   // log2 domain
                 mx = fmaxf(mx, sc[kt][e]);
             }
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(kThreads) void attn_dkdv_kernel(const T* __restrict
             for (int e = 0; e < 4; ++e) {
                 const int ql = qt * 16 + kq * 4 + e;
                 const int qrow = q0 + ql;
-                const bool ok = full || (qrow < p.t && my_k < p.s && !(p.causal && my_k > qrow));
+                const bool ok = full | ((qrow < p.t) & (my_k < p.s) & !(p.causal & (my_k > qrow)));   // bitwise: no per-element branches
                 const float pe = __builtin_amdgcn_exp2f(ok ? pt[qt][e] * sl2 - llse[ql] : -INFINITY);
                 pt[qt][e] = pe;
                 dpt[qt][e] = pe * (dpt[qt][e] - lds_[ql]);   // ds
@@ -616,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int key = k0 + kt * 16 + kq * 4 + e;
-                    const bool ok = full || (my_q < p.t && key < p.s && !(p.causal && key > my_q));
+                    const bool ok = full | ((my_q < p.t) & (key < p.s) & !(p.causal & (key > my_q)));   // bitwise: no per-element branches
                     part += __builtin_amdgcn_exp2f(ok ? sc[e] * sl2 - my_lse : -INFINITY) * (ok ? dp[e] : 0.f);
                 }
             }
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(kThreads) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int key = k0 + kt * 16 + kq * 4 + e;
-                const bool ok = full || (my_q < p.t && key < p.s && !(p.causal && key > my_q));
+                const bool ok = full | ((my_q < p.t) & (key < p.s) & !(p.causal & (key > my_q)));   // bitwise: no per-element branches
                 const float pe = __builtin_amdgcn_exp2f(ok ? sc[kt][e] * sl2 - my_lse : -INFINITY);
                 dp[kt][e] = pe * (dp[kt][e] - my_ds);
             }
