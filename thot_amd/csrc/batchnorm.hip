@@ -39,6 +39,11 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
 
 // Partial sums of (x − pivot) and (x − pivot)² over planes [n0, n1) of
 // channel blockIdx.x.  pivot = x[0, c, 0] keeps the variance well conditioned.
+// Thread t owns groups j ≡ t (mod kThreads) of each plane (a group is 4
+// pixels with VEC, else 1) and adds them image by image.  Planes of fewer
+// than kThreads groups give a thread one group per image: its loads for up
+// to kAhead images are issued before the adds, which run in the same order.
+constexpr int kAhead = 8;
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict__ x, int64_t n, int64_t c, int64_t hw,
                                                             int64_t per_split, float* __restrict__ partial) {
@@ -47,23 +52,37 @@ __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict_
     const int64_t n0 = (int64_t)blockIdx.y * per_split;
     const int64_t n1 = std::min<int64_t>(n, n0 + per_split);
     const float pivot = Io<T>::ld(x, ch * hw);
+    constexpr int V = VEC ? 4 : 1;
+    const int64_t hwg = hw / V;
     float s1 = 0.f, s2 = 0.f;
-    for (int64_t i = n0; i < n1; ++i) {
-        const T* p = x + (i * c + ch) * hw;
+    auto ld = [&](int64_t e) { return VEC ? Vec4<T>::ld(x + e) : f32x4{Io<T>::ld(x, e), 0.f, 0.f, 0.f}; };
+    auto add = [&](const f32x4& v) {
         if (VEC) {
-            for (int64_t j = (int64_t)threadIdx.x * 4; j < hw; j += kThreads * 4) {
-                f32x4 v = Vec4<T>::ld(p + j);
-                const float a = v.x - pivot, b = v.y - pivot, cc = v.z - pivot, d = v.w - pivot;
-                s1 += (a + b) + (cc + d);
-                s2 += (a * a + b * b) + (cc * cc + d * d);
-            }
+            const float a = v.x - pivot, b = v.y - pivot, cc = v.z - pivot, d = v.w - pivot;
+            s1 += (a + b) + (cc + d);
+            s2 += (a * a + b * b) + (cc * cc + d * d);
         } else {
-            for (int64_t j = threadIdx.x; j < hw; j += kThreads) {
-                const float a = Io<T>::ld(p, j) - pivot;
-                s1 += a;
-                s2 += a * a;
-            }
+            const float a = v.x - pivot;
+            s1 += a;
+            s2 += a * a;
         }
+    };
+    if (hwg >= kThreads) {
+        for (int64_t i = n0; i < n1; ++i) {
+            const int64_t base = (i * c + ch) * hw;
+            for (int64_t j = threadIdx.x; j < hwg; j += kThreads) add(ld(base + j * V));
+        }
+    } else if ((int64_t)threadIdx.x < hwg) {
+        const int64_t step = c * hw;
+        int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
+        for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
+            f32x4 v[kAhead];
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) v[u] = ld(e + u * step);
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) add(v[u]);
+        }
+        for (; i < n1; ++i, e += step) add(ld(e));
     }
     block_sum2<kWaves>(s1, s2, red);
     if (threadIdx.x == 0) {
@@ -143,16 +162,18 @@ __global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, c
 }
 
 // y = act(a_c·x + c_c [+ res]) over the whole tensor (act = ReLU or identity).
+// One thread per group (4 elements with VEC, else 1) of a flat grid: a group
+// lies in one (n, c) plane, found with two multiply-high divisions.
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t total,
-                                                             int64_t c, int64_t hw, const float* __restrict__ coef,
+__global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, uint32_t ngroups,
+                                                             FastDiv fd_hwg, FastDiv fd_c, const float* __restrict__ coef,
                                                              const T* __restrict__ res, int relu) {
-    // grid: x over the n·c planes, y over each plane's hw: no per-element division
-    const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
-    if (j >= hw) return;
-    const int64_t plane = blockIdx.x;
-    const int64_t i = plane * hw + j;
-    const int64_t ch = plane % c;
+    const uint32_t q = blockIdx.x * kThreads + threadIdx.x;
+    if (q >= ngroups) return;
+    uint32_t plane, j, img, ch;
+    fd_hwg.divmod(q, plane, j);
+    fd_c.divmod(plane, img, ch);
+    const int64_t i = (int64_t)q * (VEC ? 4 : 1);
     const float a = coef[2 * ch], b = coef[2 * ch + 1];
     if (VEC) {
         f32x4 v = Vec4<T>::ld(x + i);
@@ -168,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict
     }
 }
 
-// Backward partial sums of dy and dy·(x − μ).
+// Backward partial sums of dy and dy·(x − μ), in the order of bn_stats_kernel.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                  const float* __restrict__ mean, int64_t n, int64_t c,
@@ -182,29 +203,45 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
     float za = 0.f, zc = 0.f;   // z = za·x + zc when the gradient comes through a ReLU
     if (act.relu) bn_coef(act.gamma ? act.gamma[ch] : 1.f, act.beta ? act.beta[ch] : 0.f, mu, act.rstd[ch], za, zc);
     float s1 = 0.f, s2 = 0.f;
-    for (int64_t i = n0; i < n1; ++i) {
-        const int64_t base = (i * c + ch) * hw;
+    constexpr int V = VEC ? 4 : 1;
+    const int64_t hwg = hw / V;
+    auto ld = [&](const T* p, int64_t e) { return VEC ? Vec4<T>::ld(p + e) : f32x4{Io<T>::ld(p, e), 0.f, 0.f, 0.f}; };
+    auto add = [&](f32x4 g, const f32x4& v) {
         if (VEC) {
-            for (int64_t j = (int64_t)threadIdx.x * 4; j < hw; j += kThreads * 4) {
-                f32x4 g = Vec4<T>::ld(dy + base + j), v = Vec4<T>::ld(x + base + j);
-                if (act.relu) {
-                    if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
-                    if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
-                    if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
-                    if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
-                }
-                s1 += (g.x + g.y) + (g.z + g.w);
-                s2 += (g.x * (v.x - mu) + g.y * (v.y - mu)) + (g.z * (v.z - mu) + g.w * (v.w - mu));
+            if (act.relu) {
+                if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
+                if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
+                if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
+                if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
             }
+            s1 += (g.x + g.y) + (g.z + g.w);
+            s2 += (g.x * (v.x - mu) + g.y * (v.y - mu)) + (g.z * (v.z - mu) + g.w * (v.w - mu));
         } else {
-            for (int64_t j = threadIdx.x; j < hw; j += kThreads) {
-                const float xv = Io<T>::ld(x, base + j);
-                float g = Io<T>::ld(dy, base + j);
-                if (act.relu && bn_z(xv, za, zc) <= 0.f) g = 0.f;
-                s1 += g;
-                s2 += g * (xv - mu);
-            }
+            float gg = g.x;
+            if (act.relu && bn_z(v.x, za, zc) <= 0.f) gg = 0.f;
+            s1 += gg;
+            s2 += gg * (v.x - mu);
         }
+    };
+    if (hwg >= kThreads) {
+        for (int64_t i = n0; i < n1; ++i) {
+            const int64_t base = (i * c + ch) * hw;
+            for (int64_t j = threadIdx.x; j < hwg; j += kThreads) add(ld(dy, base + j * V), ld(x, base + j * V));
+        }
+    } else if ((int64_t)threadIdx.x < hwg) {
+        const int64_t step = c * hw;
+        int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
+        for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
+            f32x4 g[kAhead], v[kAhead];
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) {
+                g[u] = ld(dy, e + u * step);
+                v[u] = ld(x, e + u * step);
+            }
+#pragma unroll
+            for (int u = 0; u < kAhead; ++u) add(g[u], v[u]);
+        }
+        for (; i < n1; ++i, e += step) add(ld(dy, e), ld(x, e));
     }
     block_sum2<kWaves>(s1, s2, red);
     if (threadIdx.x == 0) {
@@ -238,14 +275,15 @@ __global__ __launch_bounds__(64) void bn_bwd_finalize(const float* __restrict__ 
 
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restrict__ x, const T* __restrict__ dy,
-                                                                T* __restrict__ dx, int64_t total, int64_t c,
-                                                                int64_t hw, const float* __restrict__ coef,
+                                                                T* __restrict__ dx, uint32_t ngroups, FastDiv fd_hwg,
+                                                                FastDiv fd_c, const float* __restrict__ coef,
                                                                 const float* __restrict__ mean, BnAct act) {
-    const int64_t j = ((int64_t)blockIdx.y * kThreads + threadIdx.x) * (VEC ? 4 : 1);
-    if (j >= hw) return;
-    const int64_t plane = blockIdx.x;
-    const int64_t i = plane * hw + j;
-    const int64_t ch = plane % c;
+    const uint32_t q = blockIdx.x * kThreads + threadIdx.x;
+    if (q >= ngroups) return;
+    uint32_t plane, j, img, ch;
+    fd_hwg.divmod(q, plane, j);
+    fd_c.divmod(plane, img, ch);
+    const int64_t i = (int64_t)q * (VEC ? 4 : 1);
     const float A = coef[3 * ch], B = coef[3 * ch + 1], C = coef[3 * ch + 2];
     float za = 0.f, zc = 0.f;
     if (act.relu)
@@ -291,19 +329,21 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
     const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 && ((uintptr_t)yv % (4 * sizeof(T))) == 0 &&
                      ((uintptr_t)resv % (4 * sizeof(T))) == 0;
     const dim3 g1((unsigned)c, (unsigned)splits);
+    const FastDiv fd_hwg((uint32_t)(vec ? hw / 4 : hw)), fd_c((uint32_t)c);
     if (vec)
         hipLaunchKernelGGL((bn_stats_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
     else
         hipLaunchKernelGGL((bn_stats_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
     hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial,
                        c, splits, hw, n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
-    const int64_t total = n * c * hw;
+    const uint32_t ngroups = (uint32_t)(n * c * (vec ? hw / 4 : hw));
+    const dim3 ga((unsigned)nott::ceil_div(ngroups, kThreads));
     if (vec)
-        hipLaunchKernelGGL((bn_affine_kernel<T, true>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)),
-                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef, res, relu);
+        hipLaunchKernelGGL((bn_affine_kernel<T, true>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
+                           coef, res, relu);
     else
-        hipLaunchKernelGGL((bn_affine_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
-                           dim3(kThreads), 0, ctx->stream, x, y, total, c, hw, coef, res, relu);
+        hipLaunchKernelGGL((bn_affine_kernel<T, false>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
+                           coef, res, relu);
     return nott::launch_status(ctx, "batchnorm_fwd");
 }
 
@@ -323,6 +363,7 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 &&
                      ((uintptr_t)dyv % (4 * sizeof(T))) == 0 && ((uintptr_t)dxv % (4 * sizeof(T))) == 0;
     const dim3 g1((unsigned)c, (unsigned)splits);
+    const FastDiv fd_hwg((uint32_t)(vec ? hw / 4 : hw)), fd_c((uint32_t)c);
     if (vec)
         hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
                            per, partial, act);
@@ -332,14 +373,14 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c,
                        splits, n * hw, mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
     if (dx) {
-        const int64_t total = n * c * hw;
+        const uint32_t ngroups = (uint32_t)(n * c * (vec ? hw / 4 : hw));
+        const dim3 ga((unsigned)nott::ceil_div(ngroups, kThreads));
         if (vec)
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>),
-                               dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw / 4, kThreads)), dim3(kThreads), 0,
-                               ctx->stream, x, dy, dx, total, c, hw, coef, mean, act);
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
+                               fd_hwg, fd_c, coef, mean, act);
         else
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), dim3((unsigned)(n * c), (unsigned)nott::ceil_div(hw, kThreads)),
-                               dim3(kThreads), 0, ctx->stream, x, dy, dx, total, c, hw, coef, mean, act);
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
+                               fd_hwg, fd_c, coef, mean, act);
     }
     return nott::launch_status(ctx, "batchnorm_bwd");
 }
@@ -355,7 +396,7 @@ extern "C" int nott_batchnorm2d_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t 
     NOTT_REQUIRE(ctx, (running_mean == nullptr) == (running_var == nullptr),
                  "nott_batchnorm2d_fwd: running_mean and running_var go together");
     NOTT_REQUIRE(ctx, x && y && mean && rstd, "nott_batchnorm2d_fwd: null buffer");
-    NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_fwd: tensor too large");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c * hw <= 0xffffffffll, "nott_batchnorm2d_fwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
     return dtype == NOTT_F32 ? fwd<float>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
                                           running_var, y, mean, rstd, residual, relu != 0)
@@ -377,7 +418,7 @@ extern "C" int nott_batchnorm2d_bwd_act(nott_ctx ctx, nott_dtype dtype, int64_t 
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_bwd: bad shape");
     NOTT_REQUIRE(ctx, x && dy && mean && rstd, "nott_batchnorm2d_bwd: null buffer");
-    NOTT_REQUIRE(ctx, c <= 65535 && n * c <= 0x7fffffff && hw <= 65535 * 256, "nott_batchnorm2d_bwd: tensor too large");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c * hw <= 0xffffffffll, "nott_batchnorm2d_bwd: tensor too large");
     nott::DeviceScope scope(ctx->device);
     const BnAct act{relu != 0, gamma, beta, rstd};
     return dtype == NOTT_F32 ? bwd<float>(ctx, n, c, hw, x, dy, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, act)
