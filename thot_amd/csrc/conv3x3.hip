@@ -52,34 +52,30 @@ struct SameParams {
 // (cb, cc) holds rows (tap, co) = tap·64 + co of CC channels, stored in the
 // LDS order of lds_off(row, sub) (16-row groups, sub-chunk-major inside a
 // group), so the kernels copy a slice to LDS linearly: contiguous 16-byte
-// pieces per lane, bank-conflict-free writes.
+// pieces per lane, bank-conflict-free writes.  Grid: x over one slice's
+// 9·64·CC elements, y = channel chunk cc, z = 64-channel block cb; the
+// fastest thread index runs over the source's contiguous dimension.
 template <typename T, bool DGRAD>
 __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict__ w, T* __restrict__ wp, int32_t cout,
                                                             int32_t cin) {
     // Slices cover whole 64-channel blocks; channels from cout up to the
     // block end are zero weights.
-    constexpr int CC = Chunk<T>::CC;
-    const int64_t total = (int64_t)((cout + kTileCo - 1) / kTileCo) * kTileCo * cin * 9;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    // decompose destination index
-    const int32_t cil = (int32_t)(i % CC);
-    int64_t rest = i / CC;
-    const int32_t col = (int32_t)(rest % kTileCo);
-    rest /= kTileCo;
-    const int32_t tap = (int32_t)(rest % 9);
-    rest /= 9;
-    const int32_t ncc = cin / CC;
-    const int32_t cc = (int32_t)(rest % ncc);
-    const int32_t cb = (int32_t)(rest / ncc);
+    constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
+    constexpr int32_t SLICE = 9 * kTileCo * CC;
+    const int32_t j = (int32_t)blockIdx.x * 256 + (int32_t)threadIdx.x;
+    if (j >= SLICE) return;
+    const int32_t cc = blockIdx.y, cb = blockIdx.z;
+    const int32_t tap = j / (kTileCo * CC), rem = j % (kTileCo * CC);
+    // fwd reads w[co][ci][r][s] (ci fastest); dgrad reads w[k = ci][c = co] (co fastest).
+    const int32_t cil = DGRAD ? rem / kTileCo : rem % CC;
+    const int32_t col = DGRAD ? rem % kTileCo : rem / CC;
     const int32_t co = cb * kTileCo + col, ci = cc * CC + cil;
     const int32_t r = tap / 3, s = tap % 3;
     // fwd: wt[co][ci][r][s] = w[co][ci][r][s]; dgrad: wt[co=c][ci=k][r][s] = w[k][c][2-r][2-s]
     // (in dgrad terms w is [k = cin][c = cout][3][3]).
     const int64_t src = DGRAD ? (((int64_t)ci * cout + co) * 9 + (2 - r) * 3 + (2 - s))
                               : (((int64_t)co * cin + ci) * 9 + r * 3 + s);
-    constexpr int SUB = Chunk<T>::SUB;
-    const int64_t slice = ((int64_t)cb * ncc + cc) * 9 * kTileCo * CC;
+    const int64_t slice = ((int64_t)cb * (cin / CC) + cc) * SLICE;
     T val = T(0);
     if (co < cout) val = w[src];
     wp[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = val;
@@ -440,9 +436,8 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     char* ws = static_cast<char*>(workspace(ctx, wbytes_al + pbytes));
     if (!ws) return NOTT_ERR_ALLOC;
     T* wp = reinterpret_cast<T*>(ws);
-    const int64_t welems = cbc * kTileCo * cin * 9;
-    hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(welems, 256)), dim3(256), 0,
-                       ctx->stream, wsrc, wp, cout, cin);
+    hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(9 * kTileCo * CC, 256), (unsigned)(cin / CC),
+                       (unsigned)cbc), dim3(256), 0, ctx->stream, wsrc, wp, cout, cin);
     SameParams p;
     p.n = n; p.cin = cin; p.h = h; p.w = w; p.cout = cout;
     p.hw = h * w; p.w2 = row_pitch(w); p.npix = n * h * w; p.in_rows = in_rows;

@@ -92,25 +92,22 @@ struct TapPrep {
     int64_t begin[kMaxClass + 1];          // first destination element per class
 };
 
+// Grid: x over one slice's ntap·64·CC elements, y = (cb, cc) slice of the
+// class, z = class; the fastest thread index runs over the source's
+// contiguous dimension (ci forward, co for TRANS).
 template <typename T, bool TRANS>
 __global__ __launch_bounds__(256) void conv_tap_wprep_kernel(const T* __restrict__ w, T* __restrict__ wp,
                                                              int32_t cout, int32_t cin, int32_t rsz, TapPrep tp) {
     constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= tp.begin[tp.nclass]) return;
-    int cl = 0;
-    while (cl + 1 < tp.nclass && i >= tp.begin[cl + 1]) ++cl;
+    const int32_t cl = blockIdx.z;
     const int32_t ntap = tp.ntap[cl];
-    int64_t rest = i - tp.begin[cl];
-    const int32_t cil = (int32_t)(rest % CC);
-    rest /= CC;
-    const int32_t col = (int32_t)(rest % kTileCo);
-    rest /= kTileCo;
-    const int32_t tap = (int32_t)(rest % ntap);
-    rest /= ntap;
+    const int32_t j = (int32_t)blockIdx.x * 256 + (int32_t)threadIdx.x;
+    if (j >= ntap * kTileCo * CC) return;
     const int32_t ncc = cin / CC;
-    const int32_t cc = (int32_t)(rest % ncc);
-    const int32_t cb = (int32_t)(rest / ncc);
+    const int32_t cb = (int32_t)blockIdx.y / ncc, cc = (int32_t)blockIdx.y % ncc;
+    const int32_t tap = j / (kTileCo * CC), rem = j % (kTileCo * CC);
+    const int32_t cil = TRANS ? rem / kTileCo : rem % CC;
+    const int32_t col = TRANS ? rem % kTileCo : rem / CC;
     const int32_t co = cb * kTileCo + col, ci = cc * CC + cil;
     const int32_t rsi = tp.rs_tap[cl][tap];
     const int64_t src = TRANS ? (((int64_t)ci * cout + co) * rsz + rsi) : (((int64_t)co * cin + ci) * rsz + rsi);
@@ -620,12 +617,17 @@ int run_plan(nott_ctx ctx, Plan& pl, const T* in, const T* w, bool trans, int32_
     if (!ws) return NOTT_ERR_ALLOC;
     T* wp = reinterpret_cast<T*>(ws);
     p.partial = p.splits > 1 ? reinterpret_cast<float*>(ws + wbytes) : nullptr;
+    int32_t ntap_max = 1;
+    for (int c = 0; c < nclass; ++c) ntap_max = std::max(ntap_max, pl.prep.ntap[c]);
+    constexpr int CC = Chunk<T>::CC;
+    const dim3 gw((unsigned)ceil_div(ntap_max * kTileCo * CC, 256), (unsigned)(ceil_div(p.cout, kTileCo) * (p.cin / CC)),
+                  (unsigned)nclass);
     if (trans)
-        hipLaunchKernelGGL((conv_tap_wprep_kernel<T, true>), dim3((unsigned)ceil_div(pl.welems, 256)), dim3(256), 0,
-                           ctx->stream, w, wp, p.cout, p.cin, rsz, pl.prep);
+        hipLaunchKernelGGL((conv_tap_wprep_kernel<T, true>), gw, dim3(256), 0, ctx->stream, w, wp, p.cout, p.cin, rsz,
+                           pl.prep);
     else
-        hipLaunchKernelGGL((conv_tap_wprep_kernel<T, false>), dim3((unsigned)ceil_div(pl.welems, 256)), dim3(256), 0,
-                           ctx->stream, w, wp, p.cout, p.cin, rsz, pl.prep);
+        hipLaunchKernelGGL((conv_tap_wprep_kernel<T, false>), gw, dim3(256), 0, ctx->stream, w, wp, p.cout, p.cin, rsz,
+                           pl.prep);
     const bool aligned_out = ((uintptr_t)out % 16) == 0;
     int32_t max_tiles = 0;
     for (int c = 0; c < nclass; ++c) {
