@@ -420,15 +420,15 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
     if (same_lds_bytes(h, w, sizeof(T)) > kSameLdsMax)
         return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
-    // Split the channel chunks over blockIdx.z when the grid would not give
-    // every CU two workgroups (small images, many channels).
+    // Split the channel chunks over blockIdx.z when the grid leaves
+    // workgroup slots (two per CU) idle (small images, many channels).
     const int64_t tiles = ceil_div((int64_t)n * h * w, kTilePix);
     const int64_t blocks = tiles * cbc;
     const int32_t nchunks = cin / CC;
     int32_t splits = 1;
     const int64_t npix64 = (int64_t)n * h * w;
     if (blocks < 2 * (int64_t)ctx->num_cu && nchunks > 1 && npix64 % 4 == 0)
-        splits = (int32_t)std::min<int64_t>(std::min<int64_t>(nchunks, 8), ceil_div(2 * (int64_t)ctx->num_cu, blocks));
+        splits = pick_chunk_splits(blocks, nchunks, 2 * (int64_t)ctx->num_cu, sizeof(T));
     const int32_t cc_per_split = (int32_t)ceil_div(nchunks, splits);
     splits = (int32_t)ceil_div(nchunks, cc_per_split);
     const size_t wbytes_al = (wbytes + 255) & ~(size_t)255;

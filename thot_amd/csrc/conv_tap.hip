@@ -567,8 +567,7 @@ bool make_plan(const nott_ctx ctx, int32_t n, int32_t cin, int32_t hin, int32_t 
     const int64_t blocks = tiles_total * cbc;
     const int64_t slots = (int64_t)ctx->num_cu * (pl.lds <= 80 * 1024 ? 2 : 1);
     int32_t splits = 1;
-    if (blocks < slots && nchunks > 1)
-        splits = (int32_t)std::min<int64_t>(std::min<int64_t>(nchunks, 8), ceil_div(slots, blocks));
+    if (blocks < slots && nchunks > 1) splits = pick_chunk_splits(blocks, nchunks, slots, sizeof(T));
     p.cc_per_split = (int32_t)ceil_div(nchunks, splits);
     p.splits = (int32_t)ceil_div(nchunks, p.cc_per_split);
     pl.blocks = blocks;

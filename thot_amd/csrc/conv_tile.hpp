@@ -52,6 +52,30 @@ __device__ __forceinline__ void mfma_chunk(const u32x4& a, const u32x4& b, f32x4
     }
 }
 
+// Channel-chunk split count for `blocks` output tiles on `slots` resident
+// workgroup slots.  With S splits a workgroup runs ceil(nchunks / S) chunks
+// and the grid takes ceil(S·blocks / slots) rounds, so the kernel time is
+// about rounds · (chunks + per-tile overhead), plus the split reduce when
+// S > 1 (both in units of one chunk's tap loop; measured: a tile's prologue
+// and epilogue cost about two bf16 chunks or half an fp32 one, the reduce
+// 2.5 bf16 chunks or one fp32 chunk).  The smallest S of least cost wins: a
+// grid of a few more workgroups than slots would run a whole second round.
+inline int32_t pick_chunk_splits(int64_t blocks, int32_t nchunks, int64_t slots, size_t elem) {
+    const double overhead = elem == 2 ? 2.0 : 0.5, reduce = elem == 2 ? 2.5 : 1.0;
+    double best = 0.0;
+    int32_t pick = 1;
+    for (int32_t s = 1; s <= std::min(nchunks, 8); ++s) {
+        const int64_t per = ceil_div(nchunks, s);
+        if (ceil_div(nchunks, per) != s) continue;      // same chunks per split as a smaller count
+        const double t = (double)ceil_div(s * blocks, slots) * ((double)per + overhead) + (s > 1 ? reduce : 0.0);
+        if (s == 1 || t < best) {
+            best = t;
+            pick = s;
+        }
+    }
+    return pick;
+}
+
 // Register transpose of a SUB×SUB block: in[i] holds SUB pixels of channel i,
 // out[j] holds SUB channels of pixel j.
 __device__ __forceinline__ void transpose_block(const u32x4 (&in)[8], u32x4 (&out)[8]) {
