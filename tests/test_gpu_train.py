@@ -351,10 +351,11 @@ def test_graph_step_matches_eager(host_mod, model):
 
 
 def test_graph_replay_after_workspace_growth(host_mod):
-    """A captured graph keeps the workspace pointer it was recorded with.  An
-    eager step at a larger batch on the same device afterwards must grow the
-    workspace without freeing the captured one, so later replays still match
-    an eager twin bit for bit."""
+    """A captured graph keeps the workspace pointers it was recorded with (the
+    device context's and the weight-gradient side stream's).  An eager step at
+    a larger batch on the same device afterwards must grow the workspace
+    without freeing the captured one, so later replays still match an eager
+    twin bit for bit."""
     eager = host_mod.ResNet18Trainer(0, 13, True, 1e-3, 1e-2, 1000)
     graphed = host_mod.ResNet18Trainer(0, 13, True, 1e-3, 1e-2, 1000)
     gen = torch.Generator(device="cuda").manual_seed(31)

@@ -207,10 +207,15 @@ struct Trainer {
         return out;
     }
     // forward + loss + backward (grads land in the flat gradient arena)
+    // Convolution weight gradients overlap the data-gradient chain on a
+    // side stream, joined before anything reads the gradients.
     Tensor forward_backward(const Tensor& x, const Tensor& y) {
+        const int dev = x.device().index();
+        NH::SideStreamScope side(dev);
         Tensor logits = model->forward(input(x));
         Tensor loss = NH::cross_entropy(logits, y);
         loss.backward();
+        NH::join_side_stream(dev);
         return loss.detach();
     }
     // One training step: forward, loss, backward, optimizer step with the
@@ -542,11 +547,14 @@ struct OptimizerHandle {
 
 PYBIND11_MODULE(_nott_host, m) {
     m.doc() = "C++ host layer (Nott::HIP) over libnott_hip: configs[0] and configs[4] training steps";
+    // Workspace of the device's contexts: the ordinary one and, once a
+    // trainer has run, the weight-gradient side stream's.
     m.def("workspace_bytes", [](int device) {
-        int64_t b = 0;
+        int64_t b = 0, sb = 0;
         nott_ctx c = NH::context(device);
         NH::check(nott_workspace_bytes(c, &b), c, "workspace bytes");
-        return b;
+        if (nott_ctx sc = NH::side_context(device)) NH::check(nott_workspace_bytes(sc, &sb), sc, "workspace bytes");
+        return b + sb;
     }, py::arg("device") = 0);
     // architecture.json text of a model (no device needed): "small_cnn" or
     // "resnet18" with `classes` outputs.
