@@ -27,6 +27,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <array>
+#include <atomic>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -97,6 +98,12 @@ inline Side& side(int dev) {
     static std::array<Side, 64> s;
     return s.at((size_t)dev);
 }
+// Process-wide switch (on by default); off, scopes leave everything on the
+// current stream.
+inline std::atomic<bool>& side_allowed() {
+    static std::atomic<bool> on{true};
+    return on;
+}
 inline void hip_ok(hipError_t e, const char* what) {
     if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
@@ -104,7 +111,8 @@ inline void hip_ok(hipError_t e, const char* what) {
 
 class SideStreamScope {
   public:
-    explicit SideStreamScope(int dev) : dev_(dev) {
+    explicit SideStreamScope(int dev) : dev_(dev), active_(detail::side_allowed().load()) {
+        if (!active_) return;
         detail::Side& s = detail::side(dev);
         if (!s.ctx) {
             nott_ctx c = nullptr;
@@ -123,20 +131,26 @@ class SideStreamScope {
         }
         ++s.depth;
     }
-    ~SideStreamScope() { --detail::side(dev_).depth; }
+    ~SideStreamScope() {
+        if (active_) --detail::side(dev_).depth;
+    }
     SideStreamScope(const SideStreamScope&) = delete;
     SideStreamScope& operator=(const SideStreamScope&) = delete;
 
   private:
     int dev_;
+    bool active_;
 };
+
+inline void set_side_stream_enabled(bool on) { detail::side_allowed().store(on); }
 
 // The context a weight gradient of `flops` on dy's device launches with: the
 // side stream's (ordered after the current stream's work so far, `reads`
 // recorded on it) while a scope is alive and the gradient is large enough to
 // pay for the fork and join (measured: the small CNN's convolutions, under
-// half a GFLOP, lost 8% of the step), else the ordinary one.
-constexpr double kSideMinFlops = 1e9;
+// half a GFLOP, lost 8% of the step; ResNet-18's 0.8-GFLOP 1×1 shortcuts
+// gain a little), else the ordinary one.
+constexpr double kSideMinFlops = 6e8;
 inline nott_ctx wgrad_context(const Tensor& dy, std::initializer_list<Tensor> reads, double flops) {
     nott_ctx c = bind(dy);
     const int dev = dy.device().index();

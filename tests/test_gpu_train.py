@@ -350,6 +350,39 @@ def test_graph_step_matches_eager(host_mod, model):
         assert torch.equal(be[k], bg[k]), k
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_side_stream_weight_gradients_match_one_stream(host_mod, bf16):
+    """Trainers run the large convolution weight gradients on a side stream
+    (their own context and workspace, joined after backward).  The same step
+    with the side stream switched off gives bit-identical gradients, loss and
+    updated parameters: the kernels and their summation orders do not depend
+    on the stream."""
+    gen = torch.Generator(device="cuda").manual_seed(77)
+    x = torch.rand((8, 3, 224, 224), generator=gen, device="cuda")
+    y = torch.randint(0, 1000, (8,), generator=gen, device="cuda")
+    results = []
+    try:
+        for on in (True, False):
+            host_mod.set_side_stream(on)
+            tr = host_mod.ResNet18Trainer(0, 19, bf16, 1e-3, 1e-2, 1000)
+            loss = tr.step(x, y)
+            torch.cuda.synchronize()
+            results.append((loss.clone(), {k: v.clone() for k, v in tr.params().items()}))
+            tr2 = host_mod.ResNet18Trainer(0, 19, bf16, 1e-3, 1e-2, 1000)
+            tr2.forward_backward(x, y)
+            torch.cuda.synchronize()
+            results[-1] += ({k: v.clone() for k, v in tr2.grads().items()},)
+    finally:
+        host_mod.set_side_stream(True)
+    (l1, p1, g1), (l2, p2, g2) = results
+    assert torch.equal(l1, l2), (l1.item(), l2.item())
+    assert set(g1) == set(g2) and len(g1) > 0
+    for k in g1:
+        assert torch.equal(g1[k], g2[k]), k
+    for k in p1:
+        assert torch.equal(p1[k], p2[k]), k
+
+
 def test_graph_replay_after_workspace_growth(host_mod):
     """A captured graph keeps the workspace pointers it was recorded with (the
     device context's and the weight-gradient side stream's).  An eager step at

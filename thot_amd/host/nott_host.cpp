@@ -556,6 +556,9 @@ PYBIND11_MODULE(_nott_host, m) {
         if (nott_ctx sc = NH::side_context(device)) NH::check(nott_workspace_bytes(sc, &sb), sc, "workspace bytes");
         return b + sb;
     }, py::arg("device") = 0);
+    // Whether trainers run convolution weight gradients on the side stream
+    // (on by default; the switch exists so tests can compare both orders).
+    m.def("set_side_stream", [](bool on) { NH::set_side_stream_enabled(on); }, py::arg("on"));
     // architecture.json text of a model (no device needed): "small_cnn" or
     // "resnet18" with `classes` outputs.
     m.def("architecture_json", [](const std::string& model, int64_t classes, const std::string& name) {
