@@ -271,6 +271,7 @@ struct StemWgParams {
     int32_t tiles_per_wg;
     int32_t padl;        // staged element of input column 0 (a multiple of 16 bytes, ≥ pw)
     int32_t vec_rows;    // input rows are whole, aligned 16-byte runs
+    int32_t row_runs;    // output rows hold whole runs of SUBK pixels (wo % SUBK == 0)
 };
 
 template <typename T>
@@ -373,14 +374,26 @@ __global__ __launch_bounds__(kThreads, 2) void stem_wgrad_kernel(const T* __rest
         for (int32_t k0 = 0; k0 < kTilePix; k0 += KPIX) {
             // This lane's SUBK pixels of the K step: LDS base of each pixel's
             // kernel row 0, channel 0, column 2·ow (pixels past the tile: dy 0).
+            // When output rows hold whole runs of SUBK pixels, the run starts
+            // a row and its pixels are consecutive columns of it.
             int32_t pbase[SUBK];
-#pragma unroll
-            for (int e = 0; e < SUBK; ++e) {
-                const int32_t m = min(m0 + k0 + kq * SUBK + e, m_last);
+            auto base_of = [&](int32_t m) {
                 uint32_t n, r, oh, ow;
                 p.fd_howo.divmod((uint32_t)m, n, r);
                 p.fd_wo.divmod(r, oh, ow);
-                pbase[e] = ((int32_t)n * p.hp + (int32_t)oh * p.sh - v_lo) * kStemC * rowb + 2 * (int32_t)ow * E;
+                return ((int32_t)n * p.hp + (int32_t)oh * p.sh - v_lo) * kStemC * rowb + 2 * (int32_t)ow * E;
+            };
+            if (q.row_runs) {
+                // A run never crosses m_last (tiles end on whole runs); one
+                // that starts past it repeats pixel m_last, whose staged x is
+                // finite (its dy is zero).
+                const int32_t ms = m0 + k0 + kq * SUBK;
+                const int32_t b0 = base_of(min(ms, m_last)), step = ms <= m_last ? 2 * E : 0;
+#pragma unroll
+                for (int e = 0; e < SUBK; ++e) pbase[e] = b0 + e * step;
+            } else {
+#pragma unroll
+                for (int e = 0; e < SUBK; ++e) pbase[e] = base_of(min(m0 + k0 + kq * SUBK + e, m_last));
             }
             u32x4 a[4], b[3];
 #pragma unroll
@@ -427,31 +440,37 @@ __global__ __launch_bounds__(kThreads, 2) void stem_wgrad_kernel(const T* __rest
 
 // dw[co][c][r][s] (+)= Σ_wg partial[wg][co][(c·R + r)·8 + s].  A block owns
 // 64 partial columns (lane = column, so each wave load is one 256-byte run);
-// its 4 waves take the workgroups round-robin with 8 loads in flight and
-// combine in LDS in wave order, so the summation order is fixed.
-__global__ __launch_bounds__(256) void stem_wgrad_reduce_kernel(const float* __restrict__ part, int32_t nwg, int32_t s,
-                                                                float* __restrict__ dw, int accumulate) {
-    __shared__ float red[4][64];
+// its 16 waves take the workgroups round-robin with 8 loads in flight (512
+// partial rows in four rounds) and combine in LDS in wave order, so the
+// summation order is fixed.
+constexpr int kStemRedWaves = 16;
+__global__ __launch_bounds__(64 * kStemRedWaves) void stem_wgrad_reduce_kernel(const float* __restrict__ part,
+                                                                               int32_t nwg, int32_t s,
+                                                                               float* __restrict__ dw, int accumulate) {
+    __shared__ float red[kStemRedWaves][64];
     constexpr int32_t kCols = kStemCo * kStemNB * 16;
+    constexpr int W = kStemRedWaves;
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int32_t i = blockIdx.x * 64 + lane;           // partial column: co·176 + col
     float a = 0.f;
     if (i < kCols) {
         const float* src = part + i;
         int32_t w = wid;
-        for (; w + 7 * 4 < nwg; w += 8 * 4) {
+        for (; w + 7 * W < nwg; w += 8 * W) {
             float t[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = src[(int64_t)(w + 4 * u) * kCols];
+            for (int u = 0; u < 8; ++u) t[u] = src[(int64_t)(w + W * u) * kCols];
 #pragma unroll
             for (int u = 0; u < 8; ++u) a += t[u];
         }
-        for (; w < nwg; w += 4) a += src[(int64_t)w * kCols];
+        for (; w < nwg; w += W) a += src[(int64_t)w * kCols];
     }
     red[wid][lane] = a;
     __syncthreads();
     if (wid != 0 || i >= kCols) return;
-    const float t = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < W; ++k) t += red[k][lane];
     const int32_t co = i / (kStemNB * 16), col = i % (kStemNB * 16);
     const int32_t sc = col % kStemS8, cr = col / kStemS8;
     if (cr >= kStemC * kStemR || sc >= s) return;
@@ -572,6 +591,7 @@ int stem_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy,
     const int32_t per_cu = lds <= 80 * 1024 ? 2 : 1;
     const int32_t nwg = (int32_t)std::min<int64_t>(p.tiles, (int64_t)per_cu * ctx->num_cu);
     q.tiles_per_wg = (int32_t)ceil_div(p.tiles, nwg);
+    q.row_runs = (p.wo % (16 / (int)sizeof(T)) == 0) ? 1 : 0;
     const size_t pbytes = sizeof(float) * (size_t)nwg * kStemCo * kStemNB * 16;
     float* part = static_cast<float*>(workspace(ctx, pbytes));
     if (!part) return NOTT_ERR_ALLOC;
@@ -582,7 +602,8 @@ int stem_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy,
         attr = true;
     }
     hipLaunchKernelGGL(stem_wgrad_kernel<T>, dim3((unsigned)nwg), dim3(kThreads), lds, ctx->stream, x, dy, part, q);
-    hipLaunchKernelGGL(stem_wgrad_reduce_kernel, dim3((unsigned)ceil_div(kStemCo * kStemNB * 16, 64)), dim3(256), 0,
+    hipLaunchKernelGGL(stem_wgrad_reduce_kernel, dim3((unsigned)ceil_div(kStemCo * kStemNB * 16, 64)),
+                       dim3(64 * kStemRedWaves), 0,
                        ctx->stream, part, nwg, p.s, dw, accumulate);
     return launch_status(ctx, "stem_wgrad");
 }
