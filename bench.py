@@ -438,7 +438,7 @@ class TrainStep(Workload):
     BATCH = 64
     groups = ()
 
-    graph = True   # forward + loss + backward replayed from a captured HIP graph (AdamW eager)
+    graph = True   # forward + loss + backward + AdamW replayed from a captured HIP graph
 
     def __init__(self, dtype, model):
         super().__init__(dtype)
@@ -460,12 +460,33 @@ class TrainStep(Workload):
             self.y = torch.randint(0, 1000, (self.BATCH,), generator=g, device="cuda")
             self.flop_sample = 681.5e9 / 64   # 3 x 1.814 GMAC forward - stem dgrad, per image
         self.tr.step(self.x, self.y)
+        self.mode_ms = None
         if self.graph:
             try:
                 self.tr.capture(self.x, self.y, 2)
             except RuntimeError as e:   # reported in the JSON line via hip_graph = false
                 print(f"bench: HIP graph capture failed, stepping eagerly: {e}", file=sys.stderr)
                 self.graph = False
+        if self.graph:
+            # The replayed graph and the eager step do the same work (the
+            # graph adds the two input copies); which is faster depends on
+            # the model: the eager launches overlap the weight-gradient side
+            # stream better than the replayed branches, a small model's
+            # launch overhead favours the graph.  Both are timed here, the
+            # faster one is the timed step, and both rates go in the line.
+            def ms(fn, n=8):
+                for _ in range(2):
+                    fn()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(n):
+                    fn()
+                torch.cuda.synchronize()
+                return (time.perf_counter() - t0) * 1e3 / n
+            g_ms = ms(lambda: self.tr.step_graph(self.x, self.y))
+            e_ms = ms(lambda: self.tr.step(self.x, self.y))
+            self.mode_ms = {"graph": round(g_ms, 4), "eager": round(e_ms, 4)}
+            self.graph = g_ms <= e_ms
 
     def step(self):
         if self.graph:
@@ -477,9 +498,12 @@ class TrainStep(Workload):
         return self.BATCH
 
     def config(self):
-        return {"workload": f"{self.name} training step (BASELINE configs[{0 if self.name == 'small_cnn' else 4}])",
-                "batch": self.BATCH, "optimizer": "Adam" if self.name == "small_cnn" else "AdamW",
-                "hip_graph": self.graph}
+        c = {"workload": f"{self.name} training step (BASELINE configs[{0 if self.name == 'small_cnn' else 4}])",
+             "batch": self.BATCH, "optimizer": "Adam" if self.name == "small_cnn" else "AdamW",
+             "hip_graph": self.graph}
+        if self.mode_ms:
+            c["setup_ms_per_step"] = self.mode_ms   # both modes, timed at setup; the faster is the timed step
+        return c
 
     def cpu_baseline(self, budget_s):
         ref = _ref()
