@@ -28,6 +28,7 @@
 
 #include <array>
 #include <atomic>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -45,25 +46,58 @@ using torch::autograd::AutogradContext;
 using torch::autograd::variable_list;
 
 // ------------------------------------------------------------------ runtime
-inline nott_ctx context(int device) {
+// One context per (device, stream): a context's workspace is used only by
+// launches on the stream it is bound to, so work that runs on different
+// streams at the same time never shares a workspace.
+namespace detail {
+inline std::mutex& ctx_mutex() {
     static std::mutex mu;
-    static std::array<nott_ctx, 64> ctxs{};
-    std::lock_guard<std::mutex> g(mu);
-    if (device < 0 || device >= (int)ctxs.size()) throw std::invalid_argument("Nott::HIP: bad device index");
-    if (!ctxs[device]) {
-        const int st = nott_create(device, &ctxs[device]);
-        if (st != NOTT_OK) throw std::runtime_error(std::string("nott_create: ") + nott_status_string(st));
-    }
-    return ctxs[device];
+    return mu;
+}
+inline std::map<std::pair<int, hipStream_t>, nott_ctx>& ctx_map() {
+    static std::map<std::pair<int, hipStream_t>, nott_ctx> m;
+    return m;
+}
+}  // namespace detail
+
+inline nott_ctx stream_context(int device, hipStream_t stream) {
+    if (device < 0 || device >= 64) throw std::invalid_argument("Nott::HIP: bad device index");
+    std::lock_guard<std::mutex> g(detail::ctx_mutex());
+    auto& m = detail::ctx_map();
+    auto it = m.find({device, stream});
+    if (it != m.end()) return it->second;
+    nott_ctx c = nullptr;
+    const int st = nott_create(device, &c);
+    if (st != NOTT_OK) throw std::runtime_error(std::string("nott_create: ") + nott_status_string(st));
+    nott_set_stream(c, (void*)stream);
+    m.emplace(std::make_pair(device, stream), c);
+    return c;
 }
 
-// The context of t's device, bound to that device's current HIP stream.
+// Workspace held by all contexts of `device`.
+inline int64_t device_workspace_bytes(int device) {
+    std::lock_guard<std::mutex> g(detail::ctx_mutex());
+    int64_t total = 0;
+    for (auto& kv : detail::ctx_map()) {
+        if (kv.first.first != device) continue;
+        int64_t b = 0;
+        if (nott_workspace_bytes(kv.second, &b) == NOTT_OK) total += b;
+    }
+    return total;
+}
+
+// The context of t's device and that device's current HIP stream.
 inline nott_ctx bind(const Tensor& t) {
     if (!t.is_cuda()) throw std::invalid_argument("Nott::HIP: tensor must live on a HIP device");
     const int dev = t.device().index();
-    nott_ctx c = context(dev);
-    nott_set_stream(c, (void*)c10::hip::getCurrentHIPStream(dev).stream());
-    return c;
+    return stream_context(dev, c10::hip::getCurrentHIPStream((c10::DeviceIndex)dev).stream());
+}
+
+// A HIP stream as the c10::Stream record_stream takes: tensors on these
+// devices report device type CUDA, so the stream goes under that type (same
+// stream id).
+inline c10::Stream as_tensor_stream(const c10::hip::HIPStream& s, int dev) {
+    return c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::CUDA, (c10::DeviceIndex)dev), s.id());
 }
 
 inline void check(int st, nott_ctx c, const char* what) {
@@ -115,19 +149,12 @@ class SideStreamScope {
         if (!active_) return;
         detail::Side& s = detail::side(dev);
         if (!s.ctx) {
-            nott_ctx c = nullptr;
-            const int st = nott_create(dev, &c);
-            if (st != NOTT_OK) throw std::runtime_error(std::string("nott_create: ") + nott_status_string(st));
             auto hs = c10::hip::getStreamFromPool(false, (c10::DeviceIndex)dev);
             s.stream = hs.stream();
-            // Tensors on this device report device type CUDA; record_stream
-            // wants the stream under the same device type (same stream id).
-            s.c10_stream = c10::Stream(c10::Stream::UNSAFE, c10::Device(c10::DeviceType::CUDA, (c10::DeviceIndex)dev),
-                                       hs.id());
-            detail::hip_ok(hipEventCreateWithFlags(&s.fork, hipEventDisableTiming), "side stream event");
-            detail::hip_ok(hipEventCreateWithFlags(&s.join, hipEventDisableTiming), "side stream event");
-            nott_set_stream(c, (void*)s.stream);
-            s.ctx = c;
+            s.c10_stream = as_tensor_stream(hs, dev);
+            for (hipEvent_t* e : {&s.fork, &s.join})
+                detail::hip_ok(hipEventCreateWithFlags(e, hipEventDisableTiming), "side stream event");
+            s.ctx = stream_context(dev, s.stream);
         }
         ++s.depth;
     }
@@ -164,9 +191,6 @@ inline nott_ctx wgrad_context(const Tensor& dy, std::initializer_list<Tensor> re
     s.pending = true;
     return s.ctx;
 }
-
-// The side stream's context of `dev`, or null before its first scope.
-inline nott_ctx side_context(int dev) { return detail::side(dev).ctx; }
 
 // The current stream of `dev` waits for the side stream's work.
 inline void join_side_stream(int dev) {

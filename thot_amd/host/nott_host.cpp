@@ -547,15 +547,8 @@ struct OptimizerHandle {
 
 PYBIND11_MODULE(_nott_host, m) {
     m.doc() = "C++ host layer (Nott::HIP) over libnott_hip: configs[0] and configs[4] training steps";
-    // Workspace of the device's contexts: the ordinary one and, once a
-    // trainer has run, the weight-gradient side stream's.
-    m.def("workspace_bytes", [](int device) {
-        int64_t b = 0, sb = 0;
-        nott_ctx c = NH::context(device);
-        NH::check(nott_workspace_bytes(c, &b), c, "workspace bytes");
-        if (nott_ctx sc = NH::side_context(device)) NH::check(nott_workspace_bytes(sc, &sb), sc, "workspace bytes");
-        return b + sb;
-    }, py::arg("device") = 0);
+    // Workspace held by the device's contexts (one per stream used).
+    m.def("workspace_bytes", [](int device) { return NH::device_workspace_bytes(device); }, py::arg("device") = 0);
     // Whether trainers run convolution weight gradients on the side stream
     // (on by default; the switch exists so tests can compare both orders).
     m.def("set_side_stream", [](bool on) { NH::set_side_stream_enabled(on); }, py::arg("on"));
