@@ -726,7 +726,7 @@ constexpr int NW = 4;                    // waves per workgroup, 32 fixed rows e
 constexpr int FIXED = 32 * NW;           // fixed rows per workgroup
 constexpr int TR = 64;                   // streamed rows per stage
 constexpr int TILE = TR * 128;           // one [64][64] bf16 tile
-constexpr int RING = 3;                  // stages in flight + 1
+constexpr int RING = 4;                  // stages in flight + 1
 constexpr float kLoTau = 1.f / 16;       // tile max of p above which the bf16 remainder is multiplied too
 
 __device__ __forceinline__ int toff64(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
