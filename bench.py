@@ -590,9 +590,9 @@ def group_ms(torch, wl, steps):
     return {k: sum(p[k][0].elapsed_time(p[k][1]) for p in pairs) / steps for k in wl.groups}
 
 
-def measure(torch, ops, wl, steps, warmup, cpu_budget):
-    """One leg: value from wall-clock steps, roofline from event-timed groups,
-    CPU baseline from the reference on a bounded sample."""
+def measure(torch, ops, wl, steps, warmup):
+    """One leg on the GPU: value from wall-clock steps, roofline from
+    event-timed groups."""
     wl.setup(torch, ops)
     ms = time_workload(torch, wl, steps, warmup)
     rec = {"value": round(wl.work_per_step() / (ms * 1e-3) / wl.scale, 3), "unit": wl.unit, "dtype": wl.dtype,
@@ -618,12 +618,15 @@ def measure(torch, ops, wl, steps, warmup, cpu_budget):
         rec["roofline"] = {"bound": "mfma", "kernel": f"{wl.name}: whole training step (model FLOPs)",
                            "achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s", "frac": round(ach / peak, 4),
                            "traffic": None}
-    if cpu_budget > 0:
-        try:
-            rec["cpu_baseline"] = wl.cpu_baseline(cpu_budget)
-        except Exception as e:  # reported, never fatal for the GPU measurement
-            rec["cpu_baseline"] = {"error": repr(e)}
     return rec
+
+
+def cpu_part(wl, budget):
+    """The reference's CPU path on a bounded sample of the leg's workload."""
+    try:
+        return wl.cpu_baseline(budget)
+    except Exception as e:  # reported, never fatal for the GPU measurement
+        return {"error": repr(e)}
 
 
 def main():
@@ -666,28 +669,32 @@ def main():
     TrainStep.graph = not args.eager
     dtype = args.dtype or DEFAULT_DTYPE[args.workload]
     cpu_budget = 0.0 if args.no_cpu else args.cpu_budget
-    head = measure(torch, ops, WORKLOADS[args.workload](dtype), args.steps, args.warmup, cpu_budget)
-    torch.cuda.empty_cache()
+    # Every GPU measurement runs before any CPU baseline: the baselines'
+    # worker threads keep spinning for a while after they finish, which slows
+    # the host launches of a GPU leg that follows.
+    head_wl = WORKLOADS[args.workload](dtype)
+    head = measure(torch, ops, head_wl, args.steps, args.warmup)
 
     legs = {}
+    kept = []
     if not args.no_extra and args.workload == "conv_bwd":
-        leg_budget = 0.0 if args.no_cpu else max(1.0, args.cpu_budget / 3)
         plan = [("conv_bwd", "bf16" if dtype == "f32" else "f32"), ("ln_bwd", "f32"), ("ln_bwd", "bf16"),
                 ("adamw", "f32"), ("adamw", "bf16"), ("xent", "f32"), ("xent", "bf16"), ("mha_bwd", "bf16"),
                 ("small_cnn", "f32"), ("resnet18", "bf16"), ("resnet18", "f32")]
-        cpu_done = {}
         for name, dt in plan:
             wl = WORKLOADS[name](dt)
-            # One CPU baseline per workload (the reference computes in fp32 only).
-            key = name
-            rec = measure(torch, ops, wl, args.steps, args.warmup, 0.0 if key in cpu_done else leg_budget)
-            if key in cpu_done:
-                rec["cpu_baseline"] = cpu_done[key]
-            elif "cpu_baseline" in rec:
-                cpu_done[key] = rec["cpu_baseline"]
-            legs[f"{name}_{dt}"] = rec
-            del wl
+            legs[f"{name}_{dt}"] = measure(torch, ops, wl, args.steps, args.warmup)
+            kept.append((name, dt, wl))
             torch.cuda.empty_cache()
+    if cpu_budget > 0:
+        head["cpu_baseline"] = cpu_part(head_wl, cpu_budget)
+        leg_budget = max(1.0, args.cpu_budget / 3)
+        cpu_done = {}
+        for name, dt, wl in kept:
+            # One CPU baseline per workload (the reference computes in fp32 only).
+            if name not in cpu_done:
+                cpu_done[name] = cpu_part(wl, leg_budget)
+            legs[f"{name}_{dt}"]["cpu_baseline"] = cpu_done[name]
 
     metric_part = {"conv_bwd": "conv-bwd TFLOP/s", "ln_bwd": "LN-bwd GB/s", "xent": "CE-grad GB/s",
                    "adamw": "AdamW GB/s", "mha_bwd": "MHA-bwd TFLOP/s", "small_cnn": "train samples/s",
