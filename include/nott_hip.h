@@ -103,6 +103,20 @@ int nott_conv2d_fwd_act(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtyp
 /* dgrad: dx = conv_transpose(dy, w).  (ATen convolution_backward, input grad) */
 int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
                          const void* dy, const void* w, void* dx);
+/* A 3x3 stride-1 layer's weights, re-laid out for the data gradient by the
+ * forward's own weight prep (one launch for both layouts) and kept by the
+ * caller until the backward: no counterpart in the reference (libtorch
+ * transforms the weights inside each convolution call); for host layers that
+ * run a layer's forward and backward in one step.
+ * nott_conv2d_dgrad_prep_bytes: size of wd for d (0 when the convolution does
+ * not take this path: then use nott_conv2d_fwd_act / nott_conv2d_bwd_data).
+ * nott_conv2d_fwd_prep: as nott_conv2d_fwd_act, and writes wd (16-byte aligned).
+ * nott_conv2d_bwd_data_prepped: as nott_conv2d_bwd_data, from wd. */
+int nott_conv2d_dgrad_prep_bytes(const nott_conv2d_desc* d, nott_dtype dtype, int64_t* bytes);
+int nott_conv2d_fwd_prep(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                         const void* x, const void* w, const float* b, int relu, void* y, void* wd);
+int nott_conv2d_bwd_data_prepped(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,
+                                 const void* dy, const void* wd, void* dx);
 /* wgrad: dw[k,c,r,s] = sum_{n,p,q} dy * x(shifted); db[k] = sum dy (db nullable).
  * dw, db fp32.  (ATen convolution_backward, weight and bias grads) */
 int nott_conv2d_bwd_weight(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype,

@@ -275,6 +275,29 @@ inline double conv_flops(const nott_conv2d_desc& d, const Tensor& y) {
     return 2.0 * (double)y.numel() * (double)d.c * (double)d.r * (double)d.s;
 }
 
+// When x needs a gradient and the layer takes the 3×3 stride-1 kernels, the
+// forward runs through nott_conv2d_fwd_prep, whose single weight-prep launch
+// also writes the data gradient's weight layout into the returned tensor
+// (saved for the backward, which then launches no prep); undefined
+// otherwise, and the caller runs its ordinary forward.
+inline Tensor prep_dgrad_weights(nott_ctx c, const nott_conv2d_desc& d, const Tensor& x, const Tensor& wc,
+                                 const Tensor& b, int relu, Tensor& y) {
+    int64_t bytes = 0;
+    if (!x.requires_grad() || nott_conv2d_dgrad_prep_bytes(&d, dtype_of(x), &bytes) != NOTT_OK || bytes == 0)
+        return Tensor();
+    Tensor wd = torch::empty({bytes}, x.options().dtype(torch::kUInt8));
+    check(nott_conv2d_fwd_prep(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), relu, ptr(y), wd.data_ptr()), c,
+          "conv2d forward");
+    return wd;
+}
+inline void dgrad_with(nott_ctx c, const nott_conv2d_desc& d, const Tensor& dy, const Tensor& wc, const Tensor& wd,
+                       Tensor& dx) {
+    if (wd.defined())
+        check(nott_conv2d_bwd_data_prepped(c, &d, dtype_of(dy), ptr(dy), wd.data_ptr(), ptr(dx)), c, "conv2d dgrad");
+    else
+        check(nott_conv2d_bwd_data(c, &d, dtype_of(dy), ptr(dy), ptr(wc), ptr(dx)), c, "conv2d dgrad");
+}
+
 struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
     static nott_conv2d_desc desc(const Tensor& x, const Tensor& w, const std::vector<int64_t>& g) {
         nott_conv2d_desc d{};
@@ -293,15 +316,16 @@ struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
         const int64_t q = (d.w + 2 * d.pad_w - d.dil_w * (d.s - 1) - 1) / d.stride_w + 1;
         Tensor y = torch::empty({d.n, d.k, p, q}, x.options());
         nott_ctx c = bind(x);
-        check(nott_conv2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), ptr(y)), c, "conv2d forward");
-        ctx->save_for_backward({x, w, wc, b});
+        Tensor wd = prep_dgrad_weights(c, d, x, wc, b, 0, y);
+        if (!wd.defined()) check(nott_conv2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), ptr(y)), c, "conv2d forward");
+        ctx->save_for_backward({x, w, wc, b, wd});
         ctx->saved_data["geom"] = geom;
         ctx->saved_data["needs_dx"] = x.requires_grad();
         return y;
     }
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
         auto s = ctx->get_saved_variables();
-        Tensor x = s[0], w = s[1], wc = s[2], b = s[3];
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3], wd = s[4];
         Tensor dy = contig(grads[0]);
         const auto geom = ctx->saved_data["geom"].toIntVector();
         const nott_conv2d_desc d = desc(x, wc, geom);
@@ -309,7 +333,7 @@ struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
         Tensor dx;
         if (ctx->saved_data["needs_dx"].toBool()) {
             dx = torch::empty_like(x);
-            check(nott_conv2d_bwd_data(c, &d, dtype_of(dy), ptr(dy), ptr(wc), ptr(dx)), c, "conv2d dgrad");
+            dgrad_with(c, d, dy, wc, wd, dx);
         }
         Tensor gw = grad_buffer(w), gb = grad_buffer(b);
         if (gw.defined() || gb.defined()) {
@@ -332,15 +356,17 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
         const int64_t q = (d.w + 2 * d.pad_w - d.dil_w * (d.s - 1) - 1) / d.stride_w + 1;
         Tensor y = torch::empty({d.n, d.k, p, q}, x.options());
         nott_ctx c = bind(x);
-        check(nott_conv2d_fwd_act(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), 1, ptr(y)), c, "conv2d+relu forward");
-        ctx->save_for_backward({x, w, wc, b, y});
+        Tensor wd = prep_dgrad_weights(c, d, x, wc, b, 1, y);
+        if (!wd.defined())
+            check(nott_conv2d_fwd_act(c, &d, dtype_of(x), ptr(x), ptr(wc), fptr(b), 1, ptr(y)), c, "conv2d+relu forward");
+        ctx->save_for_backward({x, w, wc, b, y, wd});
         ctx->saved_data["geom"] = geom;
         ctx->saved_data["needs_dx"] = x.requires_grad();
         return y;
     }
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
         auto s = ctx->get_saved_variables();
-        Tensor x = s[0], w = s[1], wc = s[2], b = s[3], y = s[4];
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3], y = s[4], wd = s[5];
         Tensor dy = contig(grads[0]);
         const auto geom = ctx->saved_data["geom"].toIntVector();
         const nott_conv2d_desc d = Conv2dFn::desc(x, wc, geom);
@@ -350,7 +376,7 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
         Tensor dx;
         if (ctx->saved_data["needs_dx"].toBool()) {
             dx = torch::empty_like(x);
-            check(nott_conv2d_bwd_data(c, &d, dtype_of(dz), ptr(dz), ptr(wc), ptr(dx)), c, "conv2d dgrad");
+            dgrad_with(c, d, dz, wc, wd, dx);
         }
         Tensor gw = grad_buffer(w), gb = grad_buffer(b);
         if (gw.defined() || gb.defined()) {

@@ -359,3 +359,68 @@ def test_conv_fwd_relu_fused(ops, dt, case):
     yr = ops.conv2d_fwd(xd, wd, bd, d, relu=True)
     torch.cuda.synchronize()
     assert torch.equal(yr, torch.relu(y))
+
+
+PREP_CASES = [
+    (2, 64, 14, 14, 64),     # one 64-channel block each way
+    (2, 32, 9, 7, 96),       # a partial last block of output channels
+    (4, 128, 7, 7, 256),     # channel splits (small grid)
+    (1, 64, 28, 28, 128),
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("case", PREP_CASES)
+def test_conv_prepared_dgrad_weights(ops, dt, case):
+    """nott_conv2d_fwd_prep writes the data gradient's weight layout from the
+    forward's own weight prep; its output and the prepared data gradient equal
+    nott_conv2d_fwd_act / nott_conv2d_bwd_data bit for bit."""
+    import ctypes as C
+    from thot_amd import _abi
+    n, c, h, w, k = case
+    tdt = torch.float32 if dt == "f32" else torch.bfloat16
+    code = _abi.NOTT_F32 if dt == "f32" else _abi.NOTT_BF16
+    g = torch.Generator(device="cuda").manual_seed(n * 1000 + c + k)
+    x = torch.randn((n, c, h, w), generator=g, device="cuda").to(tdt)
+    wt = (torch.randn((k, c, 3, 3), generator=g, device="cuda") / math.sqrt(9 * c)).to(tdt)
+    b = torch.randn((k,), generator=g, device="cuda")
+    dy = torch.randn((n, k, h, w), generator=g, device="cuda").to(tdt)
+    d = ops.conv_desc((n, c, h, w), (k, c, 3, 3), padding=(1, 1))
+    nb = C.c_int64()
+    assert ops.context(0).lib.nott_conv2d_dgrad_prep_bytes(C.byref(d), code, C.byref(nb)) == 0
+    assert nb.value > 0
+    wd = torch.empty((nb.value,), dtype=torch.uint8, device="cuda")
+    P = lambda t: C.c_void_p(t.data_ptr())
+    fb = C.cast(b.data_ptr(), C.POINTER(C.c_float))
+    ctx = ops.context(0)
+    for relu in (0, 1):
+        y0, y1 = torch.empty((n, k, h, w), dtype=tdt, device="cuda"), torch.empty((n, k, h, w), dtype=tdt, device="cuda")
+        ctx.call("nott_conv2d_fwd_act", C.byref(d), code, P(x), P(wt), fb, relu, P(y0))
+        ctx.call("nott_conv2d_fwd_prep", C.byref(d), code, P(x), P(wt), fb, relu, P(y1), P(wd))
+        torch.cuda.synchronize()
+        assert torch.equal(y0, y1), relu
+    dx0, dx1 = torch.empty_like(x), torch.empty_like(x)
+    ctx.call("nott_conv2d_bwd_data", C.byref(d), code, P(dy), P(wt), P(dx0))
+    ctx.call("nott_conv2d_bwd_data_prepped", C.byref(d), code, P(dy), P(wd), P(dx1))
+    torch.cuda.synchronize()
+    assert torch.equal(dx0, dx1)
+
+
+@pytest.mark.gpu
+def test_conv_prepared_dgrad_weights_other_shapes(ops):
+    """Convolutions outside the 3x3 stride-1 kernels report no prepared
+    layout, and the prepared entry points refuse them."""
+    import ctypes as C
+    from thot_amd import _abi
+    nb = C.c_int64()
+    for xs, ws, st, pd in (((2, 64, 14, 14), (64, 64, 3, 3), (2, 2), (1, 1)),
+                           ((2, 64, 14, 14), (128, 64, 1, 1), (1, 1), (0, 0)),
+                           ((2, 3, 32, 32), (64, 3, 7, 7), (2, 2), (3, 3))):
+        d = ops.conv_desc(xs, ws, stride=st, padding=pd)
+        assert ops.context(0).lib.nott_conv2d_dgrad_prep_bytes(C.byref(d), _abi.NOTT_BF16, C.byref(nb)) == 0
+        assert nb.value == 0, (xs, ws)
+        x = torch.zeros(xs, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(_abi.NottInvalidArgument):
+            ops.context(0).call("nott_conv2d_bwd_data_prepped", C.byref(d), _abi.NOTT_BF16, C.c_void_p(x.data_ptr()),
+                                C.c_void_p(x.data_ptr()), C.c_void_p(x.data_ptr()))

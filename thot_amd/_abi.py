@@ -64,6 +64,9 @@ SIGNATURES: dict[str, list] = {
     "nott_conv2d_fwd": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, vp],
     "nott_conv2d_fwd_act": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, i32, vp],
     "nott_conv2d_bwd_data": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, vp],
+    "nott_conv2d_dgrad_prep_bytes": [C.POINTER(Conv2dDesc), i32, C.POINTER(i64)],
+    "nott_conv2d_fwd_prep": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, i32, vp, vp],
+    "nott_conv2d_bwd_data_prepped": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, vp],
     "nott_conv2d_bwd_weight": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, fp, i32],
     "nott_linear_fwd": [vp, i32, i64, i64, i64, vp, vp, fp, vp],
     "nott_linear_bwd": [vp, i32, i64, i64, i64, vp, vp, vp, vp, fp, fp, i32],

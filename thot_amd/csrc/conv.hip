@@ -826,6 +826,60 @@ extern "C" int nott_conv2d_bwd_data(nott_ctx ctx, const nott_conv2d_desc* d, not
     return dtype == NOTT_F32 ? dgrad<float>(ctx, d, p, q, dy, w, dx) : dgrad<bf16_t>(ctx, d, p, q, dy, w, dx);
 }
 
+// The 3×3 stride-1 pass a layer's forward and data gradient both take: its
+// weights are re-laid out once per forward for both.
+static bool prep_pair_applies(const nott_conv2d_desc* d, nott_dtype dtype) {
+    const size_t e = dtype == NOTT_F32 ? 4 : 2;
+    return nott::conv_fast::fwd_applies(d, e) && nott::conv_fast::dgrad_applies(d, e);
+}
+
+extern "C" int nott_conv2d_dgrad_prep_bytes(const nott_conv2d_desc* d, nott_dtype dtype, int64_t* bytes) {
+    if (!d || !bytes || !nott::valid_dtype(dtype)) return NOTT_ERR_INVALID_ARG;
+    *bytes = (d->n > 0 && d->groups == 1 && d->layout == NOTT_NCHW && prep_pair_applies(d, dtype))
+                 ? nott::conv_fast::dgrad_prep_elems(d) * (dtype == NOTT_F32 ? 4 : 2)
+                 : 0;
+    return NOTT_OK;
+}
+
+extern "C" int nott_conv2d_fwd_prep(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x,
+                                    const void* w, const float* b, int relu, void* y, void* wd) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_fwd_prep: bad dtype");
+    NOTT_REQUIRE(ctx, relu == 0 || relu == 1, "nott_conv2d_fwd_prep: relu must be 0 or 1");
+    int64_t p, q;
+    int st = check_desc(ctx, d, &p, &q);
+    if (st != NOTT_OK) return st;
+    NOTT_REQUIRE(ctx, d->n > 0 && prep_pair_applies(d, dtype),
+                 "nott_conv2d_fwd_prep: not a 3x3 stride-1 convolution with prepared data-gradient weights "
+                 "(nott_conv2d_dgrad_prep_bytes gives 0)");
+    NOTT_REQUIRE(ctx, x && w && y && wd, "nott_conv2d_fwd_prep: null buffer");
+    NOTT_REQUIRE(ctx, ((uintptr_t)wd % 16) == 0, "nott_conv2d_fwd_prep: wd must be 16-byte aligned");
+    nott::DeviceScope scope(ctx->device);
+    if (dtype == NOTT_F32)
+        return nott::conv_fast::fwd_prep<float>(ctx, d, static_cast<const float*>(x), static_cast<const float*>(w), b,
+                                                static_cast<float*>(y), relu, static_cast<float*>(wd));
+    return nott::conv_fast::fwd_prep<bf16_t>(ctx, d, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(w), b,
+                                             static_cast<bf16_t*>(y), relu, static_cast<bf16_t*>(wd));
+}
+
+extern "C" int nott_conv2d_bwd_data_prepped(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* dy,
+                                            const void* wd, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_conv2d_bwd_data_prepped: bad dtype");
+    int64_t p, q;
+    int st = check_desc(ctx, d, &p, &q);
+    if (st != NOTT_OK) return st;
+    NOTT_REQUIRE(ctx, d->n > 0 && prep_pair_applies(d, dtype),
+                 "nott_conv2d_bwd_data_prepped: not a convolution nott_conv2d_fwd_prep prepares");
+    NOTT_REQUIRE(ctx, dy && wd && dx, "nott_conv2d_bwd_data_prepped: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    if (dtype == NOTT_F32)
+        return nott::conv_fast::dgrad_prepared<float>(ctx, d, static_cast<const float*>(dy), static_cast<const float*>(wd),
+                                                      static_cast<float*>(dx));
+    return nott::conv_fast::dgrad_prepared<bf16_t>(ctx, d, static_cast<const bf16_t*>(dy),
+                                                   static_cast<const bf16_t*>(wd), static_cast<bf16_t*>(dx));
+}
+
 extern "C" int nott_conv2d_bwd_weight(nott_ctx ctx, const nott_conv2d_desc* d, nott_dtype dtype, const void* x,
                                       const void* dy, float* dw, float* db, int accumulate) {
     NOTT_CHECK_CTX(ctx);

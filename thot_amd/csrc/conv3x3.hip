@@ -82,6 +82,36 @@ __global__ __launch_bounds__(256) void conv3x3_wprep_kernel(const T* __restrict_
 }
 
 
+// Both layouts of one weight tensor in one launch: blockIdx.z below cbf
+// writes the forward slices (conv3x3_wprep_kernel<T, false> of w as
+// [cout][cin]), the rest the data-gradient slices (<T, true>, cout and cin
+// exchanged) into wd.
+template <typename T>
+__global__ __launch_bounds__(256) void conv3x3_wprep2_kernel(const T* __restrict__ w, T* __restrict__ wf,
+                                                             T* __restrict__ wd, int32_t cout, int32_t cin,
+                                                             int32_t cbf) {
+    constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
+    constexpr int32_t SLICE = 9 * kTileCo * CC;
+    const int32_t j = (int32_t)blockIdx.x * 256 + (int32_t)threadIdx.x;
+    const bool dg = (int32_t)blockIdx.z >= cbf;
+    // in the data gradient's terms the input channels are cout, the outputs cin
+    const int32_t ocount = dg ? cin : cout, icount = dg ? cout : cin;
+    const int32_t cc = blockIdx.y, cb = dg ? (int32_t)blockIdx.z - cbf : (int32_t)blockIdx.z;
+    if (j >= SLICE || cc >= icount / CC) return;
+    const int32_t tap = j / (kTileCo * CC), rem = j % (kTileCo * CC);
+    const int32_t cil = dg ? rem / kTileCo : rem % CC;
+    const int32_t col = dg ? rem % kTileCo : rem / CC;
+    const int32_t co = cb * kTileCo + col, ci = cc * CC + cil;
+    const int32_t r = tap / 3, s = tap % 3;
+    const int64_t src = dg ? (((int64_t)ci * cin + co) * 9 + (2 - r) * 3 + (2 - s))
+                           : (((int64_t)co * cin + ci) * 9 + r * 3 + s);
+    T val = T(0);
+    if (co < ocount) val = w[src];
+    T* dst = dg ? wd : wf;
+    const int64_t slice = ((int64_t)cb * (icount / CC) + cc) * SLICE;
+    dst[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = val;
+}
+
 template <typename T, bool VEC, int LW>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
                                                                   const float* __restrict__ bias, T* __restrict__ out,
@@ -411,9 +441,15 @@ size_t same_lds_bytes(int32_t h, int32_t w, size_t elem) {
 constexpr size_t kSameLdsMax = 80 * 1024;   // two workgroups per CU
 
 
+// Elements of the prepared weight slices of a cin → cout 3×3 pass.
+int64_t prep_elems(int64_t cin, int64_t cout) { return ceil_div(cout, kTileCo) * kTileCo * cin * 9; }
+
+// wsrc is w in the pass's own terms; `prepared` (optional) is its slices
+// already written by a prep launch; `dg_out` (forward only, optional)
+// receives the data gradient's slices of w from the same prep launch.
 template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
-             const float* bias, T* out, int relu = 0) {
+             const float* bias, T* out, int relu = 0, const T* prepared = nullptr, T* dg_out = nullptr) {
     constexpr int CC = Chunk<T>::CC;
     const int64_t cbc = ceil_div(cout, kTileCo);                 // 64-channel blocks (the last may be partial)
     const size_t wbytes = sizeof(T) * (size_t)cbc * kTileCo * cin * 9;
@@ -436,8 +472,17 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     char* ws = static_cast<char*>(workspace(ctx, wbytes_al + pbytes));
     if (!ws) return NOTT_ERR_ALLOC;
     T* wp = reinterpret_cast<T*>(ws);
-    hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(9 * kTileCo * CC, 256), (unsigned)(cin / CC),
-                       (unsigned)cbc), dim3(256), 0, ctx->stream, wsrc, wp, cout, cin);
+    if (prepared) {
+        wp = const_cast<T*>(prepared);
+    } else if (dg_out) {
+        const int64_t cbd = ceil_div(cin, kTileCo);
+        hipLaunchKernelGGL(conv3x3_wprep2_kernel<T>, dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),
+                           (unsigned)(std::max(cin, cout) / CC), (unsigned)(cbc + cbd)), dim3(256), 0, ctx->stream,
+                           wsrc, wp, dg_out, cout, cin, (int32_t)cbc);
+    } else {
+        hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),
+                           (unsigned)(cin / CC), (unsigned)cbc), dim3(256), 0, ctx->stream, wsrc, wp, cout, cin);
+    }
     SameParams p;
     p.n = n; p.cin = cin; p.h = h; p.w = w; p.cout = cout;
     p.hw = h * w; p.w2 = row_pitch(w); p.npix = n * h * w; p.in_rows = in_rows;
@@ -861,6 +906,22 @@ int dgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* w, T* d
                              nullptr, dx);
 }
 
+// The forward with the data gradient's weight slices written by the same
+// prep launch, and the data gradient from such slices.
+template <typename T>
+int fwd_prep(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu, T* wd) {
+    return run_same<T, false>(ctx, (int32_t)d->n, (int32_t)d->c, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, x, w, b, y,
+                              relu, nullptr, wd);
+}
+
+template <typename T>
+int dgrad_prepared(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* wd, T* dx) {
+    return run_same<T, true>(ctx, (int32_t)d->n, (int32_t)d->k, (int32_t)d->h, (int32_t)d->w, (int32_t)d->c, dy, nullptr,
+                             nullptr, dx, 0, wd);
+}
+
+int64_t dgrad_prep_elems(const nott_conv2d_desc* d) { return prep_elems(d->k, d->c); }
+
 template <typename T, int LW>
 int wgrad_p(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
     switch (wgrad_slot_pitch(d->w)) {
@@ -887,6 +948,12 @@ template int fwd<float>(nott_ctx, const nott_conv2d_desc*, const float*, const f
 template int fwd<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, const float*, bf16_t*, int);
 template int dgrad<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, float*);
 template int dgrad<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, bf16_t*);
+template int fwd_prep<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, const float*, float*, int,
+                             float*);
+template int fwd_prep<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, const float*, bf16_t*,
+                              int, bf16_t*);
+template int dgrad_prepared<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, float*);
+template int dgrad_prepared<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, bf16_t*);
 template int wgrad<float>(nott_ctx, const nott_conv2d_desc*, const float*, const float*, float*, int);
 template int wgrad<bf16_t>(nott_ctx, const nott_conv2d_desc*, const bf16_t*, const bf16_t*, float*, int);
 

@@ -8,6 +8,14 @@ namespace conv_fast {
 
 bool fwd_applies(const nott_conv2d_desc* d, size_t elem);
 bool dgrad_applies(const nott_conv2d_desc* d, size_t elem);
+// The 3×3 forward that also writes the data gradient's weight slices (one
+// prep launch for both layouts), the data gradient from those slices, and
+// their element count.  Both need fwd_applies and dgrad_applies.
+template <typename T>
+int fwd_prep(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, const float* b, T* y, int relu, T* wd);
+template <typename T>
+int dgrad_prepared(nott_ctx ctx, const nott_conv2d_desc* d, const T* dy, const T* wd, T* dx);
+int64_t dgrad_prep_elems(const nott_conv2d_desc* d);
 bool wgrad_applies(const nott_conv2d_desc* d, size_t elem);
 
 template <typename T>
