@@ -678,9 +678,12 @@ def main():
     legs = {}
     kept = []
     if not args.no_extra and args.workload == "conv_bwd":
-        plan = [("conv_bwd", "bf16" if dtype == "f32" else "f32"), ("ln_bwd", "f32"), ("ln_bwd", "bf16"),
-                ("adamw", "f32"), ("adamw", "bf16"), ("xent", "f32"), ("xent", "bf16"), ("mha_bwd", "bf16"),
-                ("small_cnn", "f32"), ("resnet18", "bf16"), ("resnet18", "f32")]
+        # The training steps run right after the conv legs: their eager
+        # steps issue ~300 launches each and are the legs most sensitive to
+        # host-side state left behind by the multi-GB element-wise legs.
+        plan = [("conv_bwd", "bf16" if dtype == "f32" else "f32"), ("small_cnn", "f32"), ("resnet18", "bf16"),
+                ("resnet18", "f32"), ("ln_bwd", "f32"), ("ln_bwd", "bf16"), ("adamw", "f32"), ("adamw", "bf16"),
+                ("xent", "f32"), ("xent", "bf16"), ("mha_bwd", "bf16")]
         for name, dt in plan:
             wl = WORKLOADS[name](dt)
             legs[f"{name}_{dt}"] = measure(torch, ops, wl, args.steps, args.warmup)
