@@ -47,7 +47,7 @@ METRIC = "train samples/s; conv-bwd TFLOP/s (%MFMA peak); LN-bwd+AdamW GB/s (%HB
 # The passes and their commands are in profiles/.  Keyed by (workload, dtype,
 # kernel group); None where no pass has been recorded.
 TRAFFIC = {
-    ("conv_bwd", "f32", "dgrad"): 416.03e6,    # conv3x3_wprep + conv3x3_same
+    ("conv_bwd", "f32", "dgrad"): 446.25e6,    # conv3x3_wprep + conv3x3_same + conv3x3_split_reduce (tail tiles)
     ("conv_bwd", "f32", "wgrad"): 385.08e6,    # conv3x3_wgrad + conv3x3_wgrad_reduce
     ("conv_bwd", "bf16", "dgrad"): 182.82e6,
     ("conv_bwd", "bf16", "wgrad"): 230.20e6,

@@ -345,6 +345,39 @@ def test_conv3x3_large_grids(ops, case):
     check(host(dx), host(ref_dx), "bf16", "dx vs torch fp32")
 
 
+# fp32 3x3 grids of a little more than one round of workgroup slots (512 on
+# 256 CUs) with one output-channel block: the last tiles are split over their
+# channel chunks in the same launch (4 pieces each for 64 input channels, 8
+# for 128) and summed by the split reduce; the last tile is partial.
+TAIL3X3 = [
+    (42, 64, 56, 56, 64),      # forward and dgrad: 515 tiles, 3 split 4 ways
+    (43, 64, 56, 56, 128),     # dgrad (128 -> 64 channels): 527 tiles, 15 split 8 ways
+]
+
+
+@pytest.mark.parametrize("case", TAIL3X3)
+def test_conv3x3_tail_split_fp32(ops, case):
+    """fp32 forward (with bias) and dgrad whose last partial round of tiles is
+    split, against torch's fp32 convolution; images in the split tail and
+    before it are both checked."""
+    n, c, h, w_, k = case
+    d = ops.conv_desc((n, c, h, w_), (k, c, 3, 3), padding=(1, 1))
+    gen = torch.Generator(device="cuda").manual_seed(sum(case))
+    x = torch.randn((n, c, h, w_), generator=gen, device="cuda")
+    w = torch.randn((k, c, 3, 3), generator=gen, device="cuda") / math.sqrt(c * 9)
+    b = torch.randn((k,), generator=gen, device="cuda")
+    dy = torch.randn((n, k, h, w_), generator=gen, device="cuda")
+    y = ops.conv2d_fwd(x, w, b, d)
+    dx = ops.conv2d_bwd_data(dy, w, d)
+    torch.cuda.synchronize()
+    ref_y = torch.nn.functional.conv2d(x, w, b, padding=1)
+    ref_dx = torch.nn.grad.conv2d_input((n, c, h, w_), w, dy, padding=1)
+    check(host(y), host(ref_y), "f32", "y vs torch fp32")
+    check(host(dx), host(ref_dx), "f32", "dx vs torch fp32")
+    # the last images (the split tail) on their own
+    check(host(dx[-3:]), host(ref_dx[-3:]), "f32", "dx tail images")
+
+
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("case", [CONV[5], CONV[6], CONV[2], CONV[3], (2, 32, 10, 10, 64, 3, 3, 1, 1, 1)],
                          ids=lambda c: "n{}c{}h{}w{}k{}r{}s{}st{}".format(*c[:8]))

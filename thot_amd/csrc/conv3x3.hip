@@ -43,8 +43,12 @@ struct SameParams {
     int32_t remap;             // XCD-aware block remap active
     int32_t vec_store;         // 16-byte output runs stay inside one image plane
     int32_t relu;              // ReLU on the output (forward with a fused activation)
-    int32_t cc_per_split;      // channel chunks per blockIdx.z split
-    float* partial;            // split partials [split][cout][npix] (fp32, no bias), or null
+    int32_t cc_per_split;      // channel chunks per split (blockIdx.z, or per tail piece)
+    int32_t remap_n;           // blocks under the XCD remap (a multiple of 8)
+    int32_t tail_first;        // tail split: blocks ≥ tail_first are pieces of tiles ≥ tail_first
+    int32_t tail_splits;       // pieces per tail tile (0: no tail split)
+    int32_t part_m0, part_npix;   // pixels [part_m0, part_m0 + part_npix) have partials
+    float* partial;            // split partials [split][cout][part_npix] (fp32, no bias), or null
     FastDiv fd_hw, fd_w, fd_w2, fd_h2;
 };
 
@@ -124,8 +128,28 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 
     // Block -> pixel tile.  Consecutive tiles share halo rows; with the
     // remap, tiles that run on the same XCD (block ids ≡ mod 8) are adjacent.
-    int32_t tile = blockIdx.x;
-    if (p.remap) tile = (int32_t)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3));
+    // Tail split (one channel block, more tiles than one round of slots):
+    // blocks below tail_first are whole tiles, the rest are tail_splits
+    // channel-chunk pieces of each later tile, which fill the slots that the
+    // last whole tiles leave free instead of running a round of their own.
+    int32_t tile = blockIdx.x, split = blockIdx.z;
+    bool part = p.partial != nullptr;
+    int32_t cc0 = split * p.cc_per_split, cc1 = min(p.cin / CC, cc0 + p.cc_per_split);
+    if (p.tail_splits > 0) {
+        if (tile >= p.tail_first) {
+            const int32_t q = tile - p.tail_first;
+            tile = p.tail_first + q / p.tail_splits;
+            split = q - (tile - p.tail_first) * p.tail_splits;
+            cc0 = split * p.cc_per_split;
+            cc1 = min(p.cin / CC, cc0 + p.cc_per_split);
+        } else {
+            part = false;
+            cc0 = 0;
+            cc1 = p.cin / CC;
+        }
+    }
+    if (p.remap && tile < p.remap_n)
+        tile = (int32_t)((tile & 7) * (p.remap_n >> 3) + (tile >> 3));
     const int32_t cb = blockIdx.y;
     const int32_t m0 = tile * kTilePix;
     const int32_t m_last = min(m0 + kTilePix, p.npix) - 1;
@@ -177,9 +201,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Channel chunks [cc0, cc1) of this split (all of them without split-K).
-    const int32_t cc0 = blockIdx.z * p.cc_per_split;
-    const int32_t cc1 = min(p.cin / CC, cc0 + p.cc_per_split);
+    // Channel chunks [cc0, cc1) of this split or piece (all of them for a whole tile).
     const T* wblk = wp + (int64_t)cb * (p.cin / CC) * 9 * kTileCo * CC;
 
     // Vector fill: task = (w-chunk of SUB pixels, padded row, channel group of
@@ -314,23 +336,23 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
         }
     }
 
-    if (p.partial) {
+    if (part) {
         // Split-K: fp32 partial sums straight from the accumulators; lane holds
         // pixels 4·(lane/16) + e (consecutive, 16-byte aligned) of column co.
-        float* dst = p.partial + (int64_t)blockIdx.z * p.cout * p.npix;
+        float* dst = p.partial + (int64_t)split * p.cout * p.part_npix;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
             const int32_t co = cb * kTileCo + nt * 16 + r16;
             if (co >= p.cout) continue;
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {
-                const int32_t m = m0 + wid * 64 + mt * 16 + kq * 4;
+                const int32_t m = m0 + wid * 64 + mt * 16 + kq * 4, ml = m - p.part_m0;
                 if (m + 3 <= m_last) {
-                    *reinterpret_cast<f32x4*>(dst + (int64_t)co * p.npix + m) = acc[mt][nt];
+                    *reinterpret_cast<f32x4*>(dst + (int64_t)co * p.part_npix + ml) = acc[mt][nt];
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (m + e <= m_last) dst[(int64_t)co * p.npix + m + e] = acc[mt][nt][e];
+                        if (m + e <= m_last) dst[(int64_t)co * p.part_npix + ml + e] = acc[mt][nt][e];
                 }
             }
         }
@@ -383,19 +405,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __re
     }
 }
 
-// out[n][co][hw] = bias[co] + Σ_split partial[split][co][m] (m = n·hw + hw),
-// splits added in order.  Thread = 4 consecutive pixels of one channel.
+// out[n][co][hw] = bias[co] + Σ_split partial[split][co][m − m0] for the
+// npix pixels m = n·hw + hw from m0 on (m0 a multiple of 4), splits added in
+// order.  Thread = 4 consecutive pixels of one channel.
 template <typename T>
 __global__ __launch_bounds__(256) void conv3x3_split_reduce_kernel(const float* __restrict__ partial, int32_t splits,
-                                                                   int32_t cout, int32_t npix, FastDiv fd_hw,
-                                                                   int32_t hw, const float* __restrict__ bias,
+                                                                   int32_t cout, int32_t m0, int32_t npix,
+                                                                   FastDiv fd_hw, int32_t hw,
+                                                                   const float* __restrict__ bias,
                                                                    T* __restrict__ out, int relu) {
     const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;     // group of 4 pixels
     const int32_t groups = npix >> 2;
     if (q >= (int64_t)groups * cout) return;
-    const int32_t co = (int32_t)(q / groups), m = (int32_t)(q - (int64_t)co * groups) * 4;
+    const int32_t co = (int32_t)(q / groups), ml = (int32_t)(q - (int64_t)co * groups) * 4, m = m0 + ml;
     const int64_t stride = (int64_t)cout * npix;
-    const f32x4 s = ordered_sum4(partial + (int64_t)co * npix + m, stride, splits);
+    const f32x4 s = ordered_sum4(partial + (int64_t)co * npix + ml, stride, splits);
     const float bv = bias ? bias[co] : 0.f;
     f32x4 v;
 #pragma unroll
@@ -457,18 +481,31 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     if (same_lds_bytes(h, w, sizeof(T)) > kSameLdsMax)
         return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3: tile does not fit in LDS");
     // Split the channel chunks over blockIdx.z when the grid leaves
-    // workgroup slots (two per CU) idle (small images, many channels).
+    // workgroup slots (two per CU) idle (small images, many channels); split
+    // only the tiles of a last, partly filled round when the grid has more
+    // tiles than slots (one channel block).
     const int64_t tiles = ceil_div((int64_t)n * h * w, kTilePix);
     const int64_t blocks = tiles * cbc;
+    const int64_t slots = 2 * (int64_t)ctx->num_cu;
     const int32_t nchunks = cin / CC;
-    int32_t splits = 1;
+    int32_t splits = 1, tail = 1;
     const int64_t npix64 = (int64_t)n * h * w;
-    if (blocks < 2 * (int64_t)ctx->num_cu && nchunks > 1 && npix64 % 4 == 0)
-        splits = pick_chunk_splits(blocks, nchunks, 2 * (int64_t)ctx->num_cu, sizeof(T));
-    const int32_t cc_per_split = (int32_t)ceil_div(nchunks, splits);
-    splits = (int32_t)ceil_div(nchunks, cc_per_split);
+    if (blocks < slots && nchunks > 1 && npix64 % 4 == 0)
+        splits = pick_chunk_splits(blocks, nchunks, slots, sizeof(T));
+    else if (cbc == 1 && nchunks > 1 && npix64 % 4 == 0)
+        tail = pick_tail_splits(blocks, nchunks, slots, sizeof(T));
+    const int32_t cc_per_split = (int32_t)ceil_div(nchunks, std::max(splits, tail));
+    if (tail > 1)
+        tail = (int32_t)ceil_div(nchunks, cc_per_split);
+    else
+        splits = (int32_t)ceil_div(nchunks, cc_per_split);
+    const int64_t tail_tiles = tail > 1 ? blocks % slots : 0;
+    const int64_t tail_first = tiles - tail_tiles;
+    const int64_t part_m0 = tail > 1 ? tail_first * kTilePix : 0;
+    const int64_t part_npix = npix64 - part_m0;
+    const int32_t nsplit = std::max(splits, tail);      // partial planes
     const size_t wbytes_al = (wbytes + 255) & ~(size_t)255;
-    const size_t pbytes = splits > 1 ? sizeof(float) * (size_t)splits * cout * (size_t)npix64 : 0;
+    const size_t pbytes = nsplit > 1 ? sizeof(float) * (size_t)nsplit * cout * (size_t)part_npix : 0;
     char* ws = static_cast<char*>(workspace(ctx, wbytes_al + pbytes));
     if (!ws) return NOTT_ERR_ALLOC;
     T* wp = reinterpret_cast<T*>(ws);
@@ -492,8 +529,13 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     p.fd_h2 = FastDiv((uint32_t)(h + 2));
     p.cc_per_split = cc_per_split;
     p.relu = relu;
-    p.partial = splits > 1 ? reinterpret_cast<float*>(ws + wbytes_al) : nullptr;
-    p.remap = (tiles % 8 == 0) ? 1 : 0;
+    p.partial = nsplit > 1 ? reinterpret_cast<float*>(ws + wbytes_al) : nullptr;
+    p.tail_splits = tail > 1 ? tail : 0;
+    p.tail_first = (int32_t)tail_first;
+    p.part_m0 = (int32_t)part_m0;
+    p.part_npix = (int32_t)part_npix;
+    p.remap_n = (int32_t)tail_first;        // whole tiles (all of them without a tail split)
+    p.remap = (tail_first % 8 == 0) ? 1 : 0;
     p.vec_store = ((h * w) % (16 / (int)sizeof(T)) == 0 && ((uintptr_t)out % 16) == 0) ? 1 : 0;
     // Vector fill when the input is 16-byte aligned and image rows split into
     // 16- or 8-byte pieces (narrower pieces measured slower than the element
@@ -507,7 +549,8 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
                      : lw == 4  ? reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, 4>)
                                 : reinterpret_cast<const void*>(&conv3x3_same_kernel<T, true, sizeof(T) == 2 ? 2 : 4>);
     (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024);
-    const dim3 grid((unsigned)tiles, (unsigned)cbc, (unsigned)splits);
+    const dim3 grid = tail > 1 ? dim3((unsigned)(tail_first + tail_tiles * tail), 1u, 1u)
+                               : dim3((unsigned)tiles, (unsigned)cbc, (unsigned)splits);
     if (!vec)
         hipLaunchKernelGGL((conv3x3_same_kernel<T, false, 16>), grid, dim3(kThreads), lds, ctx->stream, in, wp, bias, out, p);
     else if (lw == 16)
@@ -519,9 +562,10 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     else
         hipLaunchKernelGGL((conv3x3_same_kernel<T, true, sizeof(T) == 2 ? 2 : 4>), grid, dim3(kThreads), lds, ctx->stream,
                            in, wp, bias, out, p);
-    if (splits > 1)
-        hipLaunchKernelGGL(conv3x3_split_reduce_kernel<T>, dim3((unsigned)ceil_div(npix64 / 4 * cout, 256)), dim3(256), 0,
-                           ctx->stream, p.partial, splits, cout, p.npix, p.fd_hw, p.hw, bias, out, p.relu);
+    if (nsplit > 1)
+        hipLaunchKernelGGL(conv3x3_split_reduce_kernel<T>, dim3((unsigned)ceil_div(part_npix / 4 * cout, 256)), dim3(256),
+                           0, ctx->stream, p.partial, nsplit, cout, p.part_m0, p.part_npix, p.fd_hw, p.hw, bias, out,
+                           p.relu);
     return launch_status(ctx, "conv3x3_same");
 }
 

@@ -76,6 +76,29 @@ inline int32_t pick_chunk_splits(int64_t blocks, int32_t nchunks, int64_t slots,
     return pick;
 }
 
+// Pieces per tile for the last `blocks % slots` tiles of a grid of more than
+// one round: whole, they would run a last round of their own (mostly one
+// workgroup per CU, taken as 0.7 of a full round's time); split over their
+// channel chunks they fill the slots that the last whole tiles free, for
+// the cost of the split reduce.  1 = no tail split.
+inline int32_t pick_tail_splits(int64_t blocks, int32_t nchunks, int64_t slots, size_t elem) {
+    const int64_t rem = blocks % slots;
+    if (blocks <= slots || rem == 0 || nchunks < 2) return 1;
+    const double overhead = elem == 2 ? 2.0 : 0.5, reduce = elem == 2 ? 2.5 : 1.0;
+    double best = 0.7 * ((double)nchunks + overhead);
+    int32_t pick = 1;
+    for (int32_t s = 2; s <= std::min(nchunks, 8); ++s) {
+        const int64_t per = ceil_div(nchunks, s);
+        if (ceil_div(nchunks, per) != s) continue;
+        const double t = (double)ceil_div(s * rem, slots) * ((double)per + overhead) + reduce;
+        if (t < best) {
+            best = t;
+            pick = s;
+        }
+    }
+    return pick;
+}
+
 // Register transpose of a SUB×SUB block: in[i] holds SUB pixels of channel i,
 // out[j] holds SUB channels of pixel j.
 __device__ __forceinline__ void transpose_block(const u32x4 (&in)[8], u32x4 (&out)[8]) {
