@@ -69,7 +69,10 @@ int nott_abi_version(void);
 /* Synchronises the stream and returns the number of data errors kernels
  * reported since the last call (labels out of range), then clears it. */
 int nott_device_errors(nott_ctx ctx, int64_t* count);
-/* Device-side workspace currently held, in bytes. */
+/* Device memory the context holds for workspace, in bytes: the live arena
+ * plus the smaller arenas retired when it grew (kept until nott_destroy,
+ * since a graph captured earlier may still use them).  The static scratch
+ * of nott_layernorm_bwd_noalloc is per GPU and not counted. */
 int nott_workspace_bytes(nott_ctx ctx, int64_t* bytes);
 
 /* ---- conv2d ------------------------------------------------------------
@@ -226,11 +229,13 @@ int nott_layernorm_bwd(nott_ctx ctx, nott_dtype dtype, int64_t rows, int64_t d,
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * Same arguments and results as nott_layernorm_bwd (the same kernels); the
  * dgamma/dbeta column partials live in a static 16 MiB device array, one per
- * GPU, instead of the context workspace.  That bounds the problem: the
- * partials take 2·16·ceil(d/16)·4 bytes per block for up to 2·(number of
- * CUs) blocks (d <= 4096 on a 256-CU MI355X), or 8·d·rows bytes when
- * d or the pointers do not allow 16-byte rows; larger problems return
- * NOTT_ERR_UNSUPPORTED with the sizes in the message.  Every call on a GPU
+ * GPU, instead of the context workspace.  That bounds the problem.  On the
+ * vector path (d <= 2048 and a multiple of 8 bf16 / 4 fp32 elements, every
+ * row pointer 16-byte aligned) the partials take 2·16·ceil(d/16)·4 bytes for
+ * each of at most (number of CUs) blocks, at most 4 MiB on a 256-CU MI355X,
+ * so every row count fits.  Otherwise the generic path needs 8·d·rows bytes
+ * (rows·d <= 2^21 elements).  Larger problems return NOTT_ERR_UNSUPPORTED
+ * with the sizes in the message.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (two streams, two
  * contexts) race.  The partials are written in full before they are read,
  * so no clearing is needed between calls. */

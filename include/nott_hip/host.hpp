@@ -27,6 +27,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <array>
+#include <cstring>
 #include <atomic>
 #include <map>
 #include <memory>
@@ -158,8 +159,17 @@ class SideStreamScope {
         }
         ++s.depth;
     }
+    // The outermost scope joins whatever is still forked (its holder joins
+    // explicitly on the normal path; this covers a backward left by an
+    // exception, so no side-stream work stays unjoined, under capture or not).
     ~SideStreamScope() {
-        if (active_) --detail::side(dev_).depth;
+        if (!active_) return;
+        detail::Side& s = detail::side(dev_);
+        if (--s.depth == 0 && s.pending) {
+            hipStream_t cur = c10::hip::getCurrentHIPStream((c10::DeviceIndex)dev_).stream();
+            if (hipEventRecord(s.join, s.stream) == hipSuccess) (void)hipStreamWaitEvent(cur, s.join, 0);
+            s.pending = false;
+        }
     }
     SideStreamScope(const SideStreamScope&) = delete;
     SideStreamScope& operator=(const SideStreamScope&) = delete;
@@ -939,15 +949,44 @@ inline Tensor cross_entropy(const Tensor& logits, const Tensor& labels, double l
     return CrossEntropyFn::apply(logits, labels, label_smoothing);
 }
 
-// Kaiming-uniform (HeUniform: kaiming_uniform_(a=0, fan_in, relu)) and bias
-// zero, reference initialization/apply.hpp:10-17,45-51; drawn from a torch
-// CPU generator seeded by the caller.
+// Kaiming-uniform (HeUniform: torch::nn::init::kaiming_uniform_(w, a = 0,
+// fan_in, relu), reference initialization/apply.hpp:45-51) drawn from a
+// torch CPU generator given by the caller.  The bound is formed as libtorch
+// forms it, sqrt(3) · (gain / sqrt(fan_in)) with gain sqrt(2), which is not
+// always the same double as sqrt(6 / fan_in); the draws are then identical.
 inline void he_uniform_(Tensor& w, torch::Generator& gen) {
     torch::NoGradGuard ng;
     const int64_t fan_in = w.numel() / w.size(0);
-    const double bound = std::sqrt(6.0 / (double)fan_in);
+    const double std_ = std::sqrt(2.0) / std::sqrt((double)fan_in);
+    const double bound = std::sqrt(3.0) * std_;
     Tensor cpu = torch::empty(w.sizes(), torch::kFloat32).uniform_(-bound, bound, gen);
     w.copy_(cpu);
+}
+
+// Draws the initial weights of a model built from Nott descriptors with
+// HeUniform initialisation exactly as the reference draws them from a
+// generator seeded with the same value: for every Conv2d and Linear in
+// registration order (pre-order over the module tree, the order Nott's
+// layer factories run), the torch::nn module's constructor first draws its
+// default initialisation (weight, then bias: one uniform draw per element;
+// conv.hpp:182 / fc.hpp:38 construct torch::nn::Conv2d / Linear), then
+// apply_module_initialization redraws the weight with HeUniform and zeroes
+// the bias (initialization/apply.hpp:10-17, 45-51).  The default draws'
+// values are overwritten, but they advance the generator, so they are made
+// with the same shapes and dtype.  BatchNorm2d draws nothing (ones / zeros).
+inline void reference_init_(torch::nn::Module& model, torch::Generator& gen) {
+    torch::NoGradGuard ng;
+    auto layer = [&](Tensor& w, Tensor& b) {
+        Tensor scratch = torch::empty(w.sizes(), torch::kFloat32);
+        scratch.uniform_(0.0, 1.0, gen);
+        if (b.defined()) torch::empty(b.sizes(), torch::kFloat32).uniform_(0.0, 1.0, gen);
+        he_uniform_(w, gen);
+        if (b.defined()) b.zero_();
+    };
+    for (auto& child : model.modules(/*include_self=*/true)) {
+        if (auto* c = child->as<Conv2dImpl>()) layer(c->weight, c->bias);
+        else if (auto* l = child->as<LinearImpl>()) layer(l->weight, l->bias);
+    }
 }
 
 // ============================================================ optimizer
@@ -999,6 +1038,7 @@ public:
         build();
     }
     ~FusedAdamImpl() override {
+        if (replayed_) (void)hipEventDestroy(replayed_);
         std::lock_guard<std::mutex> g(detail::arena_mutex());
         for (auto* impl : registered_) detail::arena_grads().erase(impl);
     }
@@ -1070,8 +1110,12 @@ public:
     // scheduler's set_lr included) into the pinned blocks and, if an eager
     // step() ran since, the host step count into the device state; after
     // it, graph_after_replay() advances the per-parameter step counts the
-    // device advanced.  Every parameter of a group must have a gradient and
-    // the group's step counts must be equal at capture.
+    // device advanced and records an event behind the replay.  A replay
+    // still queued reads the pinned block only when its optimizer node runs,
+    // so graph_sync() waits for that event before it changes a value (and
+    // only then: with unchanged options, replays queue back to back).  Every
+    // parameter of a group must have a gradient and the group's step counts
+    // must be equal at capture.
     void graph_prepare() {
         if (!P_.defined()) return;
         torch::NoGradGuard ng;
@@ -1099,6 +1143,9 @@ public:
             wd_nonzero_[gi] = o.weight_decay() != 0.0;
         }
         device_steps_stale_ = true;
+        if (!replayed_ && hipEventCreateWithFlags(&replayed_, hipEventDisableTiming) != hipSuccess)
+            throw std::runtime_error("FusedAdam graph mode: hipEventCreate failed");
+        replay_pending_ = false;
         graph_sync();
     }
     void graph_step() {
@@ -1120,15 +1167,23 @@ public:
     void graph_sync() {
         if (!hparams_.defined()) return;
         double* hp = hparams_.data_ptr<double>();
+        std::vector<double> want(5 * param_groups_.size());
         for (size_t gi = 0; gi < param_groups_.size(); ++gi) {
             const auto& o = static_cast<const TorchOptions&>(param_groups_[gi].options());
             if ((o.weight_decay() != 0.0) != (wd_nonzero_[gi] != 0))
                 throw std::logic_error("FusedAdam graph mode: weight decay switched on or off after capture");
-            hp[5 * gi + 0] = o.lr();
-            hp[5 * gi + 1] = std::get<0>(o.betas());
-            hp[5 * gi + 2] = std::get<1>(o.betas());
-            hp[5 * gi + 3] = o.eps();
-            hp[5 * gi + 4] = o.weight_decay();
+            want[5 * gi + 0] = o.lr();
+            want[5 * gi + 1] = std::get<0>(o.betas());
+            want[5 * gi + 2] = std::get<1>(o.betas());
+            want[5 * gi + 3] = o.eps();
+            want[5 * gi + 4] = o.weight_decay();
+        }
+        if (std::memcmp(want.data(), hp, want.size() * sizeof(double)) != 0) {
+            if (replay_pending_) {
+                detail::hip_ok(hipEventSynchronize(replayed_), "FusedAdam graph mode: wait for the last replay");
+                replay_pending_ = false;
+            }
+            std::memcpy(hp, want.data(), want.size() * sizeof(double));
         }
         if (device_steps_stale_) {
             Tensor host = torch::zeros({(int64_t)param_groups_.size(), 8}, torch::kInt64);
@@ -1142,6 +1197,11 @@ public:
         }
     }
     void graph_after_replay() {
+        if (replayed_) {
+            const auto stream = c10::hip::getCurrentHIPStream(P_.device().index());
+            detail::hip_ok(hipEventRecord(replayed_, stream.stream()), "FusedAdam graph mode: record the replay");
+            replay_pending_ = true;
+        }
         for (size_t gi = 0; gi < ranges_.size(); ++gi) {
             if (ranges_[gi].second <= ranges_[gi].first) continue;
             for (auto& p : param_groups_[gi].params()) {
@@ -1257,6 +1317,8 @@ private:
     size_t group_count_ = 0;
     // graph mode: per-group device state, pinned hyper-parameters, arena ranges
     Tensor dev_state_, hparams_;
+    hipEvent_t replayed_ = nullptr;   // recorded behind the last replay
+    bool replay_pending_ = false;
     std::vector<std::pair<int64_t, int64_t>> ranges_;
     std::vector<int> wd_nonzero_;
     bool device_steps_stale_ = true;

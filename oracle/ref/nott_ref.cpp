@@ -835,6 +835,35 @@ int ref_save_archive(int model, uint64_t seed, int64_t batch, const char* path) 
     });
 }
 
+// The initial parameters of the reference's configs[0] (model 0) or
+// configs[4] (model 1) model when torch's CPU generator is seeded with
+// `seed` right before the model is built: each layer factory constructs its
+// torch::nn module (whose constructor draws its default initialisation) and
+// then applies the descriptor's HeUniform (initialization/apply.hpp:45-51).
+// For each of the `count` registration keys, outs[i] receives that parameter.
+int ref_init_params(int model, uint64_t seed, int64_t count, const char* const* names, float* const* outs) {
+    return guarded([&] {
+        torch::manual_seed(seed);
+        auto copy_out = [&](torch::nn::Module& m) {
+            auto params = m.named_parameters(true);
+            for (int64_t i = 0; i < count; ++i) {
+                auto* p = params.find(names[i]);
+                if (!p) throw std::runtime_error(std::string("no parameter ") + names[i]);
+                out(*p, outs[i]);
+            }
+        };
+        if (model == 0) {
+            SmallCnnRef net;
+            copy_out(net.c.owner);
+        } else if (model == 1) {
+            ResNet18Ref net;
+            copy_out(net.owner);
+        } else {
+            throw std::invalid_argument("model must be 0 (small CNN) or 1 (ResNet-18)");
+        }
+    });
+}
+
 // Times `iters` full fp32 training steps on the CPU (forward, CE mean,
 // backward, Adam (model 0, configs[0]) or AdamW (model 1, configs[4]) step,
 // zero_grad) at the given batch; seconds per step in *sec.  Inputs

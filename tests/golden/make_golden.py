@@ -42,6 +42,45 @@ POOL_CASES = [
 ]
 
 
+NONFINITE_POOL_CASES = [
+    # name, n, c, h, w, k, stride, pad
+    ("maxpool3x3_s2p1_nan_inf", 1, 5, 9, 9, (3, 3), (2, 2), (1, 1)),   # the ResNet-18 stem pool's window
+    ("maxpool2x2_s2_nan_inf", 2, 3, 6, 6, (2, 2), (2, 2), (0, 0)),     # the small CNN's
+]
+
+
+def nonfinite_pool_input(g, n, c, h, w):
+    """Planes of non-finite windows: 0 all -inf; 1 all NaN; 2 normal values
+    with single NaNs, two NaNs in one window, a NaN beside +inf, and +inf;
+    3 whole windows (and the padded corner window) of -inf among normal
+    values, with equal maxima; 4 post-ReLU zeros with -inf and NaN mixed."""
+    x = g.standard_normal((n, c, h, w)).astype(np.float32)
+    x[:, 0] = -np.inf
+    if c > 1:
+        x[:, 1] = np.nan
+    if c > 2:
+        p = x[:, 2]
+        p[:, 0, 0] = np.nan                       # first element of a window
+        p[:, 2, 3] = np.nan                       # two NaNs in one window (the last wins)
+        p[:, 3, 3] = np.nan
+        p[:, h - 1, w - 1] = np.nan               # last element of the image
+        p[:, 4, 1] = np.inf
+        p[:, 4, 0] = np.nan                       # NaN beside +inf
+        p[:, 1, 4] = np.inf
+    if c > 3:
+        p = x[:, 3]
+        p[:, 0:2, 0:2] = -np.inf                  # the window at the padded corner
+        p[:, 2:4, 2:4] = -np.inf
+        p[:, 3:6, 3:6] = -np.inf
+        p[:, h - 2:, 0:3] = 0.75                  # equal maxima
+    if c > 4:
+        p = np.maximum(x[:, 4], 0.0)
+        p[:, ::3, ::2] = -np.inf
+        p[:, 1::4, 1::3] = np.nan
+        x[:, 4] = p
+    return x
+
+
 def save(name: str, **arrays):
     path = os.path.join(HERE, name + ".npz")
     np.savez_compressed(path, **{k: np.asarray(v) for k, v in arrays.items()})
@@ -104,6 +143,20 @@ def main():
         y, idx, dx = ref.maxpool2d(d, x, dy)
         save(name, desc=np.array([n, c, h, w, kk[0], kk[1], st[0], st[1], pd[0], pd[1], dl[0], dl[1], int(ceil)],
                                  np.int64), x=x, dy=dy, y=y, argmax=idx, dx=dx)
+
+    # Non-finite windows (pooling.hpp:144, ATen's max_pool2d rule: a NaN
+    # always takes the window, so the last NaN wins; a window of -inf only
+    # keeps its first in-image element).
+    for i, (name, n, c, h, w, kk, st, pd) in enumerate(NONFINITE_POOL_CASES):
+        g = rng(350 + i)
+        d = Pool2dDesc(n, c, h, w, kk[0], kk[1], st[0], st[1], pd[0], pd[1], 1, 1, 0, 0)
+        x = nonfinite_pool_input(g, n, c, h, w)
+        oh = (h + 2 * pd[0] - (kk[0] - 1) - 1) // st[0] + 1
+        ow = (w + 2 * pd[1] - (kk[1] - 1) - 1) // st[1] + 1
+        dy = f32(g.standard_normal((n, c, oh, ow)))
+        y, idx, dx = ref.maxpool2d(d, x, dy)
+        save(name, desc=np.array([n, c, h, w, kk[0], kk[1], st[0], st[1], pd[0], pd[1], 1, 1, 0], np.int64),
+             x=x, dy=dy, y=y, argmax=idx, dx=dx)
 
     g = rng(400)
     x = f32(g.standard_normal((2, 3, 5, 5)))

@@ -403,6 +403,18 @@ class Ref:
         which = {"small_cnn": 0, "resnet18": 1}[model]
         self._ok(self.lib.ref_save_archive(C.c_int(which), C.c_uint64(seed), i64(batch), C.c_char_p(path.encode())))
 
+    def init_params(self, model: str, seed: int, shapes: dict) -> dict:
+        """Initial parameters of the reference's "small_cnn" or "resnet18"
+        model built right after torch's CPU generator was seeded with `seed`;
+        `shapes` maps the registration keys wanted to their shapes."""
+        names = sorted(shapes)
+        outs = [np.empty(shapes[k], np.float32) for k in names]
+        cname = (C.c_char_p * len(names))(*[k.encode() for k in names])
+        ptrs = (C.c_void_p * len(outs))(*[a.ctypes.data for a in outs])
+        which = {"small_cnn": 0, "resnet18": 1}[model]
+        self._ok(self.lib.ref_init_params(C.c_int(which), C.c_uint64(seed), i64(len(names)), cname, ptrs))
+        return dict(zip(names, outs))
+
     def train_step_time(self, model: str, batch: int, iters: int) -> float:
         """Seconds per fp32 CPU training step of "small_cnn" or
         "resnet18" built from the reference's layer descriptors."""

@@ -187,6 +187,33 @@ def test_maxpool_tap(ops, oracle, dt, case):
                        dxt.view(torch.int16 if dt == "bf16" else torch.int32))
 
 
+MAXPOOL_GOLDEN = ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil", "maxpool2x2_dil2",
+                  "maxpool3x3_s2p1_nan_inf", "maxpool2x2_s2_nan_inf"]
+
+
+@pytest.mark.parametrize("name", MAXPOOL_GOLDEN)
+def test_maxpool_golden(ops, name):
+    """Both GPU max-pool paths (int64 flat index and one-byte tap) against the
+    fixtures the reference's MaxPool2d wrote (pooling.hpp:132-149), all-NaN,
+    all--inf and mixed non-finite windows included: argmax and y bit-exact,
+    dx within fp32 tolerance."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name + ".npz"))
+    n, c, h, w, kh, kw, sh, sw, ph, pw, dh, dw, ceil = (int(v) for v in z["desc"])
+    d = ops.pool_desc((n, c, h, w), (kh, kw), (sh, sw), (ph, pw), (dh, dw), bool(ceil))
+    x = dev(z["x"])
+    y, idx = ops.maxpool2d_fwd(x, d)
+    yt, tap = ops.maxpool2d_fwd_tap(x, d)
+    assert np.array_equal(idx.cpu().numpy(), z["argmax"]), "argmax routing differs from the reference's"
+    assert np.array_equal(host(y), z["y"], equal_nan=True)
+    assert torch.equal(y.view(torch.int32), yt.view(torch.int32))
+    dy = dev(z["dy"])
+    dx = ops.maxpool2d_bwd(idx, dy, d)
+    dxt = ops.maxpool2d_bwd_tap(tap, dy, d)
+    check(host(dx), z["dx"], "f32", "golden maxpool dx")
+    assert torch.equal(dx.view(torch.int32), dxt.view(torch.int32))
+
+
 def test_maxpool_tap_rejects_large_windows(ops):
     d = ops.pool_desc((1, 1, 40, 40), (17, 17), (1, 1), (0, 0), (1, 1), False)
     with pytest.raises(RuntimeError, match="256 taps"):
@@ -348,6 +375,70 @@ def test_softmax_xent(ops, oracle, dt, n, c, eps, ignore):
     # label gather is exact: the target column carries the −(1−ε)/n term
     rows = np.nonzero(y != -100)[0]
     assert (host(dl)[rows, y[rows]] < 0).all()
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_softmax_xent_full_size_config(ops, oracle, dt):
+    """configs[2]b at its benched size, 16384 x 32000, logits ~ N(0, 2),
+    labels uniform (reference ce.hpp:36): every row's gradient sums to zero
+    (in float64), the label column is the only negative entry of its row,
+    the loss matches a float64 log-sum-exp, and 64 rows spread over the
+    batch match the oracle run on those rows (its mean over 64 rows rescaled
+    by 64/16384, a power of two, so the rescale is exact)."""
+    n, c = 16384, 32000
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    z = (2 * torch.randn((n, c), generator=gen, device="cuda")).to(torch.bfloat16 if dt == "bf16" else torch.float32)
+    y = torch.randint(0, c, (n,), generator=gen, device="cuda")
+    dz, loss = ops.softmax_xent_bwd(z, y)
+    torch.cuda.synchronize()
+    # Σ_j dz_ij = (Σ_j p_ij − 1)/n = 0 in reals.  fp32: the row's softmax
+    # denominator is one fp32 sum of 32000 terms, common to the row, so Σp
+    # is 1 within ~1e-6 (bound 1e-5 of Σ|dz|, where a missing label term
+    # would give 0.5); bf16: each stored element is rounded once more, at
+    # most 2^-9 of itself.
+    row_sum = dz.double().sum(1)
+    row_abs = dz.double().abs().sum(1)
+    tol = 1e-5 if dt == "f32" else 2.0 ** -8
+    assert (row_sum.abs() <= tol * row_abs).all().item(), "rows must sum to zero"
+    at_label = dz.gather(1, y[:, None]).squeeze(1)
+    assert (at_label < 0).all().item(), "label column must carry the -1/n term"
+    neg = (dz < 0).sum(1)
+    assert (neg == 1).all().item(), "only the label column is negative"
+    zd = z.double()
+    want_loss = (torch.logsumexp(zd, 1) - zd.gather(1, y[:, None]).squeeze(1)).mean().item()
+    assert abs(loss.item() - want_loss) <= 1e-5 * abs(want_loss)
+    rows = np.linspace(0, n - 1, 64).astype(np.int64)
+    zr = host(z[rows])
+    yr = y[rows].cpu().numpy()
+    dle, _ = oracle.softmax_xent(zr, yr, 0.0)
+    check(host(dz[rows]), dle * np.float32(64.0 / n), dt, "xent dlogits rows at full size")
+    del z, dz, zd
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+def test_adamw_full_size_config(ops, oracle, dt):
+    """configs[2]c at its benched size: AdamW over one flat 1e8-parameter
+    buffer, params ~ N(0, 0.02), grads ~ N(0, 1e-3), m = v = 0, lr 3e-4,
+    wd 0.01, step 10 (reference adam.hpp:159-250).  Every element is compared
+    with the oracle: fp32 bit-exact; bf16 moments bit-exact and parameters
+    equal to the oracle's fp32 result rounded once to bf16."""
+    n = 100_000_000
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    p = (0.02 * torch.randn(n, generator=gen, device="cuda")).to(tdt)
+    gr = (1e-3 * torch.randn(n, generator=gen, device="cuda")).to(tdt)
+    m = torch.zeros(n, device="cuda")
+    v = torch.zeros(n, device="cuda")
+    ph, gh = host(p), host(gr)
+    ops.adam_step(p, gr, m, v, lr=3e-4, weight_decay=0.01, step=10, decoupled=True)
+    pe, me, ve = oracle.adam_step(1, ph, gh, np.zeros(n, np.float32), np.zeros(n, np.float32), 3e-4, 0.9, 0.999,
+                                  1e-8, 0.01, 10)
+    assert np.array_equal(host(m).view(np.int32), me.view(np.int32))
+    assert np.array_equal(host(v).view(np.int32), ve.view(np.int32))
+    if dt == "f32":
+        assert np.array_equal(host(p).view(np.int32), pe.view(np.int32))
+    else:
+        assert np.array_equal(host(p), host_input(pe, "bf16"))
 
 
 def test_softmax_xent_bad_label_is_reported(ops):

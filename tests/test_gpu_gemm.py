@@ -378,6 +378,34 @@ def test_conv3x3_tail_split_fp32(ops, case):
     check(host(dx[-3:]), host(ref_dx[-3:]), "f32", "dx tail images")
 
 
+TAIL3X3_BF16 = [
+    (42, 256, 56, 56, 64),     # forward over 256 channels (8 bf16 chunks): 515 tiles, 3 split 8 ways
+    (42, 64, 56, 56, 256),     # dgrad over dy's 256 channels: the same split
+]
+
+
+@pytest.mark.parametrize("case", TAIL3X3_BF16)
+def test_conv3x3_tail_split_bf16(ops, case):
+    """bf16 forward and dgrad whose tail tiles are split (the fp32 split
+    partials and their reduce, with bf16 stores) against torch's fp32
+    convolution of the same bf16-rounded operands."""
+    n, c, h, w_, k = case
+    d = ops.conv_desc((n, c, h, w_), (k, c, 3, 3), padding=(1, 1))
+    gen = torch.Generator(device="cuda").manual_seed(sum(case) + 1)
+    x = torch.randn((n, c, h, w_), generator=gen, device="cuda").to(torch.bfloat16)
+    w = (torch.randn((k, c, 3, 3), generator=gen, device="cuda") / math.sqrt(c * 9)).to(torch.bfloat16)
+    dy = torch.randn((n, k, h, w_), generator=gen, device="cuda").to(torch.bfloat16)
+    y = ops.conv2d_fwd(x, w, None, d)
+    dx = ops.conv2d_bwd_data(dy, w, d)
+    torch.cuda.synchronize()
+    ref_y = torch.nn.functional.conv2d(x.float(), w.float(), None, padding=1)
+    ref_dx = torch.nn.grad.conv2d_input((n, c, h, w_), w.float(), dy.float(), padding=1)
+    check(host(y), host(ref_y), "bf16", "y vs torch fp32")
+    check(host(dx), host(ref_dx), "bf16", "dx vs torch fp32")
+    check(host(y[-3:]), host(ref_y[-3:]), "bf16", "y tail images")
+    check(host(dx[-3:]), host(ref_dx[-3:]), "bf16", "dx tail images")
+
+
 @pytest.mark.parametrize("dt", DTYPES)
 @pytest.mark.parametrize("case", [CONV[5], CONV[6], CONV[2], CONV[3], (2, 32, 10, 10, 64, 3, 3, 1, 1, 1)],
                          ids=lambda c: "n{}c{}h{}w{}k{}r{}s{}st{}".format(*c[:8]))

@@ -26,6 +26,9 @@ def close(a, b, rtol=RTOL, atol=ATOL):
     nan_a, nan_b = np.isnan(a), np.isnan(b)
     assert np.array_equal(nan_a, nan_b), "NaN positions differ"
     a, b = a[~nan_a], b[~nan_b]
+    inf = np.isinf(a) | np.isinf(b)
+    assert np.array_equal(a[inf], b[inf]), "infinities differ"
+    a, b = a[~inf], b[~inf]
     err = np.abs(a - b) - (atol + rtol * np.abs(b))
     assert (err <= 0).all(), f"max excess {err.max():.3e}"
 
@@ -83,7 +86,7 @@ def test_relu_golden(oracle):
 
 
 @pytest.mark.parametrize("name", ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil",
-                                  "maxpool2x2_dil2"])
+                                  "maxpool2x2_dil2", "maxpool3x3_s2p1_nan_inf", "maxpool2x2_s2_nan_inf"])
 def test_maxpool_golden(oracle, name):
     g = load(name)
     d = pool_from(g["desc"])

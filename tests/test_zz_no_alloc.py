@@ -33,7 +33,9 @@ def _inputs(g, rows, d, dt):
 def test_noalloc_matches_layernorm_bwd(ops, dt):
     g = rng(123)
     ctx = ops.context()
-    for rows, d in ((4096, 1024), (300, 200), (7, 33)):   # second and third calls are smaller
+    # each call smaller than the one before; the first at the vector path's
+    # largest row width with a large row count (accepted: ≤ 4 MiB of partials)
+    for rows, d in ((16384, 2048), (4096, 1024), (300, 200), (7, 33)):
         print(f"noalloc case rows={rows} d={d} dtype={dt}", flush=True)
         x, gamma, beta, dy = (dev(a, dt) for a in _inputs(g, rows, d, dt))
         y, mean, rstd = ops.layernorm_fwd(x, gamma, beta)
@@ -60,8 +62,9 @@ def test_noalloc_matches_layernorm_bwd(ops, dt):
 
 
 def test_noalloc_rejects_oversized_problem(ops):
-    """d = 8192 needs 2·8192·4 bytes per block for 512 blocks (32 MiB) of
-    partials, more than the 16 MiB static scratch: a clear error, no launch."""
+    """d = 8192 is above the vector path's 2048, so the generic path needs
+    8·d·rows = 512 MiB of partials, more than the 16 MiB static scratch: a
+    clear error, no launch."""
     from thot_amd._abi import NottInvalidArgument
     rows, d = 8192, 8192
     x = torch.zeros((rows, d), device="cuda")

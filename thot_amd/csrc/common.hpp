@@ -19,6 +19,7 @@ struct nott_ctx_s {
     void* ws = nullptr;            // current device workspace
     size_t ws_bytes = 0;
     std::vector<void*> retired;    // earlier, smaller workspaces: kept until nott_destroy
+    size_t retired_bytes = 0;      // their total size
     void* ln_scratch = nullptr;    // this device's static LayerNorm scratch (nott_layernorm_bwd_noalloc)
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;

@@ -30,7 +30,10 @@ void* workspace(nott_ctx ctx, size_t bytes) {
                                       " bytes failed: " + hipGetErrorString(e));
         return nullptr;
     }
-    if (ctx->ws) ctx->retired.push_back(ctx->ws);
+    if (ctx->ws) {
+        ctx->retired.push_back(ctx->ws);
+        ctx->retired_bytes += ctx->ws_bytes;
+    }
     ctx->ws = fresh;
     ctx->ws_bytes = want;
     return ctx->ws;
@@ -132,7 +135,7 @@ int nott_device_errors(nott_ctx ctx, int64_t* count) {
 int nott_workspace_bytes(nott_ctx ctx, int64_t* bytes) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, bytes != nullptr, "bytes is null");
-    *bytes = (int64_t)ctx->ws_bytes;
+    *bytes = (int64_t)(ctx->ws_bytes + ctx->retired_bytes);
     return NOTT_OK;
 }
 

@@ -46,7 +46,9 @@ __device__ __forceinline__ uint32_t lds_addr(const char NOTT_LDS* p) { return (u
 // M0 is listed as clobbered for the reader; the compiler reserves M0 and
 // warns that it ignores the listing, which is harmless here because no
 // kernel using these helpers has any other M0 reader (the generated code
-// sets M0 only in these statements).
+// sets M0 only in these statements).  tests/test_lds_dma_m0.py compiles
+// every source that includes this header to device assembly and fails if
+// the compiler writes M0 itself or emits any other M0 reader.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {

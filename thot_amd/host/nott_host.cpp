@@ -175,11 +175,9 @@ struct Trainer {
         torch::NoGradGuard ng;
         auto gen = at::detail::createCPUGenerator(seed);
         torch::Generator g(gen);
-        for (auto& kv : model->named_parameters()) {
-            Tensor p = kv.value();
-            const auto& name = kv.key();
-            if (name.size() >= 6 && name.compare(name.size() - 6, 6, "weight") == 0 && p.dim() >= 2) NH::he_uniform_(p, g);
-        }
+        // The weights a Nott model built from the same descriptors draws
+        // after torch::manual_seed(seed).
+        NH::reference_init_(*model, g);
         model->to(torch::Device(torch::kCUDA, device));
         model->train();
         std::vector<Tensor> params;
@@ -559,6 +557,20 @@ PYBIND11_MODULE(_nott_host, m) {
         if (model == "resnet18") return NA::to_json(NA::architecture(name, ResNet18Impl::descriptors_for(classes)));
         throw std::invalid_argument("unknown model '" + model + "'");
     }, py::arg("model"), py::arg("classes") = 1000, py::arg("name") = "Nott::Model");
+    // Initial parameters (CPU tensors by registration key) of a model as the
+    // trainers initialise it from `seed` (no device needed).
+    m.def("initial_parameters", [](const std::string& model, uint64_t seed, int64_t classes) {
+        auto gen = at::detail::createCPUGenerator(seed);
+        torch::Generator g(gen);
+        std::shared_ptr<torch::nn::Module> net;
+        if (model == "small_cnn") net = SmallCNN().ptr();
+        else if (model == "resnet18") net = ResNet18(classes).ptr();
+        else throw std::invalid_argument("unknown model '" + model + "'");
+        NH::reference_init_(*net, g);
+        std::map<std::string, Tensor> out;
+        for (auto& kv : net->named_parameters()) out[kv.key()] = kv.value().detach().clone();
+        return out;
+    }, py::arg("model"), py::arg("seed"), py::arg("classes") = 1000);
     using SmallT = Trainer<SmallCNN, false>;
     py::class_<SmallT>(m, "SmallCNNTrainer")
         .def(py::init([](int device, uint64_t seed, double lr) {
