@@ -785,6 +785,8 @@ public:
         const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
         return Conv2dReluFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
     }
+    // {stride_h, stride_w, pad_h, pad_w, dil_h, dil_w}
+    const std::vector<int64_t>& geometry() const { return geom_; }
     Tensor weight, bias, weight_compute;
 private:
     std::vector<int64_t> geom_;
@@ -889,20 +891,31 @@ inline Tensor max_pool2d(const Tensor& x, int64_t k, int64_t stride, int64_t pad
 // flatten.hpp:19-41) and its checkpoint archive has the same child entries.
 class MaxPool2dImpl : public torch::nn::Module {
 public:
+    // Square window, stride and padding, no dilation.
     MaxPool2dImpl(int64_t k, int64_t stride, int64_t pad = 0, bool ceil_mode = false)
-        : k_(k), stride_(stride), pad_(pad), ceil_(ceil_mode) {}
-    Tensor forward(const Tensor& x) { return max_pool2d(x, k_, stride_, pad_, ceil_); }
+        : geom_{k, k, stride, stride, pad, pad, 1, 1, ceil_mode ? 1 : 0} {}
+    // Per-axis window, stride, padding and dilation (torch::nn::MaxPool2dOptions).
+    MaxPool2dImpl(std::array<int64_t, 2> k, std::array<int64_t, 2> stride, std::array<int64_t, 2> pad,
+                  std::array<int64_t, 2> dilation, bool ceil_mode)
+        : geom_{k[0], k[1], stride[0], stride[1], pad[0], pad[1], dilation[0], dilation[1], ceil_mode ? 1 : 0} {}
+    Tensor forward(const Tensor& x) { return MaxPool2dFn::apply(x, geom_); }
+    // {kh, kw, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, ceil_mode}
+    const std::vector<int64_t>& geometry() const { return geom_; }
 private:
-    int64_t k_, stride_, pad_;
-    bool ceil_;
+    std::vector<int64_t> geom_;
 };
 TORCH_MODULE(MaxPool2d);
 class FlattenImpl : public torch::nn::Module {
 public:
     // Nott's Flatten wraps a torch::nn::Flatten registered as "flatten"
-    // (flatten.hpp:34): an empty child entry in the archive.
-    FlattenImpl() { register_module("flatten", std::make_shared<torch::nn::Module>()); }
-    Tensor forward(const Tensor& x) { return x.flatten(1); }
+    // (flatten.hpp:34): an empty child entry in the archive.  The result is a
+    // view (x.flatten(start_dim, end_dim), as torch::nn::Flatten computes it).
+    explicit FlattenImpl(int64_t start_dim = 1, int64_t end_dim = -1) : start_(start_dim), end_(end_dim) {
+        register_module("flatten", std::make_shared<torch::nn::Module>());
+    }
+    Tensor forward(const Tensor& x) { return x.flatten(start_, end_); }
+private:
+    int64_t start_, end_;
 };
 TORCH_MODULE(Flatten);
 // AdaptiveAvgPool2d({1, 1}) (pooling.hpp:164-167): no parameters or buffers.
