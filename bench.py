@@ -72,7 +72,7 @@ def host_info() -> dict:
         aff = len(os.sched_getaffinity(0))
     except AttributeError:
         aff = os.cpu_count() or 1
-    model, phys = None, set()
+    model, phys, ident = None, set(), {}
     try:
         pid = core = None
         with open("/proc/cpuinfo") as f:
@@ -81,6 +81,8 @@ def host_info() -> dict:
                 k, v = k.strip(), v.strip()
                 if k == "model name" and model is None:
                     model = v
+                elif k in ("cpu family", "model", "stepping", "cache size", "cpu MHz") and k not in ident:
+                    ident[k] = v
                 elif k == "physical id":
                     pid = v
                 elif k == "core id":
@@ -94,6 +96,12 @@ def host_info() -> dict:
         pass
     omp = os.environ.get("OMP_NUM_THREADS")
     p = aff if not (omp and omp.isdigit() and int(omp) > 0) else min(aff, int(omp))
+    # /proc/cpuinfo's model name can be generic under virtualisation ("AMD
+    # EPYC"); the family / model / stepping numbers and the cache identify the part.
+    if model is not None and ident:
+        model = (f"{model} (family {ident.get('cpu family', '?')}, model {ident.get('model', '?')}, "
+                 f"stepping {ident.get('stepping', '?')}, cache {ident.get('cache size', '?')}, "
+                 f"{ident.get('cpu MHz', '?')} MHz)")
     return {"nproc": os.cpu_count(), "affinity_cpus": aff, "physical_cores": len(phys) or None,
             "model": model, "threads": p, "omp_num_threads": omp}
 
@@ -112,7 +120,9 @@ def _ref():
 
 
 def _iters_for(sec_one: float, budget_s: float, cap: int = 20000) -> int:
-    return max(1, min(cap, int(budget_s / max(sec_one, 1e-6))))
+    """Timed iterations for a CPU baseline: what fits the budget, at least 20
+    (the reference's times are the median of these, after 5 warm-ups)."""
+    return max(20, min(cap, int(budget_s / max(sec_one, 1e-6))))
 
 
 # ----------------------------------------------------------------- workloads
@@ -214,7 +224,7 @@ class ConvBwd(Workload):
         return {"value": round(flop / sec / 1e12, 4), "unit": "TFLOP/s", "cores": ref.get_threads(),
                 "kind": "reference",
                 "sample": f"Nott Conv2d (libtorch CPU autograd) dgrad+wgrad, fp32, N={n} of 128 "
-                          f"(per-image work, scaled by FLOPs), {iters} passes x {sec * 1e3:.1f} ms"}
+                          f"(per-image work, scaled by FLOPs), median of {iters} passes after 5 warm-ups {sec * 1e3:.1f} ms"}
 
 
 class LnBwd(Workload):
@@ -259,7 +269,7 @@ class LnBwd(Workload):
         b32 = 3 * self.R * self.D * 4 + self.D * 4 + 2 * self.R * 4 + 2 * self.D * 4
         return {"value": round(b32 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
                 "sample": f"at::native_layer_norm_backward (the op LayerNorm's autograd node runs), fp32, full "
-                          f"{self.R}x{self.D}, {iters} calls x {sec * 1e3:.2f} ms; GB/s on the fp32 algorithmic "
+                          f"{self.R}x{self.D}, median of {iters} calls after 5 warm-ups {sec * 1e3:.2f} ms; GB/s on the fp32 algorithmic "
                           f"bytes (the reference has no bf16 path)"}
 
 
@@ -300,7 +310,7 @@ class Xent(Workload):
         b32 = 2 * rows * self.C * 4 + rows * 8
         return {"value": round(b32 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
                 "sample": f"Nott CrossEntropy forward + backward (log_softmax + nll_loss, libtorch CPU autograd), "
-                          f"fp32, {rows} of {self.N} rows x {self.C}, {iters} passes x {sec * 1e3:.2f} ms; GB/s on "
+                          f"fp32, {rows} of {self.N} rows x {self.C}, median of {iters} passes after 5 warm-ups {sec * 1e3:.2f} ms; GB/s on "
                           f"the fp32 algorithmic bytes of those rows"}
 
 
@@ -339,8 +349,8 @@ class AdamW(Workload):
         iters = _iters_for(ref.adamw_time(n, 1), budget_s, 200)
         sec = ref.adamw_time(n, iters)
         return {"value": round(n * 28 / sec / 1e9, 2), "unit": "GB/s", "cores": ref.get_threads(), "kind": "reference",
-                "sample": f"Nott AdamW (torch::optim CPU) on a flat 1e7-param fp32 buffer, {iters} steps x "
-                          f"{sec * 1e3:.1f} ms"}
+                "sample": f"Nott AdamW (torch::optim CPU) on a flat 1e7-param fp32 buffer, median of "
+                          f"{iters} steps after 5 warm-ups {sec * 1e3:.1f} ms"}
 
 
 class MhaBwd(Workload):
@@ -425,7 +435,7 @@ class MhaBwd(Workload):
         return {"value": round(flop / sec / 1e12, 4), "unit": "TFLOP/s", "cores": ref.get_threads(),
                 "kind": "reference",
                 "sample": f"Nott MultiHeadAttention backward (libtorch CPU autograd through the saved graph), fp32, "
-                          f"batch {b} of {self.B}, {iters} passes x {sec * 1e3:.1f} ms; TFLOP/s on the same "
+                          f"batch {b} of {self.B}, median of {iters} passes after 5 warm-ups {sec * 1e3:.1f} ms; TFLOP/s on the same "
                           f"algorithmic FLOPs per sample"}
 
 
@@ -509,14 +519,16 @@ class TrainStep(Workload):
         ref = _ref()
         if ref is None:
             return None
-        batch = 64 if self.name == "small_cnn" else 8
-        iters = _iters_for(ref.train_step_time(self.name, batch, 1), budget_s)
+        batch = 64   # the GPU leg's batch
+        # A ResNet-18 CPU step at batch 64 takes about a second: the minimum
+        # 20 timed steps, without a probe.
+        iters = 20 if self.name == "resnet18" else _iters_for(ref.train_step_time(self.name, batch, 1), budget_s)
         sec = ref.train_step_time(self.name, batch, iters)
         what = "configs[0] small CNN + Adam" if self.name == "small_cnn" else "configs[4] ResNet-18 + AdamW"
         note = "" if self.dtype == "f32" else " (the reference has no bf16 path: its fp32 step)"
         return {"value": round(batch / sec, 2), "unit": "samples/s", "cores": ref.get_threads(), "kind": "reference",
                 "sample": f"{what}, fp32 libtorch CPU step built from Nott's layer descriptors{note}, batch {batch}, "
-                          f"{iters} steps x {sec * 1e3:.1f} ms"}
+                          f"median of {iters} steps after 5 warm-ups {sec * 1e3:.1f} ms"}
 
 
 WORKLOADS = {"conv_bwd": ConvBwd, "ln_bwd": LnBwd, "xent": Xent, "adamw": AdamW, "mha_bwd": MhaBwd,

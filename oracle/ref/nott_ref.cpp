@@ -27,6 +27,7 @@
 #include "optimizer/details/adam.hpp"
 #include "attention/details/head.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <optional>
 #include <cstring>
@@ -274,6 +275,22 @@ struct ResNet18Ref {
 torch::nn::Module& owner_of(SmallCnnRef& n) { return n.c.owner; }
 torch::nn::Module& owner_of(ResNet18Ref& n) { return n.owner; }
 
+// Median seconds of `iters` timed calls of fn after 5 untimed warm-up calls.
+constexpr int kTimingWarmup = 5;
+template <class F>
+double median_seconds(int iters, F&& fn) {
+    for (int i = 0; i < kTimingWarmup; ++i) fn();
+    std::vector<double> t(std::max(iters, 1));
+    for (auto& s : t) {
+        const auto t0 = std::chrono::steady_clock::now();
+        fn();
+        s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    }
+    std::sort(t.begin(), t.end());
+    const size_t m = t.size() / 2;
+    return t.size() % 2 ? t[m] : 0.5 * (t[m - 1] + t[m]);
+}
+
 template <class Net>
 double time_train_steps(Net& net, torch::Tensor x, torch::Tensor y, bool decoupled, int iters) {
     owner_of(net).train();
@@ -286,11 +303,7 @@ double time_train_steps(Net& net, torch::Tensor x, torch::Tensor y, bool decoupl
             opt.step();
             opt.zero_grad(false);
         };
-        step();   // warm-up (also initialises the optimizer state)
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) step();
-        auto t1 = std::chrono::steady_clock::now();
-        return std::chrono::duration<double>(t1 - t0).count() / iters;
+        return median_seconds(iters, step);   // the warm-ups also initialise the optimizer state
     };
     if (decoupled) {
         Nott::Optimizer::Details::AdamWOptions o;
@@ -329,8 +342,8 @@ int ref_conv2d(const nott_conv2d_desc* d, int with_bias, const float* x, const f
     });
 }
 
-// Times `iters` conv backward passes (dgrad + wgrad) on the CPU; returns
-// seconds per pass in *sec.  Inputs as ref_conv2d (no bias).
+// Times conv backward passes (dgrad + wgrad) on the CPU; *sec is the median
+// seconds of `iters` timed passes after 5 warm-ups (as every *_time below).  Inputs as ref_conv2d (no bias).
 int ref_conv2d_bwd_time(const nott_conv2d_desc* d, const float* x, const float* w, const float* dy, int iters,
                         double* sec) {
     return guarded([&] {
@@ -340,11 +353,7 @@ int ref_conv2d_bwd_time(const nott_conv2d_desc* d, const float* x, const float* 
         auto xt = in(x, {d->n, d->c, d->h, d->w}).requires_grad_(true);
         auto yt = layer.forward(xt);
         auto g = in(dy, yt.sizes().vec());
-        yt.backward(g, /*retain_graph=*/true);  // warm-up
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) yt.backward(g, /*retain_graph=*/true);
-        auto t1 = std::chrono::steady_clock::now();
-        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+        *sec = median_seconds(iters, [&] { yt.backward(g, /*retain_graph=*/true); });
     });
 }
 
@@ -555,7 +564,7 @@ int ref_adam_step(int decoupled, int64_t n, float* p, const float* g, float* m, 
     });
 }
 
-// Times `iters` AdamW steps over a flat n-element buffer; seconds per step.
+// Times AdamW steps over a flat n-element buffer; median seconds per step.
 int ref_adamw_time(int64_t n, int iters, double* sec) {
     return guarded([&] {
         auto pt = (torch::randn({n}) * 0.02).requires_grad_(true);
@@ -565,11 +574,7 @@ int ref_adamw_time(int64_t n, int iters, double* sec) {
         o.weight_decay = 0.01;
         Nott::Optimizer::Details::AdamW opt(std::vector<at::Tensor>{pt}, Nott::Optimizer::Details::to_torch_options(o));
         opt.ensure_state_initialized();
-        opt.step();
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) opt.step();
-        auto t1 = std::chrono::steady_clock::now();
-        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+        *sec = median_seconds(iters, [&] { opt.step(); });
     });
 }
 
@@ -587,11 +592,7 @@ int ref_layernorm_bwd_time(int64_t rows, int64_t d, int iters, double* sec) {
         const auto& mean = std::get<1>(fwd);
         const auto& rstd = std::get<2>(fwd);
         auto once = [&] { return at::native_layer_norm_backward(dy, x, {d}, mean, rstd, gamma, beta, {true, true, true}); };
-        once();
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) once();
-        auto t1 = std::chrono::steady_clock::now();
-        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+        *sec = median_seconds(iters, once);
     });
 }
 
@@ -609,11 +610,7 @@ int ref_cross_entropy_time(int64_t n, int64_t c, int iters, double* sec) {
             l.backward();
             z.mutable_grad().reset();
         };
-        once();
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) once();
-        auto t1 = std::chrono::steady_clock::now();
-        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+        *sec = median_seconds(iters, once);
     });
 }
 
@@ -637,11 +634,7 @@ int ref_mha_bwd_time(int64_t b, int64_t t, int64_t e, int64_t heads, int causal,
         auto xt = torch::randn({b, t, e}).requires_grad_(true);
         auto yt = mha->forward(xt, xt, xt);
         auto dy = torch::randn({b, t, e});
-        yt.backward(dy, /*retain_graph=*/true);
-        auto t0 = std::chrono::steady_clock::now();
-        for (int i = 0; i < iters; ++i) yt.backward(dy, /*retain_graph=*/true);
-        auto t1 = std::chrono::steady_clock::now();
-        *sec = std::chrono::duration<double>(t1 - t0).count() / iters;
+        *sec = median_seconds(iters, [&] { yt.backward(dy, /*retain_graph=*/true); });
     });
 }
 
@@ -864,9 +857,9 @@ int ref_init_params(int model, uint64_t seed, int64_t count, const char* const* 
     });
 }
 
-// Times `iters` full fp32 training steps on the CPU (forward, CE mean,
+// Times full fp32 training steps on the CPU (forward, CE mean,
 // backward, Adam (model 0, configs[0]) or AdamW (model 1, configs[4]) step,
-// zero_grad) at the given batch; seconds per step in *sec.  Inputs
+// zero_grad) at the given batch; median seconds per step in *sec.  Inputs
 // uniform[0,1), labels uniform, weights HeUniform from torch's CPU generator.
 int ref_train_step_time(int model, int64_t batch, int iters, double* sec) {
     return guarded([&] {
