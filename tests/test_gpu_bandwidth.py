@@ -361,7 +361,9 @@ def test_layernorm_full_size_invariants(ops):
 @pytest.mark.parametrize("n,c,eps,ignore", [(64, 10, 0.0, False), (64, 1000, 0.0, False), (33, 1001, 0.1, True),
                                             (256, 32000, 0.0, False), (8, 40000, 0.05, True), (5, 7, 0.0, False),
                                             # more rows than resident workgroups: each takes several rows
-                                            (2000, 5000, 0.1, True), (600, 32000, 0.0, True), (5000, 1000, 0.0, True)])
+                                            (2000, 5000, 0.1, True), (600, 32000, 0.0, True), (5000, 1000, 0.0, True),
+                                            # single-workgroup path (c <= 64, n <= 4096) at its limits
+                                            (4096, 64, 0.1, True), (3000, 33, 0.05, True), (1, 3, 0.0, False)])
 def test_softmax_xent(ops, oracle, dt, n, c, eps, ignore):
     g = rng(n + c)
     z = host_input(g.standard_normal((n, c)) * 2.0, dt)
@@ -373,8 +375,11 @@ def test_softmax_xent(ops, oracle, dt, n, c, eps, ignore):
     check(host(dl), dle, dt, "xent dlogits")
     check(loss.item(), losse, "f32", "xent loss", rtol=1e-5)
     # label gather is exact: the target column carries the −(1−ε)/n term
+    # (negative without smoothing; with it a label of probability above
+    # 1 − ε + ε/c has a positive gradient)
     rows = np.nonzero(y != -100)[0]
-    assert (host(dl)[rows, y[rows]] < 0).all()
+    if eps == 0.0:
+        assert (host(dl)[rows, y[rows]] < 0).all()
 
 
 @pytest.mark.parametrize("dt", DTYPES)
@@ -439,6 +444,31 @@ def test_adamw_full_size_config(ops, oracle, dt):
         assert np.array_equal(host(p).view(np.int32), pe.view(np.int32))
     else:
         assert np.array_equal(host(p), host_input(pe, "bf16"))
+
+
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("c", [37, 40])
+def test_softmax_xent_small_path_matches_general_path(ops, dt, c):
+    """4096 rows of c classes take the single-workgroup kernel; the same rows
+    plus one ignored row (4097 rows, same valid count) take the three-launch
+    path.  With c = 37 that path is the element kernel, whose summation order
+    the small kernel keeps: gradients and loss agree bit for bit.  With c = 40
+    it is the vector kernel (16-byte groups summed first): within rounding."""
+    g = rng(41)
+    z = host_input(g.standard_normal((4097, c)) * 2.0, dt)
+    y = g.integers(0, c, 4097).astype(np.int64)
+    y[::7] = -100
+    y[-1] = -100
+    zd, yd = dev(z, dt), torch.from_numpy(y).cuda()
+    dl_small, loss_small = ops.softmax_xent_bwd(zd[:4096].contiguous(), yd[:4096].contiguous(), label_smoothing=0.1)
+    dl_gen, loss_gen = ops.softmax_xent_bwd(zd, yd, label_smoothing=0.1)
+    torch.cuda.synchronize()
+    if c % 4 != 0:
+        assert torch.equal(dl_small, dl_gen[:4096])
+        assert torch.equal(loss_small, loss_gen)
+    else:
+        check(host(dl_small), host(dl_gen[:4096]), dt, "small vs vector path dlogits")
+        check(loss_small.item(), loss_gen.item(), "f32", "small vs vector path loss", rtol=1e-6)
 
 
 def test_softmax_xent_bad_label_is_reported(ops):

@@ -33,7 +33,10 @@ def ops():
 # ------------------------------------------------------------------ linear
 LIN = [(1, 1, 1), (7, 5, 3), (64, 3136, 128), (64, 128, 10), (64, 512, 1000), (129, 70, 33), (256, 1024, 1024),
        # bf16 fast-path shapes: partial 128-tiles, split-K over 4096 rows
-       (384, 192, 256), (136, 64, 64), (4096, 64, 64), (1024, 320, 192)]
+       (384, 192, 256), (136, 64, 64), (4096, 64, 64), (1024, 320, 192),
+       # 64x64-tile grids (run_small): forward split over 16 stages with a
+       # partial last stage; dW split over 2000 rows, ragged tiles
+       (33, 1000, 17), (2000, 40, 24)]
 
 
 @pytest.mark.parametrize("dt", DTYPES)
@@ -119,6 +122,14 @@ def test_linear_accumulate_and_partial_outputs(ops, oracle):
     check(host(dbd), db0 + rdb, what="accumulated db")
     check(host(dw2), rdw, what="dw without dx")
     check(host(db2), rdb, what="db without dx")
+    # dW split over the rows (64x64-tile grid): the reduce adds the existing values
+    x, w, dy = f32(g.standard_normal((3000, 40))), f32(g.standard_normal((30, 40))), f32(g.standard_normal((3000, 30)))
+    dwd, dbd = dev(dw0), dev(db0)
+    ops.linear_bwd(dev(dy), dev(x), dev(w), dw=dwd, db=dbd, accumulate=True, need_dx=False)
+    torch.cuda.synchronize()
+    _, rdw, rdb = oracle.linear_bwd(dy, x, w)
+    check(host(dwd), dw0 + rdw, what="accumulated split dw")
+    check(host(dbd), db0 + rdb, what="accumulated split db")
 
 
 # -------------------------------------------------------------------- conv

@@ -58,10 +58,13 @@ __device__ __forceinline__ void mfma_chunk(const u32x4& a, const u32x4& b, f32x4
 // about rounds · (chunks + per-tile overhead), plus the split reduce when
 // S > 1 (both in units of one chunk's tap loop; measured: a tile's prologue
 // and epilogue cost about two bf16 chunks or half an fp32 one, the reduce
-// 2.5 bf16 chunks or one fp32 chunk).  The smallest S of least cost wins: a
-// grid of a few more workgroups than slots would run a whole second round.
+// 2.5 bf16 chunks or three quarters of an fp32 one: a 49-tile fp32 forward
+// of two chunks, 32 -> 64 channels at 14×14, ran 28 µs whole against 16 µs
+// per single-chunk workgroup plus a 5 µs reduce).  The smallest S of least
+// cost wins: a grid of a few more workgroups than slots would run a whole
+// second round.
 inline int32_t pick_chunk_splits(int64_t blocks, int32_t nchunks, int64_t slots, size_t elem) {
-    const double overhead = elem == 2 ? 2.0 : 0.5, reduce = elem == 2 ? 2.5 : 1.0;
+    const double overhead = elem == 2 ? 2.0 : 0.5, reduce = elem == 2 ? 2.5 : 0.75;
     double best = 0.0;
     int32_t pick = 1;
     for (int32_t s = 1; s <= std::min(nchunks, 8); ++s) {

@@ -381,6 +381,146 @@ int run(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64
     return launch_status(ctx, "gemm_splitk");
 }
 
+// ---------------------------------------------------------------------------
+// Small-grid variant for products whose 128×128 grid would leave most CUs
+// idle (a Linear layer at a small batch: M = 64 rows, or a 10-column output).
+// Tile 64×64 per 256-thread workgroup (4 waves as 2×2, 32×32 each = 2×2
+// MFMA 16×16 tiles); a stage holds 256 bytes of k per row (64 fp32 / 128
+// bf16), all of it loaded at once (4 chunks per operand per thread), so a
+// one-stage workgroup has a single load round trip.  Split-K cuts the k range
+// into whole stages to give the grid ~2 workgroups per CU once a tile would
+// take more than two stages; the partials are summed in split order by the
+// same reduce kernel as above.  Operand and epilogue interfaces as gemm_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kSmallTile = 64;
+constexpr int kSmallPitch = 272;   // 256 bytes of k + 16: a quarter-wave's 16 rows hit distinct 16-byte slots
+
+template <class L>
+__device__ __forceinline__ void small_map(int i, int& row, int& ch) {
+    // i in [0, 1024): chunk index inside the 64-row × 16-chunk stage.
+    if (L::kRowFast) {
+        row = i & 63;
+        ch = i >> 6;
+    } else {
+        row = i >> 4;
+        ch = i & 15;
+    }
+}
+
+template <typename T, class LA, class LB, class EP>
+__global__ __launch_bounds__(kThreads) void gemm64_kernel(LA la, LB lb, EP ep, int64_t M, int64_t N, int64_t K,
+                                                          int64_t k_per_split) {
+    __shared__ __attribute__((aligned(16))) char lds[2][kSmallTile * kSmallPitch];
+    constexpr int E = KTraits<T>::kElemsPerChunk;
+    constexpr int KC = 16 * E;   // k elements per stage
+    const int64_t m0 = (int64_t)blockIdx.y * kSmallTile, n0 = (int64_t)blockIdx.x * kSmallTile;
+    const int64_t kb = (int64_t)blockIdx.z * k_per_split;
+    const int64_t ke = std::min<int64_t>(K, kb + k_per_split);
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+    const int wm = wid >> 1, wn = wid & 1;
+    const int r16 = lane & 15, kq = lane >> 4;
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t ns = ke > kb ? (ke - kb + KC - 1) / KC : 0;
+    u32x4 ra[4], rb[4];
+    auto fetch = [&](int64_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int row, ch;
+            small_map<LA>(tid + j * kThreads, row, ch);
+            ra[j] = la.chunk(m0 + row, k0 + ch * E);
+            small_map<LB>(tid + j * kThreads, row, ch);
+            rb[j] = lb.chunk(n0 + row, k0 + ch * E);
+        }
+    };
+    if (ns > 0) fetch(kb);
+    for (int64_t t = 0; t < ns; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int row, ch;
+            small_map<LA>(tid + j * kThreads, row, ch);
+            *reinterpret_cast<u32x4*>(lds[0] + row * kSmallPitch + ch * 16) = ra[j];
+            small_map<LB>(tid + j * kThreads, row, ch);
+            *reinterpret_cast<u32x4*>(lds[1] + row * kSmallPitch + ch * 16) = rb[j];
+        }
+        __syncthreads();
+        if (t + 1 < ns) fetch(kb + (t + 1) * KC);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {   // four 64-byte k slices
+            u32x4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const u32x4*>(lds[0] + (wm * 32 + i * 16 + r16) * kSmallPitch + s * 64 +
+                                                       kq * 16);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const u32x4*>(lds[1] + (wn * 32 + j * 16 + r16) * kSmallPitch + s * 64 +
+                                                       kq * 16);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    if constexpr (sizeof(T) == 2) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, a[i]), __builtin_bit_cast(bf16x8, b[j]), acc[i][j], 0, 0, 0);
+                    } else {
+                        const f32x4 af = __builtin_bit_cast(f32x4, a[i]);
+                        const f32x4 bf = __builtin_bit_cast(f32x4, b[j]);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc[i][j], 0, 0, 0);
+                    }
+                }
+        }
+        __syncthreads();
+    }
+    const int rq = kq * 4;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ep.store(m0 + wm * 32 + i * 16 + rq + e, n0 + wn * 32 + j * 16 + r16, acc[i][j][e]);
+}
+
+// True when the 128×128 grid of `run` would have fewer workgroups than CUs.
+inline bool small_grid(nott_ctx ctx, int64_t M, int64_t N) {
+    return ceil_div(M, BM) * ceil_div(N, BN) < ctx->num_cu;
+}
+
+// C = A·B on the 64×64 tiles, as run().
+template <typename T, class LA, class LB, class EP>
+int run_small(nott_ctx ctx, const LA& la, const LB& lb, const EP& ep, int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0) return NOTT_OK;
+    constexpr int KC = 16 * KTraits<T>::kElemsPerChunk;
+    const int64_t tn = ceil_div(N, kSmallTile), tm = ceil_div(M, kSmallTile);
+    if (tn > 0x7fffffff || tm > 65535) return fail(ctx, NOTT_ERR_UNSUPPORTED, "gemm: grid too large");
+    const int64_t stages = std::max<int64_t>(1, ceil_div(K, KC));
+    int64_t splits = 1;
+    if (stages > 2) splits = std::min<int64_t>({stages, std::max<int64_t>(1, ceil_div(2 * ctx->num_cu, tn * tm)), 65535});
+    const int64_t kps = ceil_div(stages, splits) * KC;   // whole stages per split
+    splits = std::max<int64_t>(1, ceil_div(K, kps));
+    if (splits == 1) {
+        hipLaunchKernelGGL((gemm64_kernel<T, LA, LB, EP>), dim3((unsigned)tn, (unsigned)tm, 1), dim3(kThreads), 0,
+                           ctx->stream, la, lb, ep, M, N, K, std::max<int64_t>(K, 1));
+        return launch_status(ctx, "gemm64_kernel");
+    }
+    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)(splits * M * N)));
+    if (!ws) return NOTT_ERR_ALLOC;
+    PartialStore ps{ws, M, N};
+    hipLaunchKernelGGL((gemm64_kernel<T, LA, LB, PartialStore>), dim3((unsigned)tn, (unsigned)tm, (unsigned)splits),
+                       dim3(kThreads), 0, ctx->stream, la, lb, ps, M, N, K, kps);
+    launch_splitk_reduce(ctx, ws, splits, M, N, ep);
+    return launch_status(ctx, "gemm64_splitk");
+}
+
 }  // namespace gemm
 }  // namespace nott
 

@@ -12,7 +12,8 @@
 // bf16 operands whose k extent is a multiple of 64 take the direct-to-LDS
 // GEMM (gemm_dma.hpp) when both output extents are at least 128, else the
 // register-staged fast GEMM (gemm.hpp, namespace fast); everything else the
-// generic engine.  Every product runs on the kernels in this library; no
+// generic engine, on 64×64 tiles with split-K (run_small) where its 128×128
+// grid would leave CUs idle (small batches, narrow outputs).  Every product runs on the kernels in this library; no
 // vendor GEMM is called.
 #include "gemm_dma.hpp"
 
@@ -206,6 +207,7 @@ int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const
     RowKLoader<T> la{xp, kin, m, kin, vec16<T>(x, kin)};
     RowKLoader<T> lb{wp, kin, nout, kin, vec16<T>(w, kin)};
     RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
+    if (small_grid(ctx, m, nout)) return run_small<T>(ctx, la, lb, ep, m, nout, kin);
     return run<T>(ctx, la, lb, ep, m, nout, kin);
 }
 
@@ -264,14 +266,16 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
         RowKLoader<T> la{dyp, nout, m, nout, vec16<T>(dy, nout)};
         ColKLoader<T> lb{static_cast<const T*>(w), kin, kin, nout};
         RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
-        const int st = run<T>(ctx, la, lb, ep, m, kin, nout);
+        const int st = small_grid(ctx, m, kin) ? run_small<T>(ctx, la, lb, ep, m, kin, nout)
+                                               : run<T>(ctx, la, lb, ep, m, kin, nout);
         if (st != NOTT_OK) return st;
     }
     if (dw || db) {
         ColKLoader<T> la{dyp, nout, nout, m};
         ColKOnesLoader<T> lb{static_cast<const T*>(x), kin, kin, m, db != nullptr};
         DwDbStore ep{dw, db, nout, kin, accumulate};
-        const int st = run<T>(ctx, la, lb, ep, nout, kin + 1, m);
+        const int st = small_grid(ctx, nout, kin + 1) ? run_small<T>(ctx, la, lb, ep, nout, kin + 1, m)
+                                                      : run<T>(ctx, la, lb, ep, nout, kin + 1, m);
         if (st != NOTT_OK) return st;
     }
     return NOTT_OK;

@@ -255,6 +255,73 @@ __global__ __launch_bounds__(1024) void xent_loss_kernel(const float* __restrict
 
 __global__ void xent_nan_kernel(float* __restrict__ loss) { *loss = __builtin_nanf(""); }
 
+// Small problems (c <= 64 classes, n <= kSmallRows rows; a classifier head at
+// a small batch): the label count, every row and the mean loss in one
+// 1024-thread workgroup, where the general path takes three launches.  A wave
+// owns rows wid, wid + 16, ... with lane j holding column j; the arithmetic
+// and the summation orders are those of xent_count_kernel, the element path
+// xent_row_kernel<T, 64, 16> and xent_loss_kernel, so where the general path
+// takes the element path (c not a multiple of the 16-byte group) both give
+// the same bits; its vector path sums each thread's group first.
+constexpr int64_t kSmallRows = 4096;
+template <typename T>
+__global__ __launch_bounds__(1024) void xent_small_kernel(const T* __restrict__ logits,
+                                                          const int64_t* __restrict__ labels, int64_t n, int64_t c,
+                                                          float smoothing, float grad_scale, T* __restrict__ dlogits,
+                                                          float* __restrict__ loss,
+                                                          unsigned long long* __restrict__ err) {
+    __shared__ float red[16];
+    __shared__ float rl[kSmallRows];
+    __shared__ int nvs;
+    float cnt = 0.f;
+    unsigned bad = 0;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) {
+        const int64_t y = labels[i];
+        if (y == kIgnoreIndex) continue;
+        if (y < 0 || y >= c) ++bad;
+        else cnt += 1.f;
+    }
+    const float total = block_sum<16>(cnt, red);
+    if (bad) atomicAdd(err, (unsigned long long)bad);
+    if (threadIdx.x == 0) nvs = (int)total;
+    __syncthreads();
+    const int nv = nvs;
+    constexpr float kLog2e = 1.4426950408889634f;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int ci = (int)c;
+    for (int64_t row = wid; row < n; row += 16) {
+        const T* z = logits + row * c;
+        T* dz = dlogits + row * c;
+        const int64_t y = labels[row];
+        const float v = lane < ci ? Io<T>::ld(z, lane) : -INFINITY;
+        if (!(y >= 0 && y < c)) {
+            if (lane < ci) Io<T>::st(dz, lane, 0.f);
+            if (lane == 0) rl[row] = 0.f;
+            continue;
+        }
+        const float mx = wave_max(v);
+        const float sz = smoothing != 0.f ? wave_sum(v == -INFINITY ? 0.f : v) : 0.f;
+        const float pe = __builtin_amdgcn_exp2f(fmaf(v, kLog2e, -mx * kLog2e));
+        const float se = wave_sum(pe);
+        const float lse = mx + __logf(se);
+        const float scale = grad_scale / (float)nv;
+        const float off = smoothing / (float)c;
+        const float hit = 1.f - smoothing;
+        if (lane < ci) {
+            float g = fmaf(pe, scale / se, -scale * off);
+            if (lane == (int)y) g -= scale * hit;
+            Io<T>::st(dz, lane, g);
+        }
+        if (lane == 0) rl[row] = hit * (lse - Io<T>::ld(z, y)) + off * ((float)c * lse - sz);
+    }
+    if (!loss) return;
+    __syncthreads();
+    float acc = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) acc += rl[i];
+    acc = block_sum<16>(acc, red);
+    if (threadIdx.x == 0) *loss = nv > 0 ? acc / (float)nv : __builtin_nanf("");
+}
+
 template <typename T, int NT, int EPT, bool VEC>
 void launch_rows(nott_ctx ctx, int64_t n, int64_t c, const void* logits, const int64_t* labels, float eps,
                  float scale, const int* nvalid, void* dl, float* row_loss) {
@@ -316,13 +383,24 @@ extern "C" int nott_softmax_xent_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, 
         if (loss) hipLaunchKernelGGL(xent_nan_kernel, dim3(1), dim3(1), 0, ctx->stream, loss);  // mean of nothing
         return nott::launch_status(ctx, "softmax_xent");
     }
+    const float eps = (float)label_smoothing, scale = (float)grad_scale;
+    if (c <= 64 && n <= kSmallRows) {
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL(xent_small_kernel<float>, dim3(1), dim3(1024), 0, ctx->stream,
+                               static_cast<const float*>(logits), labels, n, c, eps, scale,
+                               static_cast<float*>(dlogits), loss, ctx->err_word);
+        else
+            hipLaunchKernelGGL(xent_small_kernel<bf16_t>, dim3(1), dim3(1024), 0, ctx->stream,
+                               static_cast<const bf16_t*>(logits), labels, n, c, eps, scale,
+                               static_cast<bf16_t*>(dlogits), loss, ctx->err_word);
+        return nott::launch_status(ctx, "softmax_xent");
+    }
     // workspace: [nvalid int][pad to 256 B][row_loss n floats]
     char* ws = static_cast<char*>(nott::workspace(ctx, 256 + sizeof(float) * (size_t)n));
     if (!ws) return NOTT_ERR_ALLOC;
     int* nvalid = reinterpret_cast<int*>(ws);
     float* row_loss = loss ? reinterpret_cast<float*>(ws + 256) : nullptr;
     hipLaunchKernelGGL(xent_count_kernel, dim3(1), dim3(1024), 0, ctx->stream, labels, n, c, nvalid, ctx->err_word);
-    const float eps = (float)label_smoothing, scale = (float)grad_scale;
     if (dtype == NOTT_F32)
         dispatch<float>(ctx, n, c, logits, labels, eps, scale, nvalid, dlogits, row_loss);
     else
