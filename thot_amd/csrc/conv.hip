@@ -259,7 +259,7 @@ struct WgradStore {
 
 // db[k] = Σ_{n,p,q} dy[n,k,p,q] in two deterministic passes: workgroup
 // (k, z) sums images [z·npb, (z+1)·npb) of channel k into part[z][k], then
-// conv_db_finish_kernel adds the kDbSlabs partials of a channel in slab order.
+// conv_db_finish_kernel adds the kDbSlabs partials of a channel.
 constexpr int kDbSlabs = 32;
 template <typename T>
 __global__ __launch_bounds__(256) void conv_db_partial_kernel(const T* __restrict__ dy, Geom g, int32_t npb,
@@ -279,13 +279,16 @@ __global__ __launch_bounds__(256) void conv_db_partial_kernel(const T* __restric
     if (threadIdx.x == 0) part[(int64_t)z * g.k + ko] = s;
 }
 
+// One wave per channel: lane z loads slab z's partial (all loads in flight
+// at once), and the wave sums them in its fixed butterfly order.
 __global__ __launch_bounds__(256) void conv_db_finish_kernel(const float* __restrict__ part, int32_t k,
                                                              float* __restrict__ db, int accumulate) {
-    const int32_t ko = blockIdx.x * 256 + threadIdx.x;
+    static_assert(kDbSlabs <= 64, "one partial per lane");
+    const int32_t ko = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (ko >= k) return;
-    float s = 0.f;
-    for (int z = 0; z < kDbSlabs; ++z) s += part[(int64_t)z * k + ko];
-    db[ko] = accumulate ? db[ko] + s : s;
+    const float s = wave_sum(lane < kDbSlabs ? part[(int64_t)lane * k + ko] : 0.f);
+    if (lane == 0) db[ko] = accumulate ? db[ko] + s : s;
 }
 
 // ---------------------------------------------------------------------------
@@ -571,7 +574,7 @@ int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) 
 //   wgrad: dw[co, 0, r, s] = Σ_{n,h,w} dy[n, co, h, w] · x[n, 0, h+r−1, w+s−1]
 //   db   : db[co] = Σ_{n,h,w} dy[n, co, h, w]  (a tenth sum of the same pass)
 // wgrad is deterministic: workgroup (co, slab of images) writes 10 partial
-// sums, and a second pass adds the slabs in order.
+// sums, and a second pass adds the slabs in a fixed order (one wave per sum).
 // ---------------------------------------------------------------------------
 bool cin1_applies(const nott_conv2d_desc* d) {
     return d->layout == NOTT_NCHW && d->groups == 1 && d->c == 1 && d->r == 3 && d->s == 3 && d->stride_h == 1 &&
@@ -660,17 +663,20 @@ __global__ __launch_bounds__(256) void cin1_wgrad_partial_kernel(const T* __rest
     }
 }
 
+// One wave per output (co·10 + j, j a tap or 9 for the bias): lane z loads
+// slab z's partial and the wave sums them in its fixed butterfly order.
 __global__ __launch_bounds__(256) void cin1_wgrad_finish_kernel(const float* __restrict__ part, int32_t k,
                                                                 float* __restrict__ dw, float* __restrict__ db,
                                                                 int accumulate) {
-    const int i = blockIdx.x * 256 + threadIdx.x;     // co·10 + j (j = tap, or 9 for the bias)
+    static_assert(kCin1Slabs <= 64, "one partial per lane");
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= k * 10) return;
     const int co = i / 10, j = i - co * 10;
     float* out = j < 9 ? (dw ? dw + co * 9 + j : nullptr) : (db ? db + co : nullptr);
     if (!out) return;
-    float s = 0.f;
-    for (int z = 0; z < kCin1Slabs; ++z) s += part[((int64_t)co * kCin1Slabs + z) * 10 + j];
-    *out = accumulate ? *out + s : s;
+    const float s = wave_sum(lane < kCin1Slabs ? part[((int64_t)co * kCin1Slabs + lane) * 10 + j] : 0.f);
+    if (lane == 0) *out = accumulate ? *out + s : s;
 }
 
 template <typename T>
@@ -689,7 +695,7 @@ int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy,
     if (!part) return NOTT_ERR_ALLOC;
     hipLaunchKernelGGL(cin1_wgrad_partial_kernel<T>, dim3((unsigned)d->k, kCin1Slabs), dim3(256), 0, ctx->stream, x,
                        dy, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, part);
-    hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 10, (int64_t)256)), dim3(256), 0,
+    hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 10, (int64_t)4)), dim3(256), 0,
                        ctx->stream, part, (int32_t)d->k, dw, db, accumulate);
     return nott::launch_status(ctx, "conv2d_bwd_weight (1 input channel)");
 }
@@ -785,7 +791,7 @@ int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, int64_t p, int64_t q, const v
         const int32_t npb = (int32_t)nott::ceil_div((int64_t)d->n, (int64_t)kDbSlabs);
         hipLaunchKernelGGL(conv_db_partial_kernel<T>, dim3((unsigned)d->k, kDbSlabs), dim3(256), 0, ctx->stream,
                            static_cast<const T*>(dy), g, npb, part);
-        hipLaunchKernelGGL(conv_db_finish_kernel, dim3((unsigned)nott::ceil_div((int64_t)d->k, (int64_t)256)), dim3(256),
+        hipLaunchKernelGGL(conv_db_finish_kernel, dim3((unsigned)nott::ceil_div((int64_t)d->k, (int64_t)4)), dim3(256),
                            0, ctx->stream, part, (int32_t)d->k, db, accumulate);
         return nott::launch_status(ctx, "conv_db");
     }
