@@ -573,12 +573,14 @@ int check_desc(nott_ctx ctx, const nott_conv2d_desc* d, int64_t* p, int64_t* q) 
 //   fwd  : y[n, co, h, w] = b[co] + Σ_{r,s} x[n, 0, h+r−1, w+s−1] · wt[co, 0, r, s]
 //   wgrad: dw[co, 0, r, s] = Σ_{n,h,w} dy[n, co, h, w] · x[n, 0, h+r−1, w+s−1]
 //   db   : db[co] = Σ_{n,h,w} dy[n, co, h, w]  (a tenth sum of the same pass)
-// wgrad is deterministic: workgroup (co, slab of images) writes 10 partial
-// sums, and a second pass adds the slabs in a fixed order (one wave per sum).
+// wgrad is deterministic: workgroup (channel group, slab of images) writes
+// 10 partial sums per channel, and a second pass adds the slabs in a fixed
+// order (one wave per sum).
 // ---------------------------------------------------------------------------
 bool cin1_applies(const nott_conv2d_desc* d) {
     return d->layout == NOTT_NCHW && d->groups == 1 && d->c == 1 && d->r == 3 && d->s == 3 && d->stride_h == 1 &&
-           d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1 && d->dil_h == 1 && d->dil_w == 1 && d->k <= 256;
+           d->stride_w == 1 && d->pad_h == 1 && d->pad_w == 1 && d->dil_h == 1 && d->dil_w == 1 && d->k <= 256 &&
+           d->n * d->h * d->w < (int64_t(1) << 31);
 }
 
 // The 9 taps of x around pixel (h, w) of image plane xp (zero outside).
@@ -595,71 +597,87 @@ __device__ __forceinline__ void cin1_taps(const T* __restrict__ xp, int32_t h, i
 }
 
 // Thread = one pixel for kCin1Co output channels (grid.y = channel group;
-// weights and bias in LDS).
+// the group's weights and bias in LDS).  Pixel indices are 32-bit
+// (cin1_applies bounds n·h·w).
 constexpr int kCin1Co = 8;
 template <typename T>
 __global__ __launch_bounds__(256) void cin1_fwd_kernel(const T* __restrict__ x, const T* __restrict__ wt,
                                                        const float* __restrict__ b, T* __restrict__ y, int32_t n,
                                                        int32_t H, int32_t W, int32_t k, int relu) {
-    __shared__ float lw[256 * 9], lb[256];
-    for (int i = threadIdx.x; i < k * 9; i += 256) lw[i] = Io<T>::ld(wt, i);
-    for (int i = threadIdx.x; i < k; i += 256) lb[i] = b ? b[i] : 0.f;
+    __shared__ float lw[kCin1Co * 9], lb[kCin1Co];
+    const int co0 = blockIdx.y * kCin1Co;
+    if (threadIdx.x < kCin1Co * 9) {
+        const int co = co0 + (int)threadIdx.x / 9;
+        lw[threadIdx.x] = co < k ? Io<T>::ld(wt, co0 * 9 + threadIdx.x) : 0.f;
+    }
+    if (threadIdx.x < kCin1Co) lb[threadIdx.x] = (b && co0 + (int)threadIdx.x < k) ? b[co0 + threadIdx.x] : 0.f;
     __syncthreads();
-    const int64_t hw = (int64_t)H * W;
-    const int64_t pix = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (pix >= (int64_t)n * hw) return;
-    const int64_t img = pix / hw, in = pix - img * hw;
-    const int32_t h = (int32_t)(in / W), w = (int32_t)(in - (int64_t)h * W);
+    const uint32_t hw = (uint32_t)H * (uint32_t)W;
+    const uint32_t pix = blockIdx.x * 256u + threadIdx.x;
+    if (pix >= (uint32_t)n * hw) return;
+    const uint32_t img = pix / hw, in = pix - img * hw;
+    const int32_t h = (int32_t)(in / (uint32_t)W), w = (int32_t)(in - (uint32_t)h * (uint32_t)W);
     float t[9];
-    cin1_taps<T>(x + img * hw, h, w, H, W, t);
-    T* yp = y + img * k * hw + in;
-    const int co1 = min(k, (int)(blockIdx.y + 1) * kCin1Co);
-    for (int co = blockIdx.y * kCin1Co; co < co1; ++co) {
-        float a = lb[co];
+    cin1_taps<T>(x + (int64_t)img * hw, h, w, H, W, t);
+    T* yp = y + ((int64_t)img * k + co0) * hw + in;
 #pragma unroll
-        for (int j = 0; j < 9; ++j) a = __builtin_fmaf(t[j], lw[co * 9 + j], a);
-        Io<T>::st(yp, (int64_t)co * hw, relu ? relu_out(a) : a);
+    for (int c = 0; c < kCin1Co; ++c) {
+        if (co0 + c >= k) break;
+        float a = lb[c];
+#pragma unroll
+        for (int j = 0; j < 9; ++j) a = __builtin_fmaf(t[j], lw[c * 9 + j], a);
+        Io<T>::st(yp, (int64_t)c * hw, relu ? relu_out(a) : a);
     }
 }
 
 constexpr int kCin1Slabs = 64;
 
-// Workgroup (co, slab): 9 partial sums over the slab's images.
+// Workgroup (channel group, slab): for each of kCin1Co channels, 9 tap sums
+// and Σ dy over the slab's images.  A thread gathers a pixel's 9 taps once
+// and uses them for every channel of the group.
 template <typename T>
 __global__ __launch_bounds__(256) void cin1_wgrad_partial_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                  int32_t n, int32_t H, int32_t W, int32_t k,
                                                                  float* __restrict__ part) {
-    __shared__ float red[4][10];
-    const int co = blockIdx.x, slab = blockIdx.y;
-    const int64_t hw = (int64_t)H * W;
+    __shared__ float red[4][kCin1Co * 10];
+    const int co0 = blockIdx.x * kCin1Co, slab = blockIdx.y;
+    const uint32_t hw = (uint32_t)H * (uint32_t)W;
     const int32_t per = (n + kCin1Slabs - 1) / kCin1Slabs;
     const int32_t n0 = slab * per, n1 = min(n, n0 + per);
-    float acc[10];       // 9 taps, then Σ dy
+    const int nco = min(kCin1Co, k - co0);
+    float acc[kCin1Co][10];   // per channel: 9 taps, then Σ dy
 #pragma unroll
-    for (int j = 0; j < 10; ++j) acc[j] = 0.f;
+    for (int c = 0; c < kCin1Co; ++c)
+#pragma unroll
+        for (int j = 0; j < 10; ++j) acc[c][j] = 0.f;
     for (int32_t img = n0; img < n1; ++img) {
         const T* xp = x + (int64_t)img * hw;
-        const T* dp = dy + ((int64_t)img * k + co) * hw;
-        for (int64_t in = threadIdx.x; in < hw; in += 256) {
-            const int32_t h = (int32_t)(in / W), w = (int32_t)(in - (int64_t)h * W);
+        const T* dp = dy + ((int64_t)img * k + co0) * hw;
+        for (uint32_t in = threadIdx.x; in < hw; in += 256) {
+            const int32_t h = (int32_t)(in / (uint32_t)W), w = (int32_t)(in - (uint32_t)h * (uint32_t)W);
             float t[9];
             cin1_taps<T>(xp, h, w, H, W, t);
-            const float g = Io<T>::ld(dp, in);
 #pragma unroll
-            for (int j = 0; j < 9; ++j) acc[j] = __builtin_fmaf(g, t[j], acc[j]);
-            acc[9] += g;
+            for (int c = 0; c < kCin1Co; ++c) {
+                const float g = c < nco ? Io<T>::ld(dp, (int64_t)c * hw + in) : 0.f;
+#pragma unroll
+                for (int j = 0; j < 9; ++j) acc[c][j] = __builtin_fmaf(g, t[j], acc[c][j]);
+                acc[c][9] += g;
+            }
         }
     }
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
-    for (int j = 0; j < 10; ++j) {
-        const float v = wave_sum(acc[j]);
-        if (lane == 0) red[wid][j] = v;
-    }
+    for (int c = 0; c < kCin1Co; ++c)
+#pragma unroll
+        for (int j = 0; j < 10; ++j) {
+            const float v = wave_sum(acc[c][j]);
+            if (lane == 0) red[wid][c * 10 + j] = v;
+        }
     __syncthreads();
-    if (threadIdx.x < 10) {
-        const int j = threadIdx.x;
-        part[((int64_t)co * kCin1Slabs + slab) * 10 + j] = (red[0][j] + red[1][j]) + (red[2][j] + red[3][j]);
+    if (threadIdx.x < nco * 10) {
+        const int i = threadIdx.x, c = i / 10, j = i - c * 10;
+        part[((int64_t)(co0 + c) * kCin1Slabs + slab) * 10 + j] = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
     }
 }
 
@@ -693,8 +711,9 @@ int cin1_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy,
                int accumulate) {
     float* part = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)d->k * kCin1Slabs * 10));
     if (!part) return NOTT_ERR_ALLOC;
-    hipLaunchKernelGGL(cin1_wgrad_partial_kernel<T>, dim3((unsigned)d->k, kCin1Slabs), dim3(256), 0, ctx->stream, x,
-                       dy, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k, part);
+    hipLaunchKernelGGL(cin1_wgrad_partial_kernel<T>, dim3((unsigned)nott::ceil_div(d->k, (int64_t)kCin1Co), kCin1Slabs),
+                       dim3(256), 0, ctx->stream, x, dy, (int32_t)d->n, (int32_t)d->h, (int32_t)d->w, (int32_t)d->k,
+                       part);
     hipLaunchKernelGGL(cin1_wgrad_finish_kernel, dim3((unsigned)nott::ceil_div(d->k * 10, (int64_t)4)), dim3(256), 0,
                        ctx->stream, part, (int32_t)d->k, dw, db, accumulate);
     return nott::launch_status(ctx, "conv2d_bwd_weight (1 input channel)");
