@@ -356,6 +356,43 @@ def test_conv3x3_large_grids(ops, case):
     check(host(dx), host(ref_dx), "bf16", "dx vs torch fp32")
 
 
+# bf16 3x3 passes on the direct-to-LDS kernel (conv3x3_dma.hip: row widths
+# dividing 112, 32-channel multiples): ragged last row bands (h not a
+# multiple of the 448-pixel tile's rows), loaded pixel ranges that start off
+# a 16-byte boundary (w = 28), several output-channel blocks and input
+# chunks, 28-row tiles (w = 16) and 4-row tiles (w = 112), workgroups that
+# walk several tiles.
+# (n, c, h, w, k)
+DMA3X3 = [
+    (2, 32, 30, 56, 96),
+    (3, 96, 14, 28, 64),
+    (2, 64, 9, 16, 32),
+    (4, 32, 8, 8, 64),
+    (3, 32, 21, 16, 64),
+    (1, 32, 5, 112, 64),
+    (8, 32, 30, 56, 512),      # 16 output blocks: workgroups walk two tiles each, across images
+]
+
+
+@pytest.mark.parametrize("case", DMA3X3, ids=lambda c: "n{}c{}h{}w{}k{}".format(*c))
+def test_conv3x3_dma_vs_oracle(ops, oracle, case):
+    """bf16 forward (with bias, with and without the fused ReLU) and data
+    gradient of the DMA kernel against the oracle."""
+    n, c, h, w_, k = case
+    cc = (n, c, h, w_, k, 3, 3, 1, 1, 1)
+    d = _desc(ops, cc)
+    x, w, b, dy = _inputs(cc, "bf16", 11 + sum(case))
+    y = ops.conv2d_fwd(dev(x, "bf16"), dev(w, "bf16"), dev(b), d)
+    yr = ops.conv2d_fwd(dev(x, "bf16"), dev(w, "bf16"), dev(b), d, relu=True)
+    dx = ops.conv2d_bwd_data(dev(dy, "bf16"), dev(w, "bf16"), d)
+    torch.cuda.synchronize()
+    ry = oracle.conv2d_fwd(d, x, w, b)
+    check(host(y), ry, "bf16", "conv y")
+    check(host(yr), np.maximum(ry, 0), "bf16", "conv relu(y)")
+    assert torch.equal(yr, torch.relu(y))
+    check(host(dx), oracle.conv2d_bwd_data(d, dy, w), "bf16", "conv dx")
+
+
 # fp32 3x3 grids of a little more than one round of workgroup slots (512 on
 # 256 CUs) with one output-channel block: the last tiles are split over their
 # channel chunks in the same launch (4 pieces each for 64 input channels, 8

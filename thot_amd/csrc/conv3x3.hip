@@ -475,6 +475,35 @@ template <typename T, bool DGRAD>
 int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const T* in, const T* wsrc,
              const float* bias, T* out, int relu = 0, const T* prepared = nullptr, T* dg_out = nullptr) {
     constexpr int CC = Chunk<T>::CC;
+    if constexpr (sizeof(T) == 2) {
+        // bf16 shapes the DMA kernel takes.  Prepared slices of such a shape
+        // are in its fragment layout, so that path has no fallback.
+        const bool dma = ctx->conv_dma && dma_applies(n, cin, h, w, cout);
+        const bool aligned = ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 7) == 0;
+        if (dma && (aligned || prepared)) {
+            const bf16_t* wpp = prepared;
+            if (!wpp) {
+                bf16_t* ws = static_cast<bf16_t*>(workspace(ctx, sizeof(T) * (size_t)dma_prep_elems(cin, cout)));
+                if (!ws) return NOTT_ERR_ALLOC;
+                const int st = dma_prep<DGRAD>(ctx, wsrc, ws, cin, cout);
+                if (st != NOTT_OK) return st;
+                wpp = ws;
+            }
+            if (dg_out) {
+                // the data gradient's pass is cout → cin over the same weight
+                if (ctx->conv_dma && dma_applies(n, cout, h, w, cin)) {
+                    const int st = dma_prep<true>(ctx, wsrc, dg_out, cout, cin);
+                    if (st != NOTT_OK) return st;
+                } else {
+                    hipLaunchKernelGGL((conv3x3_wprep_kernel<T, true>),
+                                       dim3((unsigned)ceil_div(9 * kTileCo * CC, 256), (unsigned)(cout / CC),
+                                            (unsigned)ceil_div(cin, kTileCo)),
+                                       dim3(256), 0, ctx->stream, wsrc, dg_out, cin, cout);
+                }
+            }
+            return dma_run(ctx, n, cin, h, w, cout, in, wpp, bias, out, relu);
+        }
+    }
     const int64_t cbc = ceil_div(cout, kTileCo);                 // 64-channel blocks (the last may be partial)
     const size_t wbytes = sizeof(T) * (size_t)cbc * kTileCo * cin * 9;
     const int32_t in_rows = (in_rows_bound(h, w) + 15) & ~15;   // whole 16-row LDS groups
@@ -511,6 +540,13 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     T* wp = reinterpret_cast<T*>(ws);
     if (prepared) {
         wp = const_cast<T*>(prepared);
+    } else if (dg_out && sizeof(T) == 2 && ctx->conv_dma && dma_applies(n, cout, h, w, cin)) {
+        hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),
+                           (unsigned)(cin / CC), (unsigned)cbc), dim3(256), 0, ctx->stream, wsrc, wp, cout, cin);
+        if constexpr (sizeof(T) == 2) {
+            const int st = dma_prep<true>(ctx, wsrc, dg_out, cout, cin);
+            if (st != NOTT_OK) return st;
+        }
     } else if (dg_out) {
         const int64_t cbd = ceil_div(cin, kTileCo);
         hipLaunchKernelGGL(conv3x3_wprep2_kernel<T>, dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),

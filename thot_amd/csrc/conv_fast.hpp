@@ -43,6 +43,18 @@ bool stem_wgrad_applies(nott_ctx ctx, const nott_conv2d_desc* d);
 template <typename T>
 int stem_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate);
 
+// bf16 3x3 / stride-1 forward and data gradient with DMA-filled LDS stages
+// (conv3x3_dma.hip), in a pass's own terms (cin → cout).  dma_applies is a
+// function of the shape only, so a forward can decide which layout the data
+// gradient's prepared weights take; dma_prep writes dma_prep_elems elements
+// (DGRAD: from the conv weight [cin][cout][3][3] of the pass, flipped).
+bool dma_applies(int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout);
+int64_t dma_prep_elems(int32_t cin, int32_t cout);
+template <bool DGRAD>
+int dma_prep(nott_ctx ctx, const bf16_t* w, bf16_t* wp, int32_t cin, int32_t cout);
+int dma_run(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const bf16_t* in,
+            const bf16_t* wp, const float* bias, bf16_t* out, int relu);
+
 // Widest load (bytes) that keeps every image row's pieces aligned.
 int wgrad_load_width(int64_t w, size_t elem);
 
