@@ -393,6 +393,38 @@ def test_conv3x3_dma_vs_oracle(ops, oracle, case):
     check(host(dx), oracle.conv2d_bwd_data(d, dy, w), "bf16", "conv dx")
 
 
+# bf16 3x3 weight gradients on the direct-to-LDS band kernel
+# (conv3x3_dma.hip: rows of a multiple of 8 pixels dividing 224, 64-channel
+# dy blocks): ragged last bands, a partial last x-channel block, two dy
+# blocks, 7-, 14- and 28-row bands, several bands per split.  (n, c, h, w, k)
+WDMA3X3 = [
+    (2, 48, 30, 56, 64),
+    (3, 64, 13, 32, 128),
+    (2, 16, 20, 16, 64),
+    (5, 32, 9, 8, 64),
+    (6, 96, 56, 56, 64),
+]
+
+
+@pytest.mark.parametrize("case", WDMA3X3, ids=lambda c: "n{}c{}h{}w{}k{}".format(*c))
+def test_conv3x3_wgrad_dma_vs_oracle(ops, oracle, case):
+    """bf16 weight gradient (and bias gradient) of the band kernel against
+    the oracle, set and accumulated."""
+    n, c, h, w_, k = case
+    cc = (n, c, h, w_, k, 3, 3, 1, 1, 1)
+    d = _desc(ops, cc)
+    x, w, b, dy = _inputs(cc, "bf16", 17 + sum(case))
+    dw, db = ops.conv2d_bwd_weight(dev(x, "bf16"), dev(dy, "bf16"), d, need_db=True)
+    dw0 = f32(rng(5).standard_normal((k, c, 3, 3)))
+    dwa = dev(dw0)
+    ops.conv2d_bwd_weight(dev(x, "bf16"), dev(dy, "bf16"), d, dw=dwa, accumulate=True)
+    torch.cuda.synchronize()
+    rdw, rdb = oracle.conv2d_bwd_weight(d, x, dy)
+    check(host(dw), rdw, "bf16", "conv dw")
+    check(host(db), rdb, "bf16", "conv db")
+    check(host(dwa), dw0 + rdw, "bf16", "conv dw accumulated")
+
+
 # fp32 3x3 grids of a little more than one round of workgroup slots (512 on
 # 256 CUs) with one output-channel block: the last tiles are split over their
 # channel chunks in the same launch (4 pieces each for 64 input channels, 8

@@ -24,7 +24,7 @@ struct nott_ctx_s {
     unsigned long long* err_word = nullptr;  // device counter of data errors
     int num_cu = 256;
     int conv_tap = 1;              // 0: NOTT_CONV_TAP=0 in the environment at nott_create (conv_tap.hip / conv_stem.hip kernels off)
-    int conv_dma = 1;              // 0: NOTT_CONV_DMA=0 at nott_create (bf16 3x3 passes stay off conv3x3_dma.hip)
+    int conv_dma = 3;              // NOTT_CONV_DMA at nott_create: bit 0 bf16 3x3 fwd/dgrad, bit 1 bf16 3x3 wgrad on conv3x3_dma.hip
     std::string last_error;
 };
 

@@ -78,7 +78,7 @@ int nott_create(int device, nott_ctx* out) {
     // column / generic paths run instead), so both implementations can be
     // checked and timed against each other.
     if (const char* e = std::getenv("NOTT_CONV_TAP")) c->conv_tap = (e[0] != '0');
-    if (const char* e = std::getenv("NOTT_CONV_DMA")) c->conv_dma = (e[0] != '0');
+    if (const char* e = std::getenv("NOTT_CONV_DMA")) c->conv_dma = std::atoi(e);
     if (hipMalloc(&c->err_word, sizeof(unsigned long long)) != hipSuccess) {
         delete c;
         return NOTT_ERR_ALLOC;

@@ -478,7 +478,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     if constexpr (sizeof(T) == 2) {
         // bf16 shapes the DMA kernel takes.  Prepared slices of such a shape
         // are in its fragment layout, so that path has no fallback.
-        const bool dma = ctx->conv_dma && dma_applies(n, cin, h, w, cout);
+        const bool dma = (ctx->conv_dma & 1) && dma_applies(n, cin, h, w, cout);
         const bool aligned = ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 7) == 0;
         if (dma && (aligned || prepared)) {
             const bf16_t* wpp = prepared;
@@ -491,7 +491,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
             }
             if (dg_out) {
                 // the data gradient's pass is cout → cin over the same weight
-                if (ctx->conv_dma && dma_applies(n, cout, h, w, cin)) {
+                if ((ctx->conv_dma & 1) && dma_applies(n, cout, h, w, cin)) {
                     const int st = dma_prep<true>(ctx, wsrc, dg_out, cout, cin);
                     if (st != NOTT_OK) return st;
                 } else {
@@ -540,7 +540,7 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
     T* wp = reinterpret_cast<T*>(ws);
     if (prepared) {
         wp = const_cast<T*>(prepared);
-    } else if (dg_out && sizeof(T) == 2 && ctx->conv_dma && dma_applies(n, cout, h, w, cin)) {
+    } else if (dg_out && sizeof(T) == 2 && (ctx->conv_dma & 1) && dma_applies(n, cout, h, w, cin)) {
         hipLaunchKernelGGL((conv3x3_wprep_kernel<T, DGRAD>), dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),
                            (unsigned)(cin / CC), (unsigned)cbc), dim3(256), 0, ctx->stream, wsrc, wp, cout, cin);
         if constexpr (sizeof(T) == 2) {
@@ -1014,6 +1014,23 @@ int wgrad_p(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, fl
 
 template <typename T>
 int wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
+    if constexpr (sizeof(T) == 2) {
+        const int32_t n = (int32_t)d->n, c = (int32_t)d->c, h = (int32_t)d->h, w = (int32_t)d->w, k = (int32_t)d->k;
+        if ((ctx->conv_dma & 2) && wdma_applies(n, c, h, w, k) && ((uintptr_t)x & 15) == 0 && ((uintptr_t)dy & 15) == 0) {
+            float* ws = nullptr;
+            int32_t splits = 0;
+            const int st = wdma_partials(ctx, n, c, h, w, k, x, dy, &ws, &splits);
+            if (st != NOTT_OK) return st;
+            const int64_t per = (int64_t)9 * k * c;
+            if (splits >= 32)
+                hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel<16>, dim3((unsigned)ceil_div(per / 4, 16)), dim3(256),
+                                   0, ctx->stream, ws, splits, k, c, dw, accumulate);
+            else
+                hipLaunchKernelGGL(conv3x3_wgrad_reduce_kernel<4>, dim3((unsigned)ceil_div(per / 4, 64)), dim3(256),
+                                   0, ctx->stream, ws, splits, k, c, dw, accumulate);
+            return launch_status(ctx, "conv3x3_wgrad_reduce");
+        }
+    }
     switch (wgrad_load_width(d->w, sizeof(T))) {
         case 16: return wgrad_p<T, 16>(ctx, d, x, dy, dw, accumulate);
         case 8: return wgrad_p<T, 8>(ctx, d, x, dy, dw, accumulate);

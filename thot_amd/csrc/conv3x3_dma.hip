@@ -21,25 +21,28 @@
 // consecutive pixels they are a choice of register, across lane groups one
 // ds_bpermute rotation per block.
 //
-// Work decomposition.  A tile is 224 pixels of whole image rows (W divides
-// 112) × 32 output channels.  A workgroup is 4 waves: 2 pixel waves (112
+// Work decomposition.  A tile is 448 pixels of whole image rows (W divides
+// 112) × 32 output channels.  A workgroup is 8 waves: 4 pixel waves (112
 // pixels = 7 blocks of 16 each) × 2 channel waves (16 channels each), so a
 // wave holds 3 (taps s) × 7 (blocks) accumulator tiles of
 // v_mfma_f32_16x16x32_bf16 with M = pixels, N = output channels and K = 32
-// input channels per stage.  Workgroups are persistent (two per CU): each
-// walks a contiguous range of tiles, channel block fastest, so the second
-// channel block of a row band re-reads its input from L2, and a tile's halo
-// rows were just loaded by its predecessor.
+// input channels per stage.  One workgroup per CU, persistent: workgroup b
+// serves output block b / gpc and a contiguous range of that block's tiles,
+// so the block's weight fragments (all input chunks, pre-arranged by
+// dma_wprep_kernel in B-operand order) are copied into LDS once and stay
+// resident; the blocks of one row band run at the same time on workgroups
+// of the same XCD, which share the band's input rows through L2.
 //
 // Stages.  One stage = one 32-channel input chunk of one tile: the chunk's
-// rows h0−1 .. h0+rows (a contiguous pixel range of each channel plane,
-// rounded out to 16-byte pieces; pieces off the image load from a zero
-// block) and the chunk's weight fragments for the tile's 32 output channels
-// (pre-arranged by dma_wprep_kernel in B-operand order, 18 KB, copied
-// linearly).  Stages go through a 2-slot LDS ring ordered only by
-// s_waitcnt vmcnt and a fence-free s_barrier: the loads of stage j+1 are
-// issued right after the barrier that opens stage j, so they land while
-// stage j is multiplied and while the previous tile's epilogue stores.
+// rows h0−1 .. h0+rows, a contiguous pixel range of each channel plane
+// rounded out to 16-byte pieces (pieces off the image load from a zero
+// block), in a 2-slot LDS ring ordered only by s_waitcnt vmcnt and a
+// fence-free s_barrier.  The next stage's DMA instructions are issued
+// between the MFMA blocks of the current one, so the vector memory queue
+// drains while the matrix core works.  A tile's output is formed during the
+// next tile's first stage, block by block, just before that block's
+// accumulators restart, so the epilogue's shuffles, adds and stores overlap
+// matrix work in flight rather than draining the matrix core.
 #include "conv_fast.hpp"
 #include "lds_dma.hpp"
 
@@ -109,10 +112,13 @@ __device__ __forceinline__ TileInfo decode_tile(int32_t t, const DmaParams& p) {
 template <bool DGRAD>
 __global__ __launch_bounds__(256) void dma_wprep_kernel(const bf16_t* __restrict__ w, bf16_t* __restrict__ wp,
                                                         int32_t cin, int32_t cout) {
+    // one element per thread (destination order, so stores are contiguous)
     const int32_t nch = cin / kCK;
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)(cout / kCoTile) * nch * 9 * kCoWaves * 64;
-    if (g >= total) return;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = (int64_t)cout * cin * 9;
+    if (i >= total) return;
+    const int e = (int)(i & 7);
+    const int64_t g = i >> 3;
     const int l = (int)(g & 63);
     int64_t q = g >> 6;
     const int cw = (int)(q % kCoWaves);
@@ -122,20 +128,8 @@ __global__ __launch_bounds__(256) void dma_wprep_kernel(const bf16_t* __restrict
     const int c = (int)(q % nch);
     const int cb = (int)(q / nch);
     const int32_t co = cb * kCoTile + cw * 16 + (l & 15);
-    const int32_t ci0 = c * kCK + 8 * (l >> 4);
-    uint32_t pk[4];
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-        uint32_t v[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int32_t ci = ci0 + 2 * e2 + h;
-            const int64_t src = DGRAD ? (((int64_t)ci * cout + co) * 9 + (8 - t)) : (((int64_t)co * cin + ci) * 9 + t);
-            v[h] = w[src];
-        }
-        pk[e2] = v[0] | (v[1] << 16);
-    }
-    *reinterpret_cast<u32x4*>(wp + g * 8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    const int32_t ci = c * kCK + 8 * (l >> 4) + e;
+    wp[i] = w[DGRAD ? (((int64_t)ci * cout + co) * 9 + (8 - t)) : (((int64_t)co * cin + ci) * 9 + t)];
 }
 
 // LDS: [weights of the workgroup's output block, all input chunks][input
@@ -447,6 +441,271 @@ bool dma_plan(int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, int nu
     return true;
 }
 
+// ---------------------------------------------------------------------------
+// Weight gradient, bf16: dw[k, c, r, s] = Σ_{n,h,w} dy[n,k,h,w] · x[n, c, h−1+r, w−1+s]
+// (reference conv.hpp:177, ATen convolution_backward weight grad).
+//
+// GEMM with M = 64 dy channels k, N = 64 x channels c × 9 taps and the
+// reduction over pixels, which lie contiguously in both NCHW operands, so
+// fragments are plain 16-byte reads of 8 consecutive pixels.  A band is 224
+// pixels of whole image rows (W divides 224, W a multiple of 8): dy rows
+// h0 .. h0+th−1 and x rows h0−1 .. h0+th, copied untouched into LDS by
+// global_load_lds_dwordx4 (each x row between a zero 16-byte guard on each
+// side).  The reduction runs over the band's flattened pixels: tap (r, s)
+// reads x at pixel p + r·W + s − 1 of the band's x rows; s = 1 is an aligned
+// read, s = 0 and s = 2 realign it with one dword of each neighbour.  Where
+// p starts (s = 0) or ends (s = 2) an image row, the shifted x element is
+// the row padding and is set to zero, so a dy value meets exactly the zero
+// that the reference's padded input puts there.  No pixel slot is spent on
+// padding.
+//
+// 8 waves: wave w owns x channels 16·(w % 4).. +15 and dy channels
+// 32·(w / 4).. +31 for all 9 taps (18 accumulator tiles of
+// v_mfma_f32_16x16x32_bf16, M = k, N = c, K = 32 pixels).  Bands go through a
+// 2-slot LDS ring; the next band's DMA is issued between the current one's
+// k-steps.  One workgroup per CU: the pixel range is split into `splits`
+// contiguous band ranges per (k, c) tile, and partial sums go to
+// ws[split][k][c][tap] (dw's own layout) for the ordered reduce.
+constexpr int kWdWaves = 8;
+constexpr int kWdThreads = 64 * kWdWaves;
+constexpr int kWdPix = 224;                 // pixels per band: 7 k-steps of 32
+constexpr int kWdSteps = kWdPix / 32;
+constexpr int kWdMaxI = 10;                 // DMA instructions per wave per band (at most)
+
+struct WdParams {
+    int32_t n, c, k, h, w, hw;
+    int32_t th, bpi, bands;       // image rows per band, bands per image, n·bpi
+    int32_t kblocks, cblocks, tiles, splits;
+    int32_t xcd_map;              // grid grouped by XCD (see tile_split)
+    int32_t pa, pbx;              // LDS bytes per dy row and per x row (both 16·odd)
+    int32_t a_bytes, slot_bytes;  // 64·pa, 64·(pa + pbx)
+    int32_t a_instr, instr;       // DMA instructions per band: dy, all
+    int32_t xdata;                // 16-byte x data pieces per row: (th + 2)·w / 8
+};
+
+__device__ __forceinline__ u32x4 wd_shift_s0(uint32_t prev, const u32x4& c) {   // elements p−1 .. p+6
+    return u32x4{__builtin_amdgcn_alignbit(c.x, prev, 16), __builtin_amdgcn_alignbit(c.y, c.x, 16),
+                 __builtin_amdgcn_alignbit(c.z, c.y, 16), __builtin_amdgcn_alignbit(c.w, c.z, 16)};
+}
+__device__ __forceinline__ u32x4 wd_shift_s2(const u32x4& c, uint32_t next) {   // elements p+1 .. p+8
+    return u32x4{__builtin_amdgcn_alignbit(c.y, c.x, 16), __builtin_amdgcn_alignbit(c.z, c.y, 16),
+                 __builtin_amdgcn_alignbit(c.w, c.z, 16), __builtin_amdgcn_alignbit(next, c.w, 16)};
+}
+
+__global__ __launch_bounds__(kWdThreads, 1) void conv3x3_wgrad_dma_kernel(const bf16_t* __restrict__ x,
+                                                                           const bf16_t* __restrict__ dy,
+                                                                           float* __restrict__ ws, WdParams p) {
+    extern __shared__ __attribute__((aligned(1024))) char smem_raw[];
+    char NOTT_LDS* smem = (char NOTT_LDS*)smem_raw;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int cg = wid & 3, kh = wid >> 2;
+    const int G = lane >> 4, jl = lane & 15;
+
+    // Tile and split.  With the XCD map, workgroups b and b + 8 (the same
+    // XCD) take different tiles of the same split, so the x rows that the
+    // k tiles share come from that XCD's L2.
+    int32_t tile, split;
+    {
+        const int32_t b = (int32_t)blockIdx.x;
+        if (p.xcd_map) {
+            const int32_t slot = b >> 3, xcd = b & 7;
+            tile = slot % p.tiles;
+            split = (slot / p.tiles) * 8 + xcd;
+        } else {
+            tile = b % p.tiles;
+            split = b / p.tiles;
+        }
+    }
+    const int32_t kb = tile % p.kblocks, cb = tile / p.kblocks;
+    const int32_t b0 = (int32_t)(((int64_t)split * p.bands) / p.splits);
+    const int32_t b1 = (int32_t)(((int64_t)(split + 1) * p.bands) / p.splits);
+    const void* zero = g_dma_zero;
+
+    // This lane's DMA pieces: instruction ii = wid + 8k moves LDS bytes
+    // [1024·ii, 1024·ii + 1024) of a slot (dy rows first, then x rows).
+    // rel: element offset from (row 0 of the tile's channel block, band
+    // start pixel); gpx: pixel offset from the band start, or invalid.
+    int32_t rel[kWdMaxI], gpx[kWdMaxI];
+#pragma unroll
+    for (int k = 0; k < kWdMaxI; ++k) {
+        const int32_t ii = wid + kWdWaves * k;
+        const int32_t s = ii * 64 + lane;
+        int32_t row, px;
+        bool ok;
+        if (ii < p.a_instr) {
+            const int32_t ppr = p.pa >> 4;
+            row = s / ppr;
+            const int32_t g = s - row * ppr;
+            px = 8 * g;
+            ok = 8 * g < p.th * p.w;
+        } else {
+            const int32_t ppr = p.pbx >> 4, s2 = s - p.a_instr * 64;
+            row = s2 / ppr;
+            const int32_t g = s2 - row * ppr;
+            px = 8 * (g - 1) - p.w;
+            ok = g >= 1 && g <= p.xdata && cb * 64 + row < p.c;
+        }
+        rel[k] = row * p.hw + px;
+        gpx[k] = ok ? px : -(1 << 30);
+    }
+    auto issue = [&](int32_t band, int slot, int k) {
+        const int32_t ii = wid + kWdWaves * k;
+        if (ii >= p.instr) return;
+        const int32_t img = band / p.bpi, q0 = (band - img * p.bpi) * p.th * p.w;
+        const bf16_t* base = ii < p.a_instr ? dy + ((int64_t)img * p.k + kb * 64) * p.hw + q0
+                                            : x + ((int64_t)img * p.c + cb * 64) * p.hw + q0;
+        const int32_t px = q0 + gpx[k];
+        const void* src = (px >= 0 && px < p.hw) ? (const void*)(base + rel[k]) : zero;
+        dma16(src, lds_addr(smem) + (uint32_t)(slot * p.slot_bytes + ii * 1024));
+    };
+
+    // Row-edge masks of this lane's 8-pixel groups, the same for every band
+    // (a band starts at a row start): bit t of rs / re says the group of
+    // k-step t starts / ends an image row.
+    uint32_t rs = 0, re = 0;
+#pragma unroll
+    for (int t = 0; t < kWdSteps; ++t) {
+        const int32_t q = 32 * t + 8 * G;
+        if (q % p.w == 0) rs |= 1u << t;
+        if ((q + 8) % p.w == 0) re |= 1u << t;
+    }
+
+    f32x4 acc[2][9];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 9; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    struct Ops {
+        u32x4 a[2], cur[3];
+        uint32_t prev[3], next[3];
+    };
+    const int32_t nb = b1 - b0;
+    if (nb > 0) {
+#pragma unroll
+        for (int k = 0; k < kWdMaxI; ++k) issue(b0, 0, k);
+    }
+    for (int32_t i = 0; i < nb; ++i) {
+        wait_vm_lgkm0<0>();
+        barrier();
+        const bool more = i + 1 < nb;
+        const char NOTT_LDS* sa = smem + (i & 1) * p.slot_bytes + (kh * 32 + jl) * p.pa + 16 * G;
+        const char NOTT_LDS* sx = smem + (i & 1) * p.slot_bytes + p.a_bytes + (cg * 16 + jl) * p.pbx + 16 + 16 * G;
+        auto load_ops = [&](int t, Ops& o) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) o.a[mt] = *(const u32x4 NOTT_LDS*)(sa + mt * 16 * p.pa + 64 * t);
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                const char NOTT_LDS* q = sx + 64 * t + 2 * r * p.w;
+                o.cur[r] = *(const u32x4 NOTT_LDS*)q;
+                o.prev[r] = *(const uint32_t NOTT_LDS*)(q - 4);
+                o.next[r] = *(const uint32_t NOTT_LDS*)(q + 16);
+            }
+        };
+        Ops ops[2];
+        load_ops(0, ops[0]);
+#pragma unroll
+        for (int t = 0; t < kWdSteps; ++t) {
+            Ops& o = ops[t & 1];
+            if (t + 1 < kWdSteps) load_ops(t + 1, ops[(t + 1) & 1]);
+            // the next band's DMA: instructions t and t + 7
+            if (more) {
+                issue(b0 + i + 1, (i + 1) & 1, t);
+                if (t + kWdSteps < kWdMaxI) issue(b0 + i + 1, (i + 1) & 1, t + kWdSteps);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint32_t m0 = (rs >> t) & 1 ? 0xffff0000u : 0xffffffffu;
+            const uint32_t m7 = (re >> t) & 1 ? 0x0000ffffu : 0xffffffffu;
+#pragma unroll
+            for (int r = 0; r < 3; ++r) {
+                u32x4 bs0 = wd_shift_s0(o.prev[r], o.cur[r]);
+                u32x4 bs2 = wd_shift_s2(o.cur[r], o.next[r]);
+                bs0.x &= m0;
+                bs2.w &= m7;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const bf16x8 av = __builtin_bit_cast(bf16x8, o.a[mt]);
+                    acc[mt][3 * r + 0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bs0),
+                                                                                 acc[mt][3 * r + 0], 0, 0, 0);
+                    acc[mt][3 * r + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        av, __builtin_bit_cast(bf16x8, o.cur[r]), acc[mt][3 * r + 1], 0, 0, 0);
+                    acc[mt][3 * r + 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8, bs2),
+                                                                                 acc[mt][3 * r + 2], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Partials in dw's layout, ws[split][k][c][tap].  For each (mt, e) a wave
+    // holds 4 k rows (one per 16-lane group) × its 16 channels × 9 taps, i.e.
+    // 4 runs of 144 consecutive floats; they pass through the wave's own LDS
+    // slice so the global stores are whole 16-byte pieces.
+    const int32_t c0 = cb * 64 + cg * 16;
+    float* wsp = ws + (int64_t)split * 9 * p.k * p.c;
+    float NOTT_LDS* slice = (float NOTT_LDS*)smem + wid * (4 * 16 * 9);
+    wait_vm_lgkm0<0>();
+    barrier();                                    // every wave is done with the band operands
+    const int32_t cw = min(16, p.c - c0);         // channels of this wave inside c
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) slice[(G * 16 + jl) * 9 + tap] = acc[mt][tap][e];
+            // the slice is this wave's own: wave-scope ordering suffices
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            for (int q = lane; q < 4 * 36; q += 64) {
+                const int g = q / 36, j = q - g * 36;
+                const int32_t kk = kb * 64 + kh * 32 + mt * 16 + g * 4 + e;
+                if (4 * j < cw * 9)
+                    *reinterpret_cast<f32x4*>(wsp + ((int64_t)kk * p.c + c0) * 9 + 4 * j) =
+                        *(const f32x4 NOTT_LDS*)(slice + g * 144 + 4 * j);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+}
+
+bool wd_plan(int32_t n, int32_t c, int32_t h, int32_t w, int32_t k, int num_cu, WdParams& p, size_t& lds) {
+    if (w <= 0 || w % 8 != 0 || kWdPix % w != 0 || k % 64 != 0 || c % 16 != 0 || n <= 0 || h <= 0) return false;
+    if ((int64_t)n * std::max(c, k) * h * w >= (int64_t(1) << 31)) return false;
+    p.n = n; p.c = c; p.k = k; p.h = h; p.w = w; p.hw = h * w;
+    p.th = kWdPix / w;
+    p.bpi = (int32_t)ceil_div(h, p.th);
+    p.bands = n * p.bpi;
+    p.kblocks = k / 64;
+    p.cblocks = (int32_t)ceil_div(c, 64);
+    p.tiles = p.kblocks * p.cblocks;
+    // pitches that are 16·odd bytes: 16 lanes reading 16 rows at one column
+    // touch 16 distinct 16-byte slots
+    auto odd16 = [](int32_t b) {
+        b = (b + 15) & ~15;
+        return ((b >> 4) & 1) ? b : b + 16;
+    };
+    p.pa = odd16(p.th * w * 2);
+    p.pbx = odd16((p.th + 2) * w * 2 + 32);
+    p.xdata = (p.th + 2) * w / 8;
+    p.a_bytes = 64 * p.pa;
+    p.slot_bytes = 64 * (p.pa + p.pbx);
+    p.a_instr = p.pa / 16;
+    p.instr = (p.pa + p.pbx) / 16;
+    if (p.instr > kWdWaves * kWdMaxI) return false;
+    lds = std::max<size_t>(2 * (size_t)p.slot_bytes, (size_t)kWdWaves * 4 * 16 * 9 * sizeof(float));
+    if (lds > (size_t)kMaxLds) return false;
+    // one workgroup per CU
+    if (num_cu >= 8 * p.tiles) {
+        p.xcd_map = 1;
+        p.splits = 8 * (num_cu / (8 * p.tiles));
+    } else {
+        p.xcd_map = 0;
+        p.splits = std::max(1, num_cu / p.tiles);
+    }
+    p.splits = std::min(p.splits, p.bands);
+    if (p.xcd_map && p.splits % 8 != 0) p.xcd_map = 0;
+    return true;
+}
+
 }  // namespace
 
 bool dma_applies(int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout) {
@@ -458,8 +717,8 @@ int64_t dma_prep_elems(int32_t cin, int32_t cout) { return (int64_t)cout * cin *
 
 template <bool DGRAD>
 int dma_prep(nott_ctx ctx, const bf16_t* w, bf16_t* wp, int32_t cin, int32_t cout) {
-    const int64_t groups = (int64_t)(cout / kCoTile) * (cin / kCK) * 9 * kCoWaves * 64;
-    hipLaunchKernelGGL(dma_wprep_kernel<DGRAD>, dim3((unsigned)ceil_div(groups, 256)), dim3(256), 0, ctx->stream, w,
+    const int64_t elems = (int64_t)cout * cin * 9;
+    hipLaunchKernelGGL(dma_wprep_kernel<DGRAD>, dim3((unsigned)ceil_div(elems, 256)), dim3(256), 0, ctx->stream, w,
                        wp, cin, cout);
     return launch_status(ctx, "conv3x3_dma_wprep");
 }
@@ -486,6 +745,35 @@ int dma_run(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t 
         hipLaunchKernelGGL(conv3x3_dma_kernel<false>, dim3((unsigned)pl.grid), dim3(kDThreads), pl.lds, ctx->stream,
                            in, wp, bias, out, pl.p);
     return launch_status(ctx, "conv3x3_dma");
+}
+
+bool wdma_applies(int32_t n, int32_t c, int32_t h, int32_t w, int32_t k) {
+    WdParams p;
+    size_t lds;
+    return wd_plan(n, c, h, w, k, 256, p, lds);
+}
+
+int wdma_partials(nott_ctx ctx, int32_t n, int32_t c, int32_t h, int32_t w, int32_t k, const bf16_t* x,
+                  const bf16_t* dy, float** ws_out, int32_t* splits_out) {
+    WdParams p;
+    size_t lds;
+    if (!wd_plan(n, c, h, w, k, ctx->num_cu, p, lds))
+        return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad (dma): shape not supported");
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)dy & 15) != 0)
+        return fail(ctx, NOTT_ERR_UNSUPPORTED, "conv3x3 wgrad (dma): operands must be 16-byte aligned");
+    float* ws = static_cast<float*>(workspace(ctx, sizeof(float) * (size_t)p.splits * 9 * k * c));
+    if (!ws) return NOTT_ERR_ALLOC;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3x3_wgrad_dma_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(conv3x3_wgrad_dma_kernel, dim3((unsigned)(p.tiles * p.splits)), dim3(kWdThreads), lds,
+                       ctx->stream, x, dy, ws, p);
+    *ws_out = ws;
+    *splits_out = p.splits;
+    return launch_status(ctx, "conv3x3_wgrad_dma");
 }
 
 template int dma_prep<false>(nott_ctx, const bf16_t*, bf16_t*, int32_t, int32_t);

@@ -55,6 +55,13 @@ int dma_prep(nott_ctx ctx, const bf16_t* w, bf16_t* wp, int32_t cin, int32_t cou
 int dma_run(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const bf16_t* in,
             const bf16_t* wp, const float* bias, bf16_t* out, int relu);
 
+// bf16 3x3 / stride-1 weight gradient with DMA-filled LDS bands
+// (conv3x3_dma.hip): writes split partials ws[split][k][c][tap] into the
+// context workspace for the ordered reduce; returns the split count.
+bool wdma_applies(int32_t n, int32_t c, int32_t h, int32_t w, int32_t k);
+int wdma_partials(nott_ctx ctx, int32_t n, int32_t c, int32_t h, int32_t w, int32_t k, const bf16_t* x,
+                  const bf16_t* dy, float** ws_out, int32_t* splits_out);
+
 // Widest load (bytes) that keeps every image row's pieces aligned.
 int wgrad_load_width(int64_t w, size_t elem);
 
