@@ -11,6 +11,9 @@
 // per-channel finalize and one streaming apply pass.
 #include "common.hpp"
 
+#include <initializer_list>
+#include <type_traits>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -37,52 +40,113 @@ __device__ __forceinline__ void block_sum2(float& a, float& b, float* red) {
     b = tb;
 }
 
+// A group of V consecutive elements (V = 1, 4, or 8 for bf16) as floats:
+// one 4-, 8-, 16- or 16-byte access.
+template <typename T, int V>
+__device__ __forceinline__ void ld_grp(const T* __restrict__ p, float (&o)[V]) {
+    if constexpr (V == 1) {
+        o[0] = Io<T>::ld(p, 0);
+    } else if constexpr (V == 4) {
+        const f32x4 v = Vec4<T>::ld(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else {
+        static_assert(V == 8 && sizeof(T) == 2, "8-element groups are 16 bytes of bf16");
+        const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o[2 * k] = __builtin_bit_cast(float, w[k] << 16);
+            o[2 * k + 1] = __builtin_bit_cast(float, w[k] & 0xffff0000u);
+        }
+    }
+}
+template <typename T, int V>
+__device__ __forceinline__ void st_grp(T* __restrict__ p, const float (&o)[V]) {
+    if constexpr (V == 1) {
+        Io<T>::st(p, 0, o[0]);
+    } else if constexpr (V == 4) {
+        Vec4<T>::st(p, f32x4{o[0], o[1], o[2], o[3]});
+    } else {
+        static_assert(V == 8 && sizeof(T) == 2, "8-element groups are 16 bytes of bf16");
+        *reinterpret_cast<u32x4*>(p) = u32x4{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
+                                            pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
+    }
+}
+// Σ of a group in a fixed pairwise order.
+template <int V>
+__device__ __forceinline__ float grp_sum(const float (&o)[V]) {
+    if constexpr (V == 1) return o[0];
+    else if constexpr (V == 4) return (o[0] + o[1]) + (o[2] + o[3]);
+    else return ((o[0] + o[1]) + (o[2] + o[3])) + ((o[4] + o[5]) + (o[6] + o[7]));
+}
+
+// Items of the per-channel partial reductions: item k of a split is group
+// k % hwg of image n0 + k / hwg.  A thread takes items t, t + kThreads, ...,
+// kUnroll of them loaded before they are added (in item order), so the
+// summation order is fixed and several loads are in flight per thread.
+constexpr int kUnroll = 4;
+
 // Partial sums of (x − pivot) and (x − pivot)² over planes [n0, n1) of
 // channel blockIdx.x.  pivot = x[0, c, 0] keeps the variance well conditioned.
-// Thread t owns groups j ≡ t (mod kThreads) of each plane (a group is 4
-// pixels with VEC, else 1) and adds them image by image.  Planes of fewer
-// than kThreads groups give a thread one group per image: its loads for up
+// Splits of at least kThreads groups (V pixels each) are walked as items
+// (above); smaller ones give a thread one group per image: its loads for up
 // to kAhead images are issued before the adds, which run in the same order.
 constexpr int kAhead = 8;
-template <typename T, bool VEC>
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict__ x, int64_t n, int64_t c, int64_t hw,
-                                                            int64_t per_split, float* __restrict__ partial) {
+                                                            int64_t per_split, FastDiv fd_hwg,
+                                                            float* __restrict__ partial) {
     __shared__ float red[2 * kWaves];
     const int64_t ch = blockIdx.x;
     const int64_t n0 = (int64_t)blockIdx.y * per_split;
     const int64_t n1 = std::min<int64_t>(n, n0 + per_split);
     const float pivot = Io<T>::ld(x, ch * hw);
-    constexpr int V = VEC ? 4 : 1;
     const int64_t hwg = hw / V;
     float s1 = 0.f, s2 = 0.f;
-    auto ld = [&](int64_t e) { return VEC ? Vec4<T>::ld(x + e) : f32x4{Io<T>::ld(x, e), 0.f, 0.f, 0.f}; };
-    auto add = [&](const f32x4& v) {
-        if (VEC) {
-            const float a = v.x - pivot, b = v.y - pivot, cc = v.z - pivot, d = v.w - pivot;
-            s1 += (a + b) + (cc + d);
-            s2 += (a * a + b * b) + (cc * cc + d * d);
-        } else {
-            const float a = v.x - pivot;
-            s1 += a;
-            s2 += a * a;
-        }
+    auto add = [&](float (&v)[V]) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] -= pivot;
+        float sq[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) sq[e] = v[e] * v[e];
+        s1 += grp_sum<V>(v);
+        s2 += grp_sum<V>(sq);
     };
-    if (hwg >= kThreads) {
-        for (int64_t i = n0; i < n1; ++i) {
-            const int64_t base = (i * c + ch) * hw;
-            for (int64_t j = threadIdx.x; j < hwg; j += kThreads) add(ld(base + j * V));
+    if ((n1 - n0) * hwg >= kThreads) {
+        const uint32_t items = (uint32_t)((n1 - n0) * hwg);
+        auto at = [&](uint32_t k) {
+            uint32_t i, j;
+            fd_hwg.divmod(k, i, j);
+            return x + ((n0 + i) * c + ch) * hw + (int64_t)j * V;
+        };
+        uint32_t k = threadIdx.x;
+        for (; k + (kUnroll - 1) * kThreads < items; k += kUnroll * kThreads) {
+            float v[kUnroll][V];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) ld_grp<T, V>(at(k + u * kThreads), v[u]);
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) add(v[u]);
+        }
+        for (; k < items; k += kThreads) {
+            float v[V];
+            ld_grp<T, V>(at(k), v);
+            add(v);
         }
     } else if ((int64_t)threadIdx.x < hwg) {
         const int64_t step = c * hw;
         int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
         for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
-            f32x4 v[kAhead];
+            float v[kAhead][V];
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u) v[u] = ld(e + u * step);
+            for (int u = 0; u < kAhead; ++u) ld_grp<T, V>(x + e + u * step, v[u]);
 #pragma unroll
             for (int u = 0; u < kAhead; ++u) add(v[u]);
         }
-        for (; i < n1; ++i, e += step) add(ld(e));
+        for (; i < n1; ++i, e += step) {
+            float v[V];
+            ld_grp<T, V>(x + e, v);
+            add(v);
+        }
     }
     block_sum2<kWaves>(s1, s2, red);
     if (threadIdx.x == 0) {
@@ -162,9 +226,9 @@ __global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, c
 }
 
 // y = act(a_c·x + c_c [+ res]) over the whole tensor (act = ReLU or identity).
-// One thread per group (4 elements with VEC, else 1) of a flat grid: a group
-// lies in one (n, c) plane, found with two multiply-high divisions.
-template <typename T, bool VEC>
+// One thread per group of V elements of a flat grid: a group lies in one
+// (n, c) plane, found with two multiply-high divisions.
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict__ x, T* __restrict__ y, uint32_t ngroups,
                                                              FastDiv fd_hwg, FastDiv fd_c, const float* __restrict__ coef,
                                                              const T* __restrict__ res, int relu) {
@@ -173,27 +237,30 @@ __global__ __launch_bounds__(kThreads) void bn_affine_kernel(const T* __restrict
     uint32_t plane, j, img, ch;
     fd_hwg.divmod(q, plane, j);
     fd_c.divmod(plane, img, ch);
-    const int64_t i = (int64_t)q * (VEC ? 4 : 1);
+    const int64_t i = (int64_t)q * V;
     const float a = coef[2 * ch], b = coef[2 * ch + 1];
-    if (VEC) {
-        f32x4 v = Vec4<T>::ld(x + i);
-        v.x = bn_z(v.x, a, b); v.y = bn_z(v.y, a, b); v.z = bn_z(v.z, a, b); v.w = bn_z(v.w, a, b);
-        if (res) v += Vec4<T>::ld(res + i);
-        if (relu) { v.x = relu_f(v.x); v.y = relu_f(v.y); v.z = relu_f(v.z); v.w = relu_f(v.w); }
-        Vec4<T>::st(y + i, v);
-    } else {
-        float v = bn_z(Io<T>::ld(x, i), a, b);
-        if (res) v += Io<T>::ld(res, i);
-        if (relu) v = relu_f(v);
-        Io<T>::st(y, i, v);
+    float v[V];
+    ld_grp<T, V>(x + i, v);
+#pragma unroll
+    for (int e = 0; e < V; ++e) v[e] = bn_z(v[e], a, b);
+    if (res) {
+        float r[V];
+        ld_grp<T, V>(res + i, r);
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] += r[e];
     }
+    if (relu) {
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = relu_f(v[e]);
+    }
+    st_grp<T, V>(y + i, v);
 }
 
 // Backward partial sums of dy and dy·(x − μ), in the order of bn_stats_kernel.
-template <typename T, bool VEC>
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                  const float* __restrict__ mean, int64_t n, int64_t c,
-                                                                 int64_t hw, int64_t per_split,
+                                                                 int64_t hw, int64_t per_split, FastDiv fd_hwg,
                                                                  float* __restrict__ partial, BnAct act) {
     __shared__ float red[2 * kWaves];
     const int64_t ch = blockIdx.x;
@@ -203,45 +270,64 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
     float za = 0.f, zc = 0.f;   // z = za·x + zc when the gradient comes through a ReLU
     if (act.relu) bn_coef(act.gamma ? act.gamma[ch] : 1.f, act.beta ? act.beta[ch] : 0.f, mu, act.rstd[ch], za, zc);
     float s1 = 0.f, s2 = 0.f;
-    constexpr int V = VEC ? 4 : 1;
     const int64_t hwg = hw / V;
-    auto ld = [&](const T* p, int64_t e) { return VEC ? Vec4<T>::ld(p + e) : f32x4{Io<T>::ld(p, e), 0.f, 0.f, 0.f}; };
-    auto add = [&](f32x4 g, const f32x4& v) {
-        if (VEC) {
-            if (act.relu) {
-                if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
-                if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
-                if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
-                if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
-            }
-            s1 += (g.x + g.y) + (g.z + g.w);
-            s2 += (g.x * (v.x - mu) + g.y * (v.y - mu)) + (g.z * (v.z - mu) + g.w * (v.w - mu));
-        } else {
-            float gg = g.x;
-            if (act.relu && bn_z(v.x, za, zc) <= 0.f) gg = 0.f;
-            s1 += gg;
-            s2 += gg * (v.x - mu);
+    auto add = [&](float (&g)[V], const float (&v)[V]) {
+        if (act.relu) {
+#pragma unroll
+            for (int e = 0; e < V; ++e)
+                if (bn_z(v[e], za, zc) <= 0.f) g[e] = 0.f;
         }
+        float gx[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) gx[e] = g[e] * (v[e] - mu);
+        s1 += grp_sum<V>(g);
+        s2 += grp_sum<V>(gx);
     };
-    if (hwg >= kThreads) {
-        for (int64_t i = n0; i < n1; ++i) {
-            const int64_t base = (i * c + ch) * hw;
-            for (int64_t j = threadIdx.x; j < hwg; j += kThreads) add(ld(dy, base + j * V), ld(x, base + j * V));
+    if ((n1 - n0) * hwg >= kThreads) {
+        const uint32_t items = (uint32_t)((n1 - n0) * hwg);
+        auto off = [&](uint32_t k) {
+            uint32_t i, j;
+            fd_hwg.divmod(k, i, j);
+            return ((n0 + i) * c + ch) * hw + (int64_t)j * V;
+        };
+        uint32_t k = threadIdx.x;
+        for (; k + (kUnroll - 1) * kThreads < items; k += kUnroll * kThreads) {
+            float g[kUnroll][V], v[kUnroll][V];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t e = off(k + u * kThreads);
+                ld_grp<T, V>(dy + e, g[u]);
+                ld_grp<T, V>(x + e, v[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) add(g[u], v[u]);
+        }
+        for (; k < items; k += kThreads) {
+            float g[V], v[V];
+            const int64_t e = off(k);
+            ld_grp<T, V>(dy + e, g);
+            ld_grp<T, V>(x + e, v);
+            add(g, v);
         }
     } else if ((int64_t)threadIdx.x < hwg) {
         const int64_t step = c * hw;
         int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
         for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
-            f32x4 g[kAhead], v[kAhead];
+            float g[kAhead][V], v[kAhead][V];
 #pragma unroll
             for (int u = 0; u < kAhead; ++u) {
-                g[u] = ld(dy, e + u * step);
-                v[u] = ld(x, e + u * step);
+                ld_grp<T, V>(dy + e + u * step, g[u]);
+                ld_grp<T, V>(x + e + u * step, v[u]);
             }
 #pragma unroll
             for (int u = 0; u < kAhead; ++u) add(g[u], v[u]);
         }
-        for (; i < n1; ++i, e += step) add(ld(dy, e), ld(x, e));
+        for (; i < n1; ++i, e += step) {
+            float g[V], v[V];
+            ld_grp<T, V>(dy + e, g);
+            ld_grp<T, V>(x + e, v);
+            add(g, v);
+        }
     }
     block_sum2<kWaves>(s1, s2, red);
     if (threadIdx.x == 0) {
@@ -273,7 +359,7 @@ __global__ __launch_bounds__(64) void bn_bwd_finalize(const float* __restrict__ 
     coef[3 * ch + 2] = (float)C;
 }
 
-template <typename T, bool VEC>
+template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                 T* __restrict__ dx, uint32_t ngroups, FastDiv fd_hwg,
                                                                 FastDiv fd_c, const float* __restrict__ coef,
@@ -283,29 +369,38 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_apply_kernel(const T* __restr
     uint32_t plane, j, img, ch;
     fd_hwg.divmod(q, plane, j);
     fd_c.divmod(plane, img, ch);
-    const int64_t i = (int64_t)q * (VEC ? 4 : 1);
+    const int64_t i = (int64_t)q * V;
     const float A = coef[3 * ch], B = coef[3 * ch + 1], C = coef[3 * ch + 2];
     float za = 0.f, zc = 0.f;
     if (act.relu)
         bn_coef(act.gamma ? act.gamma[ch] : 1.f, act.beta ? act.beta[ch] : 0.f, mean[ch], act.rstd[ch], za, zc);
-    if (VEC) {
-        f32x4 g = Vec4<T>::ld(dy + i), v = Vec4<T>::ld(x + i);
-        if (act.relu) {
-            if (bn_z(v.x, za, zc) <= 0.f) g.x = 0.f;
-            if (bn_z(v.y, za, zc) <= 0.f) g.y = 0.f;
-            if (bn_z(v.z, za, zc) <= 0.f) g.z = 0.f;
-            if (bn_z(v.w, za, zc) <= 0.f) g.w = 0.f;
-        }
-        f32x4 r;
-        r.x = A * g.x + B * v.x + C; r.y = A * g.y + B * v.y + C;
-        r.z = A * g.z + B * v.z + C; r.w = A * g.w + B * v.w + C;
-        Vec4<T>::st(dx + i, r);
-    } else {
-        const float xv = Io<T>::ld(x, i);
-        float g = Io<T>::ld(dy, i);
-        if (act.relu && bn_z(xv, za, zc) <= 0.f) g = 0.f;
-        Io<T>::st(dx, i, A * g + B * xv + C);
+    float g[V], v[V];
+    ld_grp<T, V>(dy + i, g);
+    ld_grp<T, V>(x + i, v);
+    if (act.relu) {
+#pragma unroll
+        for (int e = 0; e < V; ++e)
+            if (bn_z(v[e], za, zc) <= 0.f) g[e] = 0.f;
     }
+    float r[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) r[e] = A * g[e] + B * v[e] + C;
+    st_grp<T, V>(dx + i, r);
+}
+
+// Elements per group of the streaming passes: 16-byte groups (8 bf16 / 4
+// fp32) when the planes are whole groups and every tensor is 16-byte
+// aligned, 4 elements at 8-byte alignment, else single elements.
+template <typename T>
+int group_width(int64_t hw, std::initializer_list<const void*> ptrs) {
+    auto aligned = [&](size_t a) {
+        for (const void* q : ptrs)
+            if (((uintptr_t)q % a) != 0) return false;
+        return true;
+    };
+    if (sizeof(T) == 2 && hw % 8 == 0 && aligned(16)) return 8;
+    if (hw % 4 == 0 && aligned(4 * sizeof(T))) return 4;
+    return 1;
 }
 
 int64_t pick_splits(int64_t n, int64_t c) {
@@ -326,24 +421,25 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
     if (!ws) return NOTT_ERR_ALLOC;
     float* partial = ws;
     float* coef = ws + 2 * c * splits;
-    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 && ((uintptr_t)yv % (4 * sizeof(T))) == 0 &&
-                     ((uintptr_t)resv % (4 * sizeof(T))) == 0;
+    const int v = group_width<T>(hw, {xv, yv, resv});
     const dim3 g1((unsigned)c, (unsigned)splits);
-    const FastDiv fd_hwg((uint32_t)(vec ? hw / 4 : hw)), fd_c((uint32_t)c);
-    if (vec)
-        hipLaunchKernelGGL((bn_stats_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
-    else
-        hipLaunchKernelGGL((bn_stats_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, partial);
-    hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial,
-                       c, splits, hw, n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
-    const uint32_t ngroups = (uint32_t)(n * c * (vec ? hw / 4 : hw));
+    const FastDiv fd_hwg((uint32_t)(hw / v)), fd_c((uint32_t)c);
+    const uint32_t ngroups = (uint32_t)(n * c * (hw / v));
     const dim3 ga((unsigned)nott::ceil_div(ngroups, kThreads));
-    if (vec)
-        hipLaunchKernelGGL((bn_affine_kernel<T, true>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
+    auto go = [&](auto vt) {
+        constexpr int V = decltype(vt)::value;
+        hipLaunchKernelGGL((bn_stats_kernel<T, V>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, fd_hwg,
+                           partial);
+        hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial, c, splits, hw,
+                           n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
+        hipLaunchKernelGGL((bn_affine_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
                            coef, res, relu);
-    else
-        hipLaunchKernelGGL((bn_affine_kernel<T, false>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
-                           coef, res, relu);
+    };
+    if constexpr (sizeof(T) == 2) {
+        if (v == 8) go(std::integral_constant<int, 8>{});
+    }
+    if (v == 4) go(std::integral_constant<int, 4>{});
+    else if (v == 1) go(std::integral_constant<int, 1>{});
     return nott::launch_status(ctx, "batchnorm_fwd");
 }
 
@@ -360,28 +456,26 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
     if (!ws) return NOTT_ERR_ALLOC;
     float* partial = ws;
     float* coef = ws + 2 * c * splits;
-    const bool vec = hw % 4 == 0 && ((uintptr_t)xv % (4 * sizeof(T))) == 0 &&
-                     ((uintptr_t)dyv % (4 * sizeof(T))) == 0 && ((uintptr_t)dxv % (4 * sizeof(T))) == 0;
+    const int v = group_width<T>(hw, {xv, dyv, dxv});
     const dim3 g1((unsigned)c, (unsigned)splits);
-    const FastDiv fd_hwg((uint32_t)(vec ? hw / 4 : hw)), fd_c((uint32_t)c);
-    if (vec)
-        hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, true>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
-                           per, partial, act);
-    else
-        hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, false>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
-                           per, partial, act);
-    hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c,
-                       splits, n * hw, mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
-    if (dx) {
-        const uint32_t ngroups = (uint32_t)(n * c * (vec ? hw / 4 : hw));
-        const dim3 ga((unsigned)nott::ceil_div(ngroups, kThreads));
-        if (vec)
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, true>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
+    const FastDiv fd_hwg((uint32_t)(hw / v)), fd_c((uint32_t)c);
+    const uint32_t ngroups = (uint32_t)(n * c * (hw / v));
+    const dim3 ga((unsigned)nott::ceil_div(ngroups, kThreads));
+    auto go = [&](auto vt) {
+        constexpr int V = decltype(vt)::value;
+        hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, V>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
+                           per, fd_hwg, partial, act);
+        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c, splits, n * hw,
+                           mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
+        if (dx)
+            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
                                fd_hwg, fd_c, coef, mean, act);
-        else
-            hipLaunchKernelGGL((bn_bwd_apply_kernel<T, false>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
-                               fd_hwg, fd_c, coef, mean, act);
+    };
+    if constexpr (sizeof(T) == 2) {
+        if (v == 8) go(std::integral_constant<int, 8>{});
     }
+    if (v == 4) go(std::integral_constant<int, 4>{});
+    else if (v == 1) go(std::integral_constant<int, 1>{});
     return nott::launch_status(ctx, "batchnorm_bwd");
 }
 
