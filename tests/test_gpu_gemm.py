@@ -425,6 +425,48 @@ def test_conv3x3_wgrad_dma_vs_oracle(ops, oracle, case):
     check(host(dwa), dw0 + rdw, "bf16", "conv dw accumulated")
 
 
+# bf16 3x3 weight gradients of images at most 15 wide that the band kernel
+# does not take: the images are stacked vertically with a zero row after
+# each, in bands of 256 slots (slot pitch 8 / 16: 32 / 16 rows), so bands
+# start and end inside images and hold several of them.  Odd widths read
+# their 2-byte-aligned rows with realigning 16-byte loads (8-element chunks
+# with a fifth dword at w = 9, 11, 15), element by element in the band that
+# holds the tensor's last row.  The 20- and 28-wide cases keep one image per
+# band.
+STACK3X3 = [
+    (3, 32, 7, 7, 64),
+    (16, 256, 7, 7, 128),
+    (4, 64, 14, 14, 64),
+    (7, 48, 5, 6, 64),
+    (5, 64, 11, 12, 64),
+    (1, 128, 3, 3, 64),
+    (4, 32, 9, 9, 64),
+    (5, 16, 13, 11, 64),
+    (2, 64, 15, 15, 64),
+    (2, 16, 28, 28, 128),
+    (3, 24, 20, 20, 64),
+]
+
+
+@pytest.mark.parametrize("case", STACK3X3, ids=lambda c: "n{}c{}h{}w{}k{}".format(*c))
+def test_conv3x3_wgrad_stacked_vs_oracle(ops, oracle, case):
+    """bf16 weight gradient (and bias gradient) over stacked-image bands
+    against the oracle, set and accumulated."""
+    n, c, h, w_, k = case
+    cc = (n, c, h, w_, k, 3, 3, 1, 1, 1)
+    d = _desc(ops, cc)
+    x, w, b, dy = _inputs(cc, "bf16", 29 + sum(case))
+    dw, db = ops.conv2d_bwd_weight(dev(x, "bf16"), dev(dy, "bf16"), d, need_db=True)
+    dw0 = f32(rng(7).standard_normal((k, c, 3, 3)))
+    dwa = dev(dw0)
+    ops.conv2d_bwd_weight(dev(x, "bf16"), dev(dy, "bf16"), d, dw=dwa, accumulate=True)
+    torch.cuda.synchronize()
+    rdw, rdb = oracle.conv2d_bwd_weight(d, x, dy)
+    check(host(dw), rdw, "bf16", "conv dw")
+    check(host(db), rdb, "bf16", "conv db")
+    check(host(dwa), dw0 + rdw, "bf16", "conv dw accumulated")
+
+
 # fp32 3x3 grids of a little more than one round of workgroup slots (512 on
 # 256 CUs) with one output-channel block: the last tiles are split over their
 # channel chunks in the same launch (4 pieces each for 64 input channels, 8

@@ -646,11 +646,26 @@ constexpr int kWgThreads = 512;
 template <typename T> struct WgCfg;
 template <> struct WgCfg<bf16_t> { static constexpr int TH = 4, E = 8, KSTEP = 32; };
 template <> struct WgCfg<float> { static constexpr int TH = 2, E = 4, KSTEP = 16; };
+// Image rows per band.  bf16 slot rows of at most 16 elements (images up to
+// 15 wide) take bands of 256 slots (8 k-steps) over the images stacked
+// vertically with one zero row after each: a band's fill and barriers are
+// then paid for by 8 k-steps instead of 1–2, and rows past an image's end
+// are that zero row.  Other shapes keep one image per band (at 28×28,
+// 8-row stacked bands measured slower than 4-row bands).
+template <typename T, int P>
+constexpr int wg_rows() {
+    return (sizeof(T) == 2 && P <= 16) ? 256 / P : WgCfg<T>::TH;
+}
+template <typename T, int P>
+constexpr bool wg_stacked() {
+    return wg_rows<T, P>() != WgCfg<T>::TH;
+}
 
 struct WgradParams {
     int32_t n, c, k, h, w;
     int32_t bands_per_img, total_bands, bands_per_split;
     int32_t kblocks;
+    FastDiv fd_h1;             // h + 1: stacked rows per image (stacked bands)
 };
 
 // Chunk j (16 bytes) of channel ch in a region of nch chunks per channel.
@@ -682,7 +697,8 @@ __device__ __forceinline__ u32x4 shift_hi<float>(const u32x4& p, const u32x4& c)
 template <typename T, int P, int LW>
 __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* __restrict__ x, const T* __restrict__ dy,
                                                                    float* __restrict__ ws, WgradParams p) {
-    constexpr int TH = WgCfg<T>::TH, E = WgCfg<T>::E, KSTEP = WgCfg<T>::KSTEP;
+    constexpr int TH = wg_rows<T, P>(), E = WgCfg<T>::E, KSTEP = WgCfg<T>::KSTEP;
+    constexpr bool STACK = wg_stacked<T, P>();
     constexpr int CPR = P / E;                          // 16-byte chunks per slot row
     constexpr int A_TOTAL = 64 * TH * CPR, B_TOTAL = 64 * (TH + 2) * CPR;   // 16-byte chunks per band
     constexpr int A_TASKS = (A_TOTAL + kWgThreads - 1) / kWgThreads;             // per thread
@@ -728,20 +744,51 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
         ch = (rest / nq) * 4 + ((t >> 2) & 3);
     };
     u32x4 ra[A_TASKS], rb[(B_TOTAL4 + kWgThreads - 1) / kWgThreads];
-    auto fetch = [&](int32_t band) {
-        const int32_t img = band / p.bands_per_img;
-        const int32_t h0 = (band - img * p.bands_per_img) * TH;
-        const T* dyb = dy + ((int64_t)img * p.k + kb * 64) * plane;
-        const T* xb = x + ((int64_t)img * p.c + cb * 64) * plane;
+    // Rows of odd bf16 width (2-byte aligned) are read with the realigning
+    // 16-byte loads, except in a band that reads the last image's last row
+    // (whose loads would reach past the tensor): element loads there.  (At
+    // 4-byte alignment the realigning loads measured slower than 4-byte
+    // pieces.)
+    auto fetch_rows = [&](int32_t band, auto fast_tag) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        auto load_row_chunk = [&](const T* row, int ch) __attribute__((always_inline)) -> u32x4 {
+            if constexpr (FAST) return load_chunk_narrow(row, ch, p.w);
+            else return load_chunk<T, LW>(row, ch, p.w);
+        };
+        // Band rows: image rows h0 .. h0 + TH − 1 of image img0, or stacked
+        // rows h0 .. (row R = image R / (h + 1), row R % (h + 1); row h of
+        // every image and rows past the last image are zero).
+        int32_t img0 = 0, h0;
+        if constexpr (STACK) {
+            h0 = band * TH;
+        } else {
+            img0 = band / p.bands_per_img;
+            h0 = (band - img0 * p.bands_per_img) * TH;
+        }
+        auto locate = [&](int32_t R, int32_t& img, int32_t& h) __attribute__((always_inline)) -> bool {
+            if constexpr (STACK) {
+                if (R < 0) return false;
+                uint32_t q, r;
+                p.fd_h1.divmod((uint32_t)R, q, r);
+                img = (int32_t)q;
+                h = (int32_t)r;
+                return h < p.h && img < p.n;
+            } else {
+                img = img0;
+                h = R;
+                return R >= 0 && R < p.h;
+            }
+        };
 #pragma unroll
         for (int i = 0; i < A_TASKS; ++i) {
             const int t = threadIdx.x + i * kWgThreads;
             int kk, j;
             task(t, QA, kk, j);
-            const int ch = j % CPR, h = h0 + j / CPR;
+            const int ch = j % CPR;
+            int32_t img, h;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((A_TOTAL % kWgThreads == 0 || t < A_TOTAL) && ch * E < p.w && h < p.h)
-                v = load_chunk<T, LW>(dyb + kk * plane + (int64_t)h * p.w, ch, p.w);
+            if ((A_TOTAL % kWgThreads == 0 || t < A_TOTAL) && ch * E < p.w && locate(h0 + j / CPR, img, h))
+                v = load_row_chunk(dy + ((int64_t)img * p.k + kb * 64 + kk) * plane + (int64_t)h * p.w, ch);
             ra[i] = v;
         }
 #pragma unroll
@@ -749,13 +796,27 @@ __global__ __launch_bounds__(kWgThreads, 1) void conv3x3_wgrad_kernel(const T* _
             const int t = threadIdx.x + i * kWgThreads;
             int cc, j;
             task(t, QB, cc, j);
-            const int ch = j % CPR, h = h0 - 1 + j / CPR;
+            const int ch = j % CPR;
+            int32_t img, h;
             u32x4 v = u32x4{0u, 0u, 0u, 0u};
-            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && h >= 0 && h < p.h &&
-                cb * 64 + cc < p.c)
-                v = load_chunk<T, LW>(xb + cc * plane + (int64_t)h * p.w, ch, p.w);
+            if ((B_TOTAL4 % kWgThreads == 0 || t < B_TOTAL4) && j < NBF && ch * E < p.w && cb * 64 + cc < p.c &&
+                locate(h0 - 1 + j / CPR, img, h))
+                v = load_row_chunk(x + ((int64_t)img * p.c + cb * 64 + cc) * plane + (int64_t)h * p.w, ch);
             rb[i] = v;
         }
+    };
+    auto fetch = [&](int32_t band) __attribute__((always_inline)) {
+        if constexpr (sizeof(T) == 2 && LW == 2) {
+            // the last valid row of the last image: stacked row n(h+1) − 2,
+            // or the last band of one-image bands
+            const bool fast = STACK ? (int64_t)band * TH + TH < (int64_t)p.n * (p.h + 1) - 2
+                                    : band + 1 < p.total_bands;
+            if (fast) {
+                fetch_rows(band, std::true_type{});
+                return;
+            }
+        }
+        fetch_rows(band, std::false_type{});
     };
     auto stash = [&]() {
 #pragma unroll
@@ -899,12 +960,13 @@ __global__ __launch_bounds__(256) void conv3x3_wgrad_reduce_kernel(const float* 
 
 template <typename T, int P, int LW>
 int run_wgrad(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* dy, float* dw, int accumulate) {
-    constexpr int TH = WgCfg<T>::TH;
+    constexpr int TH = wg_rows<T, P>();
     constexpr int RB = P * (int)sizeof(T);
     WgradParams p;
     p.n = (int32_t)d->n; p.c = (int32_t)d->c; p.k = (int32_t)d->k; p.h = (int32_t)d->h; p.w = (int32_t)d->w;
     p.bands_per_img = (p.h + TH - 1) / TH;
-    p.total_bands = p.n * p.bands_per_img;
+    p.total_bands = wg_stacked<T, P>() ? (int32_t)ceil_div((int64_t)p.n * (p.h + 1), TH) : p.n * p.bands_per_img;
+    p.fd_h1 = FastDiv((uint32_t)(p.h + 1));
     p.kblocks = p.k / 64;
     constexpr int CPR = P * (int)sizeof(T) / 16;
     const int tiles = p.kblocks * (int)ceil_div(p.c, 64);

@@ -163,5 +163,37 @@ __device__ __forceinline__ u32x4 load_chunk(const T* __restrict__ row, int ch, i
     return v;
 }
 
+// bf16 chunk ch of a row whose start is only 2-byte aligned (LW = 2 above),
+// in at most two loads: the 16 bytes from the dword at or below
+// the chunk start (one more dword when the start is odd in elements and the
+// chunk has 8 elements), realigned with funnel shifts; elements past the row
+// end read as zero.  Multi-dword global loads need only dword alignment.
+// The loads reach up to 7 elements past the row end (the next row or plane):
+// the caller must not use it on the tensor's last row.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+template <typename T>
+__device__ __forceinline__ u32x4 load_chunk_narrow(const T* __restrict__ row, int ch, int w) {
+    static_assert(sizeof(T) == 2, "realigning loads are for bf16 rows");
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    const int n = min(8, w - 8 * ch);        // elements of the chunk inside the row
+    if (n <= 0) return v;
+    const T* s = row + 8 * ch;
+    const bool odd = ((uintptr_t)s & 2) != 0;
+    const u32x4 d = *reinterpret_cast<const u32x4_a4*>(odd ? s - 1 : s);
+    if (odd) {
+        const uint32_t d4 = n == 8 ? *reinterpret_cast<const uint32_t*>(s + 7) : 0u;
+        v = u32x4{__builtin_amdgcn_alignbit(d.y, d.x, 16), __builtin_amdgcn_alignbit(d.z, d.y, 16),
+                  __builtin_amdgcn_alignbit(d.w, d.z, 16), __builtin_amdgcn_alignbit(d4, d.w, 16)};
+    } else {
+        v = d;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (2 * q >= n) v[q] = 0u;
+        else if (2 * q + 1 >= n) v[q] &= 0xffffu;
+    }
+    return v;
+}
+
 }  // namespace conv_fast
 }  // namespace nott
