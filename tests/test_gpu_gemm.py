@@ -61,8 +61,9 @@ def test_linear(ops, oracle, dt, m, kin, nout):
 # partial tiles: (4104, 192, 2056) forward on 256x128 tiles; (2048, 1288,
 # 1544) dW on 256x256 tiles split over K with the fused bias gradient;
 # (1024, 200, 320) dX on unsplit 128x128 and dW split 4 ways; (256, 384, 256)
-# dW unsplit over three tile columns (the bias gradient is summed once).
-DMA_LIN = [(4104, 192, 2056), (2048, 1288, 1544), (1024, 200, 320), (256, 384, 256)]
+# dW unsplit over three tile columns (the bias gradient is summed once);
+# (4100, 2048, 4104) forward on unsplit 256x256 tiles (17 x 17, K = 2048).
+DMA_LIN = [(4104, 192, 2056), (2048, 1288, 1544), (1024, 200, 320), (256, 384, 256), (4100, 2048, 4104)]
 
 
 def _edge(idx, n):

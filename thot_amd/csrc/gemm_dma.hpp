@@ -320,11 +320,12 @@ struct Config {
     static constexpr size_t kLds = (size_t)S * (BM + BN) * 128;
 };
 
-// Tile shapes the dispatcher picks from (all measured on the configs[3]
-// projection shapes): 256×128 with 8 waves of 64×64 and a 3-deep ring for
-// grids that fill the chip on their own; 256×256 with 8 waves of 128×64 and
-// a 2-deep ring for long-K products with few tiles (split over K); 128×128
-// with 4 waves and a 3-deep ring for the rest.
+// Tile shapes the dispatcher picks from (measured on the configs[3]
+// projection shapes and on large square products): 256×256 with 8 waves of
+// 128×64 and a 2-deep ring for long-K products, unsplit when they fill the
+// chip and split over K when they have few tiles; 256×128 with 8 waves of
+// 64×64 and a 3-deep ring for other grids that fill the chip on their own;
+// 128×128 with 4 waves and a 3-deep ring for the rest.
 enum class Shape { T256x128, T256x256, T128x128 };
 
 struct Plan {
@@ -341,7 +342,12 @@ inline Plan plan(nott_ctx ctx, int64_t M, int64_t N, int64_t K, int64_t splits) 
     // Split counts keep the grid within one round of workgroups (one per CU:
     // the 256x256 and 128x128 shapes hold 128 and 96 KB of LDS), so that a
     // few leftover splits do not cost a second round.
-    if (tiles(256, 128) >= cu) {
+    if (tiles(256, 256) >= cu && nkb >= 32) {
+        // long-K products that fill the chip with the larger tile: 8192^3
+        // 890 -> 974 TFLOP/s, 16384x4096x4096 938 -> 1070 (at K = 1024 the
+        // 256x128 tile's 3-deep ring wins)
+        p.shape = Shape::T256x256;
+    } else if (tiles(256, 128) >= cu) {
         p.shape = Shape::T256x128;
     } else if (tiles(256, 256) >= cu / 8 && nkb >= 16) {
         p.shape = Shape::T256x256;
