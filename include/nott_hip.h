@@ -137,6 +137,17 @@ int nott_linear_fwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int6
 int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
                     const void* dy, const void* x, const void* w,
                     void* dx, float* dw, float* db, int accumulate);
+/* An FC layer with its ReLU activation (fc.hpp:40 with the activation node of
+ * activation/apply.hpp:24-57, relu.hpp:13): relu = 1 gives y = relu(x·wᵀ + b)
+ * in the GEMM's epilogue, bit-identical to nott_linear_fwd then nott_relu_fwd. */
+int nott_linear_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                        const void* x, const void* w, const float* b, int relu, void* y);
+/* nott_linear_bwd where x is the output of the previous layer's ReLU
+ * (relu_input = 1): dx also takes that ReLU's backward, dx = (x <= 0) ? 0 : dy·w,
+ * bit-identical to nott_linear_bwd then nott_relu_bwd(y = x). */
+int nott_linear_bwd_act(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                        const void* dy, const void* x, const void* w,
+                        void* dx, float* dw, float* db, int accumulate, int relu_input);
 
 /* ---- ReLU -------------------------------------------------------------
  * Replaces the relu node applied after every layer by
@@ -175,6 +186,13 @@ int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype d
                            const void* x, void* y, uint8_t* tap);
 int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
                            const uint8_t* tap, const void* dy, void* dx);
+/* Max-pool backward followed by the backward of the ReLU whose output y is
+ * the pool's input (the Conv2d + ReLU + MaxPool2d layers of the small CNN:
+ * conv.hpp:177 with activation/details/relu.hpp:13, then pooling.hpp:144):
+ * dx = (y <= 0) ? 0 : maxpool_bwd(dy), bit-identical to nott_maxpool2d_bwd_tap
+ * then nott_relu_bwd, in one pass where the tiled kernels apply. */
+int nott_maxpool2d_bwd_tap_relu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                                const uint8_t* tap, const void* dy, const void* y, void* dx);
 /* y[nc] = mean over hw; dx[nc, i] = dy[nc] / hw. */
 int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
                             const void* x, void* y);

@@ -357,9 +357,12 @@ struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
 
 // Conv2d followed by ReLU, the activation fused into the convolution's
 // forward (nott_conv2d_fwd_act); backward = ReLU mask from the saved output,
-// then the convolution's gradients.
+// then the convolution's gradients.  consumer_masks: the output's only
+// consumer applies the ReLU's backward itself (a max-pool taking it with
+// forward_relu_input), so the gradient arrives masked.
 struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
-    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b, std::vector<int64_t> geom) {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b, std::vector<int64_t> geom,
+                          bool consumer_masks) {
         x = contig(x);
         const nott_conv2d_desc d = Conv2dFn::desc(x, wc, geom);
         const int64_t p = (d.h + 2 * d.pad_h - d.dil_h * (d.r - 1) - 1) / d.stride_h + 1;
@@ -372,6 +375,7 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
         ctx->save_for_backward({x, w, wc, b, y, wd});
         ctx->saved_data["geom"] = geom;
         ctx->saved_data["needs_dx"] = x.requires_grad();
+        ctx->saved_data["consumer_masks"] = consumer_masks;
         return y;
     }
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
@@ -381,8 +385,11 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
         const auto geom = ctx->saved_data["geom"].toIntVector();
         const nott_conv2d_desc d = Conv2dFn::desc(x, wc, geom);
         nott_ctx c = bind(dy);
-        Tensor dz = torch::empty_like(dy);
-        check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "relu backward");
+        Tensor dz = dy;
+        if (!ctx->saved_data["consumer_masks"].toBool()) {
+            dz = torch::empty_like(dy);
+            check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "relu backward");
+        }
         Tensor dx;
         if (ctx->saved_data["needs_dx"].toBool()) {
             dx = torch::empty_like(x);
@@ -394,35 +401,51 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
             check(nott_conv2d_bwd_weight(cw, &d, dtype_of(dz), ptr(x), ptr(dz), fptr(gw), fptr(gb), 1), cw,
                   "conv2d wgrad");
         }
-        return {dx, Tensor(), Tensor(), Tensor(), Tensor()};
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
 // --------------------------------------------------------------- Linear
+// flags: kLinRelu, the layer's ReLU fused into the forward GEMM (backward:
+// the ReLU mask from the saved output, unless kLinConsumerMasks says the
+// output's only consumer applies it); kLinReluInput, x is the previous
+// layer's ReLU output and dx takes that ReLU's backward (its producer then
+// skips it).
+constexpr int64_t kLinRelu = 1, kLinConsumerMasks = 2, kLinReluInput = 4;
 struct LinearFn : torch::autograd::Function<LinearFn> {
-    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b) {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor w, Tensor wc, Tensor b, int64_t flags) {
         x = contig(x);
         const int64_t kin = x.size(-1), m = x.numel() / kin, nout = wc.size(0);
         auto shape = x.sizes().vec();
         shape.back() = nout;
         Tensor y = torch::empty(shape, x.options());
         nott_ctx c = bind(x);
-        check(nott_linear_fwd(c, dtype_of(x), m, kin, nout, ptr(x), ptr(wc), fptr(b), ptr(y)), c, "linear forward");
-        ctx->save_for_backward({x, w, wc, b});
+        const bool relu = (flags & kLinRelu) != 0;
+        check(nott_linear_fwd_act(c, dtype_of(x), m, kin, nout, ptr(x), ptr(wc), fptr(b), relu ? 1 : 0, ptr(y)), c,
+              "linear forward");
+        ctx->save_for_backward({x, w, wc, b, relu && !(flags & kLinConsumerMasks) ? y : Tensor()});
         ctx->saved_data["needs_dx"] = x.requires_grad();
+        ctx->saved_data["flags"] = flags;
         return y;
     }
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
         auto s = ctx->get_saved_variables();
-        Tensor x = s[0], w = s[1], wc = s[2], b = s[3];
+        Tensor x = s[0], w = s[1], wc = s[2], b = s[3], y = s[4];
         Tensor dy = contig(grads[0]);
         const int64_t kin = x.size(-1), m = x.numel() / kin, nout = wc.size(0);
+        const int64_t flags = ctx->saved_data["flags"].toInt();
         nott_ctx c = bind(dy);
+        Tensor dz = dy;
+        if (y.defined()) {
+            dz = torch::empty_like(dy);
+            check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "relu backward");
+        }
         Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
         Tensor gw = grad_buffer(w), gb = grad_buffer(b);
-        check(nott_linear_bwd(c, dtype_of(dy), m, kin, nout, ptr(dy), ptr(x), ptr(wc), ptr(dx), fptr(gw), fptr(gb), 1),
+        check(nott_linear_bwd_act(c, dtype_of(dz), m, kin, nout, ptr(dz), ptr(x), ptr(wc), ptr(dx), fptr(gw), fptr(gb),
+                                  1, (flags & kLinReluInput) ? 1 : 0),
               c, "linear backward");
-        return {dx, Tensor(), Tensor(), Tensor()};
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
@@ -448,6 +471,8 @@ struct ReluFn : torch::autograd::Function<ReluFn> {
 
 // ------------------------------------------------------------ MaxPool2d
 // geometry = {kh, kw, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, ceil_mode}
+// relu_input: x is the output of a ReLU whose backward this layer's backward
+// applies (nott_maxpool2d_bwd_tap_relu), its producer skipping it.
 struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
     static nott_pool2d_desc desc(const Tensor& x, const std::vector<int64_t>& g) {
         nott_pool2d_desc d{};
@@ -462,7 +487,7 @@ struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
         if (ceil && (o - 1) * s >= in + p) --o;
         return o;
     }
-    static Tensor forward(AutogradContext* ctx, Tensor x, std::vector<int64_t> geom) {
+    static Tensor forward(AutogradContext* ctx, Tensor x, std::vector<int64_t> geom, bool relu_input) {
         x = contig(x);
         const nott_pool2d_desc d = desc(x, geom);
         const int64_t oh = out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, d.ceil_mode),
@@ -482,26 +507,32 @@ struct MaxPool2dFn : torch::autograd::Function<MaxPool2dFn> {
             check(nott_maxpool2d_fwd(c, &d, dtype_of(x), ptr(x), ptr(y), idx.data_ptr<int64_t>()), c,
                   "maxpool forward");
         }
-        ctx->save_for_backward({idx});
+        ctx->save_for_backward({idx, relu_input ? x : Tensor()});
         ctx->saved_data["geom"] = geom;
         ctx->saved_data["xshape"] = x.sizes().vec();
         ctx->mark_non_differentiable({idx});
         return y;
     }
     static variable_list backward(AutogradContext* ctx, variable_list grads) {
-        Tensor idx = ctx->get_saved_variables()[0];
+        auto s = ctx->get_saved_variables();
+        Tensor idx = s[0], rx = s[1];
         Tensor dy = contig(grads[0]);
         const auto xs = ctx->saved_data["xshape"].toIntVector();
         Tensor dx = torch::empty(xs, dy.options());
         const nott_pool2d_desc d = desc(dx, ctx->saved_data["geom"].toIntVector());
         nott_ctx c = bind(dy);
-        if (idx.scalar_type() == torch::kUInt8)
+        if (idx.scalar_type() == torch::kUInt8 && rx.defined())
+            check(nott_maxpool2d_bwd_tap_relu(c, &d, dtype_of(dy), idx.data_ptr<uint8_t>(), ptr(dy), ptr(rx), ptr(dx)),
+                  c, "maxpool+relu backward");
+        else if (idx.scalar_type() == torch::kUInt8)
             check(nott_maxpool2d_bwd_tap(c, &d, dtype_of(dy), idx.data_ptr<uint8_t>(), ptr(dy), ptr(dx)), c,
                   "maxpool backward");
         else
             check(nott_maxpool2d_bwd(c, &d, dtype_of(dy), idx.data_ptr<int64_t>(), ptr(dy), ptr(dx)), c,
                   "maxpool backward");
-        return {dx, Tensor()};
+        if (rx.defined() && idx.scalar_type() != torch::kUInt8)
+            check(nott_relu_bwd(c, dtype_of(dx), dx.numel(), ptr(rx), ptr(dx), ptr(dx)), c, "relu backward");
+        return {dx, Tensor(), Tensor()};
     }
 };
 
@@ -781,9 +812,11 @@ public:
         return Conv2dFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
     }
     // relu(forward(x)) with the activation fused into the convolution.
-    Tensor forward_relu(const Tensor& x) {
+    // consumer_masks: the result's only consumer is a MaxPool2d taking it
+    // with forward_relu_input, which applies the ReLU's backward.
+    Tensor forward_relu(const Tensor& x, bool consumer_masks = false) {
         const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
-        return Conv2dReluFn::apply(x, weight, wc, or_absent(bias, weight), geom_);
+        return Conv2dReluFn::apply(x, weight, wc, or_absent(bias, weight), geom_, consumer_masks);
     }
     // {stride_h, stride_w, pad_h, pad_w, dil_h, dil_w}
     const std::vector<int64_t>& geometry() const { return geom_; }
@@ -799,11 +832,22 @@ public:
         weight = register_parameter("weight", torch::empty({out, in}));
         if (bias) this->bias = register_parameter("bias", torch::zeros({out}));
     }
-    Tensor forward(const Tensor& x) {
-        const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
-        return LinearFn::apply(x, weight, wc, or_absent(bias, weight));
+    Tensor forward(const Tensor& x) { return apply(x, 0); }
+    // relu(forward(x)) with the activation in the GEMM's epilogue;
+    // consumer_masks: the result's only consumer is a Linear taking it with
+    // forward_relu_input, which applies the ReLU's backward.
+    Tensor forward_relu(const Tensor& x, bool consumer_masks = false) {
+        return apply(x, kLinRelu | (consumer_masks ? kLinConsumerMasks : 0));
     }
+    // x = the output of Linear::forward_relu(·, true): this layer's dx takes
+    // that ReLU's backward.
+    Tensor forward_relu_input(const Tensor& x) { return apply(x, kLinReluInput); }
     Tensor weight, bias, weight_compute;
+private:
+    Tensor apply(const Tensor& x, int64_t flags) {
+        const Tensor& wc = weight_compute.defined() ? weight_compute : weight;
+        return LinearFn::apply(x, weight, wc, or_absent(bias, weight), flags);
+    }
 };
 TORCH_MODULE(Linear);
 
@@ -883,7 +927,7 @@ inline void save_parameters(torch::nn::Module& m, const std::string& path) {
 }
 
 inline Tensor max_pool2d(const Tensor& x, int64_t k, int64_t stride, int64_t pad = 0, bool ceil_mode = false) {
-    return MaxPool2dFn::apply(x, std::vector<int64_t>{k, k, stride, stride, pad, pad, 1, 1, ceil_mode ? 1 : 0});
+    return MaxPool2dFn::apply(x, std::vector<int64_t>{k, k, stride, stride, pad, pad, 1, 1, ceil_mode ? 1 : 0}, false);
 }
 
 // Parameter-less layers as modules, so that a model registers every layer of
@@ -898,7 +942,10 @@ public:
     MaxPool2dImpl(std::array<int64_t, 2> k, std::array<int64_t, 2> stride, std::array<int64_t, 2> pad,
                   std::array<int64_t, 2> dilation, bool ceil_mode)
         : geom_{k[0], k[1], stride[0], stride[1], pad[0], pad[1], dilation[0], dilation[1], ceil_mode ? 1 : 0} {}
-    Tensor forward(const Tensor& x) { return MaxPool2dFn::apply(x, geom_); }
+    Tensor forward(const Tensor& x) { return MaxPool2dFn::apply(x, geom_, false); }
+    // x = the output of Conv2d::forward_relu(·, true): the ReLU's backward is
+    // applied here, in the pool's backward pass (one pass instead of two).
+    Tensor forward_relu_input(const Tensor& x) { return MaxPool2dFn::apply(x, geom_, true); }
     // {kh, kw, stride_h, stride_w, pad_h, pad_w, dil_h, dil_w, ceil_mode}
     const std::vector<int64_t>& geometry() const { return geom_; }
 private:

@@ -98,7 +98,7 @@ struct ConvRelu {
 };
 struct LinearRelu {
     LinearImpl* m;
-    Tensor operator()(Tensor x) const { return ::Nott::HIP::relu(m->forward(x)); }
+    Tensor operator()(Tensor x) const { return m->forward_relu(x); }
 };
 struct BatchNormRelu {
     BatchNorm2dImpl* m;

@@ -185,6 +185,13 @@ def test_maxpool_tap(ops, oracle, dt, case):
     check(host(dx), oracle.maxpool2d_bwd(d, idxe, host(dy)), dt, "maxpool dx")
     assert torch.equal(dx.view(torch.int16 if dt == "bf16" else torch.int32),
                        dxt.view(torch.int16 if dt == "bf16" else torch.int32))
+    # through the ReLU that produced the pool's input (zeros, NaN and -inf
+    # included): bit-identical to the pool backward then the ReLU backward
+    xd = dev(x, dt)
+    dxr = ops.maxpool2d_bwd_tap(tap, dy, d, relu_y=xd)
+    ref = ops.relu_bwd(xd, dxt)
+    assert torch.equal(dxr.view(torch.int16 if dt == "bf16" else torch.int32),
+                       ref.view(torch.int16 if dt == "bf16" else torch.int32))
 
 
 MAXPOOL_GOLDEN = ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil", "maxpool2x2_dil2",

@@ -98,6 +98,33 @@ def test_linear_bf16_tile_shapes(ops, oracle, m, kin, nout, accumulate):
     check(host(db)[outs], db0[outs] + rdb, dt, "db rows")
 
 
+# The FC layer's ReLU in the GEMM epilogues: forward y = relu(x·wᵀ + b), and
+# a dx that takes the previous layer's ReLU backward (x a ReLU output, zeros
+# included), each bit-identical to the separate passes; on the small CNN's
+# FC shapes (fp32) and on the bf16 direct-to-LDS / split plans.
+LIN_ACT = [("f32", 64, 3136, 128), ("f32", 64, 128, 10), ("f32", 50, 40, 30), ("bf16", 1024, 200, 320),
+           ("bf16", 4104, 192, 2056), ("bf16", 256, 384, 256), ("bf16", 2048, 1288, 1544)]
+
+
+@pytest.mark.parametrize("dt,m,kin,nout", LIN_ACT)
+def test_linear_relu_epilogues(ops, dt, m, kin, nout):
+    g = rng(17 + m + kin + nout)
+    x = host_input(g.standard_normal((m, kin)), dt)
+    w = host_input(g.standard_normal((nout, kin)) / math.sqrt(kin), dt)
+    b = f32(g.standard_normal(nout) * 0.1)
+    xd, wd, bd = dev(x, dt), dev(w, dt), dev(b)
+    iv = torch.int16 if dt == "bf16" else torch.int32
+    y = ops.linear_fwd(xd, wd, bd, relu=True)
+    y_ref = ops.relu_fwd(ops.linear_fwd(xd, wd, bd))
+    assert torch.equal(y.view(iv), y_ref.view(iv))
+    h = ops.relu_fwd(xd)                       # a ReLU output: about half zeros
+    dy = dev(host_input(g.standard_normal((m, nout)), dt), dt)
+    dx, dw, db = ops.linear_bwd(dy, h, wd, relu_input=True)
+    dx0, dw0, db0 = ops.linear_bwd(dy, h, wd)
+    assert torch.equal(dx.view(iv), ops.relu_bwd(h, dx0).view(iv))
+    assert torch.equal(dw, dw0) and torch.equal(db, db0)
+
+
 def test_linear_golden(ops):
     z = np.load(os.path.join(GOLD, "linear.npz"))
     x, w, b, dy = (f32(z[k]) for k in ("x", "w", "b", "dy"))

@@ -70,12 +70,15 @@ SIGNATURES: dict[str, list] = {
     "nott_conv2d_bwd_weight": [vp, C.POINTER(Conv2dDesc), i32, vp, vp, fp, fp, i32],
     "nott_linear_fwd": [vp, i32, i64, i64, i64, vp, vp, fp, vp],
     "nott_linear_bwd": [vp, i32, i64, i64, i64, vp, vp, vp, vp, fp, fp, i32],
+    "nott_linear_fwd_act": [vp, i32, i64, i64, i64, vp, vp, fp, i32, vp],
+    "nott_linear_bwd_act": [vp, i32, i64, i64, i64, vp, vp, vp, vp, fp, fp, i32, i32],
     "nott_relu_fwd": [vp, i32, i64, vp, vp],
     "nott_relu_bwd": [vp, i32, i64, vp, vp, vp],
     "nott_maxpool2d_fwd": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp],
     "nott_maxpool2d_bwd": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp],
     "nott_maxpool2d_fwd_tap": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp],
     "nott_maxpool2d_bwd_tap": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp],
+    "nott_maxpool2d_bwd_tap_relu": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp, vp],
     "nott_avgpool_global_fwd": [vp, i32, i64, i64, vp, vp],
     "nott_avgpool_global_bwd": [vp, i32, i64, i64, vp, vp],
     "nott_batchnorm2d_fwd": [vp, i32, i64, i64, i64, vp, fp, fp, f64, f64, fp, fp, vp, fp, fp],

@@ -112,17 +112,23 @@ struct ColKLoader {
 };
 
 // Epilogue: row-major C[m·ldc + n] (fp32 or T), optional bias[n], optional
-// accumulate into existing fp32 values.
+// accumulate into existing fp32 values; relu: a fused ReLU on the result
+// (NaN passes); mask (nullable, C's shape): the backward of a ReLU whose
+// output is mask, zero where mask <= 0.
 template <typename TC>
 struct RowMajorStore {
     TC* c;
     int64_t ldc, M, N;
     const float* bias;   // per column, nullable
     int accumulate;
+    int relu = 0;
+    const TC* mask = nullptr;
     __device__ __forceinline__ void store(int64_t m, int64_t n, float v) const {
         if (m >= M || n >= N) return;
         if (bias) v += bias[n];
         if (accumulate) v += Io<TC>::ld(c, m * ldc + n);
+        if (relu && !(v > 0.f || v != v)) v = 0.f;
+        if (mask && Io<TC>::ld(mask, m * ldc + n) <= 0.f) v = 0.f;
         Io<TC>::st(c, m * ldc + n, v);
     }
 };

@@ -195,9 +195,10 @@ int bf16_gemm(nott_ctx ctx, const bf16_t* A, int64_t lda, const bf16_t* B, int64
 }
 
 template <typename T>
-int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y) {
+int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const void* w, const float* b, void* y,
+        int relu) {
     if constexpr (sizeof(T) == 2) {
-        RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
+        RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0, relu};
         const int st = bf16_gemm<false, false>(ctx, static_cast<const T*>(x), kin, static_cast<const T*>(w), kin, ep,
                                                m, nout, kin);
         if (st != NOTT_ERR_UNSUPPORTED) return st;
@@ -206,15 +207,17 @@ int fwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* x, const
     const T* wp = static_cast<const T*>(w);
     RowKLoader<T> la{xp, kin, m, kin, vec16<T>(x, kin)};
     RowKLoader<T> lb{wp, kin, nout, kin, vec16<T>(w, kin)};
-    RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0};
+    RowMajorStore<T> ep{static_cast<T*>(y), nout, m, nout, b, 0, relu};
     if (small_grid(ctx, m, nout)) return run_small<T>(ctx, la, lb, ep, m, nout, kin);
     return run<T>(ctx, la, lb, ep, m, nout, kin);
 }
 
 template <typename T>
 int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, const void* x, const void* w, void* dx,
-        float* dw, float* db, int accumulate) {
+        float* dw, float* db, int accumulate, int relu_input) {
     const T* dyp = static_cast<const T*>(dy);
+    // relu_input: x is a ReLU's output, whose backward dx takes (zero where x <= 0)
+    const T* dx_mask = relu_input ? static_cast<const T*>(x) : nullptr;
     // A db-only request (no dw) is the column sum alone.
     if (db && !dw) {
         const int st = launch_db<T>(ctx, dyp, m, nout, db, accumulate);
@@ -229,7 +232,7 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
         const bool fw = !dw || (m % fast::BK == 0 && nout % 8 == 0 && kin % 8 == 0);
         if (fx && fw) {
             if (dx) {
-                RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
+                RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0, 0, dx_mask};
                 const int st = bf16_gemm<false, true>(ctx, dyp, nout, static_cast<const T*>(w), kin, ep, m, kin, nout);
                 if (st != NOTT_ERR_UNSUPPORTED) {
                     if (st != NOTT_OK) return st;
@@ -265,7 +268,7 @@ int bwd(nott_ctx ctx, int64_t m, int64_t kin, int64_t nout, const void* dy, cons
     if (dx) {
         RowKLoader<T> la{dyp, nout, m, nout, vec16<T>(dy, nout)};
         ColKLoader<T> lb{static_cast<const T*>(w), kin, kin, nout};
-        RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0};
+        RowMajorStore<T> ep{static_cast<T*>(dx), kin, m, kin, nullptr, 0, 0, dx_mask};
         const int st = small_grid(ctx, m, kin) ? run_small<T>(ctx, la, lb, ep, m, kin, nout)
                                                : run<T>(ctx, la, lb, ep, m, kin, nout);
         if (st != NOTT_OK) return st;
@@ -291,17 +294,31 @@ extern "C" int nott_linear_fwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_
     if (m == 0) return NOTT_OK;
     NOTT_REQUIRE(ctx, x && w && y, "nott_linear_fwd: null buffer");
     nott::DeviceScope scope(ctx->device);
-    return dtype == NOTT_F32 ? fwd<float>(ctx, m, kin, nout, x, w, b, y) : fwd<bf16_t>(ctx, m, kin, nout, x, w, b, y);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, m, kin, nout, x, w, b, y, 0) : fwd<bf16_t>(ctx, m, kin, nout, x, w, b, y, 0);
 }
 
-extern "C" int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout, const void* dy,
-                               const void* x, const void* w, void* dx, float* dw, float* db, int accumulate) {
+extern "C" int nott_linear_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                                   const void* x, const void* w, const float* b, int relu, void* y) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_linear_fwd_act: bad dtype");
+    NOTT_REQUIRE(ctx, m >= 0 && kin > 0 && nout > 0, "nott_linear_fwd_act: need m >= 0, kin > 0, nout > 0");
+    if (m == 0) return NOTT_OK;
+    NOTT_REQUIRE(ctx, x && w && y, "nott_linear_fwd_act: null buffer");
+    nott::DeviceScope scope(ctx->device);
+    const int r = relu != 0;
+    return dtype == NOTT_F32 ? fwd<float>(ctx, m, kin, nout, x, w, b, y, r) : fwd<bf16_t>(ctx, m, kin, nout, x, w, b, y, r);
+}
+
+extern "C" int nott_linear_bwd_act(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout,
+                                   const void* dy, const void* x, const void* w, void* dx, float* dw, float* db,
+                                   int accumulate, int relu_input) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), "nott_linear_bwd: bad dtype");
     NOTT_REQUIRE(ctx, m >= 0 && kin > 0 && nout > 0, "nott_linear_bwd: need m >= 0, kin > 0, nout > 0");
     NOTT_REQUIRE(ctx, dy != nullptr || m == 0, "nott_linear_bwd: null dy");
     NOTT_REQUIRE(ctx, !dx || w, "nott_linear_bwd: dx needs w");
     NOTT_REQUIRE(ctx, !dw || x || m == 0, "nott_linear_bwd: dw needs x");
+    NOTT_REQUIRE(ctx, !relu_input || !dx || x || m == 0, "nott_linear_bwd_act: relu_input needs x");
     nott::DeviceScope scope(ctx->device);
     if (m == 0) {
         // Empty batch: dx is empty; the parameter gradients sum over nothing.
@@ -311,6 +328,12 @@ extern "C" int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_
         }
         return NOTT_OK;
     }
-    return dtype == NOTT_F32 ? bwd<float>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate)
-                             : bwd<bf16_t>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate);
+    const int r = relu_input != 0 && dx != nullptr;
+    return dtype == NOTT_F32 ? bwd<float>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate, r)
+                             : bwd<bf16_t>(ctx, m, kin, nout, dy, x, w, dx, dw, db, accumulate, r);
+}
+
+extern "C" int nott_linear_bwd(nott_ctx ctx, nott_dtype dtype, int64_t m, int64_t kin, int64_t nout, const void* dy,
+                               const void* x, const void* w, void* dx, float* dw, float* db, int accumulate) {
+    return nott_linear_bwd_act(ctx, dtype, m, kin, nout, dy, x, w, dx, dw, db, accumulate, 0);
 }

@@ -249,6 +249,21 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
     }
 }
 
+// Backward through the ReLU whose output y is the pool's input (the ReLU
+// backward's rule: zero where y <= 0), applied to V consecutive dx values
+// before they are stored, so the result equals the two passes bit for bit.
+template <typename T, int V>
+__device__ __forceinline__ void relu_mask(const T* __restrict__ y, f32x4& out) {
+    if constexpr (V == 4) {
+        const f32x4 y4 = Vec4<T>::ld(y);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (y4[e] <= 0.f) out[e] = 0.f;
+    } else {
+        if (Io<T>::ld(y, 0) <= 0.f) out[0] = 0.f;
+    }
+}
+
 // Backward: workgroup (band of kPoolRows·sh input rows, plane) stages the
 // argmax (as 32-bit in-plane indices) and dy of every output row whose window
 // reaches the band in LDS, then each input gathers from the outputs that can
@@ -257,7 +272,8 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_tiled_kernel(const T* __
 template <typename T, bool VEC, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const IX* __restrict__ argmax,
                                                                      const T* __restrict__ dy, T* __restrict__ dx,
-                                                                     PoolGeom32 g, int32_t band_rows) {
+                                                                     const T* __restrict__ ry, PoolGeom32 g,
+                                                                     int32_t band_rows) {
     // VEC (w and ow multiples of 4, aligned buffers): 4 consecutive elements
     // per thread for the staging loads and for the dx stores.
     constexpr int V = VEC ? 4 : 1;
@@ -327,6 +343,7 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_tiled_kernel(const IX* _
         out[e] = acc;
       }
       const int64_t di = (int64_t)pl * g.h * g.w + (int64_t)ih_lo * g.w + j0;
+      if (ry) relu_mask<T, V>(ry + di, out);
       if constexpr (VEC) Vec4<T>::st(dx + di, out);
       else Io<T>::st(dx, di, out[0]);
     }
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_s2_kernel(const T* __res
 template <typename T, int K, int P, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_bwd_s2_kernel(const IX* __restrict__ argmax,
                                                                   const T* __restrict__ dy, T* __restrict__ dx,
-                                                                  PoolGeom32 g) {
+                                                                  const T* __restrict__ ry, PoolGeom32 g) {
     static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "window");
     constexpr int NC = K;   // candidate output columns of a 4-input group: 2q .. 2q + K − 1 (K ≤ 3)
     extern __shared__ char sm[];
@@ -495,7 +512,10 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_s2_kernel(const IX* __re
                     if (2 * j - P <= e && e <= 2 * j - P + K - 1 && cc[j] == idx) acc[e] += gg[j];
             }
         }
-        Vec4<T>::st(dx + (int64_t)pl * g.h * g.w + (int64_t)ih * g.w + iw0, f32x4{acc[0], acc[1], acc[2], acc[3]});
+        const int64_t di = (int64_t)pl * g.h * g.w + (int64_t)ih * g.w + iw0;
+        f32x4 out = f32x4{acc[0], acc[1], acc[2], acc[3]};
+        if (ry) relu_mask<T, 4>(ry + di, out);
+        Vec4<T>::st(dx + di, out);
     }
 }
 
@@ -665,7 +685,7 @@ int maxpool_fwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, 
 
 template <typename IX>
 int maxpool_bwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const IX* argmax, const void* dy,
-                     void* dx, const char* name) {
+                     void* dx, const char* name, const void* relu_y = nullptr) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), std::string(name) + ": bad dtype");
     PoolGeom g;
@@ -684,53 +704,62 @@ int maxpool_bwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, 
     const auto* db = static_cast<const bf16_t*>(dy);
     auto* xf = static_cast<float*>(dx);
     auto* xb = static_cast<bf16_t*>(dx);
-    if (fits32(planes, g) && planes <= 65535 && s2_geom(g) && vec4_ok(g, dtype, {dy, dx}) &&
+    const auto* rf = static_cast<const float*>(relu_y);
+    const auto* rb = static_cast<const bf16_t*>(relu_y);
+    bool fused = true;   // the tiled kernels apply relu_y themselves
+    if (fits32(planes, g) && planes <= 65535 && s2_geom(g) && vec4_ok(g, dtype, {dy, dx, relu_y}) &&
         ((uintptr_t)argmax % ix_align<IX>()) == 0 && s2_bwd_lds(g) <= kPoolLdsMax) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 sgrid((unsigned)nott::ceil_div(g.h, (int64_t)(2 * kS2Rows)), (unsigned)planes);
         const size_t lds = s2_bwd_lds(g);
         if (g.kh == 3 && dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_bwd_s2_kernel<float, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, argmax,
-                               df, xf, g32);
+                               df, xf, rf, g32);
         else if (g.kh == 3)
             hipLaunchKernelGGL((maxpool_bwd_s2_kernel<bf16_t, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream,
-                               argmax, db, xb, g32);
+                               argmax, db, xb, rb, g32);
         else if (dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_bwd_s2_kernel<float, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, argmax,
-                               df, xf, g32);
+                               df, xf, rf, g32);
         else
             hipLaunchKernelGGL((maxpool_bwd_s2_kernel<bf16_t, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream,
-                               argmax, db, xb, g32);
+                               argmax, db, xb, rb, g32);
     } else if (fits32(planes, g) && blds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.h, (int64_t)band_rows), (unsigned)planes);
-        const bool vec = vec4_ok(g, dtype, {dy, dx}) && ((uintptr_t)argmax % ix_align<IX>()) == 0;
+        const bool vec = vec4_ok(g, dtype, {dy, dx, relu_y}) && ((uintptr_t)argmax % ix_align<IX>()) == 0;
         if (dtype == NOTT_F32 && vec)
             hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, true, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, df, xf, g32, band_rows);
+                               argmax, df, xf, rf, g32, band_rows);
         else if (dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<float, false, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, df, xf, g32, band_rows);
+                               argmax, df, xf, rf, g32, band_rows);
         else if (vec)
             hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, true, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, db, xb, g32, band_rows);
+                               argmax, db, xb, rb, g32, band_rows);
         else
             hipLaunchKernelGGL((maxpool_bwd_tiled_kernel<bf16_t, false, IX>), tgrid, dim3(kThreads), blds, ctx->stream,
-                               argmax, db, xb, g32, band_rows);
+                               argmax, db, xb, rb, g32, band_rows);
     } else if (fits32(planes, g)) {
         const PoolGeom32 g32 = geom32(g);
+        fused = false;
         if (dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_bwd_kernel32<float, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, df, xf,
                                (uint32_t)total, g32);
         else
             hipLaunchKernelGGL((maxpool_bwd_kernel32<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, db, xb,
                                (uint32_t)total, g32);
-    } else if (dtype == NOTT_F32)
-        hipLaunchKernelGGL((maxpool_bwd_kernel<float, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, df, xf, planes,
-                           g);
-    else
-        hipLaunchKernelGGL((maxpool_bwd_kernel<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, db, xb,
-                           planes, g);
+    } else {
+        fused = false;
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((maxpool_bwd_kernel<float, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, df, xf,
+                               planes, g);
+        else
+            hipLaunchKernelGGL((maxpool_bwd_kernel<bf16_t, IX>), grid, dim3(kThreads), 0, ctx->stream, argmax, db, xb,
+                               planes, g);
+    }
+    // the untiled kernels take the ReLU's backward as a second, in-place pass
+    if (relu_y && !fused) return nott_relu_bwd(ctx, dtype, total, relu_y, dx, dx);
     return nott::launch_status(ctx, name);
 }
 
@@ -754,4 +783,11 @@ extern "C" int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, n
 extern "C" int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
                                       const void* dy, void* dx) {
     return maxpool_bwd_impl<uint8_t>(ctx, d, dtype, tap, dy, dx, "nott_maxpool2d_bwd_tap");
+}
+
+extern "C" int nott_maxpool2d_bwd_tap_relu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                                           const uint8_t* tap, const void* dy, const void* y, void* dx) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, y != nullptr, "nott_maxpool2d_bwd_tap_relu: null y");
+    return maxpool_bwd_impl<uint8_t>(ctx, d, dtype, tap, dy, dx, "nott_maxpool2d_bwd_tap_relu", y);
 }

@@ -51,11 +51,15 @@ struct SmallCNNImpl : torch::nn::Module {
                 NA::module("layer", NA::fc(128, 10, true, "identity", "he_uniform"))};
     }
     Tensor forward(Tensor x) {
-        x = pool0(conv0->forward_relu(x));   // Conv + ReLU (fused), MaxPool2
-        x = pool1(conv1->forward_relu(x));
+        // Conv + ReLU (fused), MaxPool2; the ReLU's backward runs in the
+        // pool's backward pass
+        x = pool0->forward_relu_input(conv0->forward_relu(x, true));
+        x = pool1->forward_relu_input(conv1->forward_relu(x, true));
         x = flat(x);                     // Flatten (a view)
-        x = NH::relu(fc0(x));
-        return fc1(x);
+        // FC + ReLU in the GEMM's epilogue; the ReLU's backward runs in
+        // fc1's dx epilogue
+        x = fc0->forward_relu(x, true);
+        return fc1->forward_relu_input(x);
     }
 };
 TORCH_MODULE(SmallCNN);

@@ -316,13 +316,21 @@ def maxpool2d_fwd_tap(x: torch.Tensor, d: Pool2dDesc):
     return y, tap
 
 
-def maxpool2d_bwd_tap(tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc) -> torch.Tensor:
+def maxpool2d_bwd_tap(tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc,
+                      relu_y: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dx of the pool; with relu_y (the pool's input, a ReLU output) also the
+    ReLU's backward: dx = 0 where relu_y <= 0."""
     oh = pool_out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, bool(d.ceil_mode))
     ow = pool_out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, bool(d.ceil_mode))
     _check(dy, "dy", shape=(d.n, d.c, oh, ow))
     _check(tap, "tap", shape=(d.n, d.c, oh, ow), dtype=torch.uint8, device=dy.device)
     dx = torch.empty((d.n, d.c, d.h, d.w), dtype=dy.dtype, device=dy.device)
-    _ctx_for(dy).call("nott_maxpool2d_bwd_tap", C.byref(d), nott_dtype(dy.dtype), _ptr(tap), _ptr(dy), _ptr(dx))
+    if relu_y is None:
+        _ctx_for(dy).call("nott_maxpool2d_bwd_tap", C.byref(d), nott_dtype(dy.dtype), _ptr(tap), _ptr(dy), _ptr(dx))
+    else:
+        _check(relu_y, "relu_y", shape=(d.n, d.c, d.h, d.w), dtype=dy.dtype, device=dy.device)
+        _ctx_for(dy).call("nott_maxpool2d_bwd_tap_relu", C.byref(d), nott_dtype(dy.dtype), _ptr(tap), _ptr(dy),
+                          _ptr(relu_y), _ptr(dx))
     return dx
 
 
@@ -346,7 +354,7 @@ def avgpool_global_bwd(dy: torch.Tensor, hw_shape) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------- linear
-def linear_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None) -> torch.Tensor:
+def linear_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, relu: bool = False) -> torch.Tensor:
     _check(x, "x")
     m, kin = x.reshape(-1, x.shape[-1]).shape
     nout = w.shape[0]
@@ -354,13 +362,17 @@ def linear_fwd(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = Non
     if b is not None:
         _check(b, "b", shape=(nout,), dtype=torch.float32, device=x.device)
     y = torch.empty((*x.shape[:-1], nout), dtype=x.dtype, device=x.device)
-    _ctx_for(x).call("nott_linear_fwd", nott_dtype(x.dtype), m, kin, nout, _ptr(x), _ptr(w), _ptr(b), _ptr(y))
+    if relu:
+        _ctx_for(x).call("nott_linear_fwd_act", nott_dtype(x.dtype), m, kin, nout, _ptr(x), _ptr(w), _ptr(b), 1,
+                         _ptr(y))
+    else:
+        _ctx_for(x).call("nott_linear_fwd", nott_dtype(x.dtype), m, kin, nout, _ptr(x), _ptr(w), _ptr(b), _ptr(y))
     return y
 
 
 def linear_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, *, need_dx: bool = True, need_dw: bool = True,
                need_db: bool = True, dx: Optional[torch.Tensor] = None, dw: Optional[torch.Tensor] = None,
-               db: Optional[torch.Tensor] = None, accumulate: bool = False):
+               db: Optional[torch.Tensor] = None, accumulate: bool = False, relu_input: bool = False):
     _check(x, "x")
     m, kin = x.reshape(-1, x.shape[-1]).shape
     nout = w.shape[0]
@@ -380,8 +392,8 @@ def linear_bwd(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, *, need_dx: b
         _check(dw, "dw", shape=(nout, kin), dtype=torch.float32, device=x.device)
     if db is not None:
         _check(db, "db", shape=(nout,), dtype=torch.float32, device=x.device)
-    _ctx_for(x).call("nott_linear_bwd", nott_dtype(x.dtype), m, kin, nout, _ptr(dy), _ptr(x), _ptr(w), _ptr(dx),
-                     _ptr(dw if need_dw else None), _ptr(db if need_db else None), int(accumulate))
+    _ctx_for(x).call("nott_linear_bwd_act", nott_dtype(x.dtype), m, kin, nout, _ptr(dy), _ptr(x), _ptr(w), _ptr(dx),
+                     _ptr(dw if need_dw else None), _ptr(db if need_db else None), int(accumulate), int(relu_input))
     return dx, (dw if need_dw else None), (db if need_db else None)
 
 
