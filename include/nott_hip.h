@@ -342,6 +342,12 @@ int nott_adam_step_graph(nott_ctx ctx, int decoupled, int64_t n,
 /* ---- utilities used by the host modules ---------------------------------- */
 /* dst = a + b elementwise (residual gradient fan-in, block/details/blocks/residual.hpp:131). */
 int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, void* dst);
+/* The gradient of a residual block's output, which is a ReLU output (the
+ * block's final activation, residual.hpp:130-132) used twice by the next
+ * block (branch and skip, residual.hpp:87-141): dz = (y <= 0) ? 0 : a + b,
+ * bit-identical to nott_add then nott_relu_bwd, in one pass. */
+int nott_add_relu_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, const void* y,
+                      void* dz);
 /* Dtype conversion fp32 <-> bf16 (round to nearest even). */
 int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype src_dtype, void* dst, nott_dtype dst_dtype);
 /* Fill `bytes` bytes with zero using a kernel (safe under graph capture). */

@@ -629,10 +629,11 @@ struct BatchNorm2dReluFn : torch::autograd::Function<BatchNorm2dReluFn> {
 // The second BatchNorm2d of a residual branch with the skip addition and the
 // block's final ReLU (residual.hpp:130-132): y = relu(BN(x) + skip) in one
 // apply pass.  Backward: dz = dy·[y > 0] feeds both the BN backward and the
-// skip.
+// skip; consumer_masks: y's only consumer is the next block's fork, which
+// applies the ReLU's backward itself (dz = dy then).
 struct BatchNorm2dAddReluFn : torch::autograd::Function<BatchNorm2dAddReluFn> {
     static Tensor forward(AutogradContext* ctx, Tensor x, Tensor skip, Tensor gamma, Tensor beta,
-                          Tensor running_mean, Tensor running_var, double eps, double momentum) {
+                          Tensor running_mean, Tensor running_var, double eps, double momentum, bool consumer_masks) {
         x = contig(x);
         skip = contig(skip);
         const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
@@ -644,7 +645,7 @@ struct BatchNorm2dAddReluFn : torch::autograd::Function<BatchNorm2dAddReluFn> {
                                        fptr(running_mean), fptr(running_var), ptr(skip), 1, ptr(y), fptr(mean),
                                        fptr(rstd)),
               c, "batchnorm+add+relu forward");
-        ctx->save_for_backward({x, gamma, beta, mean, rstd, y});
+        ctx->save_for_backward({x, gamma, beta, mean, rstd, consumer_masks ? Tensor() : y});
         ctx->saved_data["needs_dx"] = x.requires_grad();
         return y;
     }
@@ -653,15 +654,18 @@ struct BatchNorm2dAddReluFn : torch::autograd::Function<BatchNorm2dAddReluFn> {
         Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4], y = s[5];
         Tensor dy = contig(grads[0]);
         const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
-        Tensor dz = torch::empty_like(dy);
         nott_ctx c = bind(dy);
-        check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "block relu backward");
+        Tensor dz = dy;
+        if (y.defined()) {
+            dz = torch::empty_like(dy);
+            check(nott_relu_bwd(c, dtype_of(dy), dy.numel(), ptr(y), ptr(dy), ptr(dz)), c, "block relu backward");
+        }
         Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
         Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
         check(nott_batchnorm2d_bwd(c, dtype_of(dz), n, ch, hw, ptr(x), ptr(dz), fptr(mean), fptr(rstd), fptr(gamma),
                                    ptr(dx), fptr(gg), fptr(gbt), 1),
               c, "batchnorm backward");
-        return {dx, dz, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+        return {dx, dz, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
@@ -735,16 +739,32 @@ struct AttentionFn : torch::autograd::Function<AttentionFn> {
 
 // ---------------------------------------------------------------- Fork
 // Two uses of one tensor (residual skip): backward sums the two gradients.
+// relu_input: x is the previous block's output, a ReLU output whose backward
+// is applied here (nott_add_relu_bwd), its producer skipping it.
 struct ForkFn : torch::autograd::Function<ForkFn> {
-    static variable_list forward(AutogradContext*, Tensor x) { return {x.view(x.sizes()), x.view(x.sizes())}; }
-    static variable_list backward(AutogradContext*, variable_list grads) {
-        if (!grads[0].defined()) return {grads[1]};
-        if (!grads[1].defined()) return {grads[0]};
+    static variable_list forward(AutogradContext* ctx, Tensor x, bool relu_input) {
+        ctx->save_for_backward({relu_input ? x : Tensor()});
+        return {x.view(x.sizes()), x.view(x.sizes())};
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        Tensor y = ctx->get_saved_variables()[0];
+        if (!grads[0].defined() || !grads[1].defined()) {
+            Tensor g = contig(grads[0].defined() ? grads[0] : grads[1]);
+            if (!y.defined() || !g.defined()) return {g, Tensor()};
+            Tensor out = torch::empty_like(g);
+            nott_ctx c = bind(g);
+            check(nott_relu_bwd(c, dtype_of(g), g.numel(), ptr(y), ptr(g), ptr(out)), c, "fork relu backward");
+            return {out, Tensor()};
+        }
         Tensor a = contig(grads[0]), b = contig(grads[1]);
         Tensor out = torch::empty_like(a);
         nott_ctx c = bind(a);
-        check(nott_add(c, dtype_of(a), a.numel(), ptr(a), ptr(b), ptr(out)), c, "fork backward");
-        return {out};
+        if (y.defined())
+            check(nott_add_relu_bwd(c, dtype_of(a), a.numel(), ptr(a), ptr(b), ptr(y), ptr(out)), c,
+                  "fork add+relu backward");
+        else
+            check(nott_add(c, dtype_of(a), a.numel(), ptr(a), ptr(b), ptr(out)), c, "fork backward");
+        return {out, Tensor()};
     }
 };
 
@@ -877,10 +897,13 @@ public:
     }
     // relu(BN(x) + skip): the residual branch's last layer, skip addition and
     // final ReLU, fused.
-    Tensor forward_add_relu(const Tensor& x, const Tensor& skip) {
+    // consumer_masks: the result's only consumer is a ResidualBasicBlock
+    // taking it with relu_input, whose fork applies the ReLU's backward.
+    Tensor forward_add_relu(const Tensor& x, const Tensor& skip, bool consumer_masks = false) {
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
         ++batches_;
-        return BatchNorm2dAddReluFn::apply(x, skip, weight, bias, running_mean, running_var, eps_, momentum_);
+        return BatchNorm2dAddReluFn::apply(x, skip, weight, bias, running_mean, running_var, eps_, momentum_,
+                                           consumer_masks);
     }
     // A forward replayed from a captured graph (no host code ran), or one
     // recorded during capture / undone by a warm-up (not run as a step).
@@ -994,11 +1017,15 @@ public:
         if (projection)
             proj = register_module("conv2d_4", Conv2d(Conv2dOptions{in, out, {1, 1}, {stride, stride}, {0, 0}, {1, 1}, false}));
     }
-    Tensor forward(const Tensor& x) {
-        auto f = ForkFn::apply(x);   // x feeds the branch and the skip
+    // relu_input: x is the output of the previous block run with
+    // consumer_masks (its final ReLU's backward then runs in this block's
+    // fork); consumer_masks: the output's only consumer is the next block,
+    // run with relu_input.
+    Tensor forward(const Tensor& x, bool relu_input = false, bool consumer_masks = false) {
+        auto f = ForkFn::apply(x, relu_input);   // x feeds the branch and the skip
         Tensor h = bn1->forward_relu(conv0(f[0]));
         Tensor skip = proj ? proj(f[1]) : f[1];
-        return bn3->forward_add_relu(conv2(h), skip);
+        return bn3->forward_add_relu(conv2(h), skip, consumer_masks);
     }
     Conv2d conv0{nullptr}, conv2{nullptr}, proj{nullptr};
     BatchNorm2d bn1{nullptr}, bn3{nullptr};

@@ -194,6 +194,24 @@ def test_maxpool_tap(ops, oracle, dt, case):
                        ref.view(torch.int16 if dt == "bf16" else torch.int32))
 
 
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("n,offset", [(64 * 64 * 56 * 56, 0), (1000003, 0), (4099, 1)])
+def test_add_relu_bwd(ops, dt, n, offset):
+    """The fork gradient of a ReLU output, (y <= 0) ? 0 : a + b, against the
+    two passes, bit for bit (zeros, NaN and -inf in y; an odd length and an
+    unaligned start take the tail and two-pass paths)."""
+    g = rng(n % 1000 + offset)
+    mk = lambda: dev(host_input(g.standard_normal(n + offset), dt), dt)[offset:]
+    a, b, y = mk(), mk(), ops.relu_fwd(mk())
+    yh = y.view(-1)
+    yh[::97] = float("nan")
+    yh[::89] = float("-inf")
+    iv = torch.int16 if dt == "bf16" else torch.int32
+    dz = ops.add_relu_bwd(a, b, y)
+    ref = ops.relu_bwd(y, ops.add(a, b))
+    assert torch.equal(dz.view(iv), ref.view(iv))
+
+
 MAXPOOL_GOLDEN = ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil", "maxpool2x2_dil2",
                   "maxpool3x3_s2p1_nan_inf", "maxpool2x2_s2_nan_inf"]
 

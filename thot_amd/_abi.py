@@ -95,6 +95,7 @@ SIGNATURES: dict[str, list] = {
     "nott_adam_step_graph": [vp, i32, i64, vp, i32, vp, i32, fp, fp, vp, vp, i32, i32],
     "nott_loss_accumulate": [vp, fp, f64, vp],
     "nott_add": [vp, i32, i64, vp, vp, vp],
+    "nott_add_relu_bwd": [vp, i32, i64, vp, vp, vp, vp],
     "nott_cast": [vp, i64, vp, i32, vp, i32],
     "nott_zero": [vp, i64, vp],
     "nott_scale": [vp, i32, i64, vp, fp, vp],

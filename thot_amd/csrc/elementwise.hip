@@ -139,6 +139,51 @@ __global__ __launch_bounds__(kThreads) void avgpool_bwd_kernel(const T* __restri
     Io<T>::st(dx, i, Io<T>::ld(dy, i / hw) / (float)hw);
 }
 
+// dz = (y <= 0) ? 0 : a + b over 16-byte groups (8 bf16 / 4 fp32), the
+// sum rounded once as nott_add rounds it.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void add_relu_bwd_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                                const T* __restrict__ y, T* __restrict__ dz,
+                                                                int64_t n) {
+    constexpr int V = 16 / (int)sizeof(T);
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * V;
+    if (i + V <= n) {
+        if constexpr (sizeof(T) == 2) {
+            const u32x4 ua = *reinterpret_cast<const u32x4*>(a + i), ub = *reinterpret_cast<const u32x4*>(b + i),
+                        uy = *reinterpret_cast<const u32x4*>(y + i);
+            u32x4 out;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float r[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t sh = 16 * h;
+                    const float fa = __builtin_bit_cast(float, ((ua[k] >> sh) & 0xffffu) << 16);
+                    const float fb = __builtin_bit_cast(float, ((ub[k] >> sh) & 0xffffu) << 16);
+                    const float fy = __builtin_bit_cast(float, ((uy[k] >> sh) & 0xffffu) << 16);
+                    r[h] = (fy <= 0.f) ? 0.f : fa + fb;
+                }
+                out[k] = pack_bf16x2(r[0], r[1]);
+            }
+            *reinterpret_cast<u32x4*>(dz + i) = out;
+        } else {
+            // float vectors loaded as such (element bit-casts of an integer
+            // vector are what the compiler has mistranslated)
+            const f32x4 fa = *reinterpret_cast<const f32x4*>(a + i), fb = *reinterpret_cast<const f32x4*>(b + i),
+                        fy = *reinterpret_cast<const f32x4*>(y + i);
+            f32x4 out;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) out[k] = (fy[k] <= 0.f) ? 0.f : fa[k] + fb[k];
+            *reinterpret_cast<f32x4*>(dz + i) = out;
+        }
+    } else {
+        for (int64_t j = i; j < n; ++j) {
+            const float fy = Io<T>::ld(y, j);
+            Io<T>::st(dz, j, (fy <= 0.f) ? 0.f : Io<T>::ld(a, j) + Io<T>::ld(b, j));
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -168,6 +213,33 @@ int nott_add(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const voi
     nott::DeviceScope scope(ctx->device);
     return dtype == NOTT_F32 ? run_binary<float>(ctx, n, a, b, dst, Add{}, "add")
                              : run_binary<bf16_t>(ctx, n, a, b, dst, Add{}, "add");
+}
+
+int nott_add_relu_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, const void* a, const void* b, const void* y,
+                      void* dz) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n >= 0, "nott_add_relu_bwd: bad dtype or size");
+    NOTT_REQUIRE(ctx, n == 0 || (a && b && y && dz), "nott_add_relu_bwd: null buffer");
+    if (n == 0) return NOTT_OK;
+    nott::DeviceScope scope(ctx->device);
+    auto go = [&](auto tv) {
+        using T = decltype(tv);
+        const bool vec = ((uintptr_t)a % 16) == 0 && ((uintptr_t)b % 16) == 0 && ((uintptr_t)y % 16) == 0 &&
+                         ((uintptr_t)dz % 16) == 0;
+        if (vec) {
+            constexpr int V = 16 / (int)sizeof(T);
+            const int64_t blocks = nott::ceil_div(nott::ceil_div(n, (int64_t)V), (int64_t)kThreads);
+            hipLaunchKernelGGL((add_relu_bwd_kernel<T>), dim3((unsigned)blocks), dim3(kThreads), 0, ctx->stream,
+                               static_cast<const T*>(a), static_cast<const T*>(b), static_cast<const T*>(y),
+                               static_cast<T*>(dz), n);
+            return nott::launch_status(ctx, "add_relu_bwd");
+        }
+        // unaligned: the two passes (the same values)
+        const int st = run_binary<T>(ctx, n, a, b, dz, Add{}, "add");
+        if (st != NOTT_OK) return st;
+        return run_binary<T>(ctx, n, y, dz, dz, ReluBwd{}, "relu_bwd");
+    };
+    return dtype == NOTT_F32 ? go(float{}) : go(bf16_t{});
 }
 
 int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype st, void* dst, nott_dtype dt) {

@@ -135,8 +135,10 @@ struct ResNet18Impl : torch::nn::Module {
     Tensor forward(Tensor x) {
         x = pool(stem_bn->forward_relu(stem(x)));
         if (record) outputs.push_back(x);
-        for (auto& b : blocks) {
-            x = b(x);
+        // consecutive blocks: the final ReLU's backward of block i runs in
+        // block i + 1's fork, together with the fork's sum
+        for (size_t i = 0; i < blocks.size(); ++i) {
+            x = blocks[i]->forward(x, i > 0, i + 1 < blocks.size());
             if (record) outputs.push_back(x);
         }
         x = fc(flat(gap(x)));

@@ -138,6 +138,16 @@ def add(a: torch.Tensor, b: torch.Tensor, out: Optional[torch.Tensor] = None) ->
     return out
 
 
+def add_relu_bwd(a: torch.Tensor, b: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    """dz = (y <= 0) ? 0 : a + b (the gradient of a ReLU output used twice)."""
+    _check(a, "a")
+    _check(b, "b", shape=tuple(a.shape), dtype=a.dtype, device=a.device)
+    _check(y, "y", shape=tuple(a.shape), dtype=a.dtype, device=a.device)
+    dz = torch.empty_like(a)
+    _ctx_for(a).call("nott_add_relu_bwd", nott_dtype(a.dtype), a.numel(), _ptr(a), _ptr(b), _ptr(y), _ptr(dz))
+    return dz
+
+
 def cast(src: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     _check(src, "src")
     dst = torch.empty(src.shape, dtype=dtype, device=src.device)
