@@ -193,6 +193,16 @@ int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype d
  * then nott_relu_bwd, in one pass where the tiled kernels apply. */
 int nott_maxpool2d_bwd_tap_relu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
                                 const uint8_t* tap, const void* dy, const void* y, void* dx);
+/* The max-pool of a BatchNorm2d + ReLU output (ResNet-18's stem: batchnorm.hpp:50
+ * with its ReLU activation, then pooling.hpp:144) without that output in
+ * memory: the pool reads the BatchNorm's input x and forms relu(a·x + c) per
+ * channel, coef = {a_c, c_c} from nott_batchnorm2d_fwd_coef, as the BatchNorm's
+ * apply pass would store it; y and tap are bit-identical to
+ * nott_batchnorm2d_fwd_act (relu) then nott_maxpool2d_fwd_tap.  Stride-2 3x3
+ * (pad 1) or 2x2 (pad 0) windows on rows of whole 4-element groups only
+ * (NOTT_ERR_UNSUPPORTED otherwise). */
+int nott_maxpool2d_fwd_tap_bnrelu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                                  const void* x, const float* coef, void* y, uint8_t* tap);
 /* y[nc] = mean over hw; dx[nc, i] = dy[nc] / hw. */
 int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
                             const void* x, void* y);
@@ -205,6 +215,14 @@ int nott_avgpool_global_bwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t 
  * x [n, c, hw] NCHW; gamma, beta, mean, rstd, running stats fp32 [c].
  * Forward saves mean and rstd = 1/sqrt(var_biased + eps); running stats are
  * updated with momentum and the unbiased variance (nullable). */
+/* The statistics of the forward alone (mean, rstd, running stats) and the
+ * affine coefficients of its apply pass, y = coef[2c]·x + coef[2c+1] per
+ * channel (fp32 [2c]), for a consumer that applies them itself
+ * (nott_maxpool2d_fwd_tap_bnrelu). */
+int nott_batchnorm2d_fwd_coef(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                              const void* x, const float* gamma, const float* beta, double eps,
+                              double momentum, float* running_mean, float* running_var, float* mean,
+                              float* rstd, float* coef);
 int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
                          const void* x, const float* gamma, const float* beta,
                          double eps, double momentum, float* running_mean, float* running_var,

@@ -626,6 +626,55 @@ struct BatchNorm2dReluFn : torch::autograd::Function<BatchNorm2dReluFn> {
     }
 };
 
+// BatchNorm2d + ReLU followed by a max-pool (ResNet-18's stem: batchnorm.hpp:50
+// with its ReLU, then pooling.hpp:144) without the BatchNorm's output in
+// memory: the statistics pass, then the pool forms relu(a·x + c) from x as
+// it stages its rows (nott_batchnorm2d_fwd_coef, nott_maxpool2d_fwd_tap_bnrelu).
+// Backward: the pool's routing into a [n, c, h, w] gradient, then the
+// BatchNorm + ReLU backward (mask recomputed from x), as the two layers do.
+struct BatchNorm2dReluMaxPool2dFn : torch::autograd::Function<BatchNorm2dReluMaxPool2dFn> {
+    static Tensor forward(AutogradContext* ctx, Tensor x, Tensor gamma, Tensor beta, Tensor running_mean,
+                          Tensor running_var, double eps, double momentum, std::vector<int64_t> pool_geom) {
+        x = contig(x);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        auto fo = x.options().dtype(torch::kFloat32);
+        Tensor mean = torch::empty({ch}, fo), rstd = torch::empty({ch}, fo), coef = torch::empty({2 * ch}, fo);
+        nott_ctx c = bind(x);
+        check(nott_batchnorm2d_fwd_coef(c, dtype_of(x), n, ch, hw, ptr(x), fptr(gamma), fptr(beta), eps, momentum,
+                                        fptr(running_mean), fptr(running_var), fptr(mean), fptr(rstd), fptr(coef)),
+              c, "batchnorm statistics");
+        const nott_pool2d_desc d = MaxPool2dFn::desc(x, pool_geom);
+        const int64_t oh = MaxPool2dFn::out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, d.ceil_mode),
+                      ow = MaxPool2dFn::out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, d.ceil_mode);
+        Tensor y = torch::empty({n, ch, oh, ow}, x.options());
+        Tensor tap = torch::empty({n, ch, oh, ow}, x.options().dtype(torch::kUInt8));
+        check(nott_maxpool2d_fwd_tap_bnrelu(c, &d, dtype_of(x), ptr(x), fptr(coef), ptr(y), tap.data_ptr<uint8_t>()),
+              c, "batchnorm+relu+maxpool forward");
+        ctx->save_for_backward({x, gamma, beta, mean, rstd, tap});
+        ctx->saved_data["geom"] = pool_geom;
+        ctx->saved_data["needs_dx"] = x.requires_grad();
+        ctx->mark_non_differentiable({tap});
+        return y;
+    }
+    static variable_list backward(AutogradContext* ctx, variable_list grads) {
+        auto s = ctx->get_saved_variables();
+        Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4], tap = s[5];
+        Tensor dy = contig(grads[0]);
+        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
+        nott_ctx c = bind(dy);
+        const nott_pool2d_desc d = MaxPool2dFn::desc(x, ctx->saved_data["geom"].toIntVector());
+        Tensor dz = torch::empty(x.sizes(), dy.options());
+        check(nott_maxpool2d_bwd_tap(c, &d, dtype_of(dy), tap.data_ptr<uint8_t>(), ptr(dy), ptr(dz)), c,
+              "maxpool backward");
+        Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
+        Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
+        check(nott_batchnorm2d_bwd_act(c, dtype_of(dz), n, ch, hw, ptr(x), ptr(dz), fptr(mean), fptr(rstd),
+                                       fptr(gamma), fptr(beta), 1, ptr(dx), fptr(gg), fptr(gbt), 1),
+              c, "batchnorm+relu backward");
+        return {dx, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
 // The second BatchNorm2d of a residual branch with the skip addition and the
 // block's final ReLU (residual.hpp:130-132): y = relu(BN(x) + skip) in one
 // apply pass.  Backward: dz = dy·[y > 0] feeds both the BN backward and the
@@ -894,6 +943,15 @@ public:
         if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
         ++batches_;
         return BatchNorm2dReluFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_);
+    }
+    // maxpool(relu(BN(x))) with the pool geometry of a MaxPool2d
+    // (MaxPool2dImpl::geometry()): the BatchNorm's output is never stored.
+    Tensor forward_relu_maxpool(const Tensor& x, const std::vector<int64_t>& pool_geom) {
+        if (!is_training()) throw std::invalid_argument("Nott::HIP::BatchNorm2d: only training mode runs on HIP");
+        if (pool_geom[0] * pool_geom[1] > 256) return MaxPool2dFn::apply(forward_relu(x), pool_geom, false);
+        ++batches_;
+        return BatchNorm2dReluMaxPool2dFn::apply(x, weight, bias, running_mean, running_var, eps_, momentum_,
+                                                 pool_geom);
     }
     // relu(BN(x) + skip): the residual branch's last layer, skip addition and
     // final ReLU, fused.

@@ -212,6 +212,30 @@ def test_add_relu_bwd(ops, dt, n, offset):
     assert torch.equal(dz.view(iv), ref.view(iv))
 
 
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", [(4, 64, 112, 112, 3, 1), (3, 16, 30, 24, 3, 1), (2, 8, 17, 20, 2, 0)])
+def test_batchnorm_relu_maxpool_fused(ops, dt, case):
+    """The stem's BatchNorm + ReLU + max-pool with the BatchNorm's output never
+    stored: pooled values, taps, mean, rstd and running stats bit-identical
+    to the fused-ReLU BatchNorm followed by the pool."""
+    n, c, h, w, k, pd = case
+    g = rng(n * c + h + w)
+    x = dev(host_input(g.standard_normal((n, c, h, w)) * 2 + 0.5, dt), dt)
+    gamma = dev(f32(g.standard_normal(c)))
+    beta = dev(f32(g.standard_normal(c)))
+    d = ops.pool_desc((n, c, h, w), (k, k), (2, 2), (pd, pd), (1, 1), False)
+    rm1, rv1 = torch.zeros(c, device="cuda"), torch.ones(c, device="cuda")
+    rm2, rv2 = rm1.clone(), rv1.clone()
+    yb, m1, r1 = ops.batchnorm2d_fwd(x, gamma, beta, running_mean=rm1, running_var=rv1, relu=True)
+    yp, tap = ops.maxpool2d_fwd_tap(yb, d)
+    y2, tap2, m2, r2 = ops.batchnorm2d_relu_maxpool2d_fwd(x, gamma, beta, d, running_mean=rm2, running_var=rv2)
+    iv = torch.int16 if dt == "bf16" else torch.int32
+    assert torch.equal(yp.view(iv), y2.view(iv))
+    assert torch.equal(tap, tap2)
+    for u, v in ((m1, m2), (r1, r2), (rm1, rm2), (rv1, rv2)):
+        assert torch.equal(u, v)
+
+
 MAXPOOL_GOLDEN = ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil", "maxpool2x2_dil2",
                   "maxpool3x3_s2p1_nan_inf", "maxpool2x2_s2_nan_inf"]
 

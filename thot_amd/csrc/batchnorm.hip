@@ -408,9 +408,12 @@ int64_t pick_splits(int64_t n, int64_t c) {
     return std::max<int64_t>(1, std::min<int64_t>(s, n));
 }
 
+// coef_out (nullable): the per-channel affine coefficients (a, c) of
+// y = a·x + c go there instead of the workspace; yv null: no apply pass.
 template <typename T>
 int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const float* gamma, const float* beta,
-        float eps, float momentum, float* rm, float* rv, void* yv, float* mean, float* rstd, const void* resv, int relu) {
+        float eps, float momentum, float* rm, float* rv, void* yv, float* mean, float* rstd, const void* resv, int relu,
+        float* coef_out = nullptr) {
     const T* x = static_cast<const T*>(xv);
     const T* res = static_cast<const T*>(resv);
     T* y = static_cast<T*>(yv);
@@ -420,7 +423,7 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
     float* ws = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)(2 * c * splits + 2 * c)));
     if (!ws) return NOTT_ERR_ALLOC;
     float* partial = ws;
-    float* coef = ws + 2 * c * splits;
+    float* coef = coef_out ? coef_out : ws + 2 * c * splits;
     const int v = group_width<T>(hw, {xv, yv, resv});
     const dim3 g1((unsigned)c, (unsigned)splits);
     const FastDiv fd_hwg((uint32_t)(hw / v)), fd_c((uint32_t)c);
@@ -432,8 +435,9 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
                            partial);
         hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial, c, splits, hw,
                            n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
-        hipLaunchKernelGGL((bn_affine_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg, fd_c,
-                           coef, res, relu);
+        if (y)
+            hipLaunchKernelGGL((bn_affine_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg,
+                               fd_c, coef, res, relu);
     };
     if constexpr (sizeof(T) == 2) {
         if (v == 8) go(std::integral_constant<int, 8>{});
@@ -496,6 +500,23 @@ extern "C" int nott_batchnorm2d_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t 
                                           running_var, y, mean, rstd, residual, relu != 0)
                              : fwd<bf16_t>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
                                            running_var, y, mean, rstd, residual, relu != 0);
+}
+
+extern "C" int nott_batchnorm2d_fwd_coef(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
+                                         const void* x, const float* gamma, const float* beta, double eps,
+                                         double momentum, float* running_mean, float* running_var, float* mean,
+                                         float* rstd, float* coef) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, nott::valid_dtype(dtype) && n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_fwd_coef: bad shape");
+    NOTT_REQUIRE(ctx, (running_mean == nullptr) == (running_var == nullptr),
+                 "nott_batchnorm2d_fwd_coef: running_mean and running_var go together");
+    NOTT_REQUIRE(ctx, x && mean && rstd && coef, "nott_batchnorm2d_fwd_coef: null buffer");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c * hw <= 0xffffffffll, "nott_batchnorm2d_fwd_coef: tensor too large");
+    nott::DeviceScope scope(ctx->device);
+    return dtype == NOTT_F32 ? fwd<float>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
+                                          running_var, nullptr, mean, rstd, nullptr, 0, coef)
+                             : fwd<bf16_t>(ctx, n, c, hw, x, gamma, beta, (float)eps, (float)momentum, running_mean,
+                                           running_var, nullptr, mean, rstd, nullptr, 0, coef);
 }
 
 extern "C" int nott_batchnorm2d_fwd(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw, const void* x,

@@ -365,7 +365,8 @@ constexpr int kS2Rows = 16;
 template <typename T, int K, int P, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_fwd_s2_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                                   IX* __restrict__ argmax, PoolGeom32 g,
-                                                                  int32_t half_pitch) {
+                                                                  int32_t half_pitch, const float* __restrict__ bn,
+                                                                  int32_t nch) {
     static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "window");
     extern __shared__ float rows[];   // [row][even columns | odd columns], 2·half_pitch floats a row
     const int32_t pl = blockIdx.y;
@@ -374,10 +375,28 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_s2_kernel(const T* __res
     const int32_t ih_hi = min(g.h, 2 * (oh1 - 1) - P + K);   // exclusive
     const T* xp = x + (int64_t)pl * g.h * g.w;
     const int32_t nq = (ih_hi - ih_lo) * (g.w >> 2);
+    // bn: the input is relu(a·x + c) of the BatchNorm before the pool, formed
+    // here as that layer's apply pass forms and stores it (fma, ReLU with NaN
+    // passing, rounding to T), so the window maxima and taps are the same
+    float ba = 0.f, bc = 0.f;
+    if (bn) {
+        const int32_t ch = pl % nch;
+        ba = bn[2 * ch];
+        bc = bn[2 * ch + 1];
+    }
     for (int32_t i = threadIdx.x; i < nq; i += kThreads) {
         uint32_t r, c;
         g.fd_w.divmod((uint32_t)(4 * i), r, c);
-        const f32x4 v = Vec4<T>::ld(xp + (int64_t)(ih_lo + (int32_t)r) * g.w + c);
+        f32x4 v = Vec4<T>::ld(xp + (int64_t)(ih_lo + (int32_t)r) * g.w + c);
+        if (bn) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float z = __builtin_fmaf(v[e], ba, bc);
+                z = (z > 0.f || z != z) ? z : 0.f;
+                if constexpr (sizeof(T) == 2) z = bf16_to_f32(f32_to_bf16(z));
+                v[e] = z;
+            }
+        }
         float* row = rows + r * 2 * half_pitch + (c >> 1);
         *reinterpret_cast<f32x2*>(row) = f32x2{v.x, v.z};
         *reinterpret_cast<f32x2*>(row + half_pitch) = f32x2{v.y, v.w};
@@ -612,9 +631,24 @@ size_t s2_bwd_lds(const PoolGeom& g) {
     return 2 * sizeof(float) * ((size_t)std::min<int64_t>(g.oh, kS2Rows + 2) * g.ow + 4);
 }
 
+// relu(a_c·x + c_c) of a BatchNorm's apply pass, per element (the fallback
+// of the pools that form it while staging).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void bnrelu_apply_kernel(const T* __restrict__ x, const float* __restrict__ coef,
+                                                                int32_t nch, FastDiv fd_hw, T* __restrict__ y,
+                                                                int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t plane = fd_hw.div((uint32_t)i);
+    const int32_t ch = (int32_t)(plane % (uint32_t)nch);
+    float z = __builtin_fmaf(Io<T>::ld(x, i), coef[2 * ch], coef[2 * ch + 1]);
+    z = (z > 0.f || z != z) ? z : 0.f;
+    Io<T>::st(y, i, z);
+}
+
 template <typename IX>
 int maxpool_fwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x, void* y, IX* argmax,
-                     const char* name) {
+                     const char* name, const float* bn = nullptr) {
     NOTT_CHECK_CTX(ctx);
     NOTT_REQUIRE(ctx, nott::valid_dtype(dtype), std::string(name) + ": bad dtype");
     PoolGeom g;
@@ -638,18 +672,36 @@ int maxpool_fwd_impl(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, 
         const dim3 sgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kS2Rows), (unsigned)planes);
         const size_t lds = s2_fwd_lds(g);
         const int32_t hp = s2_half_pitch(g);
+        const int32_t nch = (int32_t)d->c;
         if (g.kh == 3 && dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_fwd_s2_kernel<float, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xf, yf,
-                               argmax, g32, hp);
+                               argmax, g32, hp, bn, nch);
         else if (g.kh == 3)
             hipLaunchKernelGGL((maxpool_fwd_s2_kernel<bf16_t, 3, 1, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xb,
-                               yb, argmax, g32, hp);
+                               yb, argmax, g32, hp, bn, nch);
         else if (dtype == NOTT_F32)
             hipLaunchKernelGGL((maxpool_fwd_s2_kernel<float, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xf, yf,
-                               argmax, g32, hp);
+                               argmax, g32, hp, bn, nch);
         else
             hipLaunchKernelGGL((maxpool_fwd_s2_kernel<bf16_t, 2, 0, IX>), sgrid, dim3(kThreads), lds, ctx->stream, xb,
-                               yb, argmax, g32, hp);
+                               yb, argmax, g32, hp, bn, nch);
+    } else if (bn) {
+        // other geometries: the BatchNorm's output formed in workspace, then
+        // the pool
+        const int64_t nx = planes * g.h * g.w;
+        if (nx >= (int64_t(1) << 32))
+            return nott::fail(ctx, NOTT_ERR_UNSUPPORTED, std::string(name) + ": tensor too large");
+        void* tmp = nott::workspace(ctx, (size_t)nx * (dtype == NOTT_F32 ? 4 : 2));
+        if (!tmp) return NOTT_ERR_ALLOC;
+        const dim3 egrid((unsigned)nott::ceil_div(nx, kThreads));
+        const FastDiv fd_hw((uint32_t)(g.h * g.w));
+        if (dtype == NOTT_F32)
+            hipLaunchKernelGGL((bnrelu_apply_kernel<float>), egrid, dim3(kThreads), 0, ctx->stream, xf, bn,
+                               (int32_t)d->c, fd_hw, static_cast<float*>(tmp), nx);
+        else
+            hipLaunchKernelGGL((bnrelu_apply_kernel<bf16_t>), egrid, dim3(kThreads), 0, ctx->stream, xb, bn,
+                               (int32_t)d->c, fd_hw, static_cast<bf16_t*>(tmp), nx);
+        return maxpool_fwd_impl<IX>(ctx, d, dtype, tmp, y, argmax, name);
     } else if (fits32(planes, g) && flds > 0 && planes <= 65535) {
         const PoolGeom32 g32 = geom32(g);
         const dim3 tgrid((unsigned)nott::ceil_div(g.oh, (int64_t)kPoolRows), (unsigned)planes);
@@ -778,6 +830,13 @@ extern "C" int nott_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_
 extern "C" int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x,
                                       void* y, uint8_t* tap) {
     return maxpool_fwd_impl<uint8_t>(ctx, d, dtype, x, y, tap, "nott_maxpool2d_fwd_tap");
+}
+
+extern "C" int nott_maxpool2d_fwd_tap_bnrelu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x,
+                                             const float* coef, void* y, uint8_t* tap) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, coef != nullptr, "nott_maxpool2d_fwd_tap_bnrelu: null coef");
+    return maxpool_fwd_impl<uint8_t>(ctx, d, dtype, x, y, tap, "nott_maxpool2d_fwd_tap_bnrelu", coef);
 }
 
 extern "C" int nott_maxpool2d_bwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,

@@ -133,7 +133,8 @@ struct ResNet18Impl : torch::nn::Module {
         return mods;
     }
     Tensor forward(Tensor x) {
-        x = pool(stem_bn->forward_relu(stem(x)));
+        // BatchNorm + ReLU + max-pool with the BatchNorm's output never stored
+        x = stem_bn->forward_relu_maxpool(stem(x), pool->geometry());
         if (record) outputs.push_back(x);
         // consecutive blocks: the final ReLU's backward of block i runs in
         // block i + 1's fork, together with the fork's sum

@@ -326,6 +326,29 @@ def maxpool2d_fwd_tap(x: torch.Tensor, d: Pool2dDesc):
     return y, tap
 
 
+def batchnorm2d_relu_maxpool2d_fwd(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, d: Pool2dDesc,
+                                   eps: float = 1e-5, momentum: float = 0.1,
+                                   running_mean: Optional[torch.Tensor] = None,
+                                   running_var: Optional[torch.Tensor] = None):
+    """maxpool(relu(BN(x))) without the BatchNorm's output in memory
+    (nott_batchnorm2d_fwd_coef, then nott_maxpool2d_fwd_tap_bnrelu):
+    returns (y, tap, mean, rstd)."""
+    _check(x, "x")
+    n, c, h, w = x.shape
+    mean = torch.empty(c, dtype=torch.float32, device=x.device)
+    rstd = torch.empty(c, dtype=torch.float32, device=x.device)
+    coef = torch.empty(2 * c, dtype=torch.float32, device=x.device)
+    ctx = _ctx_for(x)
+    ctx.call("nott_batchnorm2d_fwd_coef", nott_dtype(x.dtype), n, c, h * w, _ptr(x), _ptr(gamma), _ptr(beta),
+             float(eps), float(momentum), _ptr(running_mean), _ptr(running_var), _ptr(mean), _ptr(rstd), _ptr(coef))
+    oh = pool_out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, bool(d.ceil_mode))
+    ow = pool_out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, bool(d.ceil_mode))
+    y = torch.empty((n, c, oh, ow), dtype=x.dtype, device=x.device)
+    tap = torch.empty((n, c, oh, ow), dtype=torch.uint8, device=x.device)
+    ctx.call("nott_maxpool2d_fwd_tap_bnrelu", C.byref(d), nott_dtype(x.dtype), _ptr(x), _ptr(coef), _ptr(y), _ptr(tap))
+    return y, tap, mean, rstd
+
+
 def maxpool2d_bwd_tap(tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc,
                       relu_y: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dx of the pool; with relu_y (the pool's input, a ReLU output) also the
