@@ -203,6 +203,20 @@ int nott_maxpool2d_bwd_tap_relu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dt
  * (NOTT_ERR_UNSUPPORTED otherwise). */
 int nott_maxpool2d_fwd_tap_bnrelu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
                                   const void* x, const float* coef, void* y, uint8_t* tap);
+/* Its backward (the BatchNorm2d + ReLU backward of batchnorm.hpp:50 taking the
+ * max-pool backward of pooling.hpp:144 as its dy): dx, dgamma and dbeta of
+ * nott_maxpool2d_bwd_tap then nott_batchnorm2d_bwd_act (relu), d the pool's
+ * descriptor (x [n, c, h, w] the BatchNorm's input, tap and dy the pooled
+ * shape).  On the stride-2 shapes of nott_maxpool2d_fwd_tap_bnrelu the routed
+ * gradient is never stored: the BatchNorm's sums run over the pooled outputs
+ * and the routing carries the apply, so results agree with the two calls to
+ * rounding (each routed term enters the sums unrounded); other shapes run the
+ * two calls.  dx nullable (dgamma, dbeta only); accumulate adds into them. */
+int nott_batchnorm2d_relu_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                                        const void* x, const uint8_t* tap, const void* dy,
+                                        const float* mean, const float* rstd, const float* gamma,
+                                        const float* beta, void* dx, float* dgamma, float* dbeta,
+                                        int accumulate);
 /* y[nc] = mean over hw; dx[nc, i] = dy[nc] / hw. */
 int nott_avgpool_global_fwd(nott_ctx ctx, nott_dtype dtype, int64_t nc, int64_t hw,
                             const void* x, void* y);

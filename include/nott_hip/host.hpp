@@ -660,17 +660,14 @@ struct BatchNorm2dReluMaxPool2dFn : torch::autograd::Function<BatchNorm2dReluMax
         auto s = ctx->get_saved_variables();
         Tensor x = s[0], gamma = s[1], beta = s[2], mean = s[3], rstd = s[4], tap = s[5];
         Tensor dy = contig(grads[0]);
-        const int64_t n = x.size(0), ch = x.size(1), hw = x.size(2) * x.size(3);
         nott_ctx c = bind(dy);
         const nott_pool2d_desc d = MaxPool2dFn::desc(x, ctx->saved_data["geom"].toIntVector());
-        Tensor dz = torch::empty(x.sizes(), dy.options());
-        check(nott_maxpool2d_bwd_tap(c, &d, dtype_of(dy), tap.data_ptr<uint8_t>(), ptr(dy), ptr(dz)), c,
-              "maxpool backward");
         Tensor dx = ctx->saved_data["needs_dx"].toBool() ? torch::empty_like(x) : Tensor();
         Tensor gg = grad_buffer(gamma), gbt = grad_buffer(beta);
-        check(nott_batchnorm2d_bwd_act(c, dtype_of(dz), n, ch, hw, ptr(x), ptr(dz), fptr(mean), fptr(rstd),
-                                       fptr(gamma), fptr(beta), 1, ptr(dx), fptr(gg), fptr(gbt), 1),
-              c, "batchnorm+relu backward");
+        check(nott_batchnorm2d_relu_maxpool2d_bwd(c, &d, dtype_of(dy), ptr(x), tap.data_ptr<uint8_t>(), ptr(dy),
+                                                  fptr(mean), fptr(rstd), fptr(gamma), fptr(beta), ptr(dx), fptr(gg),
+                                                  fptr(gbt), 1),
+              c, "batchnorm+relu+maxpool backward");
         return {dx, Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };

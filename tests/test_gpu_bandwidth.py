@@ -236,6 +236,52 @@ def test_batchnorm_relu_maxpool_fused(ops, dt, case):
         assert torch.equal(u, v)
 
 
+@pytest.mark.parametrize("dt", DTYPES)
+@pytest.mark.parametrize("case", [(4, 64, 112, 112, 3, 1), (3, 16, 30, 24, 3, 1), (5, 8, 12, 16, 2, 0),
+                                  (2, 8, 17, 20, 2, 0)])
+def test_batchnorm_relu_maxpool_bwd_fused(ops, dt, case):
+    """The stem's backward with the routed gradient never stored, against the
+    pool's backward followed by the BatchNorm + ReLU backward.  The fused
+    sums take each routed term before it is rounded, so dγ and dβ agree to
+    2^-7 (bf16) or 1e-5 (fp32) of Σ|term| and dx to the same fraction of its
+    largest magnitude; shapes outside the stride-2 kernels (the last case:
+    10-wide output rows) run the two calls and match bit for bit."""
+    n, c, h, w, k, pd = case
+    g = rng(n * c + h + w + 7)
+    x = dev(host_input(g.standard_normal((n, c, h, w)) * 2 + 0.5, dt), dt)
+    gamma = dev(f32(g.standard_normal(c)))
+    beta = dev(f32(g.standard_normal(c)))
+    d = ops.pool_desc((n, c, h, w), (k, k), (2, 2), (pd, pd), (1, 1), False)
+    y, tap, mean, rstd = ops.batchnorm2d_relu_maxpool2d_fwd(x, gamma, beta, d)
+    dy = dev(host_input(g.standard_normal(tuple(y.shape)), dt), dt)
+    dz = ops.maxpool2d_bwd_tap(tap, dy, d)
+    dx1, dg1, db1 = ops.batchnorm2d_bwd(x, dz, mean, rstd, gamma, beta=beta, relu=True)
+    dx2, dg2, db2 = ops.batchnorm2d_relu_maxpool2d_bwd(x, tap, dy, d, mean, rstd, gamma, beta)
+    _, dg3, db3 = ops.batchnorm2d_relu_maxpool2d_bwd(x, tap, dy, d, mean, rstd, gamma, beta, need_dx=False)
+    assert torch.equal(dg2, dg3) and torch.equal(db2, db3)
+    fused = (w % 4 == 0) and ((w + 2 * pd - k) // 2 + 1) % 4 == 0
+    if not fused:
+        iv = torch.int16 if dt == "bf16" else torch.int32
+        assert torch.equal(dx1.view(iv), dx2.view(iv))
+        assert torch.equal(dg1, dg2) and torch.equal(db1, db2)
+    else:
+        tol = 2.0 ** -7 if dt == "bf16" else 1e-5
+        gz = dz.float() * ((x.float() * (gamma * rstd).view(1, c, 1, 1)
+                            + (beta - mean * gamma * rstd).view(1, c, 1, 1)) > 0)
+        xh = (x.float() - mean.view(1, c, 1, 1)) * rstd.view(1, c, 1, 1)
+        sb = gz.abs().sum((0, 2, 3))
+        sg = (gz * xh).abs().sum((0, 2, 3))
+        assert ((db1 - db2).abs() <= tol * sb + 1e-6).all()
+        assert ((dg1 - dg2).abs() <= tol * sg + 1e-6).all()
+        scale = dx1.float().abs().max()
+        assert ((dx1.float() - dx2.float()).abs() <= tol * scale).all()
+    # accumulate adds into the given buffers
+    dg4, db4 = dg2.clone(), db2.clone()
+    ops.batchnorm2d_relu_maxpool2d_bwd(x, tap, dy, d, mean, rstd, gamma, beta, dgamma=dg4, dbeta=db4, accumulate=True)
+    torch.testing.assert_close(dg4, 2 * dg2, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(db4, 2 * db2, rtol=1e-6, atol=1e-6)
+
+
 MAXPOOL_GOLDEN = ["maxpool2x2_s2_relu_ties", "maxpool3x3_s2p1_overlap", "maxpool3x3_s2_ceil", "maxpool2x2_dil2",
                   "maxpool3x3_s2p1_nan_inf", "maxpool2x2_s2_nan_inf"]
 

@@ -80,6 +80,8 @@ SIGNATURES: dict[str, list] = {
     "nott_maxpool2d_bwd_tap": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp],
     "nott_maxpool2d_bwd_tap_relu": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp, vp],
     "nott_maxpool2d_fwd_tap_bnrelu": [vp, C.POINTER(Pool2dDesc), i32, vp, fp, vp, vp],
+    "nott_batchnorm2d_relu_maxpool2d_bwd": [vp, C.POINTER(Pool2dDesc), i32, vp, vp, vp, fp, fp, fp, fp, vp, fp, fp,
+                                            i32],
     "nott_avgpool_global_fwd": [vp, i32, i64, i64, vp, vp],
     "nott_avgpool_global_bwd": [vp, i32, i64, i64, vp, vp],
     "nott_batchnorm2d_fwd": [vp, i32, i64, i64, i64, vp, fp, fp, f64, f64, fp, fp, vp, fp, fp],

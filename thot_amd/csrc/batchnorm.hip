@@ -448,15 +448,19 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
 }
 
 template <typename T>
+// ws_ext (nullable): (2·c·splits + 3·c) floats to use instead of the context
+// workspace.
 int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const void* dyv, const float* mean,
-        const float* rstd, const float* gamma, void* dxv, float* dgamma, float* dbeta, int accumulate, BnAct act) {
+        const float* rstd, const float* gamma, void* dxv, float* dgamma, float* dbeta, int accumulate, BnAct act,
+        float* ws_ext = nullptr) {
     const T* x = static_cast<const T*>(xv);
     const T* dy = static_cast<const T*>(dyv);
     T* dx = static_cast<T*>(dxv);
     const int64_t splits0 = pick_splits(n, c);
     const int64_t per = nott::ceil_div(n, splits0);
     const int64_t splits = nott::ceil_div(n, per);
-    float* ws = static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)(2 * c * splits + 3 * c)));
+    float* ws = ws_ext ? ws_ext
+                       : static_cast<float*>(nott::workspace(ctx, sizeof(float) * (size_t)(2 * c * splits + 3 * c)));
     if (!ws) return NOTT_ERR_ALLOC;
     float* partial = ws;
     float* coef = ws + 2 * c * splits;
@@ -484,6 +488,18 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
 }
 
 }  // namespace
+
+namespace nott {
+bool maxpool_bnrelu_bwd_applies(const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap, const void* dy,
+                                const void* x, const void* dx);
+int maxpool_bwd_tap_bnrelu_reduce(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
+                                  const void* dy, const void* x, const float* gamma, const float* beta,
+                                  const float* mean, const float* rstd, int32_t per_split, int32_t splits,
+                                  float* partial);
+int maxpool_bwd_tap_bnrelu_apply(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
+                                 const void* dy, const void* x, const float* abc, const float* gamma,
+                                 const float* beta, const float* mean, const float* rstd, void* dx);
+}  // namespace nott
 
 extern "C" int nott_batchnorm2d_fwd_act(nott_ctx ctx, nott_dtype dtype, int64_t n, int64_t c, int64_t hw,
                                         const void* x, const float* gamma, const float* beta, double eps,
@@ -545,4 +561,53 @@ extern "C" int nott_batchnorm2d_bwd(nott_ctx ctx, nott_dtype dtype, int64_t n, i
                                     float* dgamma, float* dbeta, int accumulate) {
     return nott_batchnorm2d_bwd_act(ctx, dtype, n, c, hw, x, dy, mean, rstd, gamma, nullptr, 0, dx, dgamma, dbeta,
                                     accumulate);
+}
+
+extern "C" int nott_batchnorm2d_relu_maxpool2d_bwd(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype,
+                                                   const void* x, const uint8_t* tap, const void* dy,
+                                                   const float* mean, const float* rstd, const float* gamma,
+                                                   const float* beta, void* dx, float* dgamma, float* dbeta,
+                                                   int accumulate) {
+    NOTT_CHECK_CTX(ctx);
+    NOTT_REQUIRE(ctx, d != nullptr && nott::valid_dtype(dtype), "nott_batchnorm2d_relu_maxpool2d_bwd: bad descriptor");
+    NOTT_REQUIRE(ctx, x && tap && dy && mean && rstd, "nott_batchnorm2d_relu_maxpool2d_bwd: null buffer");
+    const int64_t n = d->n, c = d->c, hw = d->h * d->w;
+    NOTT_REQUIRE(ctx, n > 0 && c > 0 && hw > 0, "nott_batchnorm2d_relu_maxpool2d_bwd: bad shape");
+    NOTT_REQUIRE(ctx, c <= 65535 && n * c * hw <= 0xffffffffll, "nott_batchnorm2d_relu_maxpool2d_bwd: tensor too large");
+    nott::DeviceScope scope(ctx->device);
+    const int64_t splits0 = pick_splits(n, c);
+    const int64_t per = nott::ceil_div(n, splits0);
+    const int64_t splits = nott::ceil_div(n, per);
+    const size_t bn_bytes = sizeof(float) * (size_t)(2 * c * splits + 3 * c);
+    if (nott::maxpool_bnrelu_bwd_applies(d, dtype, tap, dy, x, dx ? dx : x)) {
+        // the partial sums over the pooled outputs, the coefficients, then the
+        // routing with the apply in its epilogue: the routed gradient is never
+        // stored
+        float* ws = static_cast<float*>(nott::workspace(ctx, bn_bytes));
+        if (!ws) return NOTT_ERR_ALLOC;
+        float* partial = ws;
+        float* coef = ws + 2 * c * splits;
+        int st = nott::maxpool_bwd_tap_bnrelu_reduce(ctx, d, dtype, tap, dy, x, gamma, beta, mean, rstd, (int32_t)per,
+                                                     (int32_t)splits, partial);
+        if (st != NOTT_OK) return st;
+        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c, splits, n * hw,
+                           mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
+        st = nott::launch_status(ctx, "batchnorm_bwd_finalize");
+        if (st != NOTT_OK || !dx) return st;
+        return nott::maxpool_bwd_tap_bnrelu_apply(ctx, d, dtype, tap, dy, x, coef, gamma, beta, mean, rstd, dx);
+    }
+    // other shapes: the routed gradient into dx (a workspace plane when dx is
+    // null), then the BatchNorm + ReLU backward in place (each element is read
+    // before the same thread writes it)
+    const size_t zbytes = dx ? 0 : ((size_t)(n * c * hw) * (dtype == NOTT_F32 ? 4 : 2) + 255) / 256 * 256;
+    char* ws = static_cast<char*>(nott::workspace(ctx, zbytes + bn_bytes));
+    if (!ws) return NOTT_ERR_ALLOC;
+    void* dz = dx ? dx : static_cast<void*>(ws);
+    int st = nott_maxpool2d_bwd_tap(ctx, d, dtype, tap, dy, dz);
+    if (st != NOTT_OK) return st;
+    const BnAct act{1, gamma, beta, rstd};
+    float* bws = reinterpret_cast<float*>(ws + zbytes);
+    return dtype == NOTT_F32
+               ? bwd<float>(ctx, n, c, hw, x, dz, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, act, bws)
+               : bwd<bf16_t>(ctx, n, c, hw, x, dz, mean, rstd, gamma, dx, dgamma, dbeta, accumulate, act, bws);
 }

@@ -465,14 +465,45 @@ __global__ __launch_bounds__(kThreads) void maxpool_fwd_s2_kernel(const T* __res
 // right edge) of output rows ceil((ih+P−K+1)/2) .. floor((ih+P)/2); a thread
 // reads those as short runs and adds the matching dy in (oh, ow) order, the
 // generic kernels' order, so the sums are the same bit for bit.
+// The forward's z = a·x + c coefficients of a BatchNorm (a = γ·rstd,
+// c = β − μ·a, unfused), from which its ReLU mask is recomputed.
+__device__ __forceinline__ f32x2 bn_mask_coef(float g, float b, float mu, float rs) {
+#pragma clang fp contract(off)
+    const float a = g * rs;
+    return f32x2{a, b - mu * a};
+}
+
+// The backward apply of a BatchNorm + ReLU whose output the pool took
+// (x: the BatchNorm's input; abc: dx = A·g + B·x + C per channel from the
+// BatchNorm backward's finalize; gamma, beta, mean, rstd: the ReLU mask's
+// z = a·x + c, as the forward formed it).  x null: no epilogue.
+template <typename T>
+struct BnBwdEpi {
+    const T* x;
+    const float* abc;
+    const float* gamma;
+    const float* beta;
+    const float* mean;
+    const float* rstd;
+    int32_t nch;
+};
+
 template <typename T, int K, int P, typename IX>
 __global__ __launch_bounds__(kThreads) void maxpool_bwd_s2_kernel(const IX* __restrict__ argmax,
                                                                   const T* __restrict__ dy, T* __restrict__ dx,
-                                                                  const T* __restrict__ ry, PoolGeom32 g) {
+                                                                  const T* __restrict__ ry, PoolGeom32 g,
+                                                                  BnBwdEpi<T> epi = BnBwdEpi<T>{}) {
     static_assert((K == 3 && P == 1) || (K == 2 && P == 0), "window");
     constexpr int NC = K;   // candidate output columns of a 4-input group: 2q .. 2q + K − 1 (K ≤ 3)
     extern __shared__ char sm[];
     const int32_t pl = blockIdx.y;
+    f32x4 eabc = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x2 ez = f32x2{0.f, 0.f};
+    if (epi.x) {
+        const int32_t ch = pl % epi.nch;
+        eabc = f32x4{epi.abc[3 * ch], epi.abc[3 * ch + 1], epi.abc[3 * ch + 2], 0.f};
+        ez = bn_mask_coef(epi.gamma ? epi.gamma[ch] : 1.f, epi.beta ? epi.beta[ch] : 0.f, epi.mean[ch], epi.rstd[ch]);
+    }
     const int32_t ih_lo = blockIdx.x * 2 * kS2Rows, ih_hi = min(ih_lo + 2 * kS2Rows, g.h);
     const int32_t oh_lo = max(0, (ih_lo + P - K + 2) >> 1);          // ceil((ih_lo + P − K + 1) / 2)
     const int32_t oh_hi = min(g.oh - 1, (ih_hi - 1 + P) >> 1);       // floor((ih_hi − 1 + P) / 2)
@@ -534,7 +565,67 @@ __global__ __launch_bounds__(kThreads) void maxpool_bwd_s2_kernel(const IX* __re
         const int64_t di = (int64_t)pl * g.h * g.w + (int64_t)ih * g.w + iw0;
         f32x4 out = f32x4{acc[0], acc[1], acc[2], acc[3]};
         if (ry) relu_mask<T, 4>(ry + di, out);
+        if (epi.x) {
+            // the routed gradient as the pool's backward would store it, then
+            // the BatchNorm + ReLU backward's apply
+            const f32x4 xv = Vec4<T>::ld(epi.x + di);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float gr = out[e];
+                if constexpr (sizeof(T) == 2) gr = bf16_to_f32(f32_to_bf16(gr));
+                if (__builtin_fmaf(xv[e], ez.x, ez.y) <= 0.f) gr = 0.f;
+                out[e] = eabc.x * gr + eabc.y * xv[e] + eabc.z;
+            }
+        }
         Vec4<T>::st(dx + di, out);
+    }
+}
+
+// The BatchNorm backward's partial sums Σ g and Σ g·(x − μ) over the gradient
+// the pool's backward routes into a BatchNorm + ReLU output, taken over the
+// pooled outputs instead of the routed plane: each output's dy goes to the
+// input its tap names, masked where the BatchNorm's z = a·x + c <= 0.  Grid
+// (channel, split), images [y·per_split, ..) of the split; each thread takes
+// groups of 4 outputs of a row in a fixed order, then a fixed block tree, so
+// the sums do not depend on timing.  Layout of the partials as the BatchNorm
+// backward's reduce: partial[(ch·splits + split)·2 + {0, 1}].
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool_bwd_bn_reduce_kernel(const uint8_t* __restrict__ tap,
+                                                                         const T* __restrict__ dy, PoolGeom32 g,
+                                                                         BnBwdEpi<T> bn, int32_t n, int32_t per_split,
+                                                                         FastDiv fd_pg, FastDiv fd_q,
+                                                                         float* __restrict__ partial) {
+    __shared__ float red[kThreads / 64];
+    const int32_t ch = blockIdx.x;
+    const int32_t n0 = (int32_t)blockIdx.y * per_split, n1 = min(n, n0 + per_split);
+    const float mu = bn.mean[ch];
+    const f32x2 z = bn_mask_coef(bn.gamma ? bn.gamma[ch] : 1.f, bn.beta ? bn.beta[ch] : 0.f, mu, bn.rstd[ch]);
+    const int32_t oplane = g.oh * g.ow, iplane = g.h * g.w;
+    const uint32_t items = (uint32_t)(n1 - n0) * (uint32_t)(oplane / 4);
+    float s1 = 0.f, s2 = 0.f;
+    for (uint32_t k = threadIdx.x; k < items; k += kThreads) {
+        uint32_t i, j, r, q;
+        fd_pg.divmod(k, i, j);
+        fd_q.divmod(j, r, q);
+        const int32_t pl = (n0 + (int32_t)i) * bn.nch + ch;
+        const int32_t o = pl * oplane + 4 * (int32_t)j;   // row r, columns 4q .. 4q + 3
+        const uint32_t t4 = *reinterpret_cast<const uint32_t*>(tap + o);
+        const f32x4 gv = Vec4<T>::ld(dy + o);
+        const T* xp = bn.x + (int64_t)pl * iplane;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int32_t p = decode_ix<int32_t>((uint8_t)(t4 >> (8 * e)), (int32_t)r, 4 * (int32_t)q + e, g);
+            const float xv = Io<T>::ld(xp, p);
+            const float gg = __builtin_fmaf(xv, z.x, z.y) <= 0.f ? 0.f : gv[e];
+            s1 += gg;
+            s2 += gg * (xv - mu);
+        }
+    }
+    s1 = block_sum<kThreads / 64>(s1, red);
+    s2 = block_sum<kThreads / 64>(s2, red);
+    if (threadIdx.x == 0) {
+        partial[((int64_t)ch * gridDim.y + blockIdx.y) * 2 + 0] = s1;
+        partial[((int64_t)ch * gridDim.y + blockIdx.y) * 2 + 1] = s2;
     }
 }
 
@@ -831,6 +922,73 @@ extern "C" int nott_maxpool2d_fwd_tap(nott_ctx ctx, const nott_pool2d_desc* d, n
                                       void* y, uint8_t* tap) {
     return maxpool_fwd_impl<uint8_t>(ctx, d, dtype, x, y, tap, "nott_maxpool2d_fwd_tap");
 }
+
+namespace nott {
+// Whether the fused backward of a BatchNorm + ReLU + max-pool (the two
+// functions below) takes this shape: stride-2 tap geometries on rows of whole
+// 4-element groups, every buffer aligned for them.
+bool maxpool_bnrelu_bwd_applies(const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap, const void* dy,
+                                const void* x, const void* dx) {
+    PoolGeom g;
+    if (check_desc(nullptr, d, &g) != NOTT_OK) return false;
+    const int64_t planes = d->n * d->c;
+    return planes > 0 && fits32(planes, g) && planes <= 65535 && s2_geom(g) && vec4_ok(g, dtype, {dy, dx, x}) &&
+           ((uintptr_t)tap % 4) == 0 && s2_bwd_lds(g) <= kPoolLdsMax;
+}
+
+// Its first pass: the BatchNorm backward's split partial sums, over the
+// pooled outputs (images [s·per_split, ..) in split s of `splits`).
+int maxpool_bwd_tap_bnrelu_reduce(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
+                                  const void* dy, const void* x, const float* gamma, const float* beta,
+                                  const float* mean, const float* rstd, int32_t per_split, int32_t splits,
+                                  float* partial) {
+    PoolGeom g;
+    int st = check_desc(ctx, d, &g);
+    if (st != NOTT_OK) return st;
+    nott::DeviceScope scope(ctx->device);
+    const PoolGeom32 g32 = geom32(g);
+    const FastDiv fd_pg((uint32_t)(g.oh * g.ow / 4)), fd_q((uint32_t)(g.ow / 4));
+    const dim3 grid((unsigned)d->c, (unsigned)splits);
+    auto go = [&](auto tv) {
+        using T = decltype(tv);
+        const BnBwdEpi<T> bn{static_cast<const T*>(x), nullptr, gamma, beta, mean, rstd, (int32_t)d->c};
+        hipLaunchKernelGGL(maxpool_bwd_bn_reduce_kernel<T>, grid, dim3(kThreads), 0, ctx->stream, tap,
+                           static_cast<const T*>(dy), g32, bn, (int32_t)d->n, per_split, fd_pg, fd_q, partial);
+    };
+    if (dtype == NOTT_F32) go(float{});
+    else go(bf16_t{});
+    return nott::launch_status(ctx, "maxpool_bwd_bn_reduce");
+}
+
+// Its last pass: the max-pool backward with the BatchNorm + ReLU backward's
+// apply in its epilogue (abc: dx = A·g + B·x + C per channel).
+int maxpool_bwd_tap_bnrelu_apply(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const uint8_t* tap,
+                                 const void* dy, const void* x, const float* abc, const float* gamma,
+                                 const float* beta, const float* mean, const float* rstd, void* dx) {
+    PoolGeom g;
+    int st = check_desc(ctx, d, &g);
+    if (st != NOTT_OK) return st;
+    nott::DeviceScope scope(ctx->device);
+    const PoolGeom32 g32 = geom32(g);
+    const dim3 sgrid((unsigned)nott::ceil_div(g.h, (int64_t)(2 * kS2Rows)), (unsigned)(d->n * d->c));
+    const size_t lds = s2_bwd_lds(g);
+    auto go = [&](auto tv, auto kt) {
+        using T = decltype(tv);
+        constexpr int K = decltype(kt)::value, P = K == 3 ? 1 : 0;
+        const BnBwdEpi<T> epi{static_cast<const T*>(x), abc, gamma, beta, mean, rstd, (int32_t)d->c};
+        hipLaunchKernelGGL((maxpool_bwd_s2_kernel<T, K, P, uint8_t>), sgrid, dim3(kThreads), lds, ctx->stream, tap,
+                           static_cast<const T*>(dy), static_cast<T*>(dx), nullptr, g32, epi);
+    };
+    if (dtype == NOTT_F32) {
+        if (g.kh == 3) go(float{}, std::integral_constant<int, 3>{});
+        else go(float{}, std::integral_constant<int, 2>{});
+    } else {
+        if (g.kh == 3) go(bf16_t{}, std::integral_constant<int, 3>{});
+        else go(bf16_t{}, std::integral_constant<int, 2>{});
+    }
+    return nott::launch_status(ctx, "maxpool_bwd_bnrelu_apply");
+}
+}  // namespace nott
 
 extern "C" int nott_maxpool2d_fwd_tap_bnrelu(nott_ctx ctx, const nott_pool2d_desc* d, nott_dtype dtype, const void* x,
                                              const float* coef, void* y, uint8_t* tap) {

@@ -349,6 +349,33 @@ def batchnorm2d_relu_maxpool2d_fwd(x: torch.Tensor, gamma: torch.Tensor, beta: t
     return y, tap, mean, rstd
 
 
+def batchnorm2d_relu_maxpool2d_bwd(x: torch.Tensor, tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc,
+                                   mean: torch.Tensor, rstd: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor,
+                                   dgamma: Optional[torch.Tensor] = None, dbeta: Optional[torch.Tensor] = None,
+                                   accumulate: bool = False, need_dx: bool = True):
+    """Backward of batchnorm2d_relu_maxpool2d_fwd: (dx, dgamma, dbeta)
+    (nott_batchnorm2d_relu_maxpool2d_bwd; dx None when need_dx is False)."""
+    _check(x, "x")
+    n, c, h, w = x.shape
+    if (d.n, d.c, d.h, d.w) != (n, c, h, w):
+        raise ValueError("descriptor does not match x")
+    oh = pool_out(d.h, d.kh, d.stride_h, d.pad_h, d.dil_h, bool(d.ceil_mode))
+    ow = pool_out(d.w, d.kw, d.stride_w, d.pad_w, d.dil_w, bool(d.ceil_mode))
+    _check(dy, "dy", shape=(n, c, oh, ow), dtype=x.dtype, device=x.device)
+    _check(tap, "tap", shape=(n, c, oh, ow), dtype=torch.uint8, device=x.device)
+    for t, nm in ((mean, "mean"), (rstd, "rstd"), (gamma, "gamma"), (beta, "beta")):
+        _check(t, nm, shape=(c,), dtype=torch.float32, device=x.device)
+    dx = torch.empty_like(x) if need_dx else None
+    dgamma = torch.empty(c, dtype=torch.float32, device=x.device) if dgamma is None else dgamma
+    dbeta = torch.empty(c, dtype=torch.float32, device=x.device) if dbeta is None else dbeta
+    _check(dgamma, "dgamma", shape=(c,), dtype=torch.float32, device=x.device)
+    _check(dbeta, "dbeta", shape=(c,), dtype=torch.float32, device=x.device)
+    _ctx_for(x).call("nott_batchnorm2d_relu_maxpool2d_bwd", C.byref(d), nott_dtype(x.dtype), _ptr(x), _ptr(tap),
+                     _ptr(dy), _ptr(mean), _ptr(rstd), _ptr(gamma), _ptr(beta), _ptr(dx), _ptr(dgamma),
+                     _ptr(dbeta), int(accumulate))
+    return dx, dgamma, dbeta
+
+
 def maxpool2d_bwd_tap(tap: torch.Tensor, dy: torch.Tensor, d: Pool2dDesc,
                       relu_y: Optional[torch.Tensor] = None) -> torch.Tensor:
     """dx of the pool; with relu_y (the pool's input, a ReLU output) also the
