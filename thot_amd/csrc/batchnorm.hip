@@ -72,6 +72,43 @@ __device__ __forceinline__ void st_grp(T* __restrict__ p, const float (&o)[V]) {
                                             pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7])};
     }
 }
+// A group as loaded, for the reductions that keep several groups in flight:
+// bf16 groups of 4 or 8 stay packed (2 per dword) until they are added, which
+// halves the registers a batch holds; other groups are floats.
+template <typename T, int V>
+struct RawGrp {
+    static constexpr bool kPacked = sizeof(T) == 2 && V >= 4;
+    uint32_t w[kPacked ? V / 2 : 1];
+    float f[kPacked ? 1 : V];
+};
+template <typename T, int V>
+__device__ __forceinline__ void ld_raw(const T* __restrict__ p, RawGrp<T, V>& r) {
+    if constexpr (RawGrp<T, V>::kPacked) {
+        if constexpr (V == 8) {
+            const u32x4 u = *reinterpret_cast<const u32x4*>(p);
+            r.w[0] = u.x; r.w[1] = u.y; r.w[2] = u.z; r.w[3] = u.w;
+        } else {
+            const u32x2 u = *reinterpret_cast<const u32x2*>(p);
+            r.w[0] = u.x; r.w[1] = u.y;
+        }
+    } else {
+        ld_grp<T, V>(p, r.f);
+    }
+}
+template <typename T, int V>
+__device__ __forceinline__ void unpack(const RawGrp<T, V>& r, float (&o)[V]) {
+    if constexpr (RawGrp<T, V>::kPacked) {
+#pragma unroll
+        for (int k = 0; k < V / 2; ++k) {
+            o[2 * k] = __builtin_bit_cast(float, r.w[k] << 16);
+            o[2 * k + 1] = __builtin_bit_cast(float, r.w[k] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = r.f[e];
+    }
+}
+
 // Σ of a group in a fixed pairwise order.
 template <int V>
 __device__ __forceinline__ float grp_sum(const float (&o)[V]) {
@@ -85,6 +122,7 @@ __device__ __forceinline__ float grp_sum(const float (&o)[V]) {
 // kUnroll of them loaded before they are added (in item order), so the
 // summation order is fixed and several loads are in flight per thread.
 constexpr int kUnroll = 4;
+constexpr int kUnrollB = 2;   // the backward's two tensors: half the items
 
 // Partial sums of (x − pivot) and (x − pivot)² over planes [n0, n1) of
 // channel blockIdx.x.  pivot = x[0, c, 0] keeps the variance well conditioned.
@@ -92,6 +130,7 @@ constexpr int kUnroll = 4;
 // (above); smaller ones give a thread one group per image: its loads for up
 // to kAhead images are issued before the adds, which run in the same order.
 constexpr int kAhead = 8;
+constexpr int kAheadB = 2;   // the backward's two tensors: half the images
 template <typename T, int V>
 __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict__ x, int64_t n, int64_t c, int64_t hw,
                                                             int64_t per_split, FastDiv fd_hwg,
@@ -121,11 +160,15 @@ __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict_
         };
         uint32_t k = threadIdx.x;
         for (; k + (kUnroll - 1) * kThreads < items; k += kUnroll * kThreads) {
-            float v[kUnroll][V];
+            RawGrp<T, V> rv[kUnroll];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) ld_grp<T, V>(at(k + u * kThreads), v[u]);
+            for (int u = 0; u < kUnroll; ++u) ld_raw<T, V>(at(k + u * kThreads), rv[u]);
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) add(v[u]);
+            for (int u = 0; u < kUnroll; ++u) {
+                float v[V];
+                unpack<T, V>(rv[u], v);
+                add(v);
+            }
         }
         for (; k < items; k += kThreads) {
             float v[V];
@@ -136,11 +179,15 @@ __global__ __launch_bounds__(kThreads) void bn_stats_kernel(const T* __restrict_
         const int64_t step = c * hw;
         int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
         for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
-            float v[kAhead][V];
+            RawGrp<T, V> rv[kAhead];
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u) ld_grp<T, V>(x + e + u * step, v[u]);
+            for (int u = 0; u < kAhead; ++u) ld_raw<T, V>(x + e + u * step, rv[u]);
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u) add(v[u]);
+            for (int u = 0; u < kAhead; ++u) {
+                float v[V];
+                unpack<T, V>(rv[u], v);
+                add(v);
+            }
         }
         for (; i < n1; ++i, e += step) {
             float v[V];
@@ -291,16 +338,21 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
             return ((n0 + i) * c + ch) * hw + (int64_t)j * V;
         };
         uint32_t k = threadIdx.x;
-        for (; k + (kUnroll - 1) * kThreads < items; k += kUnroll * kThreads) {
-            float g[kUnroll][V], v[kUnroll][V];
+        for (; k + (kUnrollB - 1) * kThreads < items; k += kUnrollB * kThreads) {
+            RawGrp<T, V> rg[kUnrollB], rv[kUnrollB];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < kUnrollB; ++u) {
                 const int64_t e = off(k + u * kThreads);
-                ld_grp<T, V>(dy + e, g[u]);
-                ld_grp<T, V>(x + e, v[u]);
+                ld_raw<T, V>(dy + e, rg[u]);
+                ld_raw<T, V>(x + e, rv[u]);
             }
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) add(g[u], v[u]);
+            for (int u = 0; u < kUnrollB; ++u) {
+                float g[V], v[V];
+                unpack<T, V>(rg[u], g);
+                unpack<T, V>(rv[u], v);
+                add(g, v);
+            }
         }
         for (; k < items; k += kThreads) {
             float g[V], v[V];
@@ -312,15 +364,20 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
     } else if ((int64_t)threadIdx.x < hwg) {
         const int64_t step = c * hw;
         int64_t e = (n0 * c + ch) * hw + (int64_t)threadIdx.x * V, i = n0;
-        for (; i + kAhead <= n1; i += kAhead, e += kAhead * step) {
-            float g[kAhead][V], v[kAhead][V];
+        for (; i + kAheadB <= n1; i += kAheadB, e += kAheadB * step) {
+            RawGrp<T, V> rg[kAheadB], rv[kAheadB];
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u) {
-                ld_grp<T, V>(dy + e + u * step, g[u]);
-                ld_grp<T, V>(x + e + u * step, v[u]);
+            for (int u = 0; u < kAheadB; ++u) {
+                ld_raw<T, V>(dy + e + u * step, rg[u]);
+                ld_raw<T, V>(x + e + u * step, rv[u]);
             }
 #pragma unroll
-            for (int u = 0; u < kAhead; ++u) add(g[u], v[u]);
+            for (int u = 0; u < kAheadB; ++u) {
+                float g[V], v[V];
+                unpack<T, V>(rg[u], g);
+                unpack<T, V>(rv[u], v);
+                add(g, v);
+            }
         }
         for (; i < n1; ++i, e += step) {
             float g[V], v[V];
