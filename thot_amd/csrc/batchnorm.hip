@@ -224,26 +224,38 @@ struct BnAct {
     const float* rstd;
 };
 
-// Sum of the channel's split partials (pairs), one wave per channel: lanes
-// take splits s ≡ lane (mod 64) in order, then a fixed xor butterfly, so the
-// result does not depend on timing.
-__device__ __forceinline__ void wave_sum_partials(const float* __restrict__ partial, int64_t ch, int64_t splits,
-                                                  double& s1, double& s2) {
-    const int lane = threadIdx.x & 63;
+// Sum of channel ch's split partials (pairs) by one thread, in split order
+// (double accumulation; the channel's pairs are contiguous, read as
+// 16-byte pieces when aligned).
+__device__ __forceinline__ void sum_partials(const float* __restrict__ partial, int64_t ch, int64_t splits,
+                                             double& s1, double& s2) {
+    const float* q = partial + ch * splits * 2;
     s1 = 0.0;
     s2 = 0.0;
-    for (int64_t s = lane; s < splits; s += 64) {
-        s1 += partial[(ch * splits + s) * 2 + 0];
-        s2 += partial[(ch * splits + s) * 2 + 1];
-    }
+    int64_t s = 0;
+    if (((uintptr_t)q & 15) == 0) {
+        for (; s + 8 <= splits; s += 8) {
+            f32x4 v[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        s1 += __shfl_xor(s1, o);
-        s2 += __shfl_xor(s2, o);
+            for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4*>(q + 2 * s + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                s1 += v[u].x;
+                s2 += v[u].y;
+                s1 += v[u].z;
+                s2 += v[u].w;
+            }
+        }
+    }
+    for (; s < splits; ++s) {
+        s1 += q[2 * s];
+        s2 += q[2 * s + 1];
     }
 }
 
-// y = a·x + c used by the apply pass.  One wave per channel.
+// Per channel: mean, rstd, running stats and the coefficients (a, c) of
+// y = a·x + c used by the apply pass.  One thread per channel; every load
+// the channel needs is issued before its partials are summed.
 template <typename T>
 __global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, const float* __restrict__ partial, int64_t c,
                                                       int64_t splits, int64_t hw, int64_t m,
@@ -251,11 +263,13 @@ __global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, c
                                                       float eps, float momentum, float* __restrict__ running_mean,
                                                       float* __restrict__ running_var, float* __restrict__ mean,
                                                       float* __restrict__ rstd, float* __restrict__ coef) {
-    const int64_t ch = blockIdx.x;
-    double s1, s2;
-    wave_sum_partials(partial, ch, splits, s1, s2);
-    if (threadIdx.x != 0) return;
+    const int64_t ch = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (ch >= c) return;
     const float pivot = Io<T>::ld(x, ch * hw);
+    const float g = gamma ? gamma[ch] : 1.f, b = beta ? beta[ch] : 0.f;
+    const float rm0 = running_mean ? running_mean[ch] : 0.f, rv0 = running_mean ? running_var[ch] : 0.f;
+    double s1, s2;
+    sum_partials(partial, ch, splits, s1, s2);
     const double md = s1 / (double)m;
     double var = s2 / (double)m - md * md;
     if (var < 0.0) var = 0.0;
@@ -263,12 +277,11 @@ __global__ __launch_bounds__(64) void bn_fwd_finalize(const T* __restrict__ x, c
     const float rs = (float)(1.0 / sqrt(var + (double)eps));
     mean[ch] = mu;
     rstd[ch] = rs;
-    const float g = gamma ? gamma[ch] : 1.f, b = beta ? beta[ch] : 0.f;
     bn_coef(g, b, mu, rs, coef[2 * ch + 0], coef[2 * ch + 1]);
     if (running_mean) {
         const double unbiased = m > 1 ? var * (double)m / (double)(m - 1) : var;
-        running_mean[ch] = (1.f - momentum) * running_mean[ch] + momentum * mu;
-        running_var[ch] = (1.f - momentum) * running_var[ch] + momentum * (float)unbiased;
+        running_mean[ch] = (1.f - momentum) * rm0 + momentum * mu;
+        running_var[ch] = (1.f - momentum) * rv0 + momentum * (float)unbiased;
     }
 }
 
@@ -393,21 +406,23 @@ __global__ __launch_bounds__(kThreads) void bn_bwd_reduce_kernel(const T* __rest
     }
 }
 
-// dγ, dβ and the coefficients of dx = A·dy + B·x + C.  One wave per channel.
+// dγ, dβ and the coefficients of dx = A·dy + B·x + C.  One thread per
+// channel, its loads issued before the partials are summed.
 __global__ __launch_bounds__(64) void bn_bwd_finalize(const float* __restrict__ partial, int64_t c, int64_t splits,
                                                       int64_t m, const float* __restrict__ mean,
                                                       const float* __restrict__ rstd, const float* __restrict__ gamma,
                                                       float* __restrict__ dgamma, float* __restrict__ dbeta,
                                                       int accumulate, float* __restrict__ coef) {
-    const int64_t ch = blockIdx.x;
-    double sdy, sdyxc;
-    wave_sum_partials(partial, ch, splits, sdy, sdyxc);
-    if (threadIdx.x != 0) return;
+    const int64_t ch = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (ch >= c) return;
     const double rs = rstd[ch], mu = mean[ch];
-    const double sdyx = sdyxc * rs;  // Σ dy·x̂
-    if (dgamma) dgamma[ch] = accumulate ? dgamma[ch] + (float)sdyx : (float)sdyx;
-    if (dbeta) dbeta[ch] = accumulate ? dbeta[ch] + (float)sdy : (float)sdy;
     const double g = gamma ? gamma[ch] : 1.0;
+    const float dg0 = (dgamma && accumulate) ? dgamma[ch] : 0.f, db0 = (dbeta && accumulate) ? dbeta[ch] : 0.f;
+    double sdy, sdyxc;
+    sum_partials(partial, ch, splits, sdy, sdyxc);
+    const double sdyx = sdyxc * rs;  // Σ dy·x̂
+    if (dgamma) dgamma[ch] = accumulate ? dg0 + (float)sdyx : (float)sdyx;
+    if (dbeta) dbeta[ch] = accumulate ? db0 + (float)sdy : (float)sdy;
     const double A = g * rs;
     const double B = -g * rs * rs * sdyx / (double)m;
     const double C = -g * rs * sdy / (double)m - B * mu;
@@ -490,7 +505,8 @@ int fwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const fl
         constexpr int V = decltype(vt)::value;
         hipLaunchKernelGGL((bn_stats_kernel<T, V>), g1, dim3(kThreads), 0, ctx->stream, x, n, c, hw, per, fd_hwg,
                            partial);
-        hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)c), dim3(64), 0, ctx->stream, x, partial, c, splits, hw,
+        hipLaunchKernelGGL(bn_fwd_finalize<T>, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, x,
+                           partial, c, splits, hw,
                            n * hw, gamma, beta, eps, momentum, rm, rv, mean, rstd, coef);
         if (y)
             hipLaunchKernelGGL((bn_affine_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, y, ngroups, fd_hwg,
@@ -530,7 +546,8 @@ int bwd(nott_ctx ctx, int64_t n, int64_t c, int64_t hw, const void* xv, const vo
         constexpr int V = decltype(vt)::value;
         hipLaunchKernelGGL((bn_bwd_reduce_kernel<T, V>), g1, dim3(kThreads), 0, ctx->stream, x, dy, mean, n, c, hw,
                            per, fd_hwg, partial, act);
-        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c, splits, n * hw,
+        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, partial, c,
+                           splits, n * hw,
                            mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
         if (dx)
             hipLaunchKernelGGL((bn_bwd_apply_kernel<T, V>), ga, dim3(kThreads), 0, ctx->stream, x, dy, dx, ngroups,
@@ -647,7 +664,8 @@ extern "C" int nott_batchnorm2d_relu_maxpool2d_bwd(nott_ctx ctx, const nott_pool
         int st = nott::maxpool_bwd_tap_bnrelu_reduce(ctx, d, dtype, tap, dy, x, gamma, beta, mean, rstd, (int32_t)per,
                                                      (int32_t)splits, partial);
         if (st != NOTT_OK) return st;
-        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)c), dim3(64), 0, ctx->stream, partial, c, splits, n * hw,
+        hipLaunchKernelGGL(bn_bwd_finalize, dim3((unsigned)nott::ceil_div(c, 64)), dim3(64), 0, ctx->stream, partial, c,
+                           splits, n * hw,
                            mean, rstd, gamma, dgamma, dbeta, accumulate, coef);
         st = nott::launch_status(ctx, "batchnorm_bwd_finalize");
         if (st != NOTT_OK || !dx) return st;

@@ -116,6 +116,79 @@ __global__ __launch_bounds__(256) void conv3x3_wprep2_kernel(const T* __restrict
     dst[slice + (int64_t)(lds_off(tap * kTileCo + col, cil / SUB) >> 4) * SUB + cil % SUB] = val;
 }
 
+// The same two layouts when cout and cin are whole 64-channel blocks (no zero
+// rows), one 16-byte destination chunk per thread and tap: thread t < cout·cin/SUB
+// takes output channel co and the SUB input channels ci0.. of the forward
+// slices and reads their 9·SUB weights as one contiguous run; the rest take
+// (c, k0..) of the data-gradient slices, reading SUB runs of 9.
+template <typename T>
+__global__ __launch_bounds__(256) void conv3x3_wprep2v_kernel(const T* __restrict__ w, T* __restrict__ wf,
+                                                              T* __restrict__ wd, int32_t cout, int32_t cin) {
+    constexpr int CC = Chunk<T>::CC, SUB = Chunk<T>::SUB;
+    constexpr int32_t SLICE = 9 * kTileCo * CC;
+    constexpr int EB = (int)sizeof(T);
+    const int64_t per = (int64_t)cout * (cin / SUB);
+    int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool dg = t >= per;
+    if (dg) t -= per;
+    if (t >= per) return;
+    // v[tap] holds the SUB input channels' weights of one tap, packed
+    uint32_t v[9][SUB * EB / 4];
+    int32_t co, ci0, icount;
+    if (!dg) {
+        co = (int32_t)(t / (cin / SUB));
+        ci0 = (int32_t)(t % (cin / SUB)) * SUB;
+        icount = cin;
+        // 9·SUB contiguous weights w[co][ci0 + e][tap] (144 bytes, 16-byte aligned)
+        const u32x4* src = reinterpret_cast<const u32x4*>(w + ((int64_t)co * cin + ci0) * 9);
+        uint32_t raw[9 * SUB * EB / 4];
+#pragma unroll
+        for (int q = 0; q < 9 * SUB * EB / 16; ++q) {
+            const u32x4 u = src[q];
+            raw[4 * q] = u.x; raw[4 * q + 1] = u.y; raw[4 * q + 2] = u.z; raw[4 * q + 3] = u.w;
+        }
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            if constexpr (EB == 4) {
+#pragma unroll
+                for (int e = 0; e < SUB; ++e) v[tap][e] = raw[e * 9 + tap];
+            } else {
+#pragma unroll
+                for (int e = 0; e < SUB; e += 2) {
+                    const int j0 = e * 9 + tap, j1 = (e + 1) * 9 + tap;   // element indices in the run
+                    const uint32_t lo = (raw[j0 >> 1] >> (16 * (j0 & 1))) & 0xffffu;
+                    const uint32_t hi = (raw[j1 >> 1] >> (16 * (j1 & 1))) & 0xffffu;
+                    v[tap][e / 2] = lo | (hi << 16);
+                }
+            }
+        }
+    } else {
+        // the data gradient's pass: output channel co = c, input channels k0 ..
+        co = (int32_t)(t / (cout / SUB));
+        ci0 = (int32_t)(t % (cout / SUB)) * SUB;
+        icount = cout;
+        const T* src = w + ((int64_t)ci0 * cin + co) * 9;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            uint32_t x[SUB];
+#pragma unroll
+            for (int e = 0; e < SUB; ++e) {
+                T val = src[(int64_t)e * cin * 9 + (8 - tap)];
+                if constexpr (EB == 4) x[e] = __builtin_bit_cast(uint32_t, val);
+                else x[e] = (uint32_t)__builtin_bit_cast(uint16_t, val);
+            }
+#pragma unroll
+            for (int e = 0; e < SUB * EB / 4; ++e) v[tap][e] = EB == 4 ? x[e] : (x[2 * e] | (x[2 * e + 1] << 16));
+        }
+    }
+    T* dst = dg ? wd : wf;
+    const int64_t slice = ((int64_t)(co / kTileCo) * (icount / CC) + ci0 / CC) * SLICE;
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+        *reinterpret_cast<u32x4*>(dst + slice + (int64_t)(lds_off(tap * kTileCo + co % kTileCo, (ci0 % CC) / SUB) >> 4) * SUB) =
+            u32x4{v[tap][0], v[tap][1], v[tap][2], v[tap][3]};
+}
+
 template <typename T, bool VEC, int LW>
 __global__ __launch_bounds__(kThreads, 2) void conv3x3_same_kernel(const T* __restrict__ in, const T* __restrict__ wp,
                                                                   const float* __restrict__ bias, T* __restrict__ out,
@@ -482,14 +555,18 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
         const bool aligned = ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 7) == 0;
         if (dma && (aligned || prepared)) {
             const bf16_t* wpp = prepared;
+            // a forward whose data gradient takes the DMA kernel too: both
+            // layouts from one prep launch
+            const bool pair = !DGRAD && !wpp && dg_out && dma_applies(n, cout, h, w, cin);
             if (!wpp) {
                 bf16_t* ws = static_cast<bf16_t*>(workspace(ctx, sizeof(T) * (size_t)dma_prep_elems(cin, cout)));
                 if (!ws) return NOTT_ERR_ALLOC;
-                const int st = dma_prep<DGRAD>(ctx, wsrc, ws, cin, cout);
+                const int st = pair ? dma_prep_pair(ctx, wsrc, ws, dg_out, cin, cout)
+                                    : dma_prep<DGRAD>(ctx, wsrc, ws, cin, cout);
                 if (st != NOTT_OK) return st;
                 wpp = ws;
             }
-            if (dg_out) {
+            if (dg_out && !pair) {
                 // the data gradient's pass is cout → cin over the same weight
                 if ((ctx->conv_dma & 1) && dma_applies(n, cout, h, w, cin)) {
                     const int st = dma_prep<true>(ctx, wsrc, dg_out, cout, cin);
@@ -547,6 +624,11 @@ int run_same(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t
             const int st = dma_prep<true>(ctx, wsrc, dg_out, cout, cin);
             if (st != NOTT_OK) return st;
         }
+    } else if (dg_out && cout % kTileCo == 0 && cin % kTileCo == 0 && ((uintptr_t)wsrc & 15) == 0 &&
+               ((uintptr_t)dg_out & 15) == 0) {
+        const int64_t threads = 2 * (int64_t)cout * (cin / Chunk<T>::SUB);
+        hipLaunchKernelGGL(conv3x3_wprep2v_kernel<T>, dim3((unsigned)ceil_div(threads, 256)), dim3(256), 0, ctx->stream,
+                           wsrc, wp, dg_out, cout, cin);
     } else if (dg_out) {
         const int64_t cbd = ceil_div(cin, kTileCo);
         hipLaunchKernelGGL(conv3x3_wprep2_kernel<T>, dim3((unsigned)ceil_div(9 * kTileCo * CC, 256),

@@ -109,14 +109,10 @@ __device__ __forceinline__ TileInfo decode_tile(int32_t t, const DmaParams& p) {
 // e = 0..7, at byte ((((cb·nch + c)·9 + t)·2 + cw)·64 + l)·16.
 // Forward: w is [cout][cin][3][3]; data gradient: w is the conv weight
 // [cin][cout][3][3] of this pass's terms, flipped.
+// Source element of destination element i of a pass cin → cout.
 template <bool DGRAD>
-__global__ __launch_bounds__(256) void dma_wprep_kernel(const bf16_t* __restrict__ w, bf16_t* __restrict__ wp,
-                                                        int32_t cin, int32_t cout) {
-    // one element per thread (destination order, so stores are contiguous)
+__device__ __forceinline__ int64_t dma_wprep_src(int64_t i, int32_t cin, int32_t cout) {
     const int32_t nch = cin / kCK;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)cout * cin * 9;
-    if (i >= total) return;
     const int e = (int)(i & 7);
     const int64_t g = i >> 3;
     const int l = (int)(g & 63);
@@ -129,7 +125,25 @@ __global__ __launch_bounds__(256) void dma_wprep_kernel(const bf16_t* __restrict
     const int cb = (int)(q / nch);
     const int32_t co = cb * kCoTile + cw * 16 + (l & 15);
     const int32_t ci = c * kCK + 8 * (l >> 4) + e;
-    wp[i] = w[DGRAD ? (((int64_t)ci * cout + co) * 9 + (8 - t)) : (((int64_t)co * cin + ci) * 9 + t)];
+    return DGRAD ? (((int64_t)ci * cout + co) * 9 + (8 - t)) : (((int64_t)co * cin + ci) * 9 + t);
+}
+template <bool DGRAD>
+__global__ __launch_bounds__(256) void dma_wprep_kernel(const bf16_t* __restrict__ w, bf16_t* __restrict__ wp,
+                                                        int32_t cin, int32_t cout) {
+    // one element per thread (destination order, so stores are contiguous)
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)cout * cin * 9) return;
+    wp[i] = w[dma_wprep_src<DGRAD>(i, cin, cout)];
+}
+// Both passes of one conv weight w [cout][cin][3][3] in one launch: the
+// forward's slices (cin → cout) into wf and the data gradient's (cout → cin,
+// flipped) into wd.
+__global__ __launch_bounds__(256) void dma_wprep_pair_kernel(const bf16_t* __restrict__ w, bf16_t* __restrict__ wf,
+                                                             bf16_t* __restrict__ wd, int32_t cin, int32_t cout) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)cout * cin * 9) return;
+    wf[i] = w[dma_wprep_src<false>(i, cin, cout)];
+    wd[i] = w[dma_wprep_src<true>(i, cout, cin)];
 }
 
 // LDS: [weights of the workgroup's output block, all input chunks][input
@@ -721,6 +735,13 @@ int dma_prep(nott_ctx ctx, const bf16_t* w, bf16_t* wp, int32_t cin, int32_t cou
     hipLaunchKernelGGL(dma_wprep_kernel<DGRAD>, dim3((unsigned)ceil_div(elems, 256)), dim3(256), 0, ctx->stream, w,
                        wp, cin, cout);
     return launch_status(ctx, "conv3x3_dma_wprep");
+}
+
+int dma_prep_pair(nott_ctx ctx, const bf16_t* w, bf16_t* wf, bf16_t* wd, int32_t cin, int32_t cout) {
+    const int64_t elems = (int64_t)cout * cin * 9;
+    hipLaunchKernelGGL(dma_wprep_pair_kernel, dim3((unsigned)ceil_div(elems, 256)), dim3(256), 0, ctx->stream, w, wf,
+                       wd, cin, cout);
+    return launch_status(ctx, "conv3x3_dma_wprep_pair");
 }
 
 int dma_run(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const bf16_t* in,

@@ -52,6 +52,9 @@ bool dma_applies(int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout);
 int64_t dma_prep_elems(int32_t cin, int32_t cout);
 template <bool DGRAD>
 int dma_prep(nott_ctx ctx, const bf16_t* w, bf16_t* wp, int32_t cin, int32_t cout);
+// Both: the forward's slices of w (cin → cout) into wf, the data gradient's
+// into wd, one launch.
+int dma_prep_pair(nott_ctx ctx, const bf16_t* w, bf16_t* wf, bf16_t* wd, int32_t cin, int32_t cout);
 int dma_run(nott_ctx ctx, int32_t n, int32_t cin, int32_t h, int32_t w, int32_t cout, const bf16_t* in,
             const bf16_t* wp, const float* bias, bf16_t* out, int relu);
 
