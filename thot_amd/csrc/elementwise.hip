@@ -103,6 +103,17 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const TS* __restrict__ s
     if (i < n) Io<TD>::st(d, i, Io<TS>::ld(s, i));
 }
 
+// fp32 → bf16 over 8-element groups (two 16-byte loads, one 16-byte store per
+// thread), rounded as the element kernel rounds; both buffers 16-byte aligned.
+__global__ __launch_bounds__(kThreads) void cast_f32_bf16_vec_kernel(const float* __restrict__ s, bf16_t* __restrict__ d,
+                                                                    int64_t ngroups) {
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (q >= ngroups) return;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(s + 8 * q), hi = *reinterpret_cast<const f32x4*>(s + 8 * q + 4);
+    *reinterpret_cast<u32x4*>(d + 8 * q) =
+        u32x4{pack_bf16x2(lo.x, lo.y), pack_bf16x2(lo.z, lo.w), pack_bf16x2(hi.x, hi.y), pack_bf16x2(hi.z, hi.w)};
+}
+
 __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ p, int64_t nwords,
                                                         uint8_t* __restrict__ tail, int64_t ntail) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
@@ -249,7 +260,15 @@ int nott_cast(nott_ctx ctx, int64_t n, const void* src, nott_dtype st, void* dst
     if (n == 0) return NOTT_OK;
     nott::DeviceScope scope(ctx->device);
     const dim3 grid((unsigned)nott::ceil_div(n, kThreads));
-    if (st == NOTT_F32 && dt == NOTT_BF16)
+    if (st == NOTT_F32 && dt == NOTT_BF16 && ((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0 && n >= 8) {
+        // whole 8-element groups vectorised, the tail by the element kernel
+        const int64_t ng = n / 8, done = 8 * ng;
+        hipLaunchKernelGGL(cast_f32_bf16_vec_kernel, dim3((unsigned)nott::ceil_div(ng, kThreads)), dim3(kThreads), 0,
+                           ctx->stream, static_cast<const float*>(src), static_cast<bf16_t*>(dst), ng);
+        if (done < n)
+            hipLaunchKernelGGL((cast_kernel<float, bf16_t>), dim3(1), dim3(kThreads), 0, ctx->stream,
+                               static_cast<const float*>(src) + done, static_cast<bf16_t*>(dst) + done, n - done);
+    } else if (st == NOTT_F32 && dt == NOTT_BF16)
         hipLaunchKernelGGL((cast_kernel<float, bf16_t>), grid, dim3(kThreads), 0, ctx->stream,
                            static_cast<const float*>(src), static_cast<bf16_t*>(dst), n);
     else if (st == NOTT_BF16 && dt == NOTT_F32)
