@@ -347,7 +347,11 @@ struct Conv2dFn : torch::autograd::Function<Conv2dFn> {
         }
         Tensor gw = grad_buffer(w), gb = grad_buffer(b);
         if (gw.defined() || gb.defined()) {
-            nott_ctx cw = wgrad_context(dy, {x, dy}, conv_flops(d, dy));
+            // the side stream only where a data gradient runs beside it: the
+            // first layer's weight gradient (no dx) ends backward, and queued
+            // behind the side stream's backlog it would only delay the join
+            // (ResNet-18 bf16 step 3.099 -> 3.077 ms)
+            nott_ctx cw = dx.defined() ? wgrad_context(dy, {x, dy}, conv_flops(d, dy)) : c;
             check(nott_conv2d_bwd_weight(cw, &d, dtype_of(dy), ptr(x), ptr(dy), fptr(gw), fptr(gb), 1), cw,
                   "conv2d wgrad");
         }
@@ -397,7 +401,7 @@ struct Conv2dReluFn : torch::autograd::Function<Conv2dReluFn> {
         }
         Tensor gw = grad_buffer(w), gb = grad_buffer(b);
         if (gw.defined() || gb.defined()) {
-            nott_ctx cw = wgrad_context(dz, {x, dz}, conv_flops(d, dz));
+            nott_ctx cw = dx.defined() ? wgrad_context(dz, {x, dz}, conv_flops(d, dz)) : c;
             check(nott_conv2d_bwd_weight(cw, &d, dtype_of(dz), ptr(x), ptr(dz), fptr(gw), fptr(gb), 1), cw,
                   "conv2d wgrad");
         }
