@@ -148,7 +148,6 @@ __global__ __launch_bounds__(kThreads, 2) void stem_fwd_kernel(const T* __restri
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int32_t rowb = p.wrow * E;                          // bytes per staged channel row
     char* lds_x = smem;                                        // [row][c][wrow]
-    char* lds_w = smem + (size_t)p.in_rows * kStemC * rowb;    // [j][nt][lane][16 B]
 
     int32_t tile = blockIdx.x;
     if (p.remap) tile = (int32_t)((blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3));
@@ -166,11 +165,6 @@ __global__ __launch_bounds__(kThreads, 2) void stem_fwd_kernel(const T* __restri
     // Staged rows: padded column u = w + pw at element u (so that a lane's
     // first column 2·ow − pw + s0 sits at the even element 2·ow + s0).
     stem_stage_rows<T, 4>(x, lds_x, p, v_lo, nvr, p.pw, false);
-    {
-        const u32x4* src = reinterpret_cast<const u32x4*>(wf);
-        const int32_t nw = K::KSTEPS * (p.cout / 16) * 64;
-        for (int32_t t = threadIdx.x; t < nw; t += kThreads) reinterpret_cast<u32x4*>(lds_w)[t] = src[t];
-    }
     __syncthreads();
 
     const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -192,6 +186,13 @@ __global__ __launch_bounds__(kThreads, 2) void stem_fwd_kernel(const T* __restri
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // The B fragments (the pre-arranged weights, the same for every
+    // workgroup) are read from global memory, where they stay cached, one
+    // K step ahead: no weight copy in LDS, so more workgroups fit per CU.
+    const u32x4* wfv = reinterpret_cast<const u32x4*>(wf);
+    u32x4 bn[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) bn[nt] = wfv[nt * 64 + lane];
 #pragma unroll
     for (int j = 0; j < K::KSTEPS; ++j) {
         const int g = 4 * j + kq;
@@ -202,52 +203,62 @@ __global__ __launch_bounds__(kThreads, 2) void stem_fwd_kernel(const T* __restri
         const int32_t goff = ((cr % kStemR) * kStemC + cr / kStemR) * rowb + si * 16;
         u32x4 a[4], b[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) a[mt] = stem_afrag<T>(lds_x + abase[mt] + goff);
+        for (int nt = 0; nt < 4; ++nt) b[nt] = bn[nt];
+        if (j + 1 < K::KSTEPS) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-            b[nt] = reinterpret_cast<const u32x4*>(lds_w)[(j * (p.cout / 16) + nt) * 64 + lane];
+            for (int nt = 0; nt < 4; ++nt) bn[nt] = wfv[((j + 1) * (p.cout / 16) + nt) * 64 + lane];
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) a[mt] = stem_afrag<T>(lds_x + abase[mt] + goff);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int nt = 0; nt < 4; ++nt) mfma_chunk<T>(a[mt], b[nt], acc[mt][nt]);
     }
 
-    // Epilogue through LDS as [co][pixel] rows, 16-byte runs of one plane.
-    __syncthreads();
-    constexpr int OP = kTilePix * E + 16;
-    char* lds_o = smem;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-        const int32_t col = nt * 16 + r16;
-        const float bv = bias ? bias[col] : 0.f;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const int px = wid * 64 + mt * 16 + kq * 4;
-            f32x4 v = acc[mt][nt] + bv;
-            if (p.relu) {
-                v.x = relu_out(v.x); v.y = relu_out(v.y); v.z = relu_out(v.z); v.w = relu_out(v.w);
-            }
-            Vec4<T>::st(reinterpret_cast<T*>(lds_o + col * OP + px * E), v);
-        }
-    }
-    __syncthreads();
+    // Epilogue through LDS as [co][pixel] rows, 16-byte runs of one plane,
+    // 32 channels at a time.
     const int64_t plane = (int64_t)p.ho * p.wo;
+    constexpr int OP = kTilePix * E + 16;
     constexpr int E16 = 16 / E;
     constexpr int RUNS = kTilePix / E16;
-    for (int t = threadIdx.x; t < kStemCo * RUNS; t += kThreads) {
-        const int col = t / RUNS, jr = t % RUNS;
-        const int32_t m = m0 + jr * E16;
-        if (m > m_last) continue;
-        const char* src = lds_o + col * OP + jr * 16;
-        uint32_t n, hw;
-        p.fd_howo.divmod((uint32_t)m, n, hw);
-        if (p.vec_store && m + E16 - 1 <= m_last) {
-            *reinterpret_cast<u32x4*>(y + ((int64_t)n * p.cout + col) * plane + hw) = *reinterpret_cast<const u32x4*>(src);
-        } else {
-            for (int e = 0; e < E16 && m + e <= m_last; ++e) {
-                uint32_t ne, hwe;
-                p.fd_howo.divmod((uint32_t)(m + e), ne, hwe);
-                y[((int64_t)ne * p.cout + col) * plane + hwe] = reinterpret_cast<const T*>(src)[e];
+    char* lds_o = smem;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int nt = 2 * half + h;
+            const int32_t col = nt * 16 + r16;
+            const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int px = wid * 64 + mt * 16 + kq * 4;
+                f32x4 v = acc[mt][nt] + bv;
+                if (p.relu) {
+                    v.x = relu_out(v.x); v.y = relu_out(v.y); v.z = relu_out(v.z); v.w = relu_out(v.w);
+                }
+                Vec4<T>::st(reinterpret_cast<T*>(lds_o + (h * 16 + r16) * OP + px * E), v);
+            }
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < (kStemCo / 2) * RUNS; t += kThreads) {
+            const int cl = t / RUNS, jr = t % RUNS;
+            const int col = half * (kStemCo / 2) + cl;
+            const int32_t m = m0 + jr * E16;
+            if (m > m_last) continue;
+            const char* src = lds_o + cl * OP + jr * 16;
+            uint32_t n, hw;
+            p.fd_howo.divmod((uint32_t)m, n, hw);
+            if (p.vec_store && m + E16 - 1 <= m_last) {
+                *reinterpret_cast<u32x4*>(y + ((int64_t)n * p.cout + col) * plane + hw) =
+                    *reinterpret_cast<const u32x4*>(src);
+            } else {
+                for (int e = 0; e < E16 && m + e <= m_last; ++e) {
+                    uint32_t ne, hwe;
+                    p.fd_howo.divmod((uint32_t)(m + e), ne, hwe);
+                    y[((int64_t)ne * p.cout + col) * plane + hwe] = reinterpret_cast<const T*>(src)[e];
+                }
             }
         }
     }
@@ -523,8 +534,8 @@ int stem_fwd(nott_ctx ctx, const nott_conv2d_desc* d, const T* x, const T* w, co
     }
     p.in_rows = max_nvr;
     const size_t wbytes = (size_t)K::KSTEPS * (p.cout / 16) * 64 * 16;
-    const size_t lds_fill = (size_t)p.in_rows * kStemC * p.wrow * E + wbytes;
-    const size_t lds_epi = (size_t)kStemCo * (kTilePix * E + 16);
+    const size_t lds_fill = (size_t)p.in_rows * kStemC * p.wrow * E;
+    const size_t lds_epi = (size_t)(kStemCo / 2) * (kTilePix * E + 16);
     const size_t lds = std::max(lds_fill, lds_epi);
     if (lds > 160 * 1024) return fail(ctx, NOTT_ERR_UNSUPPORTED, "stem conv: tile does not fit in LDS");
     p.remap = (p.tiles % 8 == 0) ? 1 : 0;
