@@ -14,7 +14,7 @@
 // left padding chosen so that each lane's 16-byte operand starts on a
 // 4-byte boundary: the A fragment is four (bf16) or two (fp32) aligned LDS
 // reads at consecutive addresses across lanes, no im2col.  The weights are
-// pre-arranged in global memory in MFMA-fragment order and copied to LDS.
+// pre-arranged in global memory in MFMA-fragment order and read from there.
 #include "conv_tile.hpp"
 
 #include <algorithm>
